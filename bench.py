@@ -1,0 +1,368 @@
+"""KV-cache handoff benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3] [--seed 0]
+
+A step is one full handoff of the workload: every request's blocks move from
+the prefill pool to the decode pool under the destination ids a decode
+worker's BlockManager hands out (iekv.workloads). Both pools are resident in
+HBM before timing starts; the src pool holds N(0,1) values (raw random bytes
+without NaN codes for fp8). Legs:
+
+  direct       one iekv_copy_direct launch per request (the headline: 2P bytes)
+  pack_unpack  iekv_pack into a per-request staging buffer, then iekv_unpack (4P bytes)
+  batched      all requests' blocks in ONE direct launch (2P bytes)
+
+``value`` is the direct leg's algorithmic read+write bandwidth, 2P / step
+time, in GB/s (P = blocks x 2L x T). ``roofline.achieved`` is the algorithmic
+bytes per kv_move launch divided by the average launch duration, both taken
+from HIP events recorded around each launch on the launch stream during the
+timed steps. After timing, every destination tile is compared with its
+source tile on the GPU (the whole workload, bit for bit). ``cpu_baseline``
+times the NumPy restatement of the reference handoff (oracle/) on a bounded
+sample of the same shape on this host, single-threaded.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "inference-engine_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def torch_dtype(name: str):
+    import torch
+
+    return {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16,
+            "fp8_e4m3": torch.float8_e4m3fn, "uint8": torch.uint8}[name]
+
+
+def fill_pool(arrays, dtype_name: str, seed: int) -> None:
+    """N(0,1) values, or uniform random bytes without the e4m3fn NaN codes 0x7F / 0xFF."""
+    import torch
+
+    gen = torch.Generator(device=arrays[0].device)
+    gen.manual_seed(seed)
+    for t in arrays:
+        if dtype_name == "fp8_e4m3":
+            raw = t.view(torch.uint8)
+            r = torch.randint(0, 254, raw.shape, dtype=torch.int16, device=t.device,
+                              generator=gen)
+            raw.copy_((r + (r >= 0x7F).to(torch.int16)).to(torch.uint8))
+        else:
+            t.normal_(generator=gen)
+
+
+class Legs:
+    def __init__(self, workload, device, seed: int) -> None:
+        import torch
+
+        from iekv.engine.pools import KVPool, allocate_pool
+
+        self.torch = torch
+        self.w = workload
+        s = workload.shape
+        dtype = torch_dtype(s.dtype)
+        t0 = time.perf_counter()
+        self.src_k, self.src_v = allocate_pool(workload.src_pool_blocks, s.block_size, s.layers,
+                                               s.kv_heads, s.head_dim, dtype=dtype,
+                                               device=device, zero=False)
+        fill_pool(self.src_k + self.src_v, s.dtype, seed)
+        self.dst_k, self.dst_v = allocate_pool(workload.dst_pool_blocks, s.block_size, s.layers,
+                                               s.kv_heads, s.head_dim, dtype=dtype,
+                                               device=device, zero=True)
+        self.src = KVPool(self.src_k, self.src_v, s.block_size)
+        self.dst = KVPool(self.dst_k, self.dst_v, s.block_size)
+        self.src_ids = [self.src.block_ids(t) for t in workload.src_tables]
+        self.dst_ids = [self.dst.block_ids(t, unique=True) for t in workload.dst_tables]
+        self.src_all = self.src.block_ids(sum(workload.src_tables, []))
+        self.dst_all = self.dst.block_ids(sum(workload.dst_tables, []), unique=True)
+        longest = max(len(t) for t in workload.src_tables)
+        self.staging = torch.empty(longest * s.block_bytes, dtype=torch.uint8, device=device)
+        self.stream = torch.cuda.current_stream(device)
+        torch.cuda.synchronize()
+        log(f"[bench] pools ready: 2 x {workload.src_pool_blocks} blocks x {s.block_bytes} B "
+            f"({2 * workload.src_pool_blocks * s.block_bytes / 1e9:.1f} GB) in "
+            f"{time.perf_counter() - t0:.1f} s")
+
+    # -- one step of each leg; `events` collects (start, end, bytes, request) per launch ------
+    def _launch(self, fn, events, nbytes, request):
+        torch = self.torch
+        if events is None:
+            fn()
+            return
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        fn()
+        b.record(self.stream)
+        events.append((a, b, nbytes, request))
+
+    def direct(self, events=None) -> None:
+        from iekv import _native
+
+        h = self.stream.cuda_stream
+        bb = self.w.shape.block_bytes
+        for r, (s, d) in enumerate(zip(self.src_ids, self.dst_ids)):
+            n = s.numel()
+            self._launch(lambda: _native.call("iekv_copy_direct", self.src.native.handle,
+                                              self.dst.native.handle, s.data_ptr(),
+                                              d.data_ptr(), n, h), events, 2 * n * bb, r)
+
+    def pack_unpack(self, events=None) -> None:
+        from iekv import _native
+
+        h = self.stream.cuda_stream
+        bb = self.w.shape.block_bytes
+        st = self.staging
+        for r, (s, d) in enumerate(zip(self.src_ids, self.dst_ids)):
+            n = s.numel()
+            self._launch(lambda: _native.call("iekv_pack", self.src.native.handle, s.data_ptr(),
+                                              n, st.data_ptr(), st.numel(), h),
+                         events, 2 * n * bb, r)
+            self._launch(lambda: _native.call("iekv_unpack", self.dst.native.handle,
+                                              d.data_ptr(), n, st.data_ptr(), st.numel(), h),
+                         events, 2 * n * bb, r)
+
+    def batched(self, events=None) -> None:
+        from iekv import _native
+
+        n = self.src_all.numel()
+        self._launch(lambda: _native.call("iekv_copy_direct", self.src.native.handle,
+                                          self.dst.native.handle, self.src_all.data_ptr(),
+                                          self.dst_all.data_ptr(), n, self.stream.cuda_stream),
+                     events, 2 * n * self.w.shape.block_bytes, 0)
+
+    def verify(self) -> bool:
+        """Every destination tile equals its source tile (whole workload, on the GPU)."""
+        torch = self.torch
+        T = self.w.shape.tile_bytes
+        ok = True
+        for s_arr, d_arr in zip(self.src_k + self.src_v, self.dst_k + self.dst_v):
+            s_tiles = s_arr.view(torch.uint8).view(-1, T)
+            d_tiles = d_arr.view(torch.uint8).view(-1, T)
+            for lo in range(0, self.src_all.numel(), 8192):
+                si = self.src_all[lo:lo + 8192].long()
+                di = self.dst_all[lo:lo + 8192].long()
+                if not torch.equal(s_tiles.index_select(0, si), d_tiles.index_select(0, di)):
+                    ok = False
+        return ok
+
+    def clear_dst(self) -> None:
+        for t in self.dst_k + self.dst_v:
+            t.zero_()
+
+
+def time_leg(legs: Legs, step, steps: int, warmup: int):
+    torch = legs.torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    events: list = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(legs.stream)
+    for _ in range(steps):
+        step(events)
+    end.record(legs.stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(end) / steps
+    launches = [(a.elapsed_time(b), nbytes, r) for a, b, nbytes, r in events]
+    return ms_step, wall, launches
+
+
+def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: int, steps: int):
+    w = legs.w
+    durations = [ms for ms, _, _ in launches]
+    total_ms = sum(durations)
+    moved = sum(nbytes for _, nbytes, _ in launches)
+    per_request: dict[int, float] = {}
+    for ms, _, r in launches:
+        per_request[r] = per_request.get(r, 0.0) + ms
+    req_ms = sorted(v / steps for v in per_request.values())
+    gbs = bytes_per_step / (ms_step * 1e-3) / 1e9
+    kernel_gbs = moved / (total_ms * 1e-3) / 1e9 if total_ms else 0.0
+    out = {
+        "ms_per_step": round(ms_step, 4),
+        "GBps": round(gbs, 1),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "kernel_GBps": round(kernel_gbs, 1),
+        "launches_per_step": len(launches) // steps,
+        "avg_launch_us": round(1000 * total_ms / max(1, len(launches)), 2),
+        "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
+    }
+    if name != "batched":
+        out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
+                                 "p50": round(req_ms[len(req_ms) // 2], 4),
+                                 "p99": round(req_ms[min(len(req_ms) - 1,
+                                                         int(0.99 * len(req_ms)))], 4),
+                                 "max": round(req_ms[-1], 4)}
+    log(f"[bench] {name:11s} {ms_step:9.3f} ms/step  {gbs:8.1f} GB/s "
+        f"({out['pct_hbm_peak']:.1f}% of peak)  kernel {kernel_gbs:8.1f} GB/s  "
+        f"{out['avg_launch_us']:.1f} us/launch")
+    return out, kernel_gbs, 1000 * total_ms / max(1, len(launches)), moved / max(1, len(launches))
+
+
+def cpu_baseline(workload, budget_blocks: int, seed: int) -> dict:
+    """The reference handoff restated in NumPy (oracle/), single-threaded, on a bounded sample."""
+    import numpy as np
+
+    from oracle.copier import LayeredSlotCopier, pack, unpack
+
+    s = workload.shape
+    tables, total = [], 0
+    for t in workload.src_tables:
+        if total + len(t) > budget_blocks and tables:
+            break
+        tables.append(len(t))
+        total += len(t)
+    pool = total + 64
+    rng = np.random.default_rng(seed)
+    src_ids = rng.permutation(pool)[:total]
+    dst_ids = rng.permutation(pool)[:total]
+    np_dtype = {1: np.uint8, 2: np.uint16, 4: np.float32}[s.elem_bytes]
+    shape = (pool * s.block_size, s.kv_heads, s.head_dim)
+    t0 = time.perf_counter()
+    src_k = [np.full(shape, l + 1, dtype=np_dtype) for l in range(s.layers)]
+    src_v = [np.full(shape, 100 + l, dtype=np_dtype) for l in range(s.layers)]
+    dst_k = [np.full(shape, 0, dtype=np_dtype) for _ in range(s.layers)]
+    dst_v = [np.full(shape, 0, dtype=np_dtype) for _ in range(s.layers)]
+    log(f"[bench] cpu baseline: host pools of {pool} blocks ready in "
+        f"{time.perf_counter() - t0:.1f} s; {len(tables)} requests, {total} blocks")
+    src = LayeredSlotCopier(src_k, src_v, s.block_size)
+    dst = LayeredSlotCopier(dst_k, dst_v, s.block_size)
+    t0 = time.perf_counter()
+    at = 0
+    for n in tables:
+        payloads = pack(src, src_ids[at:at + n])           # disaggregated.py:50
+        unpack(dst, dst_ids[at:at + n], payloads)           # disaggregated.py:81-82
+        at += n
+    elapsed = time.perf_counter() - t0
+    payload = total * s.block_bytes
+    ok = all(dst_k[l][int(dst_ids[0]) * s.block_size, 0, 0] == l + 1 for l in range(s.layers))
+    gbs = 2 * payload / elapsed / 1e9
+    log(f"[bench] cpu baseline: {2 * payload / 1e9:.2f} GB in {elapsed:.2f} s = {gbs:.3f} GB/s")
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "seconds": round(elapsed, 2), "checked": bool(ok),
+            "ms_per_request": round(1000 * elapsed / len(tables), 3),
+            "blocks_per_s": round(total / elapsed, 1),
+            "sample": (f"{workload.name} shape, first {len(tables)} requests ({total} blocks, "
+                       f"{payload / 1e9:.2f} GB payload) on {pool}-block host pools with random "
+                       f"src/dst ids; NumPy restatement of copier.py:18-31 driven as "
+                       f"disaggregated.py:50,81-82; 1 of {os.cpu_count()} host cores")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg3", help="cfg1..cfg5 (headline: cfg3)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--legs", default="direct,pack_unpack,batched")
+    ap.add_argument("--cpu-blocks", type=int, default=1536,
+                    help="blocks in the CPU-baseline sample (0 skips it)")
+    ap.add_argument("--no-verify", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the KV handoff runs on a single MI355X here "
+              "(both pools in one HBM); multi-GPU runs are not part of this build.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from iekv import _native
+    from iekv import workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    device = torch.device("cuda", 0)
+    _native.lib()
+    w = workloads.make(args.config, args.seed)
+    log(f"[bench] {w.name}: {w.num_requests} requests, {w.num_blocks} blocks, "
+        f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B")
+    legs = Legs(w, device, args.seed)
+    P = w.payload_bytes
+    names = [x for x in args.legs.split(",") if x]
+    results: dict = {}
+    verified: dict = {}
+    primary = None
+    for name in names:
+        step = getattr(legs, name)
+        legs.clear_dst()
+        ms, wall, launches = time_leg(legs, step, args.steps, args.warmup)
+        nbytes = 4 * P if name == "pack_unpack" else 2 * P
+        res, kgbs, avg_us, avg_bytes = summarize(legs, name, ms, launches, nbytes, args.steps)
+        res["wall_s"] = round(wall, 3)
+        if name == "pack_unpack":
+            res["effective_handoff_GBps"] = round(2 * P / (ms * 1e-3) / 1e9, 1)
+        if not args.no_verify:
+            verified[name] = legs.verify()
+            log(f"[bench] {name}: destination tiles equal source tiles: {verified[name]}")
+        results[name] = res
+        if primary is None:
+            primary = (name, ms, res, kgbs, avg_us, avg_bytes)
+
+    cpu = None
+    if args.cpu_blocks > 0:
+        cpu = cpu_baseline(w, args.cpu_blocks, args.seed)
+
+    name, ms, res, kgbs, avg_us, avg_bytes = primary
+    value = 2 * P / (ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{w.name}: {w.description}",
+            "leg": name,
+            "layers": w.shape.layers, "kv_heads": w.shape.kv_heads,
+            "head_dim": w.shape.head_dim, "block_size": w.shape.block_size,
+            "kv_dtype": w.shape.dtype, "requests": w.num_requests, "blocks": w.num_blocks,
+            "payload_bytes": P, "tile_bytes": w.shape.tile_bytes,
+            "launch": _native.get_launch(),
+        },
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "blocks_per_s": res["blocks_per_s"],
+        "ms_per_request": res.get("ms_per_request"),
+        "legs": results,
+        "verified": verified,
+        "roofline": {"bound": "hbm", "achieved": round(kgbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "kv_move (direct)", "avg_launch_us": round(avg_us, 2),
+                     "algorithmic_bytes_per_launch": int(avg_bytes)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if all(verified.values()) else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,146 @@
+/*
+ * iekv.h — C-ABI of the MI355X (gfx950) KV-cache handoff library, libiekv.so.
+ *
+ * The reference engine (kuluruvineeth/inference-engine) moves KV bytes only in
+ * Python: LayeredSlotCopier.read_block / write_block (ie/engine/copier.py:18-31)
+ * behind the SlotCopier protocol (ie/core/offload.py:8-11), driven per block by
+ * PrefillWorker.prefill (ie/serve/disaggregated.py:50), DecodeWorker.admit
+ * (ie/serve/disaggregated.py:81-82), BlockManager._forget (offload,
+ * ie/core/block_manager.py:82) and BlockManager.allocate (restore,
+ * ie/core/block_manager.py:159-162). Each entry point below replaces one of
+ * those loops with one batched launch; the comment on each names the lines.
+ *
+ * Data model.
+ *   A pool is the paged KV cache of one engine: 2L arrays (K of layers 0..L-1,
+ *   then V of layers 0..L-1), each [num_blocks * block_size, H, D] contiguous,
+ *   exactly the reference's per-layer caches (ie/kernels/reference.py:39-42,
+ *   ie/kernels/torch_backend.py:6-10). Block b of array a is the contiguous
+ *   tile [b*T, (b+1)*T) bytes of that array, T = block_size*H*D*elem_bytes
+ *   (the slice copier.py:14-16 takes).
+ *   A staging buffer is block-major [n_blocks][2L][T] bytes: entry i holds the
+ *   2L tiles of the i-th listed block, K layers first, then V layers — the
+ *   byte image of the reference payload ([K_0..K_{L-1}], [V_0..V_{L-1}])
+ *   (copier.py:21-22).
+ *   Block ids are int32 in DEVICE memory. Callers validate them against the
+ *   pool size before a call; kernels skip a tile whose id is out of range so
+ *   a bad id can never address memory outside the pool.
+ *   All copies are raw bytes: fp32/fp16/bf16/fp8/int8 caches move bit-exactly.
+ *
+ * Errors. Every function returns IEKV_OK (0) or a negative IEKV_ERR_* code,
+ * and iekv_last_error() describes the last failure on the calling thread.
+ * Argument errors are detected before anything is enqueued.
+ *
+ * Streams. Work is enqueued on the hipStream_t the caller passes (typically
+ * torch.cuda.current_stream().cuda_stream); nothing synchronizes the host.
+ * The library must run on the HIP runtime the caller's streams belong to:
+ * load it into a process after that runtime (e.g. after `import torch`).
+ */
+#ifndef IEKV_H_
+#define IEKV_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IEKV_ABI_VERSION 1
+
+enum {
+  IEKV_OK = 0,
+  IEKV_ERR_INVALID = -1, /* bad argument (null pointer, size, alignment, overlap) */
+  IEKV_ERR_HIP = -2,     /* a HIP runtime call failed */
+  IEKV_ERR_CAPACITY = -3 /* a buffer is too small for the requested blocks */
+};
+
+/* Opaque handle describing one paged pool: the base address of each of its
+ * 2L arrays, the tile size and the number of blocks. Registering a pool once
+ * replaces the reference's per-call walk over the `k_caches`/`v_caches` lists
+ * that LayeredSlotCopier keeps (ie/engine/copier.py:7-12). */
+typedef struct iekv_pool iekv_pool;
+
+/* ABI version of the loaded library (IEKV_ABI_VERSION). */
+int iekv_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* iekv_last_error(void);
+
+/* Register a pool. `array_ptrs` is a HOST array of n_arrays device addresses
+ * (K arrays then V arrays), each array holding num_blocks tiles of tile_bytes.
+ * If the arrays are equally spaced (one slab) the handle stores base+stride;
+ * otherwise the address table is uploaded once to `device`.
+ * Replaces: LayeredSlotCopier.__init__ (ie/engine/copier.py:7-12). */
+int iekv_pool_create(const uint64_t* array_ptrs, int32_t n_arrays, int64_t tile_bytes,
+                     int64_t num_blocks, int32_t device, iekv_pool** out);
+
+/* Release a pool handle (not the arrays it describes). */
+int iekv_pool_destroy(iekv_pool* pool);
+
+/* Direct pool-to-pool handoff: for i < n_blocks and every array a, copy tile
+ * src_ids[i] of src array a onto tile dst_ids[i] of dst array a. No staging.
+ * Both pools must have the same n_arrays and tile_bytes.
+ * Replaces: the composition of disaggregated.py:50 (read_block per src block)
+ * and disaggregated.py:81-82 (write_block per dst block), i.e. copier.py:18-31
+ * without materialising the payloads. */
+int iekv_copy_direct(const iekv_pool* src, const iekv_pool* dst, const int32_t* src_ids,
+                     const int32_t* dst_ids, int32_t n_blocks, hipStream_t stream);
+
+/* Fused multi-layer pack (gather): staging[i][a] = tile src_ids[i] of array a.
+ * `staging` is device memory of at least n_blocks*n_arrays*tile_bytes bytes.
+ * Replaces: `[copier.read_block(b) for b in seq.block_table]`
+ * (ie/serve/disaggregated.py:50 over ie/engine/copier.py:18-22). */
+int iekv_pack(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+              void* staging, int64_t staging_bytes, hipStream_t stream);
+
+/* Unpack (scatter): tile dst_ids[i] of array a = staging[i][a].
+ * Replaces: `for block_id, payload in zip(...): copier.write_block(...)`
+ * (ie/serve/disaggregated.py:81-82 over ie/engine/copier.py:24-31), and the
+ * single-block restore write (ie/core/block_manager.py:162). */
+int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                const void* staging, int64_t staging_bytes, hipStream_t stream);
+
+/* Offload to host: pack the blocks chunk by chunk into the device staging
+ * buffer (two slots when it holds at least two blocks, else one) on
+ * `compute`, and copy each packed chunk to host_dst with hipMemcpyAsync on
+ * `copy`, so the pack of chunk k+1 overlaps the device-to-host copy of chunk
+ * k. host_dst receives the block-major image [n_blocks][2L][T]; it should be
+ * pinned host memory for the copies to be asynchronous. On return `compute`
+ * is ordered after every copy (so the staging buffer and host_dst are free /
+ * complete once `compute` reaches that point). `copy` may equal `compute`.
+ * Replaces: the payload read of the offload hook,
+ * `tier.admit(hash, tokens, copier.read_block(id))` (ie/core/block_manager.py:82),
+ * batched over many blocks. */
+int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                 void* host_dst, int64_t host_bytes, void* staging, int64_t staging_bytes,
+                 hipStream_t compute, hipStream_t copy);
+
+/* Restore from host: hipMemcpyAsync chunk k of host_src into a staging slot on
+ * `copy` while `compute` unpacks chunk k-1, then unpack onto dst_ids. On
+ * return `copy` is ordered after the last unpack, so the staging buffer may be
+ * reused by later work on either stream.
+ * Replaces: the restore write of a tier hit, `copier.write_block(block.id,
+ * entry[1])` (ie/core/block_manager.py:159-162), batched over many blocks. */
+int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                 const void* host_src, int64_t host_bytes, void* staging, int64_t staging_bytes,
+                 hipStream_t compute, hipStream_t copy);
+
+/* Launch shape of the move kernels (process-wide):
+ *   run_blocks  blocks per workgroup run, 1..64; 0 = automatic (about 128 KiB
+ *               of tiles per workgroup); -1 keeps the current setting;
+ *   unroll      16-byte accesses in flight per lane per step: 4, 8 or 16;
+ *               0 keeps the current setting;
+ *   nontemporal 1 for streaming (non-temporal) loads and stores, 0 for
+ *               ordinary ones, -1 keeps the current setting.
+ * No reference counterpart: a tuning knob for the launches the entry points
+ * above make. */
+int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal);
+
+/* Current launch shape, for reporting. */
+int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IEKV_H_ */

@@ -1,0 +1,600 @@
+// kv_handoff.hip — gfx950 (MI355X) kernels and C-ABI for the paged KV-cache
+// handoff: direct pool-to-pool copy, fused multi-layer pack, unpack, and the
+// chunked host offload / restore pipelines. The ABI is declared in iekv.h.
+//
+// All three device-side moves are one kernel template, kv_move<>, that differs
+// only in where a tile comes from and where it goes:
+//   direct : pool[a][src_ids[i]]  ->  pool[a][dst_ids[i]]
+//   pack   : pool[a][src_ids[i]]  ->  staging[i][a]
+//   unpack : staging[i][a]        ->  pool[a][dst_ids[i]]
+// One workgroup owns one (array a, run of up to `run` consecutive list
+// entries): it stages the run's block ids in LDS, then streams each tile with
+// wavefront-contiguous 16-byte loads and stores (every lane moves 16 B per
+// access, a wave64 covers 1 KiB, a workgroup 4 KiB per access step), keeping
+// `U` loads per lane in flight before the matching stores. The data is never
+// interpreted: it moves as 32-bit words, so every KV dtype is bit-exact.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "iekv.h"
+
+struct iekv_pool {
+  int32_t device;
+  int32_t n_arrays;
+  int64_t tile_bytes;
+  int64_t num_blocks;
+  uint64_t base;    // slab mode: array a starts at base + a * stride
+  int64_t stride;
+  uint64_t* table;  // table mode: device copy of the n_arrays base addresses (else null)
+  int32_t align;    // largest power of two <= 16 dividing tile_bytes and every base address
+};
+
+namespace {
+
+constexpr int kThreads = 256;  // four wave64 per workgroup
+constexpr int kMaxRun = 64;    // block ids staged in LDS per workgroup
+constexpr int64_t kMaxTileBytes = int64_t(1) << 30;
+constexpr int64_t kAutoRunBytes = int64_t(128) << 10;
+
+thread_local std::string g_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+#define IEKV_HIP(expr)                                                                   \
+  do {                                                                                   \
+    hipError_t err_ = (expr);                                                            \
+    if (err_ != hipSuccess)                                                              \
+      return set_error(IEKV_ERR_HIP, "%s: %s", #expr, hipGetErrorString(err_));          \
+  } while (0)
+
+std::atomic<int> g_run{0};       // 0 = automatic
+std::atomic<int> g_unroll{8};
+std::atomic<int> g_nontemporal{1};
+
+// ---------------------------------------------------------------------------
+// Device side
+// ---------------------------------------------------------------------------
+
+struct PoolView {
+  const uint64_t* table;
+  uint64_t base;
+  int64_t stride;
+  int64_t num_blocks;
+};
+
+PoolView view_of(const iekv_pool* p) {
+  PoolView v{};
+  if (p) {
+    v.table = p->table;
+    v.base = p->base;
+    v.stride = p->stride;
+    v.num_blocks = p->num_blocks;
+  }
+  return v;
+}
+
+__device__ __forceinline__ char* array_base(const PoolView& p, int a) {
+  return reinterpret_cast<char*>(p.table ? p.table[a]
+                                         : p.base + static_cast<uint64_t>(a) * p.stride);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename V, bool NT>
+__device__ __forceinline__ V load_vec(const V* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+template <typename V, bool NT>
+__device__ __forceinline__ void store_vec(V* p, V v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// Move one tile of `n` vectors from s to d. Lane t handles vectors
+// t, t+256, ..., issuing U loads before the U stores that consume them.
+template <typename V, int U, bool NT>
+__device__ __forceinline__ void move_tile(const V* __restrict__ s, V* __restrict__ d, int n) {
+  const int t = threadIdx.x;
+  int v = t;
+  const int full = n - (U - 1) * kThreads;  // v < full: all U vectors of the step are in range
+  for (; v < full; v += U * kThreads) {
+    V r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) r[u] = load_vec<V, NT>(s + v + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < U; ++u) store_vec<V, NT>(d + v + u * kThreads, r[u]);
+  }
+  if (v < n) {
+    V r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (v + u * kThreads < n) r[u] = load_vec<V, NT>(s + v + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (v + u * kThreads < n) store_vec<V, NT>(d + v + u * kThreads, r[u]);
+  }
+}
+
+// One workgroup per (array a, run of list entries [first, first+count)).
+// blockIdx.x = run_index * n_arrays + a, so neighbouring workgroups (which the
+// dispatcher spreads over the eight XCDs) work on different arrays of the
+// same blocks and their streams land in unrelated HBM pages.
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+__global__ void __launch_bounds__(kThreads)
+kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
+        char* __restrict__ dst_stage, const int32_t* __restrict__ src_ids,
+        const int32_t* __restrict__ dst_ids, int32_t tile_vecs, int32_t n_blocks,
+        int32_t n_arrays, int32_t run) {
+  __shared__ int32_t s_src[kMaxRun];
+  __shared__ int32_t s_dst[kMaxRun];
+  const int a = blockIdx.x % n_arrays;
+  const int first = (blockIdx.x / n_arrays) * run;
+  const int count = min(run, n_blocks - first);
+  const int t = threadIdx.x;
+  if (t < count) {
+    if constexpr (SRC_POOL) s_src[t] = src_ids[first + t];
+    if constexpr (DST_POOL) s_dst[t] = dst_ids[first + t];
+  }
+  __syncthreads();
+
+  const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
+  const char* src_arr = nullptr;
+  char* dst_arr = nullptr;
+  if constexpr (SRC_POOL) src_arr = array_base(src, a);
+  if constexpr (DST_POOL) dst_arr = array_base(dst, a);
+
+  for (int j = 0; j < count; ++j) {
+    const char* s;
+    char* d;
+    if constexpr (SRC_POOL) {
+      const int32_t id = s_src[j];
+      if (id < 0 || id >= src.num_blocks) continue;  // never address outside the pool
+      s = src_arr + id * tile_bytes;
+    } else {
+      s = src_stage + (static_cast<int64_t>(first + j) * n_arrays + a) * tile_bytes;
+    }
+    if constexpr (DST_POOL) {
+      const int32_t id = s_dst[j];
+      if (id < 0 || id >= dst.num_blocks) continue;
+      d = dst_arr + id * tile_bytes;
+    } else {
+      d = dst_stage + (static_cast<int64_t>(first + j) * n_arrays + a) * tile_bytes;
+    }
+    move_tile<V, U, NT>(reinterpret_cast<const V*>(s), reinterpret_cast<V*>(d), tile_vecs);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+using MoveKernel = void (*)(PoolView, PoolView, const char*, char*, const int32_t*,
+                            const int32_t*, int32_t, int32_t, int32_t, int32_t);
+
+template <bool SP, bool DP>
+MoveKernel pick_kernel(int align, int unroll, bool nt, int* vec_bytes) {
+  if (align >= 16) {
+    *vec_bytes = 16;
+    if (nt) {
+      if (unroll >= 16) return kv_move<u32x4, 16, true, SP, DP>;
+      if (unroll >= 8) return kv_move<u32x4, 8, true, SP, DP>;
+      return kv_move<u32x4, 4, true, SP, DP>;
+    }
+    if (unroll >= 16) return kv_move<u32x4, 16, false, SP, DP>;
+    if (unroll >= 8) return kv_move<u32x4, 8, false, SP, DP>;
+    return kv_move<u32x4, 4, false, SP, DP>;
+  }
+  if (align >= 8) { *vec_bytes = 8; return kv_move<u32x2, 4, false, SP, DP>; }
+  if (align >= 4) { *vec_bytes = 4; return kv_move<uint32_t, 4, false, SP, DP>; }
+  if (align >= 2) { *vec_bytes = 2; return kv_move<uint16_t, 4, false, SP, DP>; }
+  *vec_bytes = 1;
+  return kv_move<uint8_t, 4, false, SP, DP>;
+}
+
+int align_of_ptr(uint64_t p) {
+  int a = 16;
+  while (a > 1 && (p % a)) a >>= 1;
+  return a;
+}
+
+// Makes `device` current for the lifetime of the guard and restores the
+// caller's device afterwards.
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int device) {
+    ok_ = hipGetDevice(&prev_) == hipSuccess;
+    if (ok_ && prev_ != device) ok_ = hipSetDevice(device) == hipSuccess;
+    switched_ = ok_ && prev_ != device;
+  }
+  ~DeviceGuard() {
+    if (switched_) (void)hipSetDevice(prev_);
+  }
+  bool ok() const { return ok_; }
+
+ private:
+  int prev_ = 0;
+  bool ok_ = false;
+  bool switched_ = false;
+};
+
+int auto_run(int64_t tile_bytes) {
+  int64_t r = (kAutoRunBytes + tile_bytes - 1) / tile_bytes;
+  return static_cast<int>(std::min<int64_t>(std::max<int64_t>(r, 1), kMaxRun));
+}
+
+template <bool SP, bool DP>
+int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage, char* dst_stage,
+                const int32_t* src_ids, const int32_t* dst_ids, int32_t n_blocks,
+                int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream) {
+  if (n_blocks == 0) return IEKV_OK;
+  const int run_setting = g_run.load();
+  const int run = run_setting > 0 ? run_setting : auto_run(tile_bytes);
+  const int64_t runs = (static_cast<int64_t>(n_blocks) + run - 1) / run;
+  const int64_t grid = runs * n_arrays;
+  if (grid > INT32_MAX)
+    return set_error(IEKV_ERR_INVALID, "launch of %lld workgroups exceeds the grid limit",
+                     static_cast<long long>(grid));
+  int vec = 16;
+  MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), g_nontemporal.load() != 0, &vec);
+  const int32_t tile_vecs = static_cast<int32_t>(tile_bytes / vec);
+  hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
+                     view_of(sp), view_of(dp), src_stage, dst_stage, src_ids, dst_ids,
+                     tile_vecs, n_blocks, n_arrays, run);
+  IEKV_HIP(hipGetLastError());
+  return IEKV_OK;
+}
+
+int check_pool(const iekv_pool* p, const char* what) {
+  if (!p) return set_error(IEKV_ERR_INVALID, "%s pool is null", what);
+  return IEKV_OK;
+}
+
+int check_ids(const int32_t* ids, int32_t n_blocks, const char* what) {
+  if (n_blocks < 0) return set_error(IEKV_ERR_INVALID, "n_blocks is negative (%d)", n_blocks);
+  if (n_blocks > 0 && !ids) return set_error(IEKV_ERR_INVALID, "%s ids are null", what);
+  return IEKV_OK;
+}
+
+int check_buffer(const void* buf, int64_t bytes, int64_t need, const char* what) {
+  if (need > 0 && !buf) return set_error(IEKV_ERR_INVALID, "%s buffer is null", what);
+  if (bytes < need)
+    return set_error(IEKV_ERR_CAPACITY, "%s buffer holds %lld bytes, %lld needed", what,
+                     static_cast<long long>(bytes), static_cast<long long>(need));
+  return IEKV_OK;
+}
+
+// Bytes of n block images of pool p, or -1 on overflow.
+int64_t image_bytes(const iekv_pool* p, int64_t n) {
+  const int64_t block = p->tile_bytes * p->n_arrays;
+  if (n > 0 && block > INT64_MAX / n) return -1;
+  return block * n;
+}
+
+// A small set of events that lives for one pipeline call.
+class Events {
+ public:
+  int create(int n) {
+    ev_.assign(n, nullptr);
+    for (auto& e : ev_) IEKV_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    return IEKV_OK;
+  }
+  ~Events() {
+    for (auto e : ev_)
+      if (e) (void)hipEventDestroy(e);
+  }
+  hipEvent_t operator[](int i) const { return ev_[i]; }
+
+ private:
+  std::vector<hipEvent_t> ev_;
+};
+
+// Staging slots for a pipeline: two when the buffer holds two blocks or more.
+void plan_slots(int64_t staging_bytes, int64_t block_bytes, int32_t n_blocks, int* n_slots,
+                int64_t* slot_blocks) {
+  int64_t fit = staging_bytes / block_bytes;
+  *n_slots = fit >= 2 ? 2 : 1;
+  *slot_blocks = std::min<int64_t>(fit / *n_slots, n_blocks);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+
+extern "C" {
+
+int iekv_abi_version(void) { return IEKV_ABI_VERSION; }
+
+const char* iekv_last_error(void) { return g_error.c_str(); }
+
+int iekv_pool_create(const uint64_t* array_ptrs, int32_t n_arrays, int64_t tile_bytes,
+                     int64_t num_blocks, int32_t device, iekv_pool** out) {
+  if (!out) return set_error(IEKV_ERR_INVALID, "out is null");
+  *out = nullptr;
+  if (!array_ptrs) return set_error(IEKV_ERR_INVALID, "array_ptrs is null");
+  if (n_arrays <= 0 || n_arrays > 65536)
+    return set_error(IEKV_ERR_INVALID, "n_arrays %d out of range", n_arrays);
+  if (tile_bytes <= 0 || tile_bytes > kMaxTileBytes)
+    return set_error(IEKV_ERR_INVALID, "tile_bytes %lld out of range",
+                     static_cast<long long>(tile_bytes));
+  if (num_blocks <= 0 || num_blocks > INT32_MAX)
+    return set_error(IEKV_ERR_INVALID, "num_blocks %lld out of range",
+                     static_cast<long long>(num_blocks));
+  if (num_blocks > INT64_MAX / tile_bytes)
+    return set_error(IEKV_ERR_INVALID, "pool size overflows");
+  const int64_t array_bytes = num_blocks * tile_bytes;
+
+  int align = 16;
+  while (align > 1 && (tile_bytes % align)) align >>= 1;
+  for (int32_t a = 0; a < n_arrays; ++a) {
+    if (!array_ptrs[a]) return set_error(IEKV_ERR_INVALID, "array %d address is null", a);
+    align = std::min(align, align_of_ptr(array_ptrs[a]));
+  }
+
+  // Arrays must not overlap: every byte of every tile belongs to one array.
+  std::vector<uint64_t> sorted(array_ptrs, array_ptrs + n_arrays);
+  std::sort(sorted.begin(), sorted.end());
+  for (int32_t a = 1; a < n_arrays; ++a)
+    if (sorted[a] - sorted[a - 1] < static_cast<uint64_t>(array_bytes))
+      return set_error(IEKV_ERR_INVALID, "pool arrays overlap (%d arrays of %lld bytes)",
+                       n_arrays, static_cast<long long>(array_bytes));
+
+  bool slab = true;
+  int64_t stride = array_bytes;
+  if (n_arrays > 1) {
+    if (array_ptrs[1] <= array_ptrs[0]) {
+      slab = false;
+    } else {
+      stride = static_cast<int64_t>(array_ptrs[1] - array_ptrs[0]);
+      for (int32_t a = 2; a < n_arrays && slab; ++a)
+        slab = array_ptrs[a] == array_ptrs[0] + static_cast<uint64_t>(a) * stride;
+    }
+  }
+
+  iekv_pool* p = new (std::nothrow) iekv_pool{};
+  if (!p) return set_error(IEKV_ERR_INVALID, "out of host memory");
+  p->device = device;
+  p->n_arrays = n_arrays;
+  p->tile_bytes = tile_bytes;
+  p->num_blocks = num_blocks;
+  p->align = align;
+  if (slab) {
+    p->base = array_ptrs[0];
+    p->stride = stride;
+  } else {
+    DeviceGuard guard(device);
+    if (!guard.ok()) {
+      delete p;
+      return set_error(IEKV_ERR_HIP, "cannot make device %d current", device);
+    }
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->table), sizeof(uint64_t) * n_arrays);
+    if (e == hipSuccess)
+      e = hipMemcpy(p->table, array_ptrs, sizeof(uint64_t) * n_arrays, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      if (p->table) (void)hipFree(p->table);
+      delete p;
+      return set_error(IEKV_ERR_HIP, "uploading the pool address table: %s",
+                       hipGetErrorString(e));
+    }
+  }
+  *out = p;
+  return IEKV_OK;
+}
+
+int iekv_pool_destroy(iekv_pool* pool) {
+  if (!pool) return IEKV_OK;
+  int rc = IEKV_OK;
+  if (pool->table) {
+    DeviceGuard guard(pool->device);
+    hipError_t e = hipFree(pool->table);
+    if (e != hipSuccess) rc = set_error(IEKV_ERR_HIP, "hipFree: %s", hipGetErrorString(e));
+  }
+  delete pool;
+  return rc;
+}
+
+int iekv_copy_direct(const iekv_pool* src, const iekv_pool* dst, const int32_t* src_ids,
+                     const int32_t* dst_ids, int32_t n_blocks, hipStream_t stream) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_pool(dst, "destination"))) return rc;
+  if ((rc = check_ids(src_ids, n_blocks, "source")) ||
+      (rc = check_ids(dst_ids, n_blocks, "destination")))
+    return rc;
+  if (src->n_arrays != dst->n_arrays || src->tile_bytes != dst->tile_bytes)
+    return set_error(IEKV_ERR_INVALID,
+                     "pools differ in shape: %d arrays x %lld B vs %d arrays x %lld B",
+                     src->n_arrays, static_cast<long long>(src->tile_bytes), dst->n_arrays,
+                     static_cast<long long>(dst->tile_bytes));
+  if (src->device != dst->device)
+    return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
+                     dst->device);
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  return launch_move<true, true>(src, dst, nullptr, nullptr, src_ids, dst_ids, n_blocks,
+                                 src->tile_bytes, src->n_arrays,
+                                 std::min(src->align, dst->align), stream);
+}
+
+int iekv_pack(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, void* staging,
+              int64_t staging_bytes, hipStream_t stream) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_ids(src_ids, n_blocks, "source")))
+    return rc;
+  const int64_t need = image_bytes(src, n_blocks);
+  if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
+  if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  const int align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  return launch_move<true, false>(src, nullptr, nullptr, static_cast<char*>(staging), src_ids,
+                                  nullptr, n_blocks, src->tile_bytes, src->n_arrays, align,
+                                  stream);
+}
+
+int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                const void* staging, int64_t staging_bytes, hipStream_t stream) {
+  int rc;
+  if ((rc = check_pool(dst, "destination")) ||
+      (rc = check_ids(dst_ids, n_blocks, "destination")))
+    return rc;
+  const int64_t need = image_bytes(dst, n_blocks);
+  if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
+  if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
+  DeviceGuard guard(dst->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+  const int align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  return launch_move<false, true>(nullptr, dst, static_cast<const char*>(staging), nullptr,
+                                  nullptr, dst_ids, n_blocks, dst->tile_bytes, dst->n_arrays,
+                                  align, stream);
+}
+
+int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                 void* host_dst, int64_t host_bytes, void* staging, int64_t staging_bytes,
+                 hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_ids(src_ids, n_blocks, "source")))
+    return rc;
+  const int64_t need = image_bytes(src, n_blocks);
+  if (need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
+  if ((rc = check_buffer(host_dst, host_bytes, need, "host"))) return rc;
+  const int64_t block_bytes = image_bytes(src, 1);
+  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
+    return rc;
+  if (n_blocks == 0) return IEKV_OK;
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+
+  int n_slots;
+  int64_t slot_blocks;
+  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
+  const int align =
+      std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  Events packed, copied, fence;
+  if ((rc = packed.create(n_slots)) || (rc = copied.create(n_slots)) || (rc = fence.create(1)))
+    return rc;
+
+  // Entry fence: the copy stream must not read staging before the compute
+  // stream's earlier work on it has finished.
+  IEKV_HIP(hipEventRecord(fence[0], compute));
+  IEKV_HIP(hipStreamWaitEvent(copy, fence[0], 0));
+
+  char* host = static_cast<char*>(host_dst);
+  char* stage = static_cast<char*>(staging);
+  int last = 0;
+  for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
+    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
+    const int s = static_cast<int>(k % n_slots);
+    char* slot = stage + s * slot_blocks * block_bytes;
+    if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(compute, copied[s], 0));
+    if ((rc = launch_move<true, false>(src, nullptr, nullptr, slot, src_ids + first, nullptr,
+                                       cnt, src->tile_bytes, src->n_arrays, align, compute)))
+      return rc;
+    IEKV_HIP(hipEventRecord(packed[s], compute));
+    IEKV_HIP(hipStreamWaitEvent(copy, packed[s], 0));
+    IEKV_HIP(hipMemcpyAsync(host + first * block_bytes, slot, cnt * block_bytes,
+                            hipMemcpyDeviceToHost, copy));
+    IEKV_HIP(hipEventRecord(copied[s], copy));
+    last = s;
+  }
+  // Later compute-stream work (reuse of staging, reads of host_dst after a
+  // sync of `compute`) is ordered after the last device-to-host copy.
+  IEKV_HIP(hipStreamWaitEvent(compute, copied[last], 0));
+  return IEKV_OK;
+}
+
+int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                 const void* host_src, int64_t host_bytes, void* staging, int64_t staging_bytes,
+                 hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if ((rc = check_pool(dst, "destination")) ||
+      (rc = check_ids(dst_ids, n_blocks, "destination")))
+    return rc;
+  const int64_t need = image_bytes(dst, n_blocks);
+  if (need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
+  if ((rc = check_buffer(host_src, host_bytes, need, "host"))) return rc;
+  const int64_t block_bytes = image_bytes(dst, 1);
+  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
+    return rc;
+  if (n_blocks == 0) return IEKV_OK;
+  DeviceGuard guard(dst->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+
+  int n_slots;
+  int64_t slot_blocks;
+  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
+  const int align =
+      std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  Events loaded, unpacked, fence;
+  if ((rc = loaded.create(n_slots)) || (rc = unpacked.create(n_slots)) || (rc = fence.create(1)))
+    return rc;
+
+  // Entry fence: the copy stream must not overwrite staging while earlier
+  // compute-stream work still reads it.
+  IEKV_HIP(hipEventRecord(fence[0], compute));
+  IEKV_HIP(hipStreamWaitEvent(copy, fence[0], 0));
+
+  const char* host = static_cast<const char*>(host_src);
+  char* stage = static_cast<char*>(staging);
+  int last = 0;
+  for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
+    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
+    const int s = static_cast<int>(k % n_slots);
+    char* slot = stage + s * slot_blocks * block_bytes;
+    if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(copy, unpacked[s], 0));
+    IEKV_HIP(hipMemcpyAsync(slot, host + first * block_bytes, cnt * block_bytes,
+                            hipMemcpyHostToDevice, copy));
+    IEKV_HIP(hipEventRecord(loaded[s], copy));
+    IEKV_HIP(hipStreamWaitEvent(compute, loaded[s], 0));
+    if ((rc = launch_move<false, true>(nullptr, dst, slot, nullptr, nullptr, dst_ids + first,
+                                       cnt, dst->tile_bytes, dst->n_arrays, align, compute)))
+      return rc;
+    IEKV_HIP(hipEventRecord(unpacked[s], compute));
+    last = s;
+  }
+  // Later copy-stream work that writes staging is ordered after the last unpack.
+  IEKV_HIP(hipStreamWaitEvent(copy, unpacked[last], 0));
+  return IEKV_OK;
+}
+
+int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal) {
+  if (run_blocks < -1 || run_blocks > kMaxRun)
+    return set_error(IEKV_ERR_INVALID, "run_blocks %d out of range", run_blocks);
+  if (unroll != 0 && unroll != 4 && unroll != 8 && unroll != 16)
+    return set_error(IEKV_ERR_INVALID, "unroll must be 4, 8 or 16 (got %d)", unroll);
+  if (nontemporal < -1 || nontemporal > 1)
+    return set_error(IEKV_ERR_INVALID, "nontemporal must be -1, 0 or 1 (got %d)", nontemporal);
+  if (run_blocks >= 0) g_run.store(run_blocks);
+  if (unroll) g_unroll.store(unroll);
+  if (nontemporal >= 0) g_nontemporal.store(nontemporal);
+  return IEKV_OK;
+}
+
+int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal) {
+  if (run_blocks) *run_blocks = g_run.load();
+  if (unroll) *unroll = g_unroll.load();
+  if (nontemporal) *nontemporal = g_nontemporal.load();
+  return IEKV_OK;
+}
+
+}  // extern "C"

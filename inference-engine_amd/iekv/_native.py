@@ -1,0 +1,129 @@
+"""ctypes binding of libiekv.so, the HIP KV-handoff library (C-ABI in include/iekv.h).
+
+Loading imports torch first, so the library binds to the HIP runtime torch
+already uses and torch's streams are valid handles for it. There is no
+fallback: if the library is missing or fails to load, :func:`lib` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_p
+from pathlib import Path
+
+LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
+ABI_VERSION = 1
+
+IEKV_OK = 0
+IEKV_ERR_INVALID = -1
+IEKV_ERR_HIP = -2
+IEKV_ERR_CAPACITY = -3
+
+# Every entry point of include/iekv.h: name -> (restype, argtypes).
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "iekv_abi_version": (c_int, []),
+    "iekv_last_error": (c_char_p, []),
+    "iekv_pool_create": (c_int, [POINTER(c_uint64), c_int32, c_int64, c_int64, c_int32,
+                                 POINTER(c_void_p)]),
+    "iekv_pool_destroy": (c_int, [c_void_p]),
+    "iekv_copy_direct": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
+    "iekv_pack": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
+    "iekv_unpack": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
+    "iekv_offload": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p, c_int64,
+                             c_void_p, c_void_p]),
+    "iekv_restore": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p, c_int64,
+                             c_void_p, c_void_p]),
+    "iekv_set_launch": (c_int, [c_int32, c_int32, c_int32]),
+    "iekv_get_launch": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class NativeError(RuntimeError):
+    """A libiekv call returned a non-zero status."""
+
+    def __init__(self, function: str, code: int, message: str) -> None:
+        super().__init__(f"{function} failed ({code}): {message}")
+        self.function = function
+        self.code = code
+
+
+def library_path() -> Path:
+    override = os.environ.get("IEKV_LIBRARY")
+    return Path(override) if override else LIBRARY
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded on first use)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    import torch  # noqa: F401  (binds the library to torch's HIP runtime)
+
+    path = library_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is missing: build it with `python -m iekv.build` or "
+            "`python -c 'import __graft_entry__ as g; g.build()'` before using the HIP path")
+    handle = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = handle.iekv_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+    _lib = handle
+    return handle
+
+
+def check(function: str, code: int) -> None:
+    if code != IEKV_OK:
+        message = lib().iekv_last_error().decode(errors="replace")
+        raise NativeError(function, code, message)
+
+
+def call(function: str, *args) -> None:
+    check(function, getattr(lib(), function)(*args))
+
+
+class Pool:
+    """A registered paged pool: 2L array base addresses, tile bytes, block count."""
+
+    def __init__(self, array_ptrs: list[int], tile_bytes: int, num_blocks: int,
+                 device: int) -> None:
+        table = (c_uint64 * len(array_ptrs))(*array_ptrs)
+        out = c_void_p()
+        call("iekv_pool_create", table, len(array_ptrs), tile_bytes, num_blocks, device,
+             ctypes.byref(out))
+        self.handle = out
+        self.n_arrays = len(array_ptrs)
+        self.tile_bytes = tile_bytes
+        self.num_blocks = num_blocks
+        self.device = device
+
+    @property
+    def block_bytes(self) -> int:
+        return self.n_arrays * self.tile_bytes
+
+    def close(self) -> None:
+        if self.handle is not None and self.handle.value and _lib is not None:
+            _lib.iekv_pool_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def set_launch(run_blocks: int = -1, unroll: int = 0, nontemporal: int = -1) -> None:
+    call("iekv_set_launch", run_blocks, unroll, nontemporal)
+
+
+def get_launch() -> dict[str, int]:
+    run, unroll, nt = c_int32(), c_int32(), c_int32()
+    call("iekv_get_launch", ctypes.byref(run), ctypes.byref(unroll), ctypes.byref(nt))
+    return {"run_blocks": run.value, "unroll": unroll.value, "nontemporal": nt.value}

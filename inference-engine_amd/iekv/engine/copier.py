@@ -1,0 +1,351 @@
+"""HIP slot copier: the reference's SlotCopier protocol over libiekv.
+
+``HipSlotCopier`` is a drop-in for ``LayeredSlotCopier`` (ie/engine/copier.py:6-38):
+``read_block(id)`` returns a snapshot payload, ``write_block(id, payload)``
+scatters one back, ``blocks_read`` / ``blocks_written`` / ``bytes_moved`` count
+exactly as the reference does. It adds the batched calls the workers use so a
+request's whole block table moves in one launch instead of ``2L`` NumPy slice
+copies per block:
+
+* ``read_blocks(ids)``  -> one fused pack launch (iekv_pack), or the pinned-host
+  offload pipeline (iekv_offload) when payloads live on the host;
+* ``write_blocks(ids, payloads)`` -> one unpack launch (iekv_unpack), or the
+  restore pipeline (iekv_restore) for host payloads;
+* ``copy_blocks(source, src_ids, dst_ids)`` -> the direct pool-to-pool launch
+  (iekv_copy_direct), which never materialises payloads.
+
+Payloads are block-major byte images ``[n, 2L, T]`` (K tiles of layers
+0..L-1, then V tiles). A single block's payload iterates as
+``(k_list, v_list)`` of ``[block_size, H, D]`` tensors, the structure of the
+reference payload (ie/engine/copier.py:21-22).
+
+All work is enqueued on torch's current stream of the pool's device (host
+copies on a side stream of the copier), so it is ordered with the model's
+cache reads and writes exactly as the reference's synchronous copies are.
+"""
+from __future__ import annotations
+
+from typing import Any, Iterable, Sequence as Seq
+
+import numpy as np
+import torch
+
+from .. import _native
+from .pools import KVPool, stream_handle
+
+# Device staging the host pipelines use: two slots of at most this many bytes.
+HOST_STAGING_BYTES = 256 << 20
+
+
+class PackedBlocks:
+    """Byte images of ``n`` blocks, ``[n, 2L, T]`` uint8, on a device or in pinned host memory.
+
+    Indexing gives a :class:`BlockPayload` (an int) or a narrower
+    :class:`PackedBlocks` (a slice); ``len`` is the number of blocks, so it
+    stands in for the reference's ``block_payloads`` list (ie/serve/disaggregated.py:50-53).
+    """
+
+    def __init__(self, data: torch.Tensor, num_layers: int, tile_shape: tuple[int, ...],
+                 dtype: torch.dtype) -> None:
+        if data.dtype != torch.uint8 or data.dim() != 3 or data.shape[1] != 2 * num_layers:
+            raise ValueError(f"packed data must be uint8 [n, {2 * num_layers}, T]")
+        self.data = data
+        self.num_layers = num_layers
+        self.tile_shape = tuple(tile_shape)
+        self.dtype = dtype
+        self._event: torch.cuda.Event | None = None  # last async copy touching host data
+
+    @property
+    def on_host(self) -> bool:
+        return self.data.device.type == "cpu"
+
+    @property
+    def tile_bytes(self) -> int:
+        return self.data.shape[2]
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel()
+
+    def __len__(self) -> int:
+        return self.data.shape[0]
+
+    def __getitem__(self, index):
+        if isinstance(index, slice):
+            view = PackedBlocks(self.data[index], self.num_layers, self.tile_shape, self.dtype)
+            view._event = self._event
+            return view
+        n = len(self)
+        if index < 0:
+            index += n
+        if not 0 <= index < n:
+            raise IndexError(f"payload {index} out of range for {n} blocks")
+        return BlockPayload(self, index)
+
+    def __iter__(self):
+        return (BlockPayload(self, i) for i in range(len(self)))
+
+    def tiles(self, index: int) -> torch.Tensor:
+        """Block ``index`` as typed tiles ``[2L, *tile_shape]`` (a view)."""
+        return self.data[index].view(self.dtype).view(2 * self.num_layers, *self.tile_shape)
+
+    def mark(self, stream: torch.cuda.Stream) -> None:
+        """Record that async copies involving this (host) buffer end on ``stream``."""
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        self._event = ev
+
+    def synchronize(self) -> "PackedBlocks":
+        """Block the host until pending copies into or out of this buffer are done."""
+        if self._event is not None:
+            self._event.synchronize()
+        elif not self.on_host:
+            torch.cuda.current_stream(self.data.device).synchronize()
+        return self
+
+    def __del__(self) -> None:
+        # Pinned memory goes back to torch's host cache when this object dies;
+        # make sure no DMA still reads or writes it by then.
+        ev = self._event
+        if ev is not None:
+            try:
+                ev.synchronize()
+            except Exception:
+                pass
+
+
+class BlockPayload:
+    """One block of a :class:`PackedBlocks`; unpacks as ``(k_list, v_list)``."""
+
+    __slots__ = ("packed", "index")
+
+    def __init__(self, packed: PackedBlocks, index: int) -> None:
+        self.packed = packed
+        self.index = index
+
+    @property
+    def k(self) -> list[torch.Tensor]:
+        tiles = self.packed.tiles(self.index)
+        return [tiles[l] for l in range(self.packed.num_layers)]
+
+    @property
+    def v(self) -> list[torch.Tensor]:
+        tiles = self.packed.tiles(self.index)
+        L = self.packed.num_layers
+        return [tiles[L + l] for l in range(L)]
+
+    def __iter__(self):
+        yield self.k
+        yield self.v
+
+    def __len__(self) -> int:
+        return 2
+
+    def __getitem__(self, i: int) -> list[torch.Tensor]:
+        return (self.k, self.v)[i]
+
+    @property
+    def nbytes(self) -> int:
+        return self.packed.data[self.index].numel()
+
+
+def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
+    """The PackedBlocks slice that ``payloads`` are consecutive entries of, if any."""
+    if isinstance(payloads, PackedBlocks):
+        return payloads
+    if not payloads or not all(isinstance(p, BlockPayload) for p in payloads):
+        return None
+    base = payloads[0].packed
+    start = payloads[0].index
+    for offset, p in enumerate(payloads):
+        if p.packed is not base or p.index != start + offset:
+            return None
+    return base[start:start + len(payloads)]
+
+
+class HipSlotCopier:
+    """SlotCopier over per-layer GPU caches, backed by the HIP handoff kernels.
+
+    ``payload_location`` chooses where ``read_block``/``read_blocks`` put
+    payloads: ``"device"`` (the disaggregation transfer, a staging buffer in
+    HBM) or ``"host"`` (the offload tier, pinned host memory).
+    """
+
+    def __init__(self, k_caches: Seq[torch.Tensor], v_caches: Seq[torch.Tensor],
+                 block_size: int, *, payload_location: str = "device") -> None:
+        if payload_location not in ("device", "host"):
+            raise ValueError("payload_location must be 'device' or 'host'")
+        self.k_caches = k_caches
+        self.v_caches = v_caches
+        self.block_size = block_size
+        self.pool = KVPool(k_caches, v_caches, block_size)
+        self.payload_location = payload_location
+        self.blocks_read = 0
+        self.blocks_written = 0
+        self._copy_stream: torch.cuda.Stream | None = None
+        self._staging: torch.Tensor | None = None
+
+    # -- helpers -------------------------------------------------------------
+    @property
+    def device(self) -> torch.device:
+        return self.pool.device
+
+    def _empty_packed(self, n: int, on_host: bool) -> PackedBlocks:
+        shape = (n, self.pool.n_arrays, self.pool.tile_bytes)
+        if on_host:
+            data = torch.empty(shape, dtype=torch.uint8, pin_memory=True)
+        else:
+            data = torch.empty(shape, dtype=torch.uint8, device=self.device)
+        return PackedBlocks(data, self.pool.num_layers, self.pool.tile_shape, self.pool.dtype)
+
+    def copy_stream(self) -> torch.cuda.Stream:
+        """The side stream host copies run on (default priority)."""
+        if self._copy_stream is None:
+            self._copy_stream = torch.cuda.Stream(self.device)
+        return self._copy_stream
+
+    def _host_staging(self, n_blocks: int) -> torch.Tensor:
+        """Device staging for the host pipelines: up to two slots, bounded size."""
+        block = self.pool.block_bytes
+        want = max(1, min(2 * n_blocks, max(2, HOST_STAGING_BYTES // block))) * block
+        if self._staging is None or self._staging.numel() < want:
+            self._staging = torch.empty(want, dtype=torch.uint8, device=self.device)
+        return self._staging
+
+    def _check_packed(self, packed: PackedBlocks) -> None:
+        if (packed.data.shape[1] != self.pool.n_arrays
+                or packed.data.shape[2] != self.pool.tile_bytes):
+            raise ValueError(
+                f"payload of {packed.data.shape[1]} tiles x {packed.data.shape[2]} B does not "
+                f"fit a pool of {self.pool.n_arrays} tiles x {self.pool.tile_bytes} B")
+        if not packed.data.is_contiguous():
+            raise ValueError("payload data must be contiguous")
+        if not packed.on_host and packed.data.device != self.device:
+            raise ValueError(f"payload on {packed.data.device}, pool on {self.device}")
+
+    def _from_tiles(self, payload: Any) -> PackedBlocks:
+        """Pack a reference-structured payload ``(k_list, v_list)`` into one block image."""
+        k_list, v_list = payload
+        tiles = list(k_list) + list(v_list)
+        if len(tiles) != self.pool.n_arrays:
+            raise ValueError(f"payload has {len(tiles)} tiles, pool needs {self.pool.n_arrays}")
+        image = self._empty_packed(1, on_host=False)
+        for a, tile in enumerate(tiles):
+            t = tile if isinstance(tile, torch.Tensor) else torch.from_numpy(np.asarray(tile))
+            if tuple(t.shape) != self.pool.tile_shape:
+                raise ValueError(f"tile {a} has shape {tuple(t.shape)}, expected "
+                                 f"{self.pool.tile_shape}")
+            raw = t.contiguous().view(-1).view(torch.uint8)
+            if raw.numel() != self.pool.tile_bytes:
+                raise ValueError(f"tile {a} has {raw.numel()} bytes, expected "
+                                 f"{self.pool.tile_bytes}")
+            image.data[0, a].copy_(raw, non_blocking=True)
+        return image
+
+    # -- SlotCopier protocol (ie/core/offload.py:8-11) ---------------------------
+    def read_block(self, block_id: int) -> BlockPayload:
+        """Snapshot of one block (ie/engine/copier.py:18-22)."""
+        return self.read_blocks([block_id])[0]
+
+    def write_block(self, block_id: int, payload: Any) -> None:
+        """Scatter one payload into ``block_id`` (ie/engine/copier.py:24-31)."""
+        self.write_blocks([block_id], [payload])
+
+    # -- batched calls -------------------------------------------------------
+    def read_blocks(self, block_ids, *, location: str | None = None) -> PackedBlocks:
+        """Pack ``block_ids`` (in order) into a new payload buffer with one launch."""
+        location = location or self.payload_location
+        ids = self.pool.block_ids(block_ids, what="source block")
+        n = ids.numel()
+        out = self._empty_packed(n, on_host=(location == "host"))
+        stream = torch.cuda.current_stream(self.device)
+        if out.on_host:
+            staging = self._host_staging(n)
+            copy = self.copy_stream()
+            _native.call("iekv_offload", self.pool.native.handle, ids.data_ptr(), n,
+                         out.data.data_ptr(), out.nbytes, staging.data_ptr(), staging.numel(),
+                         stream.cuda_stream, copy.cuda_stream)
+            out.mark(stream)
+        else:
+            _native.call("iekv_pack", self.pool.native.handle, ids.data_ptr(), n,
+                         out.data.data_ptr(), out.nbytes, stream.cuda_stream)
+        self.blocks_read += n
+        return out
+
+    def write_blocks(self, block_ids, payloads) -> None:
+        """Scatter ``payloads[i]`` into ``block_ids[i]`` for every i (one launch when possible)."""
+        ids = self.pool.block_ids(block_ids, unique=True, what="destination block")
+        n = ids.numel()
+        if len(payloads) != n:
+            raise ValueError(f"{n} destination blocks for {len(payloads)} payloads")
+        packed = _consecutive_views(payloads)
+        if packed is not None:
+            self._write_packed(ids, packed)
+        else:
+            for i, payload in enumerate(payloads):
+                one = _consecutive_views([payload]) if isinstance(payload, BlockPayload) \
+                    else self._from_tiles(payload)
+                self._write_packed(ids[i:i + 1], one)
+        self.blocks_written += n
+
+    def _write_packed(self, ids: torch.Tensor, packed: PackedBlocks) -> None:
+        self._check_packed(packed)
+        n = ids.numel()
+        stream = torch.cuda.current_stream(self.device)
+        if packed.on_host:
+            staging = self._host_staging(n)
+            copy = self.copy_stream()
+            _native.call("iekv_restore", self.pool.native.handle, ids.data_ptr(), n,
+                         packed.data.data_ptr(), packed.nbytes, staging.data_ptr(),
+                         staging.numel(), stream.cuda_stream, copy.cuda_stream)
+            packed.mark(copy)
+        else:
+            _native.call("iekv_unpack", self.pool.native.handle, ids.data_ptr(), n,
+                         packed.data.data_ptr(), packed.nbytes, stream.cuda_stream)
+
+    def copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids) -> None:
+        """Direct pool-to-pool move: tile ``src_ids[i]`` of ``source`` -> ``dst_ids[i]`` here."""
+        if not self.pool.same_shape(source.pool):
+            raise ValueError("source and destination pools differ in layout")
+        if source.device != self.device:
+            raise ValueError(f"pools on {source.device} and {self.device}")
+        src = source.pool.block_ids(src_ids, what="source block")
+        dst = self.pool.block_ids(dst_ids, unique=True, what="destination block")
+        if src.numel() != dst.numel():
+            raise ValueError(f"{src.numel()} source blocks for {dst.numel()} destinations")
+        if source is self or source.pool.native.handle.value == self.pool.native.handle.value:
+            if not isinstance(src_ids, torch.Tensor) and not isinstance(dst_ids, torch.Tensor):
+                if set(map(int, src_ids)) & set(map(int, dst_ids)):
+                    raise ValueError("a direct copy within one pool needs disjoint source "
+                                     "and destination blocks")
+        n = dst.numel()
+        stream = torch.cuda.current_stream(self.device)
+        _native.call("iekv_copy_direct", source.pool.native.handle, self.pool.native.handle,
+                     src.data_ptr(), dst.data_ptr(), n, stream.cuda_stream)
+        source.blocks_read += n
+        self.blocks_written += n
+
+    @property
+    def bytes_moved(self) -> int:
+        """(reads + writes) x 2L x T, as ie/engine/copier.py:33-38 counts."""
+        return (self.blocks_read + self.blocks_written) * self.pool.block_bytes
+
+
+def copier_for(k_caches, v_caches, block_size: int, role: str = "transfer") -> HipSlotCopier:
+    """Default copier factory of the engine: device payloads for transfers, host for offload."""
+    return HipSlotCopier(k_caches, v_caches, block_size,
+                         payload_location="host" if role == "offload" else "device")
+
+
+def stack_payloads(payloads: Iterable[BlockPayload]) -> PackedBlocks:
+    """Gather arbitrary block payloads of one layout into a new contiguous PackedBlocks."""
+    items = list(payloads)
+    if not items:
+        raise ValueError("no payloads")
+    first = items[0].packed
+    data = torch.stack([p.packed.data[p.index] for p in items])
+    return PackedBlocks(data, first.num_layers, first.tile_shape, first.dtype)
+
+
+__all__ = ["BlockPayload", "HipSlotCopier", "PackedBlocks", "copier_for", "stack_payloads",
+           "stream_handle"]

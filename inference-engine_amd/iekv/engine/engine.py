@@ -1,0 +1,117 @@
+"""The engine each disaggregation worker owns: pool, block manager, scheduler, model.
+
+Behaviour follows the reference's ``Engine`` (ie/engine/engine.py:17-127) in
+everything the handoff observes: pool allocation per layer, block
+management, scheduling, prefill/decode steps and the offload-tier wiring
+(engine.py:57-63). The copier is pluggable: by default the HIP copier
+(``iekv.engine.copier.copier_for``); any object with the reference's
+``read_block``/``write_block`` protocol can be injected via ``copier_factory``
+(signature ``factory(k_caches, v_caches, block_size, role)``, ``role`` being
+``"transfer"`` or ``"offload"``).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Callable
+
+import numpy as np
+
+from ..core.block_manager import BlockManager
+from ..core.layout import build_layout
+from ..core.offload import KVTier
+from ..core.scheduler import Scheduler
+from ..core.sequence import Sequence
+
+CopierFactory = Callable[[Any, Any, int, str], Any]
+
+
+@dataclass(slots=True)
+class EngineConfig:
+    """ie/engine/engine.py:17-25. ``capture_graphs`` is accepted and ignored here."""
+
+    block_size: int = 16
+    num_blocks: int = 1024
+    max_batch_sequences: int = 64
+    max_batch_tokens: int = 2048
+    seed: int = 0
+    offload_blocks: int = 0
+    capture_graphs: bool = False
+
+
+def sample_from_logits(logits: np.ndarray, temperatures: np.ndarray,
+                       generator: np.random.Generator) -> np.ndarray:
+    """Greedy for temperature <= 0, else exponential-race sampling (ie/layers/functional.py:64-73)."""
+    greedy = temperatures <= 0.0
+    safe = np.where(greedy, 1.0, temperatures)[:, None]
+    scaled = logits.astype(np.float32) / safe
+    probs = np.exp(scaled - scaled.max(axis=-1, keepdims=True))
+    probs /= probs.sum(axis=-1, keepdims=True)
+    race = generator.exponential(1.0, size=probs.shape).clip(min=1e-10)
+    sampled = np.argmax(probs / race, axis=-1)
+    return np.where(greedy, np.argmax(logits, axis=-1), sampled)
+
+
+def default_copier_factory(k_caches, v_caches, block_size: int, role: str):
+    from .copier import copier_for  # imports torch and the HIP library lazily
+
+    return copier_for(k_caches, v_caches, block_size, role)
+
+
+class Engine:
+    def __init__(self, model, config: EngineConfig | None = None,
+                 copier_factory: CopierFactory | None = None) -> None:
+        self.model = model
+        self.config = config or EngineConfig()
+        self.copier_factory = copier_factory or default_copier_factory
+        self.blocks = BlockManager(self.config.num_blocks, self.config.block_size)
+        self.scheduler = Scheduler(self.blocks,
+                                   max_batch_sequences=self.config.max_batch_sequences,
+                                   max_batch_tokens=self.config.max_batch_tokens)
+        self.generator = np.random.default_rng(self.config.seed)
+        self.k_caches, self.v_caches = model.allocate_caches(self.config.num_blocks,
+                                                             self.config.block_size)
+        self.copier = None
+        if self.config.offload_blocks > 0:
+            self.copier = self.copier_factory(self.k_caches, self.v_caches,
+                                              self.config.block_size, "offload")
+            self.blocks.tier = KVTier(self.config.offload_blocks)
+            self.blocks.copier = self.copier
+
+    def make_copier(self, role: str = "transfer"):
+        return self.copier_factory(self.k_caches, self.v_caches, self.config.block_size, role)
+
+    def submit(self, prompt_ids: list[int], max_new_tokens: int = 32,
+               temperature: float = 1.0, eos_id: int | None = None) -> Sequence:
+        seq = Sequence(prompt_ids, block_size=self.config.block_size,
+                       max_new_tokens=max_new_tokens, temperature=temperature, eos_id=eos_id)
+        self.scheduler.add(seq)
+        return seq
+
+    def forward(self, batch):
+        layout = build_layout(batch, self.config.block_size)
+        hidden = self.model.forward(layout, self.k_caches, self.v_caches, self.config.block_size)
+        return layout, self.model.logits_for_last_token_of_each(hidden, layout.query_lens)
+
+    def step(self) -> list[Sequence]:
+        batch = self.scheduler.schedule()
+        if not batch:
+            return []
+        temperatures = np.array([s.temperature for s in batch.sequences], dtype=np.float32)
+        _, logits = self.forward(batch)
+        tokens = sample_from_logits(logits, temperatures, self.generator).tolist()
+        return self.scheduler.finish_step(batch, tokens)
+
+    def run(self, max_steps: int = 100_000) -> list[Sequence]:
+        done: list[Sequence] = []
+        for _ in range(max_steps):
+            if not self.scheduler.has_work:
+                break
+            done.extend(self.step())
+        return done
+
+    def generate(self, prompts: list[list[int]], max_new_tokens: int = 32,
+                 temperature: float = 1.0) -> list[list[int]]:
+        seqs = [self.submit(p, max_new_tokens=max_new_tokens, temperature=temperature)
+                for p in prompts]
+        self.run()
+        return [s.token_ids[s.num_prompt:] for s in seqs]

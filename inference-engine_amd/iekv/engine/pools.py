@@ -1,0 +1,116 @@
+"""Device KV pools and their registration with libiekv.
+
+A pool is what the reference's engine allocates per layer (ie/engine/engine.py:38-46,
+ie/kernels/torch_backend.py:6-10, ie/model/torch_transformer.py:82-86): for each
+layer a K and a V array of shape [num_blocks * block_size, H, D]. Here all 2L
+arrays are views of ONE slab ``[2, L, num_blocks * block_size, H, D]`` (K half
+first), so the library sees equally spaced arrays and addresses array ``a`` as
+``base + a * stride`` with no pointer table. ``k_caches[l]`` / ``v_caches[l]``
+keep the reference's per-layer shape, and the ``[N, bs, H, D]`` paged view
+(ie/kernels/flash_backend.py:15-17) stays a free reshape.
+"""
+from __future__ import annotations
+
+import math
+from typing import Sequence as Seq
+
+import numpy as np
+import torch
+
+from .. import _native
+
+
+def allocate_pool(num_blocks: int, block_size: int, num_layers: int, num_kv_heads: int,
+                  head_dim: int, *, dtype: torch.dtype = torch.float16,
+                  device: str | torch.device = "cuda", zero: bool = True
+                  ) -> tuple[list[torch.Tensor], list[torch.Tensor]]:
+    """Per-layer K and V caches as views of one slab (zero-filled like the reference)."""
+    if min(num_blocks, block_size, num_layers, num_kv_heads, head_dim) <= 0:
+        raise ValueError("pool dimensions must be positive")
+    shape = (2, num_layers, num_blocks * block_size, num_kv_heads, head_dim)
+    slab = (torch.zeros if zero else torch.empty)(shape, dtype=dtype, device=device)
+    return [slab[0, l] for l in range(num_layers)], [slab[1, l] for l in range(num_layers)]
+
+
+class KVPool:
+    """A validated, registered set of per-layer caches (K arrays then V arrays)."""
+
+    def __init__(self, k_caches: Seq[torch.Tensor], v_caches: Seq[torch.Tensor],
+                 block_size: int) -> None:
+        if block_size <= 0:
+            raise ValueError("block_size must be positive")
+        if not k_caches or len(k_caches) != len(v_caches):
+            raise ValueError("need one K and one V cache per layer")
+        arrays = list(k_caches) + list(v_caches)
+        first = arrays[0]
+        for t in arrays:
+            if not isinstance(t, torch.Tensor):
+                raise TypeError(f"caches must be torch tensors, got {type(t).__name__}")
+            if t.device.type != "cuda":
+                raise ValueError(f"the HIP copier needs GPU caches, got one on {t.device}")
+            if t.device != first.device or t.dtype != first.dtype or t.shape != first.shape:
+                raise ValueError("all caches must share device, dtype and shape")
+            if not t.is_contiguous():
+                raise ValueError("caches must be contiguous")
+        if first.dim() < 1 or first.shape[0] % block_size:
+            raise ValueError(f"cache rows {tuple(first.shape)} are not a multiple of "
+                             f"block_size {block_size}")
+        self.num_layers = len(k_caches)
+        self.block_size = block_size
+        self.num_blocks = first.shape[0] // block_size
+        self.tile_shape = (block_size, *first.shape[1:])
+        self.tile_bytes = math.prod(self.tile_shape) * first.element_size()
+        self.dtype = first.dtype
+        self.device = first.device
+        self._arrays = arrays  # keeps the memory alive while the handle exists
+        self.native = _native.Pool([t.data_ptr() for t in arrays], self.tile_bytes,
+                                   self.num_blocks, self.device.index or 0)
+
+    @property
+    def n_arrays(self) -> int:
+        return 2 * self.num_layers
+
+    @property
+    def block_bytes(self) -> int:
+        """Bytes of one block across all layers, K and V (2L * T)."""
+        return self.n_arrays * self.tile_bytes
+
+    def same_shape(self, other: "KVPool") -> bool:
+        return (self.n_arrays == other.n_arrays and self.tile_bytes == other.tile_bytes
+                and self.tile_shape == other.tile_shape and self.dtype == other.dtype)
+
+    def block_ids(self, ids, *, unique: bool = False, what: str = "block") -> torch.Tensor:
+        """Block ids as a contiguous int32 tensor on this pool's device.
+
+        Host-side ids (lists, arrays, CPU tensors) are range-checked here and
+        raise IndexError before anything is launched. Device int32 tensors are
+        taken as they are: the kernels skip ids outside the pool.
+        """
+        if isinstance(ids, torch.Tensor) and ids.device.type == "cuda":
+            if ids.dtype != torch.int32 or ids.dim() != 1 or not ids.is_contiguous():
+                raise TypeError("device block ids must be a contiguous 1-D int32 tensor")
+            if ids.device != self.device:
+                raise ValueError(f"block ids on {ids.device}, pool on {self.device}")
+            return ids
+        if isinstance(ids, torch.Tensor):
+            host = ids.detach().to(torch.int64).numpy().reshape(-1)
+        else:
+            host = np.asarray(ids, dtype=np.int64).reshape(-1)
+        if host.size:
+            lo, hi = int(host.min()), int(host.max())
+            if lo < 0 or hi >= self.num_blocks:
+                bad = lo if lo < 0 else hi
+                raise IndexError(f"{what} id {bad} out of range for a pool of "
+                                 f"{self.num_blocks} blocks")
+            if unique and np.unique(host).size != host.size:
+                raise ValueError(f"{what} ids must be distinct")
+        staged = torch.from_numpy(host.astype(np.int32))
+        if torch.cuda.is_available():
+            staged = staged.pin_memory()
+        return staged.to(self.device, non_blocking=True)
+
+
+def stream_handle(device: torch.device, stream: torch.cuda.Stream | None = None) -> int:
+    """The raw hipStream_t of ``stream`` (default: torch's current stream on ``device``)."""
+    s = stream if stream is not None else torch.cuda.current_stream(device)
+    return s.cuda_stream

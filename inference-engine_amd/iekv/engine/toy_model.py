@@ -1,0 +1,180 @@
+"""A small paged decoder that produces and consumes KV, for token-identity checks.
+
+The handoff is correct iff decode after it reads, through the new block
+tables, exactly the bytes prefill wrote. Checking that end to end needs a
+model that writes KV by slot (``write_kv``, ie/kernels/torch_backend.py:13-16) and
+reads it back through block tables (``gather_context``,
+ie/kernels/torch_backend.py:19-24). This is that model, in plain torch,
+shaped like the reference's toy transformer (ie/model/transformer.py:12-115:
+RMSNorm, GQA attention with interleaved rotary embeddings, SwiGLU MLP; weights
+drawn from ``numpy.random.default_rng(seed)`` in the same order). Attention
+math runs in float32 whatever the cache dtype. It is support code: the
+handoff never calls it.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ..core.layout import BatchLayout
+from .pools import allocate_pool
+
+
+@dataclass(slots=True)
+class ModelConfig:
+    """Shape of the toy model (ie/model/transformer.py:12-34)."""
+
+    vocab_size: int = 256
+    hidden_size: int = 64
+    num_layers: int = 2
+    num_heads: int = 4
+    num_kv_heads: int = 2
+    head_dim: int = 16
+    intermediate_size: int = 128
+    max_position: int = 2048
+    rope_base: float = 10000.0
+    norm_eps: float = 1e-6
+    rope_halved: bool = False
+
+    def __post_init__(self) -> None:
+        if self.num_heads % self.num_kv_heads:
+            raise ValueError("num_heads must be divisible by num_kv_heads")
+        if self.head_dim % 2:
+            raise ValueError("head_dim must be even for rotary embeddings")
+
+    @property
+    def kv_bytes_per_token(self) -> int:
+        return 2 * self.num_layers * self.num_kv_heads * self.head_dim * 4
+
+
+def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    scale = torch.sqrt(torch.mean(x * x, dim=-1, keepdim=True) + eps)
+    return (x / scale) * weight
+
+
+def _rope(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+          halved: bool) -> torch.Tensor:
+    c = cos[positions][:, None, :]
+    s = sin[positions][:, None, :]
+    out = torch.empty_like(x)
+    if halved:
+        half = x.shape[-1] // 2
+        left, right = x[..., :half], x[..., half:]
+        out[..., :half] = left * c - right * s
+        out[..., half:] = right * c + left * s
+    else:
+        even, odd = x[..., 0::2], x[..., 1::2]
+        out[..., 0::2] = even * c - odd * s
+        out[..., 1::2] = even * s + odd * c
+    return out
+
+
+class _Layer:
+    def __init__(self, config: ModelConfig, rng: np.random.Generator, put) -> None:
+        scale = 1.0 / np.sqrt(config.hidden_size)
+        q_out = config.num_heads * config.head_dim
+        kv_out = config.num_kv_heads * config.head_dim
+
+        def normal(*shape):
+            return put((rng.standard_normal(shape) * scale).astype(np.float32))
+
+        # Draw order matches the reference block (ie/model/transformer.py:36-60).
+        self.attn_norm = put(np.ones(config.hidden_size, dtype=np.float32))
+        self.q_proj = normal(config.hidden_size, q_out)
+        self.k_proj = normal(config.hidden_size, kv_out)
+        self.v_proj = normal(config.hidden_size, kv_out)
+        self.o_proj = normal(q_out, config.hidden_size)
+        self.mlp_norm = put(np.ones(config.hidden_size, dtype=np.float32))
+        self.gate_proj = normal(config.hidden_size, config.intermediate_size)
+        self.up_proj = normal(config.hidden_size, config.intermediate_size)
+        self.down_proj = normal(config.intermediate_size, config.hidden_size)
+
+
+class ToyTransformer:
+    """Paged toy decoder on ``device`` with KV caches of ``cache_dtype``."""
+
+    def __init__(self, config: ModelConfig, seed: int = 0, device: str | torch.device = "cuda",
+                 cache_dtype: torch.dtype = torch.float32) -> None:
+        self.config = config
+        self.device = torch.device(device)
+        self.cache_dtype = cache_dtype
+        rng = np.random.default_rng(seed)
+        scale = 1.0 / np.sqrt(config.hidden_size)
+
+        def put(array: np.ndarray) -> torch.Tensor:
+            return torch.from_numpy(np.ascontiguousarray(array)).to(self.device)
+
+        self.embedding = put((rng.standard_normal((config.vocab_size, config.hidden_size))
+                              * scale).astype(np.float32))
+        self.layers = [_Layer(config, rng, put) for _ in range(config.num_layers)]
+        self.final_norm = put(np.ones(config.hidden_size, dtype=np.float32))
+        self.lm_head = put((rng.standard_normal((config.hidden_size, config.vocab_size))
+                            * scale).astype(np.float32))
+        exponents = np.arange(0, config.head_dim, 2, dtype=np.float32) / config.head_dim
+        angles = np.outer(np.arange(config.max_position, dtype=np.float32),
+                          np.power(config.rope_base, -exponents))
+        self.cos = put(np.cos(angles))
+        self.sin = put(np.sin(angles))
+
+    def allocate_caches(self, num_blocks: int, block_size: int):
+        c = self.config
+        return allocate_pool(num_blocks, block_size, c.num_layers, c.num_kv_heads, c.head_dim,
+                             dtype=self.cache_dtype, device=self.device)
+
+    def _attend(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                layout: BatchLayout, block_size: int) -> torch.Tensor:
+        c = self.config
+        group = c.num_heads // c.num_kv_heads
+        outputs = []
+        start = 0
+        within = torch.arange(block_size, device=self.device)
+        for table, context_len, query_len in zip(layout.block_tables, layout.context_lens,
+                                                 layout.query_lens):
+            needed = -(-context_len // block_size)
+            blocks = torch.as_tensor(table[:needed], device=self.device, dtype=torch.long)
+            slots = (blocks[:, None] * block_size + within[None, :]).reshape(-1)[:context_len]
+            k = k_cache.index_select(0, slots).float().repeat_interleave(group, dim=1)
+            v = v_cache.index_select(0, slots).float().repeat_interleave(group, dim=1)
+            # [heads, tokens, dim] operands, made contiguous before the batched products.
+            qh = q[start:start + query_len].permute(1, 0, 2).contiguous()
+            kt = k.permute(1, 2, 0).contiguous()
+            vh = v.permute(1, 0, 2).contiguous()
+            scores = torch.matmul(qh, kt) / float(np.sqrt(c.head_dim))
+            rows = torch.arange(query_len, device=self.device)[:, None] + (context_len - query_len)
+            cols = torch.arange(context_len, device=self.device)[None, :]
+            scores = scores.masked_fill(~(cols <= rows), float("-inf"))
+            weights = torch.softmax(scores, dim=-1)
+            outputs.append(torch.matmul(weights, vh).permute(1, 0, 2))
+            start += query_len
+        return torch.cat(outputs, dim=0)
+
+    @torch.no_grad()
+    def forward(self, layout: BatchLayout, k_caches, v_caches, block_size: int) -> torch.Tensor:
+        c = self.config
+        tokens = torch.as_tensor(layout.token_ids, device=self.device, dtype=torch.long)
+        positions = torch.as_tensor(layout.positions, device=self.device, dtype=torch.long)
+        slots = torch.as_tensor(layout.slot_mapping, device=self.device, dtype=torch.long)
+        x = self.embedding[tokens]
+        for layer, k_cache, v_cache in zip(self.layers, k_caches, v_caches):
+            normed = _rms_norm(x, layer.attn_norm, c.norm_eps)
+            q = (normed @ layer.q_proj).view(-1, c.num_heads, c.head_dim)
+            k = (normed @ layer.k_proj).view(-1, c.num_kv_heads, c.head_dim)
+            v = (normed @ layer.v_proj).view(-1, c.num_kv_heads, c.head_dim)
+            q = _rope(q, positions, self.cos, self.sin, c.rope_halved)
+            k = _rope(k, positions, self.cos, self.sin, c.rope_halved)
+            k_cache.index_copy_(0, slots, k.to(k_cache.dtype))
+            v_cache.index_copy_(0, slots, v.to(v_cache.dtype))
+            attended = self._attend(q, k_cache, v_cache, layout, block_size)
+            x = x + attended.reshape(-1, c.num_heads * c.head_dim) @ layer.o_proj
+            normed = _rms_norm(x, layer.mlp_norm, c.norm_eps)
+            gate = normed @ layer.gate_proj
+            x = x + (gate / (1.0 + torch.exp(-gate)) * (normed @ layer.up_proj)) @ layer.down_proj
+        return _rms_norm(x, self.final_norm, c.norm_eps)
+
+    @torch.no_grad()
+    def logits_for_last_token_of_each(self, hidden: torch.Tensor,
+                                      query_lens: list[int]) -> np.ndarray:
+        ends = torch.as_tensor(np.cumsum(query_lens) - 1, device=self.device, dtype=torch.long)
+        return (hidden[ends] @ self.lm_head).float().cpu().numpy()

@@ -1,0 +1,280 @@
+"""Disaggregated prefill -> decode serving over one GPU's HBM.
+
+Public API as in the reference (ie/serve/disaggregated.py:16-130): a
+``PrefillWorker`` runs a prompt to completion in its own pool and hands a
+``KVTransfer`` to a ``DecodeWorker``, which places the blocks under freshly
+reserved ids in its pool and continues decoding. The KV bytes move through
+the copier the workers own: by default the HIP copier, so a request's whole
+block table moves in one launch.
+
+Three transfer modes (``mode=``):
+
+``"pack"`` (default, reference-exact)
+    prefill packs the blocks into a device staging buffer (one fused pack
+    launch, iekv_pack), frees its blocks, and the transfer carries the packed
+    payloads; admit reserves fresh ids (``BlockManager.reserve``) and
+    unpacks them (one launch, iekv_unpack). Block tables, counters and
+    ``bytes_moved`` are those of the reference.
+``"direct"``
+    prefill keeps its blocks referenced and the transfer carries their ids;
+    admit copies pool to pool (iekv_copy_direct, no staging, 2P bytes instead
+    of 4P) and only then releases the prefill blocks. Destination ids and
+    decode output are the same as in "pack" mode; the prefill pool's blocks
+    are released at admit instead of at the end of prefill.
+
+``prefix_aware=True`` (any mode)
+    the decode worker is asked first which leading full blocks of the prompt
+    its pool already holds under the same chain hashes; prefill moves only
+    the blocks after them, and admit claims the held ones by reference count
+    (``BlockManager.allocate`` rules, ie/core/block_manager.py:106-176) instead
+    of reserving fresh blocks for them. The reference always moves every block
+    (ie/serve/disaggregated.py:50); this mode is the build's addition for
+    prefix-sharing workloads.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Callable
+
+import numpy as np
+
+from ..core.sequence import Sequence, Status
+from ..engine.engine import CopierFactory, Engine, EngineConfig, sample_from_logits
+
+MODES = ("pack", "direct")
+
+
+@dataclass(slots=True)
+class DirectSource:
+    """Where a direct-mode transfer copies from: a copier and its block ids."""
+
+    copier: Any
+    block_ids: list[int]
+    release: Callable[[], None]
+    released: bool = False
+
+    def done(self) -> None:
+        if not self.released:
+            self.released = True
+            self.release()
+
+
+@dataclass(slots=True)
+class KVTransfer:
+    """The handoff record (ie/serve/disaggregated.py:16-25).
+
+    ``block_payloads`` holds one payload per moved block, in block-table order
+    (None for a direct-mode transfer, whose ``source`` names the blocks).
+    ``first_block`` is the index in the sequence's table of the first moved
+    block (non-zero only for prefix-aware transfers). ``bytes_moved`` is the
+    payload size of the moved blocks, one direction (B x 2L x T).
+    """
+
+    token_ids: list[int]
+    num_computed: int
+    block_payloads: Any
+    bytes_moved: int = 0
+    first_block: int = 0
+    source: DirectSource | None = None
+
+    @property
+    def num_blocks(self) -> int:
+        if self.block_payloads is not None:
+            return len(self.block_payloads)
+        return len(self.source.block_ids) if self.source is not None else 0
+
+    @property
+    def table_length(self) -> int:
+        return self.first_block + self.num_blocks
+
+
+@dataclass(slots=True)
+class DisaggregationStats:
+    prefills: int = 0
+    decodes: int = 0
+    transfers: int = 0
+    blocks_transferred: int = 0
+    bytes_transferred: int = 0
+    prefill_tokens: int = 0
+    decode_tokens: int = 0
+    blocks_skipped: int = 0
+
+
+def _per_block_bytes(engine: Engine) -> int:
+    """Payload bytes of one block, 2L x T (ie/serve/disaggregated.py:60-66)."""
+    if not engine.k_caches:
+        return 0
+    bs = engine.config.block_size
+    tile = engine.k_caches[0][0:bs]
+    nbytes = tile.nbytes if hasattr(tile, "nbytes") else tile.numel() * tile.element_size()
+    return int(nbytes) * 2 * len(engine.k_caches)
+
+
+class PrefillWorker:
+    """Runs prompts to completion and packages their KV (ie/serve/disaggregated.py:39-66)."""
+
+    def __init__(self, model, config: EngineConfig, *, mode: str = "pack",
+                 copier_factory: CopierFactory | None = None) -> None:
+        if mode not in MODES:
+            raise ValueError(f"mode must be one of {MODES}")
+        self.engine = Engine(model, config, copier_factory=copier_factory)
+        self.copier = self.engine.make_copier("transfer")
+        self.mode = mode
+
+    def prefill(self, prompt_ids: list[int], temperature: float = 0.0,
+                skip_blocks: int = 0) -> KVTransfer:
+        seq = self.engine.submit(prompt_ids, max_new_tokens=1 << 30, temperature=temperature)
+        while not seq.prompt_is_fully_computed:
+            self.engine.step()
+        if not 0 <= skip_blocks <= len(seq.block_table):
+            raise ValueError(f"cannot skip {skip_blocks} of {len(seq.block_table)} blocks")
+        moved = seq.block_table[skip_blocks:]
+        nbytes = self._payload_bytes(len(moved))
+        if self.mode == "direct":
+            source = DirectSource(self.copier, list(moved), release=lambda: self._retire(seq))
+            return KVTransfer(token_ids=list(seq.token_ids), num_computed=seq.num_computed,
+                              block_payloads=None, bytes_moved=nbytes,
+                              first_block=skip_blocks, source=source)
+        payloads = self._read(moved)
+        transfer = KVTransfer(token_ids=list(seq.token_ids), num_computed=seq.num_computed,
+                              block_payloads=payloads, bytes_moved=nbytes,
+                              first_block=skip_blocks)
+        self._retire(seq)
+        return transfer
+
+    def _read(self, block_ids: list[int]):
+        if hasattr(self.copier, "read_blocks"):
+            return self.copier.read_blocks(block_ids)          # one fused pack launch
+        return [self.copier.read_block(b) for b in block_ids]  # generic SlotCopier
+
+    def _retire(self, seq: Sequence) -> None:
+        self.engine.blocks.free(seq)
+        if seq in self.engine.scheduler.running:
+            self.engine.scheduler.running.remove(seq)
+
+    def _payload_bytes(self, num_blocks: int) -> int:
+        return num_blocks * _per_block_bytes(self.engine)
+
+
+class DecodeWorker:
+    """Admits transfers into its pool and decodes them (ie/serve/disaggregated.py:69-96)."""
+
+    def __init__(self, model, config: EngineConfig, *, prefix_aware: bool = False,
+                 copier_factory: CopierFactory | None = None) -> None:
+        self.engine = Engine(model, config, copier_factory=copier_factory)
+        self.copier = self.engine.make_copier("transfer")
+        self.prefix_aware = prefix_aware
+
+    def cached_prefix_blocks(self, prompt_ids: list[int]) -> int:
+        """Leading full blocks of ``prompt_ids`` this pool already holds (0 unless prefix-aware).
+
+        Only resident blocks count; a plan that would restore from the offload
+        tier stops there, so the transfer carries those blocks instead.
+        """
+        if not self.prefix_aware:
+            return 0
+        probe = Sequence(prompt_ids, block_size=self.engine.config.block_size)
+        resident, _ = self.engine.blocks._prefix_plan(probe)
+        return len(resident)
+
+    def admit(self, transfer: KVTransfer, max_new_tokens: int,
+              temperature: float = 0.0) -> Sequence:
+        engine = self.engine
+        seq = engine.submit(transfer.token_ids[:-1], max_new_tokens=max_new_tokens,
+                            temperature=temperature)
+        if transfer.first_block:
+            dst_ids = self._claim_with_prefix(seq, transfer)
+        else:
+            if not engine.blocks.reserve(seq, transfer.num_blocks):
+                raise RuntimeError("decode worker has no room for the transferred cache")
+            dst_ids = list(seq.block_table)
+
+        self._move(transfer, dst_ids)
+
+        seq.token_ids = list(transfer.token_ids)
+        seq.num_computed = transfer.num_computed
+        engine.scheduler.waiting.remove(seq)
+        if transfer.first_block or self.prefix_aware:
+            engine.blocks.share_computed_blocks(seq)   # later requests can share these
+        if seq.stop_reason() is not None:
+            seq.status = Status.FINISHED
+            engine.blocks.free(seq)
+            engine.scheduler.finished.append(seq)
+            return seq
+        seq.status = Status.RUNNING
+        engine.scheduler.running.append(seq)
+        return seq
+
+    def _claim_with_prefix(self, seq: Sequence, transfer: KVTransfer) -> list[int]:
+        blocks = self.engine.blocks
+        # A tier hit after the resident prefix is restored by allocate() and then
+        # overwritten by the transfer's payload for the same tokens.
+        resident, _ = blocks._prefix_plan(seq)
+        if len(resident) != transfer.first_block:
+            self.engine.scheduler.waiting.remove(seq)
+            raise RuntimeError(
+                f"decode pool holds {len(resident)} prefix blocks, the transfer assumed "
+                f"{transfer.first_block}")
+        if not blocks.can_allocate(seq):
+            self.engine.scheduler.waiting.remove(seq)
+            raise RuntimeError("decode worker has no room for the transferred cache")
+        blocks.allocate(seq)
+        if len(seq.block_table) != transfer.table_length:
+            raise RuntimeError(f"admitted table has {len(seq.block_table)} blocks, transfer "
+                               f"carries {transfer.table_length}")
+        return seq.block_table[transfer.first_block:]
+
+    def _move(self, transfer: KVTransfer, dst_ids: list[int]) -> None:
+        if transfer.source is not None:
+            src = transfer.source
+            if not hasattr(self.copier, "copy_blocks"):
+                raise TypeError("direct transfers need a copier with copy_blocks()")
+            self.copier.copy_blocks(src.copier, src.block_ids, dst_ids)
+            src.done()   # stream-ordered after the copy's reads
+        elif hasattr(self.copier, "write_blocks"):
+            self.copier.write_blocks(dst_ids, transfer.block_payloads)
+        else:
+            for block_id, payload in zip(dst_ids, transfer.block_payloads):
+                self.copier.write_block(block_id, payload)
+
+
+class DisaggregatedEngine:
+    """Prefill worker + decode worker over one model (ie/serve/disaggregated.py:99-130)."""
+
+    def __init__(self, model, config: EngineConfig | None = None, *, mode: str = "pack",
+                 prefix_aware: bool = False,
+                 copier_factory: CopierFactory | None = None) -> None:
+        config = config or EngineConfig()
+        self.prefill = PrefillWorker(model, config, mode=mode, copier_factory=copier_factory)
+        self.decode = DecodeWorker(model, config, prefix_aware=prefix_aware,
+                                   copier_factory=copier_factory)
+        self.stats = DisaggregationStats()
+
+    def handoff(self, prompt: list[int], max_new_tokens: int,
+                temperature: float = 0.0) -> Sequence:
+        """Prefill one prompt and admit it into the decode pool."""
+        skip = self.decode.cached_prefix_blocks(prompt)
+        transfer = self.prefill.prefill(prompt, temperature, skip_blocks=skip)
+        self.stats.prefills += 1
+        self.stats.transfers += 1
+        self.stats.blocks_transferred += transfer.num_blocks
+        self.stats.bytes_transferred += transfer.bytes_moved
+        self.stats.prefill_tokens += len(prompt)
+        self.stats.blocks_skipped += transfer.first_block
+        return self.decode.admit(transfer, max_new_tokens, temperature)
+
+    def generate(self, prompts: list[list[int]], max_new_tokens: int = 16,
+                 temperature: float = 0.0) -> list[list[int]]:
+        sequences = [self.handoff(p, max_new_tokens, temperature) for p in prompts]
+        engine = self.decode.engine
+        while engine.scheduler.has_work:
+            batch = engine.scheduler.schedule()
+            if not batch:
+                break
+            _, logits = engine.forward(batch)
+            temps = np.array([s.temperature for s in batch.sequences], dtype=np.float32)
+            tokens = sample_from_logits(logits, temps, engine.generator).tolist()
+            engine.scheduler.finish_step(batch, tokens)
+            self.stats.decodes += 1
+            self.stats.decode_tokens += len(batch)
+        return [s.token_ids[s.num_prompt:] for s in sequences]

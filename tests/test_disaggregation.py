@@ -1,0 +1,183 @@
+"""Disaggregated serving on the CPU: the reference's assertions (tests/test_disaggregation.py:23-84)
+and the golden tables, counters, stats and tokens the reference recorded
+(tests/golden/disaggregation.json), with KV bytes moved by the NumPy oracle.
+The same flows run on the GPU through the HIP copier in test_gpu_engine.py."""
+from __future__ import annotations
+
+import pytest
+
+from conftest import golden
+from helpers import LoggingCopier, direct_oracle_factory, oracle_factory
+
+G = golden("disaggregation")
+
+
+def model():
+    from iekv.engine.toy_model import ModelConfig, ToyTransformer
+
+    return ToyTransformer(ModelConfig(**G["model"]), seed=G["model_seed"], device="cpu")
+
+
+def engine_config(**over):
+    from iekv.engine.engine import EngineConfig
+
+    return EngineConfig(**{**G["engine"], **over})
+
+
+def colocated(max_new_tokens=10, prompts=None):
+    from iekv.engine.engine import Engine
+
+    return Engine(model(), engine_config(), copier_factory=oracle_factory).generate(
+        prompts or G["prompts"], max_new_tokens=max_new_tokens, temperature=0.0)
+
+
+def split(**kw):
+    from iekv.serve.disaggregated import DisaggregatedEngine
+
+    kw.setdefault("copier_factory", oracle_factory)
+    return DisaggregatedEngine(model(), engine_config(), **kw)
+
+
+def test_splitting_prefill_from_decode_does_not_change_the_output():
+    assert split().generate(G["prompts"], max_new_tokens=10, temperature=0.0) == colocated()
+
+
+@pytest.mark.parametrize("new_tokens", [1, 5, 12])
+def test_output_matches_at_any_generation_length(new_tokens):
+    out = split().generate(G["prompts"], max_new_tokens=new_tokens, temperature=0.0)
+    assert out == colocated(new_tokens)
+    assert out == G["disaggregated"][str(new_tokens)] == G["colocated"][str(new_tokens)]
+
+
+def test_a_sequence_that_arrives_complete_is_not_decoded_again():
+    engine = split()
+    transfer = engine.prefill.prefill(G["prompts"][0])
+    seq = engine.decode.admit(transfer, max_new_tokens=1)
+    assert seq.is_finished
+    assert seq.num_generated == 1
+    assert engine.decode.engine.blocks.num_free == engine.decode.engine.blocks.num_total
+
+
+def test_a_single_prompt_transfers_its_whole_cache():
+    engine = split()
+    prompt = G["prompts"][0]
+    transfer = engine.prefill.prefill(prompt)
+    assert transfer.num_blocks == (len(prompt) + 15) // 16
+    assert transfer.num_computed == len(prompt)
+    assert len(transfer.token_ids) == len(prompt) + 1
+    assert transfer.bytes_moved > 0
+
+
+def test_the_prefill_worker_releases_its_blocks_after_transfer():
+    engine = split()
+    engine.prefill.prefill(G["prompts"][0])
+    assert engine.prefill.engine.blocks.num_free == engine.prefill.engine.blocks.num_total
+
+
+def test_transfer_volume_grows_with_prompt_length():
+    engine = split()
+    short = engine.prefill.prefill(list(range(500, 516)))
+    long = engine.prefill.prefill(list(range(600, 700)))
+    assert long.bytes_moved > short.bytes_moved
+    assert long.num_blocks > short.num_blocks
+
+
+def test_stats_account_for_every_transfer():
+    engine = split()
+    engine.generate(G["prompts"], max_new_tokens=10, temperature=0.0)
+    st = engine.stats
+    assert {k: getattr(st, k) for k in G["stats_10"]} == G["stats_10"]
+    assert engine.decode.engine.blocks.stats() == G["decode_block_stats_10"]
+    assert list(engine.decode.engine.blocks.free_ids)[:64] == G["decode_free_ids_10"]
+
+
+def test_the_decode_worker_refuses_a_cache_it_cannot_hold():
+    from iekv.serve.disaggregated import DecodeWorker
+
+    engine = split()
+    engine.decode = DecodeWorker(model(), engine_config(num_blocks=2),
+                                 copier_factory=oracle_factory)
+    transfer = engine.prefill.prefill(list(range(300, 400)))
+    with pytest.raises(RuntimeError, match="no room"):
+        engine.decode.admit(transfer, max_new_tokens=4)
+    # Same leftovers as the reference: the partial table stays, the sequence stays waiting.
+    want = G["undersized"]
+    waiting = list(engine.decode.engine.scheduler.waiting)
+    assert transfer.num_blocks == want["transfer_blocks"]
+    assert len(waiting) == want["waiting"]
+    assert waiting[0].block_table == want["leaked_table"]
+    assert engine.decode.engine.blocks.num_free == want["decode_free"]
+
+
+def record(engine):
+    log: list = []
+    engine.prefill.copier = LoggingCopier(engine.prefill.copier, log)
+    engine.decode.copier = LoggingCopier(engine.decode.copier, log)
+    return log
+
+
+def test_block_tables_counters_and_trace_match_the_reference():
+    engine = split()
+    log = record(engine)
+    for prompt, want in zip(G["prompts"], G["requests"]):
+        before = len(log)
+        transfer = engine.prefill.prefill(prompt, 0.0)
+        src = [b for op, b in log[before:] if op == "r"]
+        seq = engine.decode.admit(transfer, 10, 0.0)
+        assert src == want["src_table"]
+        assert seq.block_table == want["dst_table"]
+        assert transfer.num_blocks == want["num_blocks"]
+        assert transfer.num_computed == want["num_computed"]
+        assert transfer.token_ids == want["token_ids"]
+        assert transfer.bytes_moved == want["bytes_moved"]
+        assert engine.prefill.engine.blocks.num_free == want["prefill_free_after"]
+    assert log == G["copier_log"]
+    for side, copier in (("prefill_copier", engine.prefill.copier),
+                         ("decode_copier", engine.decode.copier)):
+        got = {k: getattr(copier, k) for k in ("blocks_read", "blocks_written", "bytes_moved")}
+        assert got == G[side]
+    assert engine.decode.engine.blocks.num_free == G["decode_free_after_admit"]
+    assert list(engine.decode.engine.blocks.free_ids)[:64] == G["decode_free_ids_after_admit"]
+
+
+def test_direct_mode_gives_the_same_tables_and_tokens():
+    engine = split(mode="direct", copier_factory=direct_oracle_factory)
+    seqs = []
+    for prompt, want in zip(G["prompts"], G["requests"]):
+        transfer = engine.prefill.prefill(prompt, 0.0)
+        assert transfer.block_payloads is None and transfer.source.block_ids == want["src_table"]
+        # The prefill blocks stay held until the copy is enqueued.
+        assert engine.prefill.engine.blocks.num_free < engine.prefill.engine.blocks.num_total
+        seq = engine.decode.admit(transfer, 10, 0.0)
+        assert seq.block_table == want["dst_table"]
+        assert transfer.bytes_moved == want["bytes_moved"]
+        assert engine.prefill.engine.blocks.num_free == engine.prefill.engine.blocks.num_total
+        seqs.append(seq)
+    out = split(mode="direct", copier_factory=direct_oracle_factory).generate(
+        G["prompts"], max_new_tokens=10, temperature=0.0)
+    assert out == G["disaggregated"]["10"]
+
+
+def test_prefix_aware_admit_moves_only_the_unshared_blocks():
+    prefix = list(range(1000, 1064))                   # 4 full blocks of 16
+    prompts = [prefix + list(range(1200 + 40 * i, 1200 + 40 * i + 20 + 7 * i))
+               for i in range(4)]
+    plain = split().generate(prompts, max_new_tokens=6, temperature=0.0)
+    engine = split(prefix_aware=True)
+    out = engine.generate(prompts, max_new_tokens=6, temperature=0.0)
+    assert out == plain
+    # The first request moves everything; the others find the 4 prefix blocks resident.
+    assert engine.stats.blocks_skipped == 4 * (len(prompts) - 1)
+    assert engine.stats.blocks_transferred == (
+        sum(-(-len(p) // 16) for p in prompts) - engine.stats.blocks_skipped)
+
+
+def test_prefix_aware_admit_shares_blocks_by_reference_count():
+    prefix = list(range(1000, 1064))
+    engine = split(prefix_aware=True)
+    first = engine.handoff(prefix + [1, 2, 3], max_new_tokens=8)
+    second = engine.handoff(prefix + [4, 5, 6, 7], max_new_tokens=8)
+    assert second.block_table[:4] == first.block_table[:4]
+    blocks = engine.decode.engine.blocks
+    assert all(blocks.blocks[b].ref_count == 2 for b in first.block_table[:4])
+    assert set(second.block_table[4:]).isdisjoint(first.block_table)

@@ -1,0 +1,369 @@
+"""HIP handoff kernels vs the NumPy oracle, byte for byte (GPU).
+
+Every pool is filled with random BYTES (all bit patterns, NaN codes included),
+and every comparison is on bytes: the handoff must be a bitwise copy of the
+reference's NumPy slice copies for any KV dtype.
+"""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from helpers import cfg1_inputs
+from oracle.copier import LayeredSlotCopier, handoff, pack, packed_image
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16, torch.float8_e4m3fn, torch.int8,
+          torch.uint8]
+
+
+def allocate(num_blocks, bs, layers, heads, dim, dtype, device, seed):
+    from iekv.engine.pools import allocate_pool
+
+    k, v = allocate_pool(num_blocks, bs, layers, heads, dim, dtype=dtype, device=device,
+                         zero=False)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    slab = k[0]._base if k[0]._base is not None else k[0]
+    raw = slab.view(torch.uint8)
+    raw.copy_(torch.randint(0, 256, raw.shape, dtype=torch.uint8, device=device, generator=gen))
+    return k, v
+
+
+def host_bytes(arrays):
+    """Per-array uint8 copies [rows, bytes_per_row] on the host."""
+    out = []
+    for t in arrays:
+        rows = t.shape[0]
+        out.append(t.contiguous().view(torch.uint8).reshape(rows, -1).cpu().numpy().copy())
+    return out
+
+
+def oracle_of(k, v, bs):
+    return LayeredSlotCopier(host_bytes(k), host_bytes(v), bs)
+
+
+def assert_pool_equals(k, v, oracle):
+    got = host_bytes(k) + host_bytes(v)
+    want = list(oracle.k_caches) + list(oracle.v_caches)
+    for a, (g, w) in enumerate(zip(got, want)):
+        if not np.array_equal(g, w):
+            rows = np.nonzero((g != w).any(axis=1))[0]
+            raise AssertionError(f"array {a}: {rows.size} rows differ, first at row {rows[0]}")
+
+
+def random_tables(rng, n_src, n_dst, count):
+    src = [int(b) for b in rng.permutation(n_src)[:count]]
+    dst = [int(b) for b in rng.permutation(n_dst)[:count]]
+    return src, dst
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_direct_copy_matches_the_oracle(gpu, dtype):
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 16, 3, 2, 16
+    sk, sv = allocate(64, bs, layers, heads, dim, dtype, gpu, seed=1)
+    dk, dv = allocate(80, bs, layers, heads, dim, dtype, gpu, seed=2)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    rng = np.random.default_rng(3)
+    src_ids, dst_ids = random_tables(rng, 64, 80, 37)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    dst.copy_blocks(src, src_ids, dst_ids)
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    assert_pool_equals(dk, dv, dst_o)
+    assert_pool_equals(sk, sv, src_o)  # the source is untouched
+    assert src.blocks_read == 37 and dst.blocks_written == 37
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_pack_then_unpack_matches_the_oracle(gpu, dtype):
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 16, 4, 2, 32
+    sk, sv = allocate(50, bs, layers, heads, dim, dtype, gpu, seed=4)
+    dk, dv = allocate(70, bs, layers, heads, dim, dtype, gpu, seed=5)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    rng = np.random.default_rng(6)
+    src_ids, dst_ids = random_tables(rng, 50, 70, 29)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    packed = src.read_blocks(src_ids)
+    dst.write_blocks(dst_ids, packed)
+    torch.cuda.synchronize()
+    payloads = pack(src_o, src_ids)
+    assert np.array_equal(packed.data.cpu().numpy(), packed_image(payloads))
+    for d, p in zip(dst_ids, payloads):
+        dst_o.write_block(d, p)
+    assert_pool_equals(dk, dv, dst_o)
+    assert src.bytes_moved == src_o.bytes_moved
+    assert dst.bytes_moved == dst_o.bytes_moved
+
+
+@pytest.mark.parametrize("bs,heads,dim,dtype", [
+    (1, 1, 1, torch.uint8),      # 1-byte tiles
+    (3, 1, 5, torch.float16),    # 30-byte tiles (2-byte vectors)
+    (1, 1, 1, torch.float32),    # 4-byte tiles
+    (1, 1, 2, torch.float32),    # 8-byte tiles
+    (5, 3, 3, torch.uint8),      # 45-byte tiles
+    (2, 1, 24, torch.float32),   # 192 bytes: 16-byte vectors, odd array stride
+])
+def test_narrow_and_odd_tiles(gpu, bs, heads, dim, dtype):
+    from iekv.engine.copier import HipSlotCopier
+
+    layers = 2
+    sk, sv = allocate(33, bs, layers, heads, dim, dtype, gpu, seed=7)
+    dk, dv = allocate(41, bs, layers, heads, dim, dtype, gpu, seed=8)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    rng = np.random.default_rng(9)
+    src_ids, dst_ids = random_tables(rng, 33, 41, 19)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    dst.write_blocks(dst_ids[:9], src.read_blocks(src_ids[:9]))
+    dst.copy_blocks(src, src_ids[9:], dst_ids[9:])
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    assert_pool_equals(dk, dv, dst_o)
+
+
+def test_every_launch_shape_is_bit_exact(gpu):
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 16, 2, 8, 128   # 32 KiB tiles, like the Llama-3-8B shape
+    sk, sv = allocate(96, bs, layers, heads, dim, torch.bfloat16, gpu, seed=10)
+    src = HipSlotCopier(sk, sv, bs)
+    rng = np.random.default_rng(11)
+    src_ids = [int(b) for b in rng.permutation(96)[:77]]
+    want = packed_image(pack(oracle_of(sk, sv, bs), src_ids))
+    before = _native.get_launch()
+    try:
+        for run in (1, 3, 0, 64):
+            for unroll in (4, 8, 16):
+                for nt in (0, 1):
+                    _native.set_launch(run, unroll, nt)
+                    got = src.read_blocks(src_ids).data.cpu().numpy()
+                    assert np.array_equal(got, want), (run, unroll, nt)
+    finally:
+        _native.set_launch(**before)
+
+
+def test_separately_allocated_layers_use_an_address_table(gpu):
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, heads, dim = 16, 2, 16
+    k = [torch.randint(-128, 127, (40 * bs, heads, dim), dtype=torch.int8, device=gpu)
+         for _ in range(3)]
+    v = [torch.randint(-128, 127, (40 * bs, heads, dim), dtype=torch.int8, device=gpu)
+         for _ in range(3)]
+    dk = [torch.zeros_like(t) for t in k]
+    dv = [torch.zeros_like(t) for t in v]
+    src, dst = HipSlotCopier(k, v, bs), HipSlotCopier(dk, dv, bs)
+    assert src.pool.native.handle.value
+    src_o, dst_o = oracle_of(k, v, bs), oracle_of(dk, dv, bs)
+    src_ids, dst_ids = [5, 0, 39, 17], [1, 38, 2, 20]
+    dst.copy_blocks(src, src_ids, dst_ids)
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    assert_pool_equals(dk, dv, dst_o)
+
+
+def test_empty_requests_move_nothing(gpu):
+    from iekv.engine.copier import HipSlotCopier
+
+    sk, sv = allocate(8, 16, 2, 2, 16, torch.float16, gpu, seed=12)
+    dk, dv = allocate(8, 16, 2, 2, 16, torch.float16, gpu, seed=13)
+    before = host_bytes(dk) + host_bytes(dv)
+    src, dst = HipSlotCopier(sk, sv, 16), HipSlotCopier(dk, dv, 16)
+    packed = src.read_blocks([])
+    assert len(packed) == 0
+    dst.write_blocks([], packed)
+    dst.copy_blocks(src, [], [])
+    torch.cuda.synchronize()
+    assert all(np.array_equal(a, b) for a, b in zip(before, host_bytes(dk) + host_bytes(dv)))
+
+
+def test_bad_ids_raise_before_any_launch(gpu):
+    from iekv.engine.copier import HipSlotCopier
+
+    sk, sv = allocate(8, 16, 2, 2, 16, torch.float16, gpu, seed=14)
+    src = HipSlotCopier(sk, sv, 16)
+    dk, dv = allocate(8, 16, 2, 2, 16, torch.float16, gpu, seed=15)
+    dst = HipSlotCopier(dk, dv, 16)
+    before = host_bytes(dk)
+    with pytest.raises(IndexError):
+        src.read_blocks([0, 8])
+    with pytest.raises(IndexError):
+        dst.copy_blocks(src, [0], [-1])
+    with pytest.raises(ValueError, match="distinct"):
+        dst.copy_blocks(src, [0, 1], [3, 3])
+    with pytest.raises(ValueError, match="disjoint"):
+        src.copy_blocks(src, [0, 1], [1, 2])
+    with pytest.raises(ValueError):
+        dst.write_blocks([0, 1], src.read_blocks([2]))
+    torch.cuda.synchronize()
+    assert all(np.array_equal(a, b) for a, b in zip(before, host_bytes(dk)))
+
+
+def test_device_ids_outside_the_pool_are_skipped_by_the_kernel(gpu):
+    from iekv.engine.copier import HipSlotCopier
+
+    sk, sv = allocate(8, 16, 2, 2, 16, torch.float32, gpu, seed=16)
+    dk, dv = allocate(8, 16, 2, 2, 16, torch.float32, gpu, seed=17)
+    src, dst = HipSlotCopier(sk, sv, 16), HipSlotCopier(dk, dv, 16)
+    src_o, dst_o = oracle_of(sk, sv, 16), oracle_of(dk, dv, 16)
+    src_ids = torch.tensor([1, 9, 2], dtype=torch.int32, device=gpu)   # 9 is outside
+    dst_ids = torch.tensor([4, 5, 6], dtype=torch.int32, device=gpu)
+    dst.copy_blocks(src, src_ids, dst_ids)
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [[1, 2]], [[4, 6]])
+    assert_pool_equals(dk, dv, dst_o)
+
+
+def test_single_block_protocol_and_reference_payload_structure(gpu):
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 4, 3, 2, 8
+    sk, sv = allocate(10, bs, layers, heads, dim, torch.float32, gpu, seed=18)
+    dk, dv = allocate(10, bs, layers, heads, dim, torch.float32, gpu, seed=19)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    payload = src.read_block(7)
+    k_tiles, v_tiles = payload
+    assert len(k_tiles) == layers and len(v_tiles) == layers
+    for l in range(layers):
+        assert k_tiles[l].shape == (bs, heads, dim)
+        assert torch.equal(k_tiles[l].view(torch.int32), sk[l][28:32].view(torch.int32))
+        assert torch.equal(v_tiles[l].view(torch.int32), sv[l][28:32].view(torch.int32))
+    dst.write_block(2, payload)
+    # A reference-structured payload of plain tensors (and of NumPy arrays) also writes.
+    dst.write_block(5, ([t.clone() for t in k_tiles], [t.clone() for t in v_tiles]))
+    dst.write_block(9, ([t.cpu().numpy() for t in k_tiles], [t.cpu().numpy() for t in v_tiles]))
+    torch.cuda.synchronize()
+    for b in (2, 5, 9):
+        for l in range(layers):
+            assert torch.equal(dk[l][b * bs:(b + 1) * bs].view(torch.int32),
+                               sk[l][28:32].view(torch.int32))
+            assert torch.equal(dv[l][b * bs:(b + 1) * bs].view(torch.int32),
+                               sv[l][28:32].view(torch.int32))
+    assert src.blocks_read == 1 and dst.blocks_written == 3
+
+
+@pytest.mark.parametrize("staging_blocks", [1, 2, 5, 64])
+def test_host_offload_and_restore_pipelines(gpu, staging_blocks):
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 16, 2, 4, 32
+    sk, sv = allocate(60, bs, layers, heads, dim, torch.bfloat16, gpu, seed=20)
+    dk, dv = allocate(60, bs, layers, heads, dim, torch.bfloat16, gpu, seed=21)
+    src = HipSlotCopier(sk, sv, bs, payload_location="host")
+    dst = HipSlotCopier(dk, dv, bs)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    rng = np.random.default_rng(22)
+    src_ids, dst_ids = random_tables(rng, 60, 60, 23)
+    block = src.pool.block_bytes
+    staging = torch.empty(staging_blocks * block, dtype=torch.uint8, device=gpu)
+    host = torch.empty((23, src.pool.n_arrays, src.pool.tile_bytes), dtype=torch.uint8,
+                       pin_memory=True)
+    ids = src.pool.block_ids(src_ids)
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    _native.call("iekv_offload", src.pool.native.handle, ids.data_ptr(), 23, host.data_ptr(),
+                 host.numel(), staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                 side.cuda_stream)
+    stream.synchronize()
+    payloads = pack(src_o, src_ids)
+    assert np.array_equal(host.numpy(), packed_image(payloads))
+    d_ids = dst.pool.block_ids(dst_ids)
+    _native.call("iekv_restore", dst.pool.native.handle, d_ids.data_ptr(), 23, host.data_ptr(),
+                 host.numel(), staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                 side.cuda_stream)
+    torch.cuda.synchronize()
+    for d, p in zip(dst_ids, payloads):
+        dst_o.write_block(d, p)
+    assert_pool_equals(dk, dv, dst_o)
+
+
+def test_host_payloads_through_the_copier(gpu):
+    from iekv.engine.copier import HipSlotCopier
+
+    bs = 16
+    sk, sv = allocate(30, bs, 2, 2, 64, torch.float16, gpu, seed=23)
+    dk, dv = allocate(30, bs, 2, 2, 64, torch.float16, gpu, seed=24)
+    src = HipSlotCopier(sk, sv, bs, payload_location="host")
+    dst = HipSlotCopier(dk, dv, bs)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    packed = src.read_blocks([3, 14, 29, 0])
+    assert packed.on_host
+    one = src.read_block(11)
+    dst.write_blocks([7, 8, 9, 10], packed)
+    dst.write_block(12, one)
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [[3, 14, 29, 0, 11]], [[7, 8, 9, 10, 12]])
+    assert_pool_equals(dk, dv, dst_o)
+    assert np.array_equal(packed.synchronize().data.numpy(),
+                          packed_image(pack(oracle_of(sk, sv, bs), [3, 14, 29, 0])))
+
+
+def test_a_victim_read_sees_the_bytes_before_a_restore_overwrites_them(gpu):
+    """Restore into block X right after offloading X's victim (ie/core/block_manager.py:161-162)."""
+    from iekv.engine.copier import HipSlotCopier
+
+    bs = 16
+    k, v = allocate(6, bs, 2, 2, 16, torch.float32, gpu, seed=25)
+    tier_copier = HipSlotCopier(k, v, bs, payload_location="host")
+    before = host_bytes(k) + host_bytes(v)
+    saved = tier_copier.read_block(1)           # the returning prefix, offloaded earlier
+    victim = tier_copier.read_block(4)          # eviction of block 4's old contents
+    tier_copier.write_block(4, saved)           # restore lands in the same block
+    torch.cuda.synchronize()
+    got = victim.packed.synchronize().tiles(0).view(torch.uint8).reshape(4, bs, -1).numpy()
+    for a in range(4):
+        assert np.array_equal(got[a], before[a][4 * bs:5 * bs])
+    after = host_bytes(k) + host_bytes(v)
+    for a in range(4):
+        assert np.array_equal(after[a][4 * bs:5 * bs], before[a][1 * bs:2 * bs])
+
+
+def test_cfg1_handoff_reproduces_the_reference_digests(gpu):
+    """The CPU-runnable benchmark case on the GPU, checked against the reference's own output."""
+    from iekv.engine.copier import HipSlotCopier
+    from iekv.engine.pools import allocate_pool
+
+    g = golden("cfg1_handoff")
+    _, src_tables, k_np, v_np = cfg1_inputs()
+    sk, sv = allocate_pool(4096, 16, 4, 4, 32, dtype=torch.float32, device=gpu)
+    for t, a in zip(sk + sv, k_np + v_np):
+        t.copy_(torch.from_numpy(a))
+    src = HipSlotCopier(sk, sv, 16)
+
+    def digests(k, v):
+        return ([hashlib.sha256(t.cpu().numpy().tobytes()).hexdigest() for t in k],
+                [hashlib.sha256(t.cpu().numpy().tobytes()).hexdigest() for t in v])
+
+    # pack -> unpack, request by request
+    dk, dv = allocate_pool(4096, 16, 4, 4, 32, dtype=torch.float32, device=gpu)
+    dst = HipSlotCopier(dk, dv, 16)
+    image = hashlib.sha256()
+    for s_tab, d_tab in zip(src_tables, g["dst_tables"]):
+        packed = src.read_blocks(s_tab)
+        image.update(packed.data.cpu().numpy().tobytes())
+        dst.write_blocks(d_tab, packed)
+    torch.cuda.synchronize()
+    assert image.hexdigest() == g["packed_sha256"]
+    assert digests(dk, dv) == (g["dst_sha256"]["k"], g["dst_sha256"]["v"])
+    assert src.blocks_read == g["src_counters"]["blocks_read"]
+    assert src.bytes_moved == g["src_counters"]["bytes_moved"]
+    assert dst.bytes_moved == g["dst_counters"]["bytes_moved"]
+
+    # direct, all requests in one launch
+    dk2, dv2 = allocate_pool(4096, 16, 4, 4, 32, dtype=torch.float32, device=gpu)
+    dst2 = HipSlotCopier(dk2, dv2, 16)
+    dst2.copy_blocks(src, sum(src_tables, []), sum(g["dst_tables"], []))
+    torch.cuda.synchronize()
+    assert digests(dk2, dv2) == (g["dst_sha256"]["k"], g["dst_sha256"]["v"])
+    assert digests(sk, sv) == (g["src_sha256"]["k"], g["src_sha256"]["v"])

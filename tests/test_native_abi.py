@@ -1,0 +1,100 @@
+"""The C-ABI library loads and exports every entry point include/iekv.h declares.
+
+No kernel runs here (no GPU is needed): only the argument checks that return
+before any HIP call, which is where the ABI promises errors are raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "iekv.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(iekv_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from iekv import _native
+
+    if not _native.library_path().exists():
+        pytest.fail(f"{_native.library_path()} is not built (run __graft_entry__.build())")
+    return _native.lib()
+
+
+def test_every_declared_function_is_exported_and_bound(lib):
+    from iekv import _native
+
+    names = declared_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_native.SIGNATURES)
+
+
+def test_abi_version(lib):
+    assert lib.iekv_abi_version() == 1
+
+
+def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
+    from iekv import _native
+
+    out = ctypes.c_void_p()
+    table = (ctypes.c_uint64 * 2)(4096, 4096 + 1024)
+    cases = [
+        (None, 2, 64, 16, "array_ptrs is null"),
+        (table, 0, 64, 16, "n_arrays"),
+        (table, 2, 0, 16, "tile_bytes"),
+        (table, 2, 64, 0, "num_blocks"),
+        (table, 2, 64, 1 << 40, "num_blocks"),
+        (table, 2, 64, 17, "overlap"),          # 17 x 64 B > the 1024 B gap between arrays
+    ]
+    for ptrs, n, tile, blocks, message in cases:
+        rc = lib.iekv_pool_create(ptrs, n, tile, blocks, 0, ctypes.byref(out))
+        assert rc == _native.IEKV_ERR_INVALID
+        assert message in lib.iekv_last_error().decode()
+        assert not out.value
+
+
+def test_calls_reject_null_pools_and_negative_counts(lib):
+    from iekv import _native
+
+    assert lib.iekv_copy_direct(None, None, None, None, 1, None) == _native.IEKV_ERR_INVALID
+    assert lib.iekv_pack(None, None, 1, None, 0, None) == _native.IEKV_ERR_INVALID
+    assert lib.iekv_unpack(None, None, 1, None, 0, None) == _native.IEKV_ERR_INVALID
+    assert lib.iekv_offload(None, None, 1, None, 0, None, 0, None, None) == _native.IEKV_ERR_INVALID
+    assert lib.iekv_restore(None, None, 1, None, 0, None, 0, None, None) == _native.IEKV_ERR_INVALID
+    assert "null" in lib.iekv_last_error().decode()
+
+
+def test_launch_settings_are_validated(lib):
+    from iekv import _native
+
+    before = _native.get_launch()
+    with pytest.raises(_native.NativeError):
+        _native.set_launch(run_blocks=65)
+    with pytest.raises(_native.NativeError):
+        _native.set_launch(unroll=3)
+    with pytest.raises(_native.NativeError):
+        _native.set_launch(nontemporal=2)
+    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0)
+    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0}
+    _native.set_launch(**before)
+    assert _native.get_launch() == before
+
+
+def test_the_product_refuses_cpu_caches():
+    import torch
+
+    from iekv.engine.copier import HipSlotCopier
+
+    k = [torch.zeros(32, 2, 4)]
+    with pytest.raises(ValueError, match="GPU caches"):
+        HipSlotCopier(k, [t.clone() for t in k], 16)
