@@ -54,6 +54,11 @@ class PackedBlocks:
         self.tile_shape = tuple(tile_shape)
         self.dtype = dtype
         self._event: torch.cuda.Event | None = None  # last async copy touching host data
+        self._parent: PackedBlocks | None = None  # the buffer a slice views (kept alive)
+
+    @property
+    def _root(self) -> "PackedBlocks":
+        return self._parent if self._parent is not None else self
 
     @property
     def on_host(self) -> bool:
@@ -73,7 +78,7 @@ class PackedBlocks:
     def __getitem__(self, index):
         if isinstance(index, slice):
             view = PackedBlocks(self.data[index], self.num_layers, self.tile_shape, self.dtype)
-            view._event = self._event
+            view._parent = self._root
             return view
         n = len(self)
         if index < 0:
@@ -93,19 +98,22 @@ class PackedBlocks:
         """Record that async copies involving this (host) buffer end on ``stream``."""
         ev = torch.cuda.Event()
         ev.record(stream)
-        self._event = ev
+        self._root._event = ev
 
     def synchronize(self) -> "PackedBlocks":
         """Block the host until pending copies into or out of this buffer are done."""
-        if self._event is not None:
-            self._event.synchronize()
+        ev = self._root._event
+        if ev is not None:
+            ev.synchronize()
         elif not self.on_host:
             torch.cuda.current_stream(self.data.device).synchronize()
         return self
 
     def __del__(self) -> None:
-        # Pinned memory goes back to torch's host cache when this object dies;
-        # make sure no DMA still reads or writes it by then.
+        # The root owns the pinned memory, which goes back to torch's host cache
+        # when it dies (views keep it alive); no DMA may still use it by then.
+        if self._parent is not None:
+            return
         ev = self._event
         if ev is not None:
             try:
