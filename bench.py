@@ -37,6 +37,11 @@ for _p in (str(ROOT), str(ROOT / "inference-engine_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+# HBM bytes per algorithmic byte of the direct kv_move launches: (2 x FETCH_SIZE +
+# WRITE_SIZE) / (read + write bytes), from two rocprofv3 --pmc runs of this script
+# calibrated on a plain 4 GiB copy (FETCH_SIZE reads 0.5x, WRITE_SIZE 1.0x of its
+# known size); see profiles/kv_move_direct_cfg3_pmc.txt.
+PMC_TRAFFIC_RATIO = 1.0002
 METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff"
 
 
@@ -145,6 +150,17 @@ class Legs:
                                           self.dst.native.handle, self.src_all.data_ptr(),
                                           self.dst_all.data_ptr(), n, self.stream.cuda_stream),
                      events, 2 * n * self.w.shape.block_bytes, 0)
+
+    def plain_copy(self, events=None) -> None:
+        """A contiguous device-to-device copy of a known size (torch copy_), for reference."""
+        torch = self.torch
+        if not hasattr(self, "_plain"):
+            n = 4 << 30
+            self._plain = (torch.empty(n, dtype=torch.uint8, device=self.src_k[0].device),
+                           torch.zeros(n, dtype=torch.uint8, device=self.src_k[0].device))
+            self._plain[0].fill_(7)
+        a, b = self._plain
+        self._launch(lambda: b.copy_(a), events, 2 * a.numel(), 0)
 
     def verify(self) -> bool:
         """Every destination tile equals its source tile (whole workload, on the GPU)."""
@@ -286,7 +302,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg3", help="cfg1..cfg5 (headline: cfg3)")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--legs", default="direct,pack_unpack,batched")
+    ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
+                    help="comma list of direct, pack_unpack, batched, plain_copy")
     ap.add_argument("--cpu-blocks", type=int, default=1536,
                     help="blocks in the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -325,15 +342,17 @@ def main() -> int:
         legs.clear_dst()
         ms, wall, launches = time_leg(legs, step, args.steps, args.warmup)
         nbytes = 4 * P if name == "pack_unpack" else 2 * P
+        if name == "plain_copy":
+            nbytes = 2 * (4 << 30)
         res, kgbs, avg_us, avg_bytes = summarize(legs, name, ms, launches, nbytes, args.steps)
         res["wall_s"] = round(wall, 3)
         if name == "pack_unpack":
             res["effective_handoff_GBps"] = round(2 * P / (ms * 1e-3) / 1e9, 1)
-        if not args.no_verify:
+        if not args.no_verify and name != "plain_copy":
             verified[name] = legs.verify()
             log(f"[bench] {name}: destination tiles equal source tiles: {verified[name]}")
         results[name] = res
-        if primary is None:
+        if primary is None and name != "plain_copy":
             primary = (name, ms, res, kgbs, avg_us, avg_bytes)
 
     cpu = None
@@ -370,7 +389,8 @@ def main() -> int:
         "legs": results,
         "verified": verified,
         "roofline": {"bound": "hbm", "achieved": round(kgbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
+                     "traffic": int(avg_bytes * PMC_TRAFFIC_RATIO),
                      "kernel": "kv_move (direct)", "avg_launch_us": round(avg_us, 2),
                      "algorithmic_bytes_per_launch": int(avg_bytes)},
         "cpu_baseline": cpu,

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 1
+#define IEKV_ABI_VERSION 2
 
 enum {
   IEKV_OK = 0,
@@ -126,18 +126,24 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                  hipStream_t compute, hipStream_t copy);
 
 /* Launch shape of the move kernels (process-wide):
- *   run_blocks  blocks per workgroup run, 1..64; 0 = automatic (about 128 KiB
- *               of tiles per workgroup); -1 keeps the current setting;
+ *   run_blocks  blocks per workgroup run, 1..64; 0 = automatic (currently one
+ *               block per workgroup); -1 keeps the current setting;
  *   unroll      16-byte accesses in flight per lane per step: 4, 8 or 16;
  *               0 keeps the current setting;
  *   nontemporal 1 for streaming (non-temporal) loads and stores, 0 for
- *               ordinary ones, -1 keeps the current setting.
+ *               ordinary ones, -1 keeps the current setting;
+ *   block_major 1 to order workgroups block-major (the workgroups in flight
+ *               together take different blocks of one array), 0 for
+ *               array-major (they take the 2L arrays of one block), -1 keeps
+ *               the current setting.
  * No reference counterpart: a tuning knob for the launches the entry points
  * above make. */
-int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal);
+int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal,
+                    int32_t block_major);
 
 /* Current launch shape, for reporting. */
-int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal);
+int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
+                    int32_t* block_major);
 
 #ifdef __cplusplus
 }

@@ -43,7 +43,6 @@ namespace {
 constexpr int kThreads = 256;  // four wave64 per workgroup
 constexpr int kMaxRun = 64;    // block ids staged in LDS per workgroup
 constexpr int64_t kMaxTileBytes = int64_t(1) << 30;
-constexpr int64_t kAutoRunBytes = int64_t(128) << 10;
 
 thread_local std::string g_error;
 
@@ -64,9 +63,14 @@ int set_error(int code, const char* fmt, ...) {
       return set_error(IEKV_ERR_HIP, "%s: %s", #expr, hipGetErrorString(err_));          \
   } while (0)
 
+// Launch shape. Measured on MI355X over the five benchmark workloads (8 KiB to
+// 64 KiB tiles): one tile per workgroup and streaming (non-temporal) accesses
+// are best or within noise everywhere, deeper unrolling helps slightly on the
+// 16-32 KiB tiles.
 std::atomic<int> g_run{0};       // 0 = automatic
-std::atomic<int> g_unroll{8};
+std::atomic<int> g_unroll{16};
 std::atomic<int> g_nontemporal{1};
+std::atomic<int> g_block_major{0};  // array-major: higher mean over pool placements
 
 // ---------------------------------------------------------------------------
 // Device side
@@ -136,19 +140,23 @@ __device__ __forceinline__ void move_tile(const V* __restrict__ s, V* __restrict
 }
 
 // One workgroup per (array a, run of list entries [first, first+count)).
-// blockIdx.x = run_index * n_arrays + a, so neighbouring workgroups (which the
-// dispatcher spreads over the eight XCDs) work on different arrays of the
-// same blocks and their streams land in unrelated HBM pages.
+// Workgroup order: block-major (blockIdx.x = a * runs + run_index) makes the
+// workgroups in flight together — which the dispatcher spreads over the eight
+// XCDs — work on different, randomly placed blocks of one array, so their
+// tiles land on unrelated HBM channels whatever the pool's array stride is.
+// Array-major (blockIdx.x = run_index * n_arrays + a) puts the 2L tiles of one
+// block in flight together instead; their addresses differ by multiples of the
+// array stride, which can concentrate them on a few channels.
 template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
 __global__ void __launch_bounds__(kThreads)
 kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
         char* __restrict__ dst_stage, const int32_t* __restrict__ src_ids,
         const int32_t* __restrict__ dst_ids, int32_t tile_vecs, int32_t n_blocks,
-        int32_t n_arrays, int32_t run) {
+        int32_t n_arrays, int32_t run, int32_t runs, int32_t block_major) {
   __shared__ int32_t s_src[kMaxRun];
   __shared__ int32_t s_dst[kMaxRun];
-  const int a = blockIdx.x % n_arrays;
-  const int first = (blockIdx.x / n_arrays) * run;
+  const int a = block_major ? blockIdx.x / runs : blockIdx.x % n_arrays;
+  const int first = (block_major ? blockIdx.x % runs : blockIdx.x / n_arrays) * run;
   const int count = min(run, n_blocks - first);
   const int t = threadIdx.x;
   if (t < count) {
@@ -189,7 +197,8 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
 // ---------------------------------------------------------------------------
 
 using MoveKernel = void (*)(PoolView, PoolView, const char*, char*, const int32_t*,
-                            const int32_t*, int32_t, int32_t, int32_t, int32_t);
+                            const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
+                            int32_t);
 
 template <bool SP, bool DP>
 MoveKernel pick_kernel(int align, int unroll, bool nt, int* vec_bytes) {
@@ -237,10 +246,11 @@ class DeviceGuard {
   bool switched_ = false;
 };
 
-int auto_run(int64_t tile_bytes) {
-  int64_t r = (kAutoRunBytes + tile_bytes - 1) / tile_bytes;
-  return static_cast<int>(std::min<int64_t>(std::max<int64_t>(r, 1), kMaxRun));
-}
+// Blocks per workgroup when the caller has not fixed it: one tile per
+// workgroup, the fastest shape measured for every tile size the workloads use
+// (more, smaller workgroups balance the tail of each launch better than runs
+// of several tiles do).
+int auto_run(int64_t /*tile_bytes*/) { return 1; }
 
 template <bool SP, bool DP>
 int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage, char* dst_stage,
@@ -259,7 +269,8 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
   const int32_t tile_vecs = static_cast<int32_t>(tile_bytes / vec);
   hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
                      view_of(sp), view_of(dp), src_stage, dst_stage, src_ids, dst_ids,
-                     tile_vecs, n_blocks, n_arrays, run);
+                     tile_vecs, n_blocks, n_arrays, run, static_cast<int32_t>(runs),
+                     g_block_major.load());
   IEKV_HIP(hipGetLastError());
   return IEKV_OK;
 }
@@ -577,23 +588,29 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   return IEKV_OK;
 }
 
-int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal) {
+int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal,
+                    int32_t block_major) {
   if (run_blocks < -1 || run_blocks > kMaxRun)
     return set_error(IEKV_ERR_INVALID, "run_blocks %d out of range", run_blocks);
   if (unroll != 0 && unroll != 4 && unroll != 8 && unroll != 16)
     return set_error(IEKV_ERR_INVALID, "unroll must be 4, 8 or 16 (got %d)", unroll);
   if (nontemporal < -1 || nontemporal > 1)
     return set_error(IEKV_ERR_INVALID, "nontemporal must be -1, 0 or 1 (got %d)", nontemporal);
+  if (block_major < -1 || block_major > 1)
+    return set_error(IEKV_ERR_INVALID, "block_major must be -1, 0 or 1 (got %d)", block_major);
   if (run_blocks >= 0) g_run.store(run_blocks);
   if (unroll) g_unroll.store(unroll);
   if (nontemporal >= 0) g_nontemporal.store(nontemporal);
+  if (block_major >= 0) g_block_major.store(block_major);
   return IEKV_OK;
 }
 
-int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal) {
+int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
+                    int32_t* block_major) {
   if (run_blocks) *run_blocks = g_run.load();
   if (unroll) *unroll = g_unroll.load();
   if (nontemporal) *nontemporal = g_nontemporal.load();
+  if (block_major) *block_major = g_block_major.load();
   return IEKV_OK;
 }
 

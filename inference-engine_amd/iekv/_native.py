@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 IEKV_OK = 0
 IEKV_ERR_INVALID = -1
@@ -33,8 +33,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                              c_void_p, c_void_p]),
     "iekv_restore": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p, c_int64,
                              c_void_p, c_void_p]),
-    "iekv_set_launch": (c_int, [c_int32, c_int32, c_int32]),
-    "iekv_get_launch": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
+    "iekv_set_launch": (c_int, [c_int32, c_int32, c_int32, c_int32]),
+    "iekv_get_launch": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32),
+                                POINTER(c_int32)]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -119,11 +120,14 @@ class Pool:
             pass
 
 
-def set_launch(run_blocks: int = -1, unroll: int = 0, nontemporal: int = -1) -> None:
-    call("iekv_set_launch", run_blocks, unroll, nontemporal)
+def set_launch(run_blocks: int = -1, unroll: int = 0, nontemporal: int = -1,
+               block_major: int = -1) -> None:
+    call("iekv_set_launch", run_blocks, unroll, nontemporal, block_major)
 
 
 def get_launch() -> dict[str, int]:
-    run, unroll, nt = c_int32(), c_int32(), c_int32()
-    call("iekv_get_launch", ctypes.byref(run), ctypes.byref(unroll), ctypes.byref(nt))
-    return {"run_blocks": run.value, "unroll": unroll.value, "nontemporal": nt.value}
+    run, unroll, nt, bm = c_int32(), c_int32(), c_int32(), c_int32()
+    call("iekv_get_launch", ctypes.byref(run), ctypes.byref(unroll), ctypes.byref(nt),
+         ctypes.byref(bm))
+    return {"run_blocks": run.value, "unroll": unroll.value, "nontemporal": nt.value,
+            "block_major": bm.value}

@@ -145,9 +145,10 @@ def test_every_launch_shape_is_bit_exact(gpu):
         for run in (1, 3, 0, 64):
             for unroll in (4, 8, 16):
                 for nt in (0, 1):
-                    _native.set_launch(run, unroll, nt)
-                    got = src.read_blocks(src_ids).data.cpu().numpy()
-                    assert np.array_equal(got, want), (run, unroll, nt)
+                    for block_major in (0, 1):
+                        _native.set_launch(run, unroll, nt, block_major)
+                        got = src.read_blocks(src_ids).data.cpu().numpy()
+                        assert np.array_equal(got, want), (run, unroll, nt, block_major)
     finally:
         _native.set_launch(**before)
 

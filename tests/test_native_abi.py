@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 1
+    assert lib.iekv_abi_version() == 2
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -84,8 +84,8 @@ def test_launch_settings_are_validated(lib):
         _native.set_launch(unroll=3)
     with pytest.raises(_native.NativeError):
         _native.set_launch(nontemporal=2)
-    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0)
-    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0}
+    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, block_major=0)
+    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "block_major": 0}
     _native.set_launch(**before)
     assert _native.get_launch() == before
 
