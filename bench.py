@@ -41,7 +41,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # WRITE_SIZE) / (read + write bytes), from two rocprofv3 --pmc runs of this script
 # calibrated on a plain 4 GiB copy (FETCH_SIZE reads 0.5x, WRITE_SIZE 1.0x of its
 # known size); see profiles/kv_move_direct_cfg3_pmc.txt.
-PMC_TRAFFIC_RATIO = 1.0002
+PMC_TRAFFIC_RATIO = 1.0004
 METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff"
 
 
@@ -161,6 +161,66 @@ class Legs:
             self._plain[0].fill_(7)
         a, b = self._plain
         self._launch(lambda: b.copy_(a), events, 2 * a.numel(), 0)
+
+    def host_roundtrip(self, steps: int, warmup: int) -> dict:
+        """Offload every moved block to pinned host memory and restore it onto its dst id.
+
+        One iekv_offload over the whole block list (pack on the compute stream
+        overlapping device-to-host copies on a side stream), then one iekv_restore
+        (host-to-device copies overlapping the unpack). Both are bounded by the
+        host link, not HBM.
+        """
+        from iekv import _native
+        from iekv.engine.copier import HOST_STAGING_BYTES
+
+        torch = self.torch
+        P = self.w.payload_bytes
+        t0 = time.perf_counter()
+        host = torch.empty(P, dtype=torch.uint8, pin_memory=True)
+        pin_s = time.perf_counter() - t0
+        staging = torch.empty(2 * HOST_STAGING_BYTES, dtype=torch.uint8,
+                              device=self.src_k[0].device)
+        side = torch.cuda.Stream(self.src_k[0].device)
+        h = self.stream.cuda_stream
+        n = self.src_all.numel()
+
+        def offload():
+            _native.call("iekv_offload", self.src.native.handle, self.src_all.data_ptr(), n,
+                         host.data_ptr(), P, staging.data_ptr(), staging.numel(), h,
+                         side.cuda_stream)
+
+        def restore():
+            _native.call("iekv_restore", self.dst.native.handle, self.dst_all.data_ptr(), n,
+                         host.data_ptr(), P, staging.data_ptr(), staging.numel(), h,
+                         side.cuda_stream)
+
+        for _ in range(warmup):
+            offload()
+            restore()
+        torch.cuda.synchronize()
+        d2h, h2d = [], []
+        for _ in range(steps):
+            a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            a.record(self.stream)
+            offload()
+            b.record(self.stream)     # the compute stream waits for the last copy
+            restore()
+            c.record(self.stream)     # after the last unpack, which waited on its copy
+            torch.cuda.synchronize()
+            d2h.append(a.elapsed_time(b))
+            h2d.append(b.elapsed_time(c))
+        del host
+        d2h_ms, h2d_ms = statistics.median(d2h), statistics.median(h2d)
+        out = {"pinned_GB": round(P / 1e9, 2), "pin_alloc_s": round(pin_s, 2),
+               "d2h_ms": round(d2h_ms, 2), "h2d_ms": round(h2d_ms, 2),
+               "d2h_GBps": round(P / (d2h_ms * 1e-3) / 1e9, 2),
+               "h2d_GBps": round(P / (h2d_ms * 1e-3) / 1e9, 2),
+               "roundtrip_ms": round(d2h_ms + h2d_ms, 2),
+               "bound": "host link (PCIe Gen5 x16, 64 GB/s per direction theoretical)"}
+        log(f"[bench] host_roundtrip  {P / 1e9:.2f} GB pinned ({pin_s:.1f} s to pin): "
+            f"D2H {out['d2h_GBps']} GB/s, H2D {out['h2d_GBps']} GB/s, "
+            f"round trip {out['roundtrip_ms']} ms")
+        return out
 
     def verify(self) -> bool:
         """Every destination tile equals its source tile (whole workload, on the GPU)."""
@@ -295,6 +355,36 @@ def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float) ->
                        f"1 of {os.cpu_count()} host cores")}
 
 
+def sweep(legs: Legs, names: list[str]) -> list[dict]:
+    """Time each leg under every launch shape iekv_set_launch offers (3 steps after 1 warm-up)."""
+    from iekv import _native
+
+    before = _native.get_launch()
+    P = legs.w.payload_bytes
+    rows = []
+    try:
+        for block_major in (0, 1):
+            for nt in (1, 0):
+                for unroll in (4, 8, 16):
+                    for run in (1, 2, 4, 8, 16):
+                        _native.set_launch(run, unroll, nt, block_major)
+                        row = {"run_blocks": run, "unroll": unroll, "nontemporal": nt,
+                               "block_major": block_major}
+                        for name in names:
+                            ms, _, _ = time_leg(legs, getattr(legs, name), 3, 1)
+                            nbytes = 4 * P if name == "pack_unpack" else 2 * P
+                            row[name] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+                        rows.append(row)
+                        log("[sweep] " + json.dumps(row))
+    finally:
+        _native.set_launch(**before)
+    for name in names:
+        best = max(rows, key=lambda r: r[name])
+        log(f"[sweep] best {name}: {best[name]} GB/s at " + json.dumps(
+            {k: best[k] for k in ("run_blocks", "unroll", "nontemporal", "block_major")}))
+    return rows
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -303,12 +393,15 @@ def main() -> int:
     ap.add_argument("--config", default="cfg3", help="cfg1..cfg5 (headline: cfg3)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
-                    help="comma list of direct, pack_unpack, batched, plain_copy")
+                    help="comma list of direct, pack_unpack, batched, plain_copy, "
+                         "host_roundtrip")
     ap.add_argument("--cpu-blocks", type=int, default=1536,
                     help="blocks in the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="minimum CPU-baseline time (the sample handoff repeats until then)")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--sweep", action="store_true",
+                    help="time the legs under every launch shape instead of the benchmark line")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -333,11 +426,24 @@ def main() -> int:
         f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B")
     legs = Legs(w, device, args.seed)
     P = w.payload_bytes
+    if args.sweep:
+        names = [x for x in args.legs.split(",") if x in ("direct", "pack_unpack", "batched")]
+        rows = sweep(legs, names)
+        ok = legs.verify()
+        print(json.dumps({"sweep": w.name, "legs": names, "rows": rows, "verified": ok}))
+        return 0 if ok else 1
     names = [x for x in args.legs.split(",") if x]
     results: dict = {}
     verified: dict = {}
     primary = None
     for name in names:
+        if name == "host_roundtrip":
+            legs.clear_dst()
+            results[name] = legs.host_roundtrip(max(1, min(args.steps, 3)), 1)
+            if not args.no_verify:
+                verified[name] = legs.verify()
+                log(f"[bench] {name}: destination tiles equal source tiles: {verified[name]}")
+            continue
         step = getattr(legs, name)
         legs.clear_dst()
         ms, wall, launches = time_leg(legs, step, args.steps, args.warmup)

@@ -25,6 +25,7 @@ cache reads and writes exactly as the reference's synchronous copies are.
 """
 from __future__ import annotations
 
+import weakref
 from typing import Any, Iterable, Sequence as Seq
 
 import numpy as np
@@ -125,11 +126,19 @@ class PackedBlocks:
 class BlockPayload:
     """One block of a :class:`PackedBlocks`; unpacks as ``(k_list, v_list)``."""
 
-    __slots__ = ("packed", "index")
+    __slots__ = ("_packed", "_index")
 
-    def __init__(self, packed: PackedBlocks, index: int) -> None:
-        self.packed = packed
-        self.index = index
+    def __init__(self, packed: PackedBlocks | None, index: int) -> None:
+        self._packed = packed
+        self._index = index
+
+    @property
+    def packed(self) -> PackedBlocks:
+        return self._packed
+
+    @property
+    def index(self) -> int:
+        return self._index
 
     @property
     def k(self) -> list[torch.Tensor]:
@@ -157,6 +166,39 @@ class BlockPayload:
         return self.packed.data[self.index].numel()
 
 
+class DeferredBlockPayload(BlockPayload):
+    """A host payload whose bytes are gathered at its copier's next :meth:`HipSlotCopier.flush`.
+
+    Reading ``packed`` / ``index`` (or the tiles) before then flushes. The
+    snapshot is still the block's contents at ``read_block`` time: every write
+    to the pool flushes pending reads first (see ``HipSlotCopier``).
+    """
+
+    __slots__ = ("_copier", "block_id", "__weakref__")
+
+    def __init__(self, copier: "HipSlotCopier", block_id: int) -> None:
+        super().__init__(None, 0)
+        self._copier = copier
+        self.block_id = block_id
+
+    def _resolve(self, packed: PackedBlocks, index: int) -> None:
+        self._packed = packed
+        self._index = index
+        self._copier = None
+
+    @property
+    def packed(self) -> PackedBlocks:
+        if self._packed is None:
+            self._copier.flush()
+        return self._packed
+
+    @property
+    def index(self) -> int:
+        if self._packed is None:
+            self._copier.flush()
+        return self._index
+
+
 def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
     """The PackedBlocks slice that ``payloads`` are consecutive entries of, if any."""
     if isinstance(payloads, PackedBlocks):
@@ -180,7 +222,8 @@ class HipSlotCopier:
     """
 
     def __init__(self, k_caches: Seq[torch.Tensor], v_caches: Seq[torch.Tensor],
-                 block_size: int, *, payload_location: str = "device") -> None:
+                 block_size: int, *, payload_location: str = "device",
+                 defer_reads: bool | None = None) -> None:
         if payload_location not in ("device", "host"):
             raise ValueError("payload_location must be 'device' or 'host'")
         self.k_caches = k_caches
@@ -188,8 +231,15 @@ class HipSlotCopier:
         self.block_size = block_size
         self.pool = KVPool(k_caches, v_caches, block_size)
         self.payload_location = payload_location
+        # Single-block reads of host payloads (the offload hook's evictions) are
+        # batched: they queue until flush(), which gathers every still-wanted
+        # block with one iekv_offload.
+        self.defer_reads = (payload_location == "host") if defer_reads is None else defer_reads
         self.blocks_read = 0
         self.blocks_written = 0
+        self.offload_launches = 0       # iekv_offload calls made
+        self.blocks_offloaded = 0       # blocks those calls moved to the host
+        self._pending: list[tuple[int, weakref.ref]] = []
         self._copy_stream: torch.cuda.Stream | None = None
         self._staging: torch.Tensor | None = None
 
@@ -252,8 +302,42 @@ class HipSlotCopier:
 
     # -- SlotCopier protocol (ie/core/offload.py:8-11) ---------------------------
     def read_block(self, block_id: int) -> BlockPayload:
-        """Snapshot of one block (ie/engine/copier.py:18-22)."""
-        return self.read_blocks([block_id])[0]
+        """Snapshot of one block (ie/engine/copier.py:18-22).
+
+        With ``defer_reads`` the bytes are gathered at the next :meth:`flush`,
+        batched with the other reads queued since; the counter still counts
+        this read now, as the reference does.
+        """
+        if not self.defer_reads:
+            return self.read_blocks([block_id])[0]
+        block_id = int(block_id)
+        if not 0 <= block_id < self.pool.num_blocks:
+            raise IndexError(f"source block id {block_id} out of range for a pool of "
+                             f"{self.pool.num_blocks} blocks")
+        payload = DeferredBlockPayload(self, block_id)
+        self._pending.append((block_id, weakref.ref(payload)))
+        self.blocks_read += 1
+        return payload
+
+    @property
+    def pending_reads(self) -> int:
+        return len(self._pending)
+
+    def flush(self) -> int:
+        """Gather every queued read whose payload is still referenced, in one launch.
+
+        Payloads nobody holds any more (a tier that rejected, deduplicated or
+        already evicted them) are skipped. Returns the number of blocks moved.
+        """
+        if not self._pending:
+            return 0
+        pending, self._pending = self._pending, []
+        live = [(block_id, p) for block_id, ref in pending if (p := ref()) is not None]
+        if live:
+            packed = self._gather([b for b, _ in live], self.payload_location)
+            for i, (_, payload) in enumerate(live):
+                payload._resolve(packed, i)
+        return len(live)
 
     def write_block(self, block_id: int, payload: Any) -> None:
         """Scatter one payload into ``block_id`` (ie/engine/copier.py:24-31)."""
@@ -262,7 +346,11 @@ class HipSlotCopier:
     # -- batched calls -------------------------------------------------------
     def read_blocks(self, block_ids, *, location: str | None = None) -> PackedBlocks:
         """Pack ``block_ids`` (in order) into a new payload buffer with one launch."""
-        location = location or self.payload_location
+        out = self._gather(block_ids, location or self.payload_location)
+        self.blocks_read += len(out)
+        return out
+
+    def _gather(self, block_ids, location: str) -> PackedBlocks:
         ids = self.pool.block_ids(block_ids, what="source block")
         n = ids.numel()
         out = self._empty_packed(n, on_host=(location == "host"))
@@ -274,14 +362,16 @@ class HipSlotCopier:
                          out.data.data_ptr(), out.nbytes, staging.data_ptr(), staging.numel(),
                          stream.cuda_stream, copy.cuda_stream)
             out.mark(stream)
+            self.offload_launches += 1
+            self.blocks_offloaded += n
         else:
             _native.call("iekv_pack", self.pool.native.handle, ids.data_ptr(), n,
                          out.data.data_ptr(), out.nbytes, stream.cuda_stream)
-        self.blocks_read += n
         return out
 
     def write_blocks(self, block_ids, payloads) -> None:
         """Scatter ``payloads[i]`` into ``block_ids[i]`` for every i (one launch when possible)."""
+        self.flush()   # queued reads see the blocks before this write
         ids = self.pool.block_ids(block_ids, unique=True, what="destination block")
         n = ids.numel()
         if len(payloads) != n:
@@ -313,6 +403,7 @@ class HipSlotCopier:
 
     def copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids) -> None:
         """Direct pool-to-pool move: tile ``src_ids[i]`` of ``source`` -> ``dst_ids[i]`` here."""
+        self.flush()
         if not self.pool.same_shape(source.pool):
             raise ValueError("source and destination pools differ in layout")
         if source.device != self.device:
@@ -355,5 +446,5 @@ def stack_payloads(payloads: Iterable[BlockPayload]) -> PackedBlocks:
     return PackedBlocks(data, first.num_layers, first.tile_shape, first.dtype)
 
 
-__all__ = ["BlockPayload", "HipSlotCopier", "PackedBlocks", "copier_for", "stack_payloads",
-           "stream_handle"]
+__all__ = ["BlockPayload", "DeferredBlockPayload", "HipSlotCopier", "PackedBlocks", "copier_for",
+           "stack_payloads", "stream_handle"]

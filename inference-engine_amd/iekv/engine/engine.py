@@ -87,7 +87,19 @@ class Engine:
         self.scheduler.add(seq)
         return seq
 
+    def flush_offloads(self) -> None:
+        """Issue the offload reads queued by this step's evictions (one batched launch).
+
+        Called before anything writes the pool outside the offload copier (the
+        model's forward pass, an admitted transfer), so every queued read sees
+        the bytes the block held when it was evicted.
+        """
+        flush = getattr(self.copier, "flush", None)
+        if flush is not None:
+            flush()
+
     def forward(self, batch):
+        self.flush_offloads()
         layout = build_layout(batch, self.config.block_size)
         hidden = self.model.forward(layout, self.k_caches, self.v_caches, self.config.block_size)
         return layout, self.model.logits_for_last_token_of_each(hidden, layout.query_lens)

@@ -189,6 +189,7 @@ class DecodeWorker:
                 raise RuntimeError("decode worker has no room for the transferred cache")
             dst_ids = list(seq.block_table)
 
+        engine.flush_offloads()   # evictions made room for dst_ids: read them first
         self._move(transfer, dst_ids)
 
         seq.token_ids = list(transfer.token_ids)

@@ -157,3 +157,23 @@ def test_offload_does_not_change_tokens_on_gpu(gpu):
     (without, st_off), (with_tier, st_on) = results
     assert without == with_tier
     assert st_on["restored"] > 0 and st_on["computed"] < st_off["computed"]
+
+
+def test_evictions_are_offloaded_in_batches(gpu):
+    from iekv.engine.engine import Engine, EngineConfig
+    from iekv.engine.toy_model import ModelConfig, ToyTransformer
+
+    g = golden("offload")
+    m = ToyTransformer(ModelConfig(**g["model"]), seed=g["model_seed"], device=gpu)
+    engine = Engine(m, EngineConfig(block_size=16, num_blocks=12, max_batch_tokens=512,
+                                    offload_blocks=64))
+    for prompt in g["prompts"]:
+        engine.generate([prompt], max_new_tokens=2, temperature=0.0)
+    engine.generate([g["prompts"][0]], max_new_tokens=2, temperature=0.0)
+    copier = engine.copier
+    reads = sum(1 for op, _ in g["64"]["copier_log"] if op == "r")
+    assert copier.blocks_read == reads
+    assert copier.pending_reads == 0 or copier.offload_launches > 0
+    assert 0 < copier.offload_launches < reads
+    print(f"{reads} evictions offloaded in {copier.offload_launches} launches "
+          f"({copier.blocks_offloaded} blocks copied)")

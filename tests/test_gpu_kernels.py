@@ -368,3 +368,27 @@ def test_cfg1_handoff_reproduces_the_reference_digests(gpu):
     torch.cuda.synchronize()
     assert digests(dk2, dv2) == (g["dst_sha256"]["k"], g["dst_sha256"]["v"])
     assert digests(sk, sv) == (g["src_sha256"]["k"], g["src_sha256"]["v"])
+
+
+def test_deferred_host_reads_batch_and_keep_snapshot_semantics(gpu):
+    from iekv.engine.copier import DeferredBlockPayload, HipSlotCopier
+
+    bs = 16
+    k, v = allocate(12, bs, 2, 2, 16, torch.float16, gpu, seed=26)
+    before = host_bytes(k) + host_bytes(v)
+    copier = HipSlotCopier(k, v, bs, payload_location="host")
+    kept = [copier.read_block(b) for b in (3, 7, 9)]
+    dropped = copier.read_block(5)
+    assert all(isinstance(p, DeferredBlockPayload) for p in kept)
+    assert copier.pending_reads == 4 and copier.blocks_read == 4
+    del dropped                                   # nobody holds it: never copied
+    copier.write_block(7, kept[0])                # a write flushes the queued reads first
+    torch.cuda.synchronize()
+    assert copier.offload_launches == 1 and copier.blocks_offloaded == 3
+    for payload, block in zip(kept, (3, 7, 9)):
+        got = payload.packed.synchronize().tiles(payload.index).view(torch.uint8).reshape(4, bs, -1)
+        for a in range(4):
+            assert np.array_equal(got[a].numpy(), before[a][block * bs:(block + 1) * bs])
+    after = host_bytes(k) + host_bytes(v)
+    for a in range(4):
+        assert np.array_equal(after[a][7 * bs:8 * bs], before[a][3 * bs:4 * bs])
