@@ -363,13 +363,13 @@ def sweep(legs: Legs, names: list[str]) -> list[dict]:
     P = legs.w.payload_bytes
     rows = []
     try:
-        for block_major in (0, 1):
+        for order in (0, 1, 2):
             for nt in (1, 0):
                 for unroll in (4, 8, 16):
                     for run in (1, 2, 4, 8, 16):
-                        _native.set_launch(run, unroll, nt, block_major)
+                        _native.set_launch(run, unroll, nt, order)
                         row = {"run_blocks": run, "unroll": unroll, "nontemporal": nt,
-                               "block_major": block_major}
+                               "order": order}
                         for name in names:
                             ms, _, _ = time_leg(legs, getattr(legs, name), 3, 1)
                             nbytes = 4 * P if name == "pack_unpack" else 2 * P
@@ -381,7 +381,7 @@ def sweep(legs: Legs, names: list[str]) -> list[dict]:
     for name in names:
         best = max(rows, key=lambda r: r[name])
         log(f"[sweep] best {name}: {best[name]} GB/s at " + json.dumps(
-            {k: best[k] for k in ("run_blocks", "unroll", "nontemporal", "block_major")}))
+            {k: best[k] for k in ("run_blocks", "unroll", "nontemporal", "order")}))
     return rows
 
 
@@ -400,6 +400,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="minimum CPU-baseline time (the sample handoff repeats until then)")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--launch", default="",
+                    help="run_blocks,unroll,nontemporal,order for iekv_set_launch (default: "
+                         "the library's)")
     ap.add_argument("--sweep", action="store_true",
                     help="time the legs under every launch shape instead of the benchmark line")
     args = ap.parse_args()
@@ -421,6 +424,8 @@ def main() -> int:
         return 2
     device = torch.device("cuda", 0)
     _native.lib()
+    if args.launch:
+        _native.set_launch(*[int(x) for x in args.launch.split(",")])
     w = workloads.make(args.config, args.seed)
     log(f"[bench] {w.name}: {w.num_requests} requests, {w.num_blocks} blocks, "
         f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B")

@@ -132,18 +132,18 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
  *               0 keeps the current setting;
  *   nontemporal 1 for streaming (non-temporal) loads and stores, 0 for
  *               ordinary ones, -1 keeps the current setting;
- *   block_major 1 to order workgroups block-major (the workgroups in flight
- *               together take different blocks of one array), 0 for
- *               array-major (they take the 2L arrays of one block), -1 keeps
- *               the current setting.
+ *   order       which (array, block) tiles are in flight together:
+ *               0 array-major (the 2L tiles of one block), 1 block-major
+ *               (random blocks of one array), 2 diagonal (array a takes list
+ *               run r + a, so 2L arrays and 2L blocks at once); -1 keeps the
+ *               current setting.
  * No reference counterpart: a tuning knob for the launches the entry points
  * above make. */
-int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal,
-                    int32_t block_major);
+int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order);
 
 /* Current launch shape, for reporting. */
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
-                    int32_t* block_major);
+                    int32_t* order);
 
 #ifdef __cplusplus
 }

@@ -121,13 +121,14 @@ class Pool:
 
 
 def set_launch(run_blocks: int = -1, unroll: int = 0, nontemporal: int = -1,
-               block_major: int = -1) -> None:
-    call("iekv_set_launch", run_blocks, unroll, nontemporal, block_major)
+               order: int = -1) -> None:
+    """Launch shape of the move kernels; see iekv_set_launch in include/iekv.h."""
+    call("iekv_set_launch", run_blocks, unroll, nontemporal, order)
 
 
 def get_launch() -> dict[str, int]:
-    run, unroll, nt, bm = c_int32(), c_int32(), c_int32(), c_int32()
+    run, unroll, nt, order = c_int32(), c_int32(), c_int32(), c_int32()
     call("iekv_get_launch", ctypes.byref(run), ctypes.byref(unroll), ctypes.byref(nt),
-         ctypes.byref(bm))
+         ctypes.byref(order))
     return {"run_blocks": run.value, "unroll": unroll.value, "nontemporal": nt.value,
-            "block_major": bm.value}
+            "order": order.value}

@@ -145,10 +145,10 @@ def test_every_launch_shape_is_bit_exact(gpu):
         for run in (1, 3, 0, 64):
             for unroll in (4, 8, 16):
                 for nt in (0, 1):
-                    for block_major in (0, 1):
-                        _native.set_launch(run, unroll, nt, block_major)
+                    for order in (0, 1, 2):
+                        _native.set_launch(run, unroll, nt, order)
                         got = src.read_blocks(src_ids).data.cpu().numpy()
-                        assert np.array_equal(got, want), (run, unroll, nt, block_major)
+                        assert np.array_equal(got, want), (run, unroll, nt, order)
     finally:
         _native.set_launch(**before)
 
@@ -322,7 +322,7 @@ def test_a_victim_read_sees_the_bytes_before_a_restore_overwrites_them(gpu):
     victim = tier_copier.read_block(4)          # eviction of block 4's old contents
     tier_copier.write_block(4, saved)           # restore lands in the same block
     torch.cuda.synchronize()
-    got = victim.packed.synchronize().tiles(0).view(torch.uint8).reshape(4, bs, -1).numpy()
+    got = victim.packed.synchronize().tiles(victim.index).view(torch.uint8).reshape(4, bs, -1).numpy()
     for a in range(4):
         assert np.array_equal(got[a], before[a][4 * bs:5 * bs])
     after = host_bytes(k) + host_bytes(v)

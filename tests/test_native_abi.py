@@ -84,8 +84,10 @@ def test_launch_settings_are_validated(lib):
         _native.set_launch(unroll=3)
     with pytest.raises(_native.NativeError):
         _native.set_launch(nontemporal=2)
-    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, block_major=0)
-    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "block_major": 0}
+    with pytest.raises(_native.NativeError):
+        _native.set_launch(order=3)
+    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=2)
+    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "order": 2}
     _native.set_launch(**before)
     assert _native.get_launch() == before
 
