@@ -13,13 +13,16 @@ without NaN codes for fp8). Legs:
   batched      all requests' blocks in ONE direct launch (2P bytes)
 
 ``value`` is the direct leg's algorithmic read+write bandwidth, 2P / step
-time, in GB/s (P = blocks x 2L x T). ``roofline.achieved`` is the algorithmic
-bytes per kv_move launch divided by the average launch duration, both taken
-from HIP events recorded around each launch on the launch stream during the
-timed steps. After timing, every destination tile is compared with its
-source tile on the GPU (the whole workload, bit for bit). ``cpu_baseline``
-times the NumPy restatement of the reference handoff (oracle/) on a bounded
-sample of the same shape on this host, single-threaded.
+time, in GB/s (P = blocks x 2L x T); the step time comes from two HIP events
+around the timed steps on the launch stream, with nothing else added between
+launches. ``roofline.achieved`` is the algorithmic bytes per kv_move launch
+divided by the average launch duration, measured in a second timed pass over
+the same steps by HIP events that ride in each launch's own dispatch packet
+(iekv_profile_start / hipExtLaunchKernelGGL); ``ms_per_request`` comes from
+the same pass. After timing, every destination
+tile is compared with its source tile on the GPU (the whole workload, bit for
+bit). ``cpu_baseline`` times the NumPy restatement of the reference handoff
+(oracle/) on a bounded sample of the same shape on this host, single-threaded.
 """
 from __future__ import annotations
 
@@ -104,54 +107,46 @@ class Legs:
             f"({2 * workload.src_pool_blocks * s.block_bytes / 1e9:.1f} GB) in "
             f"{time.perf_counter() - t0:.1f} s")
 
-    # -- one step of each leg; `events` collects (start, end, bytes, request) per launch ------
-    def _launch(self, fn, events, nbytes, request):
-        torch = self.torch
-        if events is None:
-            fn()
-            return
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(self.stream)
-        fn()
-        b.record(self.stream)
-        events.append((a, b, nbytes, request))
+    # -- one step of each leg, and the (bytes, request) of each launch it makes -------------
+    def plan(self, name: str) -> list[tuple[int, int]]:
+        bb = self.w.shape.block_bytes
+        sizes = [len(t) for t in self.w.src_tables]
+        if name == "direct":
+            return [(2 * n * bb, r) for r, n in enumerate(sizes)]
+        if name == "pack_unpack":
+            return [x for r, n in enumerate(sizes) for x in ((2 * n * bb, r), (2 * n * bb, r))]
+        if name == "batched":
+            return [(2 * sum(sizes) * bb, 0)]
+        return []
 
-    def direct(self, events=None) -> None:
+    def direct(self) -> None:
         from iekv import _native
 
         h = self.stream.cuda_stream
-        bb = self.w.shape.block_bytes
-        for r, (s, d) in enumerate(zip(self.src_ids, self.dst_ids)):
-            n = s.numel()
-            self._launch(lambda: _native.call("iekv_copy_direct", self.src.native.handle,
-                                              self.dst.native.handle, s.data_ptr(),
-                                              d.data_ptr(), n, h), events, 2 * n * bb, r)
+        for s, d in zip(self.src_ids, self.dst_ids):
+            _native.call("iekv_copy_direct", self.src.native.handle, self.dst.native.handle,
+                         s.data_ptr(), d.data_ptr(), s.numel(), h)
 
-    def pack_unpack(self, events=None) -> None:
+    def pack_unpack(self) -> None:
         from iekv import _native
 
         h = self.stream.cuda_stream
-        bb = self.w.shape.block_bytes
         st = self.staging
-        for r, (s, d) in enumerate(zip(self.src_ids, self.dst_ids)):
+        for s, d in zip(self.src_ids, self.dst_ids):
             n = s.numel()
-            self._launch(lambda: _native.call("iekv_pack", self.src.native.handle, s.data_ptr(),
-                                              n, st.data_ptr(), st.numel(), h),
-                         events, 2 * n * bb, r)
-            self._launch(lambda: _native.call("iekv_unpack", self.dst.native.handle,
-                                              d.data_ptr(), n, st.data_ptr(), st.numel(), h),
-                         events, 2 * n * bb, r)
+            _native.call("iekv_pack", self.src.native.handle, s.data_ptr(), n, st.data_ptr(),
+                         st.numel(), h)
+            _native.call("iekv_unpack", self.dst.native.handle, d.data_ptr(), n, st.data_ptr(),
+                         st.numel(), h)
 
-    def batched(self, events=None) -> None:
+    def batched(self) -> None:
         from iekv import _native
 
-        n = self.src_all.numel()
-        self._launch(lambda: _native.call("iekv_copy_direct", self.src.native.handle,
-                                          self.dst.native.handle, self.src_all.data_ptr(),
-                                          self.dst_all.data_ptr(), n, self.stream.cuda_stream),
-                     events, 2 * n * self.w.shape.block_bytes, 0)
+        _native.call("iekv_copy_direct", self.src.native.handle, self.dst.native.handle,
+                     self.src_all.data_ptr(), self.dst_all.data_ptr(), self.src_all.numel(),
+                     self.stream.cuda_stream)
 
-    def plain_copy(self, events=None) -> None:
+    def plain_copy(self) -> None:
         """A contiguous device-to-device copy of a known size (torch copy_), for reference."""
         torch = self.torch
         if not hasattr(self, "_plain"):
@@ -160,7 +155,7 @@ class Legs:
                            torch.zeros(n, dtype=torch.uint8, device=self.src_k[0].device))
             self._plain[0].fill_(7)
         a, b = self._plain
-        self._launch(lambda: b.copy_(a), events, 2 * a.numel(), 0)
+        b.copy_(a)
 
     def host_roundtrip(self, steps: int, warmup: int) -> dict:
         """Offload every moved block to pinned host memory and restore it onto its dst id.
@@ -242,27 +237,47 @@ class Legs:
             t.zero_()
 
 
-def time_leg(legs: Legs, step, steps: int, warmup: int):
+def time_leg(legs: Legs, name: str, steps: int, warmup: int, per_launch: bool = True):
+    """Warm up, then time ``steps`` steps twice.
+
+    Pass 1 (the headline): only two HIP events around the timed steps on the
+    launch stream, so nothing is added between launches. Pass 2 (when
+    ``per_launch``): the same steps again with every kv_move launch timed by the
+    library (iekv_profile_start/stop; the events ride in each launch's own
+    dispatch packet). Returns (ms per step, wall seconds of pass 1,
+    [(launch ms, algorithmic bytes, request)] from pass 2).
+    """
+    from iekv import _native
+
     torch = legs.torch
+    step = getattr(legs, name)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    events: list = []
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(legs.stream)
     for _ in range(steps):
-        step(events)
+        step()
     end.record(legs.stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(end) / steps
-    launches = [(a.elapsed_time(b), nbytes, r) for a, b, nbytes, r in events]
+    plan = legs.plan(name)
+    if not (per_launch and plan):
+        return ms_step, wall, []
+    with _native.LaunchTimer(steps * len(plan)) as timer:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    launches = [(ms, nbytes, r) for ms, (nbytes, r) in zip(timer.durations_ms, plan * steps)]
     return ms_step, wall, launches
 
 
 def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: int, steps: int):
     w = legs.w
+    if not launches:   # not a kv_move leg: one "launch" per step, timed by the step events
+        launches = [(ms_step, bytes_per_step, 0)] * steps
     durations = [ms for ms, _, _ in launches]
     total_ms = sum(durations)
     moved = sum(nbytes for _, nbytes, _ in launches)
@@ -278,10 +293,10 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "kernel_GBps": round(kernel_gbs, 1),
         "launches_per_step": len(launches) // steps,
-        "avg_launch_us": round(1000 * total_ms / max(1, len(launches)), 2),
+        "avg_launch_us": round(1000 * total_ms / max(1, len(durations)), 2),
         "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
     }
-    if name != "batched":
+    if name in ("direct", "pack_unpack"):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
                                  "p50": round(req_ms[len(req_ms) // 2], 4),
                                  "p99": round(req_ms[min(len(req_ms) - 1,
@@ -290,7 +305,7 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
     log(f"[bench] {name:11s} {ms_step:9.3f} ms/step  {gbs:8.1f} GB/s "
         f"({out['pct_hbm_peak']:.1f}% of peak)  kernel {kernel_gbs:8.1f} GB/s  "
         f"{out['avg_launch_us']:.1f} us/launch")
-    return out, kernel_gbs, 1000 * total_ms / max(1, len(launches)), moved / max(1, len(launches))
+    return out, kernel_gbs, 1000 * total_ms / max(1, len(durations)), moved / max(1, len(durations))
 
 
 def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float) -> dict:
@@ -371,7 +386,7 @@ def sweep(legs: Legs, names: list[str]) -> list[dict]:
                         row = {"run_blocks": run, "unroll": unroll, "nontemporal": nt,
                                "order": order}
                         for name in names:
-                            ms, _, _ = time_leg(legs, getattr(legs, name), 3, 1)
+                            ms, _, _ = time_leg(legs, name, 3, 1, per_launch=False)
                             nbytes = 4 * P if name == "pack_unpack" else 2 * P
                             row[name] = round(nbytes / (ms * 1e-3) / 1e9, 1)
                         rows.append(row)
@@ -449,9 +464,8 @@ def main() -> int:
                 verified[name] = legs.verify()
                 log(f"[bench] {name}: destination tiles equal source tiles: {verified[name]}")
             continue
-        step = getattr(legs, name)
         legs.clear_dst()
-        ms, wall, launches = time_leg(legs, step, args.steps, args.warmup)
+        ms, wall, launches = time_leg(legs, name, args.steps, args.warmup)
         nbytes = 4 * P if name == "pack_unpack" else 2 * P
         if name == "plain_copy":
             nbytes = 2 * (4 << 30)

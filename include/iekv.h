@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 2
+#define IEKV_ABI_VERSION 3
 
 enum {
   IEKV_OK = 0,
@@ -140,6 +140,18 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
  * No reference counterpart: a tuning knob for the launches the entry points
  * above make. */
 int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order);
+
+/* Per-launch timing, for measurement (calling thread only). After
+ * iekv_profile_start(max_launches), each of the next max_launches kernel
+ * launches made by the entry points above carries a start/stop event pair in
+ * its own dispatch (hipExtLaunchKernelGGL), so timing adds no packets to the
+ * stream. iekv_profile_stop waits for the last timed launch, writes up to
+ * `capacity` durations in launch order to durations_ms, stores the number of
+ * timed launches in *count and ends the session.
+ * No reference counterpart: the reference times nothing below Python's
+ * perf_counter (ie/bench/harness.py:67-120). */
+int iekv_profile_start(int32_t max_launches);
+int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count);
 
 /* Current launch shape, for reporting. */
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,

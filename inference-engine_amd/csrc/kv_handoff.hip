@@ -14,6 +14,7 @@
 // `U` loads per lane in flight before the matching stores. The data is never
 // interpreted: it moves as 32-bit words, so every KV dtype is bit-exact.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -211,6 +212,27 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
 // Host side
 // ---------------------------------------------------------------------------
 
+// Per-thread launch timing: while a session is open, every kv_move launch is
+// dispatched with hipExtLaunchKernelGGL carrying a start/stop event pair, so the
+// timestamps come from the dispatch packet itself and no marker packets are
+// added to the queue between launches.
+struct Profiler {
+  bool on = false;
+  int device = -1;
+  size_t used = 0;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+
+  void release() {
+    for (auto& e : events) {
+      (void)hipEventDestroy(e.first);
+      (void)hipEventDestroy(e.second);
+    }
+    events.clear();
+  }
+  ~Profiler() { release(); }
+};
+thread_local Profiler g_profiler;
+
 using MoveKernel = void (*)(PoolView, PoolView, const char*, char*, const int32_t*,
                             const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
                             int32_t);
@@ -282,10 +304,19 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
   int vec = 16;
   MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), g_nontemporal.load() != 0, &vec);
   const int32_t tile_vecs = static_cast<int32_t>(tile_bytes / vec);
-  hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
-                     view_of(sp), view_of(dp), src_stage, dst_stage, src_ids, dst_ids,
-                     tile_vecs, n_blocks, n_arrays, run, static_cast<int32_t>(runs),
-                     g_order.load());
+  Profiler& prof = g_profiler;
+  if (prof.on && prof.used < prof.events.size()) {
+    auto& ev = prof.events[prof.used++];
+    hipExtLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
+                          ev.first, ev.second, 0, view_of(sp), view_of(dp), src_stage,
+                          dst_stage, src_ids, dst_ids, tile_vecs, n_blocks, n_arrays, run,
+                          static_cast<int32_t>(runs), g_order.load());
+  } else {
+    hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
+                       view_of(sp), view_of(dp), src_stage, dst_stage, src_ids, dst_ids,
+                       tile_vecs, n_blocks, n_arrays, run, static_cast<int32_t>(runs),
+                       g_order.load());
+  }
   IEKV_HIP(hipGetLastError());
   return IEKV_OK;
 }
@@ -600,6 +631,48 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   }
   // Later copy-stream work that writes staging is ordered after the last unpack.
   IEKV_HIP(hipStreamWaitEvent(copy, unpacked[last], 0));
+  return IEKV_OK;
+}
+
+int iekv_profile_start(int32_t max_launches) {
+  if (max_launches <= 0 || max_launches > (1 << 20))
+    return set_error(IEKV_ERR_INVALID, "max_launches %d out of range", max_launches);
+  Profiler& prof = g_profiler;
+  int device = 0;
+  IEKV_HIP(hipGetDevice(&device));
+  if (prof.device != device) {
+    prof.release();
+    prof.device = device;
+  }
+  while (prof.events.size() < static_cast<size_t>(max_launches)) {
+    hipEvent_t a = nullptr, b = nullptr;
+    IEKV_HIP(hipEventCreate(&a));
+    hipError_t e = hipEventCreate(&b);
+    if (e != hipSuccess) {
+      (void)hipEventDestroy(a);
+      return set_error(IEKV_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(e));
+    }
+    prof.events.emplace_back(a, b);
+  }
+  prof.used = 0;
+  prof.on = true;
+  return IEKV_OK;
+}
+
+int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count) {
+  Profiler& prof = g_profiler;
+  const size_t n = prof.on ? prof.used : 0;
+  prof.on = false;
+  prof.used = 0;
+  if (count) *count = static_cast<int32_t>(n);
+  if (n == 0) return IEKV_OK;
+  IEKV_HIP(hipEventSynchronize(prof.events[n - 1].second));
+  const size_t m = durations_ms ? std::min<size_t>(n, capacity > 0 ? capacity : 0) : 0;
+  for (size_t i = 0; i < m; ++i) {
+    IEKV_HIP(hipEventSynchronize(prof.events[i].second));
+    IEKV_HIP(hipEventElapsedTime(&durations_ms[i], prof.events[i].first,
+                                 prof.events[i].second));
+  }
   return IEKV_OK;
 }
 

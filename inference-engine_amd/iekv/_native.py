@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 IEKV_OK = 0
 IEKV_ERR_INVALID = -1
@@ -36,6 +36,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "iekv_set_launch": (c_int, [c_int32, c_int32, c_int32, c_int32]),
     "iekv_get_launch": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32),
                                 POINTER(c_int32)]),
+    "iekv_profile_start": (c_int, [c_int32]),
+    "iekv_profile_stop": (c_int, [POINTER(ctypes.c_float), c_int32, POINTER(c_int32)]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -132,3 +134,26 @@ def get_launch() -> dict[str, int]:
          ctypes.byref(order))
     return {"run_blocks": run.value, "unroll": unroll.value, "nontemporal": nt.value,
             "order": order.value}
+
+
+class LaunchTimer:
+    """Times every kernel launch the library makes inside a ``with`` block (this thread).
+
+    Uses iekv_profile_start/stop: the start/stop events ride in each launch's
+    own dispatch, so timing adds nothing to the stream between launches.
+    ``durations_ms`` holds one entry per launch, in launch order.
+    """
+
+    def __init__(self, max_launches: int) -> None:
+        self.max_launches = max_launches
+        self.durations_ms: list[float] = []
+
+    def __enter__(self) -> "LaunchTimer":
+        call("iekv_profile_start", self.max_launches)
+        return self
+
+    def __exit__(self, *exc) -> None:
+        out = (ctypes.c_float * self.max_launches)()
+        count = c_int32()
+        call("iekv_profile_stop", out, self.max_launches, ctypes.byref(count))
+        self.durations_ms = list(out[:min(count.value, self.max_launches)])
