@@ -66,10 +66,10 @@ int set_error(int code, const char* fmt, ...) {
 
 // Launch shape. Measured on MI355X over the five benchmark workloads (8 KiB to
 // 64 KiB tiles): one tile per workgroup and streaming (non-temporal) accesses
-// are best or within noise everywhere, deeper unrolling helps slightly on the
-// 16-32 KiB tiles.
+// are best or within noise everywhere; unroll 4, 8 and 16 are within noise of
+// each other, and 8 keeps the kernel at 58 VGPRs (full occupancy).
 std::atomic<int> g_run{0};       // 0 = automatic
-std::atomic<int> g_unroll{16};
+std::atomic<int> g_unroll{8};
 std::atomic<int> g_nontemporal{1};
 // Workgroup order (see Order below): diagonal. Over 12 pool sizes / paddings of
 // the Llama-3-8B shape it averaged 6.09 TB/s against 5.78 (array-major) and
@@ -106,14 +106,30 @@ __device__ __forceinline__ char* array_base(const PoolView& p, int a) {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Tile data is addressed through global (address space 1) pointers so the
+// compiler emits global_load/global_store rather than FLAT accesses, which
+// would also have to be waited for on the LDS counter.
+template <typename T>
+using gptr = __attribute__((address_space(1))) T*;
+
+template <typename V>
+__device__ __forceinline__ gptr<const V> as_global(const char* p) {
+  return (gptr<const V>)(reinterpret_cast<const V*>(p));
+}
+
+template <typename V>
+__device__ __forceinline__ gptr<V> as_global(char* p) {
+  return (gptr<V>)(reinterpret_cast<V*>(p));
+}
+
 template <typename V, bool NT>
-__device__ __forceinline__ V load_vec(const V* p) {
+__device__ __forceinline__ V load_vec(gptr<const V> p) {
   if constexpr (NT) return __builtin_nontemporal_load(p);
   else return *p;
 }
 
 template <typename V, bool NT>
-__device__ __forceinline__ void store_vec(V* p, V v) {
+__device__ __forceinline__ void store_vec(gptr<V> p, V v) {
   if constexpr (NT) __builtin_nontemporal_store(v, p);
   else *p = v;
 }
@@ -121,7 +137,7 @@ __device__ __forceinline__ void store_vec(V* p, V v) {
 // Move one tile of `n` vectors from s to d. Lane t handles vectors
 // t, t+256, ..., issuing U loads before the U stores that consume them.
 template <typename V, int U, bool NT>
-__device__ __forceinline__ void move_tile(const V* __restrict__ s, V* __restrict__ d, int n) {
+__device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
   const int t = threadIdx.x;
   int v = t;
   const int full = n - (U - 1) * kThreads;  // v < full: all U vectors of the step are in range
@@ -204,7 +220,7 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
     } else {
       d = dst_stage + (static_cast<int64_t>(first + j) * n_arrays + a) * tile_bytes;
     }
-    move_tile<V, U, NT>(reinterpret_cast<const V*>(s), reinterpret_cast<V*>(d), tile_vecs);
+    move_tile<V, U, NT>(as_global<V>(s), as_global<V>(d), tile_vecs);
   }
 }
 
