@@ -177,3 +177,23 @@ def test_evictions_are_offloaded_in_batches(gpu):
     assert 0 < copier.offload_launches < reads
     print(f"{reads} evictions offloaded in {copier.offload_launches} launches "
           f"({copier.blocks_offloaded} blocks copied)")
+
+
+@pytest.mark.parametrize("mode", ["pack", "direct"])
+def test_a_transfer_through_the_wire_format_decodes_identically(gpu, mode):
+    from iekv.serve.disaggregated import DisaggregatedEngine
+    from iekv.serve.wire import from_wire, to_wire
+
+    m = model(gpu, torch.bfloat16)
+    plain = DisaggregatedEngine(m, engine_config()).generate(G["prompts"], max_new_tokens=8)
+    engine = DisaggregatedEngine(m, engine_config(), mode=mode)
+    seqs = []
+    for prompt in G["prompts"]:
+        header, payload = to_wire(engine.prefill.prefill(prompt))
+        received = from_wire(header, payload.clone())      # what a remote decode GPU rebuilds
+        seqs.append(engine.decode.admit(received, max_new_tokens=8))
+    dec = engine.decode.engine
+    while dec.scheduler.has_work:
+        dec.step()
+    assert [s.token_ids[s.num_prompt:] for s in seqs] == plain
+    assert engine.prefill.engine.blocks.num_free == engine.prefill.engine.blocks.num_total
