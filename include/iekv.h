@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 3
+#define IEKV_ABI_VERSION 4
 
 enum {
   IEKV_OK = 0,
@@ -99,6 +99,25 @@ int iekv_pack(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
  * single-block restore write (ie/core/block_manager.py:162). */
 int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                 const void* staging, int64_t staging_bytes, hipStream_t stream);
+
+/* Slot scatter of one layer's new K/V rows: row i of k (and of v), each
+ * tile_bytes/block_size bytes, contiguous [n_tokens][row], lands in row
+ * slots[i] (int64, device memory) of K array `layer` (and V array L+layer).
+ * Rows whose slot is outside the pool are skipped.
+ * Replaces: write_kv, `k_cache[slots] = k` (ie/kernels/reference.py:45-51) /
+ * `index_copy_` (ie/kernels/torch_backend.py:13-16). */
+int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, const void* k,
+                     const void* v, const int64_t* slots, int32_t n_tokens, hipStream_t stream);
+
+/* Paged gather of one array's context: out row j (j < context_len) = row
+ * block_table[j / block_size] * block_size + j % block_size of array `array`;
+ * out is [context_len][row] bytes (out_bytes checked), block_table int32 in
+ * device memory. Rows of out-of-range blocks are left untouched.
+ * Replaces: gather_context (ie/kernels/reference.py:54-63,
+ * ie/kernels/torch_backend.py:19-24). */
+int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
+                     const int32_t* block_table, int32_t context_len, void* out,
+                     int64_t out_bytes, hipStream_t stream);
 
 /* Offload to host: pack the blocks chunk by chunk into the device staging
  * buffer (two slots when it holds at least two blocks, else one) on

@@ -224,6 +224,47 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
   }
 }
 
+// Row kernels on either side of the handoff. A pool row is one token's
+// H x D values of one array (tile_bytes / block_size bytes); row r of array a
+// lives at base(a) + r * row_bytes, i.e. slot r of the reference's [N*bs, H, D]
+// array. One wave moves one row with lane-contiguous vectors; a workgroup
+// (four waves) moves four rows.
+constexpr int kWave = 64;
+constexpr int kRowsPerGroup = kThreads / kWave;
+
+// write_kv: k/v row i (contiguous [n, row]) -> row slots[i] of arrays a_k / a_v.
+template <typename V>
+__global__ void __launch_bounds__(kThreads)
+kv_scatter_rows(PoolView pool, int32_t a_k, int32_t a_v, const char* __restrict__ k,
+                const char* __restrict__ v, const int64_t* __restrict__ slots, int32_t n,
+                int32_t row_vecs, int64_t pool_rows) {
+  const int i = blockIdx.x * kRowsPerGroup + threadIdx.x / kWave;
+  if (i >= n) return;
+  const int64_t slot = slots[i];
+  if (slot < 0 || slot >= pool_rows) return;  // never address outside the pool
+  const bool is_v = blockIdx.y != 0;
+  const int64_t row_bytes = static_cast<int64_t>(row_vecs) * sizeof(V);
+  gptr<const V> src = as_global<V>((is_v ? v : k) + i * row_bytes);
+  gptr<V> dst = as_global<V>(array_base(pool, is_v ? a_v : a_k) + slot * row_bytes);
+  for (int e = threadIdx.x % kWave; e < row_vecs; e += kWave) dst[e] = src[e];
+}
+
+// gather_context: out row j = row (table[j / bs] * bs + j % bs) of array a, j < n.
+template <typename V>
+__global__ void __launch_bounds__(kThreads)
+kv_gather_rows(PoolView pool, int32_t a, const int32_t* __restrict__ table, int32_t bs,
+               char* __restrict__ out, int32_t n, int32_t row_vecs) {
+  const int j = blockIdx.x * kRowsPerGroup + threadIdx.x / kWave;
+  if (j >= n) return;
+  const int32_t block = table[j / bs];
+  if (block < 0 || block >= pool.num_blocks) return;
+  const int64_t row_bytes = static_cast<int64_t>(row_vecs) * sizeof(V);
+  const int64_t row = static_cast<int64_t>(block) * bs + j % bs;
+  gptr<const V> src = as_global<V>(array_base(pool, a) + row * row_bytes);
+  gptr<V> dst = as_global<V>(out + j * row_bytes);
+  for (int e = threadIdx.x % kWave; e < row_vecs; e += kWave) dst[e] = src[e];
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -335,6 +376,14 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
   }
   IEKV_HIP(hipGetLastError());
   return IEKV_OK;
+}
+
+int row_align(int64_t row_bytes, int pool_align, std::initializer_list<const void*> ptrs) {
+  int align = 16;
+  while (align > 1 && (row_bytes % align)) align >>= 1;
+  align = std::min(align, pool_align);
+  for (const void* p : ptrs) align = std::min(align, align_of_ptr(reinterpret_cast<uint64_t>(p)));
+  return align;
 }
 
 int check_pool(const iekv_pool* p, const char* what) {
@@ -540,6 +589,80 @@ int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   return launch_move<false, true>(nullptr, dst, static_cast<const char*>(staging), nullptr,
                                   nullptr, dst_ids, n_blocks, dst->tile_bytes, dst->n_arrays,
                                   align, stream);
+}
+
+int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, const void* k,
+                     const void* v, const int64_t* slots, int32_t n_tokens, hipStream_t stream) {
+  int rc;
+  if ((rc = check_pool(pool, "destination"))) return rc;
+  const int32_t layers = pool->n_arrays / 2;
+  if (pool->n_arrays % 2 || layer < 0 || layer >= layers)
+    return set_error(IEKV_ERR_INVALID, "layer %d out of range for %d layers", layer, layers);
+  if (block_size <= 0 || pool->tile_bytes % block_size)
+    return set_error(IEKV_ERR_INVALID, "block_size %d does not divide the %lld-byte tile",
+                     block_size, static_cast<long long>(pool->tile_bytes));
+  if (n_tokens < 0) return set_error(IEKV_ERR_INVALID, "n_tokens is negative (%d)", n_tokens);
+  if (n_tokens == 0) return IEKV_OK;
+  if (!k || !v || !slots) return set_error(IEKV_ERR_INVALID, "k, v or slots is null");
+  DeviceGuard guard(pool->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", pool->device);
+  const int64_t row_bytes = pool->tile_bytes / block_size;
+  const int align = row_align(row_bytes, pool->align, {k, v});
+  const dim3 grid((n_tokens + kRowsPerGroup - 1) / kRowsPerGroup, 2);
+  const int64_t pool_rows = pool->num_blocks * block_size;
+  const char* kc = static_cast<const char*>(k);
+  const char* vc = static_cast<const char*>(v);
+  const PoolView view = view_of(pool);
+  const int32_t ak = layer, av = layers + layer;
+#define IEKV_SCATTER(T)                                                                      \
+  hipLaunchKernelGGL(kv_scatter_rows<T>, grid, dim3(kThreads), 0, stream, view, ak, av, kc, \
+                     vc, slots, n_tokens, static_cast<int32_t>(row_bytes / sizeof(T)),       \
+                     pool_rows)
+  if (align >= 16) IEKV_SCATTER(u32x4);
+  else if (align >= 8) IEKV_SCATTER(u32x2);
+  else if (align >= 4) IEKV_SCATTER(uint32_t);
+  else if (align >= 2) IEKV_SCATTER(uint16_t);
+  else IEKV_SCATTER(uint8_t);
+#undef IEKV_SCATTER
+  IEKV_HIP(hipGetLastError());
+  return IEKV_OK;
+}
+
+int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
+                     const int32_t* block_table, int32_t context_len, void* out,
+                     int64_t out_bytes, hipStream_t stream) {
+  int rc;
+  if ((rc = check_pool(pool, "source"))) return rc;
+  if (array < 0 || array >= pool->n_arrays)
+    return set_error(IEKV_ERR_INVALID, "array %d out of range for %d arrays", array,
+                     pool->n_arrays);
+  if (block_size <= 0 || pool->tile_bytes % block_size)
+    return set_error(IEKV_ERR_INVALID, "block_size %d does not divide the %lld-byte tile",
+                     block_size, static_cast<long long>(pool->tile_bytes));
+  if (context_len < 0)
+    return set_error(IEKV_ERR_INVALID, "context_len is negative (%d)", context_len);
+  if (context_len == 0) return IEKV_OK;
+  const int64_t row_bytes = pool->tile_bytes / block_size;
+  if ((rc = check_buffer(out, out_bytes, row_bytes * context_len, "output"))) return rc;
+  if (!block_table) return set_error(IEKV_ERR_INVALID, "block_table is null");
+  DeviceGuard guard(pool->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", pool->device);
+  const int align = row_align(row_bytes, pool->align, {out});
+  const dim3 grid((context_len + kRowsPerGroup - 1) / kRowsPerGroup);
+  char* oc = static_cast<char*>(out);
+  const PoolView view = view_of(pool);
+#define IEKV_GATHER(T)                                                                      \
+  hipLaunchKernelGGL(kv_gather_rows<T>, grid, dim3(kThreads), 0, stream, view, array,      \
+                     block_table, block_size, oc, context_len,                              \
+                     static_cast<int32_t>(row_bytes / sizeof(T)))
+  if (align >= 16) IEKV_GATHER(u32x4);
+  else if (align >= 8) IEKV_GATHER(u32x2);
+  else if (align >= 4) IEKV_GATHER(uint32_t);
+  else if (align >= 2) IEKV_GATHER(uint16_t);
+  else IEKV_GATHER(uint8_t);
+#undef IEKV_GATHER
+  IEKV_HIP(hipGetLastError());
+  return IEKV_OK;
 }
 
 int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,

@@ -101,6 +101,12 @@ class BlockManager:
         total = self.blocks_reused + self.blocks_computed
         return self.blocks_reused / total if total else 0.0
 
+    def flush_pending(self) -> None:
+        """Let a batching offload copier issue its queued reads (before a pool write)."""
+        flush = getattr(self.copier, "flush", None)
+        if flush is not None:
+            flush()
+
     # -- block life cycle --------------------------------------------------
     def _forget(self, block: Block) -> None:
         """Drop a block's hash; offload it first if it is that hash's canonical holder."""

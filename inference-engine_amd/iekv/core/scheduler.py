@@ -5,6 +5,12 @@ transitions the workers rely on (``waiting`` -> ``running`` -> ``finished``),
 decode-time ``append_slot`` growth of block tables, recompute preemption, and
 hashing of computed blocks after every step. Behaviour follows
 ie/core/scheduler.py:38-162.
+
+With a ``swapper`` (a copier whose payloads live in host memory), preemption
+swaps instead of recomputing: the victim's computed blocks are packed out to
+the host and freed, and when the sequence is scheduled again they are
+restored into fresh blocks, so its KV is never recomputed. Without one the
+reference's recompute preemption is used unchanged.
 """
 from __future__ import annotations
 
@@ -41,14 +47,17 @@ class SchedulerStats:
     tokens_prefilled: int = 0
     tokens_decoded: int = 0
     tokens_reused_from_cache: int = 0
+    swapped_out: int = 0
+    swapped_in: int = 0
 
 
 class Scheduler:
     """ie/core/scheduler.py:38-162."""
 
     def __init__(self, block_manager: BlockManager, max_batch_sequences: int = 256,
-                 max_batch_tokens: int = 8192) -> None:
+                 max_batch_tokens: int = 8192, swapper=None) -> None:
         self.blocks = block_manager
+        self.swapper = swapper
         self.max_batch_sequences = max_batch_sequences
         self.max_batch_tokens = max_batch_tokens
         self.waiting: deque[Sequence] = deque()
@@ -83,8 +92,12 @@ class Scheduler:
         budget = self.max_batch_tokens
         while self.waiting and len(batch) < self.max_batch_sequences and budget > 0:
             seq = self.waiting[0]
-            if not seq.block_table and not self.blocks.can_allocate(seq):
-                break
+            if not seq.block_table:
+                if seq.swapped is not None:
+                    if not self._swap_in(seq):
+                        break
+                elif not self.blocks.can_allocate(seq):
+                    break
             remaining = self._uncomputed_after_cache(seq)
             if remaining > budget and batch:
                 break
@@ -124,10 +137,47 @@ class Scheduler:
         return batch
 
     def _preempt(self, seq: Sequence) -> None:
+        if self.swapper is not None and seq.num_computed > 0:
+            self._swap_out(seq)
+            return
         self.blocks.free(seq)
         seq.discard_computation()
         self.waiting.appendleft(seq)
         self.stats.preemptions += 1
+
+    # -- swap preemption ---------------------------------------------------------
+    def _swap_out(self, seq: Sequence) -> None:
+        kept = -(-seq.num_computed // self.blocks.block_size)
+        ids = seq.block_table[:kept]
+        if hasattr(self.swapper, "read_blocks"):
+            payload = self.swapper.read_blocks(ids, location="host")   # one batched offload
+        else:
+            payload = [self.swapper.read_block(b) for b in ids]
+        seq.swapped = (payload, seq.num_computed)
+        self.blocks.free(seq)                 # the blocks may be reused at once
+        seq.status = Status.WAITING
+        seq.num_scheduled = 0
+        self.waiting.appendleft(seq)
+        self.stats.preemptions += 1
+        self.stats.swapped_out += 1
+
+    def _swap_in(self, seq: Sequence) -> bool:
+        if self.blocks.num_free < seq.num_blocks:
+            return False
+        payload, num_computed = seq.swapped
+        if not self.blocks.reserve(seq, seq.num_blocks):
+            raise RuntimeError("free blocks vanished during swap-in")
+        kept = -(-num_computed // self.blocks.block_size)
+        self.blocks.flush_pending()           # evictions above read their victims first
+        if hasattr(self.swapper, "write_blocks"):
+            self.swapper.write_blocks(seq.block_table[:kept], payload)
+        else:
+            for block_id, block_payload in zip(seq.block_table[:kept], payload):
+                self.swapper.write_block(block_id, block_payload)
+        seq.num_computed = num_computed
+        seq.swapped = None
+        self.stats.swapped_in += 1
+        return True
 
     def finish_step(self, batch: Batch, token_ids: list[int]) -> list[Sequence]:
         if len(token_ids) != len(batch):

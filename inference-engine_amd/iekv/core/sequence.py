@@ -39,6 +39,9 @@ class Sequence:
         self.num_computed = 0      # tokens whose KV is in the cache
         self.num_scheduled = 0     # tokens the current step will compute
         self.block_table: list[int] = []
+        # Set while swapped out by a swap preemption: (host payload of the first
+        # ceil(num_computed / block_size) blocks, num_computed at swap-out).
+        self.swapped: tuple | None = None
         self.max_new_tokens = max_new_tokens
         self.temperature = temperature
         self.eos_id = eos_id

@@ -431,9 +431,17 @@ class HipSlotCopier:
 
 
 def copier_for(k_caches, v_caches, block_size: int, role: str = "transfer") -> HipSlotCopier:
-    """Default copier factory of the engine: device payloads for transfers, host for offload."""
+    """Default copier factory of the engine.
+
+    ``transfer``: device payloads (the handoff); ``offload``: host payloads with
+    batched (deferred) single-block reads (the tier); ``swap``: host payloads,
+    read at once (swap preemption).
+    """
+    if role not in ("transfer", "offload", "swap"):
+        raise ValueError(f"unknown copier role {role!r}")
     return HipSlotCopier(k_caches, v_caches, block_size,
-                         payload_location="host" if role == "offload" else "device")
+                         payload_location="device" if role == "transfer" else "host",
+                         defer_reads=(role == "offload"))
 
 
 def stack_payloads(payloads: Iterable[BlockPayload]) -> PackedBlocks:

@@ -27,7 +27,11 @@ CopierFactory = Callable[[Any, Any, int, str], Any]
 
 @dataclass(slots=True)
 class EngineConfig:
-    """ie/engine/engine.py:17-25. ``capture_graphs`` is accepted and ignored here."""
+    """ie/engine/engine.py:17-25. ``capture_graphs`` is accepted and ignored here.
+
+    ``preemption`` is this build's addition: ``"recompute"`` (the reference's
+    behaviour) or ``"swap"`` (preempted sequences keep their KV in host memory).
+    """
 
     block_size: int = 16
     num_blocks: int = 1024
@@ -36,6 +40,7 @@ class EngineConfig:
     seed: int = 0
     offload_blocks: int = 0
     capture_graphs: bool = False
+    preemption: str = "recompute"
 
 
 def sample_from_logits(logits: np.ndarray, temperatures: np.ndarray,
@@ -63,13 +68,20 @@ class Engine:
         self.model = model
         self.config = config or EngineConfig()
         self.copier_factory = copier_factory or default_copier_factory
+        if self.config.preemption not in ("recompute", "swap"):
+            raise ValueError("preemption must be 'recompute' or 'swap'")
         self.blocks = BlockManager(self.config.num_blocks, self.config.block_size)
-        self.scheduler = Scheduler(self.blocks,
-                                   max_batch_sequences=self.config.max_batch_sequences,
-                                   max_batch_tokens=self.config.max_batch_tokens)
         self.generator = np.random.default_rng(self.config.seed)
         self.k_caches, self.v_caches = model.allocate_caches(self.config.num_blocks,
                                                              self.config.block_size)
+        self.swapper = None
+        if self.config.preemption == "swap":
+            self.swapper = self.copier_factory(self.k_caches, self.v_caches,
+                                               self.config.block_size, "swap")
+        self.scheduler = Scheduler(self.blocks,
+                                   max_batch_sequences=self.config.max_batch_sequences,
+                                   max_batch_tokens=self.config.max_batch_tokens,
+                                   swapper=self.swapper)
         self.copier = None
         if self.config.offload_blocks > 0:
             self.copier = self.copier_factory(self.k_caches, self.v_caches,
@@ -94,9 +106,7 @@ class Engine:
         model's forward pass, an admitted transfer), so every queued read sees
         the bytes the block held when it was evicted.
         """
-        flush = getattr(self.copier, "flush", None)
-        if flush is not None:
-            flush()
+        self.blocks.flush_pending()
 
     def forward(self, batch):
         self.flush_offloads()

@@ -1,0 +1,80 @@
+"""Slot-level KV access on either side of the handoff, through libiekv.
+
+``write_slots`` is the prefill side: it scatters a step's new K/V rows into the
+pool by slot, as the reference's ``write_kv`` does (ie/kernels/reference.py:45-51,
+ie/kernels/torch_backend.py:13-16). ``gather_rows`` is the decode side: it reads a
+sequence's context back through its block table, as ``gather_context`` does
+(ie/kernels/reference.py:54-63, ie/kernels/torch_backend.py:19-24). Slot
+``r`` is row ``r`` of a layer's ``[N*bs, H, D]`` array, so both address the same
+bytes the handoff moves.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native
+from .pools import KVPool
+
+
+def _device_slots(slots, device: torch.device) -> torch.Tensor:
+    if isinstance(slots, torch.Tensor):
+        t = slots.to(device=device, dtype=torch.int64)
+    else:
+        t = torch.as_tensor(slots, dtype=torch.int64, device=device)
+    return t.contiguous()
+
+
+def write_slots(pool: KVPool, layer: int, k: torch.Tensor, v: torch.Tensor, slots) -> None:
+    """Scatter rows ``k[i]``, ``v[i]`` ([n, H, D]) into slot ``slots[i]`` of ``layer``.
+
+    The rows are cast to the cache dtype first (as ``index_copy_`` of
+    ``k.to(cache dtype)`` does); slots are range-checked on the host when given
+    as a list.
+    """
+    n = k.shape[0]
+    if v.shape[0] != n or len(slots) != n:
+        raise ValueError(f"{len(slots)} slots for {n} K rows and {v.shape[0]} V rows")
+    if tuple(k.shape[1:]) != pool.tile_shape[1:] or tuple(v.shape[1:]) != pool.tile_shape[1:]:
+        raise ValueError(f"rows of shape {tuple(k.shape[1:])} do not fit a pool of "
+                         f"{pool.tile_shape[1:]}")
+    if not 0 <= layer < pool.num_layers:
+        raise IndexError(f"layer {layer} out of range for {pool.num_layers} layers")
+    if not isinstance(slots, torch.Tensor):
+        rows = pool.num_blocks * pool.block_size
+        bad = [s for s in slots if not 0 <= int(s) < rows]
+        if bad:
+            raise IndexError(f"slot {bad[0]} out of range for a pool of {rows} slots")
+    kc = k.to(device=pool.device, dtype=pool.dtype).contiguous()
+    vc = v.to(device=pool.device, dtype=pool.dtype).contiguous()
+    st = _device_slots(slots, pool.device)
+    stream = torch.cuda.current_stream(pool.device)
+    _native.call("iekv_write_slots", pool.native.handle, layer, pool.block_size, kc.data_ptr(),
+                 vc.data_ptr(), st.data_ptr(), n, stream.cuda_stream)
+
+
+def gather_rows(pool: KVPool, array: int, block_table, context_len: int) -> torch.Tensor:
+    """Rows ``0..context_len-1`` of a sequence in array ``array`` (K of layer l is l, V is L+l).
+
+    Returns a new ``[context_len, H, D]`` tensor of the cache dtype. Raises
+    IndexError when the table is too short for ``context_len`` (as the
+    reference does) or holds a block outside the pool.
+    """
+    bs = pool.block_size
+    needed = -(-context_len // bs)
+    if isinstance(block_table, torch.Tensor):
+        table = block_table.to(dtype=torch.int32)
+        if table.numel() < needed:
+            raise IndexError(f"context of {context_len} needs {needed} blocks, table has "
+                             f"{table.numel()}")
+        table = table[:needed].to(pool.device).contiguous()
+    else:
+        if needed > len(block_table):
+            raise IndexError(f"context of {context_len} needs {needed} blocks, table has "
+                             f"{len(block_table)}")
+        table = pool.block_ids(list(block_table[:needed]), what="context block")
+    out = torch.empty((context_len, *pool.tile_shape[1:]), dtype=pool.dtype, device=pool.device)
+    stream = torch.cuda.current_stream(pool.device)
+    _native.call("iekv_gather_rows", pool.native.handle, array, bs, table.data_ptr(),
+                 context_len, out.data_ptr(), out.numel() * out.element_size(),
+                 stream.cuda_stream)
+    return out

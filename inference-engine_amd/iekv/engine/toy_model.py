@@ -9,7 +9,9 @@ shaped like the reference's toy transformer (ie/model/transformer.py:12-115:
 RMSNorm, GQA attention with interleaved rotary embeddings, SwiGLU MLP; weights
 drawn from ``numpy.random.default_rng(seed)`` in the same order). Attention
 math runs in float32 whatever the cache dtype. It is support code: the
-handoff never calls it.
+handoff never calls it. With ``hip_kv=True`` its KV writes and context reads go
+through libiekv's slot kernels (``iekv.engine.slots``) instead of torch's
+``index_copy_`` / ``index_select``.
 """
 from __future__ import annotations
 
@@ -96,10 +98,12 @@ class ToyTransformer:
     """Paged toy decoder on ``device`` with KV caches of ``cache_dtype``."""
 
     def __init__(self, config: ModelConfig, seed: int = 0, device: str | torch.device = "cuda",
-                 cache_dtype: torch.dtype = torch.float32) -> None:
+                 cache_dtype: torch.dtype = torch.float32, hip_kv: bool = False) -> None:
         self.config = config
         self.device = torch.device(device)
         self.cache_dtype = cache_dtype
+        self.hip_kv = hip_kv
+        self._pools: dict = {}
         rng = np.random.default_rng(seed)
         scale = 1.0 / np.sqrt(config.hidden_size)
 
@@ -123,20 +127,41 @@ class ToyTransformer:
         return allocate_pool(num_blocks, block_size, c.num_layers, c.num_kv_heads, c.head_dim,
                              dtype=self.cache_dtype, device=self.device)
 
+    def _pool(self, k_caches, v_caches, block_size: int):
+        from .pools import KVPool
+
+        key = (k_caches[0].data_ptr(), v_caches[0].data_ptr(), block_size)
+        pool = self._pools.get(key)
+        if pool is None:
+            pool = self._pools[key] = KVPool(k_caches, v_caches, block_size)
+        return pool
+
+    def _context(self, cache: torch.Tensor, array: int, pool, table: list[int],
+                 context_len: int, block_size: int) -> torch.Tensor:
+        if pool is not None:
+            from .slots import gather_rows
+
+            return gather_rows(pool, array, table, context_len)
+        needed = -(-context_len // block_size)
+        blocks = torch.as_tensor(table[:needed], device=self.device, dtype=torch.long)
+        within = torch.arange(block_size, device=self.device)
+        slots = (blocks[:, None] * block_size + within[None, :]).reshape(-1)[:context_len]
+        return cache.index_select(0, slots)
+
     def _attend(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                layout: BatchLayout, block_size: int) -> torch.Tensor:
+                layout: BatchLayout, block_size: int, layer: int = 0,
+                pool=None) -> torch.Tensor:
         c = self.config
         group = c.num_heads // c.num_kv_heads
         outputs = []
         start = 0
-        within = torch.arange(block_size, device=self.device)
         for table, context_len, query_len in zip(layout.block_tables, layout.context_lens,
                                                  layout.query_lens):
-            needed = -(-context_len // block_size)
-            blocks = torch.as_tensor(table[:needed], device=self.device, dtype=torch.long)
-            slots = (blocks[:, None] * block_size + within[None, :]).reshape(-1)[:context_len]
-            k = k_cache.index_select(0, slots).float().repeat_interleave(group, dim=1)
-            v = v_cache.index_select(0, slots).float().repeat_interleave(group, dim=1)
+            k = self._context(k_cache, layer, pool, table, context_len, block_size)
+            v = self._context(v_cache, c.num_layers + layer, pool, table, context_len,
+                              block_size)
+            k = k.float().repeat_interleave(group, dim=1)
+            v = v.float().repeat_interleave(group, dim=1)
             # [heads, tokens, dim] operands, made contiguous before the batched products.
             qh = q[start:start + query_len].permute(1, 0, 2).contiguous()
             kt = k.permute(1, 2, 0).contiguous()
@@ -157,16 +182,22 @@ class ToyTransformer:
         positions = torch.as_tensor(layout.positions, device=self.device, dtype=torch.long)
         slots = torch.as_tensor(layout.slot_mapping, device=self.device, dtype=torch.long)
         x = self.embedding[tokens]
-        for layer, k_cache, v_cache in zip(self.layers, k_caches, v_caches):
+        pool = self._pool(k_caches, v_caches, block_size) if self.hip_kv else None
+        for index, (layer, k_cache, v_cache) in enumerate(zip(self.layers, k_caches, v_caches)):
             normed = _rms_norm(x, layer.attn_norm, c.norm_eps)
             q = (normed @ layer.q_proj).view(-1, c.num_heads, c.head_dim)
             k = (normed @ layer.k_proj).view(-1, c.num_kv_heads, c.head_dim)
             v = (normed @ layer.v_proj).view(-1, c.num_kv_heads, c.head_dim)
             q = _rope(q, positions, self.cos, self.sin, c.rope_halved)
             k = _rope(k, positions, self.cos, self.sin, c.rope_halved)
-            k_cache.index_copy_(0, slots, k.to(k_cache.dtype))
-            v_cache.index_copy_(0, slots, v.to(v_cache.dtype))
-            attended = self._attend(q, k_cache, v_cache, layout, block_size)
+            if pool is not None:
+                from .slots import write_slots
+
+                write_slots(pool, index, k, v, slots)
+            else:
+                k_cache.index_copy_(0, slots, k.to(k_cache.dtype))
+                v_cache.index_copy_(0, slots, v.to(v_cache.dtype))
+            attended = self._attend(q, k_cache, v_cache, layout, block_size, index, pool)
             x = x + attended.reshape(-1, c.num_heads * c.head_dim) @ layer.o_proj
             normed = _rms_norm(x, layer.mlp_norm, c.norm_eps)
             gate = normed @ layer.gate_proj

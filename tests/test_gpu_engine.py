@@ -197,3 +197,26 @@ def test_a_transfer_through_the_wire_format_decodes_identically(gpu, mode):
         dec.step()
     assert [s.token_ids[s.num_prompt:] for s in seqs] == plain
     assert engine.prefill.engine.blocks.num_free == engine.prefill.engine.blocks.num_total
+
+
+def test_swap_preemption_on_gpu_keeps_tokens(gpu):
+    from iekv.engine.copier import HipSlotCopier
+    from iekv.engine.engine import Engine, EngineConfig
+    from iekv.engine.toy_model import ModelConfig, ToyTransformer
+
+    small = ModelConfig(vocab_size=64, hidden_size=32, num_layers=2, num_heads=4,
+                        num_kv_heads=2, head_dim=8, intermediate_size=64)
+    prompts = [list(range(i, i + 12)) for i in range(4)]
+
+    def run(num_blocks, preemption):
+        m = ToyTransformer(small, seed=0, device=gpu, cache_dtype=torch.bfloat16)
+        e = Engine(m, EngineConfig(block_size=8, num_blocks=num_blocks, max_batch_tokens=256,
+                                   preemption=preemption))
+        return e.generate(prompts, max_new_tokens=10, temperature=0.0), e
+
+    expected, _ = run(256, "recompute")
+    recompute, _ = run(8, "recompute")
+    swapped, e = run(8, "swap")
+    assert isinstance(e.swapper, HipSlotCopier) and e.swapper.payload_location == "host"
+    assert swapped == recompute == expected
+    assert e.scheduler.stats.swapped_in == e.scheduler.stats.swapped_out > 0

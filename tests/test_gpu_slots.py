@@ -1,0 +1,112 @@
+"""Slot scatter (write_kv) and paged gather (gather_context) kernels vs the NumPy oracle (GPU)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.slots import gather_context, write_kv
+
+pytestmark = pytest.mark.gpu
+
+CASES = [  # block_size, heads, dim, dtype
+    (16, 8, 128, torch.bfloat16),
+    (16, 2, 16, torch.float32),
+    (4, 1, 2, torch.float32),
+    (3, 1, 5, torch.float16),     # 10-byte rows: 2-byte vectors
+    (16, 8, 128, torch.float8_e4m3fn),
+    (5, 3, 3, torch.uint8),       # 9-byte rows
+]
+
+
+def as_np(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.uint8).cpu().numpy().copy()
+
+
+def random_pool(num_blocks, bs, heads, dim, dtype, device, layers=2, seed=0):
+    from iekv.engine.pools import KVPool, allocate_pool
+
+    k, v = allocate_pool(num_blocks, bs, layers, heads, dim, dtype=dtype, device=device,
+                         zero=False)
+    k[0]._base.view(torch.uint8).random_(0, 256,
+                                          generator=torch.Generator(device).manual_seed(seed))
+    return k, v, KVPool(k, v, bs)
+
+
+def random_rows(n, heads, dim, dtype, device, seed):
+    raw = torch.randint(0, 256, (n, heads, dim * torch.tensor([], dtype=dtype).element_size()),
+                        dtype=torch.uint8, device=device,
+                        generator=torch.Generator(device).manual_seed(seed))
+    return raw.view(dtype)
+
+
+@pytest.mark.parametrize("bs,heads,dim,dtype", CASES)
+def test_write_slots_matches_write_kv(gpu, bs, heads, dim, dtype):
+    from iekv.engine.slots import write_slots
+
+    k, v, pool = random_pool(20, bs, heads, dim, dtype, gpu, seed=1)
+    oracle_k = [as_np(t) for t in k]
+    oracle_v = [as_np(t) for t in v]
+    rng = np.random.default_rng(2)
+    slots = [int(s) for s in rng.permutation(20 * bs)[:13]]
+    for layer in range(2):
+        kr = random_rows(13, heads, dim, dtype, gpu, seed=10 + layer)
+        vr = random_rows(13, heads, dim, dtype, gpu, seed=20 + layer)
+        write_slots(pool, layer, kr, vr, slots)
+        write_kv(as_np(kr), as_np(vr), oracle_k[layer], oracle_v[layer], slots)
+    torch.cuda.synchronize()
+    for got, want in zip(k + v, oracle_k + oracle_v):
+        assert np.array_equal(as_np(got), want)
+
+
+@pytest.mark.parametrize("bs,heads,dim,dtype", CASES)
+def test_gather_rows_matches_gather_context(gpu, bs, heads, dim, dtype):
+    from iekv.engine.slots import gather_rows
+
+    k, v, pool = random_pool(20, bs, heads, dim, dtype, gpu, seed=3)
+    rng = np.random.default_rng(4)
+    for context_len in (1, bs, 3 * bs + 1, 7 * bs):
+        needed = -(-context_len // bs)
+        table = [int(b) for b in rng.permutation(20)[:needed]] + [-1, -1]  # padded like layouts
+        for array, cache in enumerate(k + v):
+            got = gather_rows(pool, array, table, context_len)
+            want = gather_context(as_np(cache), table, context_len, bs)
+            assert np.array_equal(as_np(got), want), (context_len, array)
+
+
+def test_slot_calls_validate_before_launch(gpu):
+    from iekv.engine.slots import gather_rows, write_slots
+
+    k, v, pool = random_pool(4, 4, 1, 2, torch.float32, gpu)
+    rows = torch.zeros(2, 1, 2, device=gpu)
+    with pytest.raises(IndexError):
+        write_slots(pool, 0, rows, rows, [0, 16])
+    with pytest.raises(IndexError):
+        write_slots(pool, 2, rows, rows, [0, 1])
+    with pytest.raises(ValueError):
+        write_slots(pool, 0, rows, rows, [0])
+    with pytest.raises(IndexError):
+        gather_rows(pool, 0, [3], 6)
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.float32, torch.bfloat16], ids=str)
+def test_the_model_decodes_identically_through_the_slot_kernels(gpu, cache_dtype):
+    from conftest import golden
+    from iekv.engine.engine import Engine, EngineConfig
+    from iekv.engine.toy_model import ModelConfig, ToyTransformer
+    from iekv.serve.disaggregated import DisaggregatedEngine
+
+    g = golden("disaggregation")
+    cfg = EngineConfig(**g["engine"])
+
+    def model(hip_kv):
+        return ToyTransformer(ModelConfig(**g["model"]), seed=g["model_seed"], device=gpu,
+                              cache_dtype=cache_dtype, hip_kv=hip_kv)
+
+    torch_path = Engine(model(False), cfg).generate(g["prompts"], max_new_tokens=6,
+                                                    temperature=0.0)
+    hip_colocated = Engine(model(True), cfg).generate(g["prompts"], max_new_tokens=6,
+                                                      temperature=0.0)
+    hip_split = DisaggregatedEngine(model(True), cfg, mode="direct").generate(
+        g["prompts"], max_new_tokens=6, temperature=0.0)
+    assert hip_colocated == torch_path == hip_split

@@ -175,3 +175,21 @@ def test_a_planted_stale_read_fails_the_snapshot_check():
     payload = StaleRead([k], [k.copy()], 4).read_block(1)
     k[4:8] = -1
     assert list(payload[0][0][:, 0, 0]) != [4, 5, 6, 7]
+
+
+def test_slot_oracle_reproduces_the_reference_known_answers():
+    from oracle.slots import gather_context, write_kv
+
+    cache = slot_numbered_cache(8, 4)
+    gathered = gather_context(cache, [3, 1], 6, 4)
+    assert list(gathered[:, 0, 0]) == [12, 13, 14, 15, 4, 5]
+    k_cache = np.zeros((16, 1, 2), dtype=np.float32)
+    v_cache = np.zeros_like(k_cache)
+    k = np.arange(6, dtype=np.float32).reshape(3, 1, 2)
+    write_kv(k, k, k_cache, v_cache, [9, 0, 5])
+    assert np.array_equal(k_cache[9], k[0]) and np.array_equal(k_cache[0], k[1])
+    assert np.array_equal(k_cache[5], k[2])
+    with pytest.raises(ValueError):
+        write_kv(k, k, k_cache, v_cache, [0, 1])
+    with pytest.raises(IndexError):
+        gather_context(cache, [3], 6, 4)
