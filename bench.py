@@ -44,7 +44,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # WRITE_SIZE) / (read + write bytes), from two rocprofv3 --pmc runs of this script
 # calibrated on a plain 4 GiB copy (FETCH_SIZE reads 0.5x, WRITE_SIZE 1.0x of its
 # known size); see profiles/kv_move_direct_cfg3_pmc.txt.
-PMC_TRAFFIC_RATIO = 1.0004
+PMC_TRAFFIC_RATIO = 1.0001
 METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff"
 
 
@@ -407,6 +407,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg3", help="cfg1..cfg5 (headline: cfg3)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--slack", type=int, default=None,
+                    help="spare blocks per pool for cfg3/cfg4 (default 64)")
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
                     help="comma list of direct, pack_unpack, batched, plain_copy, "
                          "host_roundtrip")
@@ -441,7 +443,7 @@ def main() -> int:
     _native.lib()
     if args.launch:
         _native.set_launch(*[int(x) for x in args.launch.split(",")])
-    w = workloads.make(args.config, args.seed)
+    w = workloads.make(args.config, args.seed, args.slack)
     log(f"[bench] {w.name}: {w.num_requests} requests, {w.num_blocks} blocks, "
         f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B")
     legs = Legs(w, device, args.seed)

@@ -213,8 +213,12 @@ def cfg5(seed: int = 0) -> Workload:
 CONFIGS = {"cfg1": cfg1, "cfg2": cfg2, "cfg3": cfg3, "cfg4": cfg4, "cfg5": cfg5}
 
 
-def make(name: str, seed: int = 0) -> Workload:
-    try:
+def make(name: str, seed: int = 0, slack: int | None = None) -> Workload:
+    """Workload ``name``; ``slack`` (cfg3, cfg4) sets the spare blocks in each pool."""
+    if name not in CONFIGS:
+        raise ValueError(f"unknown workload {name!r}; choose from {sorted(CONFIGS)}")
+    if slack is None:
         return CONFIGS[name](seed)
-    except KeyError:
-        raise ValueError(f"unknown workload {name!r}; choose from {sorted(CONFIGS)}") from None
+    if name not in ("cfg3", "cfg4"):
+        raise ValueError(f"{name} has fixed pool sizes")
+    return CONFIGS[name](seed, slack=slack)
