@@ -178,7 +178,15 @@ class DecodeWorker:
         return len(resident)
 
     def admit(self, transfer: KVTransfer, max_new_tokens: int,
-              temperature: float = 0.0) -> Sequence:
+              temperature: float = 0.0, pending: list | None = None) -> Sequence:
+        """Place a transfer's blocks under fresh ids (ie/serve/disaggregated.py:75-96).
+
+        With ``pending`` (a list) a direct-mode transfer's copy is not issued
+        here: ``(source, destination ids, this copier)`` is appended for
+        :meth:`DisaggregatedEngine.flush_moves` to issue together with others.
+        A sequence that finishes on arrival is then not copied at all (its
+        blocks are freed at once and never read).
+        """
         engine = self.engine
         seq = engine.submit(transfer.token_ids[:-1], max_new_tokens=max_new_tokens,
                             temperature=temperature)
@@ -190,11 +198,18 @@ class DecodeWorker:
             dst_ids = list(seq.block_table)
 
         engine.flush_offloads()   # evictions made room for dst_ids: read them first
-        self._move(transfer, dst_ids)
+        deferred = pending is not None and transfer.source is not None
+        if not deferred:
+            self._move(transfer, dst_ids)
 
         seq.token_ids = list(transfer.token_ids)
         seq.num_computed = transfer.num_computed
         engine.scheduler.waiting.remove(seq)
+        if deferred:
+            if seq.stop_reason() is None:
+                pending.append((transfer.source, list(dst_ids), self.copier))
+            else:
+                transfer.source.done()
         if transfer.first_block or self.prefix_aware:
             engine.blocks.share_computed_blocks(seq)   # later requests can share these
         if seq.stop_reason() is not None:
@@ -251,8 +266,8 @@ class DisaggregatedEngine:
                                    copier_factory=copier_factory)
         self.stats = DisaggregationStats()
 
-    def handoff(self, prompt: list[int], max_new_tokens: int,
-                temperature: float = 0.0) -> Sequence:
+    def handoff(self, prompt: list[int], max_new_tokens: int, temperature: float = 0.0,
+                pending: list | None = None) -> Sequence:
         """Prefill one prompt and admit it into the decode pool."""
         skip = self.decode.cached_prefix_blocks(prompt)
         transfer = self.prefill.prefill(prompt, temperature, skip_blocks=skip)
@@ -262,11 +277,54 @@ class DisaggregatedEngine:
         self.stats.bytes_transferred += transfer.bytes_moved
         self.stats.prefill_tokens += len(prompt)
         self.stats.blocks_skipped += transfer.first_block
-        return self.decode.admit(transfer, max_new_tokens, temperature)
+        return self.decode.admit(transfer, max_new_tokens, temperature, pending=pending)
+
+    def flush_moves(self, pending: list) -> int:
+        """Issue deferred direct-mode copies: one pool-to-pool launch per (source, destination)
+        copier pair, then release the prefill blocks. Returns the number of blocks moved."""
+        groups: dict[tuple[int, int], tuple[Any, Any, list[int], list[int], list]] = {}
+        for source, dst_ids, dst_copier in pending:
+            key = (id(source.copier), id(dst_copier))
+            if key not in groups:
+                groups[key] = (source.copier, dst_copier, [], [], [])
+            _, _, src_all, dst_all, sources = groups[key]
+            src_all.extend(source.block_ids)
+            dst_all.extend(dst_ids)
+            sources.append(source)
+        moved = 0
+        for src_copier, dst_copier, src_all, dst_all, sources in groups.values():
+            if src_all:
+                dst_copier.copy_blocks(src_copier, src_all, dst_all)
+                moved += len(src_all)
+            for source in sources:
+                source.done()     # stream-ordered after the copy's reads
+        pending.clear()
+        return moved
+
+    def _prefill_has_room(self, prompt: list[int]) -> bool:
+        blocks = self.prefill.engine.blocks
+        probe = Sequence(prompt, block_size=self.prefill.engine.config.block_size)
+        return blocks.can_allocate(probe)
 
     def generate(self, prompts: list[list[int]], max_new_tokens: int = 16,
-                 temperature: float = 0.0) -> list[list[int]]:
-        sequences = [self.handoff(p, max_new_tokens, temperature) for p in prompts]
+                 temperature: float = 0.0, *, batch_moves: bool = False) -> list[list[int]]:
+        """Prefill, hand off and decode ``prompts`` (ie/serve/disaggregated.py:106-130).
+
+        ``batch_moves=True`` (direct mode) admits every prompt as the reference
+        does — same block tables, same order — but issues the copies of all of
+        them as one launch before decoding starts (earlier only if the prefill
+        pool runs short of room for the next prompt).
+        """
+        if batch_moves and self.prefill.mode != "direct":
+            raise ValueError("batch_moves needs mode='direct'")
+        pending: list | None = [] if batch_moves else None
+        sequences = []
+        for prompt in prompts:
+            if pending and not self._prefill_has_room(prompt):
+                self.flush_moves(pending)
+            sequences.append(self.handoff(prompt, max_new_tokens, temperature, pending))
+        if pending:
+            self.flush_moves(pending)
         engine = self.decode.engine
         while engine.scheduler.has_work:
             batch = engine.scheduler.schedule()

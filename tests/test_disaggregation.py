@@ -181,3 +181,41 @@ def test_prefix_aware_admit_shares_blocks_by_reference_count():
     blocks = engine.decode.engine.blocks
     assert all(blocks.blocks[b].ref_count == 2 for b in first.block_table[:4])
     assert set(second.block_table[4:]).isdisjoint(first.block_table)
+
+
+def test_batched_moves_keep_tables_and_tokens():
+    sequential = split(mode="direct", copier_factory=direct_oracle_factory)
+    expected = sequential.generate(G["prompts"], max_new_tokens=10, temperature=0.0)
+    batched = split(mode="direct", copier_factory=direct_oracle_factory)
+    pending: list = []
+    seqs = [batched.handoff(p, 10, 0.0, pending) for p in G["prompts"]]
+    assert [s.block_table for s in seqs] == [r["dst_table"] for r in G["requests"]]
+    assert len(pending) == len(G["prompts"])
+    # the prefill blocks stay held until the one combined copy
+    assert batched.prefill.engine.blocks.num_free < batched.prefill.engine.blocks.num_total
+    moved = batched.flush_moves(pending)
+    assert moved == sum(r["num_blocks"] for r in G["requests"])
+    assert batched.prefill.engine.blocks.num_free == batched.prefill.engine.blocks.num_total
+    fresh = split(mode="direct", copier_factory=direct_oracle_factory)
+    assert fresh.generate(G["prompts"], max_new_tokens=10, temperature=0.0,
+                          batch_moves=True) == expected == G["disaggregated"]["10"]
+
+
+def test_batched_moves_flush_early_when_the_prefill_pool_is_short():
+    from iekv.serve.disaggregated import DisaggregatedEngine
+
+    prompts = [list(range(100 + 40 * i, 100 + 40 * i + 70)) for i in range(6)]   # 5 blocks each
+    roomy = split(mode="direct", copier_factory=direct_oracle_factory)
+    expected = roomy.generate(prompts, max_new_tokens=4, temperature=0.0)
+    tight = DisaggregatedEngine(model(), engine_config(), mode="direct",
+                                copier_factory=direct_oracle_factory)
+    from iekv.serve.disaggregated import PrefillWorker
+    tight.prefill = PrefillWorker(model(), engine_config(num_blocks=12), mode="direct",
+                                  copier_factory=direct_oracle_factory)
+    assert tight.generate(prompts, max_new_tokens=4, temperature=0.0,
+                          batch_moves=True) == expected
+
+
+def test_batched_moves_need_direct_mode():
+    with pytest.raises(ValueError):
+        split().generate(G["prompts"], batch_moves=True)

@@ -220,3 +220,26 @@ def test_swap_preemption_on_gpu_keeps_tokens(gpu):
     assert isinstance(e.swapper, HipSlotCopier) and e.swapper.payload_location == "host"
     assert swapped == recompute == expected
     assert e.scheduler.stats.swapped_in == e.scheduler.stats.swapped_out > 0
+
+
+def test_batched_moves_on_gpu_are_one_launch(gpu):
+    from iekv import _native
+    from iekv.serve.disaggregated import DisaggregatedEngine
+
+    m = model(gpu, torch.bfloat16)
+    expected = DisaggregatedEngine(m, engine_config(), mode="direct").generate(
+        G["prompts"], max_new_tokens=8)
+    engine = DisaggregatedEngine(m, engine_config(), mode="direct")
+    pending: list = []
+    seqs = [engine.handoff(p, 8, 0.0, pending) for p in G["prompts"]]
+    assert [s.block_table for s in seqs] == [r["dst_table"] for r in G["requests"]]
+    with _native.LaunchTimer(64) as timer:
+        engine.flush_moves(pending)
+        torch.cuda.synchronize()
+    assert len(timer.durations_ms) == 1 and timer.durations_ms[0] > 0
+    dec = engine.decode.engine
+    while dec.scheduler.has_work:
+        dec.step()
+    assert [s.token_ids[s.num_prompt:] for s in seqs] == expected
+    fresh = DisaggregatedEngine(m, engine_config(), mode="direct")
+    assert fresh.generate(G["prompts"], max_new_tokens=8, batch_moves=True) == expected
