@@ -79,6 +79,7 @@ class Legs:
     def __init__(self, workload, device, seed: int) -> None:
         import torch
 
+        from iekv.engine.copier import issue_order
         from iekv.engine.pools import KVPool, allocate_pool
 
         self.torch = torch
@@ -95,10 +96,16 @@ class Legs:
                                                device=device, zero=True)
         self.src = KVPool(self.src_k, self.src_v, s.block_size)
         self.dst = KVPool(self.dst_k, self.dst_v, s.block_size)
+        # pack/unpack move blocks in table order (the payload layout); direct copies
+        # issue each request's pairs by destination id, as HipSlotCopier.copy_blocks does.
         self.src_ids = [self.src.block_ids(t) for t in workload.src_tables]
         self.dst_ids = [self.dst.block_ids(t, unique=True) for t in workload.dst_tables]
-        self.src_all = self.src.block_ids(sum(workload.src_tables, []))
-        self.dst_all = self.dst.block_ids(sum(workload.dst_tables, []), unique=True)
+        pairs = [issue_order(s, d) for s, d in zip(workload.src_tables, workload.dst_tables)]
+        self.src_direct = [self.src.block_ids(s) for s, _ in pairs]
+        self.dst_direct = [self.dst.block_ids(d, unique=True) for _, d in pairs]
+        src_all, dst_all = issue_order(sum(workload.src_tables, []), sum(workload.dst_tables, []))
+        self.src_all = self.src.block_ids(src_all)
+        self.dst_all = self.dst.block_ids(dst_all, unique=True)
         longest = max(len(t) for t in workload.src_tables)
         self.staging = torch.empty(longest * s.block_bytes, dtype=torch.uint8, device=device)
         self.stream = torch.cuda.current_stream(device)
@@ -123,7 +130,7 @@ class Legs:
         from iekv import _native
 
         h = self.stream.cuda_stream
-        for s, d in zip(self.src_ids, self.dst_ids):
+        for s, d in zip(self.src_direct, self.dst_direct):
             _native.call("iekv_copy_direct", self.src.native.handle, self.dst.native.handle,
                          s.data_ptr(), d.data_ptr(), s.numel(), h)
 

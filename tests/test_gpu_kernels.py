@@ -392,3 +392,21 @@ def test_deferred_host_reads_batch_and_keep_snapshot_semantics(gpu):
     after = host_bytes(k) + host_bytes(v)
     for a in range(4):
         assert np.array_equal(after[a][7 * bs:8 * bs], before[a][3 * bs:4 * bs])
+
+
+def test_launch_timer_times_each_library_launch(gpu):
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    sk, sv = allocate(40, 16, 2, 8, 128, torch.bfloat16, gpu, seed=27)
+    dk, dv = allocate(40, 16, 2, 8, 128, torch.bfloat16, gpu, seed=28)
+    src, dst = HipSlotCopier(sk, sv, 16), HipSlotCopier(dk, dv, 16)
+    with _native.LaunchTimer(8) as timer:
+        dst.copy_blocks(src, [1, 2, 3], [4, 5, 6])
+        packed = src.read_blocks([7, 8])
+        dst.write_blocks([9, 10], packed)
+    assert len(timer.durations_ms) == 3 and all(ms > 0 for ms in timer.durations_ms)
+    dst.copy_blocks(src, [11], [12])          # outside a session: launched, not timed
+    with _native.LaunchTimer(2) as timer:     # a session with no launches
+        pass
+    assert timer.durations_ms == []
