@@ -100,3 +100,18 @@ def test_the_product_refuses_cpu_caches():
     k = [torch.zeros(32, 2, 4)]
     with pytest.raises(ValueError, match="GPU caches"):
         HipSlotCopier(k, [t.clone() for t in k], 16)
+
+
+def test_direct_copy_issue_order_keeps_every_pair():
+    import numpy as np
+
+    from iekv.engine.copier import issue_order
+
+    rng = np.random.default_rng(3)
+    src = rng.permutation(500)[:200]
+    dst = rng.permutation(700)[:200]
+    s, d = issue_order(src.tolist(), dst.tolist())
+    assert list(d) == sorted(dst.tolist())
+    assert sorted(zip(s.tolist(), d.tolist())) == sorted(zip(src.tolist(), dst.tolist()))
+    with pytest.raises(ValueError):
+        issue_order([1, 2], [3])
