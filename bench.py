@@ -10,6 +10,7 @@ without NaN codes for fp8). Legs:
 
   direct       one iekv_copy_direct launch per request (the headline: 2P bytes)
   pack_unpack  iekv_pack into a per-request staging buffer, then iekv_unpack (4P bytes)
+  pack         the pack half alone (2P bytes); unpack: the unpack half alone (2P bytes)
   batched      all requests' blocks in ONE direct launch (2P bytes)
 
 ``value`` is the direct leg's algorithmic read+write bandwidth, 2P / step
@@ -109,6 +110,7 @@ class Legs:
         longest = max(len(t) for t in workload.src_tables)
         self.staging = torch.empty(longest * s.block_bytes, dtype=torch.uint8, device=device)
         self.stream = torch.cuda.current_stream(device)
+        self.step_ms: dict[str, list[float]] = {}
         torch.cuda.synchronize()
         log(f"[bench] pools ready: 2 x {workload.src_pool_blocks} blocks x {s.block_bytes} B "
             f"({2 * workload.src_pool_blocks * s.block_bytes / 1e9:.1f} GB) in "
@@ -122,6 +124,8 @@ class Legs:
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
         if name == "pack_unpack":
             return [x for r, n in enumerate(sizes) for x in ((2 * n * bb, r), (2 * n * bb, r))]
+        if name in ("pack", "unpack"):
+            return [(2 * n * bb, r) for r, n in enumerate(sizes)]
         if name == "batched":
             return [(2 * sum(sizes) * bb, 0)]
         return []
@@ -145,6 +149,26 @@ class Legs:
                          st.numel(), h)
             _native.call("iekv_unpack", self.dst.native.handle, d.data_ptr(), n, st.data_ptr(),
                          st.numel(), h)
+
+    def pack(self) -> None:
+        """The pack half alone: every request gathered into the staging buffer."""
+        from iekv import _native
+
+        h = self.stream.cuda_stream
+        st = self.staging
+        for s in self.src_ids:
+            _native.call("iekv_pack", self.src.native.handle, s.data_ptr(), s.numel(),
+                         st.data_ptr(), st.numel(), h)
+
+    def unpack(self) -> None:
+        """The unpack half alone: the staging buffer scattered onto every request's ids."""
+        from iekv import _native
+
+        h = self.stream.cuda_stream
+        st = self.staging
+        for d in self.dst_ids:
+            _native.call("iekv_unpack", self.dst.native.handle, d.data_ptr(), d.numel(),
+                         st.data_ptr(), st.numel(), h)
 
     def batched(self) -> None:
         from iekv import _native
@@ -239,6 +263,33 @@ class Legs:
                     ok = False
         return ok
 
+    def _tiles(self, arrays):
+        T = self.w.shape.tile_bytes
+        return [t.view(self.torch.uint8).view(-1, T) for t in arrays]
+
+    def verify_pack(self) -> bool:
+        """The staging buffer holds the last request's block images, [n, 2L, T]."""
+        torch = self.torch
+        s = self.w.shape
+        ids = self.src_ids[-1].long()
+        n = ids.numel()
+        image = self.staging[:n * s.block_bytes].view(n, s.n_arrays, s.tile_bytes)
+        return all(torch.equal(image[:, a], tiles.index_select(0, ids))
+                   for a, tiles in enumerate(self._tiles(self.src_k + self.src_v)))
+
+    def verify_unpack(self) -> bool:
+        """Every request's destination tiles equal the staging images it was unpacked from."""
+        torch = self.torch
+        s = self.w.shape
+        dst_tiles = self._tiles(self.dst_k + self.dst_v)
+        for d in self.dst_ids:
+            n = d.numel()
+            image = self.staging[:n * s.block_bytes].view(n, s.n_arrays, s.tile_bytes)
+            for a, tiles in enumerate(dst_tiles):
+                if not torch.equal(image[:, a], tiles.index_select(0, d.long())):
+                    return False
+        return True
+
     def clear_dst(self) -> None:
         for t in self.dst_k + self.dst_v:
             t.zero_()
@@ -247,8 +298,9 @@ class Legs:
 def time_leg(legs: Legs, name: str, steps: int, warmup: int, per_launch: bool = True):
     """Warm up, then time ``steps`` steps twice.
 
-    Pass 1 (the headline): only two HIP events around the timed steps on the
-    launch stream, so nothing is added between launches. Pass 2 (when
+    Pass 1 (the headline): HIP events only at step boundaries on the launch
+    stream, so nothing is added between the launches of a step (the per-step
+    times are kept in ``legs.step_ms``). Pass 2 (when
     ``per_launch``): the same steps again with every kv_move launch timed by the
     library (iekv_profile_start/stop; the events ride in each launch's own
     dispatch packet). Returns (ms per step, wall seconds of pass 1,
@@ -261,15 +313,16 @@ def time_leg(legs: Legs, name: str, steps: int, warmup: int, per_launch: bool = 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    start.record(legs.stream)
-    for _ in range(steps):
+    marks[0].record(legs.stream)
+    for i in range(steps):
         step()
-    end.record(legs.stream)
+        marks[i + 1].record(legs.stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_step = start.elapsed_time(end) / steps
+    ms_step = marks[0].elapsed_time(marks[-1]) / steps
+    legs.step_ms[name] = [a.elapsed_time(b) for a, b in zip(marks, marks[1:])]
     plan = legs.plan(name)
     if not (per_launch and plan):
         return ms_step, wall, []
@@ -296,6 +349,7 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
     kernel_gbs = moved / (total_ms * 1e-3) / 1e9 if total_ms else 0.0
     out = {
         "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(statistics.median(legs.step_ms.get(name, [ms_step])), 4),
         "GBps": round(gbs, 1),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "kernel_GBps": round(kernel_gbs, 1),
@@ -303,7 +357,7 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
         "avg_launch_us": round(1000 * total_ms / max(1, len(durations)), 2),
         "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
     }
-    if name in ("direct", "pack_unpack"):
+    if name in ("direct", "pack_unpack", "pack", "unpack"):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
                                  "p50": round(req_ms[len(req_ms) // 2], 4),
                                  "p99": round(req_ms[min(len(req_ms) - 1,
@@ -378,7 +432,10 @@ def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float) ->
 
 
 def sweep(legs: Legs, names: list[str]) -> list[dict]:
-    """Time each leg under every launch shape iekv_set_launch offers (3 steps after 1 warm-up)."""
+    """Time each leg under every launch shape iekv_set_launch offers (3 steps after 1 warm-up).
+
+    ``order`` sets both workgroup orders (pool-writing and staging-writing launches).
+    """
     from iekv import _native
 
     before = _native.get_launch()
@@ -389,7 +446,7 @@ def sweep(legs: Legs, names: list[str]) -> list[dict]:
             for nt in (1, 0):
                 for unroll in (4, 8, 16):
                     for run in (1, 2, 4, 8, 16):
-                        _native.set_launch(run, unroll, nt, order)
+                        _native.set_launch(run, unroll, nt, order, order)
                         row = {"run_blocks": run, "unroll": unroll, "nontemporal": nt,
                                "order": order}
                         for name in names:
@@ -417,16 +474,16 @@ def main() -> int:
     ap.add_argument("--slack", type=int, default=None,
                     help="spare blocks per pool for cfg3/cfg4 (default 64)")
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
-                    help="comma list of direct, pack_unpack, batched, plain_copy, "
-                         "host_roundtrip")
+                    help="comma list of direct, pack_unpack, pack, unpack, batched, "
+                         "plain_copy, host_roundtrip")
     ap.add_argument("--cpu-blocks", type=int, default=1536,
                     help="blocks in the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="minimum CPU-baseline time (the sample handoff repeats until then)")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--launch", default="",
-                    help="run_blocks,unroll,nontemporal,order for iekv_set_launch (default: "
-                         "the library's)")
+                    help="run_blocks,unroll,nontemporal,order[,pack_order] for "
+                         "iekv_set_launch (default: the library's)")
     ap.add_argument("--sweep", action="store_true",
                     help="time the legs under every launch shape instead of the benchmark line")
     args = ap.parse_args()
@@ -456,7 +513,8 @@ def main() -> int:
     legs = Legs(w, device, args.seed)
     P = w.payload_bytes
     if args.sweep:
-        names = [x for x in args.legs.split(",") if x in ("direct", "pack_unpack", "batched")]
+        names = [x for x in args.legs.split(",")
+                 if x in ("direct", "pack_unpack", "pack", "unpack", "batched")]
         rows = sweep(legs, names)
         ok = legs.verify()
         print(json.dumps({"sweep": w.name, "legs": names, "rows": rows, "verified": ok}))
@@ -483,8 +541,9 @@ def main() -> int:
         if name == "pack_unpack":
             res["effective_handoff_GBps"] = round(2 * P / (ms * 1e-3) / 1e9, 1)
         if not args.no_verify and name != "plain_copy":
-            verified[name] = legs.verify()
-            log(f"[bench] {name}: destination tiles equal source tiles: {verified[name]}")
+            check = {"pack": legs.verify_pack, "unpack": legs.verify_unpack}.get(name, legs.verify)
+            verified[name] = check()
+            log(f"[bench] {name}: moved tiles equal their sources: {verified[name]}")
         results[name] = res
         if primary is None and name != "plain_copy":
             primary = (name, ms, res, kgbs, avg_us, avg_bytes)
@@ -503,6 +562,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "ms_per_step_median": res["ms_per_step_median"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -525,7 +585,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(kgbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
                      "traffic": int(avg_bytes * PMC_TRAFFIC_RATIO),
-                     "kernel": "kv_move (direct)", "avg_launch_us": round(avg_us, 2),
+                     "kernel": f"kv_move ({name})", "avg_launch_us": round(avg_us, 2),
                      "algorithmic_bytes_per_launch": int(avg_bytes)},
         "cpu_baseline": cpu,
     }

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 4
+#define IEKV_ABI_VERSION 5
 
 enum {
   IEKV_OK = 0,
@@ -151,14 +151,19 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
  *               0 keeps the current setting;
  *   nontemporal 1 for streaming (non-temporal) loads and stores, 0 for
  *               ordinary ones, -1 keeps the current setting;
- *   order       which (array, block) tiles are in flight together:
+ *   order       which (array, block) tiles are in flight together in the
+ *               launches that write a pool (direct copy, unpack, restore):
  *               0 array-major (the 2L tiles of one block), 1 block-major
  *               (random blocks of one array), 2 diagonal (array a takes list
  *               run r + a, so 2L arrays and 2L blocks at once); -1 keeps the
- *               current setting.
+ *               current setting. Default 2;
+ *   pack_order  the same choice for the launches that write a staging buffer
+ *               (pack, offload). Default 0, which writes consecutive staging
+ *               tiles from consecutive workgroups.
  * No reference counterpart: a tuning knob for the launches the entry points
  * above make. */
-int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order);
+int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order,
+                    int32_t pack_order);
 
 /* Per-launch timing, for measurement (calling thread only). After
  * iekv_profile_start(max_launches), each of the next max_launches kernel
@@ -174,7 +179,7 @@ int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count);
 
 /* Current launch shape, for reporting. */
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
-                    int32_t* order);
+                    int32_t* order, int32_t* pack_order);
 
 #ifdef __cplusplus
 }

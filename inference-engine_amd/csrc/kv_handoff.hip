@@ -71,10 +71,17 @@ int set_error(int code, const char* fmt, ...) {
 std::atomic<int> g_run{0};       // 0 = automatic
 std::atomic<int> g_unroll{8};
 std::atomic<int> g_nontemporal{1};
-// Workgroup order (see Order below): diagonal. Over 12 pool sizes / paddings of
-// the Llama-3-8B shape it averaged 6.09 TB/s against 5.78 (array-major) and
-// 5.47 (block-major), lifting the layouts where array-major collides.
+// Workgroup order (see Order below) of launches that write a pool (direct,
+// unpack, restore): diagonal. Over 12 pool sizes / paddings of the Llama-3-8B
+// shape it averaged 6.09 TB/s against 5.78 (array-major) and 5.47 (block-major),
+// lifting the layouts where array-major collides.
 std::atomic<int> g_order{2};
+// Order of launches that write a staging buffer (pack, offload): array-major,
+// so consecutive workgroups write consecutive staging tiles. Over 11 pool
+// paddings each of the Llama-3-8B and 70B-share shapes it was faster than
+// diagonal on every 70B-share padding (5.82 against 5.46 TB/s on average) and
+// faster or tied on every 8B padding (5.66 against 5.62).
+std::atomic<int> g_pack_order{0};
 
 // ---------------------------------------------------------------------------
 // Device side
@@ -361,18 +368,18 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
   int vec = 16;
   MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), g_nontemporal.load() != 0, &vec);
   const int32_t tile_vecs = static_cast<int32_t>(tile_bytes / vec);
+  const int32_t order = DP ? g_order.load() : g_pack_order.load();
   Profiler& prof = g_profiler;
   if (prof.on && prof.used < prof.events.size()) {
     auto& ev = prof.events[prof.used++];
     hipExtLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
                           ev.first, ev.second, 0, view_of(sp), view_of(dp), src_stage,
                           dst_stage, src_ids, dst_ids, tile_vecs, n_blocks, n_arrays, run,
-                          static_cast<int32_t>(runs), g_order.load());
+                          static_cast<int32_t>(runs), order);
   } else {
     hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
                        view_of(sp), view_of(dp), src_stage, dst_stage, src_ids, dst_ids,
-                       tile_vecs, n_blocks, n_arrays, run, static_cast<int32_t>(runs),
-                       g_order.load());
+                       tile_vecs, n_blocks, n_arrays, run, static_cast<int32_t>(runs), order);
   }
   IEKV_HIP(hipGetLastError());
   return IEKV_OK;
@@ -815,7 +822,8 @@ int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count) {
   return IEKV_OK;
 }
 
-int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order) {
+int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order,
+                    int32_t pack_order) {
   if (run_blocks < -1 || run_blocks > kMaxRun)
     return set_error(IEKV_ERR_INVALID, "run_blocks %d out of range", run_blocks);
   if (unroll != 0 && unroll != 4 && unroll != 8 && unroll != 16)
@@ -824,19 +832,23 @@ int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int
     return set_error(IEKV_ERR_INVALID, "nontemporal must be -1, 0 or 1 (got %d)", nontemporal);
   if (order < -1 || order > 2)
     return set_error(IEKV_ERR_INVALID, "order must be -1, 0, 1 or 2 (got %d)", order);
+  if (pack_order < -1 || pack_order > 2)
+    return set_error(IEKV_ERR_INVALID, "pack_order must be -1, 0, 1 or 2 (got %d)", pack_order);
   if (run_blocks >= 0) g_run.store(run_blocks);
   if (unroll) g_unroll.store(unroll);
   if (nontemporal >= 0) g_nontemporal.store(nontemporal);
   if (order >= 0) g_order.store(order);
+  if (pack_order >= 0) g_pack_order.store(pack_order);
   return IEKV_OK;
 }
 
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
-                    int32_t* order) {
+                    int32_t* order, int32_t* pack_order) {
   if (run_blocks) *run_blocks = g_run.load();
   if (unroll) *unroll = g_unroll.load();
   if (nontemporal) *nontemporal = g_nontemporal.load();
   if (order) *order = g_order.load();
+  if (pack_order) *pack_order = g_pack_order.load();
   return IEKV_OK;
 }
 

@@ -131,24 +131,43 @@ def test_narrow_and_odd_tiles(gpu, bs, heads, dim, dtype):
 
 
 def test_every_launch_shape_is_bit_exact(gpu):
+    """Pack, unpack and direct copy under every run / unroll / non-temporal /
+    workgroup-order setting (order for the pool-writing launches, pack_order for
+    the staging-writing ones)."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
     bs, layers, heads, dim = 16, 2, 8, 128   # 32 KiB tiles, like the Llama-3-8B shape
     sk, sv = allocate(96, bs, layers, heads, dim, torch.bfloat16, gpu, seed=10)
-    src = HipSlotCopier(sk, sv, bs)
+    dk, dv = allocate(90, bs, layers, heads, dim, torch.bfloat16, gpu, seed=12)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
     rng = np.random.default_rng(11)
     src_ids = [int(b) for b in rng.permutation(96)[:77]]
-    want = packed_image(pack(oracle_of(sk, sv, bs), src_ids))
+    dst_ids = [int(b) for b in rng.permutation(90)[:77]]
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    want = packed_image(pack(src_o, src_ids))
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
     before = _native.get_launch()
     try:
         for run in (1, 3, 0, 64):
             for unroll in (4, 8, 16):
                 for nt in (0, 1):
                     for order in (0, 1, 2):
-                        _native.set_launch(run, unroll, nt, order)
-                        got = src.read_blocks(src_ids).data.cpu().numpy()
-                        assert np.array_equal(got, want), (run, unroll, nt, order)
+                        shape = (run, unroll, nt, order)
+                        _native.set_launch(run, unroll, nt, order, order)
+                        packed = src.read_blocks(src_ids)
+                        assert np.array_equal(packed.data.cpu().numpy(), want), shape
+                        for t in dk + dv:
+                            t.zero_()
+                        half = len(src_ids) // 2
+                        dst.write_blocks(dst_ids[:half], packed[:half])
+                        dst.copy_blocks(src, src_ids[half:], dst_ids[half:])
+                        torch.cuda.synchronize()
+                        got = host_bytes(dk) + host_bytes(dv)
+                        for g, w in zip(got, list(dst_o.k_caches) + list(dst_o.v_caches)):
+                            rows = np.concatenate([np.arange(b * bs, (b + 1) * bs)
+                                                   for b in dst_ids])
+                            assert np.array_equal(g[rows], w[rows]), shape
     finally:
         _native.set_launch(**before)
 

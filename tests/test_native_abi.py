@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 4
+    assert lib.iekv_abi_version() == 5
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -86,8 +86,11 @@ def test_launch_settings_are_validated(lib):
         _native.set_launch(nontemporal=2)
     with pytest.raises(_native.NativeError):
         _native.set_launch(order=3)
-    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=2)
-    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "order": 2}
+    with pytest.raises(_native.NativeError):
+        _native.set_launch(pack_order=-2)
+    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=2, pack_order=1)
+    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "order": 2,
+                                    "pack_order": 1}
     _native.set_launch(**before)
     assert _native.get_launch() == before
 
