@@ -442,7 +442,7 @@ def sweep(legs: Legs, names: list[str]) -> list[dict]:
     P = legs.w.payload_bytes
     rows = []
     try:
-        for order in (0, 1, 2):
+        for order in (0, 1, 2, 4, 5, 6):
             for nt in (1, 0):
                 for unroll in (4, 8, 16):
                     for run in (1, 2, 4, 8, 16):

@@ -155,8 +155,10 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
  *               launches that write a pool (direct copy, unpack, restore):
  *               0 array-major (the 2L tiles of one block), 1 block-major
  *               (random blocks of one array), 2 diagonal (array a takes list
- *               run r + a, so 2L arrays and 2L blocks at once); -1 keeps the
- *               current setting. Default 2;
+ *               run r + a, so 2L arrays and 2L blocks at once); adding 4
+ *               gives each of the 8 XCDs one contiguous share of that order
+ *               (with 5, its own eighth of the arrays); -1 keeps the current
+ *               setting. Default 5;
  *   pack_order  the same choice for the launches that write a staging buffer
  *               (pack, offload). Default 0, which writes consecutive staging
  *               tiles from consecutive workgroups.

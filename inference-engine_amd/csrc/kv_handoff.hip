@@ -42,6 +42,10 @@ struct iekv_pool {
 namespace {
 
 constexpr int kThreads = 256;  // four wave64 per workgroup
+constexpr int kXcds = 8;       // MI355X: the dispatcher deals workgroups to 8 XCDs in turn
+constexpr int kXcdGrouped = 4; // order flag: give each XCD a contiguous share of the work
+// Workgroup orders of kv_move (described at the kernel).
+enum Order : int32_t { kArrayMajor = 0, kBlockMajor = 1, kDiagonal = 2 };
 constexpr int kMaxRun = 64;    // block ids staged in LDS per workgroup
 constexpr int64_t kMaxTileBytes = int64_t(1) << 30;
 
@@ -71,11 +75,13 @@ int set_error(int code, const char* fmt, ...) {
 std::atomic<int> g_run{0};       // 0 = automatic
 std::atomic<int> g_unroll{8};
 std::atomic<int> g_nontemporal{1};
-// Workgroup order (see Order below) of launches that write a pool (direct,
-// unpack, restore): diagonal. Over 12 pool sizes / paddings of the Llama-3-8B
-// shape it averaged 6.09 TB/s against 5.78 (array-major) and 5.47 (block-major),
-// lifting the layouts where array-major collides.
-std::atomic<int> g_order{2};
+// Workgroup order (described at kv_move) of launches that write a pool (direct,
+// unpack, restore): XCD-grouped block-major, so each XCD streams through its
+// own eighth of the arrays. Over 11 pool paddings of the Llama-3-70B-share
+// shape it averaged 6.20 TB/s (worst 5.90) against 5.88 (worst 5.00) for
+// diagonal and 5.86 (worst 4.59) for array-major; on the Llama-3-8B shape all
+// three are within 0.2%.
+std::atomic<int> g_order{kXcdGrouped | kBlockMajor};
 // Order of launches that write a staging buffer (pack, offload): array-major,
 // so consecutive workgroups write consecutive staging tiles. Over 11 pool
 // paddings each of the Llama-3-8B and 70B-share shapes it was faster than
@@ -168,15 +174,27 @@ __device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
 
 // One workgroup per (array a, run of list entries [first, first+count)).
 // The order in which workgroups take (array, run) pairs decides which tiles
-// are in flight together (the dispatcher hands consecutive workgroups to the
-// eight XCDs in turn):
-//   kArrayMajor  blockIdx.x = run * n_arrays + a: the 2L tiles of one block;
-//                their addresses differ by multiples of the array stride;
-//   kBlockMajor  blockIdx.x = a * runs + run: random blocks of one array;
+// are in flight together. With w the workgroup's position in that order:
+//   kArrayMajor  w = run * n_arrays + a: the 2L tiles of one block; their
+//                addresses differ by multiples of the array stride;
+//   kBlockMajor  w = a * runs + run: random blocks of one array;
 //   kDiagonal    as array-major, but array a takes run (run + a) mod runs, so
 //                the tiles in flight span 2L arrays AND 2L different blocks.
-// Every order covers each (array, run) pair exactly once.
-enum Order : int32_t { kArrayMajor = 0, kBlockMajor = 1, kDiagonal = 2 };
+// Plain orders take w = blockIdx.x. The dispatcher deals consecutive
+// workgroups to the kXcds XCDs in turn, so with the kXcdGrouped flag set,
+// workgroup i (on XCD i mod kXcds) takes position w = start(XCD) + i / kXcds
+// instead: each XCD walks one contiguous share of the order (with
+// kBlockMajor, its own eighth of the arrays). Every order covers each
+// (array, run) pair exactly once.
+
+// Position of workgroup `i` of `grid` when each XCD takes a contiguous share:
+// XCD x receives workgroups x, x + kXcds, ...; the first `grid % kXcds` XCDs
+// receive one more than the rest. A bijection on [0, grid).
+__device__ __forceinline__ int xcd_grouped(int i, int grid) {
+  const int q = grid / kXcds, rem = grid % kXcds;
+  const int x = i % kXcds;
+  return x * q + min(x, rem) + i / kXcds;
+}
 
 template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
 __global__ void __launch_bounds__(kThreads)
@@ -186,14 +204,16 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
         int32_t n_arrays, int32_t run, int32_t runs, int32_t order) {
   __shared__ int32_t s_src[kMaxRun];
   __shared__ int32_t s_dst[kMaxRun];
+  const int w = (order & kXcdGrouped) ? xcd_grouped(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int base_order = order & ~kXcdGrouped;
   int a, r;
-  if (order == kBlockMajor) {
-    a = blockIdx.x / runs;
-    r = blockIdx.x % runs;
+  if (base_order == kBlockMajor) {
+    a = w / runs;
+    r = w % runs;
   } else {
-    a = blockIdx.x % n_arrays;
-    r = blockIdx.x / n_arrays;
-    if (order == kDiagonal) r = static_cast<int>((static_cast<int64_t>(r) + a) % runs);
+    a = w % n_arrays;
+    r = w / n_arrays;
+    if (base_order == kDiagonal) r = static_cast<int>((static_cast<int64_t>(r) + a) % runs);
   }
   const int first = r * run;
   const int count = min(run, n_blocks - first);
@@ -436,6 +456,12 @@ class Events {
  private:
   std::vector<hipEvent_t> ev_;
 };
+
+// -1 (keep), or a base order 0..2 with or without the kXcdGrouped flag.
+bool valid_order(int32_t order) {
+  if (order == -1) return true;
+  return order >= 0 && order <= (kXcdGrouped | kDiagonal) && (order & ~kXcdGrouped) <= kDiagonal;
+}
 
 // Staging slots for a pipeline: two when the buffer holds two blocks or more.
 void plan_slots(int64_t staging_bytes, int64_t block_bytes, int32_t n_blocks, int* n_slots,
@@ -830,10 +856,11 @@ int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int
     return set_error(IEKV_ERR_INVALID, "unroll must be 4, 8 or 16 (got %d)", unroll);
   if (nontemporal < -1 || nontemporal > 1)
     return set_error(IEKV_ERR_INVALID, "nontemporal must be -1, 0 or 1 (got %d)", nontemporal);
-  if (order < -1 || order > 2)
-    return set_error(IEKV_ERR_INVALID, "order must be -1, 0, 1 or 2 (got %d)", order);
-  if (pack_order < -1 || pack_order > 2)
-    return set_error(IEKV_ERR_INVALID, "pack_order must be -1, 0, 1 or 2 (got %d)", pack_order);
+  if (!valid_order(order))
+    return set_error(IEKV_ERR_INVALID, "order must be -1, 0, 1, 2, 4, 5 or 6 (got %d)", order);
+  if (!valid_order(pack_order))
+    return set_error(IEKV_ERR_INVALID, "pack_order must be -1, 0, 1, 2, 4, 5 or 6 (got %d)",
+                     pack_order);
   if (run_blocks >= 0) g_run.store(run_blocks);
   if (unroll) g_unroll.store(unroll);
   if (nontemporal >= 0) g_nontemporal.store(nontemporal);

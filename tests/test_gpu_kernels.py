@@ -133,7 +133,8 @@ def test_narrow_and_odd_tiles(gpu, bs, heads, dim, dtype):
 def test_every_launch_shape_is_bit_exact(gpu):
     """Pack, unpack and direct copy under every run / unroll / non-temporal /
     workgroup-order setting (order for the pool-writing launches, pack_order for
-    the staging-writing ones)."""
+    the staging-writing ones; 4-6 are the XCD-grouped orders, here on grids of
+    8 to 308 workgroups, most not a multiple of the 8 XCDs)."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -152,7 +153,7 @@ def test_every_launch_shape_is_bit_exact(gpu):
         for run in (1, 3, 0, 64):
             for unroll in (4, 8, 16):
                 for nt in (0, 1):
-                    for order in (0, 1, 2):
+                    for order in (0, 1, 2, 4, 5, 6):
                         shape = (run, unroll, nt, order)
                         _native.set_launch(run, unroll, nt, order, order)
                         packed = src.read_blocks(src_ids)

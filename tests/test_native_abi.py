@@ -74,6 +74,20 @@ def test_calls_reject_null_pools_and_negative_counts(lib):
     assert "null" in lib.iekv_last_error().decode()
 
 
+def test_default_launch_shape():
+    """A fresh process starts with the shape the header documents."""
+    import json
+    import subprocess
+    import sys
+
+    code = ("import sys; sys.path[:0] = [sys.argv[1]]; import json; from iekv import _native; "
+            "print(json.dumps(_native.get_launch()))")
+    out = subprocess.run([sys.executable, "-c", code, str(ROOT / "inference-engine_amd")],
+                         capture_output=True, text=True, check=True, timeout=120)
+    assert json.loads(out.stdout.strip().splitlines()[-1]) == {
+        "run_blocks": 0, "unroll": 8, "nontemporal": 1, "order": 5, "pack_order": 0}
+
+
 def test_launch_settings_are_validated(lib):
     from iekv import _native
 
@@ -84,12 +98,13 @@ def test_launch_settings_are_validated(lib):
         _native.set_launch(unroll=3)
     with pytest.raises(_native.NativeError):
         _native.set_launch(nontemporal=2)
-    with pytest.raises(_native.NativeError):
-        _native.set_launch(order=3)
-    with pytest.raises(_native.NativeError):
-        _native.set_launch(pack_order=-2)
-    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=2, pack_order=1)
-    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "order": 2,
+    for bad in (3, 7, 8, -2):
+        with pytest.raises(_native.NativeError):
+            _native.set_launch(order=bad)
+        with pytest.raises(_native.NativeError):
+            _native.set_launch(pack_order=bad)
+    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=6, pack_order=1)
+    assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "order": 6,
                                     "pack_order": 1}
     _native.set_launch(**before)
     assert _native.get_launch() == before
