@@ -205,12 +205,14 @@ class DecodeWorker:
         seq.token_ids = list(transfer.token_ids)
         seq.num_computed = transfer.num_computed
         engine.scheduler.waiting.remove(seq)
+        copied = True
         if deferred:
             if seq.stop_reason() is None:
                 pending.append((transfer.source, list(dst_ids), self.copier))
             else:
                 transfer.source.done()
-        if transfer.first_block or self.prefix_aware:
+                copied = False      # never moved: its blocks hold no KV to share
+        if (transfer.first_block or self.prefix_aware) and copied:
             engine.blocks.share_computed_blocks(seq)   # later requests can share these
         if seq.stop_reason() is not None:
             seq.status = Status.FINISHED
@@ -325,6 +327,12 @@ class DisaggregatedEngine:
             sequences.append(self.handoff(prompt, max_new_tokens, temperature, pending))
         if pending:
             self.flush_moves(pending)
+        self.decode_until_done()
+        return [s.token_ids[s.num_prompt:] for s in sequences]
+
+    def decode_until_done(self) -> None:
+        """Step the decode worker until every admitted sequence has finished
+        (the decode loop of ie/serve/disaggregated.py:117-129)."""
         engine = self.decode.engine
         while engine.scheduler.has_work:
             batch = engine.scheduler.schedule()
@@ -336,4 +344,3 @@ class DisaggregatedEngine:
             engine.scheduler.finish_step(batch, tokens)
             self.stats.decodes += 1
             self.stats.decode_tokens += len(batch)
-        return [s.token_ids[s.num_prompt:] for s in sequences]

@@ -216,6 +216,26 @@ def test_batched_moves_flush_early_when_the_prefill_pool_is_short():
                           batch_moves=True) == expected
 
 
+def test_a_batched_request_finished_on_arrival_leaves_no_shared_prefix():
+    """With batched moves, a request that finishes on arrival is never copied, so its
+    blocks must not be offered for prefix sharing: a later request with the same
+    prefix moves those blocks itself and decodes as if alone."""
+    from iekv.core.sequence import Status
+
+    prefix = list(range(1000, 1064))                   # 4 full blocks of 16
+    first, second = prefix + [1, 2, 3], prefix + [4, 5, 6, 7]
+    want = split().generate([second], max_new_tokens=6, temperature=0.0)[0]
+    engine = split(mode="direct", prefix_aware=True, copier_factory=direct_oracle_factory)
+    pending: list = []
+    done = engine.handoff(first, 1, 0.0, pending)
+    assert done.status == Status.FINISHED and not pending
+    seq = engine.handoff(second, 6, 0.0, pending)
+    assert engine.stats.blocks_skipped == 0
+    engine.flush_moves(pending)
+    engine.decode_until_done()
+    assert seq.token_ids[seq.num_prompt:] == want
+
+
 def test_batched_moves_need_direct_mode():
     with pytest.raises(ValueError):
         split().generate(G["prompts"], batch_moves=True)

@@ -243,3 +243,29 @@ def test_batched_moves_on_gpu_are_one_launch(gpu):
     assert [s.token_ids[s.num_prompt:] for s in seqs] == expected
     fresh = DisaggregatedEngine(m, engine_config(), mode="direct")
     assert fresh.generate(G["prompts"], max_new_tokens=8, batch_moves=True) == expected
+
+
+def test_batched_prefix_aware_moves_on_gpu(gpu):
+    """Batched direct moves with prefix sharing: a prefix whose copy is still pending
+    is shared (the one launch fills it before decode), and the blocks of a request
+    that finished on arrival, never copied, are not."""
+    from iekv.core.sequence import Status
+    from iekv.serve.disaggregated import DisaggregatedEngine
+
+    m = model(gpu, torch.bfloat16)
+    prefix = list(range(1000, 1064))
+    prompts = [prefix + list(range(1200 + 40 * i, 1200 + 40 * i + 20 + 7 * i)) for i in range(4)]
+    plain = DisaggregatedEngine(m, engine_config()).generate(prompts, max_new_tokens=6)
+    shared = DisaggregatedEngine(m, engine_config(), prefix_aware=True, mode="direct")
+    assert shared.generate(prompts, max_new_tokens=6, batch_moves=True) == plain
+    assert shared.stats.blocks_skipped == 4 * 3
+
+    engine = DisaggregatedEngine(m, engine_config(), prefix_aware=True, mode="direct")
+    pending: list = []
+    done = engine.handoff(prompts[0], 1, 0.0, pending)
+    assert done.status == Status.FINISHED and not pending
+    seq = engine.handoff(prompts[1], 6, 0.0, pending)
+    assert engine.stats.blocks_skipped == 0
+    engine.flush_moves(pending)
+    engine.decode_until_done()
+    assert seq.token_ids[seq.num_prompt:] == plain[1]
