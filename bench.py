@@ -45,7 +45,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # WRITE_SIZE) / (read + write bytes), from two rocprofv3 --pmc runs of this script
 # calibrated on a plain 4 GiB copy (FETCH_SIZE reads 0.5x, WRITE_SIZE 1.0x of its
 # known size); see profiles/kv_move_direct_cfg3_pmc.txt.
-PMC_TRAFFIC_RATIO = 1.0001
+PMC_TRAFFIC_RATIO = 1.0003
 METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff"
 
 
@@ -432,35 +432,49 @@ def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float) ->
 
 
 def sweep(legs: Legs, names: list[str]) -> list[dict]:
-    """Time each leg under every launch shape iekv_set_launch offers (3 steps after 1 warm-up).
+    """Time each leg under the launch shapes iekv_set_launch offers (3 steps after 1 warm-up).
 
-    ``order`` sets both workgroup orders (pool-writing and staging-writing launches).
+    Every workgroup order x chunk size (whole tiles, then 16 KiB down to 1 KiB
+    chunks) at one block per workgroup, unroll 8, non-temporal; then the whole-tile
+    runs of several blocks and the ordinary (temporal) accesses at each order's
+    best chunk. ``order`` sets both workgroup orders (pool-writing and
+    staging-writing launches).
     """
     from iekv import _native
 
     before = _native.get_launch()
     P = legs.w.payload_bytes
     rows = []
+
+    def measure(run, unroll, nt, order, chunk):
+        _native.set_launch(run, unroll, nt, order, order, chunk)
+        row = {"run_blocks": run, "unroll": unroll, "nontemporal": nt, "order": order,
+               "chunk_bytes": chunk}
+        for name in names:
+            ms, _, _ = time_leg(legs, name, 3, 1, per_launch=False)
+            nbytes = 4 * P if name == "pack_unpack" else 2 * P
+            row[name] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        rows.append(row)
+        log("[sweep] " + json.dumps(row))
+
     try:
         for order in (0, 1, 2, 4, 5, 6):
-            for nt in (1, 0):
-                for unroll in (4, 8, 16):
-                    for run in (1, 2, 4, 8, 16):
-                        _native.set_launch(run, unroll, nt, order, order)
-                        row = {"run_blocks": run, "unroll": unroll, "nontemporal": nt,
-                               "order": order}
-                        for name in names:
-                            ms, _, _ = time_leg(legs, name, 3, 1, per_launch=False)
-                            nbytes = 4 * P if name == "pack_unpack" else 2 * P
-                            row[name] = round(nbytes / (ms * 1e-3) / 1e9, 1)
-                        rows.append(row)
-                        log("[sweep] " + json.dumps(row))
+            for chunk in (0, 16384, 8192, 4096, 2048, 1024):
+                measure(1, 8, 1, order, chunk)
+        for order in (0, 1, 2, 4, 5, 6):
+            for run in (2, 4, 16):
+                measure(run, 8, 1, order, 0)
+            for unroll in (4, 16):
+                measure(1, unroll, 1, order, 0)
+            measure(1, 8, 0, order, 0)
+            measure(1, 8, 0, order, 4096)
     finally:
         _native.set_launch(**before)
     for name in names:
         best = max(rows, key=lambda r: r[name])
         log(f"[sweep] best {name}: {best[name]} GB/s at " + json.dumps(
-            {k: best[k] for k in ("run_blocks", "unroll", "nontemporal", "order")}))
+            {k: best[k] for k in ("run_blocks", "unroll", "nontemporal", "order",
+                                  "chunk_bytes")}))
     return rows
 
 
@@ -482,7 +496,7 @@ def main() -> int:
                     help="minimum CPU-baseline time (the sample handoff repeats until then)")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--launch", default="",
-                    help="run_blocks,unroll,nontemporal,order[,pack_order] for "
+                    help="run_blocks,unroll,nontemporal,order[,pack_order[,chunk_bytes]] for "
                          "iekv_set_launch (default: the library's)")
     ap.add_argument("--sweep", action="store_true",
                     help="time the legs under every launch shape instead of the benchmark line")

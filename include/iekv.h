@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 5
+#define IEKV_ABI_VERSION 6
 
 enum {
   IEKV_OK = 0,
@@ -144,11 +144,24 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                  const void* host_src, int64_t host_bytes, void* staging, int64_t staging_bytes,
                  hipStream_t compute, hipStream_t copy);
 
+/* Restore from scattered host images: like iekv_restore, but block i's image
+ * ([2L][T] bytes) is read from host_blocks[i], a HOST array of n_blocks host
+ * addresses (pinned memory for the copies to be asynchronous). Images that are
+ * adjacent in host memory are copied together. On return `copy` is ordered
+ * after the last unpack, as for iekv_restore.
+ * Replaces: the restore loop of a prefix plan's tier hits,
+ * `for key in offloaded: ... copier.write_block(block.id, payload)`
+ * (ie/core/block_manager.py:159-167), whose payloads the tier took one by one
+ * and which therefore live at unrelated host addresses, as one call. */
+int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                        const void* const* host_blocks, void* staging, int64_t staging_bytes,
+                        hipStream_t compute, hipStream_t copy);
+
 /* Launch shape of the move kernels (process-wide):
  *   run_blocks  blocks per workgroup run, 1..64; 0 = automatic (currently one
  *               block per workgroup); -1 keeps the current setting;
- *   unroll      16-byte accesses in flight per lane per step: 4, 8 or 16;
- *               0 keeps the current setting;
+ *   unroll      16-byte accesses in flight per lane per step: 1, 2, 4, 8 or
+ *               16 (capped by what a chunk needs); 0 keeps the current setting;
  *   nontemporal 1 for streaming (non-temporal) loads and stores, 0 for
  *               ordinary ones, -1 keeps the current setting;
  *   order       which (array, block) tiles are in flight together in the
@@ -158,14 +171,22 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
  *               run r + a, so 2L arrays and 2L blocks at once); adding 4
  *               gives each of the 8 XCDs one contiguous share of that order
  *               (with 5, its own eighth of the arrays); -1 keeps the current
- *               setting. Default 5;
+ *               setting;
  *   pack_order  the same choice for the launches that write a staging buffer
- *               (pack, offload). Default 0, which writes consecutive staging
- *               tiles from consecutive workgroups.
+ *               (pack, offload);
+ *   chunk_bytes with one block per workgroup, each tile is split into a
+ *               power-of-two number of chunks of at least this many bytes,
+ *               one workgroup per chunk (the chunks of one tile are adjacent
+ *               in the order); 0 moves whole tiles; a power of two from 64 to
+ *               1 MiB; -1 keeps the current setting. A launch that would
+ *               exceed the dispatch limit of 2^32 - 1 work-items halves the
+ *               split, then spreads over several launches.
+ * The defaults (run 0, unroll 8, nontemporal 1, order, pack_order and
+ * chunk_bytes) are the library's measured best; iekv_get_launch reports them.
  * No reference counterpart: a tuning knob for the launches the entry points
  * above make. */
 int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order,
-                    int32_t pack_order);
+                    int32_t pack_order, int32_t chunk_bytes);
 
 /* Per-launch timing, for measurement (calling thread only). After
  * iekv_profile_start(max_launches), each of the next max_launches kernel
@@ -181,7 +202,7 @@ int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count);
 
 /* Current launch shape, for reporting. */
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
-                    int32_t* order, int32_t* pack_order);
+                    int32_t* order, int32_t* pack_order, int32_t* chunk_bytes);
 
 #ifdef __cplusplus
 }

@@ -88,6 +88,13 @@ std::atomic<int> g_order{kXcdGrouped | kBlockMajor};
 // diagonal on every 70B-share padding (5.82 against 5.46 TB/s on average) and
 // faster or tied on every 8B padding (5.66 against 5.62).
 std::atomic<int> g_pack_order{0};
+// Bytes each workgroup moves of a tile: a tile larger than this splits into a
+// power-of-two number of chunks of at least this size, one workgroup each.
+// Swept on MI355X over whole tiles and 16 KiB down to 1 KiB chunks on the
+// Llama-3-8B, prefix-sharing and 70B-share workloads: 8 KiB was best or tied
+// on every leg (pack +5% on 32 KiB tiles, +1-2% elsewhere); chunks of 4 KiB
+// or less lost up to 3x to the fixed per-workgroup setup.
+std::atomic<int> g_chunk{8192};
 
 // ---------------------------------------------------------------------------
 // Device side
@@ -172,20 +179,23 @@ __device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
   }
 }
 
-// One workgroup per (array a, run of list entries [first, first+count)).
-// The order in which workgroups take (array, run) pairs decides which tiles
-// are in flight together. With w the workgroup's position in that order:
-//   kArrayMajor  w = run * n_arrays + a: the 2L tiles of one block; their
+// One workgroup per (array a, run of list entries [first, first+count), chunk
+// p of each tile). A tile of tile_vecs vectors splits into `parts` chunks of
+// tile_vecs / parts vectors; the workgroup moves chunk p of every tile in its
+// run. The order in which workgroups take (array, run) pairs decides which
+// tiles are in flight together. With u the pair's position in that order:
+//   kArrayMajor  u = run * n_arrays + a: the 2L tiles of one block; their
 //                addresses differ by multiples of the array stride;
-//   kBlockMajor  w = a * runs + run: random blocks of one array;
+//   kBlockMajor  u = a * runs + run: random blocks of one array;
 //   kDiagonal    as array-major, but array a takes run (run + a) mod runs, so
 //                the tiles in flight span 2L arrays AND 2L different blocks.
+// The chunks of one tile are consecutive: position w = u * parts + p.
 // Plain orders take w = blockIdx.x. The dispatcher deals consecutive
 // workgroups to the kXcds XCDs in turn, so with the kXcdGrouped flag set,
 // workgroup i (on XCD i mod kXcds) takes position w = start(XCD) + i / kXcds
 // instead: each XCD walks one contiguous share of the order (with
 // kBlockMajor, its own eighth of the arrays). Every order covers each
-// (array, run) pair exactly once.
+// (array, run, chunk) triple exactly once.
 
 // Position of workgroup `i` of `grid` when each XCD takes a contiguous share:
 // XCD x receives workgroups x, x + kXcds, ...; the first `grid % kXcds` XCDs
@@ -201,18 +211,20 @@ __global__ void __launch_bounds__(kThreads)
 kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
         char* __restrict__ dst_stage, const int32_t* __restrict__ src_ids,
         const int32_t* __restrict__ dst_ids, int32_t tile_vecs, int32_t n_blocks,
-        int32_t n_arrays, int32_t run, int32_t runs, int32_t order) {
+        int32_t n_arrays, int32_t run, int32_t runs, int32_t parts, int32_t order) {
   __shared__ int32_t s_src[kMaxRun];
   __shared__ int32_t s_dst[kMaxRun];
   const int w = (order & kXcdGrouped) ? xcd_grouped(blockIdx.x, gridDim.x) : blockIdx.x;
   const int base_order = order & ~kXcdGrouped;
+  const int p = w % parts;
+  const int u = w / parts;
   int a, r;
   if (base_order == kBlockMajor) {
-    a = w / runs;
-    r = w % runs;
+    a = u / runs;
+    r = u % runs;
   } else {
-    a = w % n_arrays;
-    r = w / n_arrays;
+    a = u % n_arrays;
+    r = u / n_arrays;
     if (base_order == kDiagonal) r = static_cast<int>((static_cast<int64_t>(r) + a) % runs);
   }
   const int first = r * run;
@@ -225,6 +237,8 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
   __syncthreads();
 
   const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
+  const int chunk_vecs = tile_vecs / parts;
+  const int64_t chunk_offset = static_cast<int64_t>(p) * chunk_vecs * sizeof(V);
   const char* src_arr = nullptr;
   char* dst_arr = nullptr;
   if constexpr (SRC_POOL) src_arr = array_base(src, a);
@@ -247,7 +261,8 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
     } else {
       d = dst_stage + (static_cast<int64_t>(first + j) * n_arrays + a) * tile_bytes;
     }
-    move_tile<V, U, NT>(as_global<V>(s), as_global<V>(d), tile_vecs);
+    move_tile<V, U, NT>(as_global<V>(s + chunk_offset), as_global<V>(d + chunk_offset),
+                        chunk_vecs);
   }
 }
 
@@ -319,20 +334,28 @@ thread_local Profiler g_profiler;
 
 using MoveKernel = void (*)(PoolView, PoolView, const char*, char*, const int32_t*,
                             const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
-                            int32_t);
+                            int32_t, int32_t);
 
+// Kernel for vectors of the widest width the alignment allows, keeping up to
+// `unroll` of them in flight per lane; `lane_vecs` (vectors per lane per
+// chunk) caps the unroll so small chunks do not carry dead predicated slots.
 template <bool SP, bool DP>
-MoveKernel pick_kernel(int align, int unroll, bool nt, int* vec_bytes) {
+MoveKernel pick_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
   if (align >= 16) {
     *vec_bytes = 16;
+    const int u = std::min(unroll, lane_vecs);
     if (nt) {
-      if (unroll >= 16) return kv_move<u32x4, 16, true, SP, DP>;
-      if (unroll >= 8) return kv_move<u32x4, 8, true, SP, DP>;
-      return kv_move<u32x4, 4, true, SP, DP>;
+      if (u >= 16) return kv_move<u32x4, 16, true, SP, DP>;
+      if (u >= 8) return kv_move<u32x4, 8, true, SP, DP>;
+      if (u >= 4) return kv_move<u32x4, 4, true, SP, DP>;
+      if (u >= 2) return kv_move<u32x4, 2, true, SP, DP>;
+      return kv_move<u32x4, 1, true, SP, DP>;
     }
-    if (unroll >= 16) return kv_move<u32x4, 16, false, SP, DP>;
-    if (unroll >= 8) return kv_move<u32x4, 8, false, SP, DP>;
-    return kv_move<u32x4, 4, false, SP, DP>;
+    if (u >= 16) return kv_move<u32x4, 16, false, SP, DP>;
+    if (u >= 8) return kv_move<u32x4, 8, false, SP, DP>;
+    if (u >= 4) return kv_move<u32x4, 4, false, SP, DP>;
+    if (u >= 2) return kv_move<u32x4, 2, false, SP, DP>;
+    return kv_move<u32x4, 1, false, SP, DP>;
   }
   if (align >= 8) { *vec_bytes = 8; return kv_move<u32x2, 4, false, SP, DP>; }
   if (align >= 4) { *vec_bytes = 4; return kv_move<uint32_t, 4, false, SP, DP>; }
@@ -373,6 +396,22 @@ class DeviceGuard {
 // of several tiles do).
 int auto_run(int64_t /*tile_bytes*/) { return 1; }
 
+// Chunks per tile for a requested chunk size: the largest power of two that
+// divides the tile's vector count and leaves chunks of at least chunk_bytes
+// (1 when chunk_bytes is 0 or the tile is no larger than the chunk).
+int chunk_parts(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes) {
+  if (chunk_bytes <= 0) return 1;
+  int parts = 1;
+  while (tile_vecs % (2 * parts) == 0 &&
+         (tile_vecs / (2 * parts)) * vec_bytes >= chunk_bytes)
+    parts *= 2;
+  return parts;
+}
+
+// A dispatch holds at most 2^32 - 1 work-items, so one launch takes at most
+// this many workgroups; larger moves are split over several launches.
+constexpr int64_t kMaxGrid = static_cast<int64_t>(UINT32_MAX) / kThreads;
+
 template <bool SP, bool DP>
 int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage, char* dst_stage,
                 const int32_t* src_ids, const int32_t* dst_ids, int32_t n_blocks,
@@ -380,28 +419,52 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
   if (n_blocks == 0) return IEKV_OK;
   const int run_setting = g_run.load();
   const int run = run_setting > 0 ? run_setting : auto_run(tile_bytes);
-  const int64_t runs = (static_cast<int64_t>(n_blocks) + run - 1) / run;
-  const int64_t grid = runs * n_arrays;
-  if (grid > INT32_MAX)
-    return set_error(IEKV_ERR_INVALID, "launch of %lld workgroups exceeds the grid limit",
-                     static_cast<long long>(grid));
   int vec = 16;
-  MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), g_nontemporal.load() != 0, &vec);
-  const int32_t tile_vecs = static_cast<int32_t>(tile_bytes / vec);
+  for (int a = 16; a > align; a >>= 1) vec = a >> 1;
+  const int64_t tile_vecs64 = tile_bytes / vec;
+  if (tile_vecs64 > INT32_MAX)
+    return set_error(IEKV_ERR_INVALID, "tile of %lld bytes is too large",
+                     static_cast<long long>(tile_bytes));
+  // Runs of several tiles keep whole tiles per workgroup; single-tile
+  // workgroups split each tile into chunks, halving the split while a launch
+  // of one run per array would not fit the grid.
+  int parts = run == 1 ? chunk_parts(tile_vecs64, vec, g_chunk.load()) : 1;
+  while (parts > 1 && static_cast<int64_t>(n_arrays) * parts > kMaxGrid) parts /= 2;
+  if (static_cast<int64_t>(n_arrays) * parts > kMaxGrid)
+    return set_error(IEKV_ERR_INVALID, "%d arrays exceed the grid limit", n_arrays);
+  const int64_t total_runs = (static_cast<int64_t>(n_blocks) + run - 1) / run;
+  while (parts > 1 && total_runs * n_arrays * parts > kMaxGrid) parts /= 2;
+  const int64_t lane_vecs = (tile_vecs64 / parts + kThreads - 1) / kThreads;
+  MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), static_cast<int>(
+                                         std::min<int64_t>(lane_vecs, 16)),
+                                     g_nontemporal.load() != 0, &vec);
+  const int32_t tile_vecs = static_cast<int32_t>(tile_vecs64);
   const int32_t order = DP ? g_order.load() : g_pack_order.load();
+  const int64_t runs_per_launch = std::min<int64_t>(total_runs, kMaxGrid / (int64_t(n_arrays) * parts));
+  const int64_t block_image = tile_bytes * n_arrays;
   Profiler& prof = g_profiler;
-  if (prof.on && prof.used < prof.events.size()) {
-    auto& ev = prof.events[prof.used++];
-    hipExtLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
-                          ev.first, ev.second, 0, view_of(sp), view_of(dp), src_stage,
-                          dst_stage, src_ids, dst_ids, tile_vecs, n_blocks, n_arrays, run,
-                          static_cast<int32_t>(runs), order);
-  } else {
-    hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream,
-                       view_of(sp), view_of(dp), src_stage, dst_stage, src_ids, dst_ids,
-                       tile_vecs, n_blocks, n_arrays, run, static_cast<int32_t>(runs), order);
+  for (int64_t r0 = 0; r0 < total_runs; r0 += runs_per_launch) {
+    const int64_t first = r0 * run;
+    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(runs_per_launch * run,
+                                                               n_blocks - first));
+    const int32_t runs = static_cast<int32_t>((cnt + run - 1) / run);
+    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * n_arrays * parts);
+    const int32_t* s_ids = SP ? src_ids + first : nullptr;
+    const int32_t* d_ids = DP ? dst_ids + first : nullptr;
+    const char* s_stage = SP ? nullptr : src_stage + first * block_image;
+    char* d_stage = DP ? nullptr : dst_stage + first * block_image;
+    if (prof.on && prof.used < prof.events.size()) {
+      auto& ev = prof.events[prof.used++];
+      hipExtLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, stream, ev.first, ev.second, 0,
+                            view_of(sp), view_of(dp), s_stage, d_stage, s_ids, d_ids, tile_vecs,
+                            cnt, n_arrays, run, runs, parts, order);
+    } else {
+      hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, stream, view_of(sp), view_of(dp),
+                         s_stage, d_stage, s_ids, d_ids, tile_vecs, cnt, n_arrays, run, runs,
+                         parts, order);
+    }
+    IEKV_HIP(hipGetLastError());
   }
-  IEKV_HIP(hipGetLastError());
   return IEKV_OK;
 }
 
@@ -469,6 +532,57 @@ void plan_slots(int64_t staging_bytes, int64_t block_bytes, int32_t n_blocks, in
   int64_t fit = staging_bytes / block_bytes;
   *n_slots = fit >= 2 ? 2 : 1;
   *slot_blocks = std::min<int64_t>(fit / *n_slots, n_blocks);
+}
+
+// Restore pipeline shared by iekv_restore and iekv_restore_blocks: chunk k of
+// the blocks is copied from host memory into a staging slot on `copy` (by
+// `load(slot, first, count)`) while `compute` unpacks chunk k-1 onto dst_ids.
+// Two slots when the staging buffer holds two blocks or more, else one.
+template <typename Load>
+int restore_pipeline(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                     void* staging, int64_t staging_bytes, hipStream_t compute,
+                     hipStream_t copy, Load load) {
+  int rc;
+  const int64_t block_bytes = image_bytes(dst, 1);
+  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
+    return rc;
+  if (n_blocks == 0) return IEKV_OK;
+  DeviceGuard guard(dst->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+
+  int n_slots;
+  int64_t slot_blocks;
+  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
+  const int align =
+      std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  Events loaded, unpacked, fence;
+  if ((rc = loaded.create(n_slots)) || (rc = unpacked.create(n_slots)) || (rc = fence.create(1)))
+    return rc;
+
+  // Entry fence: the copy stream must not overwrite staging while earlier
+  // compute-stream work still reads it.
+  IEKV_HIP(hipEventRecord(fence[0], compute));
+  IEKV_HIP(hipStreamWaitEvent(copy, fence[0], 0));
+
+  char* stage = static_cast<char*>(staging);
+  int last = 0;
+  for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
+    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
+    const int s = static_cast<int>(k % n_slots);
+    char* slot = stage + s * slot_blocks * block_bytes;
+    if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(copy, unpacked[s], 0));
+    if ((rc = load(slot, first, cnt))) return rc;
+    IEKV_HIP(hipEventRecord(loaded[s], copy));
+    IEKV_HIP(hipStreamWaitEvent(compute, loaded[s], 0));
+    if ((rc = launch_move<false, true>(nullptr, dst, slot, nullptr, nullptr, dst_ids + first,
+                                       cnt, dst->tile_bytes, dst->n_arrays, align, compute)))
+      return rc;
+    IEKV_HIP(hipEventRecord(unpacked[s], compute));
+    last = s;
+  }
+  // Later copy-stream work that writes staging is ordered after the last unpack.
+  IEKV_HIP(hipStreamWaitEvent(copy, unpacked[last], 0));
+  return IEKV_OK;
 }
 
 }  // namespace
@@ -636,6 +750,8 @@ int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, c
                      block_size, static_cast<long long>(pool->tile_bytes));
   if (n_tokens < 0) return set_error(IEKV_ERR_INVALID, "n_tokens is negative (%d)", n_tokens);
   if (n_tokens == 0) return IEKV_OK;
+  if (n_tokens > kMaxGrid * kRowsPerGroup)
+    return set_error(IEKV_ERR_INVALID, "%d tokens exceed one launch", n_tokens);
   if (!k || !v || !slots) return set_error(IEKV_ERR_INVALID, "k, v or slots is null");
   DeviceGuard guard(pool->device);
   if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", pool->device);
@@ -675,6 +791,8 @@ int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
   if (context_len < 0)
     return set_error(IEKV_ERR_INVALID, "context_len is negative (%d)", context_len);
   if (context_len == 0) return IEKV_OK;
+  if (context_len > kMaxGrid * kRowsPerGroup)
+    return set_error(IEKV_ERR_INVALID, "context of %d rows exceeds one launch", context_len);
   const int64_t row_bytes = pool->tile_bytes / block_size;
   if ((rc = check_buffer(out, out_bytes, row_bytes * context_len, "output"))) return rc;
   if (!block_table) return set_error(IEKV_ERR_INVALID, "block_table is null");
@@ -763,47 +881,45 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   if (need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
   if ((rc = check_buffer(host_src, host_bytes, need, "host"))) return rc;
   const int64_t block_bytes = image_bytes(dst, 1);
-  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
-    return rc;
-  if (n_blocks == 0) return IEKV_OK;
-  DeviceGuard guard(dst->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
-
-  int n_slots;
-  int64_t slot_blocks;
-  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
-  const int align =
-      std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
-  Events loaded, unpacked, fence;
-  if ((rc = loaded.create(n_slots)) || (rc = unpacked.create(n_slots)) || (rc = fence.create(1)))
-    return rc;
-
-  // Entry fence: the copy stream must not overwrite staging while earlier
-  // compute-stream work still reads it.
-  IEKV_HIP(hipEventRecord(fence[0], compute));
-  IEKV_HIP(hipStreamWaitEvent(copy, fence[0], 0));
-
   const char* host = static_cast<const char*>(host_src);
-  char* stage = static_cast<char*>(staging);
-  int last = 0;
-  for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
-    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
-    const int s = static_cast<int>(k % n_slots);
-    char* slot = stage + s * slot_blocks * block_bytes;
-    if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(copy, unpacked[s], 0));
-    IEKV_HIP(hipMemcpyAsync(slot, host + first * block_bytes, cnt * block_bytes,
-                            hipMemcpyHostToDevice, copy));
-    IEKV_HIP(hipEventRecord(loaded[s], copy));
-    IEKV_HIP(hipStreamWaitEvent(compute, loaded[s], 0));
-    if ((rc = launch_move<false, true>(nullptr, dst, slot, nullptr, nullptr, dst_ids + first,
-                                       cnt, dst->tile_bytes, dst->n_arrays, align, compute)))
-      return rc;
-    IEKV_HIP(hipEventRecord(unpacked[s], compute));
-    last = s;
-  }
-  // Later copy-stream work that writes staging is ordered after the last unpack.
-  IEKV_HIP(hipStreamWaitEvent(copy, unpacked[last], 0));
-  return IEKV_OK;
+  return restore_pipeline(
+      dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
+      [&](char* slot, int64_t first, int32_t cnt) -> int {
+        IEKV_HIP(hipMemcpyAsync(slot, host + first * block_bytes, cnt * block_bytes,
+                                hipMemcpyHostToDevice, copy));
+        return IEKV_OK;
+      });
+}
+
+int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                        const void* const* host_blocks, void* staging, int64_t staging_bytes,
+                        hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if ((rc = check_pool(dst, "destination")) ||
+      (rc = check_ids(dst_ids, n_blocks, "destination")))
+    return rc;
+  if (n_blocks > 0 && !host_blocks)
+    return set_error(IEKV_ERR_INVALID, "host block address list is null");
+  for (int32_t i = 0; i < n_blocks; ++i)
+    if (!host_blocks[i]) return set_error(IEKV_ERR_INVALID, "host block %d address is null", i);
+  const int64_t block_bytes = image_bytes(dst, 1);
+  return restore_pipeline(
+      dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
+      [&](char* slot, int64_t first, int32_t cnt) -> int {
+        // One copy per run of blocks whose images are adjacent in host memory.
+        for (int32_t i = 0; i < cnt;) {
+          const char* run_start = static_cast<const char*>(host_blocks[first + i]);
+          int32_t len = 1;
+          while (i + len < cnt &&
+                 static_cast<const char*>(host_blocks[first + i + len]) ==
+                     run_start + len * block_bytes)
+            ++len;
+          IEKV_HIP(hipMemcpyAsync(slot + i * block_bytes, run_start, len * block_bytes,
+                                  hipMemcpyHostToDevice, copy));
+          i += len;
+        }
+        return IEKV_OK;
+      });
 }
 
 int iekv_profile_start(int32_t max_launches) {
@@ -849,11 +965,11 @@ int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count) {
 }
 
 int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order,
-                    int32_t pack_order) {
+                    int32_t pack_order, int32_t chunk_bytes) {
   if (run_blocks < -1 || run_blocks > kMaxRun)
     return set_error(IEKV_ERR_INVALID, "run_blocks %d out of range", run_blocks);
-  if (unroll != 0 && unroll != 4 && unroll != 8 && unroll != 16)
-    return set_error(IEKV_ERR_INVALID, "unroll must be 4, 8 or 16 (got %d)", unroll);
+  if (unroll != 0 && unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8 && unroll != 16)
+    return set_error(IEKV_ERR_INVALID, "unroll must be 1, 2, 4, 8 or 16 (got %d)", unroll);
   if (nontemporal < -1 || nontemporal > 1)
     return set_error(IEKV_ERR_INVALID, "nontemporal must be -1, 0 or 1 (got %d)", nontemporal);
   if (!valid_order(order))
@@ -861,21 +977,28 @@ int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int
   if (!valid_order(pack_order))
     return set_error(IEKV_ERR_INVALID, "pack_order must be -1, 0, 1, 2, 4, 5 or 6 (got %d)",
                      pack_order);
+  if (chunk_bytes != -1 && chunk_bytes != 0 &&
+      (chunk_bytes < 64 || chunk_bytes > (1 << 20) || (chunk_bytes & (chunk_bytes - 1))))
+    return set_error(IEKV_ERR_INVALID,
+                     "chunk_bytes must be -1, 0 or a power of two from 64 to 1 MiB (got %d)",
+                     chunk_bytes);
   if (run_blocks >= 0) g_run.store(run_blocks);
   if (unroll) g_unroll.store(unroll);
   if (nontemporal >= 0) g_nontemporal.store(nontemporal);
   if (order >= 0) g_order.store(order);
   if (pack_order >= 0) g_pack_order.store(pack_order);
+  if (chunk_bytes >= 0) g_chunk.store(chunk_bytes);
   return IEKV_OK;
 }
 
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
-                    int32_t* order, int32_t* pack_order) {
+                    int32_t* order, int32_t* pack_order, int32_t* chunk_bytes) {
   if (run_blocks) *run_blocks = g_run.load();
   if (unroll) *unroll = g_unroll.load();
   if (nontemporal) *nontemporal = g_nontemporal.load();
   if (order) *order = g_order.load();
   if (pack_order) *pack_order = g_pack_order.load();
+  if (chunk_bytes) *chunk_bytes = g_chunk.load();
   return IEKV_OK;
 }
 

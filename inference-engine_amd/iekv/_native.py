@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 IEKV_OK = 0
 IEKV_ERR_INVALID = -1
@@ -37,9 +37,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                              c_void_p, c_void_p]),
     "iekv_restore": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p, c_int64,
                              c_void_p, c_void_p]),
-    "iekv_set_launch": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "iekv_restore_blocks": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64,
+                                    c_void_p, c_void_p]),
+    "iekv_set_launch": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "iekv_get_launch": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32),
-                                POINTER(c_int32), POINTER(c_int32)]),
+                                POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
     "iekv_profile_start": (c_int, [c_int32]),
     "iekv_profile_stop": (c_int, [POINTER(ctypes.c_float), c_int32, POINTER(c_int32)]),
 }
@@ -127,17 +129,17 @@ class Pool:
 
 
 def set_launch(run_blocks: int = -1, unroll: int = 0, nontemporal: int = -1,
-               order: int = -1, pack_order: int = -1) -> None:
+               order: int = -1, pack_order: int = -1, chunk_bytes: int = -1) -> None:
     """Launch shape of the move kernels; see iekv_set_launch in include/iekv.h."""
-    call("iekv_set_launch", run_blocks, unroll, nontemporal, order, pack_order)
+    call("iekv_set_launch", run_blocks, unroll, nontemporal, order, pack_order, chunk_bytes)
 
 
 def get_launch() -> dict[str, int]:
-    run, unroll, nt, order, pack_order = (c_int32() for _ in range(5))
+    run, unroll, nt, order, pack_order, chunk = (c_int32() for _ in range(6))
     call("iekv_get_launch", ctypes.byref(run), ctypes.byref(unroll), ctypes.byref(nt),
-         ctypes.byref(order), ctypes.byref(pack_order))
+         ctypes.byref(order), ctypes.byref(pack_order), ctypes.byref(chunk))
     return {"run_blocks": run.value, "unroll": unroll.value, "nontemporal": nt.value,
-            "order": order.value, "pack_order": pack_order.value}
+            "order": order.value, "pack_order": pack_order.value, "chunk_bytes": chunk.value}
 
 
 class LaunchTimer:

@@ -195,17 +195,28 @@ class BlockManager:
             self._claim_shared_block(block_id)
             seq.block_table.append(block_id)
 
+        # A copier with a batched write restores the whole prefix in one call
+        # after the last claim (see _write_restored); a protocol-only copier
+        # writes each block right after claiming it, as the reference does.
+        batched = getattr(self.copier, "write_blocks", None) if len(offloaded) > 1 else None
+        restores: list[tuple[int, object]] = []
         for key in offloaded:
             token_ids, payload = self.tier.take(key)
             # Claiming may offload a victim out of this very block: the victim's
-            # read is enqueued before this write, so it sees the old bytes.
+            # read is enqueued before this block's restore write, so it sees the
+            # old bytes.
             block = self._claim_free_block()
-            self.copier.write_block(block.id, payload)
+            if batched is None:
+                self.copier.write_block(block.id, payload)
+            else:
+                restores.append((block.id, payload))
             block.hash = key
             block.token_ids = list(token_ids)
             self.block_id_by_hash[key] = block.id
             seq.block_table.append(block.id)
             self.blocks_restored += 1
+        if restores:
+            self._write_restored(batched, restores)
 
         cached = len(resident) + len(offloaded)
         for _ in range(cached, seq.num_blocks):
@@ -215,6 +226,21 @@ class BlockManager:
         self.blocks_computed += seq.num_blocks - cached
         seq.num_computed = cached * self.block_size
         return seq.num_computed
+
+    @staticmethod
+    def _write_restored(write_blocks, restores: list[tuple[int, object]]) -> None:
+        """Write the tier payloads a prefix plan restored, with one batched call.
+
+        The reference writes each block right after claiming it
+        (ie/core/block_manager.py:159-167); writing them all after the last
+        claim has the same effect: a restore writes only blocks this allocation
+        claimed, which no later claim of it can take as a victim, and every
+        victim read those claims enqueued is issued before the writes (the HIP
+        copier flushes its queued reads first). The HIP copier gathers the
+        payloads' host images with one iekv_restore_blocks.
+        """
+        write_blocks([block_id for block_id, _ in restores],
+                     [payload for _, payload in restores])
 
     def free(self, seq: Sequence) -> None:
         for block_id in reversed(seq.block_table):

@@ -10,7 +10,9 @@ copies per block:
 * ``read_blocks(ids)``  -> one fused pack launch (iekv_pack), or the pinned-host
   offload pipeline (iekv_offload) when payloads live on the host;
 * ``write_blocks(ids, payloads)`` -> one unpack launch (iekv_unpack), or the
-  restore pipeline (iekv_restore) for host payloads;
+  restore pipeline for host payloads (iekv_restore for one buffer's
+  consecutive images, iekv_restore_blocks for images from unrelated buffers,
+  such as the offload tier's entries);
 * ``copy_blocks(source, src_ids, dst_ids)`` -> the direct pool-to-pool launch
   (iekv_copy_direct), which never materialises payloads.
 
@@ -25,6 +27,7 @@ cache reads and writes exactly as the reference's synchronous copies are.
 """
 from __future__ import annotations
 
+import ctypes
 import weakref
 from typing import Any, Iterable, Sequence as Seq
 
@@ -239,6 +242,7 @@ class HipSlotCopier:
         self.blocks_written = 0
         self.offload_launches = 0       # iekv_offload calls made
         self.blocks_offloaded = 0       # blocks those calls moved to the host
+        self.restore_launches = 0       # iekv_restore / iekv_restore_blocks calls made
         self._pending: list[tuple[int, weakref.ref]] = []
         self._copy_stream: torch.cuda.Stream | None = None
         self._staging: torch.Tensor | None = None
@@ -379,6 +383,8 @@ class HipSlotCopier:
         packed = _consecutive_views(payloads)
         if packed is not None:
             self._write_packed(ids, packed)
+        elif n > 1 and all(isinstance(p, BlockPayload) and p.packed.on_host for p in payloads):
+            self._restore_scattered(ids, payloads)
         else:
             for i, payload in enumerate(payloads):
                 one = _consecutive_views([payload]) if isinstance(payload, BlockPayload) \
@@ -397,9 +403,26 @@ class HipSlotCopier:
                          packed.data.data_ptr(), packed.nbytes, staging.data_ptr(),
                          staging.numel(), stream.cuda_stream, copy.cuda_stream)
             packed.mark(copy)
+            self.restore_launches += 1
         else:
             _native.call("iekv_unpack", self.pool.native.handle, ids.data_ptr(), n,
                          packed.data.data_ptr(), packed.nbytes, stream.cuda_stream)
+
+    def _restore_scattered(self, ids: torch.Tensor, payloads: Seq[BlockPayload]) -> None:
+        """Host payloads from unrelated buffers (tier entries) -> one iekv_restore_blocks."""
+        for p in payloads:
+            self._check_packed(p.packed)
+        n = ids.numel()
+        addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in payloads])
+        stream = torch.cuda.current_stream(self.device)
+        staging = self._host_staging(n)
+        copy = self.copy_stream()
+        _native.call("iekv_restore_blocks", self.pool.native.handle, ids.data_ptr(), n,
+                     addresses, staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                     copy.cuda_stream)
+        for root in {id(p.packed._root): p.packed._root for p in payloads}.values():
+            root.mark(copy)
+        self.restore_launches += 1
 
     def copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids) -> None:
         """Direct pool-to-pool move: tile ``src_ids[i]`` of ``source`` -> ``dst_ids[i]`` here."""

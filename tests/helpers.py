@@ -41,7 +41,14 @@ class RecordingCopier:
 
 
 class LoggingCopier:
-    """Wraps a copier and logs ["r"|"w", block_id] for every protocol call."""
+    """Wraps a copier and logs ["r"|"w", block_id] for every protocol call.
+
+    It offers only the reference's protocol (read_block / write_block), not the
+    HIP copier's batched calls, so callers take their per-block paths and the
+    log is the reference's call trace.
+    """
+
+    BATCHED = ("read_blocks", "write_blocks", "copy_blocks")
 
     def __init__(self, inner, log):
         self.inner = inner
@@ -56,6 +63,8 @@ class LoggingCopier:
         return self.inner.write_block(block_id, payload)
 
     def __getattr__(self, name):
+        if name in self.BATCHED:
+            raise AttributeError(name)
         return getattr(self.inner, name)
 
 

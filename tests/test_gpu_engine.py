@@ -159,6 +159,42 @@ def test_offload_does_not_change_tokens_on_gpu(gpu):
     assert st_on["restored"] > 0 and st_on["computed"] < st_off["computed"]
 
 
+def test_a_restored_prefix_is_written_with_one_batched_call(gpu):
+    """The golden scenario's revisit restores 3 tier blocks. The unwrapped HIP
+    copier writes them with one iekv_restore_blocks after the last claim; a
+    protocol-only wrapper gets the reference's three interleaved write_block
+    calls. Both leave the same block tables, tier and pool bytes."""
+    from iekv.engine.engine import Engine, EngineConfig
+    from iekv.engine.toy_model import ModelConfig, ToyTransformer
+
+    g = golden("offload")
+    runs = []
+    for wrap in (False, True):
+        m = ToyTransformer(ModelConfig(**g["model"]), seed=g["model_seed"], device=gpu)
+        engine = Engine(m, EngineConfig(block_size=16, num_blocks=12, max_batch_tokens=512,
+                                        offload_blocks=64))
+        hip = engine.blocks.copier
+        if wrap:
+            engine.blocks.copier = LoggingCopier(hip, [])
+        for prompt in g["prompts"]:
+            engine.generate([prompt], max_new_tokens=2, temperature=0.0)
+        before = hip.restore_launches
+        revisit = engine.generate([g["prompts"][0]], max_new_tokens=2, temperature=0.0)[0]
+        torch.cuda.synchronize()
+        pools = [t.clone() for t in list(hip.k_caches) + list(hip.v_caches)]
+        runs.append((revisit, hip.restore_launches - before, engine.blocks.stats(),
+                     list(engine.blocks.free_ids), list(engine.blocks.tier.entries), pools))
+    (tok_b, launches_b, st_b, free_b, keys_b, pools_b), \
+        (tok_p, launches_p, st_p, free_p, keys_p, pools_p) = runs
+    assert st_b == st_p == g["64"]["stats"] and st_b["restored"] == 3
+    assert launches_b == 1 and launches_p == 3
+    assert free_b == free_p == g["64"]["free_ids"]
+    assert keys_b == keys_p == g["64"]["tier_keys"]
+    assert tok_b == tok_p
+    for a, (x, y) in enumerate(zip(pools_b, pools_p)):
+        assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), a
+
+
 def test_evictions_are_offloaded_in_batches(gpu):
     from iekv.engine.engine import Engine, EngineConfig
     from iekv.engine.toy_model import ModelConfig, ToyTransformer

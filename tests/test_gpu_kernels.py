@@ -132,9 +132,10 @@ def test_narrow_and_odd_tiles(gpu, bs, heads, dim, dtype):
 
 def test_every_launch_shape_is_bit_exact(gpu):
     """Pack, unpack and direct copy under every run / unroll / non-temporal /
-    workgroup-order setting (order for the pool-writing launches, pack_order for
-    the staging-writing ones; 4-6 are the XCD-grouped orders, here on grids of
-    8 to 308 workgroups, most not a multiple of the 8 XCDs)."""
+    workgroup-order / chunk setting (order for the pool-writing launches,
+    pack_order for the staging-writing ones; 4-6 are the XCD-grouped orders,
+    here on grids of 8 to 19,712 workgroups, most not a multiple of the 8
+    XCDs; chunks of 64 B to whole 32 KiB tiles)."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -150,27 +151,88 @@ def test_every_launch_shape_is_bit_exact(gpu):
     handoff(src_o, dst_o, [src_ids], [dst_ids])
     before = _native.get_launch()
     try:
-        for run in (1, 3, 0, 64):
-            for unroll in (4, 8, 16):
-                for nt in (0, 1):
-                    for order in (0, 1, 2, 4, 5, 6):
-                        shape = (run, unroll, nt, order)
-                        _native.set_launch(run, unroll, nt, order, order)
-                        packed = src.read_blocks(src_ids)
-                        assert np.array_equal(packed.data.cpu().numpy(), want), shape
-                        for t in dk + dv:
-                            t.zero_()
-                        half = len(src_ids) // 2
-                        dst.write_blocks(dst_ids[:half], packed[:half])
-                        dst.copy_blocks(src, src_ids[half:], dst_ids[half:])
-                        torch.cuda.synchronize()
-                        got = host_bytes(dk) + host_bytes(dv)
-                        for g, w in zip(got, list(dst_o.k_caches) + list(dst_o.v_caches)):
-                            rows = np.concatenate([np.arange(b * bs, (b + 1) * bs)
-                                                   for b in dst_ids])
-                            assert np.array_equal(g[rows], w[rows]), shape
+        shapes = [(run, unroll, nt, order, chunk)
+                  for run in (1, 3, 0, 64) for unroll in (1, 4, 8, 16) for nt in (0, 1)
+                  for order in (0, 1, 2, 4, 5, 6) for chunk in (0, 4096)]
+        shapes += [(0, unroll, 1, order, chunk) for unroll in (1, 2, 8) for order in (0, 5)
+                   for chunk in (64, 512, 1024, 16384, 32768, 1 << 20)]
+        rows = np.concatenate([np.arange(b * bs, (b + 1) * bs) for b in dst_ids])
+        for shape in shapes:
+            run, unroll, nt, order, chunk = shape
+            _native.set_launch(run, unroll, nt, order, order, chunk)
+            packed = src.read_blocks(src_ids)
+            assert np.array_equal(packed.data.cpu().numpy(), want), shape
+            for t in dk + dv:
+                t.zero_()
+            half = len(src_ids) // 2
+            dst.write_blocks(dst_ids[:half], packed[:half])
+            dst.copy_blocks(src, src_ids[half:], dst_ids[half:])
+            torch.cuda.synchronize()
+            got = host_bytes(dk) + host_bytes(dv)
+            for g, w in zip(got, list(dst_o.k_caches) + list(dst_o.v_caches)):
+                assert np.array_equal(g[rows], w[rows]), shape
     finally:
         _native.set_launch(**before)
+
+
+def test_a_split_that_would_overflow_the_dispatch_is_halved(gpu):
+    """70,000 blocks x 4 arrays in 64-byte chunks of 4 KiB tiles would need
+    17.9M workgroups (over the 2^32 - 1 work-item limit of one dispatch): the
+    library halves the split to 32 chunks and moves every byte in one launch."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 16, 2, 2, 64   # 4 KiB uint8 tiles
+    n = 70_000
+    sk, sv = allocate(n + 16, bs, layers, heads, dim, torch.uint8, gpu, seed=21)
+    dk, dv = allocate(n + 16, bs, layers, heads, dim, torch.uint8, gpu, seed=22)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    rng = np.random.default_rng(23)
+    src_ids = rng.permutation(n + 16)[:n]
+    dst_ids = rng.permutation(n + 16)[:n]
+    before = _native.get_launch()
+    try:
+        _native.set_launch(0, 1, 1, 5, 0, 64)
+        with _native.LaunchTimer(8) as timer:
+            dst.copy_blocks(src, src_ids, dst_ids)
+        assert len(timer.durations_ms) == 1
+    finally:
+        _native.set_launch(**before)
+    torch.cuda.synchronize()
+    s_ids = torch.as_tensor(src_ids, device=gpu)
+    d_ids = torch.as_tensor(dst_ids, device=gpu)
+    for s_arr, d_arr in zip(sk + sv, dk + dv):
+        want = s_arr.view(-1, bs * heads * dim)
+        got = d_arr.view(-1, bs * heads * dim)
+        assert torch.equal(got[d_ids], want[s_ids])
+
+
+def test_a_move_beyond_one_dispatch_spreads_over_launches(gpu):
+    """9M 16-byte tiles x 2 arrays with whole-tile workgroups exceed one
+    dispatch (16,777,215 workgroups of 256 lanes): the library issues two
+    launches over consecutive entry ranges, and pack keeps the staging layout."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 1, 1, 1, 16    # 16-byte uint8 tiles
+    n = 9_000_000
+    sk, sv = allocate(n, bs, layers, heads, dim, torch.uint8, gpu, seed=31)
+    dk, dv = allocate(n, bs, layers, heads, dim, torch.uint8, gpu, seed=32)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(33)
+    src_ids = torch.randperm(n, device=gpu, generator=gen).to(torch.int32)
+    dst_ids = torch.randperm(n, device=gpu, generator=gen).to(torch.int32)
+    with _native.LaunchTimer(8) as timer:
+        dst.copy_blocks(src, src_ids, dst_ids)
+        packed = src.read_blocks(src_ids)
+    assert len(timer.durations_ms) == 4
+    torch.cuda.synchronize()
+    s_ids, d_ids = src_ids.long(), dst_ids.long()
+    for a, (s_arr, d_arr) in enumerate(zip(sk + sv, dk + dv)):
+        want = s_arr.view(n, 16)[s_ids]
+        assert torch.equal(d_arr.view(n, 16)[d_ids], want)
+        assert torch.equal(packed.data[:, a], want)
 
 
 def test_separately_allocated_layers_use_an_address_table(gpu):
@@ -328,6 +390,39 @@ def test_host_payloads_through_the_copier(gpu):
     assert_pool_equals(dk, dv, dst_o)
     assert np.array_equal(packed.synchronize().data.numpy(),
                           packed_image(pack(oracle_of(sk, sv, bs), [3, 14, 29, 0])))
+
+
+@pytest.mark.parametrize("staging_blocks", [1, 2, 3, 64])
+def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_blocks):
+    """Tier entries come from different offload batches: write_blocks gathers
+    their host images (scattered, some adjacent) with one iekv_restore_blocks,
+    through a staging buffer of 1 to 64 blocks (1 to 7 pipeline chunks)."""
+    from iekv.engine import copier as copier_mod
+    from iekv.engine.copier import HipSlotCopier
+
+    bs = 16
+    sk, sv = allocate(40, bs, 3, 2, 32, torch.bfloat16, gpu, seed=26)
+    dk, dv = allocate(40, bs, 3, 2, 32, torch.bfloat16, gpu, seed=27)
+    src = HipSlotCopier(sk, sv, bs, payload_location="host")
+    dst = HipSlotCopier(dk, dv, bs)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    first = src.read_blocks([5, 6, 7, 30])        # one offload batch
+    second = src.read_blocks([12, 0, 39])         # another
+    single = src.read_block(21)
+    payloads = [second[2], first[0], first[1], single, second[0], first[3], second[1]]
+    src_ids = [39, 5, 6, 21, 12, 30, 0]
+    dst_ids = [3, 17, 9, 33, 2, 25, 11]
+    old = copier_mod.HOST_STAGING_BYTES
+    copier_mod.HOST_STAGING_BYTES = staging_blocks * dst.pool.block_bytes
+    try:
+        dst.write_blocks(dst_ids, payloads)
+    finally:
+        copier_mod.HOST_STAGING_BYTES = old
+    assert dst.restore_launches == 1
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    assert_pool_equals(dk, dv, dst_o)
+    assert dst.blocks_written == 7
 
 
 def test_a_victim_read_sees_the_bytes_before_a_restore_overwrites_them(gpu):

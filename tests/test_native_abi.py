@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 5
+    assert lib.iekv_abi_version() == 6
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -72,6 +72,26 @@ def test_calls_reject_null_pools_and_negative_counts(lib):
     assert lib.iekv_offload(None, None, 1, None, 0, None, 0, None, None) == _native.IEKV_ERR_INVALID
     assert lib.iekv_restore(None, None, 1, None, 0, None, 0, None, None) == _native.IEKV_ERR_INVALID
     assert "null" in lib.iekv_last_error().decode()
+    assert lib.iekv_restore_blocks(None, None, 1, None, None, 0, None, None) == \
+        _native.IEKV_ERR_INVALID
+    assert "null" in lib.iekv_last_error().decode()
+
+
+def test_scattered_restore_rejects_missing_host_addresses(lib):
+    """A slab pool registers without touching the GPU; the host address list is
+    checked before anything is enqueued."""
+    from iekv import _native
+
+    pool = _native.Pool([1 << 20, (1 << 20) + 64 * 16], tile_bytes=64, num_blocks=16, device=0)
+    ids = (ctypes.c_int32 * 2)(0, 1)
+    rc = lib.iekv_restore_blocks(pool.handle, ids, 2, None, None, 0, None, None)
+    assert rc == _native.IEKV_ERR_INVALID
+    assert "host block address list is null" in lib.iekv_last_error().decode()
+    blocks = (ctypes.c_void_p * 2)(4096, None)
+    rc = lib.iekv_restore_blocks(pool.handle, ids, 2, blocks, None, 0, None, None)
+    assert rc == _native.IEKV_ERR_INVALID
+    assert "host block 1 address is null" in lib.iekv_last_error().decode()
+    pool.close()
 
 
 def test_default_launch_shape():
@@ -85,7 +105,8 @@ def test_default_launch_shape():
     out = subprocess.run([sys.executable, "-c", code, str(ROOT / "inference-engine_amd")],
                          capture_output=True, text=True, check=True, timeout=120)
     assert json.loads(out.stdout.strip().splitlines()[-1]) == {
-        "run_blocks": 0, "unroll": 8, "nontemporal": 1, "order": 5, "pack_order": 0}
+        "run_blocks": 0, "unroll": 8, "nontemporal": 1, "order": 5, "pack_order": 0,
+        "chunk_bytes": 8192}
 
 
 def test_launch_settings_are_validated(lib):
@@ -103,9 +124,15 @@ def test_launch_settings_are_validated(lib):
             _native.set_launch(order=bad)
         with pytest.raises(_native.NativeError):
             _native.set_launch(pack_order=bad)
-    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=6, pack_order=1)
+    for bad in (-2, 32, 100, 3000, 1 << 21):
+        with pytest.raises(_native.NativeError):
+            _native.set_launch(chunk_bytes=bad)
+    _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=6, pack_order=1,
+                       chunk_bytes=1024)
     assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "order": 6,
-                                    "pack_order": 1}
+                                    "pack_order": 1, "chunk_bytes": 1024}
+    _native.set_launch(unroll=1, chunk_bytes=0)
+    assert _native.get_launch()["unroll"] == 1 and _native.get_launch()["chunk_bytes"] == 0
     _native.set_launch(**before)
     assert _native.get_launch() == before
 
