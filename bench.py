@@ -45,7 +45,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # WRITE_SIZE) / (read + write bytes), from two rocprofv3 --pmc runs of this script
 # calibrated on a plain 4 GiB copy (FETCH_SIZE reads 0.5x, WRITE_SIZE 1.0x of its
 # known size); see profiles/kv_move_direct_cfg3_pmc.txt.
-PMC_TRAFFIC_RATIO = 1.0003
+PMC_TRAFFIC_RATIO = 1.0002
 METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff"
 
 

@@ -8,11 +8,14 @@
 //   pack   : pool[a][src_ids[i]]  ->  staging[i][a]
 //   unpack : staging[i][a]        ->  pool[a][dst_ids[i]]
 // One workgroup owns one (array a, run of up to `run` consecutive list
-// entries): it stages the run's block ids in LDS, then streams each tile with
-// wavefront-contiguous 16-byte loads and stores (every lane moves 16 B per
-// access, a wave64 covers 1 KiB, a workgroup 4 KiB per access step), keeping
-// `U` loads per lane in flight before the matching stores. The data is never
-// interpreted: it moves as 32-bit words, so every KV dtype is bit-exact.
+// entries, chunk of each tile). With one entry per run (the default) each tile
+// is split into chunks of at least the chunk size (4 KiB: one 16-byte vector
+// per lane), one workgroup per chunk, and the workgroup reads its id pair with
+// scalar loads; a run of several entries stages its ids in LDS. Data moves
+// with wavefront-contiguous 16-byte loads and stores (a wave64 covers 1 KiB,
+// a workgroup 4 KiB per access step), keeping up to `U` loads per lane in
+// flight before the matching stores. The data is never interpreted: it moves
+// as raw words, so every KV dtype is bit-exact.
 
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
@@ -90,11 +93,12 @@ std::atomic<int> g_order{kXcdGrouped | kBlockMajor};
 std::atomic<int> g_pack_order{0};
 // Bytes each workgroup moves of a tile: a tile larger than this splits into a
 // power-of-two number of chunks of at least this size, one workgroup each.
-// Swept on MI355X over whole tiles and 16 KiB down to 1 KiB chunks on the
-// Llama-3-8B, prefix-sharing and 70B-share workloads: 8 KiB was best or tied
-// on every leg (pack +5% on 32 KiB tiles, +1-2% elsewhere); chunks of 4 KiB
-// or less lost up to 3x to the fixed per-workgroup setup.
-std::atomic<int> g_chunk{8192};
+// Measured on MI355X (one box, all five benchmark workloads, 4 KiB against
+// 8 KiB): on 32 KiB tiles 4 KiB gains 2-6% on pack, unpack and pack->unpack
+// and ties on the direct copy; the prefix-sharing workload gains 2-6% on every
+// leg; 16 KiB tiles in 16,384-block pools (the 70B-share workload) lose 1-4%.
+// Against whole tiles, 8 KiB chunks were best or tied on every leg.
+std::atomic<int> g_chunk{4096};
 
 // ---------------------------------------------------------------------------
 // Device side
@@ -180,7 +184,7 @@ __device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
 }
 
 // One workgroup per (array a, run of list entries [first, first+count), chunk
-// p of each tile). A tile of tile_vecs vectors splits into `parts` chunks of
+// p of each tile); a run of several entries stages its ids in LDS. A tile of tile_vecs vectors splits into `parts` chunks of
 // tile_vecs / parts vectors; the workgroup moves chunk p of every tile in its
 // run. The order in which workgroups take (array, run) pairs decides which
 // tiles are in flight together. With u the pair's position in that order:
@@ -229,13 +233,6 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
   }
   const int first = r * run;
   const int count = min(run, n_blocks - first);
-  const int t = threadIdx.x;
-  if (t < count) {
-    if constexpr (SRC_POOL) s_src[t] = src_ids[first + t];
-    if constexpr (DST_POOL) s_dst[t] = dst_ids[first + t];
-  }
-  __syncthreads();
-
   const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
   const int chunk_vecs = tile_vecs / parts;
   const int64_t chunk_offset = static_cast<int64_t>(p) * chunk_vecs * sizeof(V);
@@ -243,6 +240,39 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
   char* dst_arr = nullptr;
   if constexpr (SRC_POOL) src_arr = array_base(src, a);
   if constexpr (DST_POOL) dst_arr = array_base(dst, a);
+
+  if (run == 1) {
+    // One block: its id pair is read with uniform (scalar) loads. Staging it
+    // in LDS would add a store, a barrier and a load before the first data
+    // access of a workgroup that lives for a single chunk.
+    const char* s;
+    char* d;
+    if constexpr (SRC_POOL) {
+      const int32_t id = src_ids[first];
+      if (id < 0 || id >= src.num_blocks) return;  // never address outside the pool
+      s = src_arr + id * tile_bytes;
+    } else {
+      s = src_stage + (static_cast<int64_t>(first) * n_arrays + a) * tile_bytes;
+    }
+    if constexpr (DST_POOL) {
+      const int32_t id = dst_ids[first];
+      if (id < 0 || id >= dst.num_blocks) return;
+      d = dst_arr + id * tile_bytes;
+    } else {
+      d = dst_stage + (static_cast<int64_t>(first) * n_arrays + a) * tile_bytes;
+    }
+    move_tile<V, U, NT>(as_global<V>(s + chunk_offset), as_global<V>(d + chunk_offset),
+                        chunk_vecs);
+    return;
+  }
+
+  // A run of several blocks stages its slice of the src -> dst id map in LDS.
+  const int t = threadIdx.x;
+  if (t < count) {
+    if constexpr (SRC_POOL) s_src[t] = src_ids[first + t];
+    if constexpr (DST_POOL) s_dst[t] = dst_ids[first + t];
+  }
+  __syncthreads();
 
   for (int j = 0; j < count; ++j) {
     const char* s;

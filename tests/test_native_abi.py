@@ -106,7 +106,7 @@ def test_default_launch_shape():
                          capture_output=True, text=True, check=True, timeout=120)
     assert json.loads(out.stdout.strip().splitlines()[-1]) == {
         "run_blocks": 0, "unroll": 8, "nontemporal": 1, "order": 5, "pack_order": 0,
-        "chunk_bytes": 8192}
+        "chunk_bytes": 4096}
 
 
 def test_launch_settings_are_validated(lib):
