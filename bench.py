@@ -5,7 +5,9 @@
 A step is one full handoff of the workload: every request's blocks move from
 the prefill pool to the decode pool under the destination ids a decode
 worker's BlockManager hands out (iekv.workloads). Both pools are resident in
-HBM before timing starts; the src pool holds N(0,1) values (raw random bytes
+HBM before timing starts, carved from one allocation with the prefill pool first
+(iekv.engine.pools.allocate_pool_pair, as DisaggregatedEngine allocates them;
+--separate-pools allocates them apart); the src pool holds N(0,1) values (raw random bytes
 without NaN codes for fp8). Legs:
 
   direct       one iekv_copy_direct launch per request (the headline: 2P bytes)
@@ -77,24 +79,33 @@ def fill_pool(arrays, dtype_name: str, seed: int) -> None:
 
 
 class Legs:
-    def __init__(self, workload, device, seed: int) -> None:
+    def __init__(self, workload, device, seed: int, pool_layout: str = "paired") -> None:
         import torch
 
         from iekv.engine.copier import issue_order
-        from iekv.engine.pools import KVPool, allocate_pool
+        from iekv.engine.pools import KVPool, allocate_pool, allocate_pool_pair
 
         self.torch = torch
         self.w = workload
         s = workload.shape
         dtype = torch_dtype(s.dtype)
         t0 = time.perf_counter()
-        self.src_k, self.src_v = allocate_pool(workload.src_pool_blocks, s.block_size, s.layers,
-                                               s.kv_heads, s.head_dim, dtype=dtype,
-                                               device=device, zero=False)
-        fill_pool(self.src_k + self.src_v, s.dtype, seed)
-        self.dst_k, self.dst_v = allocate_pool(workload.dst_pool_blocks, s.block_size, s.layers,
-                                               s.kv_heads, s.head_dim, dtype=dtype,
-                                               device=device, zero=True)
+        self.pool_layout = pool_layout
+        if pool_layout == "paired":
+            (self.src_k, self.src_v), (self.dst_k, self.dst_v) = allocate_pool_pair(
+                workload.src_pool_blocks, workload.dst_pool_blocks, s.block_size, s.layers,
+                s.kv_heads, s.head_dim, dtype=dtype, device=device, zero=False)
+            fill_pool(self.src_k + self.src_v, s.dtype, seed)
+            for t in self.dst_k + self.dst_v:
+                t.zero_()
+        else:
+            self.src_k, self.src_v = allocate_pool(workload.src_pool_blocks, s.block_size,
+                                                   s.layers, s.kv_heads, s.head_dim, dtype=dtype,
+                                                   device=device, zero=False)
+            fill_pool(self.src_k + self.src_v, s.dtype, seed)
+            self.dst_k, self.dst_v = allocate_pool(workload.dst_pool_blocks, s.block_size,
+                                                   s.layers, s.kv_heads, s.head_dim, dtype=dtype,
+                                                   device=device, zero=True)
         self.src = KVPool(self.src_k, self.src_v, s.block_size)
         self.dst = KVPool(self.dst_k, self.dst_v, s.block_size)
         # pack/unpack move blocks in table order (the payload layout); direct copies
@@ -500,6 +511,9 @@ def main() -> int:
                          "iekv_set_launch (default: the library's)")
     ap.add_argument("--sweep", action="store_true",
                     help="time the legs under every launch shape instead of the benchmark line")
+    ap.add_argument("--separate-pools", action="store_true",
+                    help="allocate the two pools separately instead of as one reservation "
+                         "(prefill pool first)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -524,7 +538,7 @@ def main() -> int:
     w = workloads.make(args.config, args.seed, args.slack)
     log(f"[bench] {w.name}: {w.num_requests} requests, {w.num_blocks} blocks, "
         f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B")
-    legs = Legs(w, device, args.seed)
+    legs = Legs(w, device, args.seed, "separate" if args.separate_pools else "paired")
     P = w.payload_bytes
     if args.sweep:
         names = [x for x in args.legs.split(",")
@@ -590,6 +604,8 @@ def main() -> int:
             "kv_dtype": w.shape.dtype, "requests": w.num_requests, "blocks": w.num_blocks,
             "payload_bytes": P, "tile_bytes": w.shape.tile_bytes,
             "launch": _native.get_launch(),
+            "pools": ("two allocations" if args.separate_pools
+                      else "one allocation, prefill pool first"),
         },
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "blocks_per_s": res["blocks_per_s"],

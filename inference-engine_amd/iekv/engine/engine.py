@@ -63,8 +63,16 @@ def default_copier_factory(k_caches, v_caches, block_size: int, role: str):
 
 
 class Engine:
+    """ie/engine/engine.py:28-127.
+
+    ``caches`` (this build's addition) hands the engine a pool allocated by the
+    caller, ``(k_caches, v_caches)`` with ``num_blocks * block_size`` rows per
+    array, instead of ``model.allocate_caches``; the disaggregation workers use
+    it to share one reservation.
+    """
+
     def __init__(self, model, config: EngineConfig | None = None,
-                 copier_factory: CopierFactory | None = None) -> None:
+                 copier_factory: CopierFactory | None = None, caches=None) -> None:
         self.model = model
         self.config = config or EngineConfig()
         self.copier_factory = copier_factory or default_copier_factory
@@ -72,8 +80,13 @@ class Engine:
             raise ValueError("preemption must be 'recompute' or 'swap'")
         self.blocks = BlockManager(self.config.num_blocks, self.config.block_size)
         self.generator = np.random.default_rng(self.config.seed)
-        self.k_caches, self.v_caches = model.allocate_caches(self.config.num_blocks,
-                                                             self.config.block_size)
+        if caches is None:
+            caches = model.allocate_caches(self.config.num_blocks, self.config.block_size)
+        self.k_caches, self.v_caches = caches
+        rows = self.config.num_blocks * self.config.block_size
+        if (len(self.k_caches) != len(self.v_caches)
+                or any(len(t) != rows for t in list(self.k_caches) + list(self.v_caches))):
+            raise ValueError(f"caches must hold {rows} rows per array, K and V per layer")
         self.swapper = None
         if self.config.preemption == "swap":
             self.swapper = self.copier_factory(self.k_caches, self.v_caches,

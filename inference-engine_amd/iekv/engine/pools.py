@@ -32,6 +32,38 @@ def allocate_pool(num_blocks: int, block_size: int, num_layers: int, num_kv_head
     return [slab[0, l] for l in range(num_layers)], [slab[1, l] for l in range(num_layers)]
 
 
+def allocate_pool_pair(first_blocks: int, second_blocks: int, block_size: int,
+                       num_layers: int, num_kv_heads: int, head_dim: int, *,
+                       dtype: torch.dtype = torch.float16,
+                       device: str | torch.device = "cuda", zero: bool = True):
+    """Two pools of the same layout carved from ONE allocation, the first at the lower addresses.
+
+    Returns ``((k_first, v_first), (k_second, v_second))``; each pool is the slab
+    ``[2, L, N*bs, H, D]`` that :func:`allocate_pool` makes, and the second slab
+    starts right after the first. Give the prefill (source) pool the first slot
+    and the decode (destination) pool the second: on MI355X a direct copy from
+    the lower pool of one reservation into the upper one measured 3% faster on
+    the Llama-3-8B-shape handoff (6.29 against 6.11 TB/s for two separate
+    allocations, three boxes) and 10-18% faster with 37 GB pools, and 5% slower
+    in the opposite direction; splitting each array into halves instead gained
+    nothing.
+    """
+    if min(first_blocks, second_blocks, block_size, num_layers, num_kv_heads, head_dim) <= 0:
+        raise ValueError("pool dimensions must be positive")
+    row = num_kv_heads * head_dim
+    n_first = 2 * num_layers * first_blocks * block_size * row
+    n_second = 2 * num_layers * second_blocks * block_size * row
+    flat = (torch.zeros if zero else torch.empty)(n_first + n_second, dtype=dtype, device=device)
+    pools = []
+    for start, blocks in ((0, first_blocks), (n_first, second_blocks)):
+        n = 2 * num_layers * blocks * block_size * row
+        slab = flat[start:start + n].view(2, num_layers, blocks * block_size, num_kv_heads,
+                                          head_dim)
+        pools.append(([slab[0, l] for l in range(num_layers)],
+                      [slab[1, l] for l in range(num_layers)]))
+    return pools[0], pools[1]
+
+
 class KVPool:
     """A validated, registered set of per-layer caches (K arrays then V arrays)."""
 

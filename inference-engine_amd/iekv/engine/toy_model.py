@@ -21,7 +21,7 @@ import numpy as np
 import torch
 
 from ..core.layout import BatchLayout
-from .pools import allocate_pool
+from .pools import allocate_pool, allocate_pool_pair
 
 
 @dataclass(slots=True)
@@ -126,6 +126,13 @@ class ToyTransformer:
         c = self.config
         return allocate_pool(num_blocks, block_size, c.num_layers, c.num_kv_heads, c.head_dim,
                              dtype=self.cache_dtype, device=self.device)
+
+    def allocate_cache_pair(self, first_blocks: int, second_blocks: int, block_size: int):
+        """Two pools in one reservation (prefill first); see ``allocate_pool_pair``."""
+        c = self.config
+        return allocate_pool_pair(first_blocks, second_blocks, block_size, c.num_layers,
+                                  c.num_kv_heads, c.head_dim, dtype=self.cache_dtype,
+                                  device=self.device)
 
     def _pool(self, k_caches, v_caches, block_size: int):
         from .pools import KVPool

@@ -114,10 +114,10 @@ class PrefillWorker:
     """Runs prompts to completion and packages their KV (ie/serve/disaggregated.py:39-66)."""
 
     def __init__(self, model, config: EngineConfig, *, mode: str = "pack",
-                 copier_factory: CopierFactory | None = None) -> None:
+                 copier_factory: CopierFactory | None = None, caches=None) -> None:
         if mode not in MODES:
             raise ValueError(f"mode must be one of {MODES}")
-        self.engine = Engine(model, config, copier_factory=copier_factory)
+        self.engine = Engine(model, config, copier_factory=copier_factory, caches=caches)
         self.copier = self.engine.make_copier("transfer")
         self.mode = mode
 
@@ -160,8 +160,8 @@ class DecodeWorker:
     """Admits transfers into its pool and decodes them (ie/serve/disaggregated.py:69-96)."""
 
     def __init__(self, model, config: EngineConfig, *, prefix_aware: bool = False,
-                 copier_factory: CopierFactory | None = None) -> None:
-        self.engine = Engine(model, config, copier_factory=copier_factory)
+                 copier_factory: CopierFactory | None = None, caches=None) -> None:
+        self.engine = Engine(model, config, copier_factory=copier_factory, caches=caches)
         self.copier = self.engine.make_copier("transfer")
         self.prefix_aware = prefix_aware
 
@@ -261,11 +261,19 @@ class DisaggregatedEngine:
 
     def __init__(self, model, config: EngineConfig | None = None, *, mode: str = "pack",
                  prefix_aware: bool = False,
-                 copier_factory: CopierFactory | None = None) -> None:
+                 copier_factory: CopierFactory | None = None,
+                 paired_pools: bool = True) -> None:
         config = config or EngineConfig()
-        self.prefill = PrefillWorker(model, config, mode=mode, copier_factory=copier_factory)
+        # Both pools live in one GPU's HBM: with a model that can allocate them
+        # as one reservation (prefill pool first), the handoff copies run from
+        # the lower pool into the upper one, the faster orientation on MI355X.
+        pair = getattr(model, "allocate_cache_pair", None) if paired_pools else None
+        caches = (pair(config.num_blocks, config.num_blocks, config.block_size)
+                  if pair is not None else (None, None))
+        self.prefill = PrefillWorker(model, config, mode=mode, copier_factory=copier_factory,
+                                     caches=caches[0])
         self.decode = DecodeWorker(model, config, prefix_aware=prefix_aware,
-                                   copier_factory=copier_factory)
+                                   copier_factory=copier_factory, caches=caches[1])
         self.stats = DisaggregationStats()
 
     def handoff(self, prompt: list[int], max_new_tokens: int, temperature: float = 0.0,

@@ -239,3 +239,19 @@ def test_a_batched_request_finished_on_arrival_leaves_no_shared_prefix():
 def test_batched_moves_need_direct_mode():
     with pytest.raises(ValueError):
         split().generate(G["prompts"], batch_moves=True)
+
+
+def test_the_two_pools_share_one_reservation_with_prefill_first():
+    """With a model that can allocate a pool pair, the workers' pools are one
+    allocation, prefill's below decode's; tables and tokens are unchanged, and
+    separate allocations (paired_pools=False) give the same output."""
+    paired = split()
+    pk, dk = paired.prefill.engine.k_caches, paired.decode.engine.k_caches
+    assert pk[0].untyped_storage().data_ptr() == dk[0].untyped_storage().data_ptr()
+    assert pk[0].data_ptr() < dk[0].data_ptr()
+    apart = split(paired_pools=False)
+    assert apart.prefill.engine.k_caches[0].untyped_storage().data_ptr() != \
+        apart.decode.engine.k_caches[0].untyped_storage().data_ptr()
+    want = G["disaggregated"]["10"]
+    assert paired.generate(G["prompts"], max_new_tokens=10, temperature=0.0) == want
+    assert apart.generate(G["prompts"], max_new_tokens=10, temperature=0.0) == want

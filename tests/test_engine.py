@@ -74,3 +74,40 @@ def test_swap_preemption_keeps_tokens_and_skips_recomputation():
 def test_unknown_preemption_mode_is_rejected():
     with pytest.raises(ValueError):
         engine(preemption="teleport")
+
+
+def test_a_pool_pair_is_one_allocation_with_the_first_pool_below():
+    import torch
+
+    from iekv.engine.pools import allocate_pool_pair
+
+    (ak, av), (bk, bv) = allocate_pool_pair(5, 7, 4, 3, 2, 8, dtype=torch.bfloat16, device="cpu")
+    assert len(ak) == len(av) == len(bk) == len(bv) == 3
+    assert all(t.shape == (20, 2, 8) for t in ak + av)
+    assert all(t.shape == (28, 2, 8) for t in bk + bv)
+    assert all(t.is_contiguous() for t in ak + av + bk + bv)
+    # one reservation: each pool is a [2, L, N*bs, H, D] slab, the second right after the first
+    assert ak[0].untyped_storage().data_ptr() == bk[0].untyped_storage().data_ptr()
+    first_bytes = 2 * 3 * 20 * 2 * 8 * 2
+    assert bk[0].data_ptr() - ak[0].data_ptr() == first_bytes
+    assert av[0].data_ptr() - ak[0].data_ptr() == 3 * 20 * 2 * 8 * 2
+    assert all(not t.any() for t in ak + av + bk + bv)
+    av[2].fill_(1)
+    assert all(not t.any() for t in bk + bv + ak)
+
+
+def test_the_engine_accepts_preallocated_caches_of_its_size():
+    import torch
+
+    from iekv.engine.engine import Engine, EngineConfig
+    from iekv.engine.pools import allocate_pool
+    from iekv.engine.toy_model import ModelConfig, ToyTransformer
+
+    model = ToyTransformer(ModelConfig(**SMALL), seed=0, device="cpu")
+    caches = allocate_pool(16, 8, 2, 2, 8, dtype=torch.float32, device="cpu")
+    e = Engine(model, EngineConfig(block_size=8, num_blocks=16), copier_factory=oracle_factory,
+               caches=caches)
+    assert e.k_caches is caches[0]
+    with pytest.raises(ValueError):
+        Engine(model, EngineConfig(block_size=8, num_blocks=17), copier_factory=oracle_factory,
+               caches=caches)
