@@ -130,6 +130,55 @@ def test_narrow_and_odd_tiles(gpu, bs, heads, dim, dtype):
     assert_pool_equals(dk, dv, dst_o)
 
 
+RANDOM_CASES = 48
+
+
+@pytest.mark.parametrize("case", range(RANDOM_CASES))
+def test_random_tiles_and_launch_shapes_match_the_oracle(gpu, case):
+    """Seeded random tile shapes (1 B to 96 KiB, every vector width, tiles that
+    split into uneven chunk counts), random tables and a random launch shape
+    (run, unroll, order, chunk, non-temporal); pack -> unpack for half the
+    request and the direct copy for the rest, byte for byte against the oracle."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    rng = np.random.default_rng(1000 + case)
+    dtype = [torch.uint8, torch.float16, torch.bfloat16, torch.float32][rng.integers(4)]
+    elem = torch.tensor([], dtype=dtype).element_size()
+    while True:
+        bs = int(rng.choice([1, 2, 3, 4, 8, 16, 32]))
+        heads = int(rng.integers(1, 9))
+        dim = int(rng.choice([1, 3, 8, 16, 24, 64, 96, 128]))
+        if bs * heads * dim * elem <= 96 << 10:
+            break
+    layers = int(rng.integers(1, 4))
+    n_src, n_dst = int(rng.integers(8, 48)), int(rng.integers(8, 48))
+    count = int(rng.integers(2, min(n_src, n_dst) + 1))
+    shape = (int(rng.choice([0, 1, 3])), int(rng.choice([1, 2, 4, 8, 16])), int(rng.integers(2)),
+             int(rng.choice([0, 1, 2, 4, 5, 6])), int(rng.choice([0, 1, 2, 4, 5, 6])),
+             int(rng.choice([0, 64, 256, 1024, 4096, 8192])))
+    sk, sv = allocate(n_src, bs, layers, heads, dim, dtype, gpu, seed=2000 + case)
+    dk, dv = allocate(n_dst, bs, layers, heads, dim, dtype, gpu, seed=3000 + case)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    src_ids, dst_ids = random_tables(rng, n_src, n_dst, count)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    before = _native.get_launch()
+    try:
+        _native.set_launch(*shape)
+        half = count // 2
+        packed = src.read_blocks(src_ids[:half])
+        dst.write_blocks(dst_ids[:half], packed)
+        dst.copy_blocks(src, src_ids[half:], dst_ids[half:])
+        torch.cuda.synchronize()
+    finally:
+        _native.set_launch(**before)
+    label = (case, dtype, bs, heads, dim, layers, count, shape)
+    assert np.array_equal(packed.data.cpu().numpy(),
+                          packed_image(pack(oracle_of(sk, sv, bs), src_ids[:half]))), label
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    assert_pool_equals(dk, dv, dst_o)
+
+
 def test_every_launch_shape_is_bit_exact(gpu):
     """Pack, unpack and direct copy under every run / unroll / non-temporal /
     workgroup-order / chunk setting (order for the pool-writing launches,
