@@ -15,7 +15,8 @@ without NaN codes for fp8). Legs:
   pack         the pack half alone (2P bytes); unpack: the unpack half alone (2P bytes)
   batched      all requests' blocks in ONE direct launch (2P bytes)
   copier       the drop-in Python path: HipSlotCopier.copy_blocks per request with the
-               block tables as Python lists (id checks and staging included; 2P bytes)
+               block tables as Python lists (id checks and hand-over included; 2P bytes)
+  copier_pack_unpack  the same for pack mode: read_blocks then write_blocks (4P bytes)
 
 ``value`` is the direct leg's algorithmic read+write bandwidth, 2P / step
 time, in GB/s (P = blocks x 2L x T); the step time comes from two HIP events
@@ -135,7 +136,7 @@ class Legs:
         sizes = [len(t) for t in self.w.src_tables]
         if name in ("direct", "copier"):
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
-        if name == "pack_unpack":
+        if name in ("pack_unpack", "copier_pack_unpack"):
             return [x for r, n in enumerate(sizes) for x in ((2 * n * bb, r), (2 * n * bb, r))]
         if name in ("pack", "unpack"):
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
@@ -151,18 +152,30 @@ class Legs:
             _native.call("iekv_copy_direct", self.src.native.handle, self.dst.native.handle,
                          s.data_ptr(), d.data_ptr(), s.numel(), h)
 
-    def copier(self) -> None:
-        """The drop-in Python path: HipSlotCopier.copy_blocks per request, given the
-        request's block tables as Python lists (id staging and checks included)."""
+    def _drop_in(self):
+        """HipSlotCopier pair over the two pools (the drop-in Python API)."""
         if not hasattr(self, "_copiers"):
             from iekv.engine.copier import HipSlotCopier
 
             bs = self.w.shape.block_size
             self._copiers = (HipSlotCopier(self.src_k, self.src_v, bs),
                              HipSlotCopier(self.dst_k, self.dst_v, bs))
-        src, dst = self._copiers
+        return self._copiers
+
+    def copier(self) -> None:
+        """The drop-in Python path: HipSlotCopier.copy_blocks per request, given the
+        request's block tables as Python lists (id checks and hand-over included)."""
+        src, dst = self._drop_in()
         for s, d in zip(self.w.src_tables, self.w.dst_tables):
             dst.copy_blocks(src, s, d)
+
+    def copier_pack_unpack(self) -> None:
+        """The drop-in Python path of pack mode: read_blocks then write_blocks per request
+        with the tables as Python lists (a new payload buffer per request, as the
+        reference's KVTransfer holds one)."""
+        src, dst = self._drop_in()
+        for s, d in zip(self.w.src_tables, self.w.dst_tables):
+            dst.write_blocks(d, src.read_blocks(s))
 
     def pack_unpack(self) -> None:
         from iekv import _native
@@ -383,7 +396,7 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
         "avg_launch_us": round(1000 * total_ms / max(1, len(durations)), 2),
         "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
     }
-    if name in ("direct", "copier", "pack_unpack", "pack", "unpack"):
+    if name in ("direct", "copier", "pack_unpack", "copier_pack_unpack", "pack", "unpack"):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
                                  "p50": round(req_ms[len(req_ms) // 2], 4),
                                  "p99": round(req_ms[min(len(req_ms) - 1,
@@ -515,7 +528,7 @@ def main() -> int:
                     help="spare blocks per pool for cfg3/cfg4 (default 64)")
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
                     help="comma list of direct, pack_unpack, pack, unpack, batched, copier, "
-                         "plain_copy, host_roundtrip")
+                         "copier_pack_unpack, plain_copy, host_roundtrip")
     ap.add_argument("--cpu-blocks", type=int, default=1536,
                     help="blocks in the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -576,12 +589,12 @@ def main() -> int:
             continue
         legs.clear_dst()
         ms, wall, launches = time_leg(legs, name, args.steps, args.warmup)
-        nbytes = 4 * P if name == "pack_unpack" else 2 * P
+        nbytes = 4 * P if name in ("pack_unpack", "copier_pack_unpack") else 2 * P
         if name == "plain_copy":
             nbytes = 2 * (4 << 30)
         res, kgbs, avg_us, avg_bytes = summarize(legs, name, ms, launches, nbytes, args.steps)
         res["wall_s"] = round(wall, 3)
-        if name == "pack_unpack":
+        if name in ("pack_unpack", "copier_pack_unpack"):
             res["effective_handoff_GBps"] = round(2 * P / (ms * 1e-3) / 1e9, 1)
         if not args.no_verify and name != "plain_copy":
             check = {"pack": legs.verify_pack, "unpack": legs.verify_unpack}.get(name, legs.verify)

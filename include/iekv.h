@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 6
+#define IEKV_ABI_VERSION 7
 
 enum {
   IEKV_OK = 0,
@@ -99,6 +99,24 @@ int iekv_pack(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
  * single-block restore write (ie/core/block_manager.py:162). */
 int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                 const void* staging, int64_t staging_bytes, hipStream_t stream);
+
+/* Most block ids a call with HOST ids (the *_ids entry points below) takes. */
+#define IEKV_INLINE_IDS 256
+
+/* The same three moves with the block ids given in HOST memory, for at most
+ * IEKV_INLINE_IDS blocks: the ids are range-checked on the host and travel in
+ * the launch's own kernel arguments, so the caller needs no device id buffer
+ * and no host-to-device id copy sits on the stream between launches.
+ * One block per workgroup whatever iekv_set_launch's run_blocks.
+ * Replace: the same reference lines as iekv_copy_direct, iekv_pack and
+ * iekv_unpack, for the per-request calls of the disaggregation workers
+ * (ie/serve/disaggregated.py:50, 81-82), whose tables are host lists. */
+int iekv_copy_direct_ids(const iekv_pool* src, const iekv_pool* dst, const int32_t* src_ids,
+                         const int32_t* dst_ids, int32_t n_blocks, hipStream_t stream);
+int iekv_pack_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, void* staging,
+                  int64_t staging_bytes, hipStream_t stream);
+int iekv_unpack_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                    const void* staging, int64_t staging_bytes, hipStream_t stream);
 
 /* Slot scatter of one layer's new K/V rows: row i of k (and of v), each
  * tile_bytes/block_size bytes, contiguous [n_tokens][row], lands in row

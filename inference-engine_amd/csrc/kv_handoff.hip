@@ -184,7 +184,7 @@ __device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
 }
 
 // One workgroup per (array a, run of list entries [first, first+count), chunk
-// p of each tile); a run of several entries stages its ids in LDS. A tile of tile_vecs vectors splits into `parts` chunks of
+// p of each tile). A tile of tile_vecs vectors splits into `parts` chunks of
 // tile_vecs / parts vectors; the workgroup moves chunk p of every tile in its
 // run. The order in which workgroups take (array, run) pairs decides which
 // tiles are in flight together. With u the pair's position in that order:
@@ -210,6 +210,65 @@ __device__ __forceinline__ int xcd_grouped(int i, int grid) {
   return x * q + min(x, rem) + i / kXcds;
 }
 
+// This workgroup's (array, run, chunk) in the order described above.
+struct Place {
+  int a, r, p;
+};
+
+__device__ __forceinline__ Place place_of(int32_t n_arrays, int32_t runs, int32_t parts,
+                                          int32_t order) {
+  const int w = (order & kXcdGrouped) ? xcd_grouped(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int base_order = order & ~kXcdGrouped;
+  Place pl;
+  pl.p = w % parts;
+  const int u = w / parts;
+  if (base_order == kBlockMajor) {
+    pl.a = u / runs;
+    pl.r = u % runs;
+  } else {
+    pl.a = u % n_arrays;
+    pl.r = u / n_arrays;
+    if (base_order == kDiagonal)
+      pl.r = static_cast<int>((static_cast<int64_t>(pl.r) + pl.a) % runs);
+  }
+  return pl;
+}
+
+// Move chunk p of list entry `entry` of array a: from pool tile src_id (or the
+// staging image of the entry) to pool tile dst_id (or the staging image).
+// Ids outside their pool move nothing, so a bad id never addresses memory
+// outside the pool.
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+__device__ __forceinline__ void move_entry(const PoolView& src, const PoolView& dst,
+                                           const char* src_stage, char* dst_stage,
+                                           int32_t src_id, int32_t dst_id, int64_t entry,
+                                           int a, int p, int32_t tile_vecs, int32_t parts,
+                                           int32_t n_arrays) {
+  const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
+  const int chunk_vecs = tile_vecs / parts;
+  const int64_t chunk_offset = static_cast<int64_t>(p) * chunk_vecs * sizeof(V);
+  const char* s;
+  char* d;
+  if constexpr (SRC_POOL) {
+    if (src_id < 0 || src_id >= src.num_blocks) return;
+    s = array_base(src, a) + src_id * tile_bytes;
+  } else {
+    s = src_stage + (entry * n_arrays + a) * tile_bytes;
+  }
+  if constexpr (DST_POOL) {
+    if (dst_id < 0 || dst_id >= dst.num_blocks) return;
+    d = array_base(dst, a) + dst_id * tile_bytes;
+  } else {
+    d = dst_stage + (entry * n_arrays + a) * tile_bytes;
+  }
+  move_tile<V, U, NT>(as_global<V>(s + chunk_offset), as_global<V>(d + chunk_offset),
+                      chunk_vecs);
+}
+
+// Ids in device memory. A one-block workgroup reads its id pair with uniform
+// (scalar) loads: staging it in LDS would add a store, a barrier and a load
+// before the first data access of a workgroup that lives for a single chunk.
+// A run of several blocks stages its slice of the src -> dst id map in LDS.
 template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
 __global__ void __launch_bounds__(kThreads)
 kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
@@ -218,82 +277,46 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
         int32_t n_arrays, int32_t run, int32_t runs, int32_t parts, int32_t order) {
   __shared__ int32_t s_src[kMaxRun];
   __shared__ int32_t s_dst[kMaxRun];
-  const int w = (order & kXcdGrouped) ? xcd_grouped(blockIdx.x, gridDim.x) : blockIdx.x;
-  const int base_order = order & ~kXcdGrouped;
-  const int p = w % parts;
-  const int u = w / parts;
-  int a, r;
-  if (base_order == kBlockMajor) {
-    a = u / runs;
-    r = u % runs;
-  } else {
-    a = u % n_arrays;
-    r = u / n_arrays;
-    if (base_order == kDiagonal) r = static_cast<int>((static_cast<int64_t>(r) + a) % runs);
-  }
-  const int first = r * run;
-  const int count = min(run, n_blocks - first);
-  const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
-  const int chunk_vecs = tile_vecs / parts;
-  const int64_t chunk_offset = static_cast<int64_t>(p) * chunk_vecs * sizeof(V);
-  const char* src_arr = nullptr;
-  char* dst_arr = nullptr;
-  if constexpr (SRC_POOL) src_arr = array_base(src, a);
-  if constexpr (DST_POOL) dst_arr = array_base(dst, a);
-
+  const Place pl = place_of(n_arrays, runs, parts, order);
+  const int first = pl.r * run;
   if (run == 1) {
-    // One block: its id pair is read with uniform (scalar) loads. Staging it
-    // in LDS would add a store, a barrier and a load before the first data
-    // access of a workgroup that lives for a single chunk.
-    const char* s;
-    char* d;
-    if constexpr (SRC_POOL) {
-      const int32_t id = src_ids[first];
-      if (id < 0 || id >= src.num_blocks) return;  // never address outside the pool
-      s = src_arr + id * tile_bytes;
-    } else {
-      s = src_stage + (static_cast<int64_t>(first) * n_arrays + a) * tile_bytes;
-    }
-    if constexpr (DST_POOL) {
-      const int32_t id = dst_ids[first];
-      if (id < 0 || id >= dst.num_blocks) return;
-      d = dst_arr + id * tile_bytes;
-    } else {
-      d = dst_stage + (static_cast<int64_t>(first) * n_arrays + a) * tile_bytes;
-    }
-    move_tile<V, U, NT>(as_global<V>(s + chunk_offset), as_global<V>(d + chunk_offset),
-                        chunk_vecs);
+    move_entry<V, U, NT, SRC_POOL, DST_POOL>(
+        src, dst, src_stage, dst_stage, SRC_POOL ? src_ids[first] : 0,
+        DST_POOL ? dst_ids[first] : 0, first, pl.a, pl.p, tile_vecs, parts, n_arrays);
     return;
   }
-
-  // A run of several blocks stages its slice of the src -> dst id map in LDS.
+  const int count = min(run, n_blocks - first);
   const int t = threadIdx.x;
   if (t < count) {
     if constexpr (SRC_POOL) s_src[t] = src_ids[first + t];
     if constexpr (DST_POOL) s_dst[t] = dst_ids[first + t];
   }
   __syncthreads();
+  for (int j = 0; j < count; ++j)
+    move_entry<V, U, NT, SRC_POOL, DST_POOL>(
+        src, dst, src_stage, dst_stage, SRC_POOL ? s_src[j] : 0, DST_POOL ? s_dst[j] : 0,
+        first + j, pl.a, pl.p, tile_vecs, parts, n_arrays);
+}
 
-  for (int j = 0; j < count; ++j) {
-    const char* s;
-    char* d;
-    if constexpr (SRC_POOL) {
-      const int32_t id = s_src[j];
-      if (id < 0 || id >= src.num_blocks) continue;  // never address outside the pool
-      s = src_arr + id * tile_bytes;
-    } else {
-      s = src_stage + (static_cast<int64_t>(first + j) * n_arrays + a) * tile_bytes;
-    }
-    if constexpr (DST_POOL) {
-      const int32_t id = s_dst[j];
-      if (id < 0 || id >= dst.num_blocks) continue;
-      d = dst_arr + id * tile_bytes;
-    } else {
-      d = dst_stage + (static_cast<int64_t>(first + j) * n_arrays + a) * tile_bytes;
-    }
-    move_tile<V, U, NT>(as_global<V>(s + chunk_offset), as_global<V>(d + chunk_offset),
-                        chunk_vecs);
-  }
+// Ids carried in the launch's own kernel arguments: source ids at ids[i],
+// destination ids at ids[dst_off + i], for list entries id_base + i. One block
+// per workgroup; each workgroup reads its id pair with scalar loads from the
+// kernel-argument segment, so no id buffer or upload is needed.
+struct InlineIds {
+  int32_t v[2 * IEKV_INLINE_IDS];
+};
+
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+__global__ void __launch_bounds__(kThreads)
+kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
+               char* __restrict__ dst_stage, InlineIds ids, int32_t id_base, int32_t dst_off,
+               int32_t tile_vecs, int32_t n_arrays, int32_t runs, int32_t parts,
+               int32_t order) {
+  const Place pl = place_of(n_arrays, runs, parts, order);
+  const int i = id_base + pl.r;
+  move_entry<V, U, NT, SRC_POOL, DST_POOL>(
+      src, dst, src_stage, dst_stage, SRC_POOL ? ids.v[i] : 0, DST_POOL ? ids.v[dst_off + i] : 0,
+      i, pl.a, pl.p, tile_vecs, parts, n_arrays);
 }
 
 // Row kernels on either side of the handoff. A pool row is one token's
@@ -365,34 +388,45 @@ thread_local Profiler g_profiler;
 using MoveKernel = void (*)(PoolView, PoolView, const char*, char*, const int32_t*,
                             const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
                             int32_t, int32_t);
+using InlineKernel = void (*)(PoolView, PoolView, const char*, char*, InlineIds, int32_t,
+                              int32_t, int32_t, int32_t, int32_t, int32_t, int32_t);
 
 // Kernel for vectors of the widest width the alignment allows, keeping up to
 // `unroll` of them in flight per lane; `lane_vecs` (vectors per lane per
 // chunk) caps the unroll so small chunks do not carry dead predicated slots.
+#define IEKV_PICK(KERNEL)                                                       \
+  if (align >= 16) {                                                            \
+    *vec_bytes = 16;                                                            \
+    const int u = std::min(unroll, lane_vecs);                                  \
+    if (nt) {                                                                   \
+      if (u >= 16) return KERNEL<u32x4, 16, true, SP, DP>;                      \
+      if (u >= 8) return KERNEL<u32x4, 8, true, SP, DP>;                        \
+      if (u >= 4) return KERNEL<u32x4, 4, true, SP, DP>;                        \
+      if (u >= 2) return KERNEL<u32x4, 2, true, SP, DP>;                        \
+      return KERNEL<u32x4, 1, true, SP, DP>;                                    \
+    }                                                                           \
+    if (u >= 16) return KERNEL<u32x4, 16, false, SP, DP>;                       \
+    if (u >= 8) return KERNEL<u32x4, 8, false, SP, DP>;                         \
+    if (u >= 4) return KERNEL<u32x4, 4, false, SP, DP>;                         \
+    if (u >= 2) return KERNEL<u32x4, 2, false, SP, DP>;                         \
+    return KERNEL<u32x4, 1, false, SP, DP>;                                     \
+  }                                                                             \
+  if (align >= 8) { *vec_bytes = 8; return KERNEL<u32x2, 4, false, SP, DP>; }   \
+  if (align >= 4) { *vec_bytes = 4; return KERNEL<uint32_t, 4, false, SP, DP>; } \
+  if (align >= 2) { *vec_bytes = 2; return KERNEL<uint16_t, 4, false, SP, DP>; } \
+  *vec_bytes = 1;                                                               \
+  return KERNEL<uint8_t, 4, false, SP, DP>;
+
 template <bool SP, bool DP>
 MoveKernel pick_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
-  if (align >= 16) {
-    *vec_bytes = 16;
-    const int u = std::min(unroll, lane_vecs);
-    if (nt) {
-      if (u >= 16) return kv_move<u32x4, 16, true, SP, DP>;
-      if (u >= 8) return kv_move<u32x4, 8, true, SP, DP>;
-      if (u >= 4) return kv_move<u32x4, 4, true, SP, DP>;
-      if (u >= 2) return kv_move<u32x4, 2, true, SP, DP>;
-      return kv_move<u32x4, 1, true, SP, DP>;
-    }
-    if (u >= 16) return kv_move<u32x4, 16, false, SP, DP>;
-    if (u >= 8) return kv_move<u32x4, 8, false, SP, DP>;
-    if (u >= 4) return kv_move<u32x4, 4, false, SP, DP>;
-    if (u >= 2) return kv_move<u32x4, 2, false, SP, DP>;
-    return kv_move<u32x4, 1, false, SP, DP>;
-  }
-  if (align >= 8) { *vec_bytes = 8; return kv_move<u32x2, 4, false, SP, DP>; }
-  if (align >= 4) { *vec_bytes = 4; return kv_move<uint32_t, 4, false, SP, DP>; }
-  if (align >= 2) { *vec_bytes = 2; return kv_move<uint16_t, 4, false, SP, DP>; }
-  *vec_bytes = 1;
-  return kv_move<uint8_t, 4, false, SP, DP>;
+  IEKV_PICK(kv_move)
 }
+
+template <bool SP, bool DP>
+InlineKernel pick_inline_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
+  IEKV_PICK(kv_move_inline)
+}
+#undef IEKV_PICK
 
 int align_of_ptr(uint64_t p) {
   int a = 16;
@@ -442,58 +476,110 @@ int chunk_parts(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes) {
 // this many workgroups; larger moves are split over several launches.
 constexpr int64_t kMaxGrid = static_cast<int64_t>(UINT32_MAX) / kThreads;
 
+// Launch shape of one move: blocks per run, chunks per tile, vector width,
+// vectors per lane per chunk, workgroup order, and how many runs one launch takes.
+struct MovePlan {
+  int run = 1;
+  int parts = 1;
+  int vec = 16;
+  int lane_vecs = 1;
+  int32_t tile_vecs = 0;
+  int32_t order = 0;
+  int64_t total_runs = 0;
+  int64_t runs_per_launch = 0;
+};
+
+int plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
+              bool pool_writing, bool single_blocks, MovePlan* pl) {
+  const int run_setting = g_run.load();
+  pl->run = single_blocks ? 1 : (run_setting > 0 ? run_setting : auto_run(tile_bytes));
+  pl->vec = 16;
+  for (int a = 16; a > align; a >>= 1) pl->vec = a >> 1;
+  const int64_t tile_vecs = tile_bytes / pl->vec;
+  if (tile_vecs > INT32_MAX)
+    return set_error(IEKV_ERR_INVALID, "tile of %lld bytes is too large",
+                     static_cast<long long>(tile_bytes));
+  // Runs of several tiles keep whole tiles per workgroup; single-tile
+  // workgroups split each tile into chunks, halving the split while a launch
+  // would not fit the dispatch limit.
+  pl->parts = pl->run == 1 ? chunk_parts(tile_vecs, pl->vec, g_chunk.load()) : 1;
+  while (pl->parts > 1 && static_cast<int64_t>(n_arrays) * pl->parts > kMaxGrid) pl->parts /= 2;
+  if (static_cast<int64_t>(n_arrays) * pl->parts > kMaxGrid)
+    return set_error(IEKV_ERR_INVALID, "%d arrays exceed the grid limit", n_arrays);
+  pl->total_runs = (static_cast<int64_t>(n_blocks) + pl->run - 1) / pl->run;
+  while (pl->parts > 1 && pl->total_runs * n_arrays * pl->parts > kMaxGrid) pl->parts /= 2;
+  pl->lane_vecs = static_cast<int>(
+      std::min<int64_t>((tile_vecs / pl->parts + kThreads - 1) / kThreads, 16));
+  pl->tile_vecs = static_cast<int32_t>(tile_vecs);
+  pl->order = pool_writing ? g_order.load() : g_pack_order.load();
+  pl->runs_per_launch =
+      std::min<int64_t>(pl->total_runs, kMaxGrid / (int64_t(n_arrays) * pl->parts));
+  return IEKV_OK;
+}
+
+// One dispatch; while a timing session is open it carries a start/stop event
+// pair in its own packet.
+template <typename Kernel, typename... Args>
+int dispatch(Kernel kernel, uint32_t grid, hipStream_t stream, Args... args) {
+  Profiler& prof = g_profiler;
+  if (prof.on && prof.used < prof.events.size()) {
+    auto& ev = prof.events[prof.used++];
+    hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, ev.first, ev.second,
+                          0, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, args...);
+  }
+  IEKV_HIP(hipGetLastError());
+  return IEKV_OK;
+}
+
 template <bool SP, bool DP>
 int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage, char* dst_stage,
                 const int32_t* src_ids, const int32_t* dst_ids, int32_t n_blocks,
                 int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream) {
   if (n_blocks == 0) return IEKV_OK;
-  const int run_setting = g_run.load();
-  const int run = run_setting > 0 ? run_setting : auto_run(tile_bytes);
-  int vec = 16;
-  for (int a = 16; a > align; a >>= 1) vec = a >> 1;
-  const int64_t tile_vecs64 = tile_bytes / vec;
-  if (tile_vecs64 > INT32_MAX)
-    return set_error(IEKV_ERR_INVALID, "tile of %lld bytes is too large",
-                     static_cast<long long>(tile_bytes));
-  // Runs of several tiles keep whole tiles per workgroup; single-tile
-  // workgroups split each tile into chunks, halving the split while a launch
-  // of one run per array would not fit the grid.
-  int parts = run == 1 ? chunk_parts(tile_vecs64, vec, g_chunk.load()) : 1;
-  while (parts > 1 && static_cast<int64_t>(n_arrays) * parts > kMaxGrid) parts /= 2;
-  if (static_cast<int64_t>(n_arrays) * parts > kMaxGrid)
-    return set_error(IEKV_ERR_INVALID, "%d arrays exceed the grid limit", n_arrays);
-  const int64_t total_runs = (static_cast<int64_t>(n_blocks) + run - 1) / run;
-  while (parts > 1 && total_runs * n_arrays * parts > kMaxGrid) parts /= 2;
-  const int64_t lane_vecs = (tile_vecs64 / parts + kThreads - 1) / kThreads;
-  MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), static_cast<int>(
-                                         std::min<int64_t>(lane_vecs, 16)),
-                                     g_nontemporal.load() != 0, &vec);
-  const int32_t tile_vecs = static_cast<int32_t>(tile_vecs64);
-  const int32_t order = DP ? g_order.load() : g_pack_order.load();
-  const int64_t runs_per_launch = std::min<int64_t>(total_runs, kMaxGrid / (int64_t(n_arrays) * parts));
+  MovePlan pl;
+  int rc;
+  if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, DP, false, &pl))) return rc;
+  MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
+                                     g_nontemporal.load() != 0, &pl.vec);
   const int64_t block_image = tile_bytes * n_arrays;
-  Profiler& prof = g_profiler;
-  for (int64_t r0 = 0; r0 < total_runs; r0 += runs_per_launch) {
-    const int64_t first = r0 * run;
-    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(runs_per_launch * run,
-                                                               n_blocks - first));
-    const int32_t runs = static_cast<int32_t>((cnt + run - 1) / run);
-    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * n_arrays * parts);
-    const int32_t* s_ids = SP ? src_ids + first : nullptr;
-    const int32_t* d_ids = DP ? dst_ids + first : nullptr;
-    const char* s_stage = SP ? nullptr : src_stage + first * block_image;
-    char* d_stage = DP ? nullptr : dst_stage + first * block_image;
-    if (prof.on && prof.used < prof.events.size()) {
-      auto& ev = prof.events[prof.used++];
-      hipExtLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, stream, ev.first, ev.second, 0,
-                            view_of(sp), view_of(dp), s_stage, d_stage, s_ids, d_ids, tile_vecs,
-                            cnt, n_arrays, run, runs, parts, order);
-    } else {
-      hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, stream, view_of(sp), view_of(dp),
-                         s_stage, d_stage, s_ids, d_ids, tile_vecs, cnt, n_arrays, run, runs,
-                         parts, order);
-    }
-    IEKV_HIP(hipGetLastError());
+  for (int64_t r0 = 0; r0 < pl.total_runs; r0 += pl.runs_per_launch) {
+    const int64_t first = r0 * pl.run;
+    const int32_t cnt = static_cast<int32_t>(
+        std::min<int64_t>(pl.runs_per_launch * pl.run, n_blocks - first));
+    const int32_t runs = static_cast<int32_t>((cnt + pl.run - 1) / pl.run);
+    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * n_arrays * pl.parts);
+    if ((rc = dispatch(k, grid, stream, view_of(sp), view_of(dp),
+                       SP ? nullptr : src_stage + first * block_image,
+                       DP ? nullptr : dst_stage + first * block_image,
+                       SP ? src_ids + first : nullptr, DP ? dst_ids + first : nullptr,
+                       pl.tile_vecs, cnt, n_arrays, pl.run, runs, pl.parts, pl.order)))
+      return rc;
+  }
+  return IEKV_OK;
+}
+
+// The same move with its ids in the kernel arguments (n_blocks <=
+// IEKV_INLINE_IDS): src ids at ids.v[i], dst ids at ids.v[dst_off + i].
+template <bool SP, bool DP>
+int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
+                       char* dst_stage, const InlineIds& ids, int32_t dst_off, int32_t n_blocks,
+                       int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream) {
+  if (n_blocks == 0) return IEKV_OK;
+  MovePlan pl;
+  int rc;
+  if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, DP, true, &pl))) return rc;
+  InlineKernel k = pick_inline_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
+                                              g_nontemporal.load() != 0, &pl.vec);
+  for (int64_t r0 = 0; r0 < pl.total_runs; r0 += pl.runs_per_launch) {
+    const int32_t runs = static_cast<int32_t>(std::min<int64_t>(pl.runs_per_launch,
+                                                                pl.total_runs - r0));
+    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * n_arrays * pl.parts);
+    if ((rc = dispatch(k, grid, stream, view_of(sp), view_of(dp), src_stage, dst_stage, ids,
+                       static_cast<int32_t>(r0), dst_off, pl.tile_vecs, n_arrays, runs, pl.parts,
+                       pl.order)))
+      return rc;
   }
   return IEKV_OK;
 }
@@ -612,6 +698,27 @@ int restore_pipeline(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blo
   }
   // Later copy-stream work that writes staging is ordered after the last unpack.
   IEKV_HIP(hipStreamWaitEvent(copy, unpacked[last], 0));
+  return IEKV_OK;
+}
+
+// Copy n host ids into ids->v[off..off+n), checking each against the pool.
+int fill_inline(const int32_t* host_ids, int32_t n, int64_t num_blocks, const char* what,
+                InlineIds* ids, int32_t off) {
+  for (int32_t i = 0; i < n; ++i) {
+    const int32_t id = host_ids[i];
+    if (id < 0 || id >= num_blocks)
+      return set_error(IEKV_ERR_INVALID, "%s block id %d (entry %d) is outside the pool of "
+                       "%lld blocks", what, id, i, static_cast<long long>(num_blocks));
+    ids->v[off + i] = id;
+  }
+  return IEKV_OK;
+}
+
+int check_inline_count(int32_t n_blocks, const int32_t* a, const int32_t* b) {
+  if (n_blocks < 0 || n_blocks > IEKV_INLINE_IDS)
+    return set_error(IEKV_ERR_INVALID, "n_blocks %d is outside 0..%d for host ids", n_blocks,
+                     IEKV_INLINE_IDS);
+  if (n_blocks > 0 && (!a || !b)) return set_error(IEKV_ERR_INVALID, "host ids are null");
   return IEKV_OK;
 }
 
@@ -766,6 +873,65 @@ int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   return launch_move<false, true>(nullptr, dst, static_cast<const char*>(staging), nullptr,
                                   nullptr, dst_ids, n_blocks, dst->tile_bytes, dst->n_arrays,
                                   align, stream);
+}
+
+int iekv_copy_direct_ids(const iekv_pool* src, const iekv_pool* dst, const int32_t* src_ids,
+                         const int32_t* dst_ids, int32_t n_blocks, hipStream_t stream) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_pool(dst, "destination")) ||
+      (rc = check_inline_count(n_blocks, src_ids, dst_ids)))
+    return rc;
+  if (src->n_arrays != dst->n_arrays || src->tile_bytes != dst->tile_bytes)
+    return set_error(IEKV_ERR_INVALID, "pools differ in shape");
+  if (src->device != dst->device)
+    return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
+                     dst->device);
+  InlineIds ids{};
+  if ((rc = fill_inline(src_ids, n_blocks, src->num_blocks, "source", &ids, 0)) ||
+      (rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, n_blocks)))
+    return rc;
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  return launch_move_inline<true, true>(src, dst, nullptr, nullptr, ids, n_blocks, n_blocks,
+                                        src->tile_bytes, src->n_arrays,
+                                        std::min(src->align, dst->align), stream);
+}
+
+int iekv_pack_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, void* staging,
+                  int64_t staging_bytes, hipStream_t stream) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_inline_count(n_blocks, src_ids, src_ids)))
+    return rc;
+  const int64_t need = image_bytes(src, n_blocks);
+  if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
+  if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
+  InlineIds ids{};
+  if ((rc = fill_inline(src_ids, n_blocks, src->num_blocks, "source", &ids, 0))) return rc;
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  const int align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  return launch_move_inline<true, false>(src, nullptr, nullptr, static_cast<char*>(staging), ids,
+                                         0, n_blocks, src->tile_bytes, src->n_arrays, align,
+                                         stream);
+}
+
+int iekv_unpack_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                    const void* staging, int64_t staging_bytes, hipStream_t stream) {
+  int rc;
+  if ((rc = check_pool(dst, "destination")) ||
+      (rc = check_inline_count(n_blocks, dst_ids, dst_ids)))
+    return rc;
+  const int64_t need = image_bytes(dst, n_blocks);
+  if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
+  if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
+  InlineIds ids{};
+  if ((rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, 0))) return rc;
+  DeviceGuard guard(dst->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+  const int align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  return launch_move_inline<false, true>(nullptr, dst, static_cast<const char*>(staging), nullptr,
+                                         ids, 0, n_blocks, dst->tile_bytes, dst->n_arrays, align,
+                                         stream);
 }
 
 int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, const void* k,

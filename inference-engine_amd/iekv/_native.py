@@ -12,7 +12,9 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
+
+INLINE_IDS = 256   # IEKV_INLINE_IDS: most ids a host-id call takes
 
 IEKV_OK = 0
 IEKV_ERR_INVALID = -1
@@ -29,6 +31,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "iekv_copy_direct": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
     "iekv_pack": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
     "iekv_unpack": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
+    "iekv_copy_direct_ids": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
+    "iekv_pack_ids": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
+    "iekv_unpack_ids": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
     "iekv_write_slots": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
                                  c_int32, c_void_p]),
     "iekv_gather_rows": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p,

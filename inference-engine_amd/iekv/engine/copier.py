@@ -216,6 +216,43 @@ def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
     return base[start:start + len(payloads)]
 
 
+class _BlockIds:
+    """The block ids of one call: range-checked host int32 ids, or a device tensor.
+
+    Host ids of at most ``INLINE_IDS`` blocks go to the library's host-id entry
+    points (the ids ride in the launch's kernel arguments); otherwise they are
+    uploaded once, when a call first needs them on the device.
+    """
+
+    __slots__ = ("_device", "host", "_on_device")
+
+    def __init__(self, device: torch.device, host: np.ndarray | None = None,
+                 device_ids: torch.Tensor | None = None) -> None:
+        self._device = device
+        self.host = None if host is None else np.ascontiguousarray(host, dtype=np.int32)
+        self._on_device = device_ids
+
+    def __len__(self) -> int:
+        return int(self.host.size) if self.host is not None else self._on_device.numel()
+
+    def __getitem__(self, index: slice) -> "_BlockIds":
+        if self.host is not None:
+            return _BlockIds(self._device, host=self.host[index])
+        return _BlockIds(self._device, device_ids=self._on_device[index])
+
+    @property
+    def inline(self) -> bool:
+        return self.host is not None and self.host.size <= _native.INLINE_IDS
+
+    def host_pointer(self) -> int:
+        return self.host.ctypes.data
+
+    def on_device(self) -> torch.Tensor:
+        if self._on_device is None:
+            self._on_device = stage_ids(self._device, self.host)[0]
+        return self._on_device
+
+
 class HipSlotCopier:
     """SlotCopier over per-layer GPU caches, backed by the HIP handoff kernels.
 
@@ -354,30 +391,38 @@ class HipSlotCopier:
         self.blocks_read += len(out)
         return out
 
+    def _ids(self, block_ids, *, unique: bool = False, what: str) -> "_BlockIds":
+        if isinstance(block_ids, torch.Tensor) and block_ids.device.type == "cuda":
+            return _BlockIds(self.device, device_ids=self.pool.block_ids(block_ids, what=what))
+        return _BlockIds(self.device, host=self.pool.host_ids(block_ids, unique=unique, what=what))
+
     def _gather(self, block_ids, location: str) -> PackedBlocks:
-        ids = self.pool.block_ids(block_ids, what="source block")
-        n = ids.numel()
+        ids = self._ids(block_ids, what="source block")
+        n = len(ids)
         out = self._empty_packed(n, on_host=(location == "host"))
         stream = torch.cuda.current_stream(self.device)
         if out.on_host:
             staging = self._host_staging(n)
             copy = self.copy_stream()
-            _native.call("iekv_offload", self.pool.native.handle, ids.data_ptr(), n,
+            _native.call("iekv_offload", self.pool.native.handle, ids.on_device().data_ptr(), n,
                          out.data.data_ptr(), out.nbytes, staging.data_ptr(), staging.numel(),
                          stream.cuda_stream, copy.cuda_stream)
             out.mark(stream)
             self.offload_launches += 1
             self.blocks_offloaded += n
+        elif ids.inline:
+            _native.call("iekv_pack_ids", self.pool.native.handle, ids.host_pointer(), n,
+                         out.data.data_ptr(), out.nbytes, stream.cuda_stream)
         else:
-            _native.call("iekv_pack", self.pool.native.handle, ids.data_ptr(), n,
+            _native.call("iekv_pack", self.pool.native.handle, ids.on_device().data_ptr(), n,
                          out.data.data_ptr(), out.nbytes, stream.cuda_stream)
         return out
 
     def write_blocks(self, block_ids, payloads) -> None:
         """Scatter ``payloads[i]`` into ``block_ids[i]`` for every i (one launch when possible)."""
         self.flush()   # queued reads see the blocks before this write
-        ids = self.pool.block_ids(block_ids, unique=True, what="destination block")
-        n = ids.numel()
+        ids = self._ids(block_ids, unique=True, what="destination block")
+        n = len(ids)
         if len(payloads) != n:
             raise ValueError(f"{n} destination blocks for {len(payloads)} payloads")
         packed = _consecutive_views(payloads)
@@ -392,32 +437,35 @@ class HipSlotCopier:
                 self._write_packed(ids[i:i + 1], one)
         self.blocks_written += n
 
-    def _write_packed(self, ids: torch.Tensor, packed: PackedBlocks) -> None:
+    def _write_packed(self, ids: "_BlockIds", packed: PackedBlocks) -> None:
         self._check_packed(packed)
-        n = ids.numel()
+        n = len(ids)
         stream = torch.cuda.current_stream(self.device)
         if packed.on_host:
             staging = self._host_staging(n)
             copy = self.copy_stream()
-            _native.call("iekv_restore", self.pool.native.handle, ids.data_ptr(), n,
+            _native.call("iekv_restore", self.pool.native.handle, ids.on_device().data_ptr(), n,
                          packed.data.data_ptr(), packed.nbytes, staging.data_ptr(),
                          staging.numel(), stream.cuda_stream, copy.cuda_stream)
             packed.mark(copy)
             self.restore_launches += 1
+        elif ids.inline:
+            _native.call("iekv_unpack_ids", self.pool.native.handle, ids.host_pointer(), n,
+                         packed.data.data_ptr(), packed.nbytes, stream.cuda_stream)
         else:
-            _native.call("iekv_unpack", self.pool.native.handle, ids.data_ptr(), n,
+            _native.call("iekv_unpack", self.pool.native.handle, ids.on_device().data_ptr(), n,
                          packed.data.data_ptr(), packed.nbytes, stream.cuda_stream)
 
-    def _restore_scattered(self, ids: torch.Tensor, payloads: Seq[BlockPayload]) -> None:
+    def _restore_scattered(self, ids: "_BlockIds", payloads: Seq[BlockPayload]) -> None:
         """Host payloads from unrelated buffers (tier entries) -> one iekv_restore_blocks."""
         for p in payloads:
             self._check_packed(p.packed)
-        n = ids.numel()
+        n = len(ids)
         addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in payloads])
         stream = torch.cuda.current_stream(self.device)
         staging = self._host_staging(n)
         copy = self.copy_stream()
-        _native.call("iekv_restore_blocks", self.pool.native.handle, ids.data_ptr(), n,
+        _native.call("iekv_restore_blocks", self.pool.native.handle, ids.on_device().data_ptr(), n,
                      addresses, staging.data_ptr(), staging.numel(), stream.cuda_stream,
                      copy.cuda_stream)
         for root in {id(p.packed._root): p.packed._root for p in payloads}.values():
@@ -433,14 +481,19 @@ class HipSlotCopier:
             raise ValueError(f"pools on {source.device} and {self.device}")
         on_device = (isinstance(src_ids, torch.Tensor) and src_ids.device.type == "cuda") or \
             (isinstance(dst_ids, torch.Tensor) and dst_ids.device.type == "cuda")
+        stream = torch.cuda.current_stream(self.device)
         if on_device:
             src = source.pool.block_ids(src_ids, what="source block")
             dst = self.pool.block_ids(dst_ids, unique=True, what="destination block")
             if src.numel() != dst.numel():
                 raise ValueError(f"{src.numel()} source blocks for {dst.numel()} destinations")
+            n = dst.numel()
+            _native.call("iekv_copy_direct", source.pool.native.handle, self.pool.native.handle,
+                         src.data_ptr(), dst.data_ptr(), n, stream.cuda_stream)
         else:
-            # Host ids: checked on the host, issued by destination id, and both
-            # lists uploaded with one copy.
+            # Host ids: checked on the host and issued by destination id. Up to
+            # INLINE_IDS pairs travel in the launch's kernel arguments; longer
+            # lists are uploaded together with one copy.
             s, d = issue_order(src_ids, dst_ids)
             s = source.pool.host_ids(s, what="source block")
             d = self.pool.host_ids(d, unique=True, what="destination block", ascending=True)
@@ -448,11 +501,18 @@ class HipSlotCopier:
                     bool(np.isin(s, d, assume_unique=False).any()):
                 raise ValueError("a direct copy within one pool needs disjoint source "
                                  "and destination blocks")
-            src, dst = stage_ids(self.device, s, d)
-        n = dst.numel()
-        stream = torch.cuda.current_stream(self.device)
-        _native.call("iekv_copy_direct", source.pool.native.handle, self.pool.native.handle,
-                     src.data_ptr(), dst.data_ptr(), n, stream.cuda_stream)
+            n = int(d.size)
+            if n <= _native.INLINE_IDS:
+                s32 = np.ascontiguousarray(s, dtype=np.int32)
+                d32 = np.ascontiguousarray(d, dtype=np.int32)
+                _native.call("iekv_copy_direct_ids", source.pool.native.handle,
+                             self.pool.native.handle, s32.ctypes.data, d32.ctypes.data, n,
+                             stream.cuda_stream)
+            else:
+                src, dst = stage_ids(self.device, s, d)
+                _native.call("iekv_copy_direct", source.pool.native.handle,
+                             self.pool.native.handle, src.data_ptr(), dst.data_ptr(), n,
+                             stream.cuda_stream)
         source.blocks_read += n
         self.blocks_written += n
 

@@ -162,13 +162,15 @@ def test_random_tiles_and_launch_shapes_match_the_oracle(gpu, case):
     src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
     src_ids, dst_ids = random_tables(rng, n_src, n_dst, count)
     src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    # odd cases hand the ids over as device tensors, even cases as host lists
+    ids_of = (lambda ids: torch.tensor(ids, dtype=torch.int32, device=gpu)) if case % 2 else list
     before = _native.get_launch()
     try:
         _native.set_launch(*shape)
         half = count // 2
-        packed = src.read_blocks(src_ids[:half])
-        dst.write_blocks(dst_ids[:half], packed)
-        dst.copy_blocks(src, src_ids[half:], dst_ids[half:])
+        packed = src.read_blocks(ids_of(src_ids[:half]))
+        dst.write_blocks(ids_of(dst_ids[:half]), packed)
+        dst.copy_blocks(src, ids_of(src_ids[half:]), ids_of(dst_ids[half:]))
         torch.cuda.synchronize()
     finally:
         _native.set_launch(**before)
@@ -206,22 +208,52 @@ def test_every_launch_shape_is_bit_exact(gpu):
         shapes += [(0, unroll, 1, order, chunk) for unroll in (1, 2, 8) for order in (0, 5)
                    for chunk in (64, 512, 1024, 16384, 32768, 1 << 20)]
         rows = np.concatenate([np.arange(b * bs, (b + 1) * bs) for b in dst_ids])
+        dev = lambda ids: torch.tensor(ids, dtype=torch.int32, device=gpu)  # noqa: E731
         for shape in shapes:
             run, unroll, nt, order, chunk = shape
             _native.set_launch(run, unroll, nt, order, order, chunk)
-            packed = src.read_blocks(src_ids)
-            assert np.array_equal(packed.data.cpu().numpy(), want), shape
-            for t in dk + dv:
-                t.zero_()
-            half = len(src_ids) // 2
-            dst.write_blocks(dst_ids[:half], packed[:half])
-            dst.copy_blocks(src, src_ids[half:], dst_ids[half:])
-            torch.cuda.synchronize()
-            got = host_bytes(dk) + host_bytes(dv)
-            for g, w in zip(got, list(dst_o.k_caches) + list(dst_o.v_caches)):
-                assert np.array_equal(g[rows], w[rows]), shape
+            # device ids take the kernel that honours run_blocks (LDS-staged runs);
+            # host lists take the kernel with the ids in its arguments
+            for ids_of in (dev, list):
+                packed = src.read_blocks(ids_of(src_ids))
+                assert np.array_equal(packed.data.cpu().numpy(), want), (shape, ids_of)
+                for t in dk + dv:
+                    t.zero_()
+                half = len(src_ids) // 2
+                dst.write_blocks(ids_of(dst_ids[:half]), packed[:half])
+                dst.copy_blocks(src, ids_of(src_ids[half:]), ids_of(dst_ids[half:]))
+                torch.cuda.synchronize()
+                got = host_bytes(dk) + host_bytes(dv)
+                for g, w in zip(got, list(dst_o.k_caches) + list(dst_o.v_caches)):
+                    assert np.array_equal(g[rows], w[rows]), (shape, ids_of)
     finally:
         _native.set_launch(**before)
+
+
+@pytest.mark.parametrize("count", [1, 255, 256, 257, 600])
+def test_host_ids_in_the_kernel_arguments_and_beyond(gpu, count):
+    """Host id lists of up to 256 blocks ride in the launch's kernel arguments
+    (iekv_*_ids); longer ones are uploaded. Both give the oracle's bytes."""
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 4, 2, 2, 32
+    sk, sv = allocate(700, bs, layers, heads, dim, torch.bfloat16, gpu, seed=41)
+    dk, dv = allocate(650, bs, layers, heads, dim, torch.bfloat16, gpu, seed=42)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    rng = np.random.default_rng(43)
+    src_ids, dst_ids = random_tables(rng, 700, 650, count)
+    half = count // 2
+    packed = src.read_blocks(src_ids[:half])
+    dst.write_blocks(dst_ids[:half], packed)
+    dst.copy_blocks(src, src_ids[half:], dst_ids[half:])
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    assert_pool_equals(dk, dv, dst_o)
+    assert len(packed) == half
+    if half:
+        assert np.array_equal(packed.data.cpu().numpy(),
+                              packed_image(pack(oracle_of(sk, sv, bs), src_ids[:half])))
 
 
 def test_a_split_that_would_overflow_the_dispatch_is_halved(gpu):

@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 6
+    assert lib.iekv_abi_version() == 7
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -75,6 +75,30 @@ def test_calls_reject_null_pools_and_negative_counts(lib):
     assert lib.iekv_restore_blocks(None, None, 1, None, None, 0, None, None) == \
         _native.IEKV_ERR_INVALID
     assert "null" in lib.iekv_last_error().decode()
+
+
+def test_host_id_calls_check_count_and_range_before_any_launch(lib):
+    """The *_ids entry points take at most IEKV_INLINE_IDS host ids and check each
+    against its pool; a slab pool registers without touching the GPU."""
+    from iekv import _native
+
+    pool = _native.Pool([1 << 20, (1 << 20) + 64 * 16], tile_bytes=64, num_blocks=16, device=0)
+    n = _native.INLINE_IDS + 1
+    ids = (ctypes.c_int32 * n)(*range(n))
+    assert lib.iekv_copy_direct_ids(pool.handle, pool.handle, ids, ids, n, None) == \
+        _native.IEKV_ERR_INVALID
+    assert "outside 0..256" in lib.iekv_last_error().decode()
+    assert lib.iekv_pack_ids(pool.handle, None, 3, None, 0, None) == _native.IEKV_ERR_INVALID
+    assert "null" in lib.iekv_last_error().decode()
+    bad = (ctypes.c_int32 * 3)(0, 16, 2)
+    staging = ctypes.create_string_buffer(3 * 2 * 64)
+    rc = lib.iekv_unpack_ids(pool.handle, bad, 3, staging, len(staging), None)
+    assert rc == _native.IEKV_ERR_INVALID
+    assert "destination block id 16 (entry 1)" in lib.iekv_last_error().decode()
+    rc = lib.iekv_copy_direct_ids(pool.handle, pool.handle, bad, ids, 3, None)
+    assert rc == _native.IEKV_ERR_INVALID
+    assert "source block id 16" in lib.iekv_last_error().decode()
+    pool.close()
 
 
 def test_scattered_restore_rejects_missing_host_addresses(lib):
