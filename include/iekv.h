@@ -21,9 +21,11 @@
  *   2L tiles of the i-th listed block, K layers first, then V layers — the
  *   byte image of the reference payload ([K_0..K_{L-1}], [V_0..V_{L-1}])
  *   (copier.py:21-22).
- *   Block ids are int32 in DEVICE memory. Callers validate them against the
- *   pool size before a call; kernels skip a tile whose id is out of range so
- *   a bad id can never address memory outside the pool.
+ *   Block ids are int32 in DEVICE memory, except for the *_ids entry points,
+ *   which take at most IEKV_INLINE_IDS ids in HOST memory and check them
+ *   before launching. Callers validate device ids against the pool size
+ *   before a call; kernels skip a tile whose id is out of range so a bad id
+ *   can never address memory outside the pool.
  *   All copies are raw bytes: fp32/fp16/bf16/fp8/int8 caches move bit-exactly.
  *
  * Errors. Every function returns IEKV_OK (0) or a negative IEKV_ERR_* code,
