@@ -305,3 +305,56 @@ def test_batched_prefix_aware_moves_on_gpu(gpu):
     engine.flush_moves(pending)
     engine.decode_until_done()
     assert seq.token_ids[seq.num_prompt:] == plain[1]
+
+
+def _wire_rank(rank: int, port: int, result_path: str) -> None:
+    """One side of a two-process handoff: rank 0 prefills and sends, rank 1 admits and decodes."""
+    import os
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    sys.path[:0] = [root, os.path.join(root, "inference-engine_amd"), here]
+    import torch.distributed as dist
+
+    from iekv.serve.disaggregated import DecodeWorker, DisaggregatedEngine, PrefillWorker
+    from iekv.serve.wire import recv_transfer, send_transfer
+
+    os.environ["MASTER_ADDR"] = "127.0.0.1"
+    os.environ["MASTER_PORT"] = str(port)
+    dist.init_process_group("gloo", rank=rank, world_size=2)
+    try:
+        device = torch.device("cuda", 0)
+        prompt = G["prompts"][1]
+        if rank == 0:
+            worker = PrefillWorker(model(device, torch.bfloat16), engine_config())
+            transfer = worker.prefill(prompt, 0.0)          # one iekv_pack launch
+            send_transfer(transfer, dst=1, device="cpu")    # gloo carries host tensors
+        else:
+            worker = DecodeWorker(model(device, torch.bfloat16), engine_config())
+            transfer = recv_transfer(src=0, device="cpu")
+            seq = worker.admit(transfer, max_new_tokens=8, temperature=0.0)  # iekv_restore
+            worker.engine.run()
+            got = seq.token_ids[seq.num_prompt:]
+            want = DisaggregatedEngine(model(device, torch.bfloat16), engine_config()).generate(
+                [prompt], max_new_tokens=8, temperature=0.0)[0]
+            with open(result_path, "w") as f:
+                f.write("ok" if got == want and len(got) == 8 else f"{got} != {want}")
+    finally:
+        dist.destroy_process_group()
+
+
+def test_a_transfer_sent_between_processes_decodes_identically(gpu, tmp_path):
+    """The wire format end to end: prefill and pack in one process, send the header and
+    the block-major payload over torch.distributed, restore and decode in another; the
+    tokens equal an in-process handoff's."""
+    import socket
+
+    import torch.multiprocessing as mp
+
+    with socket.socket() as s:
+        s.bind(("127.0.0.1", 0))
+        port = s.getsockname()[1]
+    result = tmp_path / "result.txt"
+    mp.spawn(_wire_rank, args=(port, str(result)), nprocs=2, join=True)
+    assert result.read_text() == "ok"
