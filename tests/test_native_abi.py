@@ -184,3 +184,37 @@ def test_direct_copy_issue_order_keeps_every_pair():
     assert sorted(zip(s.tolist(), d.tolist())) == sorted(zip(src.tolist(), dst.tolist()))
     with pytest.raises(ValueError):
         issue_order([1, 2], [3])
+
+
+def test_the_header_is_plain_c_and_links_from_c(lib, tmp_path):
+    """A C99 program includes include/iekv.h, links libiekv.so with gcc and calls it
+    (no GPU needed): the boundary is usable from any C FFI (cgo, JNI, N-API, ctypes)."""
+    import shutil
+    import subprocess
+
+    from iekv import _native
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc is not installed")
+    source = tmp_path / "abi.c"
+    source.write_text(
+        '#include "iekv.h"\n'
+        "#include <stdio.h>\n"
+        "int main(void) {\n"
+        "  if (iekv_abi_version() != IEKV_ABI_VERSION) return 1;\n"
+        "  if (iekv_copy_direct(0, 0, 0, 0, 1, 0) != IEKV_ERR_INVALID) return 2;\n"
+        "  if (iekv_copy_direct_ids(0, 0, 0, 0, IEKV_INLINE_IDS + 1, 0) != IEKV_ERR_INVALID)"
+        " return 3;\n"
+        '  printf("%d %s\\n", IEKV_ABI_VERSION, iekv_last_error());\n'
+        "  return 0;\n"
+        "}\n")
+    exe = tmp_path / "abi"
+    libdir = _native.library_path().parent
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__",
+                    f"-I{ROOT / 'include'}", "-I/opt/rocm/include", str(source),
+                    f"-L{libdir}", "-liekv", f"-Wl,-rpath,{libdir}", "-o", str(exe)],
+                   check=True, capture_output=True, timeout=120)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, (out.returncode, out.stdout, out.stderr)
+    assert out.stdout.split()[0] == str(lib.iekv_abi_version())
