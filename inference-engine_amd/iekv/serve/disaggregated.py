@@ -33,7 +33,7 @@ Three transfer modes (``mode=``):
 """
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import Any, Callable
 
 import numpy as np
