@@ -539,6 +539,9 @@ def main() -> int:
                          "iekv_set_launch (default: the library's)")
     ap.add_argument("--sweep", action="store_true",
                     help="time the legs under every launch shape instead of the benchmark line")
+    ap.add_argument("--tp", type=int, default=1,
+                    help="measure one rank's share under head-sharded tensor parallelism "
+                         "(H/tp KV heads per tile, same block tables)")
     ap.add_argument("--separate-pools", action="store_true",
                     help="allocate the two pools separately instead of as one reservation "
                          "(prefill pool first)")
@@ -563,7 +566,7 @@ def main() -> int:
     _native.lib()
     if args.launch:
         _native.set_launch(*[int(x) for x in args.launch.split(",")])
-    w = workloads.make(args.config, args.seed, args.slack)
+    w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
     log(f"[bench] {w.name}: {w.num_requests} requests, {w.num_blocks} blocks, "
         f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B")
     legs = Legs(w, device, args.seed, "separate" if args.separate_pools else "paired")
@@ -630,7 +633,7 @@ def main() -> int:
             "layers": w.shape.layers, "kv_heads": w.shape.kv_heads,
             "head_dim": w.shape.head_dim, "block_size": w.shape.block_size,
             "kv_dtype": w.shape.dtype, "requests": w.num_requests, "blocks": w.num_blocks,
-            "payload_bytes": P, "tile_bytes": w.shape.tile_bytes,
+            "payload_bytes": P, "tile_bytes": w.shape.tile_bytes, "tp_share": args.tp,
             "launch": _native.get_launch(),
             "pools": ("two allocations" if args.separate_pools
                       else "one allocation, prefill pool first"),

@@ -197,10 +197,14 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
  *   chunk_bytes with one block per workgroup, each tile is split into a
  *               power-of-two number of chunks of at least this many bytes,
  *               one workgroup per chunk (the chunks of one tile are adjacent
- *               in the order); 0 moves whole tiles; a power of two from 64 to
- *               1 MiB; -1 keeps the current setting. A launch that would
- *               exceed the dispatch limit of 2^32 - 1 work-items halves the
- *               split, then spreads over several launches.
+ *               in the order); a tile smaller than this whose 16-byte (or
+ *               narrower) vectors divide 256 lanes is grouped instead: one
+ *               workgroup moves a block's tiles in chunk_bytes / tile_bytes
+ *               consecutive arrays; 0 moves one whole tile per workgroup; a
+ *               power of two from 64 to 1 MiB; -1 keeps the current setting.
+ *               A launch that would exceed the dispatch limit of 2^32 - 1
+ *               work-items halves the split, then spreads over several
+ *               launches.
  * The defaults (run 0, unroll 8, nontemporal 1, order, pack_order and
  * chunk_bytes) are the library's measured best; iekv_get_launch reports them.
  * No reference counterpart: a tuning knob for the launches the entry points

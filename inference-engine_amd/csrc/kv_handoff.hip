@@ -11,7 +11,9 @@
 // entries, chunk of each tile). With one entry per run (the default) each tile
 // is split into chunks of at least the chunk size (4 KiB: one 16-byte vector
 // per lane), one workgroup per chunk, and the workgroup reads its id pair with
-// scalar loads; a run of several entries stages its ids in LDS. Data moves
+// scalar loads; tiles smaller than the chunk size are grouped instead, one
+// workgroup taking a block's tiles in several consecutive arrays; a run of
+// several entries stages its ids in LDS. Data moves
 // with wavefront-contiguous 16-byte loads and stores (a wave64 covers 1 KiB,
 // a workgroup 4 KiB per access step), keeping up to `U` loads per lane in
 // flight before the matching stores. The data is never interpreted: it moves
@@ -91,8 +93,10 @@ std::atomic<int> g_order{kXcdGrouped | kBlockMajor};
 // diagonal on every 70B-share padding (5.82 against 5.46 TB/s on average) and
 // faster or tied on every 8B padding (5.66 against 5.62).
 std::atomic<int> g_pack_order{0};
-// Bytes each workgroup moves of a tile: a tile larger than this splits into a
-// power-of-two number of chunks of at least this size, one workgroup each.
+// Bytes each workgroup moves: a tile larger than this splits into a
+// power-of-two number of chunks of at least this size, one workgroup each; a
+// smaller one is moved together with the same block's tiles in the next
+// arrays, up to this size per workgroup (tile_group).
 // Measured on MI355X (one box, all five benchmark workloads, 4 KiB against
 // 8 KiB): on 32 KiB tiles 4 KiB gains 2-6% on pack, unpack and pack->unpack
 // and ties on the direct copy; the prefix-sharing workload gains 2-6% on every
@@ -265,6 +269,70 @@ __device__ __forceinline__ void move_entry(const PoolView& src, const PoolView& 
                       chunk_vecs);
 }
 
+// Tiles smaller than a chunk: the workgroup moves tiles a0 .. a0 + group - 1
+// (arrays past n_arrays excepted) of list entry `entry`, i.e. one block's
+// tiles in `group` consecutive arrays. tile_vecs divides kThreads, so
+// lane t always takes vector t % tile_vecs of a tile: of tile
+// a0 + t / tile_vecs first, then of the tiles kThreads / tile_vecs further
+// on, with up to U of them in flight.
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+__device__ __forceinline__ void move_group(const PoolView& src, const PoolView& dst,
+                                           const char* src_stage, char* dst_stage,
+                                           int32_t src_id, int32_t dst_id, int64_t entry,
+                                           int a0, int32_t tile_vecs, int32_t group,
+                                           int32_t n_arrays) {
+  if constexpr (SRC_POOL) {
+    if (src_id < 0 || src_id >= src.num_blocks) return;
+  }
+  if constexpr (DST_POOL) {
+    if (dst_id < 0 || dst_id >= dst.num_blocks) return;
+  }
+  const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
+  const int t = threadIdx.x;
+  const int per_pass = kThreads / tile_vecs;
+  const int64_t lane_offset = static_cast<int64_t>(t % tile_vecs) * sizeof(V);
+  const int tiles = min(group, n_arrays - a0);
+  auto src_of = [&](int a) -> const char* {
+    if constexpr (SRC_POOL) return array_base(src, a) + src_id * tile_bytes + lane_offset;
+    else return src_stage + (entry * n_arrays + a) * tile_bytes + lane_offset;
+  };
+  auto dst_of = [&](int a) -> char* {
+    if constexpr (DST_POOL) return array_base(dst, a) + dst_id * tile_bytes + lane_offset;
+    else return dst_stage + (entry * n_arrays + a) * tile_bytes + lane_offset;
+  };
+  for (int j = t / tile_vecs; j < tiles; j += U * per_pass) {
+    V r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (j + u * per_pass < tiles)
+        r[u] = load_vec<V, NT>(as_global<V>(src_of(a0 + j + u * per_pass)));
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (j + u * per_pass < tiles)
+        store_vec<V, NT>(as_global<V>(dst_of(a0 + j + u * per_pass)), r[u]);
+  }
+}
+
+// One list entry's share of a workgroup: chunk p of its tile in array a, or,
+// with group > 1, its tiles in arrays a * group .. a * group + group - 1. The
+// grouped path keeps at most 4 vectors per lane in flight: each one carries
+// its own source and destination address, and at 8 the kernel's register
+// count would lower the occupancy of every launch it serves.
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+__device__ __forceinline__ void move_unit(const PoolView& src, const PoolView& dst,
+                                          const char* src_stage, char* dst_stage,
+                                          int32_t src_id, int32_t dst_id, int64_t entry,
+                                          int a, int p, int32_t tile_vecs, int32_t parts,
+                                          int32_t group, int32_t n_arrays) {
+  if (group > 1)
+    move_group<V, (U < 4 ? U : 4), NT, SRC_POOL, DST_POOL>(
+        src, dst, src_stage, dst_stage, src_id, dst_id, entry, a * group, tile_vecs, group,
+        n_arrays);
+  else
+    move_entry<V, U, NT, SRC_POOL, DST_POOL>(src, dst, src_stage, dst_stage, src_id, dst_id,
+                                             entry, a, p, tile_vecs, parts, n_arrays);
+}
+
 // Ids in device memory. A one-block workgroup reads its id pair with uniform
 // (scalar) loads: staging it in LDS would add a store, a barrier and a load
 // before the first data access of a workgroup that lives for a single chunk.
@@ -274,15 +342,16 @@ __global__ void __launch_bounds__(kThreads)
 kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
         char* __restrict__ dst_stage, const int32_t* __restrict__ src_ids,
         const int32_t* __restrict__ dst_ids, int32_t tile_vecs, int32_t n_blocks,
-        int32_t n_arrays, int32_t run, int32_t runs, int32_t parts, int32_t order) {
+        int32_t n_arrays, int32_t run, int32_t runs, int32_t parts, int32_t group,
+        int32_t order) {
   __shared__ int32_t s_src[kMaxRun];
   __shared__ int32_t s_dst[kMaxRun];
-  const Place pl = place_of(n_arrays, runs, parts, order);
+  const Place pl = place_of((n_arrays + group - 1) / group, runs, parts, order);
   const int first = pl.r * run;
   if (run == 1) {
-    move_entry<V, U, NT, SRC_POOL, DST_POOL>(
+    move_unit<V, U, NT, SRC_POOL, DST_POOL>(
         src, dst, src_stage, dst_stage, SRC_POOL ? src_ids[first] : 0,
-        DST_POOL ? dst_ids[first] : 0, first, pl.a, pl.p, tile_vecs, parts, n_arrays);
+        DST_POOL ? dst_ids[first] : 0, first, pl.a, pl.p, tile_vecs, parts, group, n_arrays);
     return;
   }
   const int count = min(run, n_blocks - first);
@@ -293,9 +362,9 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
   }
   __syncthreads();
   for (int j = 0; j < count; ++j)
-    move_entry<V, U, NT, SRC_POOL, DST_POOL>(
+    move_unit<V, U, NT, SRC_POOL, DST_POOL>(
         src, dst, src_stage, dst_stage, SRC_POOL ? s_src[j] : 0, DST_POOL ? s_dst[j] : 0,
-        first + j, pl.a, pl.p, tile_vecs, parts, n_arrays);
+        first + j, pl.a, pl.p, tile_vecs, parts, group, n_arrays);
 }
 
 // Ids carried in the launch's own kernel arguments: source ids at ids[i],
@@ -311,12 +380,12 @@ __global__ void __launch_bounds__(kThreads)
 kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
                char* __restrict__ dst_stage, InlineIds ids, int32_t id_base, int32_t dst_off,
                int32_t tile_vecs, int32_t n_arrays, int32_t runs, int32_t parts,
-               int32_t order) {
-  const Place pl = place_of(n_arrays, runs, parts, order);
+               int32_t group, int32_t order) {
+  const Place pl = place_of((n_arrays + group - 1) / group, runs, parts, order);
   const int i = id_base + pl.r;
-  move_entry<V, U, NT, SRC_POOL, DST_POOL>(
+  move_unit<V, U, NT, SRC_POOL, DST_POOL>(
       src, dst, src_stage, dst_stage, SRC_POOL ? ids.v[i] : 0, DST_POOL ? ids.v[dst_off + i] : 0,
-      i, pl.a, pl.p, tile_vecs, parts, n_arrays);
+      i, pl.a, pl.p, tile_vecs, parts, group, n_arrays);
 }
 
 // Row kernels on either side of the handoff. A pool row is one token's
@@ -387,9 +456,9 @@ thread_local Profiler g_profiler;
 
 using MoveKernel = void (*)(PoolView, PoolView, const char*, char*, const int32_t*,
                             const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
-                            int32_t, int32_t);
+                            int32_t, int32_t, int32_t);
 using InlineKernel = void (*)(PoolView, PoolView, const char*, char*, InlineIds, int32_t,
-                              int32_t, int32_t, int32_t, int32_t, int32_t, int32_t);
+                              int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t);
 
 // Kernel for vectors of the widest width the alignment allows, keeping up to
 // `unroll` of them in flight per lane; `lane_vecs` (vectors per lane per
@@ -472,15 +541,30 @@ int chunk_parts(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes) {
   return parts;
 }
 
+// Tiles per workgroup for tiles smaller than the chunk size: chunk_bytes /
+// tile bytes tiles of one block in consecutive arrays (at most n_arrays), when
+// a tile's vector count divides the workgroup's lanes; 1 otherwise. Measured
+// on MI355X on one rank's share of the 70B-share workload at tp=8 (2 KiB
+// tiles, 160 arrays): two tiles per workgroup (4 KiB chunks) raised the
+// per-request direct copy from 4.17 to 5.76 TB/s and pack -> unpack from 4.34
+// to 6.15 TB/s; groups of 8 and 16 KiB were no faster.
+int tile_group(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes, int32_t n_arrays) {
+  if (chunk_bytes <= 0 || tile_vecs * vec_bytes >= chunk_bytes || kThreads % tile_vecs) return 1;
+  return static_cast<int>(std::min<int64_t>(chunk_bytes / (tile_vecs * vec_bytes), n_arrays));
+}
+
 // A dispatch holds at most 2^32 - 1 work-items, so one launch takes at most
 // this many workgroups; larger moves are split over several launches.
 constexpr int64_t kMaxGrid = static_cast<int64_t>(UINT32_MAX) / kThreads;
 
-// Launch shape of one move: blocks per run, chunks per tile, vector width,
-// vectors per lane per chunk, workgroup order, and how many runs one launch takes.
+// Launch shape of one move: blocks per run, chunks per tile, tiles per
+// workgroup (group; then `units` array groups), vector width, vectors per
+// lane per workgroup, workgroup order, and how many runs one launch takes.
 struct MovePlan {
   int run = 1;
   int parts = 1;
+  int group = 1;
+  int32_t units = 0;
   int vec = 16;
   int lane_vecs = 1;
   int32_t tile_vecs = 0;
@@ -508,12 +592,15 @@ int plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
     return set_error(IEKV_ERR_INVALID, "%d arrays exceed the grid limit", n_arrays);
   pl->total_runs = (static_cast<int64_t>(n_blocks) + pl->run - 1) / pl->run;
   while (pl->parts > 1 && pl->total_runs * n_arrays * pl->parts > kMaxGrid) pl->parts /= 2;
-  pl->lane_vecs = static_cast<int>(
-      std::min<int64_t>((tile_vecs / pl->parts + kThreads - 1) / kThreads, 16));
+  pl->group = pl->run == 1 && pl->parts == 1
+                  ? tile_group(tile_vecs, pl->vec, g_chunk.load(), n_arrays) : 1;
+  pl->units = (n_arrays + pl->group - 1) / pl->group;
+  pl->lane_vecs = static_cast<int>(std::min<int64_t>(
+      (tile_vecs * pl->group / pl->parts + kThreads - 1) / kThreads, 16));
   pl->tile_vecs = static_cast<int32_t>(tile_vecs);
   pl->order = pool_writing ? g_order.load() : g_pack_order.load();
   pl->runs_per_launch =
-      std::min<int64_t>(pl->total_runs, kMaxGrid / (int64_t(n_arrays) * pl->parts));
+      std::min<int64_t>(pl->total_runs, kMaxGrid / (int64_t(pl->units) * pl->parts));
   return IEKV_OK;
 }
 
@@ -549,12 +636,13 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
     const int32_t cnt = static_cast<int32_t>(
         std::min<int64_t>(pl.runs_per_launch * pl.run, n_blocks - first));
     const int32_t runs = static_cast<int32_t>((cnt + pl.run - 1) / pl.run);
-    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * n_arrays * pl.parts);
+    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * pl.units * pl.parts);
     if ((rc = dispatch(k, grid, stream, view_of(sp), view_of(dp),
                        SP ? nullptr : src_stage + first * block_image,
                        DP ? nullptr : dst_stage + first * block_image,
                        SP ? src_ids + first : nullptr, DP ? dst_ids + first : nullptr,
-                       pl.tile_vecs, cnt, n_arrays, pl.run, runs, pl.parts, pl.order)))
+                       pl.tile_vecs, cnt, n_arrays, pl.run, runs, pl.parts, pl.group,
+                       pl.order)))
       return rc;
   }
   return IEKV_OK;
@@ -575,10 +663,10 @@ int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src
   for (int64_t r0 = 0; r0 < pl.total_runs; r0 += pl.runs_per_launch) {
     const int32_t runs = static_cast<int32_t>(std::min<int64_t>(pl.runs_per_launch,
                                                                 pl.total_runs - r0));
-    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * n_arrays * pl.parts);
+    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * pl.units * pl.parts);
     if ((rc = dispatch(k, grid, stream, view_of(sp), view_of(dp), src_stage, dst_stage, ids,
                        static_cast<int32_t>(r0), dst_off, pl.tile_vecs, n_arrays, runs, pl.parts,
-                       pl.order)))
+                       pl.group, pl.order)))
       return rc;
   }
   return IEKV_OK;

@@ -213,12 +213,35 @@ def cfg5(seed: int = 0) -> Workload:
 CONFIGS = {"cfg1": cfg1, "cfg2": cfg2, "cfg3": cfg3, "cfg4": cfg4, "cfg5": cfg5}
 
 
-def make(name: str, seed: int = 0, slack: int | None = None) -> Workload:
-    """Workload ``name``; ``slack`` (cfg3, cfg4) sets the spare blocks in each pool."""
+def tp_share(w: Workload, tp: int) -> Workload:
+    """One rank's share of ``w`` under head-sharded tensor parallelism of degree ``tp``.
+
+    Under TP each rank's caches hold ``H / tp`` of the KV heads
+    (ie/parallel/tensor_parallel.py:17-18, 76-79) while the block tables are
+    shared, so every rank moves the same block ids with tiles of
+    ``bs x (H / tp) x D x e`` bytes; the payload per rank is ``P / tp``.
+    """
+    if tp < 1 or w.shape.kv_heads % tp:
+        raise ValueError(f"tp={tp} does not divide the {w.shape.kv_heads} KV heads of {w.name}")
+    if tp == 1:
+        return w
+    s = w.shape
+    shape = Shape(s.layers, s.kv_heads // tp, s.head_dim, s.block_size, s.dtype)
+    return Workload(f"{w.name}/tp{tp}", f"{w.description}; one rank's share at tp={tp} "
+                    f"({shape.kv_heads} of {s.kv_heads} KV heads)", shape, w.lengths,
+                    w.src_tables, w.dst_tables, w.src_pool_blocks, w.dst_pool_blocks,
+                    w.skipped_blocks, w.resident_prefix)
+
+
+def make(name: str, seed: int = 0, slack: int | None = None, tp: int = 1) -> Workload:
+    """Workload ``name``; ``slack`` (cfg3, cfg4) sets the spare blocks in each pool;
+    ``tp`` > 1 gives one rank's share under head-sharded tensor parallelism."""
     if name not in CONFIGS:
         raise ValueError(f"unknown workload {name!r}; choose from {sorted(CONFIGS)}")
     if slack is None:
-        return CONFIGS[name](seed)
-    if name not in ("cfg3", "cfg4"):
+        w = CONFIGS[name](seed)
+    elif name not in ("cfg3", "cfg4"):
         raise ValueError(f"{name} has fixed pool sizes")
-    return CONFIGS[name](seed, slack=slack)
+    else:
+        w = CONFIGS[name](seed, slack=slack)
+    return tp_share(w, tp)

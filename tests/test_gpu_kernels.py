@@ -230,6 +230,56 @@ def test_every_launch_shape_is_bit_exact(gpu):
         _native.set_launch(**before)
 
 
+@pytest.mark.parametrize("bs,heads,dim,dtype,layers", [
+    (16, 1, 128, torch.uint8, 40),     # 2 KiB tiles, 80 arrays (the 70B share at tp=8)
+    (16, 1, 64, torch.bfloat16, 5),    # 2 KiB tiles, 10 arrays
+    (4, 1, 32, torch.float32, 3),      # 512 B tiles, 6 arrays: groups larger than the arrays
+    (1, 1, 8, torch.float16, 7),       # 16 B tiles, 14 arrays
+    (16, 1, 128, torch.bfloat16, 3),   # 4 KiB tiles: grouped only under larger chunks
+    (2, 3, 8, torch.float32, 4),       # 192 B tiles: 12 vectors do not divide 256 lanes
+    (3, 1, 5, torch.float16, 6),       # 30 B tiles (2-byte vectors)
+])
+def test_tiles_smaller_than_a_chunk_are_grouped_bit_exact(gpu, bs, heads, dim, dtype, layers):
+    """A tile smaller than the chunk size is moved together with the same
+    block's tiles in the next arrays by one workgroup (partial last groups
+    included). Pack, unpack and direct copy, device and kernel-argument ids,
+    under chunks that give 1 to 128 tiles per workgroup, against the oracle."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    sk, sv = allocate(60, bs, layers, heads, dim, dtype, gpu, seed=50)
+    dk, dv = allocate(50, bs, layers, heads, dim, dtype, gpu, seed=51)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    rng = np.random.default_rng(52)
+    src_ids, dst_ids = random_tables(rng, 60, 50, 37)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    want = packed_image(pack(src_o, src_ids))
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    source = host_bytes(sk) + host_bytes(sv)
+    rows = np.concatenate([np.arange(b * bs, (b + 1) * bs) for b in dst_ids])
+    dev = lambda ids: torch.tensor(ids, dtype=torch.int32, device=gpu)  # noqa: E731
+    before = _native.get_launch()
+    try:
+        for chunk in (0, 1024, 4096, 8192, 65536):
+            for unroll in (1, 4, 16):
+                _native.set_launch(0, unroll, 1, -1, -1, chunk)
+                for ids_of in (dev, list):
+                    label = (chunk, unroll, ids_of)
+                    packed = src.read_blocks(ids_of(src_ids))
+                    assert np.array_equal(packed.data.cpu().numpy(), want), label
+                    for t in dk + dv:
+                        t.zero_()
+                    dst.write_blocks(ids_of(dst_ids[:20]), packed[:20])
+                    dst.copy_blocks(src, ids_of(src_ids[20:]), ids_of(dst_ids[20:]))
+                    torch.cuda.synchronize()
+                    got = host_bytes(dk) + host_bytes(dv)
+                    for g, w in zip(got, list(dst_o.k_caches) + list(dst_o.v_caches)):
+                        assert np.array_equal(g[rows], w[rows]), label
+    finally:
+        _native.set_launch(**before)
+    assert all(np.array_equal(a, b) for a, b in zip(source, host_bytes(sk) + host_bytes(sv)))
+
+
 @pytest.mark.parametrize("count", [1, 255, 256, 257, 600])
 def test_host_ids_in_the_kernel_arguments_and_beyond(gpu, count):
     """Host id lists of up to 256 blocks ride in the launch's kernel arguments
@@ -288,10 +338,13 @@ def test_a_split_that_would_overflow_the_dispatch_is_halved(gpu):
         assert torch.equal(got[d_ids], want[s_ids])
 
 
-def test_a_move_beyond_one_dispatch_spreads_over_launches(gpu):
-    """9M 16-byte tiles x 2 arrays with whole-tile workgroups exceed one
-    dispatch (16,777,215 workgroups of 256 lanes): the library issues two
-    launches over consecutive entry ranges, and pack keeps the staging layout."""
+@pytest.mark.parametrize("chunk,launches", [(0, 4), (4096, 2)])
+def test_a_move_beyond_one_dispatch_spreads_over_launches(gpu, chunk, launches):
+    """9M 16-byte tiles x 2 arrays with one tile per workgroup (chunk 0) exceed
+    one dispatch (16,777,215 workgroups of 256 lanes): the library issues two
+    launches per move over consecutive entry ranges, and pack keeps the staging
+    layout. Under 4 KiB chunks one workgroup takes a block's tiles in both
+    arrays, so each move fits one launch."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -304,10 +357,15 @@ def test_a_move_beyond_one_dispatch_spreads_over_launches(gpu):
     gen.manual_seed(33)
     src_ids = torch.randperm(n, device=gpu, generator=gen).to(torch.int32)
     dst_ids = torch.randperm(n, device=gpu, generator=gen).to(torch.int32)
-    with _native.LaunchTimer(8) as timer:
-        dst.copy_blocks(src, src_ids, dst_ids)
-        packed = src.read_blocks(src_ids)
-    assert len(timer.durations_ms) == 4
+    before = _native.get_launch()
+    try:
+        _native.set_launch(0, 0, -1, -1, -1, chunk)
+        with _native.LaunchTimer(8) as timer:
+            dst.copy_blocks(src, src_ids, dst_ids)
+            packed = src.read_blocks(src_ids)
+        assert len(timer.durations_ms) == launches
+    finally:
+        _native.set_launch(**before)
     torch.cuda.synchronize()
     s_ids, d_ids = src_ids.long(), dst_ids.long()
     for a, (s_arr, d_arr) in enumerate(zip(sk + sv, dk + dv)):
