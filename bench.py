@@ -17,6 +17,12 @@ without NaN codes for fp8). Legs:
   copier       the drop-in Python path: HipSlotCopier.copy_blocks per request with the
                block tables as Python lists (id checks and hand-over included; 2P bytes)
   copier_pack_unpack  the same for pack mode: read_blocks then write_blocks (4P bytes)
+  write_kv     the prefill side: every request's new K/V rows scattered into the
+               prefill pool by slot, one iekv_write_slots launch per request and layer
+               (read + write of every row)
+  gather_context  the decode side: every request's context gathered from the decode pool
+               through its block table (resident prefix included), one iekv_gather_rows
+               launch per request and array (read + write of every row)
 
 ``value`` is the direct leg's algorithmic read+write bandwidth, 2P / step
 time, in GB/s (P = blocks x 2L x T); the step time comes from two HIP events
@@ -52,6 +58,10 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # known size); see profiles/kv_move_direct_cfg3_pmc.txt.
 PMC_TRAFFIC_RATIO = 1.0002
 METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff"
+# Legs that move the workload's blocks from the prefill pool to the decode pool; the
+# first of them in --legs gives the line's value (2P / step time).
+HANDOFF_LEGS = ("direct", "pack_unpack", "pack", "unpack", "batched", "copier",
+                "copier_pack_unpack")
 
 
 def log(msg: str) -> None:
@@ -142,7 +152,93 @@ class Legs:
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
         if name == "batched":
             return [(2 * sum(sizes) * bb, 0)]
+        if name in ("write_kv", "gather_context"):
+            row = self.w.shape.tile_bytes // self.w.shape.block_size
+            tokens, contexts = self._slot_sizes()
+            if name == "write_kv":   # K and V rows of one layer per launch
+                return [(4 * n * row, r) for r, n in enumerate(tokens)
+                        for _ in range(self.w.shape.layers)]
+            return [(2 * n * row, r) for r, n in enumerate(contexts)
+                    for _ in range(self.w.shape.n_arrays)]
         return []
+
+    # -- the slot kernels on either side of the handoff -------------------------------------
+    def _slot_sizes(self) -> tuple[list[int], list[int]]:
+        """Tokens each request's prefill writes (those of its moved blocks; a resident
+        prefix is not written) and the context its decode reads (all its tokens)."""
+        bs = self.w.shape.block_size
+        tokens = [n - (-(-n // bs) - len(t)) * bs for n, t in zip(self.w.lengths, self.w.src_tables)]
+        return tokens, list(self.w.lengths)
+
+    def _slot_inputs(self):
+        """Per-request slots (prefill pool), decode block tables (resident prefix first),
+        the new K/V rows and a context buffer; built once."""
+        if not hasattr(self, "_slots"):
+            torch = self.torch
+            s = self.w.shape
+            bs = s.block_size
+            dev = self.src_k[0].device
+            tokens, contexts = self._slot_sizes()
+            slots, tables = [], []
+            for n, src_t, dst_t in zip(tokens, self.w.src_tables, self.w.dst_tables):
+                pos = torch.arange(n, device=dev)
+                table = torch.tensor(src_t, dtype=torch.int64, device=dev)
+                slots.append((table[pos // bs] * bs + pos % bs).contiguous())
+                tables.append(torch.tensor(list(self.w.resident_prefix) + list(dst_t),
+                                           dtype=torch.int32, device=dev))
+            shape = (max(max(tokens), max(contexts)), s.kv_heads, s.head_dim)
+            new_k, new_v, out = (torch.empty(shape, dtype=self.src_k[0].dtype, device=dev)
+                                 for _ in range(3))
+            fill_pool([new_k, new_v], s.dtype, 12345)
+            self._slots = (tokens, contexts, slots, tables, new_k, new_v, out)
+        return self._slots
+
+    def write_kv(self) -> None:
+        from iekv import _native
+
+        tokens, _, slots, _, new_k, new_v, _ = self._slot_inputs()
+        h = self.stream.cuda_stream
+        bs = self.w.shape.block_size
+        for n, sl in zip(tokens, slots):
+            for layer in range(self.w.shape.layers):
+                _native.call("iekv_write_slots", self.src.native.handle, layer, bs,
+                             new_k.data_ptr(), new_v.data_ptr(), sl.data_ptr(), n, h)
+
+    def gather_context(self) -> None:
+        from iekv import _native
+
+        _, contexts, _, tables, _, _, out = self._slot_inputs()
+        h = self.stream.cuda_stream
+        bs = self.w.shape.block_size
+        nbytes = out.numel() * out.element_size()
+        for n, table in zip(contexts, tables):
+            for a in range(self.w.shape.n_arrays):
+                _native.call("iekv_gather_rows", self.dst.native.handle, a, bs,
+                             table.data_ptr(), n, out.data_ptr(), nbytes, h)
+
+    def verify_write_kv(self) -> bool:
+        """Every request's slots hold the new K and V rows in every layer."""
+        torch = self.torch
+        tokens, _, slots, _, new_k, new_v, _ = self._slot_inputs()
+        L = self.w.shape.layers
+        arrays = self.src_k + self.src_v
+        for n, sl in zip(tokens, slots):
+            for a, t in enumerate(arrays):
+                want = (new_k if a < L else new_v)[:n]
+                if not torch.equal(t.index_select(0, sl).view(torch.uint8),
+                                   want.view(torch.uint8)):
+                    return False
+        return True
+
+    def verify_gather(self) -> bool:
+        """The context buffer holds the last request's rows of the last array."""
+        torch = self.torch
+        _, contexts, _, tables, _, _, out = self._slot_inputs()
+        bs = self.w.shape.block_size
+        n, table = contexts[-1], tables[-1].long()
+        pos = torch.arange(n, device=table.device)
+        rows = self.dst_v[-1].index_select(0, table[pos // bs] * bs + pos % bs)
+        return torch.equal(out[:n].view(torch.uint8), rows.view(torch.uint8))
 
     def direct(self) -> None:
         from iekv import _native
@@ -396,7 +492,8 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
         "avg_launch_us": round(1000 * total_ms / max(1, len(durations)), 2),
         "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
     }
-    if name in ("direct", "copier", "pack_unpack", "copier_pack_unpack", "pack", "unpack"):
+    if name in ("direct", "copier", "pack_unpack", "copier_pack_unpack", "pack", "unpack",
+                "write_kv", "gather_context"):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
                                  "p50": round(req_ms[len(req_ms) // 2], 4),
                                  "p99": round(req_ms[min(len(req_ms) - 1,
@@ -528,7 +625,8 @@ def main() -> int:
                     help="spare blocks per pool for cfg3/cfg4 (default 64)")
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
                     help="comma list of direct, pack_unpack, pack, unpack, batched, copier, "
-                         "copier_pack_unpack, plain_copy, host_roundtrip")
+                         "copier_pack_unpack, write_kv, gather_context, plain_copy, "
+                         "host_roundtrip")
     ap.add_argument("--cpu-blocks", type=int, default=1536,
                     help="blocks in the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -579,6 +677,10 @@ def main() -> int:
         print(json.dumps({"sweep": w.name, "legs": names, "rows": rows, "verified": ok}))
         return 0 if ok else 1
     names = [x for x in args.legs.split(",") if x]
+    if not any(x in HANDOFF_LEGS for x in names):
+        print(f"--legs needs one handoff leg ({', '.join(HANDOFF_LEGS)}) for the line's value",
+              file=sys.stderr)
+        return 2
     results: dict = {}
     verified: dict = {}
     primary = None
@@ -590,21 +692,22 @@ def main() -> int:
                 verified[name] = legs.verify()
                 log(f"[bench] {name}: destination tiles equal source tiles: {verified[name]}")
             continue
-        legs.clear_dst()
+        if name != "gather_context":
+            legs.clear_dst()
         ms, wall, launches = time_leg(legs, name, args.steps, args.warmup)
-        nbytes = 4 * P if name in ("pack_unpack", "copier_pack_unpack") else 2 * P
-        if name == "plain_copy":
-            nbytes = 2 * (4 << 30)
+        nbytes = 2 * (4 << 30) if name == "plain_copy" else sum(b for b, _ in legs.plan(name))
         res, kgbs, avg_us, avg_bytes = summarize(legs, name, ms, launches, nbytes, args.steps)
         res["wall_s"] = round(wall, 3)
         if name in ("pack_unpack", "copier_pack_unpack"):
             res["effective_handoff_GBps"] = round(2 * P / (ms * 1e-3) / 1e9, 1)
         if not args.no_verify and name != "plain_copy":
-            check = {"pack": legs.verify_pack, "unpack": legs.verify_unpack}.get(name, legs.verify)
+            check = {"pack": legs.verify_pack, "unpack": legs.verify_unpack,
+                     "write_kv": legs.verify_write_kv,
+                     "gather_context": legs.verify_gather}.get(name, legs.verify)
             verified[name] = check()
             log(f"[bench] {name}: moved tiles equal their sources: {verified[name]}")
         results[name] = res
-        if primary is None and name != "plain_copy":
+        if primary is None and name in HANDOFF_LEGS:
             primary = (name, ms, res, kgbs, avg_us, avg_bytes)
 
     cpu = None

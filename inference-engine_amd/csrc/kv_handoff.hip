@@ -395,6 +395,22 @@ kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
 // (four waves) moves four rows.
 constexpr int kWave = 64;
 constexpr int kRowsPerGroup = kThreads / kWave;
+constexpr int kRowUnroll = 4;  // vectors per lane in flight: a 4 KiB row in one step
+
+// One row of row_vecs vectors, moved by one wave: lane l takes vectors
+// l, l + 64, ..., loading up to kRowUnroll of them before storing them.
+template <typename V>
+__device__ __forceinline__ void move_row(gptr<const V> s, gptr<V> d, int row_vecs) {
+  for (int e = threadIdx.x % kWave; e < row_vecs; e += kRowUnroll * kWave) {
+    V r[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u)
+      if (e + u * kWave < row_vecs) r[u] = s[e + u * kWave];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u)
+      if (e + u * kWave < row_vecs) d[e + u * kWave] = r[u];
+  }
+}
 
 // write_kv: k/v row i (contiguous [n, row]) -> row slots[i] of arrays a_k / a_v.
 template <typename V>
@@ -408,9 +424,8 @@ kv_scatter_rows(PoolView pool, int32_t a_k, int32_t a_v, const char* __restrict_
   if (slot < 0 || slot >= pool_rows) return;  // never address outside the pool
   const bool is_v = blockIdx.y != 0;
   const int64_t row_bytes = static_cast<int64_t>(row_vecs) * sizeof(V);
-  gptr<const V> src = as_global<V>((is_v ? v : k) + i * row_bytes);
-  gptr<V> dst = as_global<V>(array_base(pool, is_v ? a_v : a_k) + slot * row_bytes);
-  for (int e = threadIdx.x % kWave; e < row_vecs; e += kWave) dst[e] = src[e];
+  move_row<V>(as_global<V>((is_v ? v : k) + i * row_bytes),
+              as_global<V>(array_base(pool, is_v ? a_v : a_k) + slot * row_bytes), row_vecs);
 }
 
 // gather_context: out row j = row (table[j / bs] * bs + j % bs) of array a, j < n.
@@ -424,19 +439,18 @@ kv_gather_rows(PoolView pool, int32_t a, const int32_t* __restrict__ table, int3
   if (block < 0 || block >= pool.num_blocks) return;
   const int64_t row_bytes = static_cast<int64_t>(row_vecs) * sizeof(V);
   const int64_t row = static_cast<int64_t>(block) * bs + j % bs;
-  gptr<const V> src = as_global<V>(array_base(pool, a) + row * row_bytes);
-  gptr<V> dst = as_global<V>(out + j * row_bytes);
-  for (int e = threadIdx.x % kWave; e < row_vecs; e += kWave) dst[e] = src[e];
+  move_row<V>(as_global<V>(array_base(pool, a) + row * row_bytes),
+              as_global<V>(out + j * row_bytes), row_vecs);
 }
 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
-// Per-thread launch timing: while a session is open, every kv_move launch is
-// dispatched with hipExtLaunchKernelGGL carrying a start/stop event pair, so the
-// timestamps come from the dispatch packet itself and no marker packets are
-// added to the queue between launches.
+// Per-thread launch timing: while a session is open, every kernel launch of the
+// library (kv_move and the row kernels) is dispatched with hipExtLaunchKernelGGL
+// carrying a start/stop event pair, so the timestamps come from the dispatch
+// packet itself and no marker packets are added to the queue between launches.
 struct Profiler {
   bool on = false;
   int device = -1;
@@ -607,14 +621,14 @@ int plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
 // One dispatch; while a timing session is open it carries a start/stop event
 // pair in its own packet.
 template <typename Kernel, typename... Args>
-int dispatch(Kernel kernel, uint32_t grid, hipStream_t stream, Args... args) {
+int dispatch(Kernel kernel, dim3 grid, hipStream_t stream, Args... args) {
   Profiler& prof = g_profiler;
   if (prof.on && prof.used < prof.events.size()) {
     auto& ev = prof.events[prof.used++];
-    hipExtLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, ev.first, ev.second,
-                          0, args...);
+    hipExtLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, ev.first, ev.second, 0,
+                          args...);
   } else {
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, args...);
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, args...);
   }
   IEKV_HIP(hipGetLastError());
   return IEKV_OK;
@@ -1048,17 +1062,14 @@ int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, c
   const PoolView view = view_of(pool);
   const int32_t ak = layer, av = layers + layer;
 #define IEKV_SCATTER(T)                                                                      \
-  hipLaunchKernelGGL(kv_scatter_rows<T>, grid, dim3(kThreads), 0, stream, view, ak, av, kc, \
-                     vc, slots, n_tokens, static_cast<int32_t>(row_bytes / sizeof(T)),       \
-                     pool_rows)
-  if (align >= 16) IEKV_SCATTER(u32x4);
-  else if (align >= 8) IEKV_SCATTER(u32x2);
-  else if (align >= 4) IEKV_SCATTER(uint32_t);
-  else if (align >= 2) IEKV_SCATTER(uint16_t);
-  else IEKV_SCATTER(uint8_t);
+  dispatch(kv_scatter_rows<T>, grid, stream, view, ak, av, kc, vc, slots, n_tokens,          \
+           static_cast<int32_t>(row_bytes / sizeof(T)), pool_rows)
+  if (align >= 16) return IEKV_SCATTER(u32x4);
+  if (align >= 8) return IEKV_SCATTER(u32x2);
+  if (align >= 4) return IEKV_SCATTER(uint32_t);
+  if (align >= 2) return IEKV_SCATTER(uint16_t);
+  return IEKV_SCATTER(uint8_t);
 #undef IEKV_SCATTER
-  IEKV_HIP(hipGetLastError());
-  return IEKV_OK;
 }
 
 int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
@@ -1087,17 +1098,14 @@ int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
   char* oc = static_cast<char*>(out);
   const PoolView view = view_of(pool);
 #define IEKV_GATHER(T)                                                                      \
-  hipLaunchKernelGGL(kv_gather_rows<T>, grid, dim3(kThreads), 0, stream, view, array,      \
-                     block_table, block_size, oc, context_len,                              \
-                     static_cast<int32_t>(row_bytes / sizeof(T)))
-  if (align >= 16) IEKV_GATHER(u32x4);
-  else if (align >= 8) IEKV_GATHER(u32x2);
-  else if (align >= 4) IEKV_GATHER(uint32_t);
-  else if (align >= 2) IEKV_GATHER(uint16_t);
-  else IEKV_GATHER(uint8_t);
+  dispatch(kv_gather_rows<T>, grid, stream, view, array, block_table, block_size, oc,      \
+           context_len, static_cast<int32_t>(row_bytes / sizeof(T)))
+  if (align >= 16) return IEKV_GATHER(u32x4);
+  if (align >= 8) return IEKV_GATHER(u32x2);
+  if (align >= 4) return IEKV_GATHER(uint32_t);
+  if (align >= 2) return IEKV_GATHER(uint16_t);
+  return IEKV_GATHER(uint8_t);
 #undef IEKV_GATHER
-  IEKV_HIP(hipGetLastError());
-  return IEKV_OK;
 }
 
 int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,

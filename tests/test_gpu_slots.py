@@ -16,6 +16,8 @@ CASES = [  # block_size, heads, dim, dtype
     (3, 1, 5, torch.float16),     # 10-byte rows: 2-byte vectors
     (16, 8, 128, torch.float8_e4m3fn),
     (5, 3, 3, torch.uint8),       # 9-byte rows
+    (4, 16, 128, torch.float32),  # 8 KiB rows: two steps of four vectors per lane
+    (2, 9, 128, torch.float32),   # 4.5 KiB rows: a full step, then 32 lanes
 ]
 
 
