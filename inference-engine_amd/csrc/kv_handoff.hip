@@ -76,7 +76,7 @@ int set_error(int code, const char* fmt, ...) {
 // Launch shape. Measured on MI355X over the five benchmark workloads (8 KiB to
 // 64 KiB tiles): one tile per workgroup and streaming (non-temporal) accesses
 // are best or within noise everywhere; unroll 4, 8 and 16 are within noise of
-// each other, and 8 keeps the kernel at 58 VGPRs (full occupancy).
+// each other, and 8 keeps the kernel at 62 VGPRs (full occupancy).
 std::atomic<int> g_run{0};       // 0 = automatic
 std::atomic<int> g_unroll{8};
 std::atomic<int> g_nontemporal{1};
