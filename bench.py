@@ -645,6 +645,11 @@ def main() -> int:
                          "(prefill pool first)")
     args = ap.parse_args()
 
+    names = [x for x in args.legs.split(",") if x]
+    if not args.sweep and not any(x in HANDOFF_LEGS for x in names):
+        print(f"--legs needs one handoff leg ({', '.join(HANDOFF_LEGS)}) for the line's value",
+              file=sys.stderr)
+        return 2
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: the KV handoff runs on a single MI355X here "
@@ -676,11 +681,6 @@ def main() -> int:
         ok = legs.verify()
         print(json.dumps({"sweep": w.name, "legs": names, "rows": rows, "verified": ok}))
         return 0 if ok else 1
-    names = [x for x in args.legs.split(",") if x]
-    if not any(x in HANDOFF_LEGS for x in names):
-        print(f"--legs needs one handoff leg ({', '.join(HANDOFF_LEGS)}) for the line's value",
-              file=sys.stderr)
-        return 2
     results: dict = {}
     verified: dict = {}
     primary = None

@@ -1,0 +1,20 @@
+"""bench.py's command-line refusals (CPU): both happen before any GPU is touched."""
+from __future__ import annotations
+
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.mark.parametrize("args,message", [
+    (["--gpus", "2"], "measures one GPU"),
+    (["--legs", "write_kv,gather_context"], "needs one handoff leg"),
+])
+def test_the_bench_refuses_before_touching_a_gpu(args, message):
+    out = subprocess.run([sys.executable, "bench.py", *args], cwd=ROOT, capture_output=True,
+                         text=True, timeout=120)
+    assert out.returncode == 2 and message in out.stderr, out.stderr[-2000:]

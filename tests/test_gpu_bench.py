@@ -1,0 +1,57 @@
+"""bench.py end to end on the small workload (GPU): the JSON line's fields and every leg verified.
+
+Each case runs bench.py in a child process on cfg1 (72.5 MB payload) with a
+short timed pass, then reads its one JSON line. The second case measures one
+rank's share at tp=4 (2 KiB tiles, moved two to a workgroup).
+"""
+from __future__ import annotations
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parents[1]
+LEGS = ["direct", "pack_unpack", "pack", "unpack", "batched", "copier", "copier_pack_unpack",
+        "write_kv", "gather_context"]
+
+
+def run_bench(*args):
+    cmd = [sys.executable, "bench.py", "--config", "cfg1", "--steps", "2", "--warmup", "1",
+           "--cpu-blocks", "64", "--cpu-seconds", "0.2", *args]
+    print("running", " ".join(cmd[1:]), flush=True)
+    out = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=240)
+    assert out.returncode == 0, out.stderr[-3000:]
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
+@pytest.mark.parametrize("tp", [1, 4])
+def test_the_bench_line_keeps_its_contract(gpu, tp):
+    line = run_bench("--legs", ",".join(LEGS), "--tp", str(tp))
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+                "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
+                "roofline", "cpu_baseline"):
+        assert key in line, key
+    assert line["n_gpus"] == 1 and line["steps"] == 2 and line["warmup"] == 1
+    assert line["unit"] == "GB/s" and line["higher_is_better"] is True
+    assert line["config"]["tp_share"] == tp
+    assert line["config"]["tile_bytes"] == 8192 // tp
+    assert set(line["verified"]) == set(LEGS) and all(line["verified"].values())
+    # the value is the first handoff leg's 2P / step time
+    assert line["config"]["leg"] == "direct"
+    assert line["value"] == line["legs"]["direct"]["GBps"] > 0
+    roof = line["roofline"]
+    assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
+    assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
+    assert roof["traffic"] >= roof["algorithmic_bytes_per_launch"] > 0
+    cpu = line["cpu_baseline"]
+    assert cpu["kind"] == "port" and cpu["cores"] == 1 and cpu["value"] > 0 and cpu["checked"]
+    # one launch per request and layer for write_kv, per request and array for gather_context
+    legs = line["legs"]
+    assert legs["write_kv"]["launches_per_step"] == 64 * 4
+    assert legs["gather_context"]["launches_per_step"] == 64 * 8
+    assert legs["batched"]["launches_per_step"] == 1
