@@ -25,7 +25,10 @@
  *   which take at most IEKV_INLINE_IDS ids in HOST memory and check them
  *   before launching. Callers validate device ids against the pool size
  *   before a call; kernels skip a tile whose id is out of range so a bad id
- *   can never address memory outside the pool.
+ *   can never address memory outside the pool. The tiles of one call are
+ *   moved concurrently: destination ids must be distinct, and a direct copy
+ *   within one pool must not use a block as both source and destination
+ *   (the library checks neither; the Python layer checks host id lists).
  *   All copies are raw bytes: fp32/fp16/bf16/fp8/int8 caches move bit-exactly.
  *
  * Errors. Every function returns IEKV_OK (0) or a negative IEKV_ERR_* code,
