@@ -720,6 +720,19 @@ int64_t image_bytes(const iekv_pool* p, int64_t n) {
   return block * n;
 }
 
+// Bytes from p to the end of the HIP allocation that holds it (pinned host
+// memory included), or 0 when the runtime does not know p. A failed lookup is
+// not an error of the caller's call, so it is cleared from HIP's last error.
+int64_t bytes_to_allocation_end(const char* p) {
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<char*>(p)) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return static_cast<int64_t>(static_cast<const char*>(base) + size - p);
+}
+
 // A small set of events that lives for one pipeline call.
 class Events {
  public:
@@ -1198,13 +1211,18 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
   return restore_pipeline(
       dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
       [&](char* slot, int64_t first, int32_t cnt) -> int {
-        // One copy per run of blocks whose images are adjacent in host memory.
+        // One copy per run of blocks whose images are adjacent in host memory
+        // and lie in the allocation holding the run's first image: separately
+        // pinned buffers can be neighbours in the address space, and one copy
+        // must not run past the end of its source allocation.
         for (int32_t i = 0; i < cnt;) {
           const char* run_start = static_cast<const char*>(host_blocks[first + i]);
+          const int64_t room = bytes_to_allocation_end(run_start);
           int32_t len = 1;
           while (i + len < cnt &&
                  static_cast<const char*>(host_blocks[first + i + len]) ==
-                     run_start + len * block_bytes)
+                     run_start + len * block_bytes &&
+                 (len + 1) * block_bytes <= room)
             ++len;
           IEKV_HIP(hipMemcpyAsync(slot + i * block_bytes, run_start, len * block_bytes,
                                   hipMemcpyHostToDevice, copy));
