@@ -118,7 +118,7 @@ def run(gpu, sc, factory):
     return out
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(24))
 def test_random_serving_scenarios_match_a_plain_torch_copier(gpu, seed):
     from iekv.engine.engine import default_copier_factory
 
@@ -136,7 +136,7 @@ def test_the_scenarios_exercise_offload_restore_and_preemption(gpu):
     from iekv.engine.engine import default_copier_factory
 
     restored = tier_held = swapped = recomputed = skipped = 0
-    for seed in range(12):
+    for seed in range(24):
         sc = scenario(seed)
         out = run(gpu, sc, default_copier_factory)
         for side in ("prefill", "decode"):
