@@ -32,6 +32,7 @@
 #include <vector>
 
 #include "iekv.h"
+#include "kv_plan.h"
 
 struct iekv_pool {
   int32_t device;
@@ -46,11 +47,14 @@ struct iekv_pool {
 
 namespace {
 
-constexpr int kThreads = 256;  // four wave64 per workgroup
-constexpr int kXcds = 8;       // MI355X: the dispatcher deals workgroups to 8 XCDs in turn
-constexpr int kXcdGrouped = 4; // order flag: give each XCD a contiguous share of the work
-// Workgroup orders of kv_move (described at the kernel).
-enum Order : int32_t { kArrayMajor = 0, kBlockMajor = 1, kDiagonal = 2 };
+using iekv_plan::kBlockMajor;
+using iekv_plan::kDiagonal;
+using iekv_plan::kMaxGrid;
+using iekv_plan::kThreads;
+using iekv_plan::kXcdGrouped;
+using iekv_plan::MovePlan;
+using iekv_plan::Place;
+using iekv_plan::place_at;
 constexpr int kMaxRun = 64;    // block ids staged in LDS per workgroup
 constexpr int64_t kMaxTileBytes = int64_t(1) << 30;
 
@@ -96,7 +100,7 @@ std::atomic<int> g_pack_order{0};
 // Bytes each workgroup moves: a tile larger than this splits into a
 // power-of-two number of chunks of at least this size, one workgroup each; a
 // smaller one is moved together with the same block's tiles in the next
-// arrays, up to this size per workgroup (tile_group).
+// arrays, up to this size per workgroup (iekv_plan::tile_group).
 // Measured on MI355X (one box, all five benchmark workloads, 4 KiB against
 // 8 KiB): on 32 KiB tiles 4 KiB gains 2-6% on pack, unpack and pack->unpack
 // and ties on the direct copy; the prefix-sharing workload gains 2-6% on every
@@ -187,56 +191,8 @@ __device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
   }
 }
 
-// One workgroup per (array a, run of list entries [first, first+count), chunk
-// p of each tile). A tile of tile_vecs vectors splits into `parts` chunks of
-// tile_vecs / parts vectors; the workgroup moves chunk p of every tile in its
-// run. The order in which workgroups take (array, run) pairs decides which
-// tiles are in flight together. With u the pair's position in that order:
-//   kArrayMajor  u = run * n_arrays + a: the 2L tiles of one block; their
-//                addresses differ by multiples of the array stride;
-//   kBlockMajor  u = a * runs + run: random blocks of one array;
-//   kDiagonal    as array-major, but array a takes run (run + a) mod runs, so
-//                the tiles in flight span 2L arrays AND 2L different blocks.
-// The chunks of one tile are consecutive: position w = u * parts + p.
-// Plain orders take w = blockIdx.x. The dispatcher deals consecutive
-// workgroups to the kXcds XCDs in turn, so with the kXcdGrouped flag set,
-// workgroup i (on XCD i mod kXcds) takes position w = start(XCD) + i / kXcds
-// instead: each XCD walks one contiguous share of the order (with
-// kBlockMajor, its own eighth of the arrays). Every order covers each
-// (array, run, chunk) triple exactly once.
-
-// Position of workgroup `i` of `grid` when each XCD takes a contiguous share:
-// XCD x receives workgroups x, x + kXcds, ...; the first `grid % kXcds` XCDs
-// receive one more than the rest. A bijection on [0, grid).
-__device__ __forceinline__ int xcd_grouped(int i, int grid) {
-  const int q = grid / kXcds, rem = grid % kXcds;
-  const int x = i % kXcds;
-  return x * q + min(x, rem) + i / kXcds;
-}
-
-// This workgroup's (array, run, chunk) in the order described above.
-struct Place {
-  int a, r, p;
-};
-
-__device__ __forceinline__ Place place_of(int32_t n_arrays, int32_t runs, int32_t parts,
-                                          int32_t order) {
-  const int w = (order & kXcdGrouped) ? xcd_grouped(blockIdx.x, gridDim.x) : blockIdx.x;
-  const int base_order = order & ~kXcdGrouped;
-  Place pl;
-  pl.p = w % parts;
-  const int u = w / parts;
-  if (base_order == kBlockMajor) {
-    pl.a = u / runs;
-    pl.r = u % runs;
-  } else {
-    pl.a = u % n_arrays;
-    pl.r = u / n_arrays;
-    if (base_order == kDiagonal)
-      pl.r = static_cast<int>((static_cast<int64_t>(pl.r) + pl.a) % runs);
-  }
-  return pl;
-}
+// Workgroups take (array unit, run of list entries, chunk) triples in the
+// order iekv_plan::place_at describes (kv_plan.h).
 
 // Move chunk p of list entry `entry` of array a: from pool tile src_id (or the
 // staging image of the entry) to pool tile dst_id (or the staging image).
@@ -346,7 +302,8 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
         int32_t order) {
   __shared__ int32_t s_src[kMaxRun];
   __shared__ int32_t s_dst[kMaxRun];
-  const Place pl = place_of((n_arrays + group - 1) / group, runs, parts, order);
+  const Place pl = place_at(blockIdx.x, gridDim.x, (n_arrays + group - 1) / group, runs, parts,
+                            order);
   const int first = pl.r * run;
   if (run == 1) {
     move_unit<V, U, NT, SRC_POOL, DST_POOL>(
@@ -381,7 +338,8 @@ kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
                char* __restrict__ dst_stage, InlineIds ids, int32_t id_base, int32_t dst_off,
                int32_t tile_vecs, int32_t n_arrays, int32_t runs, int32_t parts,
                int32_t group, int32_t order) {
-  const Place pl = place_of((n_arrays + group - 1) / group, runs, parts, order);
+  const Place pl = place_at(blockIdx.x, gridDim.x, (n_arrays + group - 1) / group, runs, parts,
+                            order);
   const int i = id_base + pl.r;
   move_unit<V, U, NT, SRC_POOL, DST_POOL>(
       src, dst, src_stage, dst_stage, SRC_POOL ? ids.v[i] : 0, DST_POOL ? ids.v[dst_off + i] : 0,
@@ -537,85 +495,24 @@ class DeviceGuard {
   bool switched_ = false;
 };
 
-// Blocks per workgroup when the caller has not fixed it: one tile per
-// workgroup, the fastest shape measured for every tile size the workloads use
-// (more, smaller workgroups balance the tail of each launch better than runs
-// of several tiles do).
-int auto_run(int64_t /*tile_bytes*/) { return 1; }
-
-// Chunks per tile for a requested chunk size: the largest power of two that
-// divides the tile's vector count and leaves chunks of at least chunk_bytes
-// (1 when chunk_bytes is 0 or the tile is no larger than the chunk).
-int chunk_parts(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes) {
-  if (chunk_bytes <= 0) return 1;
-  int parts = 1;
-  while (tile_vecs % (2 * parts) == 0 &&
-         (tile_vecs / (2 * parts)) * vec_bytes >= chunk_bytes)
-    parts *= 2;
-  return parts;
-}
-
-// Tiles per workgroup for tiles smaller than the chunk size: chunk_bytes /
-// tile bytes tiles of one block in consecutive arrays (at most n_arrays), when
-// a tile's vector count divides the workgroup's lanes; 1 otherwise. Measured
-// on MI355X on one rank's share of the 70B-share workload at tp=8 (2 KiB
-// tiles, 160 arrays): two tiles per workgroup (4 KiB chunks) raised the
-// per-request direct copy from 4.17 to 5.76 TB/s and pack -> unpack from 4.34
-// to 6.15 TB/s; groups of 8 and 16 KiB were no faster.
-int tile_group(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes, int32_t n_arrays) {
-  if (chunk_bytes <= 0 || tile_vecs * vec_bytes >= chunk_bytes || kThreads % tile_vecs) return 1;
-  return static_cast<int>(std::min<int64_t>(chunk_bytes / (tile_vecs * vec_bytes), n_arrays));
-}
-
-// A dispatch holds at most 2^32 - 1 work-items, so one launch takes at most
-// this many workgroups; larger moves are split over several launches.
-constexpr int64_t kMaxGrid = static_cast<int64_t>(UINT32_MAX) / kThreads;
-
-// Launch shape of one move: blocks per run, chunks per tile, tiles per
-// workgroup (group; then `units` array groups), vector width, vectors per
-// lane per workgroup, workgroup order, and how many runs one launch takes.
-struct MovePlan {
-  int run = 1;
-  int parts = 1;
-  int group = 1;
-  int32_t units = 0;
-  int vec = 16;
-  int lane_vecs = 1;
-  int32_t tile_vecs = 0;
-  int32_t order = 0;
-  int64_t total_runs = 0;
-  int64_t runs_per_launch = 0;
-};
-
+// The launch shape of one move under the current settings (kv_plan.h).
 int plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
               bool pool_writing, bool single_blocks, MovePlan* pl) {
-  const int run_setting = g_run.load();
-  pl->run = single_blocks ? 1 : (run_setting > 0 ? run_setting : auto_run(tile_bytes));
-  pl->vec = 16;
-  for (int a = 16; a > align; a >>= 1) pl->vec = a >> 1;
-  const int64_t tile_vecs = tile_bytes / pl->vec;
-  if (tile_vecs > INT32_MAX)
-    return set_error(IEKV_ERR_INVALID, "tile of %lld bytes is too large",
-                     static_cast<long long>(tile_bytes));
-  // Runs of several tiles keep whole tiles per workgroup; single-tile
-  // workgroups split each tile into chunks, halving the split while a launch
-  // would not fit the dispatch limit.
-  pl->parts = pl->run == 1 ? chunk_parts(tile_vecs, pl->vec, g_chunk.load()) : 1;
-  while (pl->parts > 1 && static_cast<int64_t>(n_arrays) * pl->parts > kMaxGrid) pl->parts /= 2;
-  if (static_cast<int64_t>(n_arrays) * pl->parts > kMaxGrid)
-    return set_error(IEKV_ERR_INVALID, "%d arrays exceed the grid limit", n_arrays);
-  pl->total_runs = (static_cast<int64_t>(n_blocks) + pl->run - 1) / pl->run;
-  while (pl->parts > 1 && pl->total_runs * n_arrays * pl->parts > kMaxGrid) pl->parts /= 2;
-  pl->group = pl->run == 1 && pl->parts == 1
-                  ? tile_group(tile_vecs, pl->vec, g_chunk.load(), n_arrays) : 1;
-  pl->units = (n_arrays + pl->group - 1) / pl->group;
-  pl->lane_vecs = static_cast<int>(std::min<int64_t>(
-      (tile_vecs * pl->group / pl->parts + kThreads - 1) / kThreads, 16));
-  pl->tile_vecs = static_cast<int32_t>(tile_vecs);
-  pl->order = pool_writing ? g_order.load() : g_pack_order.load();
-  pl->runs_per_launch =
-      std::min<int64_t>(pl->total_runs, kMaxGrid / (int64_t(pl->units) * pl->parts));
-  return IEKV_OK;
+  iekv_plan::Settings settings;
+  settings.run = g_run.load();
+  settings.chunk_bytes = g_chunk.load();
+  settings.order = g_order.load();
+  settings.pack_order = g_pack_order.load();
+  switch (iekv_plan::plan_move(n_blocks, tile_bytes, n_arrays, align, pool_writing,
+                               single_blocks, settings, pl)) {
+    case iekv_plan::kTileTooLarge:
+      return set_error(IEKV_ERR_INVALID, "tile of %lld bytes is too large",
+                       static_cast<long long>(tile_bytes));
+    case iekv_plan::kTooManyArrays:
+      return set_error(IEKV_ERR_INVALID, "%d arrays exceed the grid limit", n_arrays);
+    default:
+      return IEKV_OK;
+  }
 }
 
 // One dispatch; while a timing session is open it carries a start/stop event

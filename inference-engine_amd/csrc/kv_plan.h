@@ -1,0 +1,163 @@
+// kv_plan.h — launch planning of the kv_move kernels in kv_handoff.hip: which
+// workgroup moves which (array, list entry, chunk of a tile), and how one move
+// is cut into launches. Plain functions for the host and for device code, so
+// the CPU tests can check them over many shapes without a GPU.
+#ifndef IEKV_KV_PLAN_H_
+#define IEKV_KV_PLAN_H_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace iekv_plan {
+
+constexpr int kThreads = 256;   // four wave64 per workgroup
+constexpr int kXcds = 8;        // MI355X: the dispatcher deals workgroups to 8 XCDs in turn
+constexpr int kXcdGrouped = 4;  // order flag: give each XCD a contiguous share of the work
+enum Order : int32_t { kArrayMajor = 0, kBlockMajor = 1, kDiagonal = 2 };
+
+// A dispatch holds at most 2^32 - 1 work-items, so one launch takes at most
+// this many workgroups; larger moves are split over several launches.
+constexpr int64_t kMaxGrid = static_cast<int64_t>(UINT32_MAX) / kThreads;
+
+// One workgroup per (unit a, run of list entries, chunk p of each tile). A unit
+// is one array, or with tile groups `group` consecutive arrays. A tile of
+// tile_vecs vectors splits into `parts` chunks of tile_vecs / parts vectors;
+// the workgroup moves chunk p of every tile in its run. The order in which
+// workgroups take (unit, run) pairs decides which tiles are in flight
+// together. With u the pair's position in that order:
+//   kArrayMajor  u = run * n_units + a: the 2L tiles of one block; their
+//                addresses differ by multiples of the array stride;
+//   kBlockMajor  u = a * runs + run: random blocks of one array;
+//   kDiagonal    as array-major, but unit a takes run (run + a) mod runs, so
+//                the tiles in flight span 2L arrays AND 2L different blocks.
+// The chunks of one tile are consecutive: position w = u * parts + p.
+// Plain orders take w = the workgroup index. The dispatcher deals consecutive
+// workgroups to the kXcds XCDs in turn, so with the kXcdGrouped flag set,
+// workgroup i (on XCD i mod kXcds) takes position w = start(XCD) + i / kXcds
+// instead: each XCD walks one contiguous share of the order (with
+// kBlockMajor, its own eighth of the arrays). Every order covers each
+// (unit, run, chunk) triple exactly once.
+
+// Position of workgroup `i` of `grid` when each XCD takes a contiguous share:
+// XCD x receives workgroups x, x + kXcds, ...; the first `grid % kXcds` XCDs
+// receive one more than the rest. A bijection on [0, grid).
+__host__ __device__ inline int xcd_grouped(int i, int grid) {
+  const int q = grid / kXcds, rem = grid % kXcds;
+  const int x = i % kXcds;
+  return x * q + (x < rem ? x : rem) + i / kXcds;
+}
+
+struct Place {
+  int a, r, p;  // unit, run, chunk
+};
+
+// The (unit, run, chunk) of workgroup `i` of a grid of n_units * runs * parts.
+__host__ __device__ inline Place place_at(int i, int grid, int32_t n_units, int32_t runs,
+                                          int32_t parts, int32_t order) {
+  const int w = (order & kXcdGrouped) ? xcd_grouped(i, grid) : i;
+  const int base_order = order & ~kXcdGrouped;
+  Place pl;
+  pl.p = w % parts;
+  const int u = w / parts;
+  if (base_order == kBlockMajor) {
+    pl.a = u / runs;
+    pl.r = u % runs;
+  } else {
+    pl.a = u % n_units;
+    pl.r = u / n_units;
+    if (base_order == kDiagonal)
+      pl.r = static_cast<int>((static_cast<int64_t>(pl.r) + pl.a) % runs);
+  }
+  return pl;
+}
+
+// Chunks per tile for a requested chunk size: the largest power of two that
+// divides the tile's vector count and leaves chunks of at least chunk_bytes
+// (1 when chunk_bytes is 0 or the tile is no larger than the chunk).
+inline int chunk_parts(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes) {
+  if (chunk_bytes <= 0) return 1;
+  int parts = 1;
+  while (tile_vecs % (2 * parts) == 0 && (tile_vecs / (2 * parts)) * vec_bytes >= chunk_bytes)
+    parts *= 2;
+  return parts;
+}
+
+// Tiles per workgroup for tiles smaller than the chunk size: chunk_bytes /
+// tile bytes tiles of one block in consecutive arrays (at most n_arrays), when
+// a tile's vector count divides the workgroup's lanes; 1 otherwise. Measured
+// on MI355X on one rank's share of the 70B-share workload at tp=8 (2 KiB
+// tiles, 160 arrays): two tiles per workgroup (4 KiB chunks) raised the
+// per-request direct copy from 4.17 to 5.76 TB/s and pack -> unpack from 4.34
+// to 6.15 TB/s; groups of 8 and 16 KiB were no faster.
+inline int tile_group(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes, int32_t n_arrays) {
+  if (chunk_bytes <= 0 || tile_vecs * vec_bytes >= chunk_bytes || kThreads % tile_vecs) return 1;
+  const int64_t group = chunk_bytes / (tile_vecs * vec_bytes);
+  return static_cast<int>(group < n_arrays ? group : n_arrays);
+}
+
+// The launch-shape settings a plan reads (iekv_set_launch).
+struct Settings {
+  int run = 0;               // blocks per workgroup run; 0 = automatic (one)
+  int64_t chunk_bytes = 0;   // bytes per workgroup (see chunk_parts, tile_group)
+  int32_t order = 0;         // order of launches that write a pool
+  int32_t pack_order = 0;    // order of launches that write a staging buffer
+};
+
+// Launch shape of one move: blocks per run, chunks per tile, tiles per
+// workgroup (group; then `units` array groups), vector width, vectors per
+// lane per workgroup, workgroup order, and how many runs one launch takes.
+struct MovePlan {
+  int run = 1;
+  int parts = 1;
+  int group = 1;
+  int32_t units = 0;
+  int vec = 16;
+  int lane_vecs = 1;
+  int32_t tile_vecs = 0;
+  int32_t order = 0;
+  int64_t total_runs = 0;
+  int64_t runs_per_launch = 0;
+};
+
+enum Status { kPlanned = 0, kTileTooLarge = 1, kTooManyArrays = 2 };
+
+// The shape of a move of n_blocks list entries of n_arrays tiles of
+// tile_bytes each, whose addresses are all multiples of `align` (a power of
+// two <= 16). `single_blocks` forces one block per workgroup (the kernel with
+// ids in its arguments). Runs of several tiles keep whole tiles per
+// workgroup; single-tile workgroups split each tile into chunks, halving the
+// split while a launch would not fit the dispatch limit, or group small
+// tiles. A launch takes runs_per_launch runs: the grid of one launch is at
+// most runs_per_launch * units * parts <= kMaxGrid workgroups.
+inline Status plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
+                        bool pool_writing, bool single_blocks, const Settings& s,
+                        MovePlan* pl) {
+  // One block per workgroup unless set otherwise: the fastest shape measured
+  // for every tile size the workloads use (more, smaller workgroups balance
+  // the tail of each launch better than runs of several tiles do).
+  pl->run = single_blocks ? 1 : (s.run > 0 ? s.run : 1);
+  pl->vec = 16;
+  for (int a = 16; a > align; a >>= 1) pl->vec = a >> 1;
+  const int64_t tile_vecs = tile_bytes / pl->vec;
+  if (tile_vecs > INT32_MAX) return kTileTooLarge;
+  pl->parts = pl->run == 1 ? chunk_parts(tile_vecs, pl->vec, s.chunk_bytes) : 1;
+  while (pl->parts > 1 && static_cast<int64_t>(n_arrays) * pl->parts > kMaxGrid) pl->parts /= 2;
+  if (static_cast<int64_t>(n_arrays) * pl->parts > kMaxGrid) return kTooManyArrays;
+  pl->total_runs = (static_cast<int64_t>(n_blocks) + pl->run - 1) / pl->run;
+  while (pl->parts > 1 && pl->total_runs * n_arrays * pl->parts > kMaxGrid) pl->parts /= 2;
+  pl->group = pl->run == 1 && pl->parts == 1
+                  ? tile_group(tile_vecs, pl->vec, s.chunk_bytes, n_arrays) : 1;
+  pl->units = (n_arrays + pl->group - 1) / pl->group;
+  const int64_t lane_vecs = (tile_vecs * pl->group / pl->parts + kThreads - 1) / kThreads;
+  pl->lane_vecs = static_cast<int>(lane_vecs < 16 ? lane_vecs : 16);
+  pl->tile_vecs = static_cast<int32_t>(tile_vecs);
+  pl->order = pool_writing ? s.order : s.pack_order;
+  const int64_t fit = kMaxGrid / (static_cast<int64_t>(pl->units) * pl->parts);
+  pl->runs_per_launch = pl->total_runs < fit ? pl->total_runs : fit;
+  return kPlanned;
+}
+
+}  // namespace iekv_plan
+
+#endif  // IEKV_KV_PLAN_H_
