@@ -657,10 +657,17 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    from iekv import workloads
+
+    try:
+        w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
+    except ValueError as err:
+        print(f"bench.py: {err}", file=sys.stderr)
+        return 2
+
     import torch
 
     from iekv import _native
-    from iekv import workloads
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -669,7 +676,6 @@ def main() -> int:
     _native.lib()
     if args.launch:
         _native.set_launch(*[int(x) for x in args.launch.split(",")])
-    w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
     log(f"[bench] {w.name}: {w.num_requests} requests, {w.num_blocks} blocks, "
         f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B")
     legs = Legs(w, device, args.seed, "separate" if args.separate_pools else "paired")

@@ -1,4 +1,4 @@
-"""bench.py's command-line refusals (CPU): both happen before any GPU is touched."""
+"""bench.py's command-line refusals (CPU): each happens before any GPU is touched."""
 from __future__ import annotations
 
 import subprocess
@@ -13,6 +13,9 @@ ROOT = Path(__file__).resolve().parents[1]
 @pytest.mark.parametrize("args,message", [
     (["--gpus", "2"], "measures one GPU"),
     (["--legs", "write_kv,gather_context"], "needs one handoff leg"),
+    (["--config", "cfg2", "--tp", "4"], "does not divide"),
+    (["--config", "cfg9"], "unknown workload"),
+    (["--config", "cfg5", "--slack", "3"], "fixed pool sizes"),
 ])
 def test_the_bench_refuses_before_touching_a_gpu(args, message):
     out = subprocess.run([sys.executable, "bench.py", *args], cwd=ROOT, capture_output=True,
