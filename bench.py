@@ -370,6 +370,35 @@ class Legs:
             torch.cuda.synchronize()
             d2h.append(a.elapsed_time(b))
             h2d.append(b.elapsed_time(c))
+        # The same pipelines called once per block, as the reference offloads one
+        # block per eviction and restores one per tier hit (ie/core/block_manager.py:82,
+        # 159-162), on a bounded sample of the blocks.
+        k = min(n, 1024)
+        bb = self.w.shape.block_bytes
+
+        def offload_each():
+            for i in range(k):
+                _native.call("iekv_offload", self.src.native.handle,
+                             self.src_all[i:].data_ptr(), 1, host.data_ptr() + i * bb, bb,
+                             staging.data_ptr(), staging.numel(), h, side.cuda_stream)
+
+        def restore_each():
+            for i in range(k):
+                _native.call("iekv_restore", self.dst.native.handle,
+                             self.dst_all[i:].data_ptr(), 1, host.data_ptr() + i * bb, bb,
+                             staging.data_ptr(), staging.numel(), h, side.cuda_stream)
+
+        offload_each()
+        restore_each()
+        torch.cuda.synchronize()
+        a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        a.record(self.stream)
+        offload_each()
+        b.record(self.stream)
+        restore_each()
+        c.record(self.stream)
+        torch.cuda.synchronize()
+        each_d2h, each_h2d = a.elapsed_time(b), b.elapsed_time(c)
         del host
         d2h_ms, h2d_ms = statistics.median(d2h), statistics.median(h2d)
         out = {"pinned_GB": round(P / 1e9, 2), "pin_alloc_s": round(pin_s, 2),
@@ -377,10 +406,18 @@ class Legs:
                "d2h_GBps": round(P / (d2h_ms * 1e-3) / 1e9, 2),
                "h2d_GBps": round(P / (h2d_ms * 1e-3) / 1e9, 2),
                "roundtrip_ms": round(d2h_ms + h2d_ms, 2),
-               "bound": "host link (PCIe Gen5 x16, 64 GB/s per direction theoretical)"}
+               "bound": "host link (PCIe Gen5 x16, 64 GB/s per direction theoretical)",
+               "one_call_per_block": {
+                   "blocks": k, "block_bytes": bb,
+                   "d2h_GBps": round(k * bb / (each_d2h * 1e-3) / 1e9, 2),
+                   "h2d_GBps": round(k * bb / (each_h2d * 1e-3) / 1e9, 2),
+                   "d2h_us_per_block": round(1000 * each_d2h / k, 2),
+                   "h2d_us_per_block": round(1000 * each_h2d / k, 2)}}
         log(f"[bench] host_roundtrip  {P / 1e9:.2f} GB pinned ({pin_s:.1f} s to pin): "
             f"D2H {out['d2h_GBps']} GB/s, H2D {out['h2d_GBps']} GB/s, "
-            f"round trip {out['roundtrip_ms']} ms")
+            f"round trip {out['roundtrip_ms']} ms; one call per block ({k} blocks): "
+            f"D2H {out['one_call_per_block']['d2h_GBps']} GB/s, "
+            f"H2D {out['one_call_per_block']['h2d_GBps']} GB/s")
         return out
 
     def verify(self) -> bool:
