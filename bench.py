@@ -382,11 +382,16 @@ class Legs:
                              self.src_all[i:].data_ptr(), 1, host.data_ptr() + i * bb, bb,
                              staging.data_ptr(), staging.numel(), h, side.cuda_stream)
 
+        # As HipSlotCopier does, a block small enough to be read by the unpack kernel
+        # itself (IEKV_HOST_DIRECT_MAX_BYTES) is restored with the compute stream as
+        # the copy stream.
+        copy_each = h if bb <= _native.HOST_DIRECT_MAX else side.cuda_stream
+
         def restore_each():
             for i in range(k):
                 _native.call("iekv_restore", self.dst.native.handle,
                              self.dst_all[i:].data_ptr(), 1, host.data_ptr() + i * bb, bb,
-                             staging.data_ptr(), staging.numel(), h, side.cuda_stream)
+                             staging.data_ptr(), staging.numel(), h, copy_each)
 
         offload_each()
         restore_each()

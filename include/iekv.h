@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 7
+#define IEKV_ABI_VERSION 8
 
 enum {
   IEKV_OK = 0,
@@ -142,14 +142,23 @@ int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
                      const int32_t* block_table, int32_t context_len, void* out,
                      int64_t out_bytes, hipStream_t stream);
 
+/* Largest host image iekv_offload and iekv_restore move directly between the
+ * pool and pinned host memory (the move kernel reads or writes the host
+ * buffer), when the host range lies in one pinned allocation mapped for the
+ * device; larger images and pageable memory go through the staging buffer. */
+#define IEKV_HOST_DIRECT_MAX_BYTES (64LL << 20)
+
 /* Offload to host: pack the blocks chunk by chunk into the device staging
  * buffer (two slots when it holds at least two blocks, else one) on
  * `compute`, and copy each packed chunk to host_dst with hipMemcpyAsync on
  * `copy`, so the pack of chunk k+1 overlaps the device-to-host copy of chunk
  * k. host_dst receives the block-major image [n_blocks][2L][T]; it should be
- * pinned host memory for the copies to be asynchronous. On return `compute`
- * is ordered after every copy (so the staging buffer and host_dst are free /
- * complete once `compute` reaches that point). `copy` may equal `compute`.
+ * pinned host memory for the copies to be asynchronous. An image of at most
+ * IEKV_HOST_DIRECT_MAX_BYTES whose host range lies in one pinned allocation
+ * mapped for the device skips the staging buffer: the pack kernel writes
+ * host_dst itself, on `compute`. On return `compute` is ordered after every copy (so the staging
+ * buffer and host_dst are free / complete once `compute` reaches that point).
+ * `copy` may equal `compute`.
  * Replaces: the payload read of the offload hook,
  * `tier.admit(hash, tokens, copier.read_block(id))` (ie/core/block_manager.py:82),
  * batched over many blocks. */
@@ -158,9 +167,12 @@ int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
                  hipStream_t compute, hipStream_t copy);
 
 /* Restore from host: hipMemcpyAsync chunk k of host_src into a staging slot on
- * `copy` while `compute` unpacks chunk k-1, then unpack onto dst_ids. On
- * return `copy` is ordered after the last unpack, so the staging buffer may be
- * reused by later work on either stream.
+ * `copy` while `compute` unpacks chunk k-1, then unpack onto dst_ids. An image
+ * of at most IEKV_HOST_DIRECT_MAX_BYTES whose host range lies in one pinned
+ * allocation mapped for the device skips the staging buffer: the unpack kernel
+ * reads host_src itself, on `compute`. On return `copy` is ordered after the last unpack, so
+ * the staging buffer and host_src may be reused by later work on either
+ * stream.
  * Replaces: the restore write of a tier hit, `copier.write_block(block.id,
  * entry[1])` (ie/core/block_manager.py:159-162), batched over many blocks. */
 int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,

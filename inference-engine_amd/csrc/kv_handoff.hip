@@ -630,6 +630,33 @@ int64_t bytes_to_allocation_end(const char* p) {
   return static_cast<int64_t>(static_cast<const char*>(base) + size - p);
 }
 
+// Host transfers of at most this many bytes skip the staging buffer when the
+// host range lies in one pinned allocation mapped for the device: the move
+// kernel writes (offload) or reads (restore) the host buffer itself over the
+// host link. Measured on MI355X against the staged pipelines, one call per
+// request: one 2 MiB block offloads in 40 us instead of 525 us and restores in
+// 52 us instead of 333 us; 64 blocks of 32 KiB move at 53 GB/s instead of
+// 7 GB/s; at 16.8 MB both reach about 50 GB/s, and from 134 MB on the staged
+// pipelines are 3-5% faster (55-56 against 53-54 GB/s).
+constexpr int64_t kZeroCopyMaxBytes = IEKV_HOST_DIRECT_MAX_BYTES;
+
+// The device address of the host range [p, p + bytes) when it lies in one
+// pinned allocation mapped for the device (HIP gives a pinned host pointer's
+// device address through hipPointerGetAttributes), else nullptr: pageable or
+// unknown memory, or a range running past its allocation. Failed lookups are
+// cleared from HIP's last error.
+char* device_view_of_host(const void* p, int64_t bytes) {
+  hipPointerAttribute_t attr{};
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (attr.type != hipMemoryTypeHost || !attr.devicePointer || !attr.hostPointer) return nullptr;
+  if (bytes_to_allocation_end(static_cast<const char*>(p)) < bytes) return nullptr;
+  return static_cast<char*>(attr.devicePointer) +
+         (static_cast<const char*>(p) - static_cast<const char*>(attr.hostPointer));
+}
+
 // A small set of events that lives for one pipeline call.
 class Events {
  public:
@@ -1033,6 +1060,13 @@ int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  if (need <= kZeroCopyMaxBytes) {
+    if (char* mapped = device_view_of_host(host_dst, need)) {
+      const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
+      return launch_move<true, false>(src, nullptr, nullptr, mapped, src_ids, nullptr, n_blocks,
+                                      src->tile_bytes, src->n_arrays, zc_align, compute);
+    }
+  }
 
   int n_slots;
   int64_t slot_blocks;
@@ -1083,6 +1117,25 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   if (need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
   if ((rc = check_buffer(host_src, host_bytes, need, "host"))) return rc;
   const int64_t block_bytes = image_bytes(dst, 1);
+  if (n_blocks > 0 && need <= kZeroCopyMaxBytes) {
+    if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
+    DeviceGuard guard(dst->device);
+    if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+    if (const char* mapped = device_view_of_host(host_src, need)) {
+      const int zc_align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
+      if ((rc = launch_move<false, true>(nullptr, dst, mapped, nullptr, nullptr, dst_ids, n_blocks,
+                                         dst->tile_bytes, dst->n_arrays, zc_align, compute)))
+        return rc;
+      // As after the staged pipeline, `copy` is ordered after the last unpack.
+      if (copy != compute) {
+        Events done;
+        if ((rc = done.create(1))) return rc;
+        IEKV_HIP(hipEventRecord(done[0], compute));
+        IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
+      }
+      return IEKV_OK;
+    }
+  }
   const char* host = static_cast<const char*>(host_src);
   return restore_pipeline(
       dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,

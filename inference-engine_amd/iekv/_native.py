@@ -12,9 +12,10 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most ids a host-id call takes
+HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
 
 IEKV_OK = 0
 IEKV_ERR_INVALID = -1

@@ -443,7 +443,10 @@ class HipSlotCopier:
         stream = torch.cuda.current_stream(self.device)
         if packed.on_host:
             staging = self._host_staging(n)
-            copy = self.copy_stream()
+            # Small pinned images are read by the unpack kernel itself on the compute
+            # stream (IEKV_HOST_DIRECT_MAX_BYTES); passing that stream as the copy
+            # stream spares the call a cross-stream hand-off it would not use.
+            copy = stream if packed.nbytes <= _native.HOST_DIRECT_MAX else self.copy_stream()
             _native.call("iekv_restore", self.pool.native.handle, ids.on_device().data_ptr(), n,
                          packed.data.data_ptr(), packed.nbytes, staging.data_ptr(),
                          staging.numel(), stream.cuda_stream, copy.cuda_stream)

@@ -474,8 +474,12 @@ def test_single_block_protocol_and_reference_payload_structure(gpu):
     assert src.blocks_read == 1 and dst.blocks_written == 3
 
 
+@pytest.mark.parametrize("pinned", [True, False], ids=["pinned", "pageable"])
 @pytest.mark.parametrize("staging_blocks", [1, 2, 5, 64])
-def test_host_offload_and_restore_pipelines(gpu, staging_blocks):
+def test_host_offload_and_restore_pipelines(gpu, staging_blocks, pinned):
+    """Offload then restore through host memory. Pinned host buffers of at most
+    64 MiB are written and read by the move kernel itself; pageable ones go
+    through the staged pipelines (1 to 23 staging chunks)."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -490,7 +494,7 @@ def test_host_offload_and_restore_pipelines(gpu, staging_blocks):
     block = src.pool.block_bytes
     staging = torch.empty(staging_blocks * block, dtype=torch.uint8, device=gpu)
     host = torch.empty((23, src.pool.n_arrays, src.pool.tile_bytes), dtype=torch.uint8,
-                       pin_memory=True)
+                       pin_memory=pinned)
     ids = src.pool.block_ids(src_ids)
     stream = torch.cuda.current_stream()
     side = torch.cuda.Stream()
@@ -505,6 +509,44 @@ def test_host_offload_and_restore_pipelines(gpu, staging_blocks):
                  host.numel(), staging.data_ptr(), staging.numel(), stream.cuda_stream,
                  side.cuda_stream)
     torch.cuda.synchronize()
+    for d, p in zip(dst_ids, payloads):
+        dst_o.write_block(d, p)
+    assert_pool_equals(dk, dv, dst_o)
+
+
+@pytest.mark.parametrize("blocks,offset", [(72, 0), (16, 4096), (1, 0)],
+                         ids=["72MiB-staged", "16MiB-interior", "1MiB"])
+def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, offset):
+    """1 MiB blocks to and from pinned host memory: 72 blocks exceed the 64 MiB
+    limit of the direct (kernel-to-host) path and go through the staged
+    pipelines; 16 blocks at an offset inside a larger pinned buffer, and a
+    single block, go direct. Bytes equal the oracle's on the host and back in
+    the pool."""
+    from iekv import _native
+    from iekv.engine.pools import KVPool
+
+    bs, layers, heads, dim = 16, 4, 8, 128     # 1 MiB block images (8 arrays x 128 KiB)
+    sk, sv = allocate(80, bs, layers, heads, dim, torch.bfloat16, gpu, seed=71)
+    dk, dv = allocate(80, bs, layers, heads, dim, torch.bfloat16, gpu, seed=72)
+    src, dst = KVPool(sk, sv, bs), KVPool(dk, dv, bs)
+    rng = np.random.default_rng(73)
+    src_ids, dst_ids = random_tables(rng, 80, 80, blocks)
+    block = src.block_bytes
+    buf = torch.empty(offset + blocks * block + 4096, dtype=torch.uint8, pin_memory=True)
+    host = buf[offset:offset + blocks * block]
+    staging = torch.empty(4 * block, dtype=torch.uint8, device=gpu)
+    stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    _native.call("iekv_offload", src.native.handle, src.block_ids(src_ids).data_ptr(), blocks,
+                 host.data_ptr(), host.numel(), staging.data_ptr(), staging.numel(),
+                 stream.cuda_stream, side.cuda_stream)
+    stream.synchronize()
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    payloads = pack(src_o, src_ids)
+    assert np.array_equal(host.numpy(), packed_image(payloads).reshape(-1))
+    _native.call("iekv_restore", dst.native.handle, dst.block_ids(dst_ids).data_ptr(), blocks,
+                 host.data_ptr(), host.numel(), staging.data_ptr(), staging.numel(),
+                 stream.cuda_stream, side.cuda_stream)
+    side.synchronize()          # the copy stream is ordered after the last unpack
     for d, p in zip(dst_ids, payloads):
         dst_o.write_block(d, p)
     assert_pool_equals(dk, dv, dst_o)

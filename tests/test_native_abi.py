@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 7
+    assert lib.iekv_abi_version() == 8
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -206,7 +206,8 @@ def test_the_header_is_plain_c_and_links_from_c(lib, tmp_path):
         "  if (iekv_copy_direct(0, 0, 0, 0, 1, 0) != IEKV_ERR_INVALID) return 2;\n"
         "  if (iekv_copy_direct_ids(0, 0, 0, 0, IEKV_INLINE_IDS + 1, 0) != IEKV_ERR_INVALID)"
         " return 3;\n"
-        '  printf("%d %s\\n", IEKV_ABI_VERSION, iekv_last_error());\n'
+        '  printf("%d %d %lld %s\\n", IEKV_ABI_VERSION, IEKV_INLINE_IDS,\n'
+        '         (long long)IEKV_HOST_DIRECT_MAX_BYTES, iekv_last_error());\n'
         "  return 0;\n"
         "}\n")
     exe = tmp_path / "abi"
@@ -217,4 +218,7 @@ def test_the_header_is_plain_c_and_links_from_c(lib, tmp_path):
                    check=True, capture_output=True, timeout=120)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0, (out.returncode, out.stdout, out.stderr)
-    assert out.stdout.split()[0] == str(lib.iekv_abi_version())
+    version, inline_ids, direct_max = out.stdout.split()[:3]
+    assert int(version) == lib.iekv_abi_version() == _native.ABI_VERSION
+    assert int(inline_ids) == _native.INLINE_IDS      # the binding mirrors the header
+    assert int(direct_max) == _native.HOST_DIRECT_MAX
