@@ -27,13 +27,16 @@ def checksum(arrays):
     return total
 
 
-@pytest.mark.parametrize("name", ["cfg2", "cfg4", "cfg5", "cfg3"])
+@pytest.mark.parametrize("name", ["cfg2", "cfg4", "cfg5", "cfg3", "cfg5/tp8"])
 def test_full_size_handoff(gpu, name):
+    """cfg5/tp8 is one tensor-parallel rank's share of cfg5: 2 KiB tiles in 160
+    arrays, which the kernels move two to a workgroup."""
     from iekv import workloads
     from iekv.engine.copier import HipSlotCopier
     from iekv.engine.pools import allocate_pool
 
-    w = workloads.make(name)
+    base, _, tp = name.partition("/tp")
+    w = workloads.make(base, tp=int(tp or 1))
     s = w.shape
     print(f"{name}: {w.num_requests} requests, {w.num_blocks} blocks, "
           f"{w.payload_bytes / 1e9:.1f} GB", flush=True)
