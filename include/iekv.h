@@ -179,11 +179,18 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                  const void* host_src, int64_t host_bytes, void* staging, int64_t staging_bytes,
                  hipStream_t compute, hipStream_t copy);
 
+/* Most images iekv_restore_blocks restores directly from pinned host memory
+ * in one launch (their addresses ride in the kernel arguments). */
+#define IEKV_INLINE_IMAGES 128
+
 /* Restore from scattered host images: like iekv_restore, but block i's image
  * ([2L][T] bytes) is read from host_blocks[i], a HOST array of n_blocks host
  * addresses (pinned memory for the copies to be asynchronous). Images that are
- * adjacent in host memory are copied together. On return `copy` is ordered
- * after the last unpack, as for iekv_restore.
+ * adjacent in host memory, within one allocation, are copied together. Up to
+ * IEKV_INLINE_IMAGES images of at most IEKV_HOST_DIRECT_MAX_BYTES in all, each
+ * in pinned host memory mapped for the device, are instead read by one unpack
+ * launch directly, on `compute`. On return `copy` is ordered after the last
+ * unpack, as for iekv_restore.
  * Replaces: the restore loop of a prefix plan's tier hits,
  * `for key in offloaded: ... copier.write_block(block.id, payload)`
  * (ie/core/block_manager.py:159-167), whose payloads the tier took one by one

@@ -346,6 +346,31 @@ kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
       i, pl.a, pl.p, tile_vecs, parts, group, n_arrays);
 }
 
+// Scattered host images restored directly: list entry i's image ([2L][T]
+// bytes, device-visible pinned host memory) starts at images.addr[i] and goes
+// to destination block dst_ids[i]. The addresses ride in the kernel
+// arguments. move_unit addresses entry i's image at stage + i * 2L * T, so
+// shifting the base back by that much points it at images.addr[i].
+struct InlineImages {
+  uint64_t addr[IEKV_INLINE_IMAGES];
+};
+
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+__global__ void __launch_bounds__(kThreads)
+kv_unpack_images(PoolView src, PoolView dst, const char* __restrict__ /*src_stage*/,
+                 char* __restrict__ /*dst_stage*/, InlineImages images,
+                 const int32_t* __restrict__ dst_ids, int32_t tile_vecs, int32_t n_arrays,
+                 int32_t runs, int32_t parts, int32_t group, int32_t order) {
+  static_assert(!SRC_POOL && DST_POOL, "images are restored into a pool");
+  const Place pl = place_at(blockIdx.x, gridDim.x, (n_arrays + group - 1) / group, runs, parts,
+                            order);
+  const int i = pl.r;
+  const uint64_t image_bytes = static_cast<uint64_t>(n_arrays) * tile_vecs * sizeof(V);
+  const char* stage = reinterpret_cast<const char*>(images.addr[i] - i * image_bytes);
+  move_unit<V, U, NT, false, true>(src, dst, stage, nullptr, 0, dst_ids[i], i, pl.a, pl.p,
+                                   tile_vecs, parts, group, n_arrays);
+}
+
 // Row kernels on either side of the handoff. A pool row is one token's
 // H x D values of one array (tile_bytes / block_size bytes); row r of array a
 // lives at base(a) + r * row_bytes, i.e. slot r of the reference's [N*bs, H, D]
@@ -429,6 +454,9 @@ thread_local Profiler g_profiler;
 using MoveKernel = void (*)(PoolView, PoolView, const char*, char*, const int32_t*,
                             const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
                             int32_t, int32_t, int32_t);
+using ImagesKernel = void (*)(PoolView, PoolView, const char*, char*, InlineImages,
+                              const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
+                              int32_t);
 using InlineKernel = void (*)(PoolView, PoolView, const char*, char*, InlineIds, int32_t,
                               int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t);
 
@@ -466,6 +494,10 @@ MoveKernel pick_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_b
 template <bool SP, bool DP>
 InlineKernel pick_inline_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
   IEKV_PICK(kv_move_inline)
+}
+template <bool SP, bool DP>
+ImagesKernel pick_images_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
+  IEKV_PICK(kv_unpack_images)
 }
 #undef IEKV_PICK
 
@@ -583,6 +615,24 @@ int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src
   return IEKV_OK;
 }
 
+// The scattered-image restore in one launch (n_blocks <= IEKV_INLINE_IMAGES).
+int launch_images(const iekv_pool* dp, const InlineImages& images, const int32_t* dst_ids,
+                  int32_t n_blocks, hipStream_t stream) {
+  int align = dp->align;
+  for (int32_t i = 0; i < n_blocks; ++i) align = std::min(align, align_of_ptr(images.addr[i]));
+  MovePlan pl;
+  int rc;
+  if ((rc = plan_move(n_blocks, dp->tile_bytes, dp->n_arrays, align, true, true, &pl))) return rc;
+  // At most IEKV_HOST_DIRECT_MAX_BYTES in chunks of at least 64 bytes: one launch holds them.
+  if (pl.runs_per_launch < n_blocks)
+    return set_error(IEKV_ERR_INVALID, "%d images do not fit one launch", n_blocks);
+  ImagesKernel k = pick_images_kernel<false, true>(align, g_unroll.load(), pl.lane_vecs,
+                                                   g_nontemporal.load() != 0, &pl.vec);
+  const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(n_blocks) * pl.units * pl.parts);
+  return dispatch(k, grid, stream, PoolView{}, view_of(dp), nullptr, nullptr, images, dst_ids,
+                  pl.tile_vecs, dp->n_arrays, n_blocks, pl.parts, pl.group, pl.order);
+}
+
 int row_align(int64_t row_bytes, int pool_align, std::initializer_list<const void*> ptrs) {
   int align = 16;
   while (align > 1 && (row_bytes % align)) align >>= 1;
@@ -655,6 +705,28 @@ char* device_view_of_host(const void* p, int64_t bytes) {
   if (bytes_to_allocation_end(static_cast<const char*>(p)) < bytes) return nullptr;
   return static_cast<char*>(attr.devicePointer) +
          (static_cast<const char*>(p) - static_cast<const char*>(attr.hostPointer));
+}
+
+// Device addresses of n host images of `bytes` each, when every one lies in a
+// pinned allocation mapped for the device (one lookup per allocation: an
+// image inside the range of the previous lookup reuses it). False otherwise.
+bool device_views_of_images(const void* const* images, int32_t n, int64_t bytes,
+                            uint64_t* out) {
+  const char* lo = nullptr;
+  const char* hi = nullptr;
+  int64_t shift = 0;
+  for (int32_t i = 0; i < n; ++i) {
+    const char* p = static_cast<const char*>(images[i]);
+    if (!(lo && p >= lo && p + bytes <= hi)) {
+      char* view = device_view_of_host(p, bytes);
+      if (!view) return false;
+      lo = p;
+      hi = p + bytes_to_allocation_end(p);
+      shift = view - p;
+    }
+    out[i] = reinterpret_cast<uint64_t>(p + shift);
+  }
+  return true;
 }
 
 // A small set of events that lives for one pipeline call.
@@ -1158,6 +1230,24 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
   for (int32_t i = 0; i < n_blocks; ++i)
     if (!host_blocks[i]) return set_error(IEKV_ERR_INVALID, "host block %d address is null", i);
   const int64_t block_bytes = image_bytes(dst, 1);
+  if (n_blocks > 0 && n_blocks <= IEKV_INLINE_IMAGES &&
+      block_bytes * n_blocks <= kZeroCopyMaxBytes) {
+    if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
+    DeviceGuard guard(dst->device);
+    if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+    InlineImages images{};
+    if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
+      if ((rc = launch_images(dst, images, dst_ids, n_blocks, compute))) return rc;
+      // As after the staged pipeline, `copy` is ordered after the last unpack.
+      if (copy != compute) {
+        Events done;
+        if ((rc = done.create(1))) return rc;
+        IEKV_HIP(hipEventRecord(done[0], compute));
+        IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
+      }
+      return IEKV_OK;
+    }
+  }
   return restore_pipeline(
       dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
       [&](char* slot, int64_t first, int32_t cnt) -> int {

@@ -16,6 +16,7 @@ ABI_VERSION = 8
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most ids a host-id call takes
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
+INLINE_IMAGES = 128          # IEKV_INLINE_IMAGES: scattered host images restored in one launch
 
 IEKV_OK = 0
 IEKV_ERR_INVALID = -1

@@ -446,7 +446,8 @@ class HipSlotCopier:
             # Small pinned images are read by the unpack kernel itself on the compute
             # stream (IEKV_HOST_DIRECT_MAX_BYTES); passing that stream as the copy
             # stream spares the call a cross-stream hand-off it would not use.
-            copy = stream if packed.nbytes <= _native.HOST_DIRECT_MAX else self.copy_stream()
+            direct = packed.nbytes <= _native.HOST_DIRECT_MAX and packed.data.is_pinned()
+            copy = stream if direct else self.copy_stream()
             _native.call("iekv_restore", self.pool.native.handle, ids.on_device().data_ptr(), n,
                          packed.data.data_ptr(), packed.nbytes, staging.data_ptr(),
                          staging.numel(), stream.cuda_stream, copy.cuda_stream)
@@ -467,7 +468,11 @@ class HipSlotCopier:
         addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in payloads])
         stream = torch.cuda.current_stream(self.device)
         staging = self._host_staging(n)
-        copy = self.copy_stream()
+        # Few, small pinned images are read by one unpack launch on the compute stream
+        # (IEKV_INLINE_IMAGES, IEKV_HOST_DIRECT_MAX_BYTES): no cross-stream hand-off.
+        direct = (n <= _native.INLINE_IMAGES and n * self.pool.block_bytes <= _native.HOST_DIRECT_MAX
+                  and all(p.packed.data.is_pinned() for p in payloads))
+        copy = stream if direct else self.copy_stream()
         _native.call("iekv_restore_blocks", self.pool.native.handle, ids.on_device().data_ptr(), n,
                      addresses, staging.data_ptr(), staging.numel(), stream.cuda_stream,
                      copy.cuda_stream)

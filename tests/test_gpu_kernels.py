@@ -573,13 +573,16 @@ def test_host_payloads_through_the_copier(gpu):
                           packed_image(pack(oracle_of(sk, sv, bs), [3, 14, 29, 0])))
 
 
+@pytest.mark.parametrize("pinned", [True, False], ids=["pinned", "pageable"])
 @pytest.mark.parametrize("staging_blocks", [1, 2, 3, 64])
-def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_blocks):
+def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_blocks, pinned):
     """Tier entries come from different offload batches: write_blocks gathers
-    their host images (scattered, some adjacent) with one iekv_restore_blocks,
-    through a staging buffer of 1 to 64 blocks (1 to 7 pipeline chunks)."""
+    their host images (scattered, some adjacent) with one iekv_restore_blocks.
+    Pinned images are read by one unpack launch directly; pageable copies of the
+    same buffers go through a staging buffer of 1 to 64 blocks (1 to 7
+    pipeline chunks)."""
     from iekv.engine import copier as copier_mod
-    from iekv.engine.copier import HipSlotCopier
+    from iekv.engine.copier import HipSlotCopier, PackedBlocks
 
     bs = 16
     sk, sv = allocate(40, bs, 3, 2, 32, torch.bfloat16, gpu, seed=26)
@@ -590,6 +593,14 @@ def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_b
     first = src.read_blocks([5, 6, 7, 30])        # one offload batch
     second = src.read_blocks([12, 0, 39])         # another
     single = src.read_block(21)
+    if not pinned:
+        def pageable(packed):
+            packed.synchronize()
+            data = torch.empty(packed.data.shape, dtype=torch.uint8).copy_(packed.data)
+            assert not data.is_pinned()
+            return PackedBlocks(data, packed.num_layers, packed.tile_shape, packed.dtype)
+        first, second = pageable(first), pageable(second)
+        single = pageable(single.packed[single.index:single.index + 1])[0]
     payloads = [second[2], first[0], first[1], single, second[0], first[3], second[1]]
     src_ids = [39, 5, 6, 21, 12, 30, 0]
     dst_ids = [3, 17, 9, 33, 2, 25, 11]
@@ -647,6 +658,29 @@ def test_a_restore_never_merges_copies_across_pinned_allocations(gpu):
                                             host_bytes(dk) + host_bytes(dv))):
         for s, d in zip(src_ids, dst_ids):
             assert np.array_equal(d_arr[d * bs:(d + 1) * bs], s_arr[s * bs:(s + 1) * bs]), (a, s, d)
+
+
+def test_more_scattered_images_than_one_direct_launch_takes(gpu):
+    """130 one-block tier payloads (more than IEKV_INLINE_IMAGES) restore through
+    the staged pipeline in one call, bytes equal to the oracle's."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    bs = 4
+    sk, sv = allocate(140, bs, 1, 1, 32, torch.float32, gpu, seed=81)   # 512 B tiles
+    dk, dv = allocate(140, bs, 1, 1, 32, torch.float32, gpu, seed=82)
+    src = HipSlotCopier(sk, sv, bs, payload_location="host", defer_reads=False)
+    dst = HipSlotCopier(dk, dv, bs)
+    n = _native.INLINE_IMAGES + 2
+    rng = np.random.default_rng(83)
+    src_ids, dst_ids = random_tables(rng, 140, 140, n)
+    payloads = [src.read_blocks([b])[0] for b in src_ids]
+    dst.write_blocks(dst_ids, payloads)
+    assert dst.restore_launches == 1
+    torch.cuda.synchronize()
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    assert_pool_equals(dk, dv, dst_o)
 
 
 def test_a_victim_read_sees_the_bytes_before_a_restore_overwrites_them(gpu):

@@ -206,8 +206,9 @@ def test_the_header_is_plain_c_and_links_from_c(lib, tmp_path):
         "  if (iekv_copy_direct(0, 0, 0, 0, 1, 0) != IEKV_ERR_INVALID) return 2;\n"
         "  if (iekv_copy_direct_ids(0, 0, 0, 0, IEKV_INLINE_IDS + 1, 0) != IEKV_ERR_INVALID)"
         " return 3;\n"
-        '  printf("%d %d %lld %s\\n", IEKV_ABI_VERSION, IEKV_INLINE_IDS,\n'
-        '         (long long)IEKV_HOST_DIRECT_MAX_BYTES, iekv_last_error());\n'
+        '  printf("%d %d %lld %d %s\\n", IEKV_ABI_VERSION, IEKV_INLINE_IDS,\n'
+        '         (long long)IEKV_HOST_DIRECT_MAX_BYTES, IEKV_INLINE_IMAGES,\n'
+        '         iekv_last_error());\n'
         "  return 0;\n"
         "}\n")
     exe = tmp_path / "abi"
@@ -218,7 +219,8 @@ def test_the_header_is_plain_c_and_links_from_c(lib, tmp_path):
                    check=True, capture_output=True, timeout=120)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0, (out.returncode, out.stdout, out.stderr)
-    version, inline_ids, direct_max = out.stdout.split()[:3]
+    version, inline_ids, direct_max, inline_images = out.stdout.split()[:4]
+    assert int(inline_images) == _native.INLINE_IMAGES
     assert int(version) == lib.iekv_abi_version() == _native.ABI_VERSION
     assert int(inline_ids) == _native.INLINE_IDS      # the binding mirrors the header
     assert int(direct_max) == _native.HOST_DIRECT_MAX
