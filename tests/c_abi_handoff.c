@@ -3,8 +3,11 @@
  * with no Python or torch: two pools in one HIP allocation, a direct copy with
  * device ids, the same with host ids (kernel-argument ids), and a pack ->
  * unpack through a staging buffer. Every moved tile and every untouched tile
- * is checked byte for byte on the host. Exit status 0 and "c-abi handoff ok"
- * on success.
+ * is checked byte for byte on the host. Then host offload / restore of the
+ * moved blocks, through pinned memory (hipHostMalloc: the move kernel reads
+ * and writes it directly) and through pageable memory (malloc: the staged
+ * pipelines), each image checked on the host and restored into a cleared
+ * pool. Exit status 0 and "c-abi handoff ok" on success.
  *
  * Built by __graft_entry__.build() with gcc into tests/c_abi_handoff (run by
  * tests/test_gpu_c_abi.py on a GPU).
@@ -128,6 +131,51 @@ int main(void) {
       for (int i = 0; i < TILE; ++i)
         if (host[((size_t)a * BLOCKS + b) * TILE + i] != byte_at(0, a, b, i)) return 6;
 
+  /* Host offload of batch 0's source blocks, then restore onto batch 0's
+   * destination blocks of a cleared destination pool: once through pinned
+   * memory, once through pageable memory. */
+  hipStream_t side;
+  CHECK_HIP(hipStreamCreate(&side));
+  const int64_t image_bytes = (int64_t)MOVED * ARRAYS * TILE;
+  for (int pinned = 1; pinned >= 0; --pinned) {
+    unsigned char* image = NULL;
+    if (pinned) {
+      CHECK_HIP(hipHostMalloc((void**)&image, (size_t)image_bytes, 0));
+    } else {
+      image = (unsigned char*)malloc((size_t)image_bytes);
+      if (!image) return 4;
+    }
+    memset(image, 0, (size_t)image_bytes);
+    CHECK_IEKV(iekv_offload(src, dev_ids, MOVED, image, image_bytes, staging, staging_bytes,
+                            stream, side));
+    CHECK_HIP(hipStreamSynchronize(stream));
+    for (int k = 0; k < MOVED; ++k) /* image k = the 2L tiles of source block s_ids[0][k] */
+      for (int a = 0; a < ARRAYS; ++a)
+        for (int i = 0; i < TILE; ++i)
+          if (image[((size_t)k * ARRAYS + a) * TILE + i] != byte_at(0, a, s_ids[0][k], i))
+            return pinned ? 7 : 8;
+    CHECK_HIP(hipMemset(slab + POOL, 0, POOL));
+    CHECK_IEKV(iekv_restore(dst, dev_ids + MOVED, MOVED, image, image_bytes, staging,
+                            staging_bytes, stream, side));
+    CHECK_HIP(hipStreamSynchronize(side)); /* `side` is ordered after the last unpack */
+    CHECK_HIP(hipMemcpy(host + POOL, slab + POOL, POOL, hipMemcpyDeviceToHost));
+    for (int a = 0; a < ARRAYS; ++a)
+      for (int b = 0; b < BLOCKS; ++b) {
+        const unsigned char* tile = host + POOL + ((size_t)a * BLOCKS + b) * TILE;
+        int from = -1;
+        for (int k = 0; k < MOVED; ++k)
+          if (d_ids[0][k] == b) from = s_ids[0][k];
+        for (int i = 0; i < TILE; ++i)
+          if (tile[i] != (from >= 0 ? byte_at(0, a, from, i) : 0)) return pinned ? 9 : 10;
+      }
+    if (pinned) {
+      CHECK_HIP(hipHostFree(image));
+    } else {
+      free(image);
+    }
+  }
+  CHECK_HIP(hipStreamDestroy(side));
+
   CHECK_IEKV(iekv_pool_destroy(src));
   CHECK_IEKV(iekv_pool_destroy(dst));
   CHECK_HIP(hipFree(staging));
@@ -135,6 +183,7 @@ int main(void) {
   CHECK_HIP(hipFree(slab));
   CHECK_HIP(hipStreamDestroy(stream));
   free(host);
-  printf("c-abi handoff ok: %d blocks x %d tiles of %d B in 4 calls\n", 3 * MOVED, ARRAYS, TILE);
+  printf("c-abi handoff ok: %d blocks x %d tiles of %d B in 4 calls, host round trips pinned "
+         "and pageable\n", 3 * MOVED, ARRAYS, TILE);
   return 0;
 }

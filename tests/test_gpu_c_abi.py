@@ -2,7 +2,9 @@
 
 tests/c_abi_handoff.c (built by __graft_entry__.build() against the in-tree
 libiekv.so) allocates two pools in one HIP allocation, runs a direct copy with
-device ids, one with host ids, and a pack -> unpack, then checks every byte.
+device ids, one with host ids, and a pack -> unpack, then checks every byte; then
+offloads to and restores from host memory, pinned (read and written by the move
+kernel directly) and pageable (the staged pipelines), checking every byte again.
 """
 from __future__ import annotations
 
