@@ -573,14 +573,14 @@ def test_host_payloads_through_the_copier(gpu):
                           packed_image(pack(oracle_of(sk, sv, bs), [3, 14, 29, 0])))
 
 
-@pytest.mark.parametrize("pinned", [True, False], ids=["pinned", "pageable"])
+@pytest.mark.parametrize("memory", ["pinned", "pageable", "mixed"])
 @pytest.mark.parametrize("staging_blocks", [1, 2, 3, 64])
-def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_blocks, pinned):
+def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_blocks, memory):
     """Tier entries come from different offload batches: write_blocks gathers
     their host images (scattered, some adjacent) with one iekv_restore_blocks.
     Pinned images are read by one unpack launch directly; pageable copies of the
-    same buffers go through a staging buffer of 1 to 64 blocks (1 to 7
-    pipeline chunks)."""
+    same buffers, or a mix of pinned and pageable ones, go through a staging
+    buffer of 1 to 64 blocks (1 to 7 pipeline chunks)."""
     from iekv.engine import copier as copier_mod
     from iekv.engine.copier import HipSlotCopier, PackedBlocks
 
@@ -593,13 +593,16 @@ def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_b
     first = src.read_blocks([5, 6, 7, 30])        # one offload batch
     second = src.read_blocks([12, 0, 39])         # another
     single = src.read_block(21)
-    if not pinned:
-        def pageable(packed):
-            packed.synchronize()
-            data = torch.empty(packed.data.shape, dtype=torch.uint8).copy_(packed.data)
-            assert not data.is_pinned()
-            return PackedBlocks(data, packed.num_layers, packed.tile_shape, packed.dtype)
-        first, second = pageable(first), pageable(second)
+    def pageable(packed):
+        packed.synchronize()
+        data = torch.empty(packed.data.shape, dtype=torch.uint8).copy_(packed.data)
+        assert not data.is_pinned()
+        return PackedBlocks(data, packed.num_layers, packed.tile_shape, packed.dtype)
+
+    if memory != "pinned":
+        first = pageable(first)
+    if memory == "pageable":
+        second = pageable(second)
         single = pageable(single.packed[single.index:single.index + 1])[0]
     payloads = [second[2], first[0], first[1], single, second[0], first[3], second[1]]
     src_ids = [39, 5, 6, 21, 12, 30, 0]
