@@ -23,6 +23,9 @@ without NaN codes for fp8). Legs:
   gather_context  the decode side: every request's context gathered from the decode pool
                through its block table (resident prefix included), one iekv_gather_rows
                launch per request and array (read + write of every row)
+  host_roundtrip  every moved block offloaded to pinned host memory with one iekv_offload
+               and restored with one iekv_restore (host-link bound), then the same
+               pipelines called once per block on up to 1,024 blocks
 
 ``value`` is the direct leg's algorithmic read+write bandwidth, 2P / step
 time, in GB/s (P = blocks x 2L x T); the step time comes from two HIP events
