@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 8
+#define IEKV_ABI_VERSION 9
 
 enum {
   IEKV_OK = 0,
@@ -165,6 +165,30 @@ int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
 int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
                  void* host_dst, int64_t host_bytes, void* staging, int64_t staging_bytes,
                  hipStream_t compute, hipStream_t copy);
+
+/* Size of the device staging buffer iekv_offload_static uses (32 MiB), held by
+ * the library on every GPU it runs on until the process ends. */
+#define IEKV_STATIC_STAGING_BYTES (32LL << 20)
+
+/* Allocation-free offload: iekv_offload with the staging buffer taken from a
+ * buffer of IEKV_STATIC_STAGING_BYTES the library holds in each device's
+ * memory (two slots when it holds two block images, else one), and with
+ * HIP events created once per device; the call itself allocates nothing. The
+ * first call on a device sets that device's buffer address and events up.
+ * A block image (2L * T bytes) larger than IEKV_STATIC_STAGING_BYTES is
+ * rejected with IEKV_ERR_CAPACITY before anything is enqueued. Every call on
+ * one device shares that device's buffer and events: calls that overlap on
+ * one device (other host threads, or streams not ordered after the previous
+ * call's `compute`) race. The buffer keeps the last call's bytes; nothing in
+ * it needs to start at zero. Streams, host image and ordering on return as
+ * for iekv_offload.
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate device memory or call allocating routines (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); it runs the
+ * kernels of iekv_offload. */
+int iekv_offload_static(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                        void* host_dst, int64_t host_bytes, hipStream_t compute,
+                        hipStream_t copy);
 
 /* Restore from host: hipMemcpyAsync chunk k of host_src into a staging slot on
  * `copy` while `compute` unpacks chunk k-1, then unpack onto dst_ids. An image

@@ -27,6 +27,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -44,6 +45,12 @@ struct iekv_pool {
   uint64_t* table;  // table mode: device copy of the n_arrays base addresses (else null)
   int32_t align;    // largest power of two <= 16 dividing tile_bytes and every base address
 };
+
+// Staging buffer of iekv_offload_static, the allocation-free offload: every
+// GPU the library runs on holds its own copy from module load until the
+// process ends. Host code passes kernels the address hipGetSymbolAddress
+// reports for the current device, never this name (see static_staging).
+static __device__ __align__(256) unsigned char scratch[IEKV_STATIC_STAGING_BYTES];
 
 namespace {
 
@@ -833,6 +840,132 @@ int check_inline_count(int32_t n_blocks, const int32_t* a, const int32_t* b) {
   return IEKV_OK;
 }
 
+
+// Events of one offload pipeline call: per staging slot, "packed" (recorded on
+// the compute stream after the slot's pack) and "copied" (on the copy stream
+// after its device-to-host copy), plus the entry fence.
+struct OffloadEvents {
+  hipEvent_t packed[2];
+  hipEvent_t copied[2];
+  hipEvent_t fence;
+};
+
+// Arguments of an offload, checked before anything touches the GPU; *need is
+// the host image size.
+int check_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                  const void* host_dst, int64_t host_bytes, int64_t* need) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_ids(src_ids, n_blocks, "source")))
+    return rc;
+  *need = image_bytes(src, n_blocks);
+  if (*need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
+  return check_buffer(host_dst, host_bytes, *need, "host");
+}
+
+// The offload of n_blocks >= 1 checked blocks with src's device current. An
+// image of at most kZeroCopyMaxBytes in one pinned, device-mapped allocation
+// is written by the pack kernel directly. Otherwise chunk k is packed into a
+// staging slot on `compute` while `copy` moves chunk k-1 to the host (two
+// slots when the staging holds two blocks or more, else one). `preset` gives
+// the events to use; without it the call creates its own.
+int run_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, void* host_dst,
+                int64_t need, char* staging, int64_t staging_bytes, hipStream_t compute,
+                hipStream_t copy, const OffloadEvents* preset) {
+  int rc;
+  if (need <= kZeroCopyMaxBytes) {
+    if (char* mapped = device_view_of_host(host_dst, need)) {
+      const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
+      return launch_move<true, false>(src, nullptr, nullptr, mapped, src_ids, nullptr, n_blocks,
+                                      src->tile_bytes, src->n_arrays, zc_align, compute);
+    }
+  }
+  const int64_t block_bytes = image_bytes(src, 1);
+  int n_slots;
+  int64_t slot_blocks;
+  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
+  const int align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  Events own;
+  OffloadEvents ev{};
+  if (preset) {
+    ev = *preset;
+  } else {
+    if ((rc = own.create(2 * n_slots + 1))) return rc;
+    for (int s = 0; s < n_slots; ++s) {
+      ev.packed[s] = own[2 * s];
+      ev.copied[s] = own[2 * s + 1];
+    }
+    ev.fence = own[2 * n_slots];
+  }
+
+  // Entry fence: the copy stream must not read staging before the compute
+  // stream's earlier work on it has finished.
+  IEKV_HIP(hipEventRecord(ev.fence, compute));
+  IEKV_HIP(hipStreamWaitEvent(copy, ev.fence, 0));
+
+  char* host = static_cast<char*>(host_dst);
+  int last = 0;
+  for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
+    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
+    const int s = static_cast<int>(k % n_slots);
+    char* slot = staging + s * slot_blocks * block_bytes;
+    if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(compute, ev.copied[s], 0));
+    if ((rc = launch_move<true, false>(src, nullptr, nullptr, slot, src_ids + first, nullptr,
+                                       cnt, src->tile_bytes, src->n_arrays, align, compute)))
+      return rc;
+    IEKV_HIP(hipEventRecord(ev.packed[s], compute));
+    IEKV_HIP(hipStreamWaitEvent(copy, ev.packed[s], 0));
+    IEKV_HIP(hipMemcpyAsync(host + first * block_bytes, slot, cnt * block_bytes,
+                            hipMemcpyDeviceToHost, copy));
+    IEKV_HIP(hipEventRecord(ev.copied[s], copy));
+    last = s;
+  }
+  // Later compute-stream work (reuse of staging, reads of host_dst after a
+  // sync of `compute`) is ordered after the last device-to-host copy.
+  IEKV_HIP(hipStreamWaitEvent(compute, ev.copied[last], 0));
+  return IEKV_OK;
+}
+
+// The staging of iekv_offload_static on one device: the device address of
+// `scratch` there and the pipeline's events, set up by the first call on
+// that device and kept until the process ends.
+struct StaticStaging {
+  bool ready = false;
+  char* ptr = nullptr;
+  OffloadEvents events{};
+};
+constexpr int kMaxStaticDevices = 64;
+std::mutex g_static_mu;
+StaticStaging g_static[kMaxStaticDevices];
+
+// The static staging of `device`, which must be the current device.
+int static_staging(int device, const StaticStaging** out) {
+  if (device < 0 || device >= kMaxStaticDevices)
+    return set_error(IEKV_ERR_INVALID, "device %d is outside 0..%d", device,
+                     kMaxStaticDevices - 1);
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  StaticStaging& st = g_static[device];
+  if (!st.ready) {
+    // `scratch` names the host-side stand-in of the device array; the address
+    // kernels may use is the one HIP reports for the current device.
+    void* addr = nullptr;
+    IEKV_HIP(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+    if (!addr) return set_error(IEKV_ERR_HIP, "hipGetSymbolAddress gave a null address");
+    hipEvent_t ev[5] = {};
+    for (int i = 0; i < 5; ++i) {
+      const hipError_t e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
+      if (e != hipSuccess) {
+        for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
+        return set_error(IEKV_ERR_HIP, "hipEventCreateWithFlags: %s", hipGetErrorString(e));
+      }
+    }
+    st.events = OffloadEvents{{ev[0], ev[1]}, {ev[2], ev[3]}, ev[4]};
+    st.ptr = static_cast<char*>(addr);
+    st.ready = true;
+  }
+  *out = &st;
+  return IEKV_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1121,61 +1254,38 @@ int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
                  void* host_dst, int64_t host_bytes, void* staging, int64_t staging_bytes,
                  hipStream_t compute, hipStream_t copy) {
   int rc;
-  if ((rc = check_pool(src, "source")) || (rc = check_ids(src_ids, n_blocks, "source")))
-    return rc;
-  const int64_t need = image_bytes(src, n_blocks);
-  if (need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
-  if ((rc = check_buffer(host_dst, host_bytes, need, "host"))) return rc;
-  const int64_t block_bytes = image_bytes(src, 1);
-  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
+  int64_t need = 0;
+  if ((rc = check_offload(src, src_ids, n_blocks, host_dst, host_bytes, &need))) return rc;
+  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? image_bytes(src, 1) : 0,
+                         "staging")))
     return rc;
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
-  if (need <= kZeroCopyMaxBytes) {
-    if (char* mapped = device_view_of_host(host_dst, need)) {
-      const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
-      return launch_move<true, false>(src, nullptr, nullptr, mapped, src_ids, nullptr, n_blocks,
-                                      src->tile_bytes, src->n_arrays, zc_align, compute);
-    }
-  }
+  return run_offload(src, src_ids, n_blocks, host_dst, need, static_cast<char*>(staging),
+                     staging_bytes, compute, copy, nullptr);
+}
 
-  int n_slots;
-  int64_t slot_blocks;
-  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
-  const int align =
-      std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
-  Events packed, copied, fence;
-  if ((rc = packed.create(n_slots)) || (rc = copied.create(n_slots)) || (rc = fence.create(1)))
-    return rc;
-
-  // Entry fence: the copy stream must not read staging before the compute
-  // stream's earlier work on it has finished.
-  IEKV_HIP(hipEventRecord(fence[0], compute));
-  IEKV_HIP(hipStreamWaitEvent(copy, fence[0], 0));
-
-  char* host = static_cast<char*>(host_dst);
-  char* stage = static_cast<char*>(staging);
-  int last = 0;
-  for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
-    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
-    const int s = static_cast<int>(k % n_slots);
-    char* slot = stage + s * slot_blocks * block_bytes;
-    if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(compute, copied[s], 0));
-    if ((rc = launch_move<true, false>(src, nullptr, nullptr, slot, src_ids + first, nullptr,
-                                       cnt, src->tile_bytes, src->n_arrays, align, compute)))
-      return rc;
-    IEKV_HIP(hipEventRecord(packed[s], compute));
-    IEKV_HIP(hipStreamWaitEvent(copy, packed[s], 0));
-    IEKV_HIP(hipMemcpyAsync(host + first * block_bytes, slot, cnt * block_bytes,
-                            hipMemcpyDeviceToHost, copy));
-    IEKV_HIP(hipEventRecord(copied[s], copy));
-    last = s;
-  }
-  // Later compute-stream work (reuse of staging, reads of host_dst after a
-  // sync of `compute`) is ordered after the last device-to-host copy.
-  IEKV_HIP(hipStreamWaitEvent(compute, copied[last], 0));
-  return IEKV_OK;
+int iekv_offload_static(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                        void* host_dst, int64_t host_bytes, hipStream_t compute,
+                        hipStream_t copy) {
+  int rc;
+  int64_t need = 0;
+  if ((rc = check_offload(src, src_ids, n_blocks, host_dst, host_bytes, &need))) return rc;
+  const int64_t block_bytes = image_bytes(src, 1);
+  if (block_bytes > IEKV_STATIC_STAGING_BYTES)
+    return set_error(IEKV_ERR_CAPACITY,
+                     "a block image of %lld bytes exceeds the %lld-byte static staging buffer; "
+                     "use iekv_offload with a staging buffer of at least one block image",
+                     static_cast<long long>(block_bytes),
+                     static_cast<long long>(IEKV_STATIC_STAGING_BYTES));
+  if (n_blocks == 0) return IEKV_OK;
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  const StaticStaging* st = nullptr;
+  if ((rc = static_staging(src->device, &st))) return rc;
+  return run_offload(src, src_ids, n_blocks, host_dst, need, st->ptr, IEKV_STATIC_STAGING_BYTES,
+                     compute, copy, &st->events);
 }
 
 int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,

@@ -12,11 +12,12 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most ids a host-id call takes
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
 INLINE_IMAGES = 128          # IEKV_INLINE_IMAGES: scattered host images restored in one launch
+STATIC_STAGING = 32 << 20    # IEKV_STATIC_STAGING_BYTES: staging of iekv_offload_static
 
 IEKV_OK = 0
 IEKV_ERR_INVALID = -1
@@ -42,6 +43,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                  c_int64, c_void_p]),
     "iekv_offload": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p, c_int64,
                              c_void_p, c_void_p]),
+    "iekv_offload_static": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p,
+                                    c_void_p]),
     "iekv_restore": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p, c_int64,
                              c_void_p, c_void_p]),
     "iekv_restore_blocks": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64,

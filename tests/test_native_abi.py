@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 8
+    assert lib.iekv_abi_version() == 9
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -116,6 +116,32 @@ def test_scattered_restore_rejects_missing_host_addresses(lib):
     assert rc == _native.IEKV_ERR_INVALID
     assert "host block 1 address is null" in lib.iekv_last_error().decode()
     pool.close()
+
+
+def test_static_offload_refuses_blocks_larger_than_its_buffer(lib):
+    """iekv_offload_static checks its arguments, and that one block image fits the
+    library's static staging buffer, before anything touches the GPU."""
+    from iekv import _native
+
+    small = _native.Pool([1 << 20, (1 << 20) + 64 * 16], tile_bytes=64, num_blocks=16, device=0)
+    ids = (ctypes.c_int32 * 2)(0, 1)
+    host = ctypes.create_string_buffer(2 * 2 * 64)
+    assert lib.iekv_offload_static(None, ids, 2, host, len(host), None, None) == \
+        _native.IEKV_ERR_INVALID
+    assert lib.iekv_offload_static(small.handle, None, 2, host, len(host), None, None) == \
+        _native.IEKV_ERR_INVALID
+    rc = lib.iekv_offload_static(small.handle, ids, 2, host, len(host) - 1, None, None)
+    assert rc == _native.IEKV_ERR_CAPACITY
+    assert "host buffer" in lib.iekv_last_error().decode()
+    small.close()
+    # Two arrays of 17 MiB tiles: a 34 MiB block image, over the 32 MiB buffer.
+    tile = 17 << 20
+    big = _native.Pool([1 << 40, (1 << 40) + 4 * tile], tile_bytes=tile, num_blocks=4, device=0)
+    rc = lib.iekv_offload_static(big.handle, ids, 1, host, 1 << 40, None, None)
+    assert rc == _native.IEKV_ERR_CAPACITY
+    message = lib.iekv_last_error().decode()
+    assert f"{2 * tile}" in message and f"{_native.STATIC_STAGING}-byte static staging" in message
+    big.close()
 
 
 def test_default_launch_shape():
