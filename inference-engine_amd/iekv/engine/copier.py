@@ -95,8 +95,22 @@ class PackedBlocks:
         return (BlockPayload(self, i) for i in range(len(self)))
 
     def tiles(self, index: int) -> torch.Tensor:
-        """Block ``index`` as typed tiles ``[2L, *tile_shape]`` (a view)."""
+        """Block ``index`` as typed tiles ``[2L, *tile_shape]`` (a view).
+
+        Host data is read by the CPU as soon as the view exists, so a view of a
+        buffer that an asynchronous copy is still filling waits for that copy
+        first: the payload is a finished snapshot, as the reference's
+        ``read_block`` returns one (ie/engine/copier.py:18-22).
+        """
+        if self.on_host:
+            self.synchronize()
         return self.data[index].view(self.dtype).view(2 * self.num_layers, *self.tile_shape)
+
+    def host_data(self) -> torch.Tensor:
+        """``data`` of a host buffer once every pending copy into it has finished."""
+        if not self.on_host:
+            raise ValueError("the payload is in device memory")
+        return self.synchronize().data
 
     def mark(self, stream: torch.cuda.Stream) -> None:
         """Record that async copies involving this (host) buffer end on ``stream``."""

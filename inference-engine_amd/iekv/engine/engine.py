@@ -87,6 +87,11 @@ class Engine:
         if (len(self.k_caches) != len(self.v_caches)
                 or any(len(t) != rows for t in list(self.k_caches) + list(self.v_caches))):
             raise ValueError(f"caches must hold {rows} rows per array, K and V per layer")
+        # Per-pool state the model keeps for these caches (the toy model's slot-kernel
+        # pool registration); held here so it lives exactly as long as the engine.
+        bind = getattr(model, "bind_caches", None)
+        self.model_state = bind(self.k_caches, self.v_caches, self.config.block_size) \
+            if bind is not None else None
         self.swapper = None
         if self.config.preemption == "swap":
             self.swapper = self.copier_factory(self.k_caches, self.v_caches,

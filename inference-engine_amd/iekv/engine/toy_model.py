@@ -15,6 +15,7 @@ through libiekv's slot kernels (``iekv.engine.slots``) instead of torch's
 """
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -103,7 +104,8 @@ class ToyTransformer:
         self.device = torch.device(device)
         self.cache_dtype = cache_dtype
         self.hip_kv = hip_kv
-        self._pools: dict = {}
+        # Registered pools by cache address; an engine holds each one (bind_caches).
+        self._pools: weakref.WeakValueDictionary = weakref.WeakValueDictionary()
         rng = np.random.default_rng(seed)
         scale = 1.0 / np.sqrt(config.hidden_size)
 
@@ -134,13 +136,29 @@ class ToyTransformer:
                                   c.num_kv_heads, c.head_dim, dtype=self.cache_dtype,
                                   device=self.device)
 
-    def _pool(self, k_caches, v_caches, block_size: int):
+    def bind_caches(self, k_caches, v_caches, block_size: int):
+        """Register a pool for the slot kernels; the caller keeps the returned
+        handle for as long as it uses the caches (an Engine holds it for its
+        lifetime). The model itself keeps only a weak reference, so a pool is
+        released with the engine that owns it. None without ``hip_kv``."""
+        if not self.hip_kv:
+            return None
         from .pools import KVPool
 
         key = (k_caches[0].data_ptr(), v_caches[0].data_ptr(), block_size)
         pool = self._pools.get(key)
         if pool is None:
-            pool = self._pools[key] = KVPool(k_caches, v_caches, block_size)
+            pool = KVPool(k_caches, v_caches, block_size)
+            self._pools[key] = pool
+        return pool
+
+    def _pool(self, k_caches, v_caches, block_size: int):
+        key = (k_caches[0].data_ptr(), v_caches[0].data_ptr(), block_size)
+        pool = self._pools.get(key)
+        if pool is None:      # caches nobody bound: a pool for this call only
+            from .pools import KVPool
+
+            pool = KVPool(k_caches, v_caches, block_size)
         return pool
 
     def _context(self, cache: torch.Tensor, array: int, pool, table: list[int],

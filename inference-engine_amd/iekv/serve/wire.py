@@ -97,7 +97,9 @@ def decode_header(buf: bytes) -> dict[str, Any]:
 def to_wire(transfer: KVTransfer) -> tuple[bytes, torch.Tensor]:
     """(header bytes, payload tensor [B, 2L, T] uint8). Direct-mode transfers are packed first."""
     packed = _packed_of(transfer)
-    return encode_header(transfer, packed), packed.data
+    # A host payload may still be filling from the device: hand out finished bytes.
+    data = packed.host_data() if packed.on_host else packed.data
+    return encode_header(transfer, packed), data
 
 
 def from_wire(header: bytes, payload: torch.Tensor) -> KVTransfer:
