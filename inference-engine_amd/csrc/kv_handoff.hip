@@ -77,11 +77,16 @@ int set_error(int code, const char* fmt, ...) {
   return code;
 }
 
+// A failed HIP call returns IEKV_ERR_HIP with the runtime's message, and
+// leaves HIP's last error clear: the next call's own check after its launch
+// must not see this failure again.
 #define IEKV_HIP(expr)                                                                   \
   do {                                                                                   \
     hipError_t err_ = (expr);                                                            \
-    if (err_ != hipSuccess)                                                              \
+    if (err_ != hipSuccess) {                                                            \
+      (void)hipGetLastError();                                                           \
       return set_error(IEKV_ERR_HIP, "%s: %s", #expr, hipGetErrorString(err_));          \
+    }                                                                                    \
   } while (0)
 
 // Launch shape. Measured on MI355X over the five benchmark workloads (8 KiB to
@@ -518,19 +523,26 @@ int align_of_ptr(uint64_t p) {
 // caller's device afterwards.
 class DeviceGuard {
  public:
-  explicit DeviceGuard(int device) {
-    ok_ = hipGetDevice(&prev_) == hipSuccess;
-    if (ok_ && prev_ != device) ok_ = hipSetDevice(device) == hipSuccess;
-    switched_ = ok_ && prev_ != device;
+  explicit DeviceGuard(int device) : device_(device) {
+    err_ = hipGetDevice(&prev_);
+    if (err_ == hipSuccess && prev_ != device) err_ = hipSetDevice(device);
+    if (err_ != hipSuccess) (void)hipGetLastError();   // reported through fail()
+    switched_ = err_ == hipSuccess && prev_ != device;
   }
   ~DeviceGuard() {
     if (switched_) (void)hipSetDevice(prev_);
   }
-  bool ok() const { return ok_; }
+  bool ok() const { return err_ == hipSuccess; }
+  // The error a caller returns when ok() is false: IEKV_ERR_HIP with the runtime's message.
+  int fail() const {
+    return set_error(IEKV_ERR_HIP, "cannot make device %d current: %s", device_,
+                     hipGetErrorString(err_));
+  }
 
  private:
+  int device_;
   int prev_ = 0;
-  bool ok_ = false;
+  hipError_t err_ = hipSuccess;
   bool switched_ = false;
 };
 
@@ -782,7 +794,7 @@ int restore_pipeline(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blo
     return rc;
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(dst->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+  if (!guard.ok()) return guard.fail();
 
   int n_slots;
   int64_t slot_blocks;
@@ -954,6 +966,7 @@ int static_staging(int device, const StaticStaging** out) {
     for (int i = 0; i < 5; ++i) {
       const hipError_t e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
       if (e != hipSuccess) {
+        (void)hipGetLastError();
         for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
         return set_error(IEKV_ERR_HIP, "hipEventCreateWithFlags: %s", hipGetErrorString(e));
       }
@@ -1036,12 +1049,13 @@ int iekv_pool_create(const uint64_t* array_ptrs, int32_t n_arrays, int64_t tile_
     DeviceGuard guard(device);
     if (!guard.ok()) {
       delete p;
-      return set_error(IEKV_ERR_HIP, "cannot make device %d current", device);
+      return guard.fail();
     }
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->table), sizeof(uint64_t) * n_arrays);
     if (e == hipSuccess)
       e = hipMemcpy(p->table, array_ptrs, sizeof(uint64_t) * n_arrays, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
+      (void)hipGetLastError();
       if (p->table) (void)hipFree(p->table);
       delete p;
       return set_error(IEKV_ERR_HIP, "uploading the pool address table: %s",
@@ -1058,7 +1072,10 @@ int iekv_pool_destroy(iekv_pool* pool) {
   if (pool->table) {
     DeviceGuard guard(pool->device);
     hipError_t e = hipFree(pool->table);
-    if (e != hipSuccess) rc = set_error(IEKV_ERR_HIP, "hipFree: %s", hipGetErrorString(e));
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      rc = set_error(IEKV_ERR_HIP, "hipFree: %s", hipGetErrorString(e));
+    }
   }
   delete pool;
   return rc;
@@ -1080,7 +1097,7 @@ int iekv_copy_direct(const iekv_pool* src, const iekv_pool* dst, const int32_t* 
     return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
                      dst->device);
   DeviceGuard guard(src->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  if (!guard.ok()) return guard.fail();
   return launch_move<true, true>(src, dst, nullptr, nullptr, src_ids, dst_ids, n_blocks,
                                  src->tile_bytes, src->n_arrays,
                                  std::min(src->align, dst->align), stream);
@@ -1095,7 +1112,7 @@ int iekv_pack(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, vo
   if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
   if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
   DeviceGuard guard(src->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  if (!guard.ok()) return guard.fail();
   const int align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
   return launch_move<true, false>(src, nullptr, nullptr, static_cast<char*>(staging), src_ids,
                                   nullptr, n_blocks, src->tile_bytes, src->n_arrays, align,
@@ -1112,7 +1129,7 @@ int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
   if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
   DeviceGuard guard(dst->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+  if (!guard.ok()) return guard.fail();
   const int align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
   return launch_move<false, true>(nullptr, dst, static_cast<const char*>(staging), nullptr,
                                   nullptr, dst_ids, n_blocks, dst->tile_bytes, dst->n_arrays,
@@ -1135,7 +1152,7 @@ int iekv_copy_direct_ids(const iekv_pool* src, const iekv_pool* dst, const int32
       (rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, n_blocks)))
     return rc;
   DeviceGuard guard(src->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  if (!guard.ok()) return guard.fail();
   return launch_move_inline<true, true>(src, dst, nullptr, nullptr, ids, n_blocks, n_blocks,
                                         src->tile_bytes, src->n_arrays,
                                         std::min(src->align, dst->align), stream);
@@ -1152,7 +1169,7 @@ int iekv_pack_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks
   InlineIds ids{};
   if ((rc = fill_inline(src_ids, n_blocks, src->num_blocks, "source", &ids, 0))) return rc;
   DeviceGuard guard(src->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  if (!guard.ok()) return guard.fail();
   const int align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
   return launch_move_inline<true, false>(src, nullptr, nullptr, static_cast<char*>(staging), ids,
                                          0, n_blocks, src->tile_bytes, src->n_arrays, align,
@@ -1171,7 +1188,7 @@ int iekv_unpack_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_bloc
   InlineIds ids{};
   if ((rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, 0))) return rc;
   DeviceGuard guard(dst->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+  if (!guard.ok()) return guard.fail();
   const int align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
   return launch_move_inline<false, true>(nullptr, dst, static_cast<const char*>(staging), nullptr,
                                          ids, 0, n_blocks, dst->tile_bytes, dst->n_arrays, align,
@@ -1194,7 +1211,7 @@ int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, c
     return set_error(IEKV_ERR_INVALID, "%d tokens exceed one launch", n_tokens);
   if (!k || !v || !slots) return set_error(IEKV_ERR_INVALID, "k, v or slots is null");
   DeviceGuard guard(pool->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", pool->device);
+  if (!guard.ok()) return guard.fail();
   const int64_t row_bytes = pool->tile_bytes / block_size;
   const int align = row_align(row_bytes, pool->align, {k, v});
   const dim3 grid((n_tokens + kRowsPerGroup - 1) / kRowsPerGroup, 2);
@@ -1234,7 +1251,7 @@ int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
   if ((rc = check_buffer(out, out_bytes, row_bytes * context_len, "output"))) return rc;
   if (!block_table) return set_error(IEKV_ERR_INVALID, "block_table is null");
   DeviceGuard guard(pool->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", pool->device);
+  if (!guard.ok()) return guard.fail();
   const int align = row_align(row_bytes, pool->align, {out});
   const dim3 grid((context_len + kRowsPerGroup - 1) / kRowsPerGroup);
   char* oc = static_cast<char*>(out);
@@ -1261,7 +1278,7 @@ int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
     return rc;
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  if (!guard.ok()) return guard.fail();
   return run_offload(src, src_ids, n_blocks, host_dst, need, static_cast<char*>(staging),
                      staging_bytes, compute, copy, nullptr);
 }
@@ -1281,7 +1298,7 @@ int iekv_offload_static(const iekv_pool* src, const int32_t* src_ids, int32_t n_
                      static_cast<long long>(IEKV_STATIC_STAGING_BYTES));
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
-  if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", src->device);
+  if (!guard.ok()) return guard.fail();
   const StaticStaging* st = nullptr;
   if ((rc = static_staging(src->device, &st))) return rc;
   return run_offload(src, src_ids, n_blocks, host_dst, need, st->ptr, IEKV_STATIC_STAGING_BYTES,
@@ -1302,7 +1319,7 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   if (n_blocks > 0 && need <= kZeroCopyMaxBytes) {
     if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
     DeviceGuard guard(dst->device);
-    if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+    if (!guard.ok()) return guard.fail();
     if (const char* mapped = device_view_of_host(host_src, need)) {
       const int zc_align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
       if ((rc = launch_move<false, true>(nullptr, dst, mapped, nullptr, nullptr, dst_ids, n_blocks,
@@ -1344,7 +1361,7 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
       block_bytes * n_blocks <= kZeroCopyMaxBytes) {
     if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
     DeviceGuard guard(dst->device);
-    if (!guard.ok()) return set_error(IEKV_ERR_HIP, "cannot make device %d current", dst->device);
+    if (!guard.ok()) return guard.fail();
     InlineImages images{};
     if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
       if ((rc = launch_images(dst, images, dst_ids, n_blocks, compute))) return rc;
@@ -1361,23 +1378,20 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
   return restore_pipeline(
       dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
       [&](char* slot, int64_t first, int32_t cnt) -> int {
-        // One copy per run of blocks whose images are adjacent in host memory
-        // and lie in the allocation holding the run's first image: separately
-        // pinned buffers can be neighbours in the address space, and one copy
-        // must not run past the end of its source allocation.
-        for (int32_t i = 0; i < cnt;) {
-          const char* run_start = static_cast<const char*>(host_blocks[first + i]);
-          const int64_t room = bytes_to_allocation_end(run_start);
-          int32_t len = 1;
-          while (i + len < cnt &&
-                 static_cast<const char*>(host_blocks[first + i + len]) ==
-                     run_start + len * block_bytes &&
-                 (len + 1) * block_bytes <= room)
-            ++len;
-          IEKV_HIP(hipMemcpyAsync(slot + i * block_bytes, run_start, len * block_bytes,
-                                  hipMemcpyHostToDevice, copy));
-          i += len;
-        }
+        // One copy per run of images that are adjacent in host memory within
+        // one allocation (iekv_plan::image_runs).
+        hipError_t err = hipSuccess;
+        iekv_plan::image_runs(
+            host_blocks + first, cnt, block_bytes,
+            [](uint64_t address) {
+              return bytes_to_allocation_end(reinterpret_cast<const char*>(address));
+            },
+            [&](int32_t i, int32_t len) {
+              if (err == hipSuccess)
+                err = hipMemcpyAsync(slot + i * block_bytes, host_blocks[first + i],
+                                     len * block_bytes, hipMemcpyHostToDevice, copy);
+            });
+        IEKV_HIP(err);
         return IEKV_OK;
       });
 }
@@ -1397,6 +1411,7 @@ int iekv_profile_start(int32_t max_launches) {
     IEKV_HIP(hipEventCreate(&a));
     hipError_t e = hipEventCreate(&b);
     if (e != hipSuccess) {
+      (void)hipGetLastError();
       (void)hipEventDestroy(a);
       return set_error(IEKV_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(e));
     }

@@ -158,6 +158,32 @@ inline Status plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, 
   return kPlanned;
 }
 
+// Copies of a scattered restore (iekv_restore_blocks): list entry i's host
+// image of image_bytes bytes starts at address images[i]. Consecutive entries
+// whose images follow each other in memory are copied with one transfer, but
+// a run never extends past the end of the allocation that holds its first
+// image: separately allocated buffers can be neighbours in the address space,
+// and one copy must not read past the end of its source allocation.
+// room(address) gives the bytes from `address` to the end of the allocation
+// holding it (0 when unknown, which leaves each image on its own). emit(first,
+// count) is called once per run, in list order; the runs cover [0, n).
+template <typename Room, typename Emit>
+inline void image_runs(const void* const* images, int32_t n, int64_t image_bytes, Room room,
+                       Emit emit) {
+  for (int32_t i = 0; i < n;) {
+    const uint64_t start = reinterpret_cast<uint64_t>(images[i]);
+    const int64_t space = room(start);
+    int32_t len = 1;
+    while (i + len < n &&
+           reinterpret_cast<uint64_t>(images[i + len]) ==
+               start + static_cast<uint64_t>(len) * static_cast<uint64_t>(image_bytes) &&
+           static_cast<int64_t>(len + 1) * image_bytes <= space)
+      ++len;
+    emit(i, len);
+    i += len;
+  }
+}
+
 }  // namespace iekv_plan
 
 #endif  // IEKV_KV_PLAN_H_

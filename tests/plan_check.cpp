@@ -8,11 +8,17 @@
 //     rules and the vector width, over a sweep of tiles, alignments, arrays,
 //     block counts and settings;
 //  4. simulating every launch and workgroup of small plans moves every vector
-//     of every listed tile exactly once.
+//     of every listed tile exactly once;
+//  5. image_runs (the copies of a scattered restore) covers every image once,
+//     in order, merges only images adjacent in memory within the allocation of
+//     the run's first image, and merges every such pair: fixed layouts (one
+//     allocation, neighbouring allocations, gaps, unknown memory, descending
+//     addresses) and random ones.
 // Prints "plan ok" and exits 0, or names the first failure and exits 1.
 #include <algorithm>
 #include <cstdint>
 #include <cstdio>
+#include <random>
 #include <vector>
 
 #include "../inference-engine_amd/csrc/kv_plan.h"
@@ -134,6 +140,130 @@ static void simulate(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int
   }
 }
 
+
+// Synthetic allocations [lo, hi) for image_runs: room(address) is the distance
+// to the end of the allocation holding it, 0 outside every allocation.
+struct Allocations {
+  std::vector<std::pair<uint64_t, uint64_t>> ranges;
+  int64_t room(uint64_t address) const {
+    for (const auto& r : ranges)
+      if (address >= r.first && address < r.second) return static_cast<int64_t>(r.second - address);
+    return 0;
+  }
+};
+
+// The runs image_runs makes for `addresses`, as (first, count) pairs.
+static std::vector<std::pair<int32_t, int32_t>> runs_of(const std::vector<uint64_t>& addresses,
+                                                        int64_t image_bytes,
+                                                        const Allocations& alloc) {
+  std::vector<const void*> images;
+  for (uint64_t a : addresses) images.push_back(reinterpret_cast<const void*>(a));
+  std::vector<std::pair<int32_t, int32_t>> runs;
+  image_runs(images.data(), static_cast<int32_t>(images.size()), image_bytes,
+             [&](uint64_t a) { return alloc.room(a); },
+             [&](int32_t first, int32_t count) { runs.emplace_back(first, count); });
+  return runs;
+}
+
+// The properties every split must have: runs cover [0, n) in order; inside a
+// run the images follow each other and stay within the allocation of its
+// first image; and a run ends only where the next image is not adjacent or
+// would cross that allocation's end (the split is as coarse as allowed).
+static void check_runs(const std::vector<uint64_t>& addresses, int64_t image_bytes,
+                       const Allocations& alloc, const char* what) {
+  const auto runs = runs_of(addresses, image_bytes, alloc);
+  int32_t next = 0;
+  for (const auto& run : runs) {
+    const int32_t first = run.first, count = run.second;
+    EXPECT(first == next && count >= 1, "%s: run (%d, %d) does not continue at %d", what, first,
+           count, next);
+    const uint64_t start = addresses[first];
+    const int64_t room = alloc.room(start);
+    if (count > 1)
+      EXPECT(count * image_bytes <= room, "%s: run at %d crosses its allocation's end", what,
+             first);
+    for (int32_t j = 1; j < count; ++j)
+      EXPECT(addresses[first + j] == start + j * image_bytes, "%s: run at %d merges image %d, "
+             "which is not adjacent", what, first, first + j);
+    const int32_t end = first + count;
+    if (end < static_cast<int32_t>(addresses.size()))
+      EXPECT(addresses[end] != start + count * image_bytes || (count + 1) * image_bytes > room,
+             "%s: run at %d stops before image %d, which it could take", what, first, end);
+    next = end;
+  }
+  EXPECT(next == static_cast<int32_t>(addresses.size()), "%s: runs end at %d of %zu", what, next,
+         addresses.size());
+}
+
+static void check_image_runs() {
+  const int64_t img = 2 << 20;   // a Llama-3-8B-shape block image
+  const uint64_t base = uint64_t(1) << 40;
+  std::vector<uint64_t> eight;
+  for (int i = 0; i < 8; ++i) eight.push_back(base + i * img);
+
+  Allocations one{{{base, base + 8 * img}}};
+  EXPECT(runs_of(eight, img, one) == (std::vector<std::pair<int32_t, int32_t>>{{0, 8}}),
+         "8 adjacent images in one allocation are one copy");
+  check_runs(eight, img, one, "one allocation");
+
+  Allocations separate;
+  for (int i = 0; i < 8; ++i) separate.ranges.push_back({base + i * img, base + (i + 1) * img});
+  EXPECT(runs_of(eight, img, separate).size() == 8,
+         "8 images in 8 neighbouring allocations are 8 copies");
+  check_runs(eight, img, separate, "neighbouring allocations");
+
+  Allocations split{{{base, base + 3 * img}, {base + 3 * img, base + 8 * img}}};
+  EXPECT(runs_of(eight, img, split) == (std::vector<std::pair<int32_t, int32_t>>{{0, 3}, {3, 5}}),
+         "adjacent images across an allocation boundary split there");
+  check_runs(eight, img, split, "allocation boundary");
+
+  Allocations unknown;
+  EXPECT(runs_of(eight, img, unknown).size() == 8, "images in unknown memory are copied alone");
+
+  std::vector<uint64_t> gapped = {base, base + img, base + 3 * img, base + 4 * img,
+                                  base + 5 * img + 64};
+  Allocations big{{{base, base + 16 * img}}};
+  EXPECT(runs_of(gapped, img, big) ==
+             (std::vector<std::pair<int32_t, int32_t>>{{0, 2}, {2, 2}, {4, 1}}),
+         "a gap ends a run");
+  check_runs(gapped, img, big, "gaps");
+
+  std::vector<uint64_t> descending(eight.rbegin(), eight.rend());
+  EXPECT(runs_of(descending, img, one).size() == 8, "descending images are copied alone");
+
+  // An allocation that ends inside the second image: the first is copied alone.
+  Allocations short_alloc{{{base, base + img + img / 2}}};
+  EXPECT(runs_of({base, base + img}, img, short_alloc).size() == 2,
+         "a run never extends past its allocation's end");
+
+  // Random layouts: images drawn from a few allocations, mostly in ascending
+  // runs with occasional jumps, gaps and repeats of neighbouring buffers.
+  std::mt19937_64 rng(7);
+  for (int trial = 0; trial < 3000; ++trial) {
+    const int64_t size = int64_t(64) << (rng() % 6);
+    Allocations alloc;
+    uint64_t at = base;
+    const int n_alloc = 1 + static_cast<int>(rng() % 6);
+    for (int a = 0; a < n_alloc; ++a) {
+      const uint64_t len = size * (1 + rng() % 6) + (rng() % 3 == 0 ? size / 2 : 0);
+      alloc.ranges.push_back({at, at + len});
+      at += len + (rng() % 2 ? 0 : size);   // neighbouring or separated allocations
+    }
+    std::vector<uint64_t> addresses;
+    const int n = 1 + static_cast<int>(rng() % 24);
+    uint64_t cursor = alloc.ranges[0].first;
+    for (int i = 0; i < n; ++i) {
+      const int pick = static_cast<int>(rng() % 8);
+      if (pick == 0) cursor = alloc.ranges[rng() % alloc.ranges.size()].first;
+      else if (pick == 1) cursor += size / 2;
+      else if (pick == 2 && cursor > base + size) cursor -= size;
+      addresses.push_back(cursor);
+      cursor += size;
+    }
+    check_runs(addresses, size, alloc, "random layout");
+  }
+}
+
 int main() {
   for (int grid = 1; grid <= 4096; ++grid) check_xcd_grouped(grid);
   for (int grid : {98816, 1048575, 4194304, 16777215}) check_xcd_grouped(grid);
@@ -192,6 +322,8 @@ int main() {
             s.chunk_bytes = chunk;
             simulate(13, tile, n_arrays, pow2_divisor(tile), s, order);
           }
+
+  check_image_runs();
 
   if (failures) {
     std::printf("%d failures\n", failures);

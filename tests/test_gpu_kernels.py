@@ -552,6 +552,76 @@ def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, o
     assert_pool_equals(dk, dv, dst_o)
 
 
+def test_host_payload_views_wait_for_their_copy(gpu):
+    """A host payload is read right after read_block / read_blocks returns, with no
+    synchronisation by the caller: its tiles must already be the finished snapshot,
+    for one block (written by the pack kernel), for 80 MiB (the staged pipeline)
+    and for a deferred single-block read (flushed by its first access)."""
+    from iekv.engine.copier import HipSlotCopier
+    from iekv.serve.disaggregated import KVTransfer
+    from iekv.serve.wire import to_wire
+
+    bs, layers, heads, dim = 16, 4, 8, 128       # 1 MiB block images
+    sk, sv = allocate(96, bs, layers, heads, dim, torch.bfloat16, gpu, seed=81)
+    src_o = oracle_of(sk, sv, bs)
+    eager = HipSlotCopier(sk, sv, bs, payload_location="host", defer_reads=False)
+    deferred = HipSlotCopier(sk, sv, bs, payload_location="host", defer_reads=True)
+
+    def as_bytes(tiles):
+        return [t.contiguous().view(torch.uint8).reshape(bs, -1).numpy() for t in tiles]
+
+    def expect(block_id, k_list, v_list):
+        want_k, want_v = src_o.read_block(block_id)
+        got = as_bytes(k_list) + as_bytes(v_list)
+        for g, w in zip(got, list(want_k) + list(want_v)):
+            assert np.array_equal(g, w)
+
+    one = eager.read_block(17)
+    k_list, v_list = one
+    expect(17, k_list, v_list)
+    ids = [int(b) for b in np.random.default_rng(82).permutation(96)[:80]]
+    many = eager.read_blocks(ids)
+    last = many[len(ids) - 1]
+    expect(ids[-1], last.k, last.v)
+    payload = deferred.read_block(5)
+    expect(5, payload.k, payload.v)
+    # The wire sender hands out the finished bytes of a host payload as well.
+    again = eager.read_blocks(ids)
+    _, data = to_wire(KVTransfer(token_ids=[1], num_computed=0, block_payloads=again))
+    assert np.array_equal(data.numpy(), packed_image(pack(src_o, ids)))
+
+
+def test_a_hip_failure_raises_and_leaves_no_error_behind(gpu):
+    """A HIP call that fails inside the library (switching to a device that does not
+    exist, to upload an address table) raises NativeError with IEKV_ERR_HIP and the
+    runtime's message, and leaves HIP's last error clear: the next call's launch
+    check must not report it again, and that call moves its blocks bit-exactly."""
+    import ctypes
+
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    _native.lib()
+    runtime = [line.split()[-1] for line in open("/proc/self/maps")
+               if line.rstrip().endswith("libamdhip64.so")][0]
+    hip = ctypes.CDLL(runtime)      # the runtime instance torch and libiekv share
+    missing = torch.cuda.device_count() + 7
+    with pytest.raises(_native.NativeError) as err:
+        _native.Pool([1 << 30, (1 << 30) + 4096, (1 << 30) + 3 * 4096], tile_bytes=64,
+                     num_blocks=16, device=missing)
+    assert err.value.code == _native.IEKV_ERR_HIP
+    assert f"cannot make device {missing} current: " in str(err.value)
+    assert hip.hipGetLastError() == 0
+    bs = 16
+    sk, sv = allocate(16, bs, 2, 2, 32, torch.float16, gpu, seed=85)
+    dk, dv = allocate(16, bs, 2, 2, 32, torch.float16, gpu, seed=86)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    HipSlotCopier(dk, dv, bs).copy_blocks(HipSlotCopier(sk, sv, bs), [3, 9], [0, 15])
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [[3, 9]], [[0, 15]])
+    assert_pool_equals(dk, dv, dst_o)
+
+
 def test_host_payloads_through_the_copier(gpu):
     from iekv.engine.copier import HipSlotCopier
 

@@ -144,6 +144,29 @@ def test_static_offload_refuses_blocks_larger_than_its_buffer(lib):
     big.close()
 
 
+def test_a_failing_hip_call_surfaces_as_a_hip_error(lib):
+    """A HIP runtime failure inside the library comes back as IEKV_ERR_HIP with the
+    runtime's own message, and in Python as NativeError (a RuntimeError, the
+    reference's failure type, ie/serve/disaggregated.py:78-79). Arrays that are not
+    equally spaced need an address table on the device, so registering them on a
+    device that does not exist makes the runtime refuse to switch to it."""
+    from iekv import _native
+
+    ptrs = [1 << 30, (1 << 30) + 4096, (1 << 30) + 3 * 4096]
+    out = ctypes.c_void_p()
+    table = (ctypes.c_uint64 * 3)(*ptrs)
+    rc = lib.iekv_pool_create(table, 3, 64, 16, 99, ctypes.byref(out))
+    assert rc == _native.IEKV_ERR_HIP
+    message = lib.iekv_last_error().decode()
+    assert message.startswith("cannot make device 99 current: ")
+    assert len(message) > len("cannot make device 99 current: ")   # the runtime's text
+    assert not out.value
+    with pytest.raises(_native.NativeError) as err:
+        _native.Pool(ptrs, tile_bytes=64, num_blocks=16, device=99)
+    assert err.value.code == _native.IEKV_ERR_HIP
+    assert isinstance(err.value, RuntimeError)
+
+
 def test_default_launch_shape():
     """A fresh process starts with the shape the header documents."""
     import json

@@ -3,8 +3,10 @@
 tests/plan_check.cpp includes the header the kernels use and checks it
 exhaustively: the XCD-grouped workgroup order is a bijection, every workgroup
 order visits each (array unit, run, chunk) once, plans respect the dispatch
-limit, chunk and tile-group rules, and a simulation of every launch and
-workgroup of small plans moves every vector of every tile exactly once.
+limit, chunk and tile-group rules, a simulation of every launch and
+workgroup of small plans moves every vector of every tile exactly once, and
+the copies of a scattered restore (image_runs) merge exactly the images that
+are adjacent within one allocation, over fixed and random layouts.
 """
 from __future__ import annotations
 
