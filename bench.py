@@ -55,11 +55,14 @@ for _p in (str(ROOT), str(ROOT / "inference-engine_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
-# HBM bytes per algorithmic byte of the direct kv_move launches: (2 x FETCH_SIZE +
-# WRITE_SIZE) / (read + write bytes), from two rocprofv3 --pmc runs of this script
-# calibrated on a plain 4 GiB copy (FETCH_SIZE reads 0.5x, WRITE_SIZE 1.0x of its
-# known size); see profiles/kv_move_direct_cfg3_pmc.txt.
-PMC_TRAFFIC_RATIO = 1.0002
+# HBM bytes per algorithmic byte of the direct kv_move launches on cfg3 with the
+# library's default launch shape, from two rocprofv3 --pmc runs (FETCH_SIZE, then
+# WRITE_SIZE) calibrated on a plain 4 GiB copy; the summary states the command and
+# ends with a "traffic_ratio <x>" line. Used only for the configuration it measured.
+PMC_SUMMARY = ROOT / "profiles" / "kv_move_direct_cfg3_pmc.txt"
+# Names of the cache dtypes in the bench line (the kernels move their raw bits).
+DTYPE_NAMES = {"float32": "f32", "float16": "f16", "bfloat16": "bf16", "fp8_e4m3": "fp8_e4m3",
+               "uint8": "u8"}
 METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff"
 # Legs that move the workload's blocks from the prefill pool to the decode pool; the
 # first of them in --legs gives the line's value (2P / step time).
@@ -69,6 +72,29 @@ HANDOFF_LEGS = ("direct", "pack_unpack", "pack", "unpack", "batched", "copier",
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+DEFAULT_LAUNCH = {"run_blocks": 0, "unroll": 8, "nontemporal": 1, "order": 5, "pack_order": 0,
+                  "chunk_bytes": 4096}
+
+
+def measured_traffic(config: str, tp: int, leg: str, launch: dict, separate: bool,
+                     bytes_per_launch: float) -> tuple[int | None, str]:
+    """HBM bytes per launch of the dominant kernel from the committed PMC summary, and
+    where that figure comes from. Only the case the summary measured (cfg3, whole
+    heads, the direct leg, default launch shape, paired pools) gets a number."""
+    if (config, tp, leg, separate) != ("cfg3", 1, "direct", False) or launch != DEFAULT_LAUNCH:
+        return None, f"not measured for this case (PMC summary covers cfg3 direct: {PMC_SUMMARY.name})"
+    ratio = None
+    if PMC_SUMMARY.exists():
+        for line in PMC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_ratio "):
+                ratio = float(line.split()[1])
+    if ratio is None:
+        return None, f"{PMC_SUMMARY.name} holds no traffic_ratio line"
+    return int(bytes_per_launch * ratio), (
+        f"{PMC_SUMMARY.relative_to(ROOT)}: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 "
+        f"(calibrated on a 4 GiB copy) = {ratio} x the algorithmic bytes per launch")
 
 
 def torch_dtype(name: str):
@@ -550,14 +576,19 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
     return out, kernel_gbs, 1000 * total_ms / max(1, len(durations)), moved / max(1, len(durations))
 
 
-def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float) -> dict:
+def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float,
+                 source_arrays) -> dict:
     """The reference handoff restated in NumPy (oracle/), single-threaded, on a bounded sample.
 
     The sample is the workload's first requests up to ``budget_blocks`` blocks, on
     host pools just large enough for them, with random src/dst ids; the handoff
-    of the sample is repeated until ``min_seconds`` have passed.
+    of the sample is repeated until ``min_seconds`` have passed. The host source
+    pool holds the GPU leg's own source bytes (the first blocks of each of
+    ``source_arrays``, N(0,1) values), and afterwards every moved destination
+    tile is compared byte for byte with its source tile.
     """
     import numpy as np
+    import torch
 
     from oracle.copier import LayeredSlotCopier, pack, unpack
 
@@ -568,19 +599,20 @@ def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float) ->
             break
         sizes.append(len(t))
         total += len(t)
-    pool = total + 64
+    pool = min(total + 64, workload.src_pool_blocks)
     rng = np.random.default_rng(seed)
     src_ids = rng.permutation(pool)[:total]
     dst_ids = rng.permutation(pool)[:total]
-    np_dtype = {1: np.uint8, 2: np.uint16, 4: np.float32}[s.elem_bytes]
-    shape = (pool * s.block_size, s.kv_heads, s.head_dim)
+    raw_view = {1: torch.uint8, 2: torch.int16, 4: torch.float32}[s.elem_bytes]
+    rows = pool * s.block_size
     t0 = time.perf_counter()
-    # Pages are written once here so the timed copies do not pay first-touch faults.
-    src_k = [np.full(shape, l + 1, dtype=np_dtype) for l in range(s.layers)]
-    src_v = [np.full(shape, 100 + l, dtype=np_dtype) for l in range(s.layers)]
-    dst_k = [np.full(shape, 0, dtype=np_dtype) for _ in range(s.layers)]
-    dst_v = [np.full(shape, 0, dtype=np_dtype) for _ in range(s.layers)]
-    log(f"[bench] cpu baseline: host pools of {pool} blocks ready in "
+    # The copies to host memory write every page once, so the timed copies do not pay
+    # first-touch faults on the source; the destination pools are written here too.
+    src_arrays = [a[:rows].view(raw_view).cpu().numpy() for a in source_arrays]
+    src_k, src_v = src_arrays[:s.layers], src_arrays[s.layers:]
+    dst_k = [np.zeros_like(a) for a in src_k]
+    dst_v = [np.zeros_like(a) for a in src_v]
+    log(f"[bench] cpu baseline: host pools of {pool} blocks (the GPU source's bytes) ready in "
         f"{time.perf_counter() - t0:.1f} s; {len(sizes)} requests, {total} blocks per pass")
     src = LayeredSlotCopier(src_k, src_v, s.block_size)
     dst = LayeredSlotCopier(dst_k, dst_v, s.block_size)
@@ -597,7 +629,10 @@ def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float) ->
         if elapsed >= min_seconds:
             break
     payload = total * s.block_bytes
-    ok = all(dst_k[l][int(dst_ids[0]) * s.block_size, 0, 0] == l + 1 for l in range(s.layers))
+    # Every moved tile, byte for byte: destination tile dst_ids[i] of each array
+    # equals source tile src_ids[i] of the same array.
+    ok = all(np.array_equal(d.reshape(pool, -1)[dst_ids], a.reshape(pool, -1)[src_ids])
+             for d, a in zip(dst_k + dst_v, src_k + src_v))
     gbs = 2 * payload * passes / elapsed / 1e9
     log(f"[bench] cpu baseline: {passes} passes, {2 * payload * passes / 1e9:.2f} GB in "
         f"{elapsed:.2f} s = {gbs:.3f} GB/s")
@@ -605,11 +640,13 @@ def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float) ->
             "seconds": round(elapsed, 2), "passes": passes, "checked": bool(ok),
             "ms_per_request": round(1000 * elapsed / (passes * len(sizes)), 3),
             "blocks_per_s": round(total * passes / elapsed, 1),
+            "checked_what": (f"every moved tile ({total} blocks x {s.n_arrays} arrays) "
+                             "equals its source tile byte for byte"),
             "sample": (f"{workload.name} shape, first {len(sizes)} requests ({total} blocks, "
-                       f"{payload / 1e9:.2f} GB payload) on {pool}-block host pools with random "
-                       f"src/dst ids, repeated {passes}x; NumPy restatement of "
-                       f"copier.py:18-31 driven as disaggregated.py:50,81-82; "
-                       f"1 of {os.cpu_count()} host cores")}
+                       f"{payload / 1e9:.2f} GB payload) on {pool}-block host pools holding "
+                       f"the GPU source pool's N(0,1) bytes, random src/dst ids, repeated "
+                       f"{passes}x; NumPy restatement of copier.py:18-31 driven as "
+                       f"disaggregated.py:50,81-82; 1 of {os.cpu_count()} host cores")}
 
 
 def sweep(legs: Legs, names: list[str]) -> list[dict]:
@@ -763,10 +800,14 @@ def main() -> int:
 
     cpu = None
     if args.cpu_blocks > 0:
-        cpu = cpu_baseline(w, args.cpu_blocks, args.seed, args.cpu_seconds)
+        cpu = cpu_baseline(w, args.cpu_blocks, args.seed, args.cpu_seconds,
+                           legs.src_k + legs.src_v)
 
     name, ms, res, kgbs, avg_us, avg_bytes = primary
     value = 2 * P / (ms * 1e-3) / 1e9
+    launch = _native.get_launch()
+    traffic, traffic_source = measured_traffic(w.name, args.tp, name, launch,
+                                               args.separate_pools, avg_bytes)
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -779,7 +820,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8",
+        "dtype": DTYPE_NAMES[w.shape.dtype],
+        "dtype_note": "the cache dtype; the kernels move its raw bits in 16-byte words",
         "data": "synthetic",
         "config": {
             "workload": f"{w.name}: {w.description}",
@@ -788,7 +830,7 @@ def main() -> int:
             "head_dim": w.shape.head_dim, "block_size": w.shape.block_size,
             "kv_dtype": w.shape.dtype, "requests": w.num_requests, "blocks": w.num_blocks,
             "payload_bytes": P, "tile_bytes": w.shape.tile_bytes, "tp_share": args.tp,
-            "launch": _native.get_launch(),
+            "launch": launch,
             "pools": ("two allocations" if args.separate_pools
                       else "one allocation, prefill pool first"),
         },
@@ -799,7 +841,7 @@ def main() -> int:
         "verified": verified,
         "roofline": {"bound": "hbm", "achieved": round(kgbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
-                     "traffic": int(avg_bytes * PMC_TRAFFIC_RATIO),
+                     "traffic": traffic, "traffic_source": traffic_source,
                      "kernel": f"kv_move ({name})", "avg_launch_us": round(avg_us, 2),
                      "algorithmic_bytes_per_launch": int(avg_bytes)},
         "cpu_baseline": cpu,
