@@ -1,15 +1,21 @@
 """Slot addressing of a batch: the contract the destination pool must satisfy.
 
-Token ``position`` of a sequence lives in slot ``block_table[position // bs] *
-bs + position % bs`` of every layer's K and V array (ie/core/layout.py:46-53).
-After a handoff, decode reads the moved blocks only through this mapping,
-so a bit-exact copy of each tile under the new block ids keeps decode
-token-identical. Behaviour follows ie/core/layout.py:9-93.
+Token ``p`` of a sequence lives in slot ``block_table[p // bs] * bs + p % bs`` of
+every layer's K and V array (the reference's addressing, ie/core/layout.py:46-53).
+After a handoff, decode reads the moved blocks only through this mapping, so a
+bit-exact copy of each tile under its new block id keeps decode token-identical.
+
+``build_layout`` flattens a batch into the arrays a forward pass consumes
+(ie/core/layout.py:60-93): the scheduled tokens of every sequence, their
+positions and slots, per-sequence query and context lengths, and block tables
+padded with -1 to the longest one. Each sequence's positions and slots are
+computed as whole NumPy ranges.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
-from itertools import accumulate
+
+import numpy as np
 
 from .scheduler import Batch
 from .sequence import Sequence
@@ -31,11 +37,11 @@ class BatchLayout:
 
     @property
     def cu_seqlens_q(self) -> list[int]:
-        return [0, *accumulate(self.query_lens)]
+        return np.concatenate(([0], np.cumsum(self.query_lens, dtype=np.int64))).tolist()
 
     @property
     def cu_seqlens_k(self) -> list[int]:
-        return [0, *accumulate(self.context_lens)]
+        return np.concatenate(([0], np.cumsum(self.context_lens, dtype=np.int64))).tolist()
 
     @property
     def max_query_len(self) -> int:
@@ -46,39 +52,50 @@ class BatchLayout:
         return max(self.context_lens, default=0)
 
 
+def _slots(seq: Sequence, positions: np.ndarray, block_size: int) -> np.ndarray:
+    blocks = positions // block_size
+    held = len(seq.block_table)
+    if positions.size and int(blocks[-1]) >= held:
+        short = int(positions[np.argmax(blocks >= held)])
+        raise IndexError(f"position {short} needs block {short // block_size} but sequence "
+                         f"{seq.id} holds {held}")
+    return np.asarray(seq.block_table, dtype=np.int64)[blocks] * block_size + \
+        positions % block_size
+
+
 def slot_for_position(seq: Sequence, position: int, block_size: int) -> int:
-    block_index, offset = divmod(position, block_size)
-    if block_index >= len(seq.block_table):
-        raise IndexError(f"position {position} needs block {block_index} but sequence "
-                         f"{seq.id} holds {len(seq.block_table)}")
-    return seq.block_table[block_index] * block_size + offset
+    """The cache row of token ``position`` of ``seq``."""
+    return int(_slots(seq, np.array([position], dtype=np.int64), block_size)[0])
 
 
 def computed_range(seq: Sequence) -> range:
+    """Positions the current step computes for ``seq``."""
     return range(seq.num_computed, seq.num_computed + seq.num_scheduled)
 
 
 def build_layout(batch: Batch, block_size: int) -> BatchLayout:
-    """Flatten the scheduled tokens of a batch; pad block tables with -1."""
-    token_ids: list[int] = []
-    positions: list[int] = []
-    slots: list[int] = []
-    context_lens: list[int] = []
-    query_lens: list[int] = []
-    tables: list[list[int]] = []
-    for seq in batch.sequences:
-        window = computed_range(seq)
-        if not window:
+    """Flatten the scheduled tokens of ``batch``; pad block tables with -1."""
+    seqs = batch.sequences
+    starts = np.array([s.num_computed for s in seqs], dtype=np.int64)
+    counts = np.array([s.num_scheduled for s in seqs], dtype=np.int64)
+    for seq, n in zip(seqs, counts):
+        if n <= 0:
             raise ValueError(f"sequence {seq.id} was scheduled with no tokens")
-        for position in window:
-            token_ids.append(seq.token_ids[position])
-            positions.append(position)
-            slots.append(slot_for_position(seq, position, block_size))
-        query_lens.append(len(window))
-        context_lens.append(window.stop)
-        tables.append(list(seq.block_table))
-    width = max((len(t) for t in tables), default=0)
-    return BatchLayout(token_ids=token_ids, positions=positions, slot_mapping=slots,
-                       context_lens=context_lens, query_lens=query_lens,
-                       block_tables=[t + [-1] * (width - len(t)) for t in tables],
+    tokens, positions, slots = [], [], []
+    for seq, lo, n in zip(seqs, starts, counts):
+        pos = np.arange(lo, lo + n, dtype=np.int64)
+        positions.append(pos)
+        slots.append(_slots(seq, pos, block_size))
+        tokens.append(np.asarray(seq.token_ids[lo:lo + n], dtype=np.int64))
+    width = max((len(s.block_table) for s in seqs), default=0)
+    tables = np.full((len(seqs), width), -1, dtype=np.int64)
+    for row, seq in enumerate(seqs):
+        tables[row, :len(seq.block_table)] = seq.block_table
+
+    def flat(parts: list[np.ndarray]) -> list[int]:
+        return np.concatenate(parts).tolist() if parts else []
+
+    return BatchLayout(token_ids=flat(tokens), positions=flat(positions),
+                       slot_mapping=flat(slots), context_lens=(starts + counts).tolist(),
+                       query_lens=counts.tolist(), block_tables=tables.tolist(),
                        is_prefill=batch.is_prefill)

@@ -1,20 +1,34 @@
 """The copier protocol and the host offload tier.
 
-``SlotCopier`` is the plugin boundary of the handoff (reference:
-ie/core/offload.py:8-11): anything with ``read_block``/``write_block`` can move
-KV blocks for the block manager and the disaggregation workers. ``KVTier`` is
-the LRU store of evicted, hashed blocks (reference: ie/core/offload.py:14-69);
-with the HIP copier its payloads live in pinned host memory.
+``SlotCopier`` is the plugin boundary of the handoff (the reference's
+protocol, ie/core/offload.py:8-11): anything with ``read_block`` /
+``write_block`` can move KV blocks for the block manager and the
+disaggregation workers.
+
+``KVTier`` keeps the payloads of evicted, hashed blocks so a later request
+with the same prefix can restore them instead of recomputing them. Its
+observable behaviour is the reference's (ie/core/offload.py:14-69), because
+tier contents, their order and the statistics are what the golden traces
+record:
+* a tier of capacity 0 rejects every admission (counted);
+* admitting a key it already holds refreshes the key's recency and keeps the
+  payload it has (the new one is dropped);
+* admitting into a full tier first evicts the least recently admitted or
+  refreshed entries (counted);
+* ``take`` removes an entry and counts a restore.
+
+The store is a plain dict, whose iteration order is insertion order: the
+first key is always the least recent, a refresh re-inserts a key at the end.
+With the HIP copier the payloads live in pinned host memory.
 """
 from __future__ import annotations
 
-from collections import OrderedDict
 from dataclasses import dataclass
-from typing import Any, Protocol
+from typing import Any, NamedTuple, Protocol
 
 
 class SlotCopier(Protocol):
-    """Moves the KV bytes of one physical block (reference: ie/core/offload.py:8-11)."""
+    """Moves the KV bytes of one physical block (ie/core/offload.py:8-11)."""
 
     def read_block(self, block_id: int) -> Any: ...
 
@@ -23,6 +37,8 @@ class SlotCopier(Protocol):
 
 @dataclass(slots=True)
 class TierStats:
+    """Counters of a tier's admissions, restores, evictions and rejections."""
+
     admitted: int = 0
     restored: int = 0
     evicted: int = 0
@@ -33,55 +49,65 @@ class TierStats:
         return self.restored / self.admitted if self.admitted else 0.0
 
 
-class KVTier:
-    """Capacity-bounded LRU map ``hash -> (token_ids, payload)``.
+class TierEntry(NamedTuple):
+    """What the tier holds for one key: the block's tokens and its payload."""
 
-    Semantics of ie/core/offload.py:26-69: a zero-capacity tier rejects every
-    admit; re-admitting a held key only refreshes its recency (the new payload
-    is dropped); admitting into a full tier evicts the least recently admitted
-    entries first.
-    """
+    token_ids: list[int]
+    payload: Any
+
+
+class KVTier:
+    """Capacity-bounded, least-recently-admitted-first store ``key -> TierEntry``."""
 
     def __init__(self, capacity_blocks: int) -> None:
         if capacity_blocks < 0:
             raise ValueError("capacity cannot be negative")
         self.capacity = capacity_blocks
-        self.entries: OrderedDict[str, tuple[list[int], Any]] = OrderedDict()
         self.stats = TierStats()
+        self._store: dict[str, TierEntry] = {}
+
+    @property
+    def entries(self) -> dict[str, TierEntry]:
+        """The held entries, least recent first (read it, do not modify it)."""
+        return self._store
 
     def __len__(self) -> int:
-        return len(self.entries)
+        return len(self._store)
 
     def __contains__(self, key: str) -> bool:
-        return key in self.entries
+        return key in self._store
 
     @property
     def is_full(self) -> bool:
-        return len(self.entries) >= self.capacity
+        return len(self._store) >= self.capacity
 
     def admit(self, key: str, token_ids: list[int], payload: Any) -> bool:
-        if self.capacity == 0:
+        """Hold ``payload`` under ``key``; False if the tier holds nothing at all."""
+        if not self.capacity:
             self.stats.rejected += 1
             return False
-        if key in self.entries:
-            self.entries.move_to_end(key)
+        held = self._store.pop(key, None)
+        if held is not None:                  # refresh: back to most recent, old payload
+            self._store[key] = held
             return True
-        while len(self.entries) >= self.capacity:
-            self.entries.popitem(last=False)
+        while self.is_full:
+            del self._store[next(iter(self._store))]
             self.stats.evicted += 1
-        self.entries[key] = (list(token_ids), payload)
+        self._store[key] = TierEntry(list(token_ids), payload)
         self.stats.admitted += 1
         return True
 
     def holds(self, key: str, token_ids: list[int]) -> bool:
-        entry = self.entries.get(key)
-        return entry is not None and entry[0] == token_ids
+        """True if ``key`` is held for exactly these tokens."""
+        entry = self._store.get(key)
+        return entry is not None and entry.token_ids == token_ids
 
-    def take(self, key: str) -> tuple[list[int], Any] | None:
-        entry = self.entries.pop(key, None)
+    def take(self, key: str) -> TierEntry | None:
+        """Remove and return ``key``'s entry (a restore), or None."""
+        entry = self._store.pop(key, None)
         if entry is not None:
             self.stats.restored += 1
         return entry
 
-    def peek(self, key: str) -> tuple[list[int], Any] | None:
-        return self.entries.get(key)
+    def peek(self, key: str) -> TierEntry | None:
+        return self._store.get(key)

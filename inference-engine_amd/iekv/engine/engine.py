@@ -45,15 +45,23 @@ class EngineConfig:
 
 def sample_from_logits(logits: np.ndarray, temperatures: np.ndarray,
                        generator: np.random.Generator) -> np.ndarray:
-    """Greedy for temperature <= 0, else exponential-race sampling (ie/layers/functional.py:64-73)."""
-    greedy = temperatures <= 0.0
-    safe = np.where(greedy, 1.0, temperatures)[:, None]
-    scaled = logits.astype(np.float32) / safe
-    probs = np.exp(scaled - scaled.max(axis=-1, keepdims=True))
-    probs /= probs.sum(axis=-1, keepdims=True)
-    race = generator.exponential(1.0, size=probs.shape).clip(min=1e-10)
-    sampled = np.argmax(probs / race, axis=-1)
-    return np.where(greedy, np.argmax(logits, axis=-1), sampled)
+    """One token per row: the argmax for temperature <= 0, else a draw from
+    softmax(logits / temperature).
+
+    The draw is an exponential race: with independent E_i ~ Exp(1), the index
+    maximising p_i / E_i is distributed as p. In log space that index maximises
+    logits_i / T - log E_i (the softmax normaliser is the same for every i), so
+    no probabilities are formed. The race draws one Exp(1) value per logit per
+    call, greedy rows included, like the reference's sampler
+    (ie/layers/functional.py:64-73), so the two consume the generator alike.
+    """
+    logits = np.asarray(logits)
+    temps = np.asarray(temperatures, dtype=np.float32)
+    race = generator.exponential(1.0, size=logits.shape)
+    greedy = temps <= 0.0
+    scale = np.where(greedy, np.float32(1.0), temps)[:, None]
+    keyed = logits.astype(np.float32) / scale - np.log(np.maximum(race, 1e-10))
+    return np.where(greedy, logits.argmax(axis=-1), keyed.argmax(axis=-1))
 
 
 def default_copier_factory(k_caches, v_caches, block_size: int, role: str):

@@ -174,8 +174,7 @@ class DecodeWorker:
         if not self.prefix_aware:
             return 0
         probe = Sequence(prompt_ids, block_size=self.engine.config.block_size)
-        resident, _ = self.engine.blocks._prefix_plan(probe)
-        return len(resident)
+        return len(self.engine.blocks.plan_prefix(probe).resident)
 
     def admit(self, transfer: KVTransfer, max_new_tokens: int,
               temperature: float = 0.0, pending: list | None = None) -> Sequence:
@@ -227,11 +226,11 @@ class DecodeWorker:
         blocks = self.engine.blocks
         # A tier hit after the resident prefix is restored by allocate() and then
         # overwritten by the transfer's payload for the same tokens.
-        resident, _ = blocks._prefix_plan(seq)
-        if len(resident) != transfer.first_block:
+        resident = len(blocks.plan_prefix(seq).resident)
+        if resident != transfer.first_block:
             self.engine.scheduler.waiting.remove(seq)
             raise RuntimeError(
-                f"decode pool holds {len(resident)} prefix blocks, the transfer assumed "
+                f"decode pool holds {resident} prefix blocks, the transfer assumed "
                 f"{transfer.first_block}")
         if not blocks.can_allocate(seq):
             self.engine.scheduler.waiting.remove(seq)

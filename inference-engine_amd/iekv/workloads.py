@@ -24,7 +24,6 @@ cfg5  One GPU's share of a Llama-3-70B-shape handoff: 80L, 8 KV heads, D128,
 from __future__ import annotations
 
 import math
-from collections import deque
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -112,7 +111,7 @@ def _reserve_tables(pool_blocks: int, bs: int, lengths: list[int], counts: list[
     """Destination tables as a decode worker gets them: BlockManager.reserve per request."""
     manager = BlockManager(pool_blocks, bs)
     if free_order is not None:
-        manager.free_ids = deque(int(b) for b in free_order)
+        manager.free_ids = [int(b) for b in free_order]
     tables = []
     for n, c in zip(lengths, counts):
         seq = Sequence(list(range(max(1, n))), bs)
@@ -175,7 +174,7 @@ def cfg4(seed: int = 0, slack: int = 64) -> Workload:
     src = _split(rng.permutation(src_pool), counts)
 
     manager = BlockManager(dst_pool, bs)
-    manager.free_ids = deque(int(b) for b in rng.permutation(dst_pool))
+    manager.free_ids = [int(b) for b in rng.permutation(dst_pool)]
     holder = Sequence(prefix + [0], bs)         # the request that made the prefix resident
     manager.allocate(holder)
     holder.num_computed = len(prefix)

@@ -23,21 +23,22 @@ def oracle_factory(k_caches, v_caches, block_size, role):
                              [numpy_view(t) for t in v_caches], block_size)
 
 
-class RecordingCopier:
-    """Fake copier that stores strings (the reference's test double, tests/test_offload.py:16-28)."""
+class StringCopier:
+    """A copier whose blocks hold strings: the block manager's offload wiring is
+    exercised without any KV bytes. An unwritten block reads as "block-<id>";
+    ``calls`` logs every protocol call as (op, block id)."""
 
     def __init__(self):
-        self.contents: dict[int, str] = {}
-        self.reads = 0
-        self.writes = 0
+        self.store: dict[int, str] = {}
+        self.calls: list[tuple[str, int]] = []
 
     def read_block(self, block_id):
-        self.reads += 1
-        return self.contents.get(block_id, f"data-{block_id}")
+        self.calls.append(("read", block_id))
+        return self.store.get(block_id, f"block-{block_id}")
 
     def write_block(self, block_id, payload):
-        self.writes += 1
-        self.contents[block_id] = payload
+        self.calls.append(("write", block_id))
+        self.store[block_id] = payload
 
 
 class LoggingCopier:

@@ -80,9 +80,10 @@ def test_decode_is_token_identical_after_the_handoff(gpu, cache_dtype):
                                                              temperature=0.0)
     direct = DisaggregatedEngine(m, engine_config(), mode="direct").generate(
         G["prompts"], max_new_tokens=10, temperature=0.0)
+    # Identity is among this build's own paths: the model's float32 products on the
+    # GPU need not round like the reference's NumPy ones, so its golden tokens are
+    # asserted on the CPU (test_disaggregation.py).
     assert packed == direct == colocated
-    if cache_dtype == torch.float32:
-        print("golden (NumPy reference) tokens equal:", packed == G["disaggregated"]["10"])
 
 
 def test_the_decode_worker_refuses_a_cache_it_cannot_hold_on_gpu(gpu):
@@ -136,7 +137,6 @@ def test_offload_tier_on_gpu_matches_the_reference_trace(gpu, capacity):
         held = next(iter(engine.blocks.tier.entries.values()))[1]
         assert held.packed.on_host
     # Token values come from a GPU model run; their invariance is the next test's job.
-    print("revisit tokens equal the NumPy reference's:", revisit == want["revisit"])
 
 
 def test_offload_does_not_change_tokens_on_gpu(gpu):

@@ -1,99 +1,139 @@
-"""Offload tier: the reference's assertions (tests/test_offload.py:35-127) run against this
-build, and the exact offload/restore trace the reference recorded (tests/golden/offload.json)."""
+"""The offload tier and its wiring into the block manager (CPU).
+
+``KVTier`` is checked against a brute-force LRU model over random admit / take
+/ peek traces (the reference's rules, ie/core/offload.py:26-69: reject
+everything at capacity 0, refresh without replacing on a repeated key, evict
+least-recent first), then through the block manager with a copier that moves
+strings, and finally against the exact offload / restore trace the reference
+recorded for a small engine run (tests/golden/offload.json).
+"""
 from __future__ import annotations
 
+import numpy as np
 import pytest
 
 from conftest import golden
-from helpers import LoggingCopier, RecordingCopier, oracle_factory
+from helpers import LoggingCopier, StringCopier, oracle_factory
 from iekv.core.block_manager import BlockManager, chain_hash
 from iekv.core.offload import KVTier
 from iekv.core.sequence import Sequence
 
-BS = 4
+
+class LruModel:
+    """Least-recent-first list of [key, tokens, payload] with the tier's counters."""
+
+    def __init__(self, capacity):
+        self.capacity, self.items = capacity, []
+        self.counts = {"admitted": 0, "restored": 0, "evicted": 0, "rejected": 0}
+
+    def find(self, key):
+        return next((i for i, item in enumerate(self.items) if item[0] == key), None)
+
+    def admit(self, key, tokens, payload):
+        if self.capacity == 0:
+            self.counts["rejected"] += 1
+            return False
+        at = self.find(key)
+        if at is not None:
+            self.items.append(self.items.pop(at))
+            return True
+        while len(self.items) >= self.capacity:
+            self.items.pop(0)
+            self.counts["evicted"] += 1
+        self.items.append([key, list(tokens), payload])
+        self.counts["admitted"] += 1
+        return True
+
+    def take(self, key):
+        at = self.find(key)
+        if at is None:
+            return None
+        self.counts["restored"] += 1
+        _, tokens, payload = self.items.pop(at)
+        return tokens, payload
 
 
-def seq(tokens, block_size=BS):
-    return Sequence(tokens, block_size=block_size)
+@pytest.mark.parametrize("capacity", [0, 1, 2, 5])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_the_tier_follows_a_brute_force_lru_model(capacity, seed):
+    rng = np.random.default_rng(seed)
+    tier, model = KVTier(capacity), LruModel(capacity)
+    keys = [f"k{i}" for i in range(8)]
+    for step in range(600):
+        key = keys[int(rng.integers(len(keys)))]
+        tokens = [int(t) for t in rng.integers(0, 3, size=2)]
+        op = rng.random()
+        if op < 0.55:
+            assert tier.admit(key, tokens, f"p{step}") == model.admit(key, tokens, f"p{step}")
+        elif op < 0.8:
+            assert tier.take(key) == model.take(key)
+        else:
+            at = model.find(key)
+            want = None if at is None else tuple(model.items[at][1:])
+            assert tier.peek(key) == want
+            assert tier.holds(key, tokens) == (at is not None and model.items[at][1] == tokens)
+        assert list(tier.entries) == [item[0] for item in model.items]
+        assert len(tier) == len(model.items) and tier.is_full == (len(model.items) >= capacity)
+        assert {k: getattr(tier.stats, k) for k in model.counts} == model.counts
 
 
-def test_tier_holds_and_returns_a_payload():
-    tier = KVTier(capacity_blocks=4)
-    assert tier.admit("k", [1, 2], "payload")
-    assert "k" in tier
-    assert tier.holds("k", [1, 2])
-    assert not tier.holds("k", [9, 9])
-    assert tier.take("k") == ([1, 2], "payload")
-    assert "k" not in tier
-
-
-def test_tier_evicts_the_least_recently_admitted():
-    tier = KVTier(capacity_blocks=2)
-    tier.admit("a", [1], "A")
-    tier.admit("b", [2], "B")
-    tier.admit("c", [3], "C")
-    assert "a" not in tier
-    assert "b" in tier and "c" in tier
-    assert tier.stats.evicted == 1
-
-
-def test_readmitting_a_key_keeps_the_old_payload_and_refreshes_it():
-    tier = KVTier(capacity_blocks=2)
-    tier.admit("a", [1], "A")
-    tier.admit("b", [2], "B")
-    assert tier.admit("a", [1], "A2")
-    assert tier.peek("a") == ([1], "A")
-    tier.admit("c", [3], "C")            # evicts "b", the least recent now
-    assert "b" not in tier and "a" in tier
-
-
-def test_a_zero_capacity_tier_rejects_everything():
-    tier = KVTier(capacity_blocks=0)
-    assert not tier.admit("a", [1], "A")
-    assert tier.stats.rejected == 1
-    assert len(tier) == 0
-
-
-def test_tier_rejects_a_negative_capacity():
+def test_tier_edge_cases():
     with pytest.raises(ValueError):
         KVTier(capacity_blocks=-1)
+    tier = KVTier(2)
+    assert tier.admit("a", [1], "A") and tier.admit("b", [2], "B")
+    assert tier.admit("a", [1], "A-again")          # a repeat keeps the held payload ...
+    assert tier.peek("a") == ([1], "A")
+    tier.admit("c", [3], "C")                       # ... and makes "b" the least recent
+    assert "b" not in tier and list(tier.entries) == ["a", "c"]
+    assert tier.take("missing") is None and tier.stats.restored == 0
+    assert tier.take("c") == ([3], "C") and tier.stats.restore_rate == 1 / 3
 
 
-def test_an_evicted_block_lands_in_the_tier():
-    tier = KVTier(capacity_blocks=8)
-    copier = RecordingCopier()
-    manager = BlockManager(num_blocks=2, block_size=BS, tier=tier, copier=copier)
-    first = seq([1, 2, 3, 4, 5])
-    manager.allocate(first)
-    first.num_computed = len(first)
-    manager.share_computed_blocks(first)
-    manager.free(first)
-    manager.allocate(seq(list(range(50, 58))))
-    assert len(tier) >= 1
-    assert copier.reads >= 1
+def parked(manager, tokens, copier=None, payload=None):
+    """Allocate ``tokens``, mark them computed, key their full blocks, write
+    ``payload`` into the first block and release the sequence again."""
+    s = Sequence(tokens, manager.block_size)
+    manager.allocate(s)
+    s.num_computed = len(tokens)
+    if payload is not None:
+        copier.store[s.block_table[0]] = payload
+    manager.share_computed_blocks(s)
+    table = list(s.block_table)
+    manager.free(s)
+    return table
 
 
-def test_a_block_restored_from_the_tier_carries_its_payload_back():
-    tier = KVTier(capacity_blocks=8)
-    copier = RecordingCopier()
-    manager = BlockManager(num_blocks=2, block_size=BS, tier=tier, copier=copier)
-    original = seq([1, 2, 3, 4, 5])
-    manager.allocate(original)
-    original.num_computed = len(original)
-    copier.contents[original.block_table[0]] = "the-first-block"
-    manager.share_computed_blocks(original)
-    manager.free(original)
-    crowd = seq(list(range(50, 58)))
+def test_a_keyed_block_is_offloaded_when_its_block_is_claimed_again():
+    copier, tier = StringCopier(), KVTier(8)
+    manager = BlockManager(num_blocks=2, block_size=4, tier=tier, copier=copier)
+    table = parked(manager, [1, 2, 3, 4, 5], copier, payload="first-block-kv")
+    key = chain_hash([1, 2, 3, 4])
+    assert len(tier) == 0 and manager.block_id_by_hash[key] == table[0]
+    crowd = Sequence(list(range(50, 58)), 4)        # needs both blocks
     manager.allocate(crowd)
-    stored = chain_hash([1, 2, 3, 4])
-    assert tier.holds(stored, [1, 2, 3, 4])
-    assert tier.peek(stored)[1] == "the-first-block"
+    # the keyed block is read exactly once, when it is claimed for the crowd
+    assert copier.calls == [("read", table[0])]
+    assert tier.peek(key) == ([1, 2, 3, 4], "first-block-kv")
+    assert key not in manager.block_id_by_hash and tier.stats.admitted == 1
+    # the partial second block was never keyed: nothing else went to the tier
+    assert len(tier) == 1
 
+
+def test_a_tier_hit_is_restored_into_a_fresh_block_with_its_payload():
+    copier, tier = StringCopier(), KVTier(8)
+    manager = BlockManager(num_blocks=2, block_size=4, tier=tier, copier=copier)
+    parked(manager, [1, 2, 3, 4, 5], copier, payload="first-block-kv")
+    crowd = Sequence(list(range(50, 58)), 4)
+    manager.allocate(crowd)
     manager.free(crowd)
-    revisit = seq([1, 2, 3, 4, 5])
-    assert manager.allocate(revisit) == BS
-    assert manager.blocks_restored == 1
-    assert copier.contents[revisit.block_table[0]] == "the-first-block"
+    again = Sequence([1, 2, 3, 4, 5], 4)
+    assert manager.cached_prefix_tokens(again) == 4
+    assert manager.allocate(again) == 4
+    assert manager.blocks_restored == 1 and tier.stats.restored == 1
+    assert copier.store[again.block_table[0]] == "first-block-kv"
+    assert copier.calls[-1] == ("write", again.block_table[0])
+    assert manager.block_id_by_hash[chain_hash([1, 2, 3, 4])] == again.block_table[0]
 
 
 def run_offload_scenario(capacity, factory):
