@@ -120,8 +120,9 @@ class Engine:
 
     def submit(self, prompt_ids: list[int], max_new_tokens: int = 32,
                temperature: float = 1.0, eos_id: int | None = None) -> Sequence:
-        seq = Sequence(prompt_ids, block_size=self.config.block_size,
-                       max_new_tokens=max_new_tokens, temperature=temperature, eos_id=eos_id)
+        """Queue a request; it starts at the next step the pool has room for it."""
+        seq = Sequence(prompt_ids, self.config.block_size, max_new_tokens=max_new_tokens,
+                       temperature=temperature, eos_id=eos_id)
         self.scheduler.add(seq)
         return seq
 
@@ -135,30 +136,40 @@ class Engine:
         self.blocks.flush_pending()
 
     def forward(self, batch):
+        """Run the model over a scheduled batch; returns (layout, last-token logits)."""
         self.flush_offloads()
         layout = build_layout(batch, self.config.block_size)
         hidden = self.model.forward(layout, self.k_caches, self.v_caches, self.config.block_size)
         return layout, self.model.logits_for_last_token_of_each(hidden, layout.query_lens)
 
-    def step(self) -> list[Sequence]:
+    def _advance(self):
+        """One scheduled step: forward, sample one token per sequence, commit.
+        Returns (batch, sequences that finished), or (None, []) when nothing ran."""
         batch = self.scheduler.schedule()
         if not batch:
-            return []
-        temperatures = np.array([s.temperature for s in batch.sequences], dtype=np.float32)
+            return None, []
         _, logits = self.forward(batch)
-        tokens = sample_from_logits(logits, temperatures, self.generator).tolist()
-        return self.scheduler.finish_step(batch, tokens)
+        temps = np.fromiter((s.temperature for s in batch.sequences), dtype=np.float32,
+                            count=len(batch))
+        tokens = sample_from_logits(logits, temps, self.generator)
+        return batch, self.scheduler.finish_step(batch, [int(t) for t in tokens])
+
+    def step(self) -> list[Sequence]:
+        """Run one step; returns the sequences it finished."""
+        return self._advance()[1]
 
     def run(self, max_steps: int = 100_000) -> list[Sequence]:
-        done: list[Sequence] = []
-        for _ in range(max_steps):
-            if not self.scheduler.has_work:
-                break
-            done.extend(self.step())
-        return done
+        """Step until every queued request finished (or ``max_steps``)."""
+        finished: list[Sequence] = []
+        steps = 0
+        while steps < max_steps and self.scheduler.has_work:
+            finished += self.step()
+            steps += 1
+        return finished
 
     def generate(self, prompts: list[list[int]], max_new_tokens: int = 32,
                  temperature: float = 1.0) -> list[list[int]]:
+        """Serve ``prompts`` to completion; the generated tokens of each, in order."""
         seqs = [self.submit(p, max_new_tokens=max_new_tokens, temperature=temperature)
                 for p in prompts]
         self.run()

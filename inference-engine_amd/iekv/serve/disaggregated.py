@@ -36,10 +36,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Any, Callable
 
-import numpy as np
-
 from ..core.sequence import Sequence, Status
-from ..engine.engine import CopierFactory, Engine, EngineConfig, sample_from_logits
+from ..engine.engine import CopierFactory, Engine, EngineConfig
 
 MODES = ("pack", "direct")
 
@@ -342,12 +340,8 @@ class DisaggregatedEngine:
         (the decode loop of ie/serve/disaggregated.py:117-129)."""
         engine = self.decode.engine
         while engine.scheduler.has_work:
-            batch = engine.scheduler.schedule()
-            if not batch:
+            batch, _ = engine._advance()
+            if batch is None:
                 break
-            _, logits = engine.forward(batch)
-            temps = np.array([s.temperature for s in batch.sequences], dtype=np.float32)
-            tokens = sample_from_logits(logits, temps, engine.generator).tolist()
-            engine.scheduler.finish_step(batch, tokens)
             self.stats.decodes += 1
             self.stats.decode_tokens += len(batch)
