@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 9
+#define IEKV_ABI_VERSION 10
 
 enum {
   IEKV_OK = 0,
@@ -141,6 +141,31 @@ int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, c
 int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
                      const int32_t* block_table, int32_t context_len, void* out,
                      int64_t out_bytes, hipStream_t stream);
+
+/* write_kv for several layers in one launch: for l < n_layers, row i of layer
+ * l of k (and of v), each tile_bytes/block_size bytes at k + l * layer_stride +
+ * i * row bytes, lands in row slots[i] (int64, device memory) of K array
+ * first_layer + l (and of V array L + first_layer + l). Rows whose slot is
+ * outside the pool are skipped. layer_stride may be 0 (every layer takes the
+ * same rows).
+ * Replaces: the reference's write_kv call in each layer's forward
+ * (ie/kernels/reference.py:45-51 / ie/kernels/torch_backend.py:13-16, called
+ * once per layer from ie/model/transformer.py:105-110), n_layers calls at once. */
+int iekv_write_slots_layers(const iekv_pool* pool, int32_t first_layer, int32_t n_layers,
+                            int32_t block_size, const void* k, const void* v,
+                            int64_t layer_stride, const int64_t* slots, int32_t n_tokens,
+                            hipStream_t stream);
+
+/* gather_context for several arrays in one launch: out is [n_arrays][context_len]
+ * [row] bytes (out_bytes checked); its slab y holds the context of array
+ * first_array + y, row j = row block_table[j / block_size] * block_size +
+ * j % block_size of that array. Rows of out-of-range blocks are left untouched.
+ * Replaces: the reference's gather_context calls for the K and V cache of every
+ * layer (ie/kernels/reference.py:54-63, ie/kernels/torch_backend.py:19-24, once
+ * per array per layer in paged attention), n_arrays calls at once. */
+int iekv_gather_rows_arrays(const iekv_pool* pool, int32_t first_array, int32_t n_arrays,
+                            int32_t block_size, const int32_t* block_table, int32_t context_len,
+                            void* out, int64_t out_bytes, hipStream_t stream);
 
 /* Largest host image iekv_offload and iekv_restore move directly between the
  * pool and pinned host memory (the move kernel reads or writes the host

@@ -386,56 +386,114 @@ kv_unpack_images(PoolView src, PoolView dst, const char* __restrict__ /*src_stag
 // Row kernels on either side of the handoff. A pool row is one token's
 // H x D values of one array (tile_bytes / block_size bytes); row r of array a
 // lives at base(a) + r * row_bytes, i.e. slot r of the reference's [N*bs, H, D]
-// array. One wave moves one row with lane-contiguous vectors; a workgroup
-// (four waves) moves four rows.
+// array. `lanes` lanes (a power of two, at most a wave) move one row with
+// lane-contiguous vectors, so a workgroup moves kThreads / lanes consecutive
+// rows of one array, and short rows do not leave most of a wave idle; a lane
+// keeps up to U vectors of its row in flight before storing them.
+// A launch covers `chunks` groups of rows in each of its arrays, workgroup w
+// taking group w % chunks of array w / chunks; with `xcd`, position w is
+// XCD-grouped (kv_plan.h), so each of the 8 XCDs walks its own contiguous
+// share of arrays and rows. The scatter takes the XCD grouping from the order
+// of pool-writing launches, the gather from that of staging-writing ones.
+// Measured on MI355X, one launch per request, every layer or array at once
+// (GB/s, one box):
+//   Llama-3-8B shape (2 KiB rows): scatter 5,351 plain order -> 6,407 grouped,
+//     with non-temporal loads and stores (6,188 with ordinary stores); gather
+//     6,050 plain -> 5,698 grouped, so the gather stays in plain order;
+//   70B share, fp8 (1 KiB rows): scatter 5,677 plain, 5,566 grouped;
+//   one tensor-parallel rank of the 8B shape (256 B rows): scatter 4,880 plain,
+//     4,480 grouped, 5,091 with ordinary accesses.
+// One row per lane group beat two to eight in flight on both shapes.
 constexpr int kWave = 64;
-constexpr int kRowsPerGroup = kThreads / kWave;
-constexpr int kRowUnroll = 4;  // vectors per lane in flight: a 4 KiB row in one step
+constexpr int kRowU = 4;  // vectors per lane in flight: a 4 KiB row in one step
+// Stores of the scatter are non-temporal when the launch setting asks for
+// non-temporal accesses (the gather's always are then).
+#ifndef IEKV_SCATTER_NT_STORES
+#define IEKV_SCATTER_NT_STORES 1
+#endif
 
-// One row of row_vecs vectors, moved by one wave: lane l takes vectors
-// l, l + 64, ..., loading up to kRowUnroll of them before storing them.
-template <typename V>
-__device__ __forceinline__ void move_row(gptr<const V> s, gptr<V> d, int row_vecs) {
-  for (int e = threadIdx.x % kWave; e < row_vecs; e += kRowUnroll * kWave) {
-    V r[kRowUnroll];
+struct RowShape {
+  int32_t row_vecs;  // vectors per row
+  int32_t lanes;     // lanes per row (a power of two dividing kWave)
+  int32_t chunks;    // groups of kThreads / lanes rows per array
+  int32_t xcd;       // 1: XCD-grouped workgroup positions
+};
+
+// The (array index, first row) of this workgroup.
+__device__ __forceinline__ void row_place(const RowShape& sh, int* array, int64_t* first) {
+  const int w = sh.xcd ? iekv_plan::xcd_grouped(blockIdx.x, gridDim.x) : blockIdx.x;
+  *array = w / sh.chunks;
+  *first = static_cast<int64_t>(w % sh.chunks) * (kThreads / sh.lanes);
+}
+
+// Row `row` (< n) of this workgroup's share: addr(row, &src, &dst) gives its
+// addresses, or false to skip it (an id outside the pool).
+template <typename V, bool NTL, bool NTS, typename RowAddr>
+__device__ __forceinline__ void move_row(int64_t first, int32_t n, const RowShape& sh,
+                                         RowAddr addr) {
+  const int lane = threadIdx.x & (sh.lanes - 1);
+  const int64_t row = first + threadIdx.x / sh.lanes;
+  gptr<const V> s;
+  gptr<V> d;
+  if (row >= n || !addr(row, &s, &d)) return;
+  for (int e = lane; e < sh.row_vecs; e += kRowU * sh.lanes) {
+    V v[kRowU];
 #pragma unroll
-    for (int u = 0; u < kRowUnroll; ++u)
-      if (e + u * kWave < row_vecs) r[u] = s[e + u * kWave];
+    for (int u = 0; u < kRowU; ++u)
+      if (e + u * sh.lanes < sh.row_vecs) v[u] = load_vec<V, NTL>(s + e + u * sh.lanes);
 #pragma unroll
-    for (int u = 0; u < kRowUnroll; ++u)
-      if (e + u * kWave < row_vecs) d[e + u * kWave] = r[u];
+    for (int u = 0; u < kRowU; ++u)
+      if (e + u * sh.lanes < sh.row_vecs) store_vec<V, NTS>(d + e + u * sh.lanes, v[u]);
   }
 }
 
-// write_kv: k/v row i (contiguous [n, row]) -> row slots[i] of arrays a_k / a_v.
-template <typename V>
+// write_kv over layers: row i of layer l of k (and of v), at
+// k + l * layer_stride + i * row_bytes, lands in row slots[i] of K array
+// first_layer + l (and of V array layers + first_layer + l). Array index y of
+// the launch is K of layer y for y < n_layers, then V.
+template <typename V, bool NTL, bool NTS>
 __global__ void __launch_bounds__(kThreads)
-kv_scatter_rows(PoolView pool, int32_t a_k, int32_t a_v, const char* __restrict__ k,
-                const char* __restrict__ v, const int64_t* __restrict__ slots, int32_t n,
-                int32_t row_vecs, int64_t pool_rows) {
-  const int i = blockIdx.x * kRowsPerGroup + threadIdx.x / kWave;
-  if (i >= n) return;
-  const int64_t slot = slots[i];
-  if (slot < 0 || slot >= pool_rows) return;  // never address outside the pool
-  const bool is_v = blockIdx.y != 0;
-  const int64_t row_bytes = static_cast<int64_t>(row_vecs) * sizeof(V);
-  move_row<V>(as_global<V>((is_v ? v : k) + i * row_bytes),
-              as_global<V>(array_base(pool, is_v ? a_v : a_k) + slot * row_bytes), row_vecs);
+kv_scatter_rows(PoolView pool, int32_t layers, int32_t first_layer, int32_t n_layers,
+                const char* __restrict__ k, const char* __restrict__ v, int64_t layer_stride,
+                const int64_t* __restrict__ slots, int32_t n, RowShape sh, int64_t pool_rows) {
+  int y;
+  int64_t first;
+  row_place(sh, &y, &first);
+  const bool is_v = y >= n_layers;
+  const int l = is_v ? y - n_layers : y;
+  const int64_t row_bytes = static_cast<int64_t>(sh.row_vecs) * sizeof(V);
+  const char* src = (is_v ? v : k) + l * layer_stride;
+  char* dst = array_base(pool, (is_v ? layers : 0) + first_layer + l);
+  move_row<V, NTL, NTS>(first, n, sh, [&](int64_t i, gptr<const V>* s, gptr<V>* d) {
+    const int64_t slot = slots[i];
+    if (slot < 0 || slot >= pool_rows) return false;  // never address outside the pool
+    *s = as_global<V>(src + i * row_bytes);
+    *d = as_global<V>(dst + slot * row_bytes);
+    return true;
+  });
 }
 
-// gather_context: out row j = row (table[j / bs] * bs + j % bs) of array a, j < n.
-template <typename V>
+// gather_context over arrays: out row j (j < n) of array first_array + y, at
+// out + y * out_stride + j * row_bytes, is row table[j / bs] * bs + j % bs of
+// that array.
+template <typename V, bool NTL, bool NTS>
 __global__ void __launch_bounds__(kThreads)
-kv_gather_rows(PoolView pool, int32_t a, const int32_t* __restrict__ table, int32_t bs,
-               char* __restrict__ out, int32_t n, int32_t row_vecs) {
-  const int j = blockIdx.x * kRowsPerGroup + threadIdx.x / kWave;
-  if (j >= n) return;
-  const int32_t block = table[j / bs];
-  if (block < 0 || block >= pool.num_blocks) return;
-  const int64_t row_bytes = static_cast<int64_t>(row_vecs) * sizeof(V);
-  const int64_t row = static_cast<int64_t>(block) * bs + j % bs;
-  move_row<V>(as_global<V>(array_base(pool, a) + row * row_bytes),
-              as_global<V>(out + j * row_bytes), row_vecs);
+kv_gather_rows(PoolView pool, int32_t first_array, const int32_t* __restrict__ table,
+               int32_t bs, char* __restrict__ out, int64_t out_stride, int32_t n,
+               RowShape sh) {
+  int y;
+  int64_t first;
+  row_place(sh, &y, &first);
+  const int64_t row_bytes = static_cast<int64_t>(sh.row_vecs) * sizeof(V);
+  const char* base = array_base(pool, first_array + y);
+  char* dst = out + y * out_stride;
+  move_row<V, NTL, NTS>(first, n, sh, [&](int64_t j, gptr<const V>* s, gptr<V>* d) {
+    const int32_t block = table[j / bs];
+    if (block < 0 || block >= pool.num_blocks) return false;
+    *s = as_global<V>(base + (static_cast<int64_t>(block) * bs + j % bs) * row_bytes);
+    *d = as_global<V>(dst + j * row_bytes);
+    return true;
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -650,6 +708,24 @@ int launch_images(const iekv_pool* dp, const InlineImages& images, const int32_t
   const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(n_blocks) * pl.units * pl.parts);
   return dispatch(k, grid, stream, PoolView{}, view_of(dp), nullptr, nullptr, images, dst_ids,
                   pl.tile_vecs, dp->n_arrays, n_blocks, pl.parts, pl.group, pl.order);
+}
+
+// The shape of a row launch over n rows in each of n_arrays arrays: lanes per
+// row (the smallest power of two with a vector of the row for every lane, at
+// most a wave), row groups per array, and the workgroup order. False when the
+// launch would exceed the dispatch limit.
+bool row_shape(int64_t row_bytes, int vec_bytes, int64_t n, int32_t n_arrays, bool xcd,
+               RowShape* sh, uint32_t* grid) {
+  sh->row_vecs = static_cast<int32_t>(row_bytes / vec_bytes);
+  sh->lanes = 1;
+  while (sh->lanes < kWave && sh->lanes < sh->row_vecs) sh->lanes <<= 1;
+  const int64_t per_group = kThreads / sh->lanes;
+  const int64_t chunks = (n + per_group - 1) / per_group;
+  if (chunks * n_arrays > kMaxGrid) return false;
+  sh->chunks = static_cast<int32_t>(chunks);
+  sh->xcd = xcd ? 1 : 0;
+  *grid = static_cast<uint32_t>(chunks * n_arrays);
+  return true;
 }
 
 int row_align(int64_t row_bytes, int pool_align, std::initializer_list<const void*> ptrs) {
@@ -1195,76 +1271,114 @@ int iekv_unpack_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_bloc
                                          stream);
 }
 
-int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, const void* k,
-                     const void* v, const int64_t* slots, int32_t n_tokens, hipStream_t stream) {
+int iekv_write_slots_layers(const iekv_pool* pool, int32_t first_layer, int32_t n_layers,
+                            int32_t block_size, const void* k, const void* v,
+                            int64_t layer_stride, const int64_t* slots, int32_t n_tokens,
+                            hipStream_t stream) {
   int rc;
   if ((rc = check_pool(pool, "destination"))) return rc;
   const int32_t layers = pool->n_arrays / 2;
-  if (pool->n_arrays % 2 || layer < 0 || layer >= layers)
-    return set_error(IEKV_ERR_INVALID, "layer %d out of range for %d layers", layer, layers);
+  if (pool->n_arrays % 2 || first_layer < 0 || n_layers <= 0 ||
+      first_layer > layers - n_layers)
+    return set_error(IEKV_ERR_INVALID, "layers %d..%d out of range for %d layers", first_layer,
+                     first_layer + n_layers - 1, layers);
   if (block_size <= 0 || pool->tile_bytes % block_size)
     return set_error(IEKV_ERR_INVALID, "block_size %d does not divide the %lld-byte tile",
                      block_size, static_cast<long long>(pool->tile_bytes));
+  if (layer_stride < 0)
+    return set_error(IEKV_ERR_INVALID, "layer_stride is negative (%lld)",
+                     static_cast<long long>(layer_stride));
   if (n_tokens < 0) return set_error(IEKV_ERR_INVALID, "n_tokens is negative (%d)", n_tokens);
   if (n_tokens == 0) return IEKV_OK;
-  if (n_tokens > kMaxGrid * kRowsPerGroup)
-    return set_error(IEKV_ERR_INVALID, "%d tokens exceed one launch", n_tokens);
   if (!k || !v || !slots) return set_error(IEKV_ERR_INVALID, "k, v or slots is null");
+  const int64_t row_bytes = pool->tile_bytes / block_size;
+  const int align = std::min(row_align(row_bytes, pool->align, {k, v}),
+                             layer_stride ? align_of_ptr(static_cast<uint64_t>(layer_stride))
+                                          : 16);
+  RowShape sh;
+  uint32_t grid = 0;
+  const int vec = align >= 16 ? 16 : align;
+  if (!row_shape(row_bytes, vec, n_tokens, 2 * n_layers,
+                 (g_order.load() & iekv_plan::kXcdGrouped) != 0, &sh, &grid))
+    return set_error(IEKV_ERR_INVALID, "%d tokens in %d layers exceed one launch", n_tokens,
+                     n_layers);
   DeviceGuard guard(pool->device);
   if (!guard.ok()) return guard.fail();
-  const int64_t row_bytes = pool->tile_bytes / block_size;
-  const int align = row_align(row_bytes, pool->align, {k, v});
-  const dim3 grid((n_tokens + kRowsPerGroup - 1) / kRowsPerGroup, 2);
   const int64_t pool_rows = pool->num_blocks * block_size;
   const char* kc = static_cast<const char*>(k);
   const char* vc = static_cast<const char*>(v);
   const PoolView view = view_of(pool);
-  const int32_t ak = layer, av = layers + layer;
+  const bool nt = g_nontemporal.load() != 0;
+  constexpr bool kNts = IEKV_SCATTER_NT_STORES != 0;
 #define IEKV_SCATTER(T)                                                                      \
-  dispatch(kv_scatter_rows<T>, grid, stream, view, ak, av, kc, vc, slots, n_tokens,          \
-           static_cast<int32_t>(row_bytes / sizeof(T)), pool_rows)
-  if (align >= 16) return IEKV_SCATTER(u32x4);
-  if (align >= 8) return IEKV_SCATTER(u32x2);
-  if (align >= 4) return IEKV_SCATTER(uint32_t);
-  if (align >= 2) return IEKV_SCATTER(uint16_t);
+  (nt ? dispatch(kv_scatter_rows<T, true, kNts>, dim3(grid), stream, view, layers,          \
+                 first_layer, n_layers, kc, vc, layer_stride, slots, n_tokens, sh, pool_rows) \
+      : dispatch(kv_scatter_rows<T, false, false>, dim3(grid), stream, view, layers,         \
+                 first_layer, n_layers, kc, vc, layer_stride, slots, n_tokens, sh, pool_rows))
+  if (vec >= 16) return IEKV_SCATTER(u32x4);
+  if (vec >= 8) return IEKV_SCATTER(u32x2);
+  if (vec >= 4) return IEKV_SCATTER(uint32_t);
+  if (vec >= 2) return IEKV_SCATTER(uint16_t);
   return IEKV_SCATTER(uint8_t);
 #undef IEKV_SCATTER
 }
 
-int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
-                     const int32_t* block_table, int32_t context_len, void* out,
-                     int64_t out_bytes, hipStream_t stream) {
+int iekv_write_slots(const iekv_pool* pool, int32_t layer, int32_t block_size, const void* k,
+                     const void* v, const int64_t* slots, int32_t n_tokens, hipStream_t stream) {
+  return iekv_write_slots_layers(pool, layer, 1, block_size, k, v, 0, slots, n_tokens, stream);
+}
+
+int iekv_gather_rows_arrays(const iekv_pool* pool, int32_t first_array, int32_t n_arrays,
+                            int32_t block_size, const int32_t* block_table, int32_t context_len,
+                            void* out, int64_t out_bytes, hipStream_t stream) {
   int rc;
   if ((rc = check_pool(pool, "source"))) return rc;
-  if (array < 0 || array >= pool->n_arrays)
-    return set_error(IEKV_ERR_INVALID, "array %d out of range for %d arrays", array,
-                     pool->n_arrays);
+  if (first_array < 0 || n_arrays <= 0 || first_array > pool->n_arrays - n_arrays)
+    return set_error(IEKV_ERR_INVALID, "arrays %d..%d out of range for %d arrays", first_array,
+                     first_array + n_arrays - 1, pool->n_arrays);
   if (block_size <= 0 || pool->tile_bytes % block_size)
     return set_error(IEKV_ERR_INVALID, "block_size %d does not divide the %lld-byte tile",
                      block_size, static_cast<long long>(pool->tile_bytes));
   if (context_len < 0)
     return set_error(IEKV_ERR_INVALID, "context_len is negative (%d)", context_len);
   if (context_len == 0) return IEKV_OK;
-  if (context_len > kMaxGrid * kRowsPerGroup)
-    return set_error(IEKV_ERR_INVALID, "context of %d rows exceeds one launch", context_len);
   const int64_t row_bytes = pool->tile_bytes / block_size;
-  if ((rc = check_buffer(out, out_bytes, row_bytes * context_len, "output"))) return rc;
+  const int64_t out_stride = row_bytes * context_len;
+  if (n_arrays > 1 && out_stride > INT64_MAX / n_arrays)
+    return set_error(IEKV_ERR_INVALID, "output size overflows");
+  if ((rc = check_buffer(out, out_bytes, out_stride * n_arrays, "output"))) return rc;
   if (!block_table) return set_error(IEKV_ERR_INVALID, "block_table is null");
+  const int align = row_align(row_bytes, pool->align, {out});
+  const int vec = align >= 16 ? 16 : align;
+  RowShape sh;
+  uint32_t grid = 0;
+  if (!row_shape(row_bytes, vec, context_len, n_arrays,
+                 (g_pack_order.load() & iekv_plan::kXcdGrouped) != 0, &sh, &grid))
+    return set_error(IEKV_ERR_INVALID, "a context of %d rows in %d arrays exceeds one launch",
+                     context_len, n_arrays);
   DeviceGuard guard(pool->device);
   if (!guard.ok()) return guard.fail();
-  const int align = row_align(row_bytes, pool->align, {out});
-  const dim3 grid((context_len + kRowsPerGroup - 1) / kRowsPerGroup);
   char* oc = static_cast<char*>(out);
   const PoolView view = view_of(pool);
+  const bool nt = g_nontemporal.load() != 0;
 #define IEKV_GATHER(T)                                                                      \
-  dispatch(kv_gather_rows<T>, grid, stream, view, array, block_table, block_size, oc,      \
-           context_len, static_cast<int32_t>(row_bytes / sizeof(T)))
-  if (align >= 16) return IEKV_GATHER(u32x4);
-  if (align >= 8) return IEKV_GATHER(u32x2);
-  if (align >= 4) return IEKV_GATHER(uint32_t);
-  if (align >= 2) return IEKV_GATHER(uint16_t);
+  (nt ? dispatch(kv_gather_rows<T, true, true>, dim3(grid), stream, view, first_array,      \
+                 block_table, block_size, oc, out_stride, context_len, sh)                  \
+      : dispatch(kv_gather_rows<T, false, false>, dim3(grid), stream, view, first_array,    \
+                 block_table, block_size, oc, out_stride, context_len, sh))
+  if (vec >= 16) return IEKV_GATHER(u32x4);
+  if (vec >= 8) return IEKV_GATHER(u32x2);
+  if (vec >= 4) return IEKV_GATHER(uint32_t);
+  if (vec >= 2) return IEKV_GATHER(uint16_t);
   return IEKV_GATHER(uint8_t);
 #undef IEKV_GATHER
+}
+
+int iekv_gather_rows(const iekv_pool* pool, int32_t array, int32_t block_size,
+                     const int32_t* block_table, int32_t context_len, void* out,
+                     int64_t out_bytes, hipStream_t stream) {
+  return iekv_gather_rows_arrays(pool, array, 1, block_size, block_table, context_len, out,
+                                 out_bytes, stream);
 }
 
 int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,

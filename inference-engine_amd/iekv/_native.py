@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most ids a host-id call takes
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
@@ -41,6 +41,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                  c_int32, c_void_p]),
     "iekv_gather_rows": (c_int, [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p,
                                  c_int64, c_void_p]),
+    "iekv_write_slots_layers": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                        c_int64, c_void_p, c_int32, c_void_p]),
+    "iekv_gather_rows_arrays": (c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_int32,
+                                        c_void_p, c_int64, c_void_p]),
     "iekv_offload": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p, c_int64,
                              c_void_p, c_void_p]),
     "iekv_offload_static": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p,

@@ -27,6 +27,7 @@ cache reads and writes exactly as the reference's synchronous copies are.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import weakref
 from typing import Any, Iterable, Sequence as Seq
@@ -399,9 +400,23 @@ class HipSlotCopier:
         self.write_blocks([block_id], [payload])
 
     # -- batched calls -------------------------------------------------------
-    def read_blocks(self, block_ids, *, location: str | None = None) -> PackedBlocks:
-        """Pack ``block_ids`` (in order) into a new payload buffer with one launch."""
-        out = self._gather(block_ids, location or self.payload_location)
+    @staticmethod
+    def _on(stream: torch.cuda.Stream | None):
+        """Run a call as if ``stream`` were the current stream (its launches, id uploads
+        and new buffers are then ordered on it); None keeps the current stream."""
+        return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+
+    def read_blocks(self, block_ids, *, location: str | None = None,
+                    stream: torch.cuda.Stream | None = None) -> PackedBlocks:
+        """Pack ``block_ids`` (in order) into a new payload buffer with one launch.
+
+        ``stream`` runs the call on that stream instead of the current one; the
+        caller orders it after the work that wrote the blocks. Independent
+        requests issued on different streams let one request's launch start
+        while the previous one drains.
+        """
+        with self._on(stream):
+            out = self._gather(block_ids, location or self.payload_location)
         self.blocks_read += len(out)
         return out
 
@@ -432,8 +447,17 @@ class HipSlotCopier:
                          out.data.data_ptr(), out.nbytes, stream.cuda_stream)
         return out
 
-    def write_blocks(self, block_ids, payloads) -> None:
-        """Scatter ``payloads[i]`` into ``block_ids[i]`` for every i (one launch when possible)."""
+    def write_blocks(self, block_ids, payloads, *,
+                     stream: torch.cuda.Stream | None = None) -> None:
+        """Scatter ``payloads[i]`` into ``block_ids[i]`` for every i (one launch when possible).
+
+        ``stream`` runs the call on that stream; it must be ordered after the work
+        that produced the payloads (the same stream as their read_blocks, say).
+        """
+        with self._on(stream):
+            self._write_blocks(block_ids, payloads)
+
+    def _write_blocks(self, block_ids, payloads) -> None:
         self.flush()   # queued reads see the blocks before this write
         ids = self._ids(block_ids, unique=True, what="destination block")
         n = len(ids)
@@ -494,8 +518,18 @@ class HipSlotCopier:
             root.mark(copy)
         self.restore_launches += 1
 
-    def copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids) -> None:
-        """Direct pool-to-pool move: tile ``src_ids[i]`` of ``source`` -> ``dst_ids[i]`` here."""
+    def copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids, *,
+                    stream: torch.cuda.Stream | None = None) -> None:
+        """Direct pool-to-pool move: tile ``src_ids[i]`` of ``source`` -> ``dst_ids[i]`` here.
+
+        ``stream`` runs the copy on that stream instead of the current one; the
+        caller orders it after the writes of the source blocks and orders later
+        readers of the destination blocks after it.
+        """
+        with self._on(stream):
+            self._copy_blocks(source, src_ids, dst_ids)
+
+    def _copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids) -> None:
         self.flush()
         if not self.pool.same_shape(source.pool):
             raise ValueError("source and destination pools differ in layout")

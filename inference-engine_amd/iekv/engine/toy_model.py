@@ -161,30 +161,23 @@ class ToyTransformer:
             pool = KVPool(k_caches, v_caches, block_size)
         return pool
 
-    def _context(self, cache: torch.Tensor, array: int, pool, table: list[int],
-                 context_len: int, block_size: int) -> torch.Tensor:
-        if pool is not None:
-            from .slots import gather_rows
-
-            return gather_rows(pool, array, table, context_len)
+    def _cached_rows(self, cache: torch.Tensor, table: list[int], context_len: int,
+                     block_size: int) -> torch.Tensor:
+        """Rows 0..context_len-1 of a sequence in one cache array (torch's index_select)."""
         needed = -(-context_len // block_size)
         blocks = torch.as_tensor(table[:needed], device=self.device, dtype=torch.long)
         within = torch.arange(block_size, device=self.device)
         slots = (blocks[:, None] * block_size + within[None, :]).reshape(-1)[:context_len]
         return cache.index_select(0, slots)
 
-    def _attend(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                layout: BatchLayout, block_size: int, layer: int = 0,
-                pool=None) -> torch.Tensor:
+    def _attend(self, q: torch.Tensor, contexts, layout: BatchLayout) -> torch.Tensor:
+        """Causal attention of each sequence's queries over its (K, V) context rows."""
         c = self.config
         group = c.num_heads // c.num_kv_heads
         outputs = []
         start = 0
-        for table, context_len, query_len in zip(layout.block_tables, layout.context_lens,
-                                                 layout.query_lens):
-            k = self._context(k_cache, layer, pool, table, context_len, block_size)
-            v = self._context(v_cache, c.num_layers + layer, pool, table, context_len,
-                              block_size)
+        for (k, v), context_len, query_len in zip(contexts, layout.context_lens,
+                                                  layout.query_lens):
             k = k.float().repeat_interleave(group, dim=1)
             v = v.float().repeat_interleave(group, dim=1)
             # [heads, tokens, dim] operands, made contiguous before the batched products.
@@ -202,12 +195,31 @@ class ToyTransformer:
 
     @torch.no_grad()
     def forward(self, layout: BatchLayout, k_caches, v_caches, block_size: int) -> torch.Tensor:
+        """One step over the layout's tokens; writes their K/V rows into the caches.
+
+        The torch path writes each layer's rows with index_copy_ and reads each
+        sequence's context back with index_select, layer by layer. With ``hip_kv``
+        the slot kernels do it in two kinds of launch: before the layers, one
+        iekv_gather_rows_arrays per sequence fetches its earlier context (the rows
+        before this step) from every layer's K and V cache; each layer then
+        attends over that context followed by this step's rows, cast to the cache
+        dtype exactly as a cache read returns them; after the layers, one
+        iekv_write_slots_layers writes every layer's new rows.
+        """
         c = self.config
         tokens = torch.as_tensor(layout.token_ids, device=self.device, dtype=torch.long)
         positions = torch.as_tensor(layout.positions, device=self.device, dtype=torch.long)
         slots = torch.as_tensor(layout.slot_mapping, device=self.device, dtype=torch.long)
         x = self.embedding[tokens]
         pool = self._pool(k_caches, v_caches, block_size) if self.hip_kv else None
+        if pool is not None:
+            from .slots import gather_rows_arrays, write_slots_layers
+
+            earlier = [gather_rows_arrays(pool, table, ctx - n) if ctx > n else None
+                       for table, ctx, n in zip(layout.block_tables, layout.context_lens,
+                                                layout.query_lens)]
+            new_k, new_v = [], []
+        bounds = np.concatenate(([0], np.cumsum(layout.query_lens))).tolist()
         for index, (layer, k_cache, v_cache) in enumerate(zip(self.layers, k_caches, v_caches)):
             normed = _rms_norm(x, layer.attn_norm, c.norm_eps)
             q = (normed @ layer.q_proj).view(-1, c.num_heads, c.head_dim)
@@ -215,18 +227,30 @@ class ToyTransformer:
             v = (normed @ layer.v_proj).view(-1, c.num_kv_heads, c.head_dim)
             q = _rope(q, positions, self.cos, self.sin, c.rope_halved)
             k = _rope(k, positions, self.cos, self.sin, c.rope_halved)
+            kc, vc = k.to(k_cache.dtype), v.to(v_cache.dtype)
             if pool is not None:
-                from .slots import write_slots
-
-                write_slots(pool, index, k, v, slots)
+                new_k.append(kc)
+                new_v.append(vc)
+                contexts = []
+                for s, prior in enumerate(earlier):
+                    ks, vs = kc[bounds[s]:bounds[s + 1]], vc[bounds[s]:bounds[s + 1]]
+                    if prior is not None:
+                        ks = torch.cat((prior[index], ks))
+                        vs = torch.cat((prior[c.num_layers + index], vs))
+                    contexts.append((ks, vs))
             else:
-                k_cache.index_copy_(0, slots, k.to(k_cache.dtype))
-                v_cache.index_copy_(0, slots, v.to(v_cache.dtype))
-            attended = self._attend(q, k_cache, v_cache, layout, block_size, index, pool)
+                k_cache.index_copy_(0, slots, kc)
+                v_cache.index_copy_(0, slots, vc)
+                contexts = [(self._cached_rows(k_cache, t, n, block_size),
+                             self._cached_rows(v_cache, t, n, block_size))
+                            for t, n in zip(layout.block_tables, layout.context_lens)]
+            attended = self._attend(q, contexts, layout)
             x = x + attended.reshape(-1, c.num_heads * c.head_dim) @ layer.o_proj
             normed = _rms_norm(x, layer.mlp_norm, c.norm_eps)
             gate = normed @ layer.gate_proj
             x = x + (gate / (1.0 + torch.exp(-gate)) * (normed @ layer.up_proj)) @ layer.down_proj
+        if pool is not None and layout.num_tokens:
+            write_slots_layers(pool, torch.stack(new_k), torch.stack(new_v), slots)
         return _rms_norm(x, self.final_norm, c.norm_eps)
 
     @torch.no_grad()

@@ -17,7 +17,8 @@ pytestmark = pytest.mark.gpu
 
 ROOT = Path(__file__).resolve().parents[1]
 LEGS = ["direct", "pack_unpack", "pack", "unpack", "batched", "copier", "copier_pack_unpack",
-        "write_kv", "gather_context", "host_roundtrip"]
+        "write_kv", "write_kv_per_layer", "gather_context", "gather_per_array",
+        "host_roundtrip"]
 
 
 def run_bench(*args):
@@ -53,10 +54,13 @@ def test_the_bench_line_keeps_its_contract(gpu, tp):
     assert line["dtype"] == "f32"
     cpu = line["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["cores"] == 1 and cpu["value"] > 0 and cpu["checked"]
-    # one launch per request and layer for write_kv, per request and array for gather_context
+    # one launch per request for write_kv and gather_context (every layer / array at once);
+    # per request and layer, and per request and array, for their reference-granularity legs
     legs = line["legs"]
-    assert legs["write_kv"]["launches_per_step"] == 64 * 4
-    assert legs["gather_context"]["launches_per_step"] == 64 * 8
+    assert legs["write_kv"]["launches_per_step"] == 64
+    assert legs["write_kv_per_layer"]["launches_per_step"] == 64 * 4
+    assert legs["gather_context"]["launches_per_step"] == 64
+    assert legs["gather_per_array"]["launches_per_step"] == 64 * 8
     assert legs["batched"]["launches_per_step"] == 1
     # the host tier's round trip: the whole block list each way, then one call per block
     host = legs["host_roundtrip"]

@@ -622,6 +622,48 @@ def test_a_hip_failure_raises_and_leaves_no_error_behind(gpu):
     assert_pool_equals(dk, dv, dst_o)
 
 
+def test_requests_issued_on_alternating_streams_are_bit_exact(gpu):
+    """Independent requests on two side streams (copy_blocks / read_blocks /
+    write_blocks with stream=), forked from and joined back into the current
+    stream: every destination tile equals the oracle's, source untouched."""
+    from iekv.engine.copier import HipSlotCopier
+
+    bs = 16
+    sk, sv = allocate(200, bs, 3, 4, 32, torch.bfloat16, gpu, seed=87)
+    dk, dv = allocate(200, bs, 3, 4, 32, torch.bfloat16, gpu, seed=88)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    rng = np.random.default_rng(89)
+    src_perm, dst_perm = rng.permutation(200), rng.permutation(200)
+    sizes = [int(n) for n in rng.integers(1, 12, size=16)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    main = torch.cuda.current_stream()
+    start = torch.cuda.Event()
+    start.record(main)
+    for st in streams:
+        st.wait_event(start)
+    at, src_tables, dst_tables = 0, [], []
+    for k, n in enumerate(sizes):
+        s_ids = [int(b) for b in src_perm[at:at + n]]
+        d_ids = [int(b) for b in dst_perm[at:at + n]]
+        at += n
+        st = streams[k % 2]
+        if k % 3:
+            dst.copy_blocks(src, s_ids, d_ids, stream=st)
+        else:
+            dst.write_blocks(d_ids, src.read_blocks(s_ids, stream=st), stream=st)
+        src_tables.append(s_ids)
+        dst_tables.append(d_ids)
+    for st in streams:
+        done = torch.cuda.Event()
+        done.record(st)
+        main.wait_event(done)
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, src_tables, dst_tables)
+    assert_pool_equals(dk, dv, dst_o)
+    assert_pool_equals(sk, sv, src_o)
+
+
 def test_host_payloads_through_the_copier(gpu):
     from iekv.engine.copier import HipSlotCopier
 

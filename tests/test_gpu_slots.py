@@ -76,6 +76,58 @@ def test_gather_rows_matches_gather_context(gpu, bs, heads, dim, dtype):
             assert np.array_equal(as_np(got), want), (context_len, array)
 
 
+@pytest.mark.parametrize("bs,heads,dim,dtype", CASES)
+def test_one_launch_writes_every_layer_like_write_kv_per_layer(gpu, bs, heads, dim, dtype):
+    """iekv_write_slots_layers: all four layers at once, then layers 1..2 with new
+    rows, then (layer_stride 0) the same rows into every layer; each against the
+    oracle's write_kv per layer."""
+    from iekv import _native
+    from iekv.engine.slots import write_slots_layers
+
+    L = 4
+    k, v, pool = random_pool(20, bs, heads, dim, dtype, gpu, layers=L, seed=5)
+    oracle_k = [as_np(t) for t in k]
+    oracle_v = [as_np(t) for t in v]
+    rng = np.random.default_rng(6)
+    for first, n_layers, seed in ((0, L, 30), (1, 2, 40)):
+        slots = [int(x) for x in rng.permutation(20 * bs)[:13]]
+        kr = random_rows(n_layers * 13, heads, dim, dtype, gpu, seed).view(n_layers, 13, heads, dim)
+        vr = random_rows(n_layers * 13, heads, dim, dtype, gpu, seed + 1).view(
+            n_layers, 13, heads, dim)
+        write_slots_layers(pool, kr, vr, slots, first_layer=first)
+        for l in range(n_layers):
+            write_kv(as_np(kr[l]), as_np(vr[l]), oracle_k[first + l], oracle_v[first + l], slots)
+    slots = [int(x) for x in rng.permutation(20 * bs)[:7]]
+    kr, vr = (random_rows(7, heads, dim, dtype, gpu, seed) for seed in (50, 51))
+    dev_slots = torch.tensor(slots, dtype=torch.int64, device=gpu)
+    _native.call("iekv_write_slots_layers", pool.native.handle, 0, L, bs, kr.data_ptr(),
+                 vr.data_ptr(), 0, dev_slots.data_ptr(), 7,
+                 torch.cuda.current_stream().cuda_stream)
+    for l in range(L):
+        write_kv(as_np(kr), as_np(vr), oracle_k[l], oracle_v[l], slots)
+    torch.cuda.synchronize()
+    for got, want in zip(k + v, oracle_k + oracle_v):
+        assert np.array_equal(as_np(got), want)
+
+
+@pytest.mark.parametrize("bs,heads,dim,dtype", CASES)
+def test_one_launch_gathers_every_array_like_gather_context(gpu, bs, heads, dim, dtype):
+    from iekv.engine.slots import gather_rows_arrays
+
+    k, v, pool = random_pool(20, bs, heads, dim, dtype, gpu, layers=3, seed=7)
+    rng = np.random.default_rng(8)
+    for context_len in (1, bs, 3 * bs + 1, 7 * bs):
+        needed = -(-context_len // bs)
+        table = [int(b) for b in rng.permutation(20)[:needed]] + [-1]
+        got = gather_rows_arrays(pool, table, context_len)
+        assert got.shape[:2] == (6, context_len)
+        for array, cache in enumerate(k + v):
+            want = gather_context(as_np(cache), table, context_len, bs)
+            assert np.array_equal(as_np(got[array]), want), (context_len, array)
+        part = gather_rows_arrays(pool, table, context_len, first_array=2, n_arrays=3)
+        assert torch.equal(part.view(torch.uint8), got[2:5].contiguous().view(torch.uint8))
+
+
 def test_slot_calls_validate_before_launch(gpu):
     from iekv.engine.slots import gather_rows, write_slots
 
@@ -89,6 +141,13 @@ def test_slot_calls_validate_before_launch(gpu):
         write_slots(pool, 0, rows, rows, [0])
     with pytest.raises(IndexError):
         gather_rows(pool, 0, [3], 6)
+    from iekv.engine.slots import gather_rows_arrays, write_slots_layers
+
+    with pytest.raises(IndexError):
+        write_slots_layers(pool, rows[None].expand(2, -1, -1, -1), rows[None].expand(2, -1, -1, -1),
+                           [0, 1], first_layer=1)
+    with pytest.raises(IndexError):
+        gather_rows_arrays(pool, [0, 1], 6, first_array=3, n_arrays=2)
 
 
 @pytest.mark.parametrize("cache_dtype", [torch.float32, torch.bfloat16], ids=str)
