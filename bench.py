@@ -809,7 +809,8 @@ def main() -> int:
     ap.add_argument("--config", default="cfg3", help="cfg1..cfg5 (headline: cfg3)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--slack", type=int, default=None,
-                    help="spare blocks per pool for cfg3/cfg4 (default 64)")
+                    help="size cfg3's or cfg4's pools to the workload's needs plus SLACK blocks "
+                         "(default: cfg3 64; cfg4 the cfg3 engine's pools, 49,598 blocks)")
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
                     help="comma list of direct, pack_unpack, pack, unpack, batched, copier, "
                          "copier_pack_unpack, write_kv, write_kv_per_layer, gather_context, "

@@ -55,6 +55,14 @@ def test_a_tensor_parallel_share_moves_the_same_blocks_with_smaller_tiles(tp, ti
     assert share.name == ("cfg3" if tp == 1 else f"cfg3/tp{tp}")
 
 
+def test_cfg4_runs_on_the_llama8b_engine_pools():
+    """cfg4 is the cfg3 model, so by default its pools have cfg3's size."""
+    cfg3, cfg4 = workloads.make("cfg3"), workloads.make("cfg4")
+    assert workloads.llama8b_engine_blocks(0) == cfg3.src_pool_blocks == 49598
+    assert cfg4.src_pool_blocks == cfg4.dst_pool_blocks == 49598
+    assert cfg4.num_blocks == 17803
+
+
 def test_a_tensor_parallel_degree_must_divide_the_kv_heads():
     with pytest.raises(ValueError, match="does not divide"):
         workloads.make("cfg3", tp=3)
@@ -66,6 +74,8 @@ def test_a_tensor_parallel_degree_must_divide_the_kv_heads():
 
 def test_slack_applies_to_cfg3_and_cfg4_only():
     assert workloads.make("cfg3", slack=0).src_pool_blocks == 49534
+    dense = workloads.make("cfg4", slack=64)
+    assert (dense.src_pool_blocks, dense.dst_pool_blocks) == (17867, 17996)
     with pytest.raises(ValueError, match="fixed pool sizes"):
         workloads.make("cfg5", slack=4)
     with pytest.raises(ValueError, match="unknown workload"):
