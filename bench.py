@@ -801,6 +801,83 @@ def sweep(legs: Legs, names: list[str]) -> list[dict]:
     return rows
 
 
+def ab_ok(spec: str, config: str) -> bool:
+    """Whether an --ab setting is well formed for this workload."""
+    key, _, raw = spec.partition("=")
+    values = [v for v in raw.split(",") if v]
+    if not values:
+        return False
+    if key == "streams":
+        return all(v.isdigit() and 1 <= int(v) <= 8 for v in values)
+    if key == "slack":
+        return config in ("cfg3", "cfg4") and all(v == "engine" or v.isdigit() for v in values)
+    return False
+
+
+def ab(args, names: list[str], device) -> int:
+    """In-process A/B of one setting, values alternated over rounds on one box.
+
+    ``streams=1,2,4``: one set of pools, request streams switched between
+    values. ``slack=64,6600,engine``: pools re-made for each value (cfg3 or
+    cfg4 sized to the workload plus that many spare blocks, ``engine`` for the
+    default pools), so every round also draws a new physical placement. Prints
+    one JSON line with every measurement and the per-value means.
+    """
+    import torch
+
+    from iekv import workloads
+
+    key, _, raw = args.ab.partition("=")
+    values = [v for v in raw.split(",") if v]
+    legs_names = [n for n in names if n in HANDOFF_LEGS]
+    rows, ok = [], True
+    legs = None
+
+    def measure(legs, rnd, value):
+        w = legs.w
+        row = {"round": rnd, "value": value,
+               "pools": [w.src_pool_blocks, w.dst_pool_blocks]}
+        for name in legs_names:
+            ms, _, _ = time_leg(legs, name, args.steps, args.warmup, per_launch=False)
+            row[name] = round(sum(b for b, _ in legs.plan(name)) / (ms * 1e-3) / 1e9, 1)
+        rows.append(row)
+        log("[ab] " + json.dumps(row))
+
+    if key == "streams":
+        counts = [int(v) for v in values]
+        w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
+        legs = Legs(w, device, args.seed, "separate" if args.separate_pools else "paired",
+                    streams=max(counts))
+        streams, stagings = legs.streams, legs.stagings
+        for rnd in range(args.rounds):
+            for n in counts:
+                legs.streams, legs.stagings = streams[:n], stagings[:n]
+                measure(legs, rnd, n)
+        legs.streams, legs.stagings = streams, stagings
+        ok = legs.verify()
+    else:
+        for rnd in range(args.rounds):
+            for v in values:
+                slack = None if v == "engine" else int(v)
+                w = workloads.make(args.config, args.seed, slack, tp=args.tp)
+                legs = Legs(w, device, args.seed,
+                            "separate" if args.separate_pools else "paired",
+                            streams=args.streams)
+                measure(legs, rnd, v)
+                ok = legs.verify() and ok
+                del legs
+                torch.cuda.empty_cache()
+    means = {}
+    for v in values:
+        vv = int(v) if key == "streams" else v
+        mine = [r for r in rows if r["value"] == vv]
+        means[v] = {n: round(statistics.fmean(r[n] for r in mine), 1) for n in legs_names}
+    print(json.dumps({"ab": key, "workload": args.config, "tp_share": args.tp,
+                      "values": values, "rounds": args.rounds, "legs": legs_names, "unit": "GB/s",
+                      "rows": rows, "mean": means, "verified": ok}))
+    return 0 if ok else 1
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -832,6 +909,10 @@ def main() -> int:
                     help="issue request k of the per-request legs on stream k mod STREAMS "
                          "(default 2: on the Llama-3-8B shape the direct leg gained 2.3%% over "
                          "one stream; the per-launch timing pass always uses one)")
+    ap.add_argument("--ab", default="",
+                    help="in-process A/B instead of the benchmark line: streams=1,2,4 (one set "
+                         "of pools) or slack=64,6600,engine (pools re-made per value; cfg3/cfg4)")
+    ap.add_argument("--rounds", type=int, default=3, help="rounds of an --ab comparison")
     ap.add_argument("--separate-pools", action="store_true",
                     help="allocate the two pools separately instead of as one reservation "
                          "(prefill pool first)")
@@ -840,6 +921,10 @@ def main() -> int:
     names = [x for x in args.legs.split(",") if x]
     if not args.sweep and not any(x in HANDOFF_LEGS for x in names):
         print(f"--legs needs one handoff leg ({', '.join(HANDOFF_LEGS)}) for the line's value",
+              file=sys.stderr)
+        return 2
+    if args.ab and not ab_ok(args.ab, args.config):
+        print("--ab takes streams=N,... (N in 1..8) or, for cfg3 and cfg4, slack=N|engine,...",
               file=sys.stderr)
         return 2
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -873,6 +958,8 @@ def main() -> int:
     if not 1 <= args.streams <= 8:
         print("--streams must be 1..8", file=sys.stderr)
         return 2
+    if args.ab:
+        return ab(args, names, device)
     legs = Legs(w, device, args.seed, "separate" if args.separate_pools else "paired",
                 streams=args.streams)
     P = w.payload_bytes
