@@ -36,7 +36,7 @@ import numpy as np
 import torch
 
 from .. import _native
-from .pools import KVPool, stage_ids, stream_handle
+from .pools import KVPool, StreamScope, current_stream_handle, stage_ids, stream_handle
 
 # Device staging the host pipelines use: two slots of at most this many bytes.
 HOST_STAGING_BYTES = 256 << 20
@@ -234,37 +234,48 @@ def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
 class _BlockIds:
     """The block ids of one call: range-checked host int32 ids, or a device tensor.
 
-    Host ids of at most ``INLINE_IDS`` blocks go to the library's host-id entry
-    points (the ids ride in the launch's kernel arguments); otherwise they are
-    uploaded once, when a call first needs them on the device.
+    Host ids are a NumPy int32 array, or a ctypes int32 array for a short Python
+    list (:meth:`KVPool.short_host_ids`). Host ids of at most ``INLINE_IDS``
+    blocks go to the library's host-id entry points (the ids ride in the
+    launch's kernel arguments); otherwise they are uploaded once, when a call
+    first needs them on the device.
     """
 
     __slots__ = ("_device", "host", "_on_device")
 
-    def __init__(self, device: torch.device, host: np.ndarray | None = None,
+    def __init__(self, device: torch.device, host=None,
                  device_ids: torch.Tensor | None = None) -> None:
         self._device = device
-        self.host = None if host is None else np.ascontiguousarray(host, dtype=np.int32)
+        if host is not None and not isinstance(host, ctypes.Array):
+            host = np.ascontiguousarray(host, dtype=np.int32)
+        self.host = host
         self._on_device = device_ids
 
     def __len__(self) -> int:
-        return int(self.host.size) if self.host is not None else self._on_device.numel()
+        return len(self.host) if self.host is not None else self._on_device.numel()
+
+    def _host_array(self) -> np.ndarray:
+        host = self.host
+        return np.frombuffer(host, dtype=np.int32) if isinstance(host, ctypes.Array) else host
 
     def __getitem__(self, index: slice) -> "_BlockIds":
         if self.host is not None:
-            return _BlockIds(self._device, host=self.host[index])
+            return _BlockIds(self._device, host=self._host_array()[index])
         return _BlockIds(self._device, device_ids=self._on_device[index])
 
     @property
     def inline(self) -> bool:
-        return self.host is not None and self.host.size <= _native.INLINE_IDS
+        return self.host is not None and len(self.host) <= _native.INLINE_IDS
 
     def host_pointer(self) -> int:
-        return self.host.ctypes.data
+        host = self.host
+        if isinstance(host, ctypes.Array):
+            return ctypes.addressof(host)
+        return host.__array_interface__["data"][0]
 
     def on_device(self) -> torch.Tensor:
         if self._on_device is None:
-            self._on_device = stage_ids(self._device, self.host)[0]
+            self._on_device = stage_ids(self._device, self._host_array())[0]
         return self._on_device
 
 
@@ -400,11 +411,14 @@ class HipSlotCopier:
         self.write_blocks([block_id], [payload])
 
     # -- batched calls -------------------------------------------------------
-    @staticmethod
-    def _on(stream: torch.cuda.Stream | None):
+    def _on(self, stream: torch.cuda.Stream | None):
         """Run a call as if ``stream`` were the current stream (its launches, id uploads
         and new buffers are then ordered on it); None keeps the current stream."""
-        return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+        if stream is None:
+            return contextlib.nullcontext()
+        if stream.device != self.device:
+            raise ValueError(f"stream on {stream.device}, pool on {self.device}")
+        return StreamScope(stream)
 
     def read_blocks(self, block_ids, *, location: str | None = None,
                     stream: torch.cuda.Stream | None = None) -> PackedBlocks:
@@ -423,14 +437,17 @@ class HipSlotCopier:
     def _ids(self, block_ids, *, unique: bool = False, what: str) -> "_BlockIds":
         if isinstance(block_ids, torch.Tensor) and block_ids.device.type == "cuda":
             return _BlockIds(self.device, device_ids=self.pool.block_ids(block_ids, what=what))
+        short = self.pool.short_host_ids(block_ids, unique=unique, what=what)
+        if short is not None:
+            return _BlockIds(self.device, host=short)
         return _BlockIds(self.device, host=self.pool.host_ids(block_ids, unique=unique, what=what))
 
     def _gather(self, block_ids, location: str) -> PackedBlocks:
         ids = self._ids(block_ids, what="source block")
         n = len(ids)
         out = self._empty_packed(n, on_host=(location == "host"))
-        stream = torch.cuda.current_stream(self.device)
         if out.on_host:
+            stream = torch.cuda.current_stream(self.device)
             staging = self._host_staging(n)
             copy = self.copy_stream()
             _native.call("iekv_offload", self.pool.native.handle, ids.on_device().data_ptr(), n,
@@ -441,10 +458,10 @@ class HipSlotCopier:
             self.blocks_offloaded += n
         elif ids.inline:
             _native.call("iekv_pack_ids", self.pool.native.handle, ids.host_pointer(), n,
-                         out.data.data_ptr(), out.nbytes, stream.cuda_stream)
+                         out.data.data_ptr(), out.nbytes, current_stream_handle(self.device))
         else:
             _native.call("iekv_pack", self.pool.native.handle, ids.on_device().data_ptr(), n,
-                         out.data.data_ptr(), out.nbytes, stream.cuda_stream)
+                         out.data.data_ptr(), out.nbytes, current_stream_handle(self.device))
         return out
 
     def write_blocks(self, block_ids, payloads, *,
@@ -478,8 +495,8 @@ class HipSlotCopier:
     def _write_packed(self, ids: "_BlockIds", packed: PackedBlocks) -> None:
         self._check_packed(packed)
         n = len(ids)
-        stream = torch.cuda.current_stream(self.device)
         if packed.on_host:
+            stream = torch.cuda.current_stream(self.device)
             staging = self._host_staging(n)
             # Small pinned images are read by the unpack kernel itself on the compute
             # stream (IEKV_HOST_DIRECT_MAX_BYTES); passing that stream as the copy
@@ -493,10 +510,10 @@ class HipSlotCopier:
             self.restore_launches += 1
         elif ids.inline:
             _native.call("iekv_unpack_ids", self.pool.native.handle, ids.host_pointer(), n,
-                         packed.data.data_ptr(), packed.nbytes, stream.cuda_stream)
+                         packed.data.data_ptr(), packed.nbytes, current_stream_handle(self.device))
         else:
             _native.call("iekv_unpack", self.pool.native.handle, ids.on_device().data_ptr(), n,
-                         packed.data.data_ptr(), packed.nbytes, stream.cuda_stream)
+                         packed.data.data_ptr(), packed.nbytes, current_stream_handle(self.device))
 
     def _restore_scattered(self, ids: "_BlockIds", payloads: Seq[BlockPayload]) -> None:
         """Host payloads from unrelated buffers (tier entries) -> one iekv_restore_blocks."""
@@ -526,18 +543,22 @@ class HipSlotCopier:
         caller orders it after the writes of the source blocks and orders later
         readers of the destination blocks after it.
         """
-        with self._on(stream):
-            self._copy_blocks(source, src_ids, dst_ids)
+        scope = self._on(stream)        # validates the stream's device
+        if self._pending:
+            with scope:                 # queued reads see the blocks before this write
+                self.flush()
+        self._copy_blocks(source, src_ids, dst_ids, stream)
 
-    def _copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids) -> None:
-        self.flush()
+    def _copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids,
+                     on: torch.cuda.Stream | None) -> None:
         if not self.pool.same_shape(source.pool):
             raise ValueError("source and destination pools differ in layout")
         if source.device != self.device:
             raise ValueError(f"pools on {source.device} and {self.device}")
         on_device = (isinstance(src_ids, torch.Tensor) and src_ids.device.type == "cuda") or \
             (isinstance(dst_ids, torch.Tensor) and dst_ids.device.type == "cuda")
-        stream = torch.cuda.current_stream(self.device)
+        stream = on.cuda_stream if on is not None else current_stream_handle(self.device)
+        same_pool = source.pool.native.handle.value == self.pool.native.handle.value
         if on_device:
             src = source.pool.block_ids(src_ids, what="source block")
             dst = self.pool.block_ids(dst_ids, unique=True, what="destination block")
@@ -545,30 +566,47 @@ class HipSlotCopier:
                 raise ValueError(f"{src.numel()} source blocks for {dst.numel()} destinations")
             n = dst.numel()
             _native.call("iekv_copy_direct", source.pool.native.handle, self.pool.native.handle,
-                         src.data_ptr(), dst.data_ptr(), n, stream.cuda_stream)
-        else:
-            # Host ids: checked on the host and issued by destination id. Up to
-            # INLINE_IDS pairs travel in the launch's kernel arguments; longer
-            # lists are uploaded together with one copy.
-            s, d = issue_order(src_ids, dst_ids)
-            s = source.pool.host_ids(s, what="source block")
-            d = self.pool.host_ids(d, unique=True, what="destination block", ascending=True)
-            if source.pool.native.handle.value == self.pool.native.handle.value and \
-                    bool(np.isin(s, d, assume_unique=False).any()):
-                raise ValueError("a direct copy within one pool needs disjoint source "
-                                 "and destination blocks")
-            n = int(d.size)
-            if n <= _native.INLINE_IDS:
-                s32 = np.ascontiguousarray(s, dtype=np.int32)
-                d32 = np.ascontiguousarray(d, dtype=np.int32)
+                         src.data_ptr(), dst.data_ptr(), n, stream)
+            source.blocks_read += n
+            self.blocks_written += n
+            return
+        # Host ids: checked on the host and issued by destination id. Up to
+        # INLINE_IDS pairs travel in the launch's kernel arguments; longer lists
+        # are uploaded together with one copy. A short Python table is checked
+        # without NumPy.
+        pairs = short_issue_order(src_ids, dst_ids)
+        if pairs is not None:
+            s = source.pool.short_host_ids(pairs[0], what="source block")
+            d = self.pool.short_host_ids(pairs[1], unique=True, what="destination block")
+            if s is not None and d is not None:
+                if same_pool and not set(pairs[0]).isdisjoint(pairs[1]):
+                    raise ValueError("a direct copy within one pool needs disjoint source "
+                                     "and destination blocks")
+                n = len(d)
                 _native.call("iekv_copy_direct_ids", source.pool.native.handle,
-                             self.pool.native.handle, s32.ctypes.data, d32.ctypes.data, n,
-                             stream.cuda_stream)
-            else:
+                             self.pool.native.handle, ctypes.addressof(s), ctypes.addressof(d),
+                             n, stream)
+                source.blocks_read += n
+                self.blocks_written += n
+                return
+        s, d = issue_order(src_ids, dst_ids)
+        s = source.pool.host_ids(s, what="source block")
+        d = self.pool.host_ids(d, unique=True, what="destination block", ascending=True)
+        if same_pool and bool(np.isin(s, d, assume_unique=False).any()):
+            raise ValueError("a direct copy within one pool needs disjoint source "
+                             "and destination blocks")
+        n = int(d.size)
+        if n <= _native.INLINE_IDS:
+            s32 = np.ascontiguousarray(s, dtype=np.int32)
+            d32 = np.ascontiguousarray(d, dtype=np.int32)
+            _native.call("iekv_copy_direct_ids", source.pool.native.handle,
+                         self.pool.native.handle, s32.__array_interface__["data"][0],
+                         d32.__array_interface__["data"][0], n, stream)
+        else:
+            with self._on(on):          # the upload is ordered on the copy's stream
                 src, dst = stage_ids(self.device, s, d)
-                _native.call("iekv_copy_direct", source.pool.native.handle,
-                             self.pool.native.handle, src.data_ptr(), dst.data_ptr(), n,
-                             stream.cuda_stream)
+            _native.call("iekv_copy_direct", source.pool.native.handle,
+                         self.pool.native.handle, src.data_ptr(), dst.data_ptr(), n, stream)
         source.blocks_read += n
         self.blocks_written += n
 
@@ -576,6 +614,22 @@ class HipSlotCopier:
     def bytes_moved(self) -> int:
         """(reads + writes) x 2L x T, as ie/engine/copier.py:33-38 counts."""
         return (self.blocks_read + self.blocks_written) * self.pool.block_bytes
+
+
+def short_issue_order(src_ids, dst_ids):
+    """:func:`issue_order` for short Python tables: ``(src, dst)`` lists sorted by
+    destination id, or None when either table is not a list or tuple of at most
+    ``INLINE_IDS`` entries (``issue_order`` takes those)."""
+    if type(src_ids) not in (list, tuple) or type(dst_ids) not in (list, tuple) \
+            or len(dst_ids) > _native.INLINE_IDS:
+        return None
+    if len(src_ids) != len(dst_ids):
+        raise ValueError(f"{len(src_ids)} source blocks for {len(dst_ids)} destinations")
+    try:
+        order = sorted(range(len(dst_ids)), key=dst_ids.__getitem__)
+    except TypeError:
+        return None
+    return [src_ids[i] for i in order], [dst_ids[i] for i in order]
 
 
 def issue_order(src_ids, dst_ids) -> tuple[np.ndarray, np.ndarray]:
@@ -621,4 +675,4 @@ def stack_payloads(payloads: Iterable[BlockPayload]) -> PackedBlocks:
 
 
 __all__ = ["BlockPayload", "DeferredBlockPayload", "HipSlotCopier", "PackedBlocks", "copier_for",
-           "issue_order", "stack_payloads", "stream_handle"]
+           "issue_order", "short_issue_order", "stack_payloads", "stream_handle"]

@@ -11,6 +11,7 @@ keep the reference's per-layer shape, and the ``[N, bs, H, D]`` paged view
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Sequence as Seq
 
@@ -127,6 +128,32 @@ class KVPool:
             return ids
         return stage_ids(self.device, self.host_ids(ids, unique=unique, what=what))[0]
 
+    def short_host_ids(self, ids, *, unique: bool = False, what: str = "block"):
+        """A short Python list or tuple of ids (at most ``INLINE_IDS``, the most a
+        host-id launch carries) as a ctypes int32 array, checked as :meth:`host_ids`
+        checks (IndexError for an id outside the pool, ValueError for a repeat with
+        ``unique``). None for anything else, which :meth:`host_ids` takes.
+
+        A block table is a short list in the serving loop; checking it in plain
+        Python costs well under a microsecond, against several for the NumPy
+        conversions of :meth:`host_ids`.
+        """
+        if type(ids) not in (list, tuple) or len(ids) > _native.INLINE_IDS:
+            return None
+        n = len(ids)
+        try:
+            lo, hi = (min(ids), max(ids)) if n else (0, 0)
+            out = (ctypes.c_int32 * n)(*ids)
+        except TypeError:
+            return None        # not plain integers: the NumPy path converts them
+        if lo < 0 or hi >= self.num_blocks:
+            bad = lo if lo < 0 else hi
+            raise IndexError(f"{what} id {bad} out of range for a pool of "
+                             f"{self.num_blocks} blocks")
+        if unique and n > 1 and len(set(ids)) != n:
+            raise ValueError(f"{what} ids must be distinct")
+        return out
+
     def host_ids(self, ids, *, unique: bool = False, what: str = "block",
                  ascending: bool = False) -> np.ndarray:
         """Host-side ids as int64 NumPy, range-checked against this pool (IndexError)
@@ -176,5 +203,64 @@ def stage_ids(device: torch.device, *arrays: np.ndarray) -> list[torch.Tensor]:
 
 def stream_handle(device: torch.device, stream: torch.cuda.Stream | None = None) -> int:
     """The raw hipStream_t of ``stream`` (default: torch's current stream on ``device``)."""
-    s = stream if stream is not None else torch.cuda.current_stream(device)
-    return s.cuda_stream
+    return stream.cuda_stream if stream is not None else current_stream_handle(device)
+
+
+_raw_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream_handle(device: torch.device) -> int:
+    """The raw hipStream_t of torch's current stream on ``device`` (a CUDA device;
+    without an index, the current one).
+
+    torch's own ``current_stream(device)`` builds a Stream object and costs the
+    host about 3 us, longer than issuing the launch the handle is for; the raw
+    accessor skips that.
+    """
+    if _raw_current_stream is not None:
+        index = device.index
+        return _raw_current_stream(torch.cuda.current_device() if index is None else index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+_get_stream = getattr(torch._C, "_cuda_getCurrentStream", None)
+_set_stream = getattr(torch._C, "_cuda_setStream", None)
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+_set_device = getattr(torch._C, "_cuda_setDevice", None)
+_LIGHT_SCOPE = None not in (_get_stream, _set_stream, _get_device, _set_device)
+
+
+class StreamScope:
+    """Make ``stream`` torch's current stream on its device for a ``with`` block.
+
+    What ``torch.cuda.stream(stream)`` does for one device (launches, id uploads
+    and new buffers inside the block are ordered on ``stream``), through torch's
+    raw stream accessors: the public context manager costs the host about 6 us
+    per use, more than the launch it wraps. The current device is restored too.
+    Falls back to ``torch.cuda.stream`` where the raw accessors are missing.
+    """
+
+    __slots__ = ("stream", "_prev", "_device", "_fallback")
+
+    def __init__(self, stream: torch.cuda.Stream) -> None:
+        self.stream = stream
+        self._fallback = None if _LIGHT_SCOPE else torch.cuda.stream(stream)
+
+    def __enter__(self) -> torch.cuda.Stream:
+        if self._fallback is not None:
+            return self._fallback.__enter__()
+        s = self.stream
+        self._device = _get_device()
+        self._prev = _get_stream(s.device_index)
+        _set_stream(stream_id=s.stream_id, device_index=s.device_index,
+                    device_type=s.device_type)
+        return s
+
+    def __exit__(self, *exc) -> None:
+        if self._fallback is not None:
+            self._fallback.__exit__(*exc)
+            return
+        stream_id, device_index, device_type = self._prev
+        _set_stream(stream_id=stream_id, device_index=device_index, device_type=device_type)
+        if _get_device() != self._device:
+            _set_device(self._device)

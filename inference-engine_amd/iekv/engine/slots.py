@@ -17,7 +17,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from .pools import KVPool
+from .pools import KVPool, current_stream_handle
 
 
 def _device_slots(slots, device: torch.device) -> torch.Tensor:
@@ -51,9 +51,9 @@ def write_slots(pool: KVPool, layer: int, k: torch.Tensor, v: torch.Tensor, slot
     kc = k.to(device=pool.device, dtype=pool.dtype).contiguous()
     vc = v.to(device=pool.device, dtype=pool.dtype).contiguous()
     st = _device_slots(slots, pool.device)
-    stream = torch.cuda.current_stream(pool.device)
+    stream = current_stream_handle(pool.device)
     _native.call("iekv_write_slots", pool.native.handle, layer, pool.block_size, kc.data_ptr(),
-                 vc.data_ptr(), st.data_ptr(), n, stream.cuda_stream)
+                 vc.data_ptr(), st.data_ptr(), n, stream)
 
 
 def gather_rows(pool: KVPool, array: int, block_table, context_len: int) -> torch.Tensor:
@@ -77,10 +77,10 @@ def gather_rows(pool: KVPool, array: int, block_table, context_len: int) -> torc
                              f"{len(block_table)}")
         table = pool.block_ids(list(block_table[:needed]), what="context block")
     out = torch.empty((context_len, *pool.tile_shape[1:]), dtype=pool.dtype, device=pool.device)
-    stream = torch.cuda.current_stream(pool.device)
+    stream = current_stream_handle(pool.device)
     _native.call("iekv_gather_rows", pool.native.handle, array, bs, table.data_ptr(),
                  context_len, out.data_ptr(), out.numel() * out.element_size(),
-                 stream.cuda_stream)
+                 stream)
     return out
 
 
@@ -113,10 +113,10 @@ def write_slots_layers(pool: KVPool, k: torch.Tensor, v: torch.Tensor, slots,
     vc = v.to(device=pool.device, dtype=pool.dtype).contiguous()
     st = _device_slots(slots, pool.device)
     stride = n * kc.shape[2] * kc.shape[3] * kc.element_size()
-    stream = torch.cuda.current_stream(pool.device)
+    stream = current_stream_handle(pool.device)
     _native.call("iekv_write_slots_layers", pool.native.handle, first_layer, n_layers,
                  pool.block_size, kc.data_ptr(), vc.data_ptr(), stride, st.data_ptr(), n,
-                 stream.cuda_stream)
+                 stream)
 
 
 def gather_rows_arrays(pool: KVPool, block_table, context_len: int, first_array: int = 0,
@@ -143,8 +143,8 @@ def gather_rows_arrays(pool: KVPool, block_table, context_len: int, first_array:
         table = pool.block_ids(list(block_table[:needed]), what="context block")
     out = torch.empty((n_arrays, context_len, *pool.tile_shape[1:]), dtype=pool.dtype,
                       device=pool.device)
-    stream = torch.cuda.current_stream(pool.device)
+    stream = current_stream_handle(pool.device)
     _native.call("iekv_gather_rows_arrays", pool.native.handle, first_array, n_arrays, bs,
                  table.data_ptr(), context_len, out.data_ptr(), out.numel() * out.element_size(),
-                 stream.cuda_stream)
+                 stream)
     return out

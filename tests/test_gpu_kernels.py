@@ -664,6 +664,55 @@ def test_requests_issued_on_alternating_streams_are_bit_exact(gpu):
     assert_pool_equals(sk, sv, src_o)
 
 
+def test_short_python_tables_and_numpy_tables_move_the_same_bytes(gpu):
+    """Short Python tables take the plain-Python id checks, NumPy arrays and long
+    lists the NumPy ones; both must move the same tiles and refuse the same ids.
+    Includes a table of exactly INLINE_IDS blocks, one past it, and a direct copy
+    within one pool."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    bs = 16
+    n_blocks = 700
+    sk, sv = allocate(n_blocks, bs, 2, 2, 32, torch.float16, gpu, seed=91)
+    src = HipSlotCopier(sk, sv, bs)
+    sizes = [1, 2, 7, _native.INLINE_IDS, _native.INLINE_IDS + 1]
+    results = []
+    for as_numpy in (False, True):
+        dk, dv = allocate(n_blocks, bs, 2, 2, 32, torch.float16, gpu, seed=93)
+        dst = HipSlotCopier(dk, dv, bs)
+        r = np.random.default_rng(94)
+        for n in sizes:
+            s_ids = r.permutation(n_blocks)[:n]
+            d_ids = r.permutation(n_blocks)[:n]
+            if as_numpy:
+                dst.copy_blocks(src, s_ids, d_ids)
+            else:
+                dst.copy_blocks(src, [int(b) for b in s_ids], [int(b) for b in d_ids])
+            s2 = r.permutation(n_blocks)[:n]
+            d2 = r.permutation(n_blocks)[:n]
+            payload = src.read_blocks(s2 if as_numpy else [int(b) for b in s2])
+            dst.write_blocks(d2 if as_numpy else [int(b) for b in d2], payload)
+        # within one pool: disjoint source and destination halves
+        within = r.permutation(n_blocks)[:20]
+        a, b = within[:10], within[10:]
+        dst.copy_blocks(dst, a if as_numpy else [int(x) for x in a],
+                        b if as_numpy else [int(x) for x in b])
+        torch.cuda.synchronize()
+        results.append(host_bytes(dk + dv))
+        for bad in ([0, n_blocks], [-1, 3]):
+            with pytest.raises(IndexError, match="out of range"):
+                dst.copy_blocks(src, [1, 2], np.array(bad) if as_numpy else bad)
+        with pytest.raises(ValueError, match="must be distinct"):
+            dst.copy_blocks(src, [1, 2], np.array([5, 5]) if as_numpy else [5, 5])
+        with pytest.raises(ValueError, match="disjoint"):
+            dst.copy_blocks(dst, np.array([1, 2]) if as_numpy else [1, 2],
+                            np.array([2, 3]) if as_numpy else [2, 3])
+        with pytest.raises(ValueError, match="2 source blocks for 3 destinations"):
+            dst.copy_blocks(src, [1, 2], np.array([4, 5, 6]) if as_numpy else [4, 5, 6])
+    assert all(np.array_equal(x, y) for x, y in zip(*results))
+
+
 def test_host_payloads_through_the_copier(gpu):
     from iekv.engine.copier import HipSlotCopier
 
