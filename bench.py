@@ -186,6 +186,7 @@ class Legs:
         self._fork_event = torch.cuda.Event()
         self._join_events = [torch.cuda.Event() for _ in self.streams[1:]]
         self.step_ms: dict[str, list[float]] = {}
+        self.issue_ms: dict[str, list[float]] = {}   # host time to issue each timed step
         torch.cuda.synchronize()
         log(f"[bench] pools ready: 2 x {workload.src_pool_blocks} blocks x {s.block_bytes} B "
             f"({2 * workload.src_pool_blocks * s.block_bytes / 1e9:.1f} GB) in "
@@ -601,7 +602,8 @@ def time_leg(legs: Legs, name: str, steps: int, warmup: int, per_launch: bool = 
 
     Pass 1 (the headline): HIP events only at step boundaries on the launch
     stream, so nothing is added between the launches of a step (the per-step
-    times are kept in ``legs.step_ms``). Pass 2 (when
+    times are kept in ``legs.step_ms``, and the host's time to issue each step in
+    ``legs.issue_ms``). Pass 2 (when
     ``per_launch``): the same steps again with every kv_move launch timed by the
     library (iekv_profile_start/stop; the events ride in each launch's own
     dispatch packet). Returns (ms per step, wall seconds of pass 1,
@@ -615,12 +617,16 @@ def time_leg(legs: Legs, name: str, steps: int, warmup: int, per_launch: bool = 
         step()
     torch.cuda.synchronize()
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    issue = []
     t0 = time.perf_counter()
     marks[0].record(legs.stream)
     for i in range(steps):
+        h0 = time.perf_counter()
         step()
         marks[i + 1].record(legs.stream)
+        issue.append(1000 * (time.perf_counter() - h0))
     torch.cuda.synchronize()
+    legs.issue_ms[name] = issue
     wall = time.perf_counter() - t0
     ms_step = marks[0].elapsed_time(marks[-1]) / steps
     legs.step_ms[name] = [a.elapsed_time(b) for a, b in zip(marks, marks[1:])]
@@ -661,6 +667,10 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
     out = {
         "ms_per_step": round(ms_step, 4),
         "ms_per_step_median": round(statistics.median(legs.step_ms.get(name, [ms_step])), 4),
+        # The host's time to issue one step's launches: the fastest timed step (a
+        # full launch queue can only make the host wait longer). Close to
+        # ms_per_step means the leg is bound by issuing launches, not by HBM.
+        "host_issue_ms_per_step": round(min(legs.issue_ms.get(name, [0.0])), 4),
         "GBps": round(gbs, 1),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "kernel_GBps": round(kernel_gbs, 1),
@@ -677,7 +687,8 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
                                  "max": round(req_ms[-1], 4)}
     log(f"[bench] {name:11s} {ms_step:9.3f} ms/step  {gbs:8.1f} GB/s "
         f"({out['pct_hbm_peak']:.1f}% of peak)  kernel {kernel_gbs:8.1f} GB/s  "
-        f"{out['avg_launch_us']:.1f} us/launch")
+        f"{out['avg_launch_us']:.1f} us/launch  host issue {out['host_issue_ms_per_step']:.3f} "
+        f"ms/step")
     return out, kernel_gbs, 1000 * total_ms / max(1, len(durations)), moved / max(1, len(durations))
 
 

@@ -50,13 +50,16 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 10
+#define IEKV_ABI_VERSION 11
 
 enum {
   IEKV_OK = 0,
   IEKV_ERR_INVALID = -1, /* bad argument (null pointer, size, alignment, overlap) */
   IEKV_ERR_HIP = -2,     /* a HIP runtime call failed */
-  IEKV_ERR_CAPACITY = -3 /* a buffer is too small for the requested blocks */
+  IEKV_ERR_CAPACITY = -3, /* a buffer is too small for the requested blocks */
+  IEKV_ERR_RANGE = -4,   /* a host block id outside its pool (the *_ids entry points) */
+  IEKV_ERR_IDS = -5      /* host ids that conflict: a destination block twice in one call,
+                            or a copy within one pool whose sources overlap its destinations */
 };
 
 /* Opaque handle describing one paged pool: the base address of each of its
@@ -109,10 +112,15 @@ int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
 #define IEKV_INLINE_IDS 256
 
 /* The same three moves with the block ids given in HOST memory, for at most
- * IEKV_INLINE_IDS blocks: the ids are range-checked on the host and travel in
- * the launch's own kernel arguments, so the caller needs no device id buffer
- * and no host-to-device id copy sits on the stream between launches.
- * One block per workgroup whatever iekv_set_launch's run_blocks.
+ * IEKV_INLINE_IDS blocks: the ids travel in the launch's own kernel arguments,
+ * so the caller needs no device id buffer and no host-to-device id copy sits on
+ * the stream between launches. One block per workgroup whatever
+ * iekv_set_launch's run_blocks. The ids are checked on the host before anything
+ * is enqueued: an id outside its pool returns IEKV_ERR_RANGE; a destination id
+ * given twice (iekv_copy_direct_ids, iekv_unpack_ids), or a copy within one pool
+ * whose sources overlap its destinations, returns IEKV_ERR_IDS. iekv_copy_direct_ids
+ * issues its (src, dst) pairs in ascending destination order (the pairs are
+ * independent; neighbouring destination tiles are then written together).
  * Replace: the same reference lines as iekv_copy_direct, iekv_pack and
  * iekv_unpack, for the per-request calls of the disaggregation workers
  * (ie/serve/disaggregated.py:50, 81-82), whose tables are host lists. */

@@ -913,9 +913,53 @@ int fill_inline(const int32_t* host_ids, int32_t n, int64_t num_blocks, const ch
   for (int32_t i = 0; i < n; ++i) {
     const int32_t id = host_ids[i];
     if (id < 0 || id >= num_blocks)
-      return set_error(IEKV_ERR_INVALID, "%s block id %d (entry %d) is outside the pool of "
+      return set_error(IEKV_ERR_RANGE, "%s block id %d (entry %d) out of range for a pool of "
                        "%lld blocks", what, id, i, static_cast<long long>(num_blocks));
     ids->v[off + i] = id;
+  }
+  return IEKV_OK;
+}
+
+// IEKV_ERR_IDS unless the n (<= IEKV_INLINE_IDS) ids at v are distinct.
+int check_distinct(const int32_t* v, int32_t n, const char* what) {
+  int32_t sorted[IEKV_INLINE_IDS];
+  std::copy(v, v + n, sorted);
+  std::sort(sorted, sorted + n);
+  for (int32_t i = 1; i < n; ++i)
+    if (sorted[i] == sorted[i - 1])
+      return set_error(IEKV_ERR_IDS, "%s block ids must be distinct (id %d given twice)", what,
+                       sorted[i]);
+  return IEKV_OK;
+}
+
+// The checked (src, dst) pairs of a host-id direct copy, reordered by ascending
+// destination id: sources at ids->v[0..n), destinations at ids->v[n..2n).
+// IEKV_ERR_IDS for a destination given twice, and, when both sides are the same
+// pool, for a block that is both a source and a destination (its bytes would
+// depend on the order the workgroups run in).
+int order_pairs(InlineIds* ids, int32_t n, bool same_pool) {
+  uint64_t key[IEKV_INLINE_IDS];   // destination in the high half: sorting orders by it
+  for (int32_t i = 0; i < n; ++i)
+    key[i] = (static_cast<uint64_t>(static_cast<uint32_t>(ids->v[n + i])) << 32) |
+             static_cast<uint32_t>(ids->v[i]);
+  std::sort(key, key + n);
+  for (int32_t i = 0; i < n; ++i) {
+    ids->v[i] = static_cast<int32_t>(key[i] & 0xffffffffu);
+    ids->v[n + i] = static_cast<int32_t>(key[i] >> 32);
+    if (i > 0 && ids->v[n + i] == ids->v[n + i - 1])
+      return set_error(IEKV_ERR_IDS, "destination block ids must be distinct (id %d given "
+                       "twice)", ids->v[n + i]);
+  }
+  if (same_pool) {
+    int32_t srcs[IEKV_INLINE_IDS];
+    std::copy(ids->v, ids->v + n, srcs);
+    std::sort(srcs, srcs + n);
+    for (int32_t i = 0, j = 0; i < n && j < n;) {   // destinations ids->v[n..2n) ascend
+      if (srcs[i] == ids->v[n + j])
+        return set_error(IEKV_ERR_IDS, "a direct copy within one pool needs disjoint source "
+                         "and destination blocks (block %d is both)", srcs[i]);
+      if (srcs[i] < ids->v[n + j]) ++i; else ++j;
+    }
   }
   return IEKV_OK;
 }
@@ -1225,7 +1269,8 @@ int iekv_copy_direct_ids(const iekv_pool* src, const iekv_pool* dst, const int32
                      dst->device);
   InlineIds ids{};
   if ((rc = fill_inline(src_ids, n_blocks, src->num_blocks, "source", &ids, 0)) ||
-      (rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, n_blocks)))
+      (rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, n_blocks)) ||
+      (rc = order_pairs(&ids, n_blocks, src == dst)))
     return rc;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
@@ -1262,7 +1307,9 @@ int iekv_unpack_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_bloc
   if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
   if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
   InlineIds ids{};
-  if ((rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, 0))) return rc;
+  if ((rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, 0)) ||
+      (rc = check_distinct(ids.v, n_blocks, "destination")))
+    return rc;
   DeviceGuard guard(dst->device);
   if (!guard.ok()) return guard.fail();
   const int align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));

@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most ids a host-id call takes
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
@@ -23,6 +23,8 @@ IEKV_OK = 0
 IEKV_ERR_INVALID = -1
 IEKV_ERR_HIP = -2
 IEKV_ERR_CAPACITY = -3
+IEKV_ERR_RANGE = -4      # a host block id outside its pool
+IEKV_ERR_IDS = -5        # host ids that conflict (a destination twice; overlap within a pool)
 
 # Every entry point of include/iekv.h: name -> (restype, argtypes).
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -72,6 +74,17 @@ class NativeError(RuntimeError):
         self.code = code
 
 
+class NativeIndexError(NativeError, IndexError):
+    """IEKV_ERR_RANGE: a block id outside its pool, the reference's IndexError."""
+
+
+class NativeValueError(NativeError, ValueError):
+    """IEKV_ERR_IDS: ids that conflict (a destination twice; overlap within a pool)."""
+
+
+_ERRORS = {IEKV_ERR_RANGE: NativeIndexError, IEKV_ERR_IDS: NativeValueError}
+
+
 def library_path() -> Path:
     override = os.environ.get("IEKV_LIBRARY")
     return Path(override) if override else LIBRARY
@@ -102,9 +115,11 @@ def lib() -> ctypes.CDLL:
 
 
 def check(function: str, code: int) -> None:
+    """Raise for a non-zero status: IndexError / ValueError kinds for the id checks
+    (IEKV_ERR_RANGE, IEKV_ERR_IDS), NativeError (a RuntimeError) for the rest."""
     if code != IEKV_OK:
         message = lib().iekv_last_error().decode(errors="replace")
-        raise NativeError(function, code, message)
+        raise _ERRORS.get(code, NativeError)(function, code, message)
 
 
 _functions: dict[str, ctypes._CFuncPtr] = {}

@@ -30,6 +30,7 @@ from __future__ import annotations
 import contextlib
 import ctypes
 import weakref
+from array import array
 from typing import Any, Iterable, Sequence as Seq
 
 import numpy as np
@@ -231,23 +232,44 @@ def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
     return base[start:start + len(payloads)]
 
 
-class _BlockIds:
-    """The block ids of one call: range-checked host int32 ids, or a device tensor.
+def _host_id_array(ids) -> array | None:
+    """A Python list or tuple of at most ``INLINE_IDS`` ids as ``array('i')``, for the
+    library's host-id entry points, which check the ids themselves (IEKV_ERR_RANGE,
+    IEKV_ERR_IDS); None for anything else (NumPy arrays, tensors, long lists, values
+    that are not 32-bit integers), which the pool checks in NumPy.
 
-    Host ids are a NumPy int32 array, or a ctypes int32 array for a short Python
-    list (:meth:`KVPool.short_host_ids`). Host ids of at most ``INLINE_IDS``
-    blocks go to the library's host-id entry points (the ids ride in the
-    launch's kernel arguments); otherwise they are uploaded once, when a call
-    first needs them on the device.
+    A serving loop's block tables are short lists; converting one costs the host
+    about a microsecond for a few hundred ids, where the NumPy checks cost
+    10-30 us, more than the launch they precede.
+    """
+    if type(ids) not in (list, tuple) or len(ids) > _native.INLINE_IDS:
+        return None
+    try:
+        return array("i", ids)
+    except (TypeError, OverflowError):
+        return None
+
+
+class _BlockIds:
+    """The block ids of one call: host int32 ids, or a device tensor.
+
+    Host ids are a NumPy int32 array the pool has checked, or an ``array('i')`` of a
+    short Python list that only the library's host-id entry points check. Host ids
+    of at most ``INLINE_IDS`` blocks go to those entry points (the ids ride in the
+    launch's kernel arguments); a call that needs them on the device checks them
+    here first (range, and distinctness for destinations) and uploads them once.
     """
 
-    __slots__ = ("_device", "host", "_on_device")
+    __slots__ = ("_pool", "host", "_on_device", "_unique", "_what", "_checked")
 
-    def __init__(self, device: torch.device, host=None,
-                 device_ids: torch.Tensor | None = None) -> None:
-        self._device = device
-        if host is not None and not isinstance(host, ctypes.Array):
-            host = np.ascontiguousarray(host, dtype=np.int32)
+    def __init__(self, pool: KVPool, host=None, device_ids: torch.Tensor | None = None,
+                 unique: bool = False, what: str = "block") -> None:
+        self._pool = pool
+        self._unique = unique
+        self._what = what
+        self._checked = None
+        if host is not None and not isinstance(host, array):
+            host = self._checked = np.ascontiguousarray(host, dtype=np.int32)
         self.host = host
         self._on_device = device_ids
 
@@ -255,13 +277,17 @@ class _BlockIds:
         return len(self.host) if self.host is not None else self._on_device.numel()
 
     def _host_array(self) -> np.ndarray:
-        host = self.host
-        return np.frombuffer(host, dtype=np.int32) if isinstance(host, ctypes.Array) else host
+        """The host ids as a checked NumPy int32 array."""
+        if self._checked is None:
+            ids = self._pool.host_ids(np.frombuffer(self.host, dtype=np.int32),
+                                      unique=self._unique, what=self._what)
+            self._checked = np.ascontiguousarray(ids, dtype=np.int32)
+        return self._checked
 
     def __getitem__(self, index: slice) -> "_BlockIds":
         if self.host is not None:
-            return _BlockIds(self._device, host=self._host_array()[index])
-        return _BlockIds(self._device, device_ids=self._on_device[index])
+            return _BlockIds(self._pool, host=self._host_array()[index])
+        return _BlockIds(self._pool, device_ids=self._on_device[index])
 
     @property
     def inline(self) -> bool:
@@ -269,13 +295,13 @@ class _BlockIds:
 
     def host_pointer(self) -> int:
         host = self.host
-        if isinstance(host, ctypes.Array):
-            return ctypes.addressof(host)
+        if isinstance(host, array):
+            return host.buffer_info()[0]
         return host.__array_interface__["data"][0]
 
     def on_device(self) -> torch.Tensor:
         if self._on_device is None:
-            self._on_device = stage_ids(self._device, self._host_array())[0]
+            self._on_device = stage_ids(self._pool.device, self._host_array())[0]
         return self._on_device
 
 
@@ -436,11 +462,11 @@ class HipSlotCopier:
 
     def _ids(self, block_ids, *, unique: bool = False, what: str) -> "_BlockIds":
         if isinstance(block_ids, torch.Tensor) and block_ids.device.type == "cuda":
-            return _BlockIds(self.device, device_ids=self.pool.block_ids(block_ids, what=what))
-        short = self.pool.short_host_ids(block_ids, unique=unique, what=what)
+            return _BlockIds(self.pool, device_ids=self.pool.block_ids(block_ids, what=what))
+        short = _host_id_array(block_ids)
         if short is not None:
-            return _BlockIds(self.device, host=short)
-        return _BlockIds(self.device, host=self.pool.host_ids(block_ids, unique=unique, what=what))
+            return _BlockIds(self.pool, host=short, unique=unique, what=what)
+        return _BlockIds(self.pool, host=self.pool.host_ids(block_ids, unique=unique, what=what))
 
     def _gather(self, block_ids, location: str) -> PackedBlocks:
         ids = self._ids(block_ids, what="source block")
@@ -570,25 +596,21 @@ class HipSlotCopier:
             source.blocks_read += n
             self.blocks_written += n
             return
-        # Host ids: checked on the host and issued by destination id. Up to
-        # INLINE_IDS pairs travel in the launch's kernel arguments; longer lists
-        # are uploaded together with one copy. A short Python table is checked
-        # without NumPy.
-        pairs = short_issue_order(src_ids, dst_ids)
-        if pairs is not None:
-            s = source.pool.short_host_ids(pairs[0], what="source block")
-            d = self.pool.short_host_ids(pairs[1], unique=True, what="destination block")
-            if s is not None and d is not None:
-                if same_pool and not set(pairs[0]).isdisjoint(pairs[1]):
-                    raise ValueError("a direct copy within one pool needs disjoint source "
-                                     "and destination blocks")
-                n = len(d)
-                _native.call("iekv_copy_direct_ids", source.pool.native.handle,
-                             self.pool.native.handle, ctypes.addressof(s), ctypes.addressof(d),
-                             n, stream)
-                source.blocks_read += n
-                self.blocks_written += n
-                return
+        # Host ids, issued by destination id. Up to INLINE_IDS pairs travel in the
+        # launch's kernel arguments, and the library checks and orders them (a
+        # serving loop's short Python tables go there unconverted by NumPy);
+        # longer lists are checked here and uploaded together with one copy.
+        s, d = _host_id_array(src_ids), _host_id_array(dst_ids)
+        if s is not None and d is not None:
+            if len(s) != len(d):
+                raise ValueError(f"{len(s)} source blocks for {len(d)} destinations")
+            n = len(d)
+            _native.call("iekv_copy_direct_ids", source.pool.native.handle,
+                         self.pool.native.handle, s.buffer_info()[0], d.buffer_info()[0], n,
+                         stream)
+            source.blocks_read += n
+            self.blocks_written += n
+            return
         s, d = issue_order(src_ids, dst_ids)
         s = source.pool.host_ids(s, what="source block")
         d = self.pool.host_ids(d, unique=True, what="destination block", ascending=True)
@@ -614,22 +636,6 @@ class HipSlotCopier:
     def bytes_moved(self) -> int:
         """(reads + writes) x 2L x T, as ie/engine/copier.py:33-38 counts."""
         return (self.blocks_read + self.blocks_written) * self.pool.block_bytes
-
-
-def short_issue_order(src_ids, dst_ids):
-    """:func:`issue_order` for short Python tables: ``(src, dst)`` lists sorted by
-    destination id, or None when either table is not a list or tuple of at most
-    ``INLINE_IDS`` entries (``issue_order`` takes those)."""
-    if type(src_ids) not in (list, tuple) or type(dst_ids) not in (list, tuple) \
-            or len(dst_ids) > _native.INLINE_IDS:
-        return None
-    if len(src_ids) != len(dst_ids):
-        raise ValueError(f"{len(src_ids)} source blocks for {len(dst_ids)} destinations")
-    try:
-        order = sorted(range(len(dst_ids)), key=dst_ids.__getitem__)
-    except TypeError:
-        return None
-    return [src_ids[i] for i in order], [dst_ids[i] for i in order]
 
 
 def issue_order(src_ids, dst_ids) -> tuple[np.ndarray, np.ndarray]:
@@ -675,4 +681,4 @@ def stack_payloads(payloads: Iterable[BlockPayload]) -> PackedBlocks:
 
 
 __all__ = ["BlockPayload", "DeferredBlockPayload", "HipSlotCopier", "PackedBlocks", "copier_for",
-           "issue_order", "short_issue_order", "stack_payloads", "stream_handle"]
+           "issue_order", "stack_payloads", "stream_handle"]

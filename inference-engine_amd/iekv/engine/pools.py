@@ -11,7 +11,6 @@ keep the reference's per-layer shape, and the ``[N, bs, H, D]`` paged view
 """
 from __future__ import annotations
 
-import ctypes
 import math
 from typing import Sequence as Seq
 
@@ -127,32 +126,6 @@ class KVPool:
                 raise ValueError(f"block ids on {ids.device}, pool on {self.device}")
             return ids
         return stage_ids(self.device, self.host_ids(ids, unique=unique, what=what))[0]
-
-    def short_host_ids(self, ids, *, unique: bool = False, what: str = "block"):
-        """A short Python list or tuple of ids (at most ``INLINE_IDS``, the most a
-        host-id launch carries) as a ctypes int32 array, checked as :meth:`host_ids`
-        checks (IndexError for an id outside the pool, ValueError for a repeat with
-        ``unique``). None for anything else, which :meth:`host_ids` takes.
-
-        A block table is a short list in the serving loop; checking it in plain
-        Python costs well under a microsecond, against several for the NumPy
-        conversions of :meth:`host_ids`.
-        """
-        if type(ids) not in (list, tuple) or len(ids) > _native.INLINE_IDS:
-            return None
-        n = len(ids)
-        try:
-            lo, hi = (min(ids), max(ids)) if n else (0, 0)
-            out = (ctypes.c_int32 * n)(*ids)
-        except TypeError:
-            return None        # not plain integers: the NumPy path converts them
-        if lo < 0 or hi >= self.num_blocks:
-            bad = lo if lo < 0 else hi
-            raise IndexError(f"{what} id {bad} out of range for a pool of "
-                             f"{self.num_blocks} blocks")
-        if unique and n > 1 and len(set(ids)) != n:
-            raise ValueError(f"{what} ids must be distinct")
-        return out
 
     def host_ids(self, ids, *, unique: bool = False, what: str = "block",
                  ascending: bool = False) -> np.ndarray:

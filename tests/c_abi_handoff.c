@@ -120,9 +120,12 @@ int main(void) {
   CHECK_IEKV(iekv_unpack(dst, dev_ids + 3 * MOVED, MOVED, staging, staging_bytes, stream));
   CHECK_HIP(hipStreamSynchronize(stream));
 
-  /* An out-of-range host id is refused before anything is enqueued. */
+  /* An out-of-range host id, and a destination given twice, are refused before
+   * anything is enqueued. */
   int bad[1] = {BLOCKS};
-  if (iekv_copy_direct_ids(src, dst, bad, d_ids[0], 1, stream) != IEKV_ERR_INVALID) return 5;
+  if (iekv_copy_direct_ids(src, dst, bad, d_ids[0], 1, stream) != IEKV_ERR_RANGE) return 5;
+  int twice[2] = {d_ids[0][0], d_ids[0][0]};
+  if (iekv_copy_direct_ids(src, dst, s_ids[0], twice, 2, stream) != IEKV_ERR_IDS) return 5;
 
   CHECK_HIP(hipMemcpy(host, slab, 2 * POOL, hipMemcpyDeviceToHost));
   if (check(host + POOL, moved_to, moved_from)) return 1;

@@ -62,6 +62,11 @@ def test_the_bench_line_keeps_its_contract(gpu, tp):
     assert legs["gather_context"]["launches_per_step"] == 64
     assert legs["gather_per_array"]["launches_per_step"] == 64 * 8
     assert legs["batched"]["launches_per_step"] == 1
+    # the host's time to issue a step: positive, and within the timed pass's wall time
+    # (wall_s is rounded to milliseconds)
+    for name, leg in legs.items():
+        if "ms_per_step" in leg:
+            assert 0 < leg["host_issue_ms_per_step"] <= 1000 * leg["wall_s"] + 1.0, name
     # the host tier's round trip: the whole block list each way, then one call per block
     host = legs["host_roundtrip"]
     assert host["d2h_GBps"] > 0 and host["h2d_GBps"] > 0

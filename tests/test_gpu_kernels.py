@@ -665,10 +665,12 @@ def test_requests_issued_on_alternating_streams_are_bit_exact(gpu):
 
 
 def test_short_python_tables_and_numpy_tables_move_the_same_bytes(gpu):
-    """Short Python tables take the plain-Python id checks, NumPy arrays and long
-    lists the NumPy ones; both must move the same tiles and refuse the same ids.
-    Includes a table of exactly INLINE_IDS blocks, one past it, and a direct copy
-    within one pool."""
+    """Short Python tables go to the library unconverted (it checks and orders the
+    ids), NumPy arrays and long lists through the NumPy checks; both must move the
+    same tiles and refuse the same ids.
+    Table lengths sit on either side of INLINE_IDS (the most ids a launch's
+    arguments carry, and the longest list the library checks), and one direct
+    copy stays within one pool."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -676,7 +678,7 @@ def test_short_python_tables_and_numpy_tables_move_the_same_bytes(gpu):
     n_blocks = 700
     sk, sv = allocate(n_blocks, bs, 2, 2, 32, torch.float16, gpu, seed=91)
     src = HipSlotCopier(sk, sv, bs)
-    sizes = [1, 2, 7, _native.INLINE_IDS, _native.INLINE_IDS + 1]
+    sizes = [1, 2, 7, 100, _native.INLINE_IDS, _native.INLINE_IDS + 1]
     results = []
     for as_numpy in (False, True):
         dk, dv = allocate(n_blocks, bs, 2, 2, 32, torch.float16, gpu, seed=93)

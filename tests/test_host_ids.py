@@ -1,9 +1,15 @@
-"""Host-side id checks: the plain-Python path for short tables against the NumPy path.
+"""Host block ids: the library's checks of host-id calls against the pool's NumPy checks.
 
-``KVPool.short_host_ids`` and ``short_issue_order`` take a serving loop's short
-block tables without NumPy; for every input they accept they must give what
-``KVPool.host_ids`` and ``issue_order`` give, and raise what those raise. Both
-are pure host logic, so they run here on pools described by a block count.
+A serving loop hands the copier short Python tables; those go to the library's
+host-id entry points unconverted by NumPy (``_host_id_array``), and the library
+checks them (IEKV_ERR_RANGE for an id outside the pool, IEKV_ERR_IDS for a
+destination given twice or a copy within one pool whose sources overlap its
+destinations), which Python raises as IndexError / ValueError like the NumPy
+checks of ``KVPool.host_ids``. For every table, both must accept or refuse alike.
+
+No kernel runs: the pools are registered on a device that does not exist (their
+arrays are equally spaced, so registering touches no GPU), so a call whose ids
+pass every check stops at the device switch with IEKV_ERR_HIP.
 """
 from types import SimpleNamespace
 
@@ -11,68 +17,123 @@ import numpy as np
 import pytest
 
 from iekv import _native
-from iekv.engine.copier import issue_order, short_issue_order
+from iekv.engine.copier import _host_id_array, issue_order
 from iekv.engine.pools import KVPool
 
-
-def pool(num_blocks):
-    return SimpleNamespace(num_blocks=num_blocks)
+NO_DEVICE = 99
 
 
-def outcome(fn, *args, **kwargs):
+def pool(num_blocks, tile=64, arrays=2):
+    ptrs = [(1 << 30) + a * num_blocks * tile for a in range(arrays)]
+    return _native.Pool(ptrs, tile_bytes=tile, num_blocks=num_blocks, device=NO_DEVICE)
+
+
+def library_outcome(fn, *args):
+    """"pass" when every id check passed (the call then fails at the device switch),
+    else the exception type the id check raised."""
     try:
-        return "ok", np.asarray(fn(*args, **kwargs), dtype=np.int64).reshape(-1).tolist()
-    except (IndexError, ValueError) as e:
-        return type(e).__name__, str(e)
+        _native.call(fn, *args)
+    except (_native.NativeIndexError, _native.NativeValueError) as e:
+        assert isinstance(e, (IndexError, ValueError)) and isinstance(e, RuntimeError)
+        return "IndexError" if isinstance(e, IndexError) else "ValueError"
+    except _native.NativeError as e:
+        assert e.code == _native.IEKV_ERR_HIP, str(e)
+        return "pass"
+    raise AssertionError("a call on a device that does not exist succeeded")
 
 
-@pytest.mark.parametrize("seed", range(6))
-def test_short_tables_are_checked_like_the_numpy_path(seed):
-    rng = np.random.default_rng(seed)
-    for _ in range(400):
-        num_blocks = int(rng.integers(1, 40))
-        n = int(rng.integers(0, 12))
-        ids = [int(x) for x in rng.integers(-2, num_blocks + 2, size=n)]
-        kind = rng.integers(2)
-        table = ids if kind else tuple(ids)
-        unique = bool(rng.integers(2))
-        p = pool(num_blocks)
-        short = outcome(KVPool.short_host_ids, p, table, unique=unique, what="x")
-        ref = outcome(KVPool.host_ids, p, table, unique=unique, what="x")
-        assert short == ref, (table, unique, num_blocks)
+def numpy_outcome(check):
+    try:
+        check()
+    except IndexError:
+        return "IndexError"
+    except ValueError:
+        return "ValueError"
+    return "pass"
 
 
-def test_short_tables_take_only_short_lists_of_integers():
-    p = pool(1000)
-    assert KVPool.short_host_ids(p, np.arange(3)) is None            # arrays: NumPy path
-    assert KVPool.short_host_ids(p, [1.0, 2.0]) is None              # floats: NumPy path
-    assert KVPool.short_host_ids(p, list(range(_native.INLINE_IDS + 1))) is None
-    got = KVPool.short_host_ids(p, list(range(_native.INLINE_IDS)))
-    assert list(got) == list(range(_native.INLINE_IDS))
-    assert list(KVPool.short_host_ids(p, [np.int64(7), True])) == [7, 1]
-    assert len(KVPool.short_host_ids(p, [])) == 0
-    with pytest.raises(IndexError, match="id 1000 out of range"):
-        KVPool.short_host_ids(p, [3, 1000])
-    with pytest.raises(IndexError, match="id -1 out of range"):
-        KVPool.short_host_ids(p, (-1, 5))
-    with pytest.raises(ValueError, match="must be distinct"):
-        KVPool.short_host_ids(p, [4, 4], unique=True)
-    assert list(KVPool.short_host_ids(p, [4, 4])) == [4, 4]          # repeats allowed for sources
+def addr(a):
+    return a.buffer_info()[0]
+
+
+def test_short_lists_become_int32_arrays_and_the_rest_stays_with_numpy():
+    assert list(_host_id_array([3, 1, 2])) == [3, 1, 2]
+    assert list(_host_id_array((np.int64(7), True, -1))) == [7, 1, -1]   # the library checks
+    assert len(_host_id_array([])) == 0
+    assert _host_id_array(list(range(_native.INLINE_IDS))) is not None
+    assert _host_id_array(list(range(_native.INLINE_IDS + 1))) is None   # uploaded instead
+    assert _host_id_array(np.arange(3)) is None
+    assert _host_id_array([1.0, 2.0]) is None                            # not integers
+    assert _host_id_array([1 << 40]) is None                             # not 32-bit
 
 
 @pytest.mark.parametrize("seed", range(4))
-def test_short_issue_order_sorts_like_issue_order(seed):
+def test_direct_copy_ids_are_refused_alike_by_the_library_and_numpy(seed):
     rng = np.random.default_rng(seed)
-    for _ in range(300):
-        n = int(rng.integers(0, 20))
-        dst = [int(x) for x in rng.permutation(64)[:n]]
-        src = [int(x) for x in rng.integers(0, 64, size=n)]
-        s, d = short_issue_order(src, dst)
-        rs, rd = issue_order(src, dst)
-        assert s == rs.tolist() and d == rd.tolist()
-    with pytest.raises(ValueError, match="3 source blocks for 2 destinations"):
-        short_issue_order([1, 2, 3], [4, 5])
-    with pytest.raises(ValueError, match="3 source blocks for 2 destinations"):
-        issue_order([1, 2, 3], [4, 5])
-    assert short_issue_order(np.arange(2), [1, 2]) is None
-    assert short_issue_order([1] * 300, [2] * 300) is None
+    for case in range(300):
+        num_blocks = int(rng.integers(2, 40))
+        n = int(rng.integers(0, 10)) if case % 5 else int(rng.integers(200, _native.INLINE_IDS + 1))
+        src = [int(x) for x in rng.integers(-1, num_blocks + 1, size=n)]
+        if rng.integers(2):     # distinct, sometimes one past either end of the pool
+            dst = [int(x) for x in rng.permutation(max(n, num_blocks + 1))[:n]
+                   - rng.integers(0, 2)]
+        else:                   # repeats likely
+            dst = [int(x) for x in rng.integers(0, num_blocks, size=n)]
+        assert len(src) == len(dst) == n
+        same = bool(rng.integers(3) == 0)
+        a = pool(num_blocks)
+        b = a if same else pool(num_blocks)
+        s, d = _host_id_array(src), _host_id_array(dst)
+        if s is None or d is None:
+            continue
+        got = library_outcome("iekv_copy_direct_ids", a.handle, b.handle, addr(s), addr(d),
+                              n, None)
+
+        def numpy_check():
+            ss, dd = issue_order(src, dst)
+            ss = KVPool.host_ids(SimpleNamespace(num_blocks=num_blocks), ss, what="source block")
+            dd = KVPool.host_ids(SimpleNamespace(num_blocks=num_blocks), dd, unique=True,
+                                 what="destination block", ascending=True)
+            if same and np.isin(ss, dd).any():
+                raise ValueError("overlap")
+
+        assert got == numpy_outcome(numpy_check), (src, dst, same, num_blocks)
+        a.close()
+        b.close()
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_pack_and_unpack_ids_are_refused_alike_by_the_library_and_numpy(seed):
+    rng = np.random.default_rng(100 + seed)
+    for _ in range(200):
+        num_blocks = int(rng.integers(2, 30))
+        n = int(rng.integers(1, 12))
+        ids = [int(x) for x in rng.integers(-1, num_blocks + 1, size=n)]
+        p = pool(num_blocks)
+        h = _host_id_array(ids)
+        staging = np.zeros(n * p.block_bytes, dtype=np.uint8)
+        sp = staging.__array_interface__["data"][0]
+        fake = SimpleNamespace(num_blocks=num_blocks)
+        got = library_outcome("iekv_pack_ids", p.handle, addr(h), n, sp, staging.size, None)
+        assert got == numpy_outcome(lambda: KVPool.host_ids(fake, ids)), ids
+        got = library_outcome("iekv_unpack_ids", p.handle, addr(h), n, sp, staging.size, None)
+        assert got == numpy_outcome(lambda: KVPool.host_ids(fake, ids, unique=True)), ids
+        p.close()
+
+
+def test_the_library_names_the_offending_id():
+    p, q = pool(16), pool(16)
+    tables = {name: _host_id_array(t) for name, t in
+              {"a": [0, 1], "b": [3, 16], "c": [0, 1, 2], "d": [5, 9, 5], "e": [4, 1],
+               "f": [2, 4]}.items()}       # held here: the library reads them during the call
+    with pytest.raises(IndexError, match=r"destination block id 16 \(entry 1\) out of range"):
+        _native.call("iekv_copy_direct_ids", p.handle, q.handle, addr(tables["a"]),
+                     addr(tables["b"]), 2, None)
+    with pytest.raises(ValueError, match=r"destination block ids must be distinct \(id 5 given"):
+        _native.call("iekv_copy_direct_ids", p.handle, q.handle, addr(tables["c"]),
+                     addr(tables["d"]), 3, None)
+    with pytest.raises(ValueError, match=r"disjoint source and destination blocks \(block 4 is"):
+        _native.call("iekv_copy_direct_ids", p.handle, p.handle, addr(tables["e"]),
+                     addr(tables["f"]), 2, None)
+    p.close()
+    q.close()

@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 10
+    assert lib.iekv_abi_version() == 11
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -93,10 +93,10 @@ def test_host_id_calls_check_count_and_range_before_any_launch(lib):
     bad = (ctypes.c_int32 * 3)(0, 16, 2)
     staging = ctypes.create_string_buffer(3 * 2 * 64)
     rc = lib.iekv_unpack_ids(pool.handle, bad, 3, staging, len(staging), None)
-    assert rc == _native.IEKV_ERR_INVALID
+    assert rc == _native.IEKV_ERR_RANGE
     assert "destination block id 16 (entry 1)" in lib.iekv_last_error().decode()
     rc = lib.iekv_copy_direct_ids(pool.handle, pool.handle, bad, ids, 3, None)
-    assert rc == _native.IEKV_ERR_INVALID
+    assert rc == _native.IEKV_ERR_RANGE
     assert "source block id 16" in lib.iekv_last_error().decode()
     pool.close()
 
