@@ -586,8 +586,9 @@ class HipSlotCopier:
         stream = on.cuda_stream if on is not None else current_stream_handle(self.device)
         same_pool = source.pool.native.handle.value == self.pool.native.handle.value
         if on_device:
-            src = source.pool.block_ids(src_ids, what="source block")
-            dst = self.pool.block_ids(dst_ids, unique=True, what="destination block")
+            with self._on(on):          # a host-side table's upload is ordered on the copy's stream
+                src = source.pool.block_ids(src_ids, what="source block")
+                dst = self.pool.block_ids(dst_ids, unique=True, what="destination block")
             if src.numel() != dst.numel():
                 raise ValueError(f"{src.numel()} source blocks for {dst.numel()} destinations")
             n = dst.numel()

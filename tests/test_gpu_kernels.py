@@ -625,7 +625,9 @@ def test_a_hip_failure_raises_and_leaves_no_error_behind(gpu):
 def test_requests_issued_on_alternating_streams_are_bit_exact(gpu):
     """Independent requests on two side streams (copy_blocks / read_blocks /
     write_blocks with stream=), forked from and joined back into the current
-    stream: every destination tile equals the oracle's, source untouched."""
+    stream: every destination tile equals the oracle's, source untouched. One
+    request in three mixes a host source table with device destination ids, whose
+    host side is uploaded on the request's stream."""
     from iekv.engine.copier import HipSlotCopier
 
     bs = 16
@@ -636,24 +638,27 @@ def test_requests_issued_on_alternating_streams_are_bit_exact(gpu):
     rng = np.random.default_rng(89)
     src_perm, dst_perm = rng.permutation(200), rng.permutation(200)
     sizes = [int(n) for n in rng.integers(1, 12, size=16)]
+    at, src_tables, dst_tables = 0, [], []
+    for n in sizes:
+        src_tables.append([int(b) for b in src_perm[at:at + n]])
+        dst_tables.append([int(b) for b in dst_perm[at:at + n]])
+        at += n
+    # device ids made (and complete) before the fork; held until after the join
+    dst_on_device = [torch.tensor(d, dtype=torch.int32, device=gpu) for d in dst_tables]
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
     main = torch.cuda.current_stream()
     start = torch.cuda.Event()
     start.record(main)
     for st in streams:
         st.wait_event(start)
-    at, src_tables, dst_tables = 0, [], []
-    for k, n in enumerate(sizes):
-        s_ids = [int(b) for b in src_perm[at:at + n]]
-        d_ids = [int(b) for b in dst_perm[at:at + n]]
-        at += n
+    for k, (s_ids, d_ids) in enumerate(zip(src_tables, dst_tables)):
         st = streams[k % 2]
-        if k % 3:
+        if k % 3 == 1:
+            dst.copy_blocks(src, s_ids, dst_on_device[k], stream=st)
+        elif k % 3:
             dst.copy_blocks(src, s_ids, d_ids, stream=st)
         else:
             dst.write_blocks(d_ids, src.read_blocks(s_ids, stream=st), stream=st)
-        src_tables.append(s_ids)
-        dst_tables.append(d_ids)
     for st in streams:
         done = torch.cuda.Event()
         done.record(st)
@@ -662,6 +667,7 @@ def test_requests_issued_on_alternating_streams_are_bit_exact(gpu):
     handoff(src_o, dst_o, src_tables, dst_tables)
     assert_pool_equals(dk, dv, dst_o)
     assert_pool_equals(sk, sv, src_o)
+    del dst_on_device
 
 
 def test_short_python_tables_and_numpy_tables_move_the_same_bytes(gpu):
