@@ -20,6 +20,8 @@ without NaN codes for fp8). Legs:
   copier       the drop-in Python path: HipSlotCopier.copy_blocks per request with the
                block tables as Python lists (id checks and hand-over included; 2P bytes)
   copier_pack_unpack  the same for pack mode: read_blocks then write_blocks (4P bytes)
+  requests     the direct leg's per-request launches issued by the library in one call
+               per step (iekv_copy_direct_requests), without a Python loop (2P bytes)
   write_kv     the prefill side: every request's new K/V rows of every layer scattered
                into the prefill pool by slot, one iekv_write_slots_layers launch per
                request (read + write of every row); write_kv_per_layer: one
@@ -75,7 +77,7 @@ METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff
 # Legs that move the workload's blocks from the prefill pool to the decode pool; the
 # first of them in --legs gives the line's value (2P / step time).
 HANDOFF_LEGS = ("direct", "pack_unpack", "pack", "unpack", "batched", "copier",
-                "copier_pack_unpack")
+                "copier_pack_unpack", "requests")
 # The slot kernels on either side of the handoff (prefill's KV writes, decode's reads).
 SLOT_LEGS = ("write_kv", "write_kv_per_layer", "gather_context", "gather_per_array")
 
@@ -196,7 +198,7 @@ class Legs:
     def plan(self, name: str) -> list[tuple[int, int]]:
         bb = self.w.shape.block_bytes
         sizes = [len(t) for t in self.w.src_tables]
-        if name in ("direct", "copier"):
+        if name in ("direct", "copier", "requests"):
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
         if name in ("pack_unpack", "copier_pack_unpack"):
             return [x for r, n in enumerate(sizes) for x in ((2 * n * bb, r), (2 * n * bb, r))]
@@ -421,6 +423,26 @@ class Legs:
             st = self.stagings[k % len(hs)]
             _native.call("iekv_unpack", self.dst.native.handle, d.data_ptr(), d.numel(),
                          st.data_ptr(), st.numel(), hs[k % len(hs)])
+        self._join()
+
+    def requests(self) -> None:
+        """The direct leg's per-request launches issued by the library in one call
+        (iekv_copy_direct_requests), request k on request stream k mod S."""
+        import ctypes
+        from array import array
+
+        from iekv import _native
+
+        if not hasattr(self, "_requests"):
+            torch = self.torch
+            self._requests = (array("i", [t.numel() for t in self.src_direct]),
+                              torch.cat(self.src_direct), torch.cat(self.dst_direct))
+        counts, src, dst = self._requests
+        hs = self._fork()
+        handles = (ctypes.c_void_p * len(hs))(*hs)
+        _native.call("iekv_copy_direct_requests", self.src.native.handle, self.dst.native.handle,
+                     len(counts), counts.buffer_info()[0], src.data_ptr(), dst.data_ptr(),
+                     handles, len(hs), None)
         self._join()
 
     def batched(self) -> None:
@@ -678,8 +700,8 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
         "avg_launch_us": round(1000 * total_ms / max(1, len(durations)), 2),
         "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
     }
-    if name in ("direct", "copier", "pack_unpack", "copier_pack_unpack", "pack", "unpack",
-                *SLOT_LEGS):
+    if name in ("direct", "copier", "requests", "pack_unpack", "copier_pack_unpack", "pack",
+                "unpack", *SLOT_LEGS):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
                                  "p50": round(req_ms[len(req_ms) // 2], 4),
                                  "p99": round(req_ms[min(len(req_ms) - 1,
@@ -901,8 +923,8 @@ def main() -> int:
                          "(default: cfg3 64; cfg4 the cfg3 engine's pools, 49,598 blocks)")
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
                     help="comma list of direct, pack_unpack, pack, unpack, batched, copier, "
-                         "copier_pack_unpack, write_kv, write_kv_per_layer, gather_context, "
-                         "gather_per_array, plain_copy, host_roundtrip")
+                         "copier_pack_unpack, requests, write_kv, write_kv_per_layer, "
+                         "gather_context, gather_per_array, plain_copy, host_roundtrip")
     ap.add_argument("--cpu-blocks", type=int, default=1536,
                     help="blocks in the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,

@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 11
+#define IEKV_ABI_VERSION 12
 
 enum {
   IEKV_OK = 0,
@@ -107,6 +107,25 @@ int iekv_pack(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
  * single-block restore write (ie/core/block_manager.py:162). */
 int iekv_unpack(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                 const void* staging, int64_t staging_bytes, hipStream_t stream);
+
+/* Several independent direct handoffs in one call, one launch per request, as a
+ * decode step admits several prefilled requests: request k moves counts[k]
+ * (host array) blocks, its ids following request k-1's in src_ids / dst_ids
+ * (device memory, as iekv_copy_direct takes them), on streams[k % n_streams].
+ * When done_events is not null, done_events[k] (created by the caller) is
+ * recorded on that stream right after request k's launch, so a consumer can
+ * wait for exactly that request. Requests must not share destination blocks.
+ * The caller orders every stream after the writes of the source blocks, and
+ * waits on the streams or events before reading a destination. Each request's
+ * launch is iekv_copy_direct's, issued without a call per request from the
+ * caller: the host's cost per request is then HIP's own launch cost (measured
+ * 2.3-4.5 us on MI355X boxes, against 0.3 us more through a Python loop).
+ * Replaces: the per-prompt handoffs of DisaggregatedEngine.generate
+ * (ie/serve/disaggregated.py:106-116), each of them disaggregated.py:50 + :81-82. */
+int iekv_copy_direct_requests(const iekv_pool* src, const iekv_pool* dst, int32_t n_requests,
+                              const int32_t* counts, const int32_t* src_ids,
+                              const int32_t* dst_ids, const hipStream_t* streams,
+                              int32_t n_streams, hipEvent_t* done_events);
 
 /* Most block ids a call with HOST ids (the *_ids entry points below) takes. */
 #define IEKV_INLINE_IDS 256

@@ -1223,6 +1223,49 @@ int iekv_copy_direct(const iekv_pool* src, const iekv_pool* dst, const int32_t* 
                                  std::min(src->align, dst->align), stream);
 }
 
+int iekv_copy_direct_requests(const iekv_pool* src, const iekv_pool* dst, int32_t n_requests,
+                              const int32_t* counts, const int32_t* src_ids,
+                              const int32_t* dst_ids, const hipStream_t* streams,
+                              int32_t n_streams, hipEvent_t* done_events) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_pool(dst, "destination"))) return rc;
+  if (n_requests < 0)
+    return set_error(IEKV_ERR_INVALID, "n_requests is negative (%d)", n_requests);
+  if (n_requests == 0) return IEKV_OK;
+  if (!counts) return set_error(IEKV_ERR_INVALID, "counts is null");
+  if (n_streams <= 0 || !streams)
+    return set_error(IEKV_ERR_INVALID, "need at least one stream (n_streams %d)", n_streams);
+  int64_t total = 0;
+  for (int32_t k = 0; k < n_requests; ++k) {
+    if (counts[k] < 0)
+      return set_error(IEKV_ERR_INVALID, "request %d has a negative count (%d)", k, counts[k]);
+    total += counts[k];
+  }
+  if (total > INT32_MAX)
+    return set_error(IEKV_ERR_INVALID, "%lld blocks exceed one call", static_cast<long long>(total));
+  if ((rc = check_ids(src_ids, static_cast<int32_t>(total), "source")) ||
+      (rc = check_ids(dst_ids, static_cast<int32_t>(total), "destination")))
+    return rc;
+  if (src->n_arrays != dst->n_arrays || src->tile_bytes != dst->tile_bytes)
+    return set_error(IEKV_ERR_INVALID, "pools differ in shape");
+  if (src->device != dst->device)
+    return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
+                     dst->device);
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return guard.fail();
+  const int align = std::min(src->align, dst->align);
+  int64_t at = 0;
+  for (int32_t k = 0; k < n_requests; ++k) {
+    hipStream_t stream = streams[k % n_streams];
+    if ((rc = launch_move<true, true>(src, dst, nullptr, nullptr, src_ids + at, dst_ids + at,
+                                      counts[k], src->tile_bytes, src->n_arrays, align, stream)))
+      return rc;
+    if (done_events) IEKV_HIP(hipEventRecord(done_events[k], stream));
+    at += counts[k];
+  }
+  return IEKV_OK;
+}
+
 int iekv_pack(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, void* staging,
               int64_t staging_bytes, hipStream_t stream) {
   int rc;

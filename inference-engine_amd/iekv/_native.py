@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most ids a host-id call takes
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
@@ -34,6 +34,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                  POINTER(c_void_p)]),
     "iekv_pool_destroy": (c_int, [c_void_p]),
     "iekv_copy_direct": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
+    "iekv_copy_direct_requests": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
+                                          c_void_p, c_void_p, c_int32, c_void_p]),
     "iekv_pack": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
     "iekv_unpack": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p]),
     "iekv_copy_direct_ids": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),

@@ -633,6 +633,72 @@ class HipSlotCopier:
         source.blocks_read += n
         self.blocks_written += n
 
+    def copy_requests(self, source: "HipSlotCopier", tables, *,
+                      streams: Seq[torch.cuda.Stream] | None = None,
+                      done_events: Seq[torch.cuda.Event] | None = None) -> None:
+        """Direct moves of several independent requests, one launch each, in one call.
+
+        ``tables`` holds one ``(src_ids, dst_ids)`` pair of host tables per request
+        (iekv_copy_direct_requests). Request k runs on ``streams[k % len(streams)]``
+        (default: the current stream); every stream is first ordered after the
+        current stream, where the ids are uploaded, and the caller orders later
+        readers of the destinations after the streams, or after ``done_events[k]``,
+        recorded right after request k's launch. Ids are checked as
+        :meth:`copy_blocks` checks them, and requests may not share destination
+        blocks. Each request's pairs are issued by destination id.
+        """
+        if not self.pool.same_shape(source.pool):
+            raise ValueError("source and destination pools differ in layout")
+        if source.device != self.device:
+            raise ValueError(f"pools on {source.device} and {self.device}")
+        streams = list(streams) if streams else [torch.cuda.current_stream(self.device)]
+        for st in streams:
+            if st.device != self.device:
+                raise ValueError(f"stream on {st.device}, pool on {self.device}")
+        if done_events is not None and len(done_events) != len(tables):
+            raise ValueError(f"{len(done_events)} events for {len(tables)} requests")
+        self.flush()
+        counts, src_all, dst_all = [], [], []
+        for src_ids, dst_ids in tables:
+            s, d = issue_order(src_ids, dst_ids)
+            counts.append(int(d.size))
+            src_all.append(s)
+            dst_all.append(d)
+        s = source.pool.host_ids(np.concatenate(src_all) if src_all else [], what="source block")
+        d = self.pool.host_ids(np.concatenate(dst_all) if dst_all else [], unique=True,
+                               what="destination block")
+        if source.pool.native.handle.value == self.pool.native.handle.value and \
+                bool(np.isin(s, d).any()):
+            raise ValueError("a direct copy within one pool needs disjoint source "
+                             "and destination blocks")
+        if not counts:
+            return
+        src, dst = stage_ids(self.device, s, d)
+        current = torch.cuda.current_stream(self.device)
+        uploaded = torch.cuda.Event()
+        uploaded.record(current)
+        for st in streams:
+            if st != current:
+                st.wait_event(uploaded)
+        events = None
+        if done_events is not None:
+            for ev in done_events:
+                if not ev.cuda_event:         # torch creates its events at the first record
+                    ev.record(current)
+            events = (ctypes.c_void_p * len(done_events))(*[ev.cuda_event for ev in done_events])
+        handles = (ctypes.c_void_p * len(streams))(*[st.cuda_stream for st in streams])
+        count_array = array("i", counts)
+        _native.call("iekv_copy_direct_requests", source.pool.native.handle,
+                     self.pool.native.handle, len(counts), count_array.buffer_info()[0],
+                     src.data_ptr(), dst.data_ptr(), handles, len(streams), events)
+        for st in streams:          # the id buffers are freed on the current stream
+            if st != current:
+                src.record_stream(st)
+                dst.record_stream(st)
+        total = int(d.size)
+        source.blocks_read += total
+        self.blocks_written += total
+
     @property
     def bytes_moved(self) -> int:
         """(reads + writes) x 2L x T, as ie/engine/copier.py:33-38 counts."""

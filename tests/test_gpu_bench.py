@@ -17,6 +17,7 @@ pytestmark = pytest.mark.gpu
 
 ROOT = Path(__file__).resolve().parents[1]
 LEGS = ["direct", "pack_unpack", "pack", "unpack", "batched", "copier", "copier_pack_unpack",
+        "requests",
         "write_kv", "write_kv_per_layer", "gather_context", "gather_per_array",
         "host_roundtrip"]
 
@@ -62,6 +63,7 @@ def test_the_bench_line_keeps_its_contract(gpu, tp):
     assert legs["gather_context"]["launches_per_step"] == 64
     assert legs["gather_per_array"]["launches_per_step"] == 64 * 8
     assert legs["batched"]["launches_per_step"] == 1
+    assert legs["requests"]["launches_per_step"] == legs["direct"]["launches_per_step"] == 64
     # the host's time to issue a step: positive, and within the timed pass's wall time
     # (wall_s is rounded to milliseconds)
     for name, leg in legs.items():

@@ -670,6 +670,55 @@ def test_requests_issued_on_alternating_streams_are_bit_exact(gpu):
     del dst_on_device
 
 
+def test_a_request_list_moves_each_request_on_its_stream_with_its_event(gpu):
+    """copy_requests (iekv_copy_direct_requests): one launch per request on streams
+    in turn, an event per request; once request k's event completes, its tiles are
+    in place. Empty requests, requests of one block and of hundreds, three streams;
+    the whole pool equals the oracle's at the end, and bad tables are refused
+    before anything is enqueued."""
+    from iekv.engine.copier import HipSlotCopier
+
+    bs = 16
+    sk, sv = allocate(900, bs, 2, 2, 32, torch.float16, gpu, seed=101)
+    dk, dv = allocate(900, bs, 2, 2, 32, torch.float16, gpu, seed=102)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    rng = np.random.default_rng(103)
+    sizes = [3, 0, 1, 300, 17, 0, 2, 260, 40, 5]
+    src_perm, dst_perm = rng.permutation(900), rng.permutation(900)
+    tables, at = [], 0
+    for n in sizes:
+        tables.append(([int(b) for b in src_perm[at:at + n]],
+                       [int(b) for b in dst_perm[at:at + n]]))
+        at += n
+    streams = [torch.cuda.current_stream(), torch.cuda.Stream(), torch.cuda.Stream()]
+    events = [torch.cuda.Event() for _ in tables]
+    dst.copy_requests(src, tables, streams=streams, done_events=events)
+    src_bytes = host_bytes(sk + sv)
+    for (s_ids, d_ids), ev in zip(tables, events):
+        ev.synchronize()
+        if not d_ids:
+            continue
+        d_t = torch.tensor(d_ids, device=gpu)
+        for a, cache in enumerate(dk + dv):
+            rows = torch.stack([d_t * bs + r for r in range(bs)], 1).reshape(-1)
+            got = cache.view(torch.uint8).reshape(cache.shape[0], -1)[rows].cpu().numpy()
+            want = np.concatenate([src_bytes[a][b * bs:(b + 1) * bs] for b in s_ids])
+            assert np.array_equal(got, want), (a, len(d_ids))
+    for st in streams:
+        st.synchronize()
+    handoff(src_o, dst_o, [t[0] for t in tables], [t[1] for t in tables])
+    assert_pool_equals(dk, dv, dst_o)
+    assert src.blocks_read == dst.blocks_written == sum(sizes)
+    with pytest.raises(ValueError, match="must be distinct"):       # shared destination
+        dst.copy_requests(src, [([1], [5]), ([2], [5])])
+    with pytest.raises(IndexError, match="out of range"):
+        dst.copy_requests(src, [([1], [900])])
+    with pytest.raises(ValueError, match="2 events for 1 requests"):
+        dst.copy_requests(src, [([1], [5])], done_events=[torch.cuda.Event()] * 2)
+    assert dst.blocks_written == sum(sizes)
+
+
 def test_short_python_tables_and_numpy_tables_move_the_same_bytes(gpu):
     """Short Python tables go to the library unconverted (it checks and orders the
     ids), NumPy arrays and long lists through the NumPy checks; both must move the

@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 11
+    assert lib.iekv_abi_version() == 12
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -98,6 +98,33 @@ def test_host_id_calls_check_count_and_range_before_any_launch(lib):
     rc = lib.iekv_copy_direct_ids(pool.handle, pool.handle, bad, ids, 3, None)
     assert rc == _native.IEKV_ERR_RANGE
     assert "source block id 16" in lib.iekv_last_error().decode()
+    pool.close()
+
+
+def test_request_lists_are_checked_before_any_launch(lib):
+    """iekv_copy_direct_requests checks its counts, ids and streams first; a slab
+    pool registers without touching the GPU."""
+    from iekv import _native
+
+    pool = _native.Pool([1 << 20, (1 << 20) + 64 * 16], tile_bytes=64, num_blocks=16, device=0)
+    h = pool.handle
+    counts = (ctypes.c_int32 * 2)(1, 2)
+    ids = (ctypes.c_int32 * 3)(0, 1, 2)
+    streams = (ctypes.c_void_p * 1)(None)
+    cases = [
+        ((h, h, -1, counts, ids, ids, streams, 1, None), "n_requests is negative"),
+        ((h, h, 2, None, ids, ids, streams, 1, None), "counts is null"),
+        ((h, h, 2, counts, ids, ids, None, 1, None), "need at least one stream"),
+        ((h, h, 2, counts, ids, ids, streams, 0, None), "need at least one stream"),
+        ((h, h, 2, (ctypes.c_int32 * 2)(1, -2), ids, ids, streams, 1, None),
+         "request 1 has a negative count"),
+        ((h, h, 2, counts, None, ids, streams, 1, None), "source ids are null"),
+        ((None, h, 2, counts, ids, ids, streams, 1, None), "null"),
+    ]
+    for args, message in cases:
+        assert lib.iekv_copy_direct_requests(*args) == _native.IEKV_ERR_INVALID, message
+        assert message in lib.iekv_last_error().decode(), message
+    assert lib.iekv_copy_direct_requests(h, h, 0, None, None, None, None, 0, None) == 0
     pool.close()
 
 
