@@ -198,10 +198,25 @@ class Legs:
     def plan(self, name: str) -> list[tuple[int, int]]:
         bb = self.w.shape.block_bytes
         sizes = [len(t) for t in self.w.src_tables]
-        if name in ("direct", "copier", "requests"):
+        if name in ("direct", "requests"):
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
-        if name in ("pack_unpack", "copier_pack_unpack"):
+        if name == "pack_unpack":
             return [x for r, n in enumerate(sizes) for x in ((2 * n * bb, r), (2 * n * bb, r))]
+        if name in ("copier", "copier_pack_unpack"):
+            # the copier hands a table of up to HOST_IDS_MAX ids to the library's
+            # host-id entry points, which issue INLINE_IDS ids per launch; a longer
+            # table is uploaded and moved in one launch
+            from iekv import _native
+            from iekv.engine.copier import HOST_IDS_MAX
+
+            def launches(n, r):
+                if n > HOST_IDS_MAX:
+                    return [(2 * n * bb, r)]
+                step = _native.INLINE_IDS
+                return [(2 * min(step, n - k) * bb, r) for k in range(0, n, step)]
+
+            per = 2 if name == "copier_pack_unpack" else 1   # pack, then unpack
+            return [x for r, n in enumerate(sizes) for _ in range(per) for x in launches(n, r)]
         if name in ("pack", "unpack"):
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
         if name == "batched":
@@ -662,13 +677,17 @@ def time_leg(legs: Legs, name: str, steps: int, warmup: int, per_launch: bool = 
     streams, stagings = legs.streams, legs.stagings
     legs.streams, legs.stagings = streams[:1], stagings[:1]
     try:
-        with _native.LaunchTimer(steps * len(plan)) as timer:
+        # one spare slot: a leg that launches more than its plan says is caught below
+        with _native.LaunchTimer(steps * len(plan) + 1) as timer:
             for _ in range(steps):
                 step()
             torch.cuda.synchronize()
         legs.last_streams = 1
     finally:
         legs.streams, legs.stagings = streams, stagings
+    if len(timer.durations_ms) != steps * len(plan):
+        raise RuntimeError(f"{name}: {len(timer.durations_ms)} launches timed, the leg's plan "
+                           f"has {steps * len(plan)}")
     launches = [(ms, nbytes, r) for ms, (nbytes, r) in zip(timer.durations_ms, plan * steps)]
     return ms_step, wall, launches
 

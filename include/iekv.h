@@ -22,8 +22,7 @@
  *   byte image of the reference payload ([K_0..K_{L-1}], [V_0..V_{L-1}])
  *   (copier.py:21-22).
  *   Block ids are int32 in DEVICE memory, except for the *_ids entry points,
- *   which take at most IEKV_INLINE_IDS ids in HOST memory and check them
- *   before launching. Callers validate device ids against the pool size
+ *   which take ids in HOST memory and check them before launching. Callers validate device ids against the pool size
  *   before a call; kernels skip a tile whose id is out of range so a bad id
  *   can never address memory outside the pool. The tiles of one call are
  *   moved concurrently: destination ids must be distinct, and a direct copy
@@ -50,7 +49,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 12
+#define IEKV_ABI_VERSION 13
 
 enum {
   IEKV_OK = 0,
@@ -127,14 +126,16 @@ int iekv_copy_direct_requests(const iekv_pool* src, const iekv_pool* dst, int32_
                               const int32_t* dst_ids, const hipStream_t* streams,
                               int32_t n_streams, hipEvent_t* done_events);
 
-/* Most block ids a call with HOST ids (the *_ids entry points below) takes. */
+/* Most block ids one launch of a host-id call (the *_ids entry points below)
+ * carries in its kernel arguments. */
 #define IEKV_INLINE_IDS 256
 
-/* The same three moves with the block ids given in HOST memory, for at most
- * IEKV_INLINE_IDS blocks: the ids travel in the launch's own kernel arguments,
- * so the caller needs no device id buffer and no host-to-device id copy sits on
- * the stream between launches. One block per workgroup whatever
- * iekv_set_launch's run_blocks. The ids are checked on the host before anything
+/* The same three moves with the block ids given in HOST memory, any number of
+ * them: the ids travel in the launches' own kernel arguments, IEKV_INLINE_IDS
+ * blocks per launch (a longer list is issued as consecutive launches), so the
+ * caller needs no device id buffer and no host-to-device id copy sits on the
+ * stream between launches. One block per workgroup whatever iekv_set_launch's
+ * run_blocks. The ids are checked on the host before anything
  * is enqueued: an id outside its pool returns IEKV_ERR_RANGE; a destination id
  * given twice (iekv_copy_direct_ids, iekv_unpack_ids), or a copy within one pool
  * whose sources overlap its destinations, returns IEKV_ERR_IDS. iekv_copy_direct_ids

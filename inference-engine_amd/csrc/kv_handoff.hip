@@ -907,24 +907,21 @@ int restore_pipeline(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blo
   return IEKV_OK;
 }
 
-// Copy n host ids into ids->v[off..off+n), checking each against the pool.
-int fill_inline(const int32_t* host_ids, int32_t n, int64_t num_blocks, const char* what,
-                InlineIds* ids, int32_t off) {
+// IEKV_ERR_RANGE unless each of the n host ids lies in [0, num_blocks).
+int check_host_range(const int32_t* host_ids, int32_t n, int64_t num_blocks, const char* what) {
   for (int32_t i = 0; i < n; ++i) {
     const int32_t id = host_ids[i];
     if (id < 0 || id >= num_blocks)
       return set_error(IEKV_ERR_RANGE, "%s block id %d (entry %d) out of range for a pool of "
                        "%lld blocks", what, id, i, static_cast<long long>(num_blocks));
-    ids->v[off + i] = id;
   }
   return IEKV_OK;
 }
 
-// IEKV_ERR_IDS unless the n (<= IEKV_INLINE_IDS) ids at v are distinct.
+// IEKV_ERR_IDS unless the n ids at v are distinct.
 int check_distinct(const int32_t* v, int32_t n, const char* what) {
-  int32_t sorted[IEKV_INLINE_IDS];
-  std::copy(v, v + n, sorted);
-  std::sort(sorted, sorted + n);
+  std::vector<int32_t> sorted(v, v + n);
+  std::sort(sorted.begin(), sorted.end());
   for (int32_t i = 1; i < n; ++i)
     if (sorted[i] == sorted[i - 1])
       return set_error(IEKV_ERR_IDS, "%s block ids must be distinct (id %d given twice)", what,
@@ -933,42 +930,72 @@ int check_distinct(const int32_t* v, int32_t n, const char* what) {
 }
 
 // The checked (src, dst) pairs of a host-id direct copy, reordered by ascending
-// destination id: sources at ids->v[0..n), destinations at ids->v[n..2n).
-// IEKV_ERR_IDS for a destination given twice, and, when both sides are the same
-// pool, for a block that is both a source and a destination (its bytes would
-// depend on the order the workgroups run in).
-int order_pairs(InlineIds* ids, int32_t n, bool same_pool) {
-  uint64_t key[IEKV_INLINE_IDS];   // destination in the high half: sorting orders by it
+// destination id into src_out / dst_out. IEKV_ERR_IDS for a destination given
+// twice, and, when both sides are the same pool, for a block that is both a
+// source and a destination (its bytes would depend on the order the workgroups
+// run in).
+int order_pairs(const int32_t* src_ids, const int32_t* dst_ids, int32_t n, bool same_pool,
+                std::vector<int32_t>* src_out, std::vector<int32_t>* dst_out) {
+  std::vector<uint64_t> key(n);   // destination in the high half: sorting orders by it
   for (int32_t i = 0; i < n; ++i)
-    key[i] = (static_cast<uint64_t>(static_cast<uint32_t>(ids->v[n + i])) << 32) |
-             static_cast<uint32_t>(ids->v[i]);
-  std::sort(key, key + n);
+    key[i] = (static_cast<uint64_t>(static_cast<uint32_t>(dst_ids[i])) << 32) |
+             static_cast<uint32_t>(src_ids[i]);
+  std::sort(key.begin(), key.end());
+  src_out->resize(n);
+  dst_out->resize(n);
+  int32_t* s = src_out->data();
+  int32_t* d = dst_out->data();
   for (int32_t i = 0; i < n; ++i) {
-    ids->v[i] = static_cast<int32_t>(key[i] & 0xffffffffu);
-    ids->v[n + i] = static_cast<int32_t>(key[i] >> 32);
-    if (i > 0 && ids->v[n + i] == ids->v[n + i - 1])
+    s[i] = static_cast<int32_t>(key[i] & 0xffffffffu);
+    d[i] = static_cast<int32_t>(key[i] >> 32);
+    if (i > 0 && d[i] == d[i - 1])
       return set_error(IEKV_ERR_IDS, "destination block ids must be distinct (id %d given "
-                       "twice)", ids->v[n + i]);
+                       "twice)", d[i]);
   }
   if (same_pool) {
-    int32_t srcs[IEKV_INLINE_IDS];
-    std::copy(ids->v, ids->v + n, srcs);
-    std::sort(srcs, srcs + n);
-    for (int32_t i = 0, j = 0; i < n && j < n;) {   // destinations ids->v[n..2n) ascend
-      if (srcs[i] == ids->v[n + j])
+    std::vector<int32_t> srcs(s, s + n);
+    std::sort(srcs.begin(), srcs.end());
+    for (int32_t i = 0, j = 0; i < n && j < n;) {   // d ascends
+      if (srcs[i] == d[j])
         return set_error(IEKV_ERR_IDS, "a direct copy within one pool needs disjoint source "
                          "and destination blocks (block %d is both)", srcs[i]);
-      if (srcs[i] < ids->v[n + j]) ++i; else ++j;
+      if (srcs[i] < d[j]) ++i; else ++j;
     }
   }
   return IEKV_OK;
 }
 
-int check_inline_count(int32_t n_blocks, const int32_t* a, const int32_t* b) {
-  if (n_blocks < 0 || n_blocks > IEKV_INLINE_IDS)
-    return set_error(IEKV_ERR_INVALID, "n_blocks %d is outside 0..%d for host ids", n_blocks,
-                     IEKV_INLINE_IDS);
+int check_host_count(int32_t n_blocks, const int32_t* a, const int32_t* b) {
+  if (n_blocks < 0)
+    return set_error(IEKV_ERR_INVALID, "n_blocks is negative (%d) for host ids", n_blocks);
   if (n_blocks > 0 && (!a || !b)) return set_error(IEKV_ERR_INVALID, "host ids are null");
+  return IEKV_OK;
+}
+
+// A move whose (checked) ids are in host memory, in launches of at most
+// IEKV_INLINE_IDS blocks that carry their ids in their kernel arguments. src_ids
+// (when the source is a pool) and dst_ids (when the destination is) hold
+// n_blocks ids; staging images follow the list order.
+template <bool SP, bool DP>
+int launch_host_ids(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
+                    char* dst_stage, const int32_t* src_ids, const int32_t* dst_ids,
+                    int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
+                    hipStream_t stream) {
+  const int64_t image = tile_bytes * n_arrays;
+  for (int32_t first = 0; first < n_blocks; first += IEKV_INLINE_IDS) {
+    const int32_t m = std::min<int32_t>(IEKV_INLINE_IDS, n_blocks - first);
+    InlineIds ids{};
+    int32_t dst_off = 0;
+    if (SP) {
+      std::copy(src_ids + first, src_ids + first + m, ids.v);
+      dst_off = m;
+    }
+    if (DP) std::copy(dst_ids + first, dst_ids + first + m, ids.v + dst_off);
+    const int rc = launch_move_inline<SP, DP>(
+        sp, dp, SP ? nullptr : src_stage + first * image, DP ? nullptr : dst_stage + first * image,
+        ids, dst_off, m, tile_bytes, n_arrays, align, stream);
+    if (rc) return rc;
+  }
   return IEKV_OK;
 }
 
@@ -1303,62 +1330,60 @@ int iekv_copy_direct_ids(const iekv_pool* src, const iekv_pool* dst, const int32
                          const int32_t* dst_ids, int32_t n_blocks, hipStream_t stream) {
   int rc;
   if ((rc = check_pool(src, "source")) || (rc = check_pool(dst, "destination")) ||
-      (rc = check_inline_count(n_blocks, src_ids, dst_ids)))
+      (rc = check_host_count(n_blocks, src_ids, dst_ids)))
     return rc;
   if (src->n_arrays != dst->n_arrays || src->tile_bytes != dst->tile_bytes)
     return set_error(IEKV_ERR_INVALID, "pools differ in shape");
   if (src->device != dst->device)
     return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
                      dst->device);
-  InlineIds ids{};
-  if ((rc = fill_inline(src_ids, n_blocks, src->num_blocks, "source", &ids, 0)) ||
-      (rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, n_blocks)) ||
-      (rc = order_pairs(&ids, n_blocks, src == dst)))
+  std::vector<int32_t> s, d;
+  if ((rc = check_host_range(src_ids, n_blocks, src->num_blocks, "source")) ||
+      (rc = check_host_range(dst_ids, n_blocks, dst->num_blocks, "destination")) ||
+      (rc = order_pairs(src_ids, dst_ids, n_blocks, src == dst, &s, &d)))
     return rc;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
-  return launch_move_inline<true, true>(src, dst, nullptr, nullptr, ids, n_blocks, n_blocks,
-                                        src->tile_bytes, src->n_arrays,
-                                        std::min(src->align, dst->align), stream);
+  return launch_host_ids<true, true>(src, dst, nullptr, nullptr, s.data(), d.data(), n_blocks,
+                                     src->tile_bytes, src->n_arrays,
+                                     std::min(src->align, dst->align), stream);
 }
 
 int iekv_pack_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, void* staging,
                   int64_t staging_bytes, hipStream_t stream) {
   int rc;
-  if ((rc = check_pool(src, "source")) || (rc = check_inline_count(n_blocks, src_ids, src_ids)))
+  if ((rc = check_pool(src, "source")) || (rc = check_host_count(n_blocks, src_ids, src_ids)))
     return rc;
   const int64_t need = image_bytes(src, n_blocks);
   if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
   if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
-  InlineIds ids{};
-  if ((rc = fill_inline(src_ids, n_blocks, src->num_blocks, "source", &ids, 0))) return rc;
+  if ((rc = check_host_range(src_ids, n_blocks, src->num_blocks, "source"))) return rc;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
   const int align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
-  return launch_move_inline<true, false>(src, nullptr, nullptr, static_cast<char*>(staging), ids,
-                                         0, n_blocks, src->tile_bytes, src->n_arrays, align,
-                                         stream);
+  return launch_host_ids<true, false>(src, nullptr, nullptr, static_cast<char*>(staging), src_ids,
+                                      nullptr, n_blocks, src->tile_bytes, src->n_arrays, align,
+                                      stream);
 }
 
 int iekv_unpack_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                     const void* staging, int64_t staging_bytes, hipStream_t stream) {
   int rc;
   if ((rc = check_pool(dst, "destination")) ||
-      (rc = check_inline_count(n_blocks, dst_ids, dst_ids)))
+      (rc = check_host_count(n_blocks, dst_ids, dst_ids)))
     return rc;
   const int64_t need = image_bytes(dst, n_blocks);
   if (need < 0) return set_error(IEKV_ERR_INVALID, "staging size overflows");
   if ((rc = check_buffer(staging, staging_bytes, need, "staging"))) return rc;
-  InlineIds ids{};
-  if ((rc = fill_inline(dst_ids, n_blocks, dst->num_blocks, "destination", &ids, 0)) ||
-      (rc = check_distinct(ids.v, n_blocks, "destination")))
+  if ((rc = check_host_range(dst_ids, n_blocks, dst->num_blocks, "destination")) ||
+      (rc = check_distinct(dst_ids, n_blocks, "destination")))
     return rc;
   DeviceGuard guard(dst->device);
   if (!guard.ok()) return guard.fail();
   const int align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
-  return launch_move_inline<false, true>(nullptr, dst, static_cast<const char*>(staging), nullptr,
-                                         ids, 0, n_blocks, dst->tile_bytes, dst->n_arrays, align,
-                                         stream);
+  return launch_host_ids<false, true>(nullptr, dst, static_cast<const char*>(staging), nullptr,
+                                      nullptr, dst_ids, n_blocks, dst->tile_bytes, dst->n_arrays,
+                                      align, stream);
 }
 
 int iekv_write_slots_layers(const iekv_pool* pool, int32_t first_layer, int32_t n_layers,

@@ -41,6 +41,12 @@ from .pools import KVPool, StreamScope, current_stream_handle, stage_ids, stream
 
 # Device staging the host pipelines use: two slots of at most this many bytes.
 HOST_STAGING_BYTES = 256 << 20
+# Longest host id list handed to the library's host-id entry points, which issue
+# INLINE_IDS ids per launch: two launches cover every per-request table of the
+# benchmark workloads (at most 508 blocks). A longer list is uploaded once and
+# moved in one launch, where hundreds of 256-id launches would each add a launch's
+# fixed cost.
+HOST_IDS_MAX = 2 * _native.INLINE_IDS
 
 
 class PackedBlocks:
@@ -233,16 +239,17 @@ def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
 
 
 def _host_id_array(ids) -> array | None:
-    """A Python list or tuple of at most ``INLINE_IDS`` ids as ``array('i')``, for the
-    library's host-id entry points, which check the ids themselves (IEKV_ERR_RANGE,
-    IEKV_ERR_IDS); None for anything else (NumPy arrays, tensors, long lists, values
-    that are not 32-bit integers), which the pool checks in NumPy.
+    """A Python list or tuple of at most ``HOST_IDS_MAX`` ids as ``array('i')``, for
+    the library's host-id entry points, which check the ids themselves
+    (IEKV_ERR_RANGE, IEKV_ERR_IDS); None for anything else (NumPy arrays, tensors,
+    longer lists, values that are not 32-bit integers), which the pool checks in
+    NumPy.
 
-    A serving loop's block tables are short lists; converting one costs the host
-    about a microsecond for a few hundred ids, where the NumPy checks cost
-    10-30 us, more than the launch they precede.
+    A serving loop's block tables are lists; converting one costs the host about a
+    microsecond for a few hundred ids, where the NumPy checks cost 10-30 us, more
+    than the launch they precede.
     """
-    if type(ids) not in (list, tuple) or len(ids) > _native.INLINE_IDS:
+    if type(ids) not in (list, tuple) or len(ids) > HOST_IDS_MAX:
         return None
     try:
         return array("i", ids)
@@ -254,10 +261,11 @@ class _BlockIds:
     """The block ids of one call: host int32 ids, or a device tensor.
 
     Host ids are a NumPy int32 array the pool has checked, or an ``array('i')`` of a
-    short Python list that only the library's host-id entry points check. Host ids
-    of at most ``INLINE_IDS`` blocks go to those entry points (the ids ride in the
-    launch's kernel arguments); a call that needs them on the device checks them
-    here first (range, and distinctness for destinations) and uploads them once.
+    Python list that only the library's host-id entry points check. Up to
+    ``HOST_IDS_MAX`` host ids go to those entry points (the ids ride in the
+    launches' kernel arguments, INLINE_IDS per launch); a call that needs them on
+    the device (a longer list, the host-memory pipelines) checks them here first
+    (range, and distinctness for destinations) and uploads them once.
     """
 
     __slots__ = ("_pool", "host", "_on_device", "_unique", "_what", "_checked")
@@ -291,7 +299,8 @@ class _BlockIds:
 
     @property
     def inline(self) -> bool:
-        return self.host is not None and len(self.host) <= _native.INLINE_IDS
+        """Host ids the host-id entry points take (in their launches' arguments)."""
+        return self.host is not None and len(self.host) <= HOST_IDS_MAX
 
     def host_pointer(self) -> int:
         host = self.host
@@ -597,10 +606,11 @@ class HipSlotCopier:
             source.blocks_read += n
             self.blocks_written += n
             return
-        # Host ids, issued by destination id. Up to INLINE_IDS pairs travel in the
-        # launch's kernel arguments, and the library checks and orders them (a
-        # serving loop's short Python tables go there unconverted by NumPy);
-        # longer lists are checked here and uploaded together with one copy.
+        # Host ids, issued by destination id. Up to HOST_IDS_MAX pairs go to the
+        # library, which checks and orders them, and travel in the launches' kernel
+        # arguments (INLINE_IDS per launch); a serving loop's Python tables go there
+        # unconverted by NumPy. Other host tables (arrays, CPU tensors) are checked
+        # here first, and longer ones are uploaded together with one copy.
         s, d = _host_id_array(src_ids), _host_id_array(dst_ids)
         if s is not None and d is not None:
             if len(s) != len(d):
@@ -619,7 +629,7 @@ class HipSlotCopier:
             raise ValueError("a direct copy within one pool needs disjoint source "
                              "and destination blocks")
         n = int(d.size)
-        if n <= _native.INLINE_IDS:
+        if n <= HOST_IDS_MAX:
             s32 = np.ascontiguousarray(s, dtype=np.int32)
             d32 = np.ascontiguousarray(d, dtype=np.int32)
             _native.call("iekv_copy_direct_ids", source.pool.native.handle,

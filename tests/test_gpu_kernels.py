@@ -280,19 +280,21 @@ def test_tiles_smaller_than_a_chunk_are_grouped_bit_exact(gpu, bs, heads, dim, d
     assert all(np.array_equal(a, b) for a, b in zip(source, host_bytes(sk) + host_bytes(sv)))
 
 
-@pytest.mark.parametrize("count", [1, 255, 256, 257, 600])
+@pytest.mark.parametrize("count", [1, 255, 256, 257, 600, 1300])
 def test_host_ids_in_the_kernel_arguments_and_beyond(gpu, count):
-    """Host id lists of up to 256 blocks ride in the launch's kernel arguments
-    (iekv_*_ids); longer ones are uploaded. Both give the oracle's bytes."""
+    """Host id lists ride in the launches' kernel arguments (iekv_*_ids), 256 per
+    launch: lists of 1 to 256 blocks in one launch, 257 and 300 in two; a longer
+    one (650 of a 1300-block request) is uploaded and moved in one launch. All
+    give the oracle's bytes."""
     from iekv.engine.copier import HipSlotCopier
 
     bs, layers, heads, dim = 4, 2, 2, 32
-    sk, sv = allocate(700, bs, layers, heads, dim, torch.bfloat16, gpu, seed=41)
-    dk, dv = allocate(650, bs, layers, heads, dim, torch.bfloat16, gpu, seed=42)
+    sk, sv = allocate(1400, bs, layers, heads, dim, torch.bfloat16, gpu, seed=41)
+    dk, dv = allocate(1350, bs, layers, heads, dim, torch.bfloat16, gpu, seed=42)
     src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
     src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
     rng = np.random.default_rng(43)
-    src_ids, dst_ids = random_tables(rng, 700, 650, count)
+    src_ids, dst_ids = random_tables(rng, 1400, 1350, count)
     half = count // 2
     packed = src.read_blocks(src_ids[:half])
     dst.write_blocks(dst_ids[:half], packed)
@@ -723,9 +725,9 @@ def test_short_python_tables_and_numpy_tables_move_the_same_bytes(gpu):
     """Short Python tables go to the library unconverted (it checks and orders the
     ids), NumPy arrays and long lists through the NumPy checks; both must move the
     same tiles and refuse the same ids.
-    Table lengths sit on either side of INLINE_IDS (the most ids a launch's
-    arguments carry, and the longest list the library checks), and one direct
-    copy stays within one pool."""
+    Table lengths sit on either side of INLINE_IDS (the most ids one launch's
+    arguments carry; longer tables take several launches), and one direct copy
+    stays within one pool."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -733,7 +735,7 @@ def test_short_python_tables_and_numpy_tables_move_the_same_bytes(gpu):
     n_blocks = 700
     sk, sv = allocate(n_blocks, bs, 2, 2, 32, torch.float16, gpu, seed=91)
     src = HipSlotCopier(sk, sv, bs)
-    sizes = [1, 2, 7, 100, _native.INLINE_IDS, _native.INLINE_IDS + 1]
+    sizes = [1, 2, 7, 100, _native.INLINE_IDS, _native.INLINE_IDS + 1, 600]
     results = []
     for as_numpy in (False, True):
         dk, dv = allocate(n_blocks, bs, 2, 2, 32, torch.float16, gpu, seed=93)

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 from iekv import _native
-from iekv.engine.copier import _host_id_array, issue_order
+from iekv.engine.copier import HOST_IDS_MAX, _host_id_array, issue_order
 from iekv.engine.pools import KVPool
 
 NO_DEVICE = 99
@@ -60,8 +60,8 @@ def test_short_lists_become_int32_arrays_and_the_rest_stays_with_numpy():
     assert list(_host_id_array([3, 1, 2])) == [3, 1, 2]
     assert list(_host_id_array((np.int64(7), True, -1))) == [7, 1, -1]   # the library checks
     assert len(_host_id_array([])) == 0
-    assert _host_id_array(list(range(_native.INLINE_IDS))) is not None
-    assert _host_id_array(list(range(_native.INLINE_IDS + 1))) is None   # uploaded instead
+    assert len(_host_id_array(list(range(HOST_IDS_MAX)))) == HOST_IDS_MAX
+    assert _host_id_array(list(range(HOST_IDS_MAX + 1))) is None     # uploaded instead
     assert _host_id_array(np.arange(3)) is None
     assert _host_id_array([1.0, 2.0]) is None                            # not integers
     assert _host_id_array([1 << 40]) is None                             # not 32-bit
@@ -72,7 +72,7 @@ def test_direct_copy_ids_are_refused_alike_by_the_library_and_numpy(seed):
     rng = np.random.default_rng(seed)
     for case in range(300):
         num_blocks = int(rng.integers(2, 40))
-        n = int(rng.integers(0, 10)) if case % 5 else int(rng.integers(200, _native.INLINE_IDS + 1))
+        n = int(rng.integers(0, 10)) if case % 5 else int(rng.integers(200, 700))
         src = [int(x) for x in rng.integers(-1, num_blocks + 1, size=n)]
         if rng.integers(2):     # distinct, sometimes one past either end of the pool
             dst = [int(x) for x in rng.permutation(max(n, num_blocks + 1))[:n]

@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 12
+    assert lib.iekv_abi_version() == 13
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -78,16 +78,20 @@ def test_calls_reject_null_pools_and_negative_counts(lib):
 
 
 def test_host_id_calls_check_count_and_range_before_any_launch(lib):
-    """The *_ids entry points take at most IEKV_INLINE_IDS host ids and check each
-    against its pool; a slab pool registers without touching the GPU."""
+    """The *_ids entry points take any number of host ids (IEKV_INLINE_IDS per
+    launch) and check each against its pool before anything is enqueued; a slab
+    pool registers without touching the GPU."""
     from iekv import _native
 
     pool = _native.Pool([1 << 20, (1 << 20) + 64 * 16], tile_bytes=64, num_blocks=16, device=0)
     n = _native.INLINE_IDS + 1
     ids = (ctypes.c_int32 * n)(*range(n))
-    assert lib.iekv_copy_direct_ids(pool.handle, pool.handle, ids, ids, n, None) == \
+    assert lib.iekv_copy_direct_ids(pool.handle, pool.handle, ids, ids, -1, None) == \
         _native.IEKV_ERR_INVALID
-    assert "outside 0..256" in lib.iekv_last_error().decode()
+    assert "n_blocks is negative" in lib.iekv_last_error().decode()
+    assert lib.iekv_copy_direct_ids(pool.handle, pool.handle, ids, ids, n, None) == \
+        _native.IEKV_ERR_RANGE                        # a long list: every id checked
+    assert "source block id 16 (entry 16)" in lib.iekv_last_error().decode()
     assert lib.iekv_pack_ids(pool.handle, None, 3, None, 0, None) == _native.IEKV_ERR_INVALID
     assert "null" in lib.iekv_last_error().decode()
     bad = (ctypes.c_int32 * 3)(0, 16, 2)
