@@ -24,9 +24,12 @@ def engine(**kw):
 
 def test_batched_generation_matches_one_at_a_time():
     prompts = [[1, 2, 3], [9, 8, 7, 6], [4, 4, 4, 4, 4, 4]]
-    together = engine().generate(prompts, max_new_tokens=5, temperature=0.0)
+    batch = engine()
+    together = batch.generate(prompts, max_new_tokens=5, temperature=0.0)
     apart = [engine().generate([p], max_new_tokens=5, temperature=0.0)[0] for p in prompts]
     assert together == apart
+    # every finished request gave its blocks back (tests/test_engine.py:170-173)
+    assert batch.blocks.num_free == batch.blocks.num_total
 
 
 def test_chunked_prefill_does_not_change_the_output():
@@ -50,8 +53,11 @@ PROMPTS = [list(range(i, i + 12)) for i in range(4)]
 
 
 def test_preemption_does_not_change_the_output():
-    expected = engine(num_blocks=256, max_batch_tokens=256).generate(PROMPTS, max_new_tokens=10,
-                                                                     temperature=0.0)
+    roomy = engine(num_blocks=256, max_batch_tokens=256)
+    expected = roomy.generate(PROMPTS, max_new_tokens=10, temperature=0.0)
+    # with room for every sequence, blocks are taken only as tokens need them and
+    # nothing is preempted (tests/test_engine.py:162-168)
+    assert roomy.scheduler.stats.preemptions == 0
     tight = engine(num_blocks=8, max_batch_tokens=256)
     assert tight.generate(PROMPTS, max_new_tokens=10, temperature=0.0) == expected
     assert tight.scheduler.stats.preemptions > 0
