@@ -427,24 +427,46 @@ __device__ __forceinline__ void row_place(const RowShape& sh, int* array, int64_
 }
 
 // Row `row` (< n) of this workgroup's share: addr(row, &src, &dst) gives its
-// addresses, or false to skip it (an id outside the pool).
-template <typename V, bool NTL, bool NTS, typename RowAddr>
-__device__ __forceinline__ void move_row(int64_t first, int32_t n, const RowShape& sh,
-                                         RowAddr addr) {
-  const int lane = threadIdx.x & (sh.lanes - 1);
-  const int64_t row = first + threadIdx.x / sh.lanes;
+// addresses, or false to skip it (an id outside the pool). With WAVE_ROW (a
+// row spans the whole wave) the row index is made wave-uniform, so the id the
+// row's addresses depend on (a slot, a table entry) is read with one scalar load
+// instead of a vector load by all 64 lanes.
+template <bool WAVE_ROW, typename V, bool NTL, bool NTS, typename RowAddr>
+__device__ __forceinline__ void move_row_as(int64_t first, int32_t n, const RowShape& sh,
+                                            RowAddr addr) {
+  const int lanes = WAVE_ROW ? kWave : sh.lanes;
+  const int lane = threadIdx.x & (lanes - 1);
+  const int64_t row =
+      first + (WAVE_ROW ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave)
+                        : static_cast<int>(threadIdx.x) / lanes);
   gptr<const V> s;
   gptr<V> d;
   if (row >= n || !addr(row, &s, &d)) return;
-  for (int e = lane; e < sh.row_vecs; e += kRowU * sh.lanes) {
+  for (int e = lane; e < sh.row_vecs; e += kRowU * lanes) {
     V v[kRowU];
 #pragma unroll
     for (int u = 0; u < kRowU; ++u)
-      if (e + u * sh.lanes < sh.row_vecs) v[u] = load_vec<V, NTL>(s + e + u * sh.lanes);
+      if (e + u * lanes < sh.row_vecs) v[u] = load_vec<V, NTL>(s + e + u * lanes);
 #pragma unroll
     for (int u = 0; u < kRowU; ++u)
-      if (e + u * sh.lanes < sh.row_vecs) store_vec<V, NTS>(d + e + u * sh.lanes, v[u]);
+      if (e + u * lanes < sh.row_vecs) store_vec<V, NTS>(d + e + u * lanes, v[u]);
   }
+}
+
+// The gather reads its table entry with a scalar load when a row spans the
+// wave; the scatter keeps the vector load of its slot. Measured in alternating
+// processes on MI355X (two rounds each): the scalar load took the gather from
+// 6,388 / 6,385 to 6,664 / 6,713 GB/s on the 70B-shape share's 1 KiB rows and
+// from 6,096 / 6,100 to 6,148 / 6,151 on the 8B shape's 2 KiB rows; the scatter
+// read 5,322 / 5,342 with it against 5,592 / 6,156 without on the 1 KiB rows,
+// and tied on the 2 KiB rows.
+template <bool UNIFORM_IDS, typename V, bool NTL, bool NTS, typename RowAddr>
+__device__ __forceinline__ void move_row(int64_t first, int32_t n, const RowShape& sh,
+                                         RowAddr addr) {
+  if (UNIFORM_IDS && sh.lanes == kWave)
+    move_row_as<true, V, NTL, NTS>(first, n, sh, addr);
+  else
+    move_row_as<false, V, NTL, NTS>(first, n, sh, addr);
 }
 
 // write_kv over layers: row i of layer l of k (and of v), at
@@ -464,7 +486,7 @@ kv_scatter_rows(PoolView pool, int32_t layers, int32_t first_layer, int32_t n_la
   const int64_t row_bytes = static_cast<int64_t>(sh.row_vecs) * sizeof(V);
   const char* src = (is_v ? v : k) + l * layer_stride;
   char* dst = array_base(pool, (is_v ? layers : 0) + first_layer + l);
-  move_row<V, NTL, NTS>(first, n, sh, [&](int64_t i, gptr<const V>* s, gptr<V>* d) {
+  move_row<false, V, NTL, NTS>(first, n, sh, [&](int64_t i, gptr<const V>* s, gptr<V>* d) {
     const int64_t slot = slots[i];
     if (slot < 0 || slot >= pool_rows) return false;  // never address outside the pool
     *s = as_global<V>(src + i * row_bytes);
@@ -487,7 +509,7 @@ kv_gather_rows(PoolView pool, int32_t first_array, const int32_t* __restrict__ t
   const int64_t row_bytes = static_cast<int64_t>(sh.row_vecs) * sizeof(V);
   const char* base = array_base(pool, first_array + y);
   char* dst = out + y * out_stride;
-  move_row<V, NTL, NTS>(first, n, sh, [&](int64_t j, gptr<const V>* s, gptr<V>* d) {
+  move_row<true, V, NTL, NTS>(first, n, sh, [&](int64_t j, gptr<const V>* s, gptr<V>* d) {
     const int32_t block = table[j / bs];
     if (block < 0 || block >= pool.num_blocks) return false;
     *s = as_global<V>(base + (static_cast<int64_t>(block) * bs + j % bs) * row_bytes);
