@@ -460,6 +460,10 @@ __device__ __forceinline__ void move_row_as(int64_t first, int32_t n, const RowS
 // from 6,096 / 6,100 to 6,148 / 6,151 on the 8B shape's 2 KiB rows; the scatter
 // read 5,322 / 5,342 with it against 5,592 / 6,156 without on the 1 KiB rows,
 // and tied on the 2 KiB rows.
+#ifndef IEKV_GATHER_UNIFORM_IDS
+#define IEKV_GATHER_UNIFORM_IDS 1
+#endif
+
 template <bool UNIFORM_IDS, typename V, bool NTL, bool NTS, typename RowAddr>
 __device__ __forceinline__ void move_row(int64_t first, int32_t n, const RowShape& sh,
                                          RowAddr addr) {
@@ -565,7 +569,8 @@ kv_gather_rows(PoolView pool, int32_t first_array, const int32_t* __restrict__ t
   const int64_t row_bytes = static_cast<int64_t>(sh.row_vecs) * sizeof(V);
   const char* base = array_base(pool, first_array + y);
   char* dst = out + y * out_stride;
-  move_row<true, V, NTL, NTS>(first, n, sh, [&](int64_t j, gptr<const V>* s, gptr<V>* d) {
+  move_row<IEKV_GATHER_UNIFORM_IDS != 0, V, NTL, NTS>(
+      first, n, sh, [&](int64_t j, gptr<const V>* s, gptr<V>* d) {
     const int32_t block = table[j / bs];
     if (block < 0 || block >= pool.num_blocks) return false;
     *s = as_global<V>(base + (static_cast<int64_t>(block) * bs + j % bs) * row_bytes);
