@@ -206,6 +206,10 @@ __device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
 // Workgroups take (array unit, run of list entries, chunk) triples in the
 // order iekv_plan::place_at describes (kv_plan.h).
 
+#ifndef IEKV_UNPACK_LOAD_FIRST
+#define IEKV_UNPACK_LOAD_FIRST 1
+#endif
+
 // Move chunk p of list entry `entry` of array a: from pool tile src_id (or the
 // staging image of the entry) to pool tile dst_id (or the staging image).
 // Ids outside their pool move nothing, so a bad id never addresses memory
@@ -219,6 +223,26 @@ __device__ __forceinline__ void move_entry(const PoolView& src, const PoolView& 
   const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
   const int chunk_vecs = tile_vecs / parts;
   const int64_t chunk_offset = static_cast<int64_t>(p) * chunk_vecs * sizeof(V);
+  if constexpr (IEKV_UNPACK_LOAD_FIRST && !SRC_POOL && DST_POOL) {
+    // Staging to pool: the chunk's address in the staging image does not depend
+    // on the destination id, so its first vectors are loaded before the id is
+    // checked and the two latencies overlap.
+    const gptr<const V> gs =
+        as_global<V>(src_stage + (entry * n_arrays + a) * tile_bytes + chunk_offset);
+    const int t = threadIdx.x;
+    V r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (t + u * kThreads < chunk_vecs) r[u] = load_vec<V, NT>(gs + t + u * kThreads);
+    if (dst_id < 0 || dst_id >= dst.num_blocks) return;
+    const gptr<V> gd = as_global<V>(array_base(dst, a) + dst_id * tile_bytes + chunk_offset);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (t + u * kThreads < chunk_vecs) store_vec<V, NT>(gd + t + u * kThreads, r[u]);
+    if (chunk_vecs > U * kThreads)
+      move_tile<V, U, NT>(gs + U * kThreads, gd + U * kThreads, chunk_vecs - U * kThreads);
+    return;
+  }
   const char* s;
   char* d;
   if constexpr (SRC_POOL) {
