@@ -87,7 +87,7 @@ def log(msg: str) -> None:
 
 
 DEFAULT_LAUNCH = {"run_blocks": 0, "unroll": 8, "nontemporal": 1, "order": 5, "pack_order": 0,
-                  "chunk_bytes": 4096}
+                  "chunk_bytes": 4096, "direct_chunk_bytes": 8192}
 
 
 def measured_traffic(config: str, tp: int, leg: str, launch: dict, separate: bool,
@@ -950,8 +950,9 @@ def main() -> int:
                     help="minimum CPU-baseline time (the sample handoff repeats until then)")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--launch", default="",
-                    help="run_blocks,unroll,nontemporal,order[,pack_order[,chunk_bytes]] for "
-                         "iekv_set_launch (default: the library's)")
+                    help="run_blocks,unroll,nontemporal,order[,pack_order[,chunk_bytes"
+                         "[,direct_chunk_bytes]]] for iekv_set_launch and "
+                         "iekv_set_direct_chunk (default: the library's)")
     ap.add_argument("--sweep", action="store_true",
                     help="time the legs under every launch shape instead of the benchmark line")
     ap.add_argument("--tp", type=int, default=1,

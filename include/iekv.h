@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 13
+#define IEKV_ABI_VERSION 14
 
 enum {
   IEKV_OK = 0,
@@ -303,9 +303,12 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
  *               power of two from 64 to 1 MiB; -1 keeps the current setting.
  *               A launch that would exceed the dispatch limit of 2^32 - 1
  *               work-items halves the split, then spreads over several
- *               launches.
+ *               launches. This sets the chunk size of every move, pool-to-
+ *               pool moves included (iekv_set_direct_chunk sets theirs
+ *               alone).
  * The defaults (run 0, unroll 8, nontemporal 1, order, pack_order and
- * chunk_bytes) are the library's measured best; iekv_get_launch reports them.
+ * chunk_bytes 4096; 8192 for pool-to-pool moves) are the library's measured
+ * best; iekv_get_launch and iekv_get_direct_chunk report them.
  * No reference counterpart: a tuning knob for the launches the entry points
  * above make. */
 int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int32_t order,
@@ -326,6 +329,15 @@ int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count);
 /* Current launch shape, for reporting. */
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
                     int32_t* order, int32_t* pack_order, int32_t* chunk_bytes);
+
+/* chunk_bytes of iekv_set_launch for the pool-to-pool moves alone
+ * (iekv_copy_direct, iekv_copy_direct_ids and iekv_copy_direct_requests):
+ * the same values and meaning; -1 keeps the current
+ * setting. iekv_get_direct_chunk reports it (chunk_bytes of iekv_get_launch is
+ * the setting of the other moves).
+ * No reference counterpart: a tuning knob, like iekv_set_launch. */
+int iekv_set_direct_chunk(int32_t chunk_bytes);
+int iekv_get_direct_chunk(int32_t* chunk_bytes);
 
 #ifdef __cplusplus
 }

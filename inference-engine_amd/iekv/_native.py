@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most host ids one launch carries in its arguments
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
@@ -58,6 +58,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "iekv_restore_blocks": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64,
                                     c_void_p, c_void_p]),
     "iekv_set_launch": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "iekv_set_direct_chunk": (c_int, [c_int32]),
+    "iekv_get_direct_chunk": (c_int, [POINTER(c_int32)]),
     "iekv_get_launch": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32),
                                 POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
     "iekv_profile_start": (c_int, [c_int32]),
@@ -174,17 +176,26 @@ class Pool:
 
 
 def set_launch(run_blocks: int = -1, unroll: int = 0, nontemporal: int = -1,
-               order: int = -1, pack_order: int = -1, chunk_bytes: int = -1) -> None:
-    """Launch shape of the move kernels; see iekv_set_launch in include/iekv.h."""
+               order: int = -1, pack_order: int = -1, chunk_bytes: int = -1,
+               direct_chunk_bytes: int = -1) -> None:
+    """Launch shape of the move kernels; see iekv_set_launch in include/iekv.h.
+
+    ``chunk_bytes`` sets the chunk size of every move; ``direct_chunk_bytes``
+    (iekv_set_direct_chunk) then sets the pool-to-pool moves' own, when not -1.
+    """
     call("iekv_set_launch", run_blocks, unroll, nontemporal, order, pack_order, chunk_bytes)
+    call("iekv_set_direct_chunk", direct_chunk_bytes)
 
 
 def get_launch() -> dict[str, int]:
     run, unroll, nt, order, pack_order, chunk = (c_int32() for _ in range(6))
     call("iekv_get_launch", ctypes.byref(run), ctypes.byref(unroll), ctypes.byref(nt),
          ctypes.byref(order), ctypes.byref(pack_order), ctypes.byref(chunk))
+    direct = c_int32()
+    call("iekv_get_direct_chunk", ctypes.byref(direct))
     return {"run_blocks": run.value, "unroll": unroll.value, "nontemporal": nt.value,
-            "order": order.value, "pack_order": pack_order.value, "chunk_bytes": chunk.value}
+            "order": order.value, "pack_order": pack_order.value, "chunk_bytes": chunk.value,
+            "direct_chunk_bytes": direct.value}
 
 
 class LaunchTimer:

@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 13
+    assert lib.iekv_abi_version() == 14
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -210,7 +210,7 @@ def test_default_launch_shape():
                          capture_output=True, text=True, check=True, timeout=120)
     assert json.loads(out.stdout.strip().splitlines()[-1]) == {
         "run_blocks": 0, "unroll": 8, "nontemporal": 1, "order": 5, "pack_order": 0,
-        "chunk_bytes": 4096}
+        "chunk_bytes": 4096, "direct_chunk_bytes": 8192}
 
 
 def test_launch_settings_are_validated(lib):
@@ -231,12 +231,22 @@ def test_launch_settings_are_validated(lib):
     for bad in (-2, 32, 100, 3000, 1 << 21):
         with pytest.raises(_native.NativeError):
             _native.set_launch(chunk_bytes=bad)
+        with pytest.raises(_native.NativeError):
+            _native.set_launch(direct_chunk_bytes=bad)
     _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=6, pack_order=1,
                        chunk_bytes=1024)
+    # chunk_bytes sets the pool-to-pool moves' chunk too.
     assert _native.get_launch() == {"run_blocks": 8, "unroll": 16, "nontemporal": 0, "order": 6,
-                                    "pack_order": 1, "chunk_bytes": 1024}
+                                    "pack_order": 1, "chunk_bytes": 1024,
+                                    "direct_chunk_bytes": 1024}
     _native.set_launch(unroll=1, chunk_bytes=0)
     assert _native.get_launch()["unroll"] == 1 and _native.get_launch()["chunk_bytes"] == 0
+    assert _native.get_launch()["direct_chunk_bytes"] == 0
+    _native.set_launch(direct_chunk_bytes=16384)
+    assert _native.get_launch()["chunk_bytes"] == 0
+    assert _native.get_launch()["direct_chunk_bytes"] == 16384
+    with pytest.raises(_native.NativeError):
+        _native.call("iekv_get_direct_chunk", None)
     _native.set_launch(**before)
     assert _native.get_launch() == before
 
