@@ -863,6 +863,10 @@ def ab_ok(spec: str, config: str) -> bool:
         return all(v.isdigit() and 1 <= int(v) <= 8 for v in values)
     if key == "slack":
         return config in ("cfg3", "cfg4") and all(v == "engine" or v.isdigit() for v in values)
+    if key == "direct_chunk":
+        return all(v.isdigit() and (int(v) == 0 or (64 <= int(v) <= 1 << 20
+                                                     and int(v) & (int(v) - 1) == 0))
+                   for v in values)
     return False
 
 
@@ -872,12 +876,15 @@ def ab(args, names: list[str], device) -> int:
     ``streams=1,2,4``: one set of pools, request streams switched between
     values. ``slack=64,6600,engine``: pools re-made for each value (cfg3 or
     cfg4 sized to the workload plus that many spare blocks, ``engine`` for the
-    default pools), so every round also draws a new physical placement. Prints
-    one JSON line with every measurement and the per-value means.
+    default pools), so every round also draws a new physical placement.
+    ``direct_chunk=4096,8192,0``: pools re-made for each round, and every value
+    of iekv_set_direct_chunk measured on the same pools within the round, so
+    each placement compares all values. Prints one JSON line with every
+    measurement and the per-value means.
     """
     import torch
 
-    from iekv import workloads
+    from iekv import _native, workloads
 
     key, _, raw = args.ab.partition("=")
     values = [v for v in raw.split(",") if v]
@@ -907,6 +914,22 @@ def ab(args, names: list[str], device) -> int:
                 measure(legs, rnd, n)
         legs.streams, legs.stagings = streams, stagings
         ok = legs.verify()
+    elif key == "direct_chunk":
+        before = _native.get_launch()
+        try:
+            for rnd in range(args.rounds):
+                w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
+                legs = Legs(w, device, args.seed,
+                            "separate" if args.separate_pools else "paired",
+                            streams=args.streams)
+                for v in values:
+                    _native.set_launch(direct_chunk_bytes=int(v))
+                    measure(legs, rnd, v)
+                ok = legs.verify() and ok
+                del legs
+                torch.cuda.empty_cache()
+        finally:
+            _native.set_launch(**before)
     else:
         for rnd in range(args.rounds):
             for v in values:
@@ -964,7 +987,9 @@ def main() -> int:
                          "one stream; the per-launch timing pass always uses one)")
     ap.add_argument("--ab", default="",
                     help="in-process A/B instead of the benchmark line: streams=1,2,4 (one set "
-                         "of pools) or slack=64,6600,engine (pools re-made per value; cfg3/cfg4)")
+                         "of pools), slack=64,6600,engine (pools re-made per value; cfg3/cfg4) "
+                         "or direct_chunk=4096,8192,0 (pools re-made per round, every value "
+                         "on each)")
     ap.add_argument("--rounds", type=int, default=3, help="rounds of an --ab comparison")
     ap.add_argument("--separate-pools", action="store_true",
                     help="allocate the two pools separately instead of as one reservation "
@@ -977,8 +1002,8 @@ def main() -> int:
               file=sys.stderr)
         return 2
     if args.ab and not ab_ok(args.ab, args.config):
-        print("--ab takes streams=N,... (N in 1..8) or, for cfg3 and cfg4, slack=N|engine,...",
-              file=sys.stderr)
+        print("--ab takes streams=N,... (N in 1..8), direct_chunk=B,... (0 or a power of two "
+              "from 64 to 1 MiB) or, for cfg3 and cfg4, slack=N|engine,...", file=sys.stderr)
         return 2
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -19,6 +19,8 @@ ROOT = Path(__file__).resolve().parents[1]
     (["--ab", "streams=0,2"], "--ab takes"),
     (["--ab", "unroll=4"], "--ab takes"),
     (["--config", "cfg5", "--ab", "slack=64,engine"], "--ab takes"),
+    (["--ab", "direct_chunk=4096,3000"], "--ab takes"),
+    (["--ab", "direct_chunk=32"], "--ab takes"),
 ])
 def test_the_bench_refuses_before_touching_a_gpu(args, message):
     out = subprocess.run([sys.executable, "bench.py", *args], cwd=ROOT, capture_output=True,
