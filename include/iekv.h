@@ -27,7 +27,8 @@
  *   can never address memory outside the pool. The tiles of one call are
  *   moved concurrently: destination ids must be distinct, and a direct copy
  *   within one pool must not use a block as both source and destination
- *   (the library checks neither; the Python layer checks host id lists).
+ *   (the calls taking device ids check neither; iekv_check_ids checks a
+ *   device list on the GPU, and the host-id calls check their own).
  *   All copies are raw bytes: fp32/fp16/bf16/fp8/int8 caches move bit-exactly.
  *
  * Errors. Every function returns IEKV_OK (0) or a negative IEKV_ERR_* code,
@@ -49,7 +50,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 14
+#define IEKV_ABI_VERSION 15
 
 enum {
   IEKV_OK = 0,
@@ -325,6 +326,37 @@ int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int
  * perf_counter (ie/bench/harness.py:67-120). */
 int iekv_profile_start(int32_t max_launches);
 int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count);
+
+/* Bits iekv_check_ids writes to *status (0 = every check passed). */
+#define IEKV_IDS_SRC_RANGE 1    /* a source id outside [0, num_blocks) of its pool */
+#define IEKV_IDS_DST_RANGE 2    /* a destination id outside its pool */
+#define IEKV_IDS_DST_REPEATED 4 /* a destination id given more than once */
+#define IEKV_IDS_OVERLAP 8      /* src == dst and a block is both a source and a destination */
+
+/* Bytes of workspace iekv_check_ids needs for a destination pool of num_blocks:
+ * one bit per block, in 32-bit words. */
+#define IEKV_CHECK_WORKSPACE_BYTES(num_blocks) ((((int64_t)(num_blocks)) + 31) / 32 * 4)
+
+/* Check a list of block ids held in DEVICE memory on the GPU, as the host-id
+ * calls check theirs on the host, before a call that takes the list (in stream
+ * order, so the check sees the ids that call will read). Either pool may be
+ * null: with src, src_ids[0..n_blocks) are checked against src's size; with
+ * dst, dst_ids are checked against dst's size and for repeats; with src == dst,
+ * also that no block is both a source and a destination (a direct copy within
+ * one pool). `workspace` is device memory of at least
+ * IEKV_CHECK_WORKSPACE_BYTES(dst->num_blocks) bytes (none without dst);
+ * `status` is one device int32, overwritten with the IEKV_IDS_* bits of the
+ * failed checks. Two or three small launches on `stream`, no host
+ * synchronisation: the caller reads *status after the stream has passed them
+ * (and may skip the move, or read it after the move, to report). The launches
+ * are not timed by iekv_profile_start. Calls that share a workspace or status
+ * word must be ordered on one stream.
+ * No reference counterpart: the reference's copier slices its caches one block
+ * at a time (ie/engine/copier.py:14-31) and checks no id; this gives callers
+ * that keep ids on the device the checks the host-id calls make. */
+int iekv_check_ids(const iekv_pool* src, const int32_t* src_ids, const iekv_pool* dst,
+                   const int32_t* dst_ids, int32_t n_blocks, void* workspace,
+                   int64_t workspace_bytes, int32_t* status, hipStream_t stream);
 
 /* Current launch shape, for reporting. */
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,

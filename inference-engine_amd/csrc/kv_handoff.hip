@@ -610,6 +610,48 @@ kv_gather_rows(PoolView pool, int32_t first_array, const int32_t* __restrict__ t
   });
 }
 
+// Block-id checks of iekv_check_ids, three launches in stream order: clear the
+// destination bitmap (one bit per destination block) and the status word; mark
+// every destination id in the bitmap (the atomic's old word tells whether the
+// id came earlier); probe every source id (against the bitmap when both lists
+// index one pool). A bit of *status is set only when a check fails, so a valid
+// list costs one id load and, for a destination, one bitmap atomic per id.
+__global__ void __launch_bounds__(kThreads)
+ids_clear(uint32_t* __restrict__ bitmap, int64_t words, int32_t* __restrict__ status) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; w < words;
+       w += stride)
+    bitmap[w] = 0u;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *status = 0;
+}
+
+__global__ void __launch_bounds__(kThreads)
+ids_mark(const int32_t* __restrict__ ids, int32_t n, int64_t num_blocks,
+         uint32_t* __restrict__ bitmap, int32_t* __restrict__ status) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int32_t id = ids[i];
+  if (id < 0 || id >= num_blocks) {
+    atomicOr(status, IEKV_IDS_DST_RANGE);
+    return;
+  }
+  const uint32_t bit = 1u << (id & 31);
+  if (atomicOr(&bitmap[id >> 5], bit) & bit) atomicOr(status, IEKV_IDS_DST_REPEATED);
+}
+
+__global__ void __launch_bounds__(kThreads)
+ids_probe(const int32_t* __restrict__ ids, int32_t n, int64_t num_blocks,
+          const uint32_t* __restrict__ bitmap, int32_t* __restrict__ status) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int32_t id = ids[i];
+  if (id < 0 || id >= num_blocks) {
+    atomicOr(status, IEKV_IDS_SRC_RANGE);
+    return;
+  }
+  if (bitmap && (bitmap[id >> 5] >> (id & 31)) & 1u) atomicOr(status, IEKV_IDS_OVERLAP);
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -1744,6 +1786,48 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
         IEKV_HIP(err);
         return IEKV_OK;
       });
+}
+
+int iekv_check_ids(const iekv_pool* src, const int32_t* src_ids, const iekv_pool* dst,
+                   const int32_t* dst_ids, int32_t n_blocks, void* workspace,
+                   int64_t workspace_bytes, int32_t* status, hipStream_t stream) {
+  int rc;
+  if (!src && !dst) return set_error(IEKV_ERR_INVALID, "no source or destination pool");
+  if (src && (rc = check_ids(src_ids, n_blocks, "source"))) return rc;
+  if (dst && (rc = check_ids(dst_ids, n_blocks, "destination"))) return rc;
+  if (!status) return set_error(IEKV_ERR_INVALID, "status is null");
+  if (reinterpret_cast<uintptr_t>(status) % alignof(int32_t))
+    return set_error(IEKV_ERR_INVALID, "status is not 4-byte aligned");
+  if (src && dst && src->device != dst->device)
+    return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
+                     dst->device);
+  const int64_t words = dst ? (dst->num_blocks + 31) / 32 : 0;
+  if ((rc = check_buffer(workspace, workspace_bytes, words * 4, "workspace"))) return rc;
+  if (words && reinterpret_cast<uintptr_t>(workspace) % alignof(uint32_t))
+    return set_error(IEKV_ERR_INVALID, "workspace is not 4-byte aligned");
+  DeviceGuard guard((src ? src : dst)->device);
+  if (!guard.ok()) return guard.fail();
+  auto* bitmap = static_cast<uint32_t*>(workspace);
+  const uint32_t clear_grid =
+      static_cast<uint32_t>(std::clamp<int64_t>((words + kThreads - 1) / kThreads, 1, 4096));
+  hipLaunchKernelGGL(ids_clear, dim3(clear_grid), dim3(kThreads), 0, stream, bitmap, words,
+                     status);
+  IEKV_HIP(hipGetLastError());
+  if (n_blocks == 0) return IEKV_OK;
+  const uint32_t grid = static_cast<uint32_t>((static_cast<int64_t>(n_blocks) + kThreads - 1) /
+                                              kThreads);
+  if (dst) {
+    hipLaunchKernelGGL(ids_mark, dim3(grid), dim3(kThreads), 0, stream, dst_ids, n_blocks,
+                       dst->num_blocks, bitmap, status);
+    IEKV_HIP(hipGetLastError());
+  }
+  if (src) {
+    hipLaunchKernelGGL(ids_probe, dim3(grid), dim3(kThreads), 0, stream, src_ids, n_blocks,
+                       src->num_blocks, src == dst ? static_cast<const uint32_t*>(bitmap)
+                                                   : nullptr, status);
+    IEKV_HIP(hipGetLastError());
+  }
+  return IEKV_OK;
 }
 
 int iekv_profile_start(int32_t max_launches) {

@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most host ids one launch carries in its arguments
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
@@ -25,6 +25,16 @@ IEKV_ERR_HIP = -2
 IEKV_ERR_CAPACITY = -3
 IEKV_ERR_RANGE = -4      # a host block id outside its pool
 IEKV_ERR_IDS = -5        # host ids that conflict (a destination twice; overlap within a pool)
+# Bits iekv_check_ids writes to its status word.
+IEKV_IDS_SRC_RANGE = 1
+IEKV_IDS_DST_RANGE = 2
+IEKV_IDS_DST_REPEATED = 4
+IEKV_IDS_OVERLAP = 8
+
+
+def check_workspace_bytes(num_blocks: int) -> int:
+    """Workspace iekv_check_ids needs for a destination pool of num_blocks blocks."""
+    return (num_blocks + 31) // 32 * 4
 
 # Every entry point of include/iekv.h: name -> (restype, argtypes).
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -62,6 +72,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "iekv_get_direct_chunk": (c_int, [POINTER(c_int32)]),
     "iekv_get_launch": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32),
                                 POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
+    "iekv_check_ids": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
+                               c_int64, c_void_p, c_void_p]),
     "iekv_profile_start": (c_int, [c_int32]),
     "iekv_profile_stop": (c_int, [POINTER(ctypes.c_float), c_int32, POINTER(c_int32)]),
 }
@@ -79,7 +91,7 @@ class NativeError(RuntimeError):
 
 
 class NativeIndexError(NativeError, IndexError):
-    """IEKV_ERR_RANGE: a block id outside its pool, the reference's IndexError."""
+    """IEKV_ERR_RANGE: a block id outside its pool (Python's IndexError kind)."""
 
 
 class NativeValueError(NativeError, ValueError):

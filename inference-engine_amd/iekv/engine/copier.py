@@ -37,7 +37,8 @@ import numpy as np
 import torch
 
 from .. import _native
-from .pools import KVPool, StreamScope, current_stream_handle, stage_ids, stream_handle
+from .pools import (KVPool, StreamScope, check_device_ids, current_stream_handle, stage_ids,
+                    stream_handle)
 
 # Device staging the host pipelines use: two slots of at most this many bytes.
 HOST_STAGING_BYTES = 256 << 20
@@ -320,11 +321,17 @@ class HipSlotCopier:
     ``payload_location`` chooses where ``read_block``/``read_blocks`` put
     payloads: ``"device"`` (the disaggregation transfer, a staging buffer in
     HBM) or ``"host"`` (the offload tier, pinned host memory).
+    ``check_device_ids`` checks block ids given as device tensors on the GPU
+    before each move (range; distinct destinations; disjoint source and
+    destination within one pool) and raises as host lists do; the check waits
+    for its answer, so it is for callers that prefer the error to the speed.
+    Without it, device ids are taken as they are (the kernels skip ids outside
+    the pool).
     """
 
     def __init__(self, k_caches: Seq[torch.Tensor], v_caches: Seq[torch.Tensor],
                  block_size: int, *, payload_location: str = "device",
-                 defer_reads: bool | None = None) -> None:
+                 defer_reads: bool | None = None, check_device_ids: bool = False) -> None:
         if payload_location not in ("device", "host"):
             raise ValueError("payload_location must be 'device' or 'host'")
         self.k_caches = k_caches
@@ -332,6 +339,7 @@ class HipSlotCopier:
         self.block_size = block_size
         self.pool = KVPool(k_caches, v_caches, block_size)
         self.payload_location = payload_location
+        self.check_device_ids = check_device_ids
         # Single-block reads of host payloads (the offload hook's evictions) are
         # batched: they queue until flush(), which gathers every still-wanted
         # block with one iekv_offload.
@@ -471,7 +479,13 @@ class HipSlotCopier:
 
     def _ids(self, block_ids, *, unique: bool = False, what: str) -> "_BlockIds":
         if isinstance(block_ids, torch.Tensor) and block_ids.device.type == "cuda":
-            return _BlockIds(self.pool, device_ids=self.pool.block_ids(block_ids, what=what))
+            ids = self.pool.block_ids(block_ids, what=what)
+            if self.check_device_ids:
+                if unique:
+                    check_device_ids(None, None, self.pool, ids)
+                else:
+                    check_device_ids(self.pool, ids, None, None)
+            return _BlockIds(self.pool, device_ids=ids)
         short = _host_id_array(block_ids)
         if short is not None:
             return _BlockIds(self.pool, host=short, unique=unique, what=what)
@@ -601,6 +615,9 @@ class HipSlotCopier:
             if src.numel() != dst.numel():
                 raise ValueError(f"{src.numel()} source blocks for {dst.numel()} destinations")
             n = dst.numel()
+            if self.check_device_ids:
+                with self._on(on):
+                    check_device_ids(source.pool, src, self.pool, dst)
             _native.call("iekv_copy_direct", source.pool.native.handle, self.pool.native.handle,
                          src.data_ptr(), dst.data_ptr(), n, stream)
             source.blocks_read += n

@@ -97,6 +97,7 @@ class KVPool:
         self._arrays = arrays  # keeps the memory alive while the handle exists
         self.native = _native.Pool([t.data_ptr() for t in arrays], self.tile_bytes,
                                    self.num_blocks, self.device.index or 0)
+        self._check_buffers: tuple[torch.Tensor, torch.Tensor] | None = None
 
     @property
     def n_arrays(self) -> int:
@@ -106,6 +107,15 @@ class KVPool:
     def block_bytes(self) -> int:
         """Bytes of one block across all layers, K and V (2L * T)."""
         return self.n_arrays * self.tile_bytes
+
+    def check_buffers(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The device workspace (a bitmap of this pool's blocks) and status word that
+        :func:`check_device_ids` hands iekv_check_ids, made on first use."""
+        if self._check_buffers is None:
+            words = _native.check_workspace_bytes(self.num_blocks) // 4
+            self._check_buffers = (torch.empty(words, dtype=torch.int32, device=self.device),
+                                   torch.empty(1, dtype=torch.int32, device=self.device))
+        return self._check_buffers
 
     def same_shape(self, other: "KVPool") -> bool:
         return (self.n_arrays == other.n_arrays and self.tile_bytes == other.tile_bytes
@@ -148,6 +158,62 @@ class KVPool:
                 if host.size > 1 and bool((ordered[1:] == ordered[:-1]).any()):
                     raise ValueError(f"{what} ids must be distinct")
         return host
+
+
+def _device_list(ids: torch.Tensor, pool: KVPool, what: str) -> torch.Tensor:
+    if not (isinstance(ids, torch.Tensor) and ids.device.type == "cuda"):
+        raise TypeError(f"{what} ids must be a device tensor")
+    if ids.dtype != torch.int32 or ids.dim() != 1 or not ids.is_contiguous():
+        raise TypeError("device block ids must be a contiguous 1-D int32 tensor")
+    if ids.device != pool.device:
+        raise ValueError(f"block ids on {ids.device}, pool on {pool.device}")
+    return ids
+
+
+def check_device_ids(src_pool: KVPool | None, src_ids: torch.Tensor | None,
+                     dst_pool: KVPool | None, dst_ids: torch.Tensor | None) -> None:
+    """Check block ids held on the GPU (iekv_check_ids) and wait for the answer.
+
+    Source ids are checked against ``src_pool``'s size, destination ids against
+    ``dst_pool``'s and for repeats, and when both pools are the same registered
+    pool, that no block is both a source and a destination. The check runs on
+    the current stream, ordered after whatever wrote the ids, and this call
+    synchronises that stream to read the result: IndexError for an id outside
+    its pool, ValueError for a repeated destination or an overlap.
+    """
+    if src_pool is None and dst_pool is None:
+        raise ValueError("no pool to check against")
+    n = None
+    if src_pool is not None:
+        src_ids = _device_list(src_ids, src_pool, "source")
+        n = src_ids.numel()
+    if dst_pool is not None:
+        dst_ids = _device_list(dst_ids, dst_pool, "destination")
+        if n is not None and dst_ids.numel() != n:
+            raise ValueError(f"{n} source blocks for {dst_ids.numel()} destinations")
+        n = dst_ids.numel()
+    owner = dst_pool if dst_pool is not None else src_pool
+    workspace, status = owner.check_buffers()
+    _native.call("iekv_check_ids",
+                 src_pool.native.handle if src_pool is not None else None,
+                 src_ids.data_ptr() if src_pool is not None else None,
+                 dst_pool.native.handle if dst_pool is not None else None,
+                 dst_ids.data_ptr() if dst_pool is not None else None,
+                 n, workspace.data_ptr() if dst_pool is not None else None,
+                 workspace.numel() * 4 if dst_pool is not None else 0, status.data_ptr(),
+                 current_stream_handle(owner.device))
+    bits = int(status.item())
+    if bits & _native.IEKV_IDS_SRC_RANGE:
+        raise IndexError(f"source block id out of range for a pool of "
+                         f"{src_pool.num_blocks} blocks")
+    if bits & _native.IEKV_IDS_DST_RANGE:
+        raise IndexError(f"destination block id out of range for a pool of "
+                         f"{dst_pool.num_blocks} blocks")
+    if bits & _native.IEKV_IDS_DST_REPEATED:
+        raise ValueError("destination block ids must be distinct")
+    if bits & _native.IEKV_IDS_OVERLAP:
+        raise ValueError("a direct copy within one pool needs disjoint source and "
+                         "destination blocks")
 
 
 def stage_ids(device: torch.device, *arrays: np.ndarray) -> list[torch.Tensor]:

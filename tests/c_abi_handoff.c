@@ -1,7 +1,8 @@
 /*
  * c_abi_handoff.c — the KV handoff driven from plain C through include/iekv.h,
- * with no Python or torch: two pools in one HIP allocation, a direct copy with
- * device ids, the same with host ids (kernel-argument ids), and a pack ->
+ * with no Python or torch: two pools in one HIP allocation, the GPU-side check
+ * of device id lists, a direct copy with device ids, the same with host ids
+ * (kernel-argument ids), and a pack ->
  * unpack through a staging buffer. Every moved tile and every untouched tile
  * is checked byte for byte on the host. Then host offload / restore of the
  * moved blocks, through pinned memory (hipHostMalloc: the move kernel reads
@@ -113,6 +114,31 @@ int main(void) {
   CHECK_HIP(hipMalloc(&staging, (size_t)staging_bytes));
   hipStream_t stream;
   CHECK_HIP(hipStreamCreate(&stream));
+
+  /* The device id lists pass the GPU-side checks (status 0); a destination
+   * list that names one block twice sets IEKV_IDS_DST_REPEATED. */
+  int32_t* status = NULL;
+  void* bitmap = NULL;
+  CHECK_HIP(hipMalloc((void**)&status, sizeof(int32_t)));
+  CHECK_HIP(hipMalloc(&bitmap, (size_t)IEKV_CHECK_WORKSPACE_BYTES(BLOCKS)));
+  int32_t verdict = -1;
+  CHECK_IEKV(iekv_check_ids(src, dev_ids, dst, dev_ids + MOVED, MOVED, bitmap,
+                            IEKV_CHECK_WORKSPACE_BYTES(BLOCKS), status, stream));
+  CHECK_HIP(hipMemcpyAsync(&verdict, status, sizeof(verdict), hipMemcpyDeviceToHost, stream));
+  CHECK_HIP(hipStreamSynchronize(stream));
+  if (verdict != 0) return 7;
+  int32_t repeated[2] = {d_ids[0][0], d_ids[0][0]};
+  int32_t* dev_repeated = NULL;
+  CHECK_HIP(hipMalloc((void**)&dev_repeated, sizeof(repeated)));
+  CHECK_HIP(hipMemcpy(dev_repeated, repeated, sizeof(repeated), hipMemcpyHostToDevice));
+  CHECK_IEKV(iekv_check_ids(src, dev_ids, dst, dev_repeated, 2, bitmap,
+                            IEKV_CHECK_WORKSPACE_BYTES(BLOCKS), status, stream));
+  CHECK_HIP(hipMemcpyAsync(&verdict, status, sizeof(verdict), hipMemcpyDeviceToHost, stream));
+  CHECK_HIP(hipStreamSynchronize(stream));
+  if (verdict != IEKV_IDS_DST_REPEATED) return 7;
+  CHECK_HIP(hipFree(dev_repeated));
+  CHECK_HIP(hipFree(bitmap));
+  CHECK_HIP(hipFree(status));
 
   CHECK_IEKV(iekv_copy_direct(src, dst, dev_ids, dev_ids + MOVED, MOVED, stream));
   CHECK_IEKV(iekv_copy_direct_ids(src, dst, s_ids[1], d_ids[1], MOVED, stream));

@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 14
+    assert lib.iekv_abi_version() == 15
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -129,6 +129,48 @@ def test_request_lists_are_checked_before_any_launch(lib):
         assert lib.iekv_copy_direct_requests(*args) == _native.IEKV_ERR_INVALID, message
         assert message in lib.iekv_last_error().decode(), message
     assert lib.iekv_copy_direct_requests(h, h, 0, None, None, None, None, 0, None) == 0
+    pool.close()
+
+
+def test_device_id_checks_validate_their_arguments_before_any_launch(lib):
+    """iekv_check_ids needs a pool, ids for each pool it is given, a status word and,
+    with a destination pool, a bitmap workspace of one bit per block."""
+    from iekv import _native
+
+    pool = _native.Pool([1 << 20, (1 << 20) + 64 * 100], tile_bytes=64, num_blocks=100,
+                        device=99)
+    h = pool.handle
+    ids = ctypes.c_void_p(1 << 24)                  # never read: every case fails first
+    status = ctypes.c_void_p(1 << 24)
+    need = _native.check_workspace_bytes(100)
+    assert need == 16                                # 100 bits in four 32-bit words
+    cases = [
+        ((None, None, None, None, 1, None, 0, status, None), _native.IEKV_ERR_INVALID,
+         "no source or destination pool"),
+        ((h, None, None, None, 1, None, 0, status, None), _native.IEKV_ERR_INVALID,
+         "source ids are null"),
+        ((None, None, h, None, 1, ids, need, status, None), _native.IEKV_ERR_INVALID,
+         "destination ids are null"),
+        ((h, ids, None, None, -1, None, 0, status, None), _native.IEKV_ERR_INVALID,
+         "n_blocks is negative"),
+        ((h, ids, None, None, 1, None, 0, None, None), _native.IEKV_ERR_INVALID,
+         "status is null"),
+        ((h, ids, None, None, 1, None, 0, ctypes.c_void_p((1 << 24) + 2), None),
+         _native.IEKV_ERR_INVALID, "status is not 4-byte aligned"),
+        ((None, None, h, ids, 1, None, need, status, None), _native.IEKV_ERR_INVALID,
+         "workspace buffer is null"),
+        ((None, None, h, ids, 1, ids, need - 4, status, None), _native.IEKV_ERR_CAPACITY,
+         "workspace buffer holds 12 bytes, 16 needed"),
+        ((None, None, h, ids, 1, ctypes.c_void_p((1 << 24) + 1), need, status, None),
+         _native.IEKV_ERR_INVALID, "workspace is not 4-byte aligned"),
+    ]
+    for args, code, message in cases:
+        assert lib.iekv_check_ids(*args) == code, message
+        assert message in lib.iekv_last_error().decode(), message
+    # Valid arguments reach the device switch (device 99 does not exist).
+    assert lib.iekv_check_ids(h, ids, h, ids, 1, ids, need, status, None) == _native.IEKV_ERR_HIP
+    assert lib.iekv_check_ids(h, ids, None, None, 0, None, 0, status, None) == \
+        _native.IEKV_ERR_HIP
     pool.close()
 
 
