@@ -68,6 +68,7 @@ class PackedBlocks:
         self.dtype = dtype
         self._event: torch.cuda.Event | None = None  # last async copy touching host data
         self._parent: PackedBlocks | None = None  # the buffer a slice views (kept alive)
+        self._offset: int | None = 0   # first row in the root buffer (None: a strided view)
 
     @property
     def _root(self) -> "PackedBlocks":
@@ -92,6 +93,9 @@ class PackedBlocks:
         if isinstance(index, slice):
             view = PackedBlocks(self.data[index], self.num_layers, self.tile_shape, self.dtype)
             view._parent = self._root
+            start, _, step = index.indices(len(self))
+            view._offset = self._offset + start if step == 1 and self._offset is not None \
+                else None
             return view
         n = len(self)
         if index < 0:
@@ -226,17 +230,32 @@ class DeferredBlockPayload(BlockPayload):
 
 
 def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
-    """The PackedBlocks slice that ``payloads`` are consecutive entries of, if any."""
+    """The PackedBlocks slice that ``payloads`` are consecutive rows of, if any.
+
+    Payloads from different slices of one buffer count when their rows follow
+    each other there (a staging buffer filled request by request)."""
     if isinstance(payloads, PackedBlocks):
         return payloads
     if not payloads or not all(isinstance(p, BlockPayload) for p in payloads):
         return None
-    base = payloads[0].packed
-    start = payloads[0].index
-    for offset, p in enumerate(payloads):
-        if p.packed is not base or p.index != start + offset:
+    first = payloads[0].packed
+    if first._offset is None:
+        return None
+    root = first._root
+    start = first._offset + payloads[0].index
+    for k, p in enumerate(payloads):
+        packed = p.packed
+        if packed._root is not root or packed._offset is None or \
+                packed._offset + p.index != start + k:
             return None
-    return base[start:start + len(payloads)]
+    return root[start:start + len(payloads)]
+
+
+def join_payloads(parts: Seq[Any]) -> PackedBlocks | None:
+    """One PackedBlocks for several payload lists whose rows follow each other in one
+    buffer (so a single unpack moves them all), else None."""
+    rows = [p for part in parts for p in part]
+    return _consecutive_views(rows) if rows else None
 
 
 def _host_id_array(ids) -> array | None:
@@ -464,18 +483,25 @@ class HipSlotCopier:
         return StreamScope(stream)
 
     def read_blocks(self, block_ids, *, location: str | None = None,
-                    stream: torch.cuda.Stream | None = None) -> PackedBlocks:
+                    stream: torch.cuda.Stream | None = None,
+                    into: PackedBlocks | None = None) -> PackedBlocks:
         """Pack ``block_ids`` (in order) into a new payload buffer with one launch.
 
         ``stream`` runs the call on that stream instead of the current one; the
         caller orders it after the work that wrote the blocks. Independent
         requests issued on different streams let one request's launch start
-        while the previous one drains.
+        while the previous one drains. ``into`` (device payloads of exactly
+        ``len(block_ids)`` blocks, such as a slice of :meth:`empty_payloads`)
+        receives the pack instead of a new buffer, and is returned.
         """
         with self._on(stream):
-            out = self._gather(block_ids, location or self.payload_location)
+            out = self._gather(block_ids, location or self.payload_location, into)
         self.blocks_read += len(out)
         return out
+
+    def empty_payloads(self, n_blocks: int) -> PackedBlocks:
+        """An uninitialised device payload buffer of ``n_blocks`` blocks of this pool."""
+        return self._empty_packed(n_blocks, on_host=False)
 
     def _ids(self, block_ids, *, unique: bool = False, what: str) -> "_BlockIds":
         if isinstance(block_ids, torch.Tensor) and block_ids.device.type == "cuda":
@@ -491,10 +517,19 @@ class HipSlotCopier:
             return _BlockIds(self.pool, host=short, unique=unique, what=what)
         return _BlockIds(self.pool, host=self.pool.host_ids(block_ids, unique=unique, what=what))
 
-    def _gather(self, block_ids, location: str) -> PackedBlocks:
+    def _gather(self, block_ids, location: str, into: PackedBlocks | None = None) -> PackedBlocks:
         ids = self._ids(block_ids, what="source block")
         n = len(ids)
-        out = self._empty_packed(n, on_host=(location == "host"))
+        if into is not None:
+            self._check_packed(into)
+            if into.on_host:
+                raise ValueError("read_blocks(into=...) takes device payloads")
+            if len(into) != n:
+                raise ValueError(f"read_blocks(into=...) got {len(into)} payload rows for "
+                                 f"{n} blocks")
+            out = into
+        else:
+            out = self._empty_packed(n, on_host=(location == "host"))
         if out.on_host:
             stream = torch.cuda.current_stream(self.device)
             staging = self._host_staging(n)

@@ -37,9 +37,14 @@ from dataclasses import dataclass
 from typing import Any, Callable
 
 from ..core.sequence import Sequence, Status
+from ..engine.copier import join_payloads
 from ..engine.engine import CopierFactory, Engine, EngineConfig
 
 MODES = ("pack", "direct")
+
+# Largest device staging buffer a batched pack-mode generate() fills before it
+# unpacks what it holds (then it starts again at the beginning).
+STAGING_ARENA_BYTES = 4 << 30
 
 
 @dataclass(slots=True)
@@ -55,6 +60,46 @@ class DirectSource:
         if not self.released:
             self.released = True
             self.release()
+
+
+@dataclass(slots=True)
+class PendingMove:
+    """A move ``admit`` deferred for :meth:`DisaggregatedEngine.flush_moves`: a direct
+    copy from ``source``, or an unpack of ``payloads``, into ``dst_ids`` of ``copier``."""
+
+    copier: Any
+    dst_ids: list[int]
+    source: DirectSource | None = None
+    payloads: Any = None
+
+
+class _StagingArena:
+    """Consecutive device payload slices for a batched pack-mode ``generate``.
+
+    Each prefill packs into the next slice, so the payloads of every admitted
+    request lie one after another and one unpack moves them all. When the
+    buffer is full the pending unpacks are issued (stream-ordered before the
+    packs that then reuse the buffer) and filling starts again.
+    """
+
+    def __init__(self, engine: "DisaggregatedEngine", capacity: int, pending: list) -> None:
+        self.engine = engine
+        self.capacity = capacity
+        self.pending = pending
+        self.buffer = None
+        self.used = 0
+
+    def take(self, n_blocks: int):
+        if n_blocks == 0 or n_blocks > self.capacity:
+            return None                        # a payload of its own
+        if self.used + n_blocks > self.capacity:
+            self.engine.flush_moves(self.pending)
+            self.used = 0
+        if self.buffer is None:
+            self.buffer = self.engine.prefill.copier.empty_payloads(self.capacity)
+        view = self.buffer[self.used:self.used + n_blocks]
+        self.used += n_blocks
+        return view
 
 
 @dataclass(slots=True)
@@ -120,7 +165,12 @@ class PrefillWorker:
         self.mode = mode
 
     def prefill(self, prompt_ids: list[int], temperature: float = 0.0,
-                skip_blocks: int = 0) -> KVTransfer:
+                skip_blocks: int = 0, payload_buffer: Callable | None = None) -> KVTransfer:
+        """Run a prompt to completion and package its KV (ie/serve/disaggregated.py:45-57).
+
+        In pack mode ``payload_buffer(n)`` may supply the device payloads the
+        ``n`` moved blocks are packed into (None: a new buffer).
+        """
         seq = self.engine.submit(prompt_ids, max_new_tokens=1 << 30, temperature=temperature)
         while not seq.prompt_is_fully_computed:
             self.engine.step()
@@ -133,15 +183,18 @@ class PrefillWorker:
             return KVTransfer(token_ids=list(seq.token_ids), num_computed=seq.num_computed,
                               block_payloads=None, bytes_moved=nbytes,
                               first_block=skip_blocks, source=source)
-        payloads = self._read(moved)
+        payloads = self._read(moved, payload_buffer)
         transfer = KVTransfer(token_ids=list(seq.token_ids), num_computed=seq.num_computed,
                               block_payloads=payloads, bytes_moved=nbytes,
                               first_block=skip_blocks)
         self._retire(seq)
         return transfer
 
-    def _read(self, block_ids: list[int]):
+    def _read(self, block_ids: list[int], payload_buffer: Callable | None = None):
         if hasattr(self.copier, "read_blocks"):
+            into = payload_buffer(len(block_ids)) if payload_buffer is not None else None
+            if into is not None:
+                return self.copier.read_blocks(block_ids, into=into)
             return self.copier.read_blocks(block_ids)          # one fused pack launch
         return [self.copier.read_block(b) for b in block_ids]  # generic SlotCopier
 
@@ -178,11 +231,11 @@ class DecodeWorker:
               temperature: float = 0.0, pending: list | None = None) -> Sequence:
         """Place a transfer's blocks under fresh ids (ie/serve/disaggregated.py:75-96).
 
-        With ``pending`` (a list) a direct-mode transfer's copy is not issued
-        here: ``(source, destination ids, this copier)`` is appended for
-        :meth:`DisaggregatedEngine.flush_moves` to issue together with others.
-        A sequence that finishes on arrival is then not copied at all (its
-        blocks are freed at once and never read).
+        With ``pending`` (a list) the transfer's move (a direct copy, or the
+        unpack of its payloads) is not issued here: a :class:`PendingMove` is
+        appended for :meth:`DisaggregatedEngine.flush_moves` to issue together
+        with others. A sequence that finishes on arrival is then not moved at
+        all (its blocks are freed at once and never read).
         """
         engine = self.engine
         seq = engine.submit(transfer.token_ids[:-1], max_new_tokens=max_new_tokens,
@@ -195,7 +248,7 @@ class DecodeWorker:
             dst_ids = list(seq.block_table)
 
         engine.flush_offloads()   # evictions made room for dst_ids: read them first
-        deferred = pending is not None and transfer.source is not None
+        deferred = pending is not None
         if not deferred:
             self._move(transfer, dst_ids)
 
@@ -205,9 +258,11 @@ class DecodeWorker:
         copied = True
         if deferred:
             if seq.stop_reason() is None:
-                pending.append((transfer.source, list(dst_ids), self.copier))
+                pending.append(PendingMove(self.copier, list(dst_ids), transfer.source,
+                                           transfer.block_payloads))
             else:
-                transfer.source.done()
+                if transfer.source is not None:
+                    transfer.source.done()
                 copied = False      # never moved: its blocks hold no KV to share
         if (transfer.first_block or self.prefix_aware) and copied:
             engine.blocks.share_computed_blocks(seq)   # later requests can share these
@@ -246,11 +301,17 @@ class DecodeWorker:
                 raise TypeError("direct transfers need a copier with copy_blocks()")
             self.copier.copy_blocks(src.copier, src.block_ids, dst_ids)
             src.done()   # stream-ordered after the copy's reads
-        elif hasattr(self.copier, "write_blocks"):
-            self.copier.write_blocks(dst_ids, transfer.block_payloads)
         else:
-            for block_id, payload in zip(dst_ids, transfer.block_payloads):
-                self.copier.write_block(block_id, payload)
+            _write(self.copier, dst_ids, transfer.block_payloads)
+
+
+def _write(copier, dst_ids: list[int], payloads) -> None:
+    """Scatter payloads into dst_ids: one batched call, or the protocol's per-block writes."""
+    if hasattr(copier, "write_blocks"):
+        copier.write_blocks(dst_ids, payloads)
+    else:
+        for block_id, payload in zip(dst_ids, payloads):
+            copier.write_block(block_id, payload)
 
 
 class DisaggregatedEngine:
@@ -274,10 +335,13 @@ class DisaggregatedEngine:
         self.stats = DisaggregationStats()
 
     def handoff(self, prompt: list[int], max_new_tokens: int, temperature: float = 0.0,
-                pending: list | None = None) -> Sequence:
-        """Prefill one prompt and admit it into the decode pool."""
+                pending: list | None = None, payload_buffer: Callable | None = None
+                ) -> Sequence:
+        """Prefill one prompt and admit it into the decode pool (its move deferred into
+        ``pending`` when given; pack-mode payloads from ``payload_buffer`` when given)."""
         skip = self.decode.cached_prefix_blocks(prompt)
-        transfer = self.prefill.prefill(prompt, temperature, skip_blocks=skip)
+        transfer = self.prefill.prefill(prompt, temperature, skip_blocks=skip,
+                                        payload_buffer=payload_buffer)
         self.stats.prefills += 1
         self.stats.transfers += 1
         self.stats.blocks_transferred += transfer.num_blocks
@@ -287,24 +351,43 @@ class DisaggregatedEngine:
         return self.decode.admit(transfer, max_new_tokens, temperature, pending=pending)
 
     def flush_moves(self, pending: list) -> int:
-        """Issue deferred direct-mode copies: one pool-to-pool launch per (source, destination)
-        copier pair, then release the prefill blocks. Returns the number of blocks moved."""
-        groups: dict[tuple[int, int], tuple[Any, Any, list[int], list[int], list]] = {}
-        for source, dst_ids, dst_copier in pending:
-            key = (id(source.copier), id(dst_copier))
-            if key not in groups:
-                groups[key] = (source.copier, dst_copier, [], [], [])
-            _, _, src_all, dst_all, sources = groups[key]
-            src_all.extend(source.block_ids)
-            dst_all.extend(dst_ids)
-            sources.append(source)
+        """Issue deferred moves and return the number of blocks moved.
+
+        Direct copies: one pool-to-pool launch per (source, destination) copier
+        pair, then the prefill blocks are released. Unpacks: per destination
+        copier, one launch when the payloads lie one after another in one buffer
+        (a batched pack-mode ``generate``), else one per transfer.
+        """
+        copies: dict[tuple[int, int], tuple[Any, Any, list[int], list[int], list]] = {}
+        unpacks: dict[int, tuple[Any, list[list[int]], list]] = {}
+        for move in pending:
+            if move.source is not None:
+                key = (id(move.source.copier), id(move.copier))
+                if key not in copies:
+                    copies[key] = (move.source.copier, move.copier, [], [], [])
+                _, _, src_all, dst_all, sources = copies[key]
+                src_all.extend(move.source.block_ids)
+                dst_all.extend(move.dst_ids)
+                sources.append(move.source)
+            else:
+                entry = unpacks.setdefault(id(move.copier), (move.copier, [], []))
+                entry[1].append(move.dst_ids)
+                entry[2].append(move.payloads)
         moved = 0
-        for src_copier, dst_copier, src_all, dst_all, sources in groups.values():
+        for src_copier, dst_copier, src_all, dst_all, sources in copies.values():
             if src_all:
                 dst_copier.copy_blocks(src_copier, src_all, dst_all)
                 moved += len(src_all)
             for source in sources:
                 source.done()     # stream-ordered after the copy's reads
+        for dst_copier, dst_lists, payload_lists in unpacks.values():
+            joined = join_payloads(payload_lists) if hasattr(dst_copier, "write_blocks") else None
+            if joined is not None:
+                dst_copier.write_blocks([b for ids in dst_lists for b in ids], joined)
+            else:
+                for ids, payloads in zip(dst_lists, payload_lists):
+                    _write(dst_copier, ids, payloads)
+            moved += sum(len(ids) for ids in dst_lists)
         pending.clear()
         return moved
 
@@ -317,19 +400,32 @@ class DisaggregatedEngine:
                  temperature: float = 0.0, *, batch_moves: bool = False) -> list[list[int]]:
         """Prefill, hand off and decode ``prompts`` (ie/serve/disaggregated.py:106-130).
 
-        ``batch_moves=True`` (direct mode) admits every prompt as the reference
-        does — same block tables, same order — but issues the copies of all of
-        them as one launch before decoding starts (earlier only if the prefill
-        pool runs short of room for the next prompt).
+        ``batch_moves=True`` admits every prompt as the reference does — same
+        block tables, same order — but moves the KV of all of them together
+        before decoding starts:
+        - direct mode: one copy launch (earlier only if the prefill pool runs
+          short of room for the next prompt, its blocks being held until then);
+        - pack mode: each prompt is still packed with one launch and its prefill
+          blocks freed at once, as in the reference, but into the next slice of
+          one device staging buffer, so a single unpack launch places every
+          request (earlier only when that buffer, at most STAGING_ARENA_BYTES,
+          is full).
         """
-        if batch_moves and self.prefill.mode != "direct":
-            raise ValueError("batch_moves needs mode='direct'")
         pending: list | None = [] if batch_moves else None
+        payload_buffer = None
+        if batch_moves and self.prefill.mode == "pack" and \
+                hasattr(self.prefill.copier, "empty_payloads"):
+            bs = self.prefill.engine.config.block_size
+            need = sum(-(-(len(p) + 1) // bs) for p in prompts)
+            block = max(1, _per_block_bytes(self.prefill.engine))
+            capacity = max(1, min(need, STAGING_ARENA_BYTES // block))
+            payload_buffer = _StagingArena(self, capacity, pending).take
         sequences = []
         for prompt in prompts:
-            if pending and not self._prefill_has_room(prompt):
+            if pending and self.prefill.mode == "direct" and not self._prefill_has_room(prompt):
                 self.flush_moves(pending)
-            sequences.append(self.handoff(prompt, max_new_tokens, temperature, pending))
+            sequences.append(self.handoff(prompt, max_new_tokens, temperature, pending,
+                                          payload_buffer))
         if pending:
             self.flush_moves(pending)
         self.decode_until_done()

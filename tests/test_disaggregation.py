@@ -237,9 +237,32 @@ def test_a_batched_request_finished_on_arrival_leaves_no_shared_prefix():
     assert seq.token_ids[seq.num_prompt:] == want
 
 
-def test_batched_moves_need_direct_mode():
-    with pytest.raises(ValueError):
-        split().generate(G["prompts"], batch_moves=True)
+def test_batched_pack_moves_keep_the_reference_reads_and_defer_the_writes():
+    """Pack mode with batched moves: every prompt is packed and its prefill blocks
+    freed as the reference does (the same source tables and free counts), admission
+    reserves the same destination tables, and the writes wait for one flush. The
+    trace then holds the reference's calls, its reads in order and all writes after
+    them, and the tokens are the reference's."""
+    engine = split()
+    log = record(engine)
+    pending: list = []
+    seqs = []
+    for prompt, want in zip(G["prompts"], G["requests"]):
+        before = len(log)
+        seqs.append(engine.handoff(prompt, 10, 0.0, pending))
+        assert [b for op, b in log[before:] if op == "r"] == want["src_table"]
+        assert all(op == "r" for op, _ in log[before:])
+        assert seqs[-1].block_table == want["dst_table"]
+        assert engine.prefill.engine.blocks.num_free == want["prefill_free_after"]
+    assert len(pending) == len(G["prompts"])
+    before = len(log)
+    assert engine.flush_moves(pending) == sum(r["num_blocks"] for r in G["requests"])
+    assert log[before:] == [["w", b] for r in G["requests"] for b in r["dst_table"]]
+    assert sorted(map(tuple, log)) == sorted(map(tuple, G["copier_log"]))
+    engine.decode_until_done()
+    assert [s.token_ids[s.num_prompt:] for s in seqs] == G["disaggregated"]["10"]
+    assert split().generate(G["prompts"], max_new_tokens=10, temperature=0.0,
+                            batch_moves=True) == G["disaggregated"]["10"]
 
 
 def test_the_two_pools_share_one_reservation_with_prefill_first():

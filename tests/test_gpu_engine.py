@@ -281,6 +281,46 @@ def test_batched_moves_on_gpu_are_one_launch(gpu):
     assert fresh.generate(G["prompts"], max_new_tokens=8, batch_moves=True) == expected
 
 
+def test_batched_pack_moves_on_gpu_unpack_in_one_launch(gpu, monkeypatch):
+    """Pack mode with batched moves: each prompt packs into the next slice of one
+    staging buffer and the flush unpacks every request with one launch; the decode
+    pool then holds the same bytes as after per-request admission, and decoding
+    gives the same tokens. A buffer too small for the batch flushes when full."""
+    from iekv import _native
+    from iekv.serve import disaggregated
+    from iekv.serve.disaggregated import DisaggregatedEngine
+
+    m = model(gpu, torch.bfloat16)
+    bs = G["engine"]["block_size"]
+    plain = DisaggregatedEngine(m, engine_config())
+    plain_seqs = [plain.handoff(p, 8, 0.0) for p in G["prompts"]]
+    engine = DisaggregatedEngine(m, engine_config())
+    pending: list = []
+    total = sum(r["num_blocks"] for r in G["requests"])
+    arena = disaggregated._StagingArena(engine, total, pending)
+    seqs = [engine.handoff(p, 8, 0.0, pending, arena.take) for p in G["prompts"]]
+    assert [s.block_table for s in seqs] == [r["dst_table"] for r in G["requests"]]
+    assert arena.used == total and len(pending) == len(G["prompts"])
+    with _native.LaunchTimer(64) as timer:
+        assert engine.flush_moves(pending) == total
+        torch.cuda.synchronize()
+    assert len(timer.durations_ms) == 1 and timer.durations_ms[0] > 0
+    caches = lambda e: e.decode.engine.k_caches + e.decode.engine.v_caches
+    for a, b in zip(tiles(caches(plain), [x for s in plain_seqs for x in s.block_table], bs),
+                    tiles(caches(engine), [x for s in seqs for x in s.block_table], bs)):
+        assert torch.equal(a, b)
+    plain.decode_until_done()
+    engine.decode_until_done()
+    expected = [s.token_ids[s.num_prompt:] for s in plain_seqs]
+    assert [s.token_ids[s.num_prompt:] for s in seqs] == expected
+    fresh = DisaggregatedEngine(m, engine_config())
+    assert fresh.generate(G["prompts"], max_new_tokens=8, batch_moves=True) == expected
+    block = disaggregated._per_block_bytes(fresh.prefill.engine)
+    monkeypatch.setattr(disaggregated, "STAGING_ARENA_BYTES", 5 * block)
+    small = DisaggregatedEngine(m, engine_config())
+    assert small.generate(G["prompts"], max_new_tokens=8, batch_moves=True) == expected
+
+
 def test_batched_prefix_aware_moves_on_gpu(gpu):
     """Batched direct moves with prefix sharing: a prefix whose copy is still pending
     is shared (the one launch fills it before decode), and the blocks of a request

@@ -79,7 +79,7 @@ def scenario(seed):
         "preemption": str(rng.choice(["recompute", "swap"])),
         "mode": mode,
         "prefix_aware": bool(rng.integers(2)),
-        "batch_moves": mode == "direct" and bool(rng.integers(2)),
+        "batch_moves": bool(rng.integers(2)),
         "cache_dtype": [torch.float32, torch.bfloat16][int(rng.integers(2))],
         "rounds": rounds,
         "max_new": max_new,

@@ -79,6 +79,12 @@ def test_splitting_prefill_from_decode_never_changes_the_tokens(seed):
     got = engine.generate(w["prompts"], max_new_tokens=w["max_new"], temperature=0.0,
                           batch_moves=True)
     assert got == want, (seed, "batch_moves")
+    for kw in (dict(), dict(prefix_aware=True)):
+        engine = DisaggregatedEngine(model(w), config(w, w["ample"]), mode="pack",
+                                     copier_factory=oracle_factory, **kw)
+        got = engine.generate(w["prompts"], max_new_tokens=w["max_new"], temperature=0.0,
+                              batch_moves=True)
+        assert got == want, (seed, "pack batch_moves", kw)
 
 
 @pytest.mark.parametrize("seed", range(10))
