@@ -633,6 +633,15 @@ class Legs:
         for t in self.dst_k + self.dst_v:
             t.zero_()
 
+    def check(self, name: str) -> bool:
+        """The check that fits what leg ``name`` leaves behind, right after it ran."""
+        return {"pack": self.verify_pack, "unpack": self.verify_unpack,
+                "write_kv": self.verify_write_kv,
+                "write_kv_per_layer": self.verify_write_kv,
+                "gather_context": self.verify_gather,
+                "gather_per_array": lambda: self.verify_gather(packed=False)
+                }.get(name, self.verify)()
+
 
 def time_leg(legs: Legs, name: str, steps: int, warmup: int, per_launch: bool = True):
     """Warm up, then time ``steps`` steps twice.
@@ -853,6 +862,23 @@ def sweep(legs: Legs, names: list[str]) -> list[dict]:
     return rows
 
 
+def _chunk_ok(v: int) -> bool:
+    return v == 0 or (64 <= v <= 1 << 20 and v & (v - 1) == 0)
+
+
+# --ab keys that set one launch setting (iekv_set_launch / iekv_set_direct_chunk):
+# the setting's name there and the values iekv.h allows.
+LAUNCH_AB = {
+    "direct_chunk": ("direct_chunk_bytes", _chunk_ok),
+    "chunk": ("chunk_bytes", _chunk_ok),
+    "order": ("order", lambda v: v in (0, 1, 2, 4, 5, 6)),
+    "pack_order": ("pack_order", lambda v: v in (0, 1, 2, 4, 5, 6)),
+    "unroll": ("unroll", lambda v: v in (1, 2, 4, 8, 16)),
+    "nontemporal": ("nontemporal", lambda v: v in (0, 1)),
+    "run": ("run_blocks", lambda v: 0 <= v <= 64),
+}
+
+
 def ab_ok(spec: str, config: str) -> bool:
     """Whether an --ab setting is well formed for this workload."""
     key, _, raw = spec.partition("=")
@@ -863,10 +889,8 @@ def ab_ok(spec: str, config: str) -> bool:
         return all(v.isdigit() and 1 <= int(v) <= 8 for v in values)
     if key == "slack":
         return config in ("cfg3", "cfg4") and all(v == "engine" or v.isdigit() for v in values)
-    if key == "direct_chunk":
-        return all(v.isdigit() and (int(v) == 0 or (64 <= int(v) <= 1 << 20
-                                                     and int(v) & (int(v) - 1) == 0))
-                   for v in values)
+    if key in LAUNCH_AB:
+        return all(v.isdigit() and LAUNCH_AB[key][1](int(v)) for v in values)
     return False
 
 
@@ -877,9 +901,10 @@ def ab(args, names: list[str], device) -> int:
     values. ``slack=64,6600,engine``: pools re-made for each value (cfg3 or
     cfg4 sized to the workload plus that many spare blocks, ``engine`` for the
     default pools), so every round also draws a new physical placement.
-    ``direct_chunk=4096,8192,0``: pools re-made for each round, and every value
-    of iekv_set_direct_chunk measured on the same pools within the round, so
-    each placement compares all values. Prints one JSON line with every
+    ``direct_chunk=4096,8192,0`` (or another launch setting: ``chunk``,
+    ``order``, ``pack_order``, ``unroll``, ``nontemporal``, ``run``): pools
+    re-made for each round, and every value of the setting measured on the same
+    pools within the round, so each placement compares all values. Prints one JSON line with every
     measurement and the per-value means.
     """
     import torch
@@ -893,12 +918,18 @@ def ab(args, names: list[str], device) -> int:
     legs = None
 
     def measure(legs, rnd, value):
+        """Time every leg on these pools, each checked right after its own run."""
+        nonlocal ok
         w = legs.w
         row = {"round": rnd, "value": value,
                "pools": [w.src_pool_blocks, w.dst_pool_blocks]}
         for name in legs_names:
+            legs.clear_dst()
             ms, _, _ = time_leg(legs, name, args.steps, args.warmup, per_launch=False)
             row[name] = round(sum(b for b, _ in legs.plan(name)) / (ms * 1e-3) / 1e9, 1)
+            if not legs.check(name):
+                row.setdefault("failed", []).append(name)
+                ok = False
         rows.append(row)
         log("[ab] " + json.dumps(row))
 
@@ -913,8 +944,7 @@ def ab(args, names: list[str], device) -> int:
                 legs.streams, legs.stagings = streams[:n], stagings[:n]
                 measure(legs, rnd, n)
         legs.streams, legs.stagings = streams, stagings
-        ok = legs.verify()
-    elif key == "direct_chunk":
+    elif key in LAUNCH_AB:
         before = _native.get_launch()
         try:
             for rnd in range(args.rounds):
@@ -923,9 +953,8 @@ def ab(args, names: list[str], device) -> int:
                             "separate" if args.separate_pools else "paired",
                             streams=args.streams)
                 for v in values:
-                    _native.set_launch(direct_chunk_bytes=int(v))
+                    _native.set_launch(**{LAUNCH_AB[key][0]: int(v)})
                     measure(legs, rnd, v)
-                ok = legs.verify() and ok
                 del legs
                 torch.cuda.empty_cache()
         finally:
@@ -939,7 +968,6 @@ def ab(args, names: list[str], device) -> int:
                             "separate" if args.separate_pools else "paired",
                             streams=args.streams)
                 measure(legs, rnd, v)
-                ok = legs.verify() and ok
                 del legs
                 torch.cuda.empty_cache()
     means = {}
@@ -987,8 +1015,9 @@ def main() -> int:
                          "one stream; the per-launch timing pass always uses one)")
     ap.add_argument("--ab", default="",
                     help="in-process A/B instead of the benchmark line: streams=1,2,4 (one set "
-                         "of pools), slack=64,6600,engine (pools re-made per value; cfg3/cfg4) "
-                         "or direct_chunk=4096,8192,0 (pools re-made per round, every value "
+                         "of pools), slack=64,6600,engine (pools re-made per value; cfg3/cfg4), "
+                         "or a launch setting such as direct_chunk=4096,8192,0 or "
+                         "pack_order=0,4 (pools re-made per round, every value "
                          "on each)")
     ap.add_argument("--rounds", type=int, default=3, help="rounds of an --ab comparison")
     ap.add_argument("--separate-pools", action="store_true",
@@ -1002,8 +1031,9 @@ def main() -> int:
               file=sys.stderr)
         return 2
     if args.ab and not ab_ok(args.ab, args.config):
-        print("--ab takes streams=N,... (N in 1..8), direct_chunk=B,... (0 or a power of two "
-              "from 64 to 1 MiB) or, for cfg3 and cfg4, slack=N|engine,...", file=sys.stderr)
+        print("--ab takes streams=N,... (N in 1..8), a launch setting ("
+              + ", ".join(f"{k}=V,..." for k in LAUNCH_AB)
+              + ") or, for cfg3 and cfg4, slack=N|engine,...", file=sys.stderr)
         return 2
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -1068,13 +1098,7 @@ def main() -> int:
         if name in ("pack_unpack", "copier_pack_unpack"):
             res["effective_handoff_GBps"] = round(2 * P / (ms * 1e-3) / 1e9, 1)
         if not args.no_verify and name != "plain_copy":
-            check = {"pack": legs.verify_pack, "unpack": legs.verify_unpack,
-                     "write_kv": legs.verify_write_kv,
-                     "write_kv_per_layer": legs.verify_write_kv,
-                     "gather_context": legs.verify_gather,
-                     "gather_per_array": lambda: legs.verify_gather(packed=False)
-                     }.get(name, legs.verify)
-            verified[name] = check()
+            verified[name] = legs.check(name)
             log(f"[bench] {name}: moved tiles equal their sources: {verified[name]}")
         results[name] = res
         if primary is None and name in HANDOFF_LEGS:

@@ -17,10 +17,12 @@ ROOT = Path(__file__).resolve().parents[1]
     (["--config", "cfg9"], "unknown workload"),
     (["--config", "cfg5", "--slack", "3"], "fixed pool sizes"),
     (["--ab", "streams=0,2"], "--ab takes"),
-    (["--ab", "unroll=4"], "--ab takes"),
+    (["--ab", "width=4"], "--ab takes"),
     (["--config", "cfg5", "--ab", "slack=64,engine"], "--ab takes"),
     (["--ab", "direct_chunk=4096,3000"], "--ab takes"),
     (["--ab", "direct_chunk=32"], "--ab takes"),
+    (["--ab", "pack_order=0,3"], "--ab takes"),
+    (["--ab", "unroll=0"], "--ab takes"),
 ])
 def test_the_bench_refuses_before_touching_a_gpu(args, message):
     out = subprocess.run([sys.executable, "bench.py", *args], cwd=ROOT, capture_output=True,
