@@ -73,3 +73,18 @@ def test_the_bench_line_keeps_its_contract(gpu, tp):
     host = legs["host_roundtrip"]
     assert host["d2h_GBps"] > 0 and host["h2d_GBps"] > 0
     assert host["one_call_per_block"]["blocks"] == min(1024, line["config"]["blocks"])
+
+
+@pytest.mark.parametrize("spec", ["pack_order=0,4", "direct_chunk=4096,8192", "streams=1,2"])
+def test_in_process_ab_checks_every_leg(gpu, spec):
+    """--ab prints one JSON line: one row per (round, value), every leg checked right
+    after its run (unpack after direct included)."""
+    line = run_bench("--ab", spec, "--rounds", "2", "--legs", "direct,unpack,pack,pack_unpack")
+    key, _, raw = spec.partition("=")
+    values = raw.split(",")
+    assert line["ab"] == key and line["values"] == values and line["verified"] is True
+    assert len(line["rows"]) == 2 * len(values)
+    assert all("failed" not in row for row in line["rows"])
+    assert set(line["mean"]) == set(values)
+    for row in line["rows"]:
+        assert all(row[leg] > 0 for leg in ("direct", "unpack", "pack", "pack_unpack"))
