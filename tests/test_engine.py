@@ -22,31 +22,49 @@ def engine(**kw):
                   EngineConfig(**cfg), copier_factory=oracle_factory)
 
 
-def test_batched_generation_matches_one_at_a_time():
-    prompts = [[1, 2, 3], [9, 8, 7, 6], [4, 4, 4, 4, 4, 4]]
-    batch = engine()
-    together = batch.generate(prompts, max_new_tokens=5, temperature=0.0)
-    apart = [engine().generate([p], max_new_tokens=5, temperature=0.0)[0] for p in prompts]
-    assert together == apart
-    # every finished request gave its blocks back (tests/test_engine.py:170-173)
-    assert batch.blocks.num_free == batch.blocks.num_total
+def _prompts(seed, n, lo, hi):
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    return [[int(t) for t in rng.integers(0, SMALL["vocab_size"], size=int(rng.integers(lo, hi)))]
+            for _ in range(n)]
 
 
-def test_chunked_prefill_does_not_change_the_output():
-    prompt = [list(range(40))]
-    whole = engine(max_batch_tokens=512).generate(prompt, max_new_tokens=6, temperature=0.0)
-    chunked = engine(max_batch_tokens=12).generate(prompt, max_new_tokens=6, temperature=0.0)
-    assert whole == chunked
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_a_batch_decodes_as_its_requests_would_alone(seed):
+    """Requests sharing the scheduler's steps get the tokens each gets alone, and the
+    pool gets every block back once they finish (the reference's batching invariant,
+    tests/test_engine.py:104-110, 168-171)."""
+    prompts = _prompts(seed, 4, 1, 20)
+    shared = engine()
+    together = shared.generate(prompts, max_new_tokens=6, temperature=0.0)
+    assert together == [engine().generate([p], max_new_tokens=6, temperature=0.0)[0]
+                        for p in prompts]
+    assert shared.blocks.num_free == shared.blocks.num_total
 
 
-def test_prefix_cache_does_not_change_the_output():
-    shared = list(range(24))
-    cold = engine().generate([shared + [7]], max_new_tokens=6, temperature=0.0)
-    warm = engine()
-    warm.generate([shared + [1]], max_new_tokens=6, temperature=0.0)
-    reused = warm.generate([shared + [7]], max_new_tokens=6, temperature=0.0)
-    assert warm.blocks.blocks_reused > 0
-    assert reused == cold
+@pytest.mark.parametrize("budget", [5, 8, 13, 64])
+def test_prefill_split_over_steps_decodes_the_same(budget):
+    """A prompt prefilled a few tokens per step decodes what one full-prompt step
+    decodes (tests/test_engine.py:113-122)."""
+    prompt = _prompts(7, 1, 30, 31)
+    one_step = engine(max_batch_tokens=1024).generate(prompt, max_new_tokens=5, temperature=0.0)
+    assert engine(max_batch_tokens=budget).generate(prompt, max_new_tokens=5,
+                                                    temperature=0.0) == one_step
+
+
+def test_a_cached_prefix_decodes_as_a_fresh_one():
+    """A prompt whose leading full blocks are already cached (shared from an earlier
+    request) decodes what it decodes in an empty engine (tests/test_engine.py:124-133);
+    the shared blocks are reused, not recomputed."""
+    head = _prompts(11, 1, 32, 33)[0]                 # four full blocks of 8
+    first, second = head + [3, 1], head + [5]
+    fresh = engine().generate([second], max_new_tokens=5, temperature=0.0)
+    primed = engine()
+    primed.generate([first], max_new_tokens=5, temperature=0.0)
+    before = primed.blocks.blocks_reused
+    assert primed.generate([second], max_new_tokens=5, temperature=0.0) == fresh
+    assert primed.blocks.blocks_reused - before == 4
 
 
 PROMPTS = [list(range(i, i + 12)) for i in range(4)]
@@ -56,7 +74,7 @@ def test_preemption_does_not_change_the_output():
     roomy = engine(num_blocks=256, max_batch_tokens=256)
     expected = roomy.generate(PROMPTS, max_new_tokens=10, temperature=0.0)
     # with room for every sequence, blocks are taken only as tokens need them and
-    # nothing is preempted (tests/test_engine.py:162-168)
+    # nothing is preempted (tests/test_engine.py:160-165)
     assert roomy.scheduler.stats.preemptions == 0
     tight = engine(num_blocks=8, max_batch_tokens=256)
     assert tight.generate(PROMPTS, max_new_tokens=10, temperature=0.0) == expected
