@@ -9,8 +9,9 @@
 //   unpack : staging[i][a]        ->  pool[a][dst_ids[i]]
 // One workgroup owns one (array a, run of up to `run` consecutive list
 // entries, chunk of each tile). With one entry per run (the default) each tile
-// is split into chunks of at least the chunk size (4 KiB: one 16-byte vector
-// per lane), one workgroup per chunk, and the workgroup reads its id pair with
+// is split into chunks of at least the chunk size (4 KiB for launches that
+// read or write staging: one 16-byte vector per lane; 8 KiB for pool-to-pool
+// copies: two), one workgroup per chunk, and the workgroup reads its id pair with
 // scalar loads; tiles smaller than the chunk size are grouped instead, one
 // workgroup taking a block's tiles in several consecutive arrays; a run of
 // several entries stages its ids in LDS. Data moves
@@ -120,11 +121,13 @@ std::atomic<int> g_pack_order{0};
 // Against whole tiles, 8 KiB chunks were best or tied on every leg.
 std::atomic<int> g_chunk{4096};
 // The same setting for pool-to-pool moves (copy_direct and its variants).
-// Measured on MI355X (one box, two request streams, the Llama-3-8B,
-// prefix-sharing and 70B-share workloads, each setting in two processes):
-// 8 KiB chunks moved the direct copy at 6.49 / 6.47 / 6.44 TB/s against
-// 6.41 / 6.25 / 6.31 for 4 KiB, and were also ahead of whole tiles and of
-// two-block runs on all three.
+// Measured on MI355X in one process per workload, pools made anew each round
+// and every setting timed on the same pools, two request streams: 8 KiB chunks
+// moved the per-request direct copy at 6.52 / 6.50 / 6.41 TB/s (Llama-3-8B,
+// prefix-sharing, 70B-share workloads) against 6.44 / 6.42 / 6.37 for 4 KiB,
+// ahead in every placement; whole tiles tied 8 KiB on the first two and lost
+// on the third. The one loss: a small move issued as one launch (0.3 GB in
+// about 37,000 workgroups) ran 4.7% slower than with 4 KiB chunks.
 std::atomic<int> g_direct_chunk{8192};
 
 // ---------------------------------------------------------------------------
