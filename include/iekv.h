@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 15
+#define IEKV_ABI_VERSION 16
 
 enum {
   IEKV_OK = 0,
@@ -276,6 +276,25 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
 int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                         const void* const* host_blocks, void* staging, int64_t staging_bytes,
                         hipStream_t compute, hipStream_t copy);
+
+/* The three host-tier calls above with their block ids in HOST memory, any
+ * number of them, as the *_ids handoff calls take theirs: the ids are checked
+ * first (IEKV_ERR_RANGE for an id outside the pool; for the restores,
+ * IEKV_ERR_IDS for a destination given twice), then travel in the launches'
+ * own kernel arguments, so no id upload precedes the move on the stream.
+ * Otherwise each behaves exactly as the call it mirrors.
+ * Replace: the same reference lines as iekv_offload, iekv_restore and
+ * iekv_restore_blocks, for callers whose block lists are host-side (the
+ * block manager's tables). */
+int iekv_offload_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                     void* host_dst, int64_t host_bytes, void* staging, int64_t staging_bytes,
+                     hipStream_t compute, hipStream_t copy);
+int iekv_restore_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                     const void* host_src, int64_t host_bytes, void* staging,
+                     int64_t staging_bytes, hipStream_t compute, hipStream_t copy);
+int iekv_restore_blocks_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                            const void* const* host_blocks, void* staging,
+                            int64_t staging_bytes, hipStream_t compute, hipStream_t copy);
 
 /* Launch shape of the move kernels (process-wide):
  *   run_blocks  blocks per workgroup run, 1..64; 0 = automatic (currently one

@@ -394,11 +394,12 @@ kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
 
 // Scattered host images restored directly: list entry i's image ([2L][T]
 // bytes, device-visible pinned host memory) starts at images.addr[i] and goes
-// to destination block dst_ids[i]. The addresses ride in the kernel
-// arguments. move_unit addresses entry i's image at stage + i * 2L * T, so
+// to destination block dst_ids[i] (images.ids[i] when dst_ids is null). The
+// addresses, and host-side ids, ride in the kernel arguments. move_unit addresses entry i's image at stage + i * 2L * T, so
 // shifting the base back by that much points it at images.addr[i].
 struct InlineImages {
   uint64_t addr[IEKV_INLINE_IMAGES];
+  int32_t ids[IEKV_INLINE_IMAGES];  // destination ids, when they come from host memory
 };
 
 template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
@@ -413,8 +414,9 @@ kv_unpack_images(PoolView src, PoolView dst, const char* __restrict__ /*src_stag
   const int i = pl.r;
   const uint64_t image_bytes = static_cast<uint64_t>(n_arrays) * tile_vecs * sizeof(V);
   const char* stage = reinterpret_cast<const char*>(images.addr[i] - i * image_bytes);
-  move_unit<V, U, NT, false, true>(src, dst, stage, nullptr, 0, dst_ids[i], i, pl.a, pl.p,
-                                   tile_vecs, parts, group, n_arrays);
+  const int32_t id = dst_ids ? dst_ids[i] : images.ids[i];
+  move_unit<V, U, NT, false, true>(src, dst, stage, nullptr, 0, id, i, pl.a, pl.p, tile_vecs,
+                                   parts, group, n_arrays);
 }
 
 // Row kernels on either side of the handoff. A pool row is one token's
@@ -1022,57 +1024,6 @@ void plan_slots(int64_t staging_bytes, int64_t block_bytes, int32_t n_blocks, in
   *slot_blocks = std::min<int64_t>(fit / *n_slots, n_blocks);
 }
 
-// Restore pipeline shared by iekv_restore and iekv_restore_blocks: chunk k of
-// the blocks is copied from host memory into a staging slot on `copy` (by
-// `load(slot, first, count)`) while `compute` unpacks chunk k-1 onto dst_ids.
-// Two slots when the staging buffer holds two blocks or more, else one.
-template <typename Load>
-int restore_pipeline(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
-                     void* staging, int64_t staging_bytes, hipStream_t compute,
-                     hipStream_t copy, Load load) {
-  int rc;
-  const int64_t block_bytes = image_bytes(dst, 1);
-  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
-    return rc;
-  if (n_blocks == 0) return IEKV_OK;
-  DeviceGuard guard(dst->device);
-  if (!guard.ok()) return guard.fail();
-
-  int n_slots;
-  int64_t slot_blocks;
-  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
-  const int align =
-      std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
-  Events loaded, unpacked, fence;
-  if ((rc = loaded.create(n_slots)) || (rc = unpacked.create(n_slots)) || (rc = fence.create(1)))
-    return rc;
-
-  // Entry fence: the copy stream must not overwrite staging while earlier
-  // compute-stream work still reads it.
-  IEKV_HIP(hipEventRecord(fence[0], compute));
-  IEKV_HIP(hipStreamWaitEvent(copy, fence[0], 0));
-
-  char* stage = static_cast<char*>(staging);
-  int last = 0;
-  for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
-    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
-    const int s = static_cast<int>(k % n_slots);
-    char* slot = stage + s * slot_blocks * block_bytes;
-    if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(copy, unpacked[s], 0));
-    if ((rc = load(slot, first, cnt))) return rc;
-    IEKV_HIP(hipEventRecord(loaded[s], copy));
-    IEKV_HIP(hipStreamWaitEvent(compute, loaded[s], 0));
-    if ((rc = launch_move<false, true>(nullptr, dst, slot, nullptr, nullptr, dst_ids + first,
-                                       cnt, dst->tile_bytes, dst->n_arrays, align, compute)))
-      return rc;
-    IEKV_HIP(hipEventRecord(unpacked[s], compute));
-    last = s;
-  }
-  // Later copy-stream work that writes staging is ordered after the last unpack.
-  IEKV_HIP(hipStreamWaitEvent(copy, unpacked[last], 0));
-  return IEKV_OK;
-}
-
 // IEKV_ERR_RANGE unless each of the n host ids lies in [0, num_blocks).
 int check_host_range(const int32_t* host_ids, int32_t n, int64_t num_blocks, const char* what) {
   for (int32_t i = 0; i < n; ++i) {
@@ -1166,6 +1117,83 @@ int launch_host_ids(const iekv_pool* sp, const iekv_pool* dp, const char* src_st
 }
 
 
+// The block ids of a host pipeline call: in device memory (the kernels read
+// them) or in host memory (checked before the call, then carried in the
+// launches' kernel arguments, IEKV_INLINE_IDS per launch).
+struct IdList {
+  const int32_t* ids;
+  bool on_host;
+  IdList from(int64_t first) const { return {ids + first, on_host}; }
+};
+
+// A pack (SP: pool -> staging) or unpack (DP: staging -> pool) of n_blocks
+// blocks of `pool` whose ids are an IdList.
+template <bool SP, bool DP>
+int launch_list(const iekv_pool* pool, const char* src_stage, char* dst_stage, IdList list,
+                int32_t n_blocks, int align, hipStream_t stream) {
+  static_assert(SP != DP, "a pack or an unpack");
+  const iekv_pool* sp = SP ? pool : nullptr;
+  const iekv_pool* dp = DP ? pool : nullptr;
+  const int32_t* s = SP ? list.ids : nullptr;
+  const int32_t* d = DP ? list.ids : nullptr;
+  if (list.on_host)
+    return launch_host_ids<SP, DP>(sp, dp, src_stage, dst_stage, s, d, n_blocks,
+                                   pool->tile_bytes, pool->n_arrays, align, stream);
+  return launch_move<SP, DP>(sp, dp, src_stage, dst_stage, s, d, n_blocks, pool->tile_bytes,
+                             pool->n_arrays, align, stream);
+}
+
+// Restore pipeline shared by the iekv_restore* calls: chunk k of the blocks is
+// copied from host memory into a staging slot on `copy` (by
+// `load(slot, first, count)`) while `compute` unpacks chunk k-1 onto dst_ids.
+// Two slots when the staging buffer holds two blocks or more, else one.
+template <typename Load>
+int restore_pipeline(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
+                     void* staging, int64_t staging_bytes, hipStream_t compute,
+                     hipStream_t copy, Load load) {
+  int rc;
+  const int64_t block_bytes = image_bytes(dst, 1);
+  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
+    return rc;
+  if (n_blocks == 0) return IEKV_OK;
+  DeviceGuard guard(dst->device);
+  if (!guard.ok()) return guard.fail();
+
+  int n_slots;
+  int64_t slot_blocks;
+  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
+  const int align =
+      std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
+  Events loaded, unpacked, fence;
+  if ((rc = loaded.create(n_slots)) || (rc = unpacked.create(n_slots)) || (rc = fence.create(1)))
+    return rc;
+
+  // Entry fence: the copy stream must not overwrite staging while earlier
+  // compute-stream work still reads it.
+  IEKV_HIP(hipEventRecord(fence[0], compute));
+  IEKV_HIP(hipStreamWaitEvent(copy, fence[0], 0));
+
+  char* stage = static_cast<char*>(staging);
+  int last = 0;
+  for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
+    const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
+    const int s = static_cast<int>(k % n_slots);
+    char* slot = stage + s * slot_blocks * block_bytes;
+    if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(copy, unpacked[s], 0));
+    if ((rc = load(slot, first, cnt))) return rc;
+    IEKV_HIP(hipEventRecord(loaded[s], copy));
+    IEKV_HIP(hipStreamWaitEvent(compute, loaded[s], 0));
+    if ((rc = launch_list<false, true>(dst, slot, nullptr, dst_ids.from(first), cnt, align,
+                                       compute)))
+      return rc;
+    IEKV_HIP(hipEventRecord(unpacked[s], compute));
+    last = s;
+  }
+  // Later copy-stream work that writes staging is ordered after the last unpack.
+  IEKV_HIP(hipStreamWaitEvent(copy, unpacked[last], 0));
+  return IEKV_OK;
+}
+
 // Events of one offload pipeline call: per staging slot, "packed" (recorded on
 // the compute stream after the slot's pack) and "copied" (on the copy stream
 // after its device-to-host copy), plus the entry fence.
@@ -1193,15 +1221,14 @@ int check_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks
 // staging slot on `compute` while `copy` moves chunk k-1 to the host (two
 // slots when the staging holds two blocks or more, else one). `preset` gives
 // the events to use; without it the call creates its own.
-int run_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, void* host_dst,
+int run_offload(const iekv_pool* src, IdList src_ids, int32_t n_blocks, void* host_dst,
                 int64_t need, char* staging, int64_t staging_bytes, hipStream_t compute,
                 hipStream_t copy, const OffloadEvents* preset) {
   int rc;
   if (need <= kZeroCopyMaxBytes) {
     if (char* mapped = device_view_of_host(host_dst, need)) {
       const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
-      return launch_move<true, false>(src, nullptr, nullptr, mapped, src_ids, nullptr, n_blocks,
-                                      src->tile_bytes, src->n_arrays, zc_align, compute);
+      return launch_list<true, false>(src, nullptr, mapped, src_ids, n_blocks, zc_align, compute);
     }
   }
   const int64_t block_bytes = image_bytes(src, 1);
@@ -1234,8 +1261,8 @@ int run_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks, 
     const int s = static_cast<int>(k % n_slots);
     char* slot = staging + s * slot_blocks * block_bytes;
     if (k >= n_slots) IEKV_HIP(hipStreamWaitEvent(compute, ev.copied[s], 0));
-    if ((rc = launch_move<true, false>(src, nullptr, nullptr, slot, src_ids + first, nullptr,
-                                       cnt, src->tile_bytes, src->n_arrays, align, compute)))
+    if ((rc = launch_list<true, false>(src, nullptr, slot, src_ids.from(first), cnt, align,
+                                       compute)))
       return rc;
     IEKV_HIP(hipEventRecord(ev.packed[s], compute));
     IEKV_HIP(hipStreamWaitEvent(copy, ev.packed[s], 0));
@@ -1290,6 +1317,97 @@ int static_staging(int device, const StaticStaging** out) {
   }
   *out = &st;
   return IEKV_OK;
+}
+
+// iekv_restore / iekv_restore_ids after their id checks: one contiguous host
+// image of n_blocks block images onto dst_ids.
+int restore_image(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks, const void* host_src,
+                  int64_t host_bytes, void* staging, int64_t staging_bytes, hipStream_t compute,
+                  hipStream_t copy) {
+  int rc;
+  const int64_t need = image_bytes(dst, n_blocks);
+  if (need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
+  if ((rc = check_buffer(host_src, host_bytes, need, "host"))) return rc;
+  const int64_t block_bytes = image_bytes(dst, 1);
+  if (n_blocks > 0 && need <= kZeroCopyMaxBytes) {
+    if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
+    DeviceGuard guard(dst->device);
+    if (!guard.ok()) return guard.fail();
+    if (const char* mapped = device_view_of_host(host_src, need)) {
+      const int zc_align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
+      if ((rc = launch_list<false, true>(dst, mapped, nullptr, dst_ids, n_blocks, zc_align,
+                                         compute)))
+        return rc;
+      // As after the staged pipeline, `copy` is ordered after the last unpack.
+      if (copy != compute) {
+        Events done;
+        if ((rc = done.create(1))) return rc;
+        IEKV_HIP(hipEventRecord(done[0], compute));
+        IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
+      }
+      return IEKV_OK;
+    }
+  }
+  const char* host = static_cast<const char*>(host_src);
+  return restore_pipeline(
+      dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
+      [&](char* slot, int64_t first, int32_t cnt) -> int {
+        IEKV_HIP(hipMemcpyAsync(slot, host + first * block_bytes, cnt * block_bytes,
+                                hipMemcpyHostToDevice, copy));
+        return IEKV_OK;
+      });
+}
+
+// iekv_restore_blocks / iekv_restore_blocks_ids after their id checks: block
+// image i at host_blocks[i] onto dst_ids[i].
+int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
+                   const void* const* host_blocks, void* staging, int64_t staging_bytes,
+                   hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if (n_blocks > 0 && !host_blocks)
+    return set_error(IEKV_ERR_INVALID, "host block address list is null");
+  for (int32_t i = 0; i < n_blocks; ++i)
+    if (!host_blocks[i]) return set_error(IEKV_ERR_INVALID, "host block %d address is null", i);
+  const int64_t block_bytes = image_bytes(dst, 1);
+  if (n_blocks > 0 && n_blocks <= IEKV_INLINE_IMAGES &&
+      block_bytes * n_blocks <= kZeroCopyMaxBytes) {
+    if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
+    DeviceGuard guard(dst->device);
+    if (!guard.ok()) return guard.fail();
+    InlineImages images{};
+    if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
+      const int32_t* device_ids = dst_ids.on_host ? nullptr : dst_ids.ids;
+      if (dst_ids.on_host) std::copy(dst_ids.ids, dst_ids.ids + n_blocks, images.ids);
+      if ((rc = launch_images(dst, images, device_ids, n_blocks, compute))) return rc;
+      // As after the staged pipeline, `copy` is ordered after the last unpack.
+      if (copy != compute) {
+        Events done;
+        if ((rc = done.create(1))) return rc;
+        IEKV_HIP(hipEventRecord(done[0], compute));
+        IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
+      }
+      return IEKV_OK;
+    }
+  }
+  return restore_pipeline(
+      dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
+      [&](char* slot, int64_t first, int32_t cnt) -> int {
+        // One copy per run of images that are adjacent in host memory within
+        // one allocation (iekv_plan::image_runs).
+        hipError_t err = hipSuccess;
+        iekv_plan::image_runs(
+            host_blocks + first, cnt, block_bytes,
+            [](uint64_t address) {
+              return bytes_to_allocation_end(reinterpret_cast<const char*>(address));
+            },
+            [&](int32_t i, int32_t len) {
+              if (err == hipSuccess)
+                err = hipMemcpyAsync(slot + i * block_bytes, host_blocks[first + i],
+                                     len * block_bytes, hipMemcpyHostToDevice, copy);
+            });
+        IEKV_HIP(err);
+        return IEKV_OK;
+      });
 }
 
 }  // namespace
@@ -1674,8 +1792,26 @@ int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
-  return run_offload(src, src_ids, n_blocks, host_dst, need, static_cast<char*>(staging),
-                     staging_bytes, compute, copy, nullptr);
+  return run_offload(src, {src_ids, false}, n_blocks, host_dst, need,
+                     static_cast<char*>(staging), staging_bytes, compute, copy, nullptr);
+}
+
+int iekv_offload_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                     void* host_dst, int64_t host_bytes, void* staging, int64_t staging_bytes,
+                     hipStream_t compute, hipStream_t copy) {
+  int rc;
+  int64_t need = 0;
+  if ((rc = check_offload(src, src_ids, n_blocks, host_dst, host_bytes, &need)) ||
+      (rc = check_host_range(src_ids, n_blocks, src->num_blocks, "source")))
+    return rc;
+  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? image_bytes(src, 1) : 0,
+                         "staging")))
+    return rc;
+  if (n_blocks == 0) return IEKV_OK;
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return guard.fail();
+  return run_offload(src, {src_ids, true}, n_blocks, host_dst, need,
+                     static_cast<char*>(staging), staging_bytes, compute, copy, nullptr);
 }
 
 int iekv_offload_static(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
@@ -1696,8 +1832,8 @@ int iekv_offload_static(const iekv_pool* src, const int32_t* src_ids, int32_t n_
   if (!guard.ok()) return guard.fail();
   const StaticStaging* st = nullptr;
   if ((rc = static_staging(src->device, &st))) return rc;
-  return run_offload(src, src_ids, n_blocks, host_dst, need, st->ptr, IEKV_STATIC_STAGING_BYTES,
-                     compute, copy, &st->events);
+  return run_offload(src, {src_ids, false}, n_blocks, host_dst, need, st->ptr,
+                     IEKV_STATIC_STAGING_BYTES, compute, copy, &st->events);
 }
 
 int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
@@ -1707,37 +1843,21 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
   if ((rc = check_pool(dst, "destination")) ||
       (rc = check_ids(dst_ids, n_blocks, "destination")))
     return rc;
-  const int64_t need = image_bytes(dst, n_blocks);
-  if (need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
-  if ((rc = check_buffer(host_src, host_bytes, need, "host"))) return rc;
-  const int64_t block_bytes = image_bytes(dst, 1);
-  if (n_blocks > 0 && need <= kZeroCopyMaxBytes) {
-    if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
-    DeviceGuard guard(dst->device);
-    if (!guard.ok()) return guard.fail();
-    if (const char* mapped = device_view_of_host(host_src, need)) {
-      const int zc_align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
-      if ((rc = launch_move<false, true>(nullptr, dst, mapped, nullptr, nullptr, dst_ids, n_blocks,
-                                         dst->tile_bytes, dst->n_arrays, zc_align, compute)))
-        return rc;
-      // As after the staged pipeline, `copy` is ordered after the last unpack.
-      if (copy != compute) {
-        Events done;
-        if ((rc = done.create(1))) return rc;
-        IEKV_HIP(hipEventRecord(done[0], compute));
-        IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
-      }
-      return IEKV_OK;
-    }
-  }
-  const char* host = static_cast<const char*>(host_src);
-  return restore_pipeline(
-      dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
-      [&](char* slot, int64_t first, int32_t cnt) -> int {
-        IEKV_HIP(hipMemcpyAsync(slot, host + first * block_bytes, cnt * block_bytes,
-                                hipMemcpyHostToDevice, copy));
-        return IEKV_OK;
-      });
+  return restore_image(dst, {dst_ids, false}, n_blocks, host_src, host_bytes, staging,
+                       staging_bytes, compute, copy);
+}
+
+int iekv_restore_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                     const void* host_src, int64_t host_bytes, void* staging,
+                     int64_t staging_bytes, hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if ((rc = check_pool(dst, "destination")) ||
+      (rc = check_ids(dst_ids, n_blocks, "destination")) ||
+      (rc = check_host_range(dst_ids, n_blocks, dst->num_blocks, "destination")) ||
+      (rc = check_distinct(dst_ids, n_blocks, "destination")))
+    return rc;
+  return restore_image(dst, {dst_ids, true}, n_blocks, host_src, host_bytes, staging,
+                       staging_bytes, compute, copy);
 }
 
 int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
@@ -1747,48 +1867,21 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
   if ((rc = check_pool(dst, "destination")) ||
       (rc = check_ids(dst_ids, n_blocks, "destination")))
     return rc;
-  if (n_blocks > 0 && !host_blocks)
-    return set_error(IEKV_ERR_INVALID, "host block address list is null");
-  for (int32_t i = 0; i < n_blocks; ++i)
-    if (!host_blocks[i]) return set_error(IEKV_ERR_INVALID, "host block %d address is null", i);
-  const int64_t block_bytes = image_bytes(dst, 1);
-  if (n_blocks > 0 && n_blocks <= IEKV_INLINE_IMAGES &&
-      block_bytes * n_blocks <= kZeroCopyMaxBytes) {
-    if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
-    DeviceGuard guard(dst->device);
-    if (!guard.ok()) return guard.fail();
-    InlineImages images{};
-    if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
-      if ((rc = launch_images(dst, images, dst_ids, n_blocks, compute))) return rc;
-      // As after the staged pipeline, `copy` is ordered after the last unpack.
-      if (copy != compute) {
-        Events done;
-        if ((rc = done.create(1))) return rc;
-        IEKV_HIP(hipEventRecord(done[0], compute));
-        IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
-      }
-      return IEKV_OK;
-    }
-  }
-  return restore_pipeline(
-      dst, dst_ids, n_blocks, staging, staging_bytes, compute, copy,
-      [&](char* slot, int64_t first, int32_t cnt) -> int {
-        // One copy per run of images that are adjacent in host memory within
-        // one allocation (iekv_plan::image_runs).
-        hipError_t err = hipSuccess;
-        iekv_plan::image_runs(
-            host_blocks + first, cnt, block_bytes,
-            [](uint64_t address) {
-              return bytes_to_allocation_end(reinterpret_cast<const char*>(address));
-            },
-            [&](int32_t i, int32_t len) {
-              if (err == hipSuccess)
-                err = hipMemcpyAsync(slot + i * block_bytes, host_blocks[first + i],
-                                     len * block_bytes, hipMemcpyHostToDevice, copy);
-            });
-        IEKV_HIP(err);
-        return IEKV_OK;
-      });
+  return restore_images(dst, {dst_ids, false}, n_blocks, host_blocks, staging, staging_bytes,
+                        compute, copy);
+}
+
+int iekv_restore_blocks_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
+                            const void* const* host_blocks, void* staging,
+                            int64_t staging_bytes, hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if ((rc = check_pool(dst, "destination")) ||
+      (rc = check_ids(dst_ids, n_blocks, "destination")) ||
+      (rc = check_host_range(dst_ids, n_blocks, dst->num_blocks, "destination")) ||
+      (rc = check_distinct(dst_ids, n_blocks, "destination")))
+    return rc;
+  return restore_images(dst, {dst_ids, true}, n_blocks, host_blocks, staging, staging_bytes,
+                        compute, copy);
 }
 
 int iekv_check_ids(const iekv_pool* src, const int32_t* src_ids, const iekv_pool* dst,

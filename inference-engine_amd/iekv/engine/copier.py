@@ -16,6 +16,10 @@ copies per block:
 * ``copy_blocks(source, src_ids, dst_ids)`` -> the direct pool-to-pool launch
   (iekv_copy_direct), which never materialises payloads.
 
+Host block lists of up to ``HOST_IDS_MAX`` ids go to the ``*_ids`` variants of
+these calls, which check them and carry them in the launches' kernel arguments;
+longer lists are checked here and uploaded once.
+
 Payloads are block-major byte images ``[n, 2L, T]`` (K tiles of layers
 0..L-1, then V tiles). A single block's payload iterates as
 ``(k_list, v_list)`` of ``[block_size, H, D]`` tensors, the structure of the
@@ -534,9 +538,12 @@ class HipSlotCopier:
             stream = torch.cuda.current_stream(self.device)
             staging = self._host_staging(n)
             copy = self.copy_stream()
-            _native.call("iekv_offload", self.pool.native.handle, ids.on_device().data_ptr(), n,
-                         out.data.data_ptr(), out.nbytes, staging.data_ptr(), staging.numel(),
-                         stream.cuda_stream, copy.cuda_stream)
+            # Short host lists ride in the launches' kernel arguments (no id upload).
+            fn, id_ptr = ("iekv_offload_ids", ids.host_pointer()) if ids.inline else \
+                ("iekv_offload", ids.on_device().data_ptr())
+            _native.call(fn, self.pool.native.handle, id_ptr, n, out.data.data_ptr(), out.nbytes,
+                         staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                         copy.cuda_stream)
             out.mark(stream)
             self.offload_launches += 1
             self.blocks_offloaded += n
@@ -587,9 +594,11 @@ class HipSlotCopier:
             # stream spares the call a cross-stream hand-off it would not use.
             direct = packed.nbytes <= _native.HOST_DIRECT_MAX and packed.data.is_pinned()
             copy = stream if direct else self.copy_stream()
-            _native.call("iekv_restore", self.pool.native.handle, ids.on_device().data_ptr(), n,
-                         packed.data.data_ptr(), packed.nbytes, staging.data_ptr(),
-                         staging.numel(), stream.cuda_stream, copy.cuda_stream)
+            fn, id_ptr = ("iekv_restore_ids", ids.host_pointer()) if ids.inline else \
+                ("iekv_restore", ids.on_device().data_ptr())
+            _native.call(fn, self.pool.native.handle, id_ptr, n, packed.data.data_ptr(),
+                         packed.nbytes, staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                         copy.cuda_stream)
             packed.mark(copy)
             self.restore_launches += 1
         elif ids.inline:
@@ -612,9 +621,10 @@ class HipSlotCopier:
         direct = (n <= _native.INLINE_IMAGES and n * self.pool.block_bytes <= _native.HOST_DIRECT_MAX
                   and all(p.packed.data.is_pinned() for p in payloads))
         copy = stream if direct else self.copy_stream()
-        _native.call("iekv_restore_blocks", self.pool.native.handle, ids.on_device().data_ptr(), n,
-                     addresses, staging.data_ptr(), staging.numel(), stream.cuda_stream,
-                     copy.cuda_stream)
+        fn, id_ptr = ("iekv_restore_blocks_ids", ids.host_pointer()) if ids.inline else \
+            ("iekv_restore_blocks", ids.on_device().data_ptr())
+        _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging.data_ptr(),
+                     staging.numel(), stream.cuda_stream, copy.cuda_stream)
         for root in {id(p.packed._root): p.packed._root for p in payloads}.values():
             root.mark(copy)
         self.restore_launches += 1

@@ -6,6 +6,7 @@ reference's NumPy slice copies for any KV dtype.
 """
 from __future__ import annotations
 
+import ctypes
 import hashlib
 
 import numpy as np
@@ -551,6 +552,64 @@ def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, o
     side.synchronize()          # the copy stream is ordered after the last unpack
     for d, p in zip(dst_ids, payloads):
         dst_o.write_block(d, p)
+    assert_pool_equals(dk, dv, dst_o)
+
+
+@pytest.mark.parametrize("shape,blocks,pinned", [
+    ("64k", 1, True), ("64k", 257, True), ("64k", 300, False), ("64k", 600, True),
+    ("1m", 72, True), ("1m", 5, False)])
+def test_host_tier_calls_with_host_ids(gpu, shape, blocks, pinned):
+    """iekv_offload_ids, iekv_restore_ids and iekv_restore_blocks_ids take their
+    ids from host memory (IEKV_INLINE_IDS per launch): bytes equal the oracle's on
+    the direct paths (pinned images of at most 64 MiB, scattered images at most
+    IEKV_INLINE_IMAGES) and on the staged pipelines (pageable memory, more than
+    64 MiB or more images), for lists shorter and longer than one launch's ids."""
+    from array import array
+
+    from iekv import _native
+    from iekv.engine.pools import KVPool
+
+    bs, layers, heads, dim, dt, n_pool = ((16, 4, 4, 32, torch.float32, 640) if shape == "64k"
+                                          else (16, 4, 8, 128, torch.bfloat16, 80))
+    sk, sv = allocate(n_pool, bs, layers, heads, dim, dt, gpu, seed=91)
+    dk, dv = allocate(n_pool, bs, layers, heads, dim, dt, gpu, seed=92)
+    src, dst = KVPool(sk, sv, bs), KVPool(dk, dv, bs)
+    rng = np.random.default_rng(93 + blocks)
+    src_ids, dst_ids = random_tables(rng, n_pool, n_pool, blocks)
+    s_host, d_host = array("i", src_ids), array("i", dst_ids)
+    block = src.block_bytes
+    host = torch.empty(blocks * block, dtype=torch.uint8, pin_memory=pinned)
+    staging = torch.empty(4 * block, dtype=torch.uint8, device=gpu)
+    stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    print(f"offload_ids {shape} x {blocks} pinned={pinned}", flush=True)
+    _native.call("iekv_offload_ids", src.native.handle, s_host.buffer_info()[0], blocks,
+                 host.data_ptr(), host.numel(), staging.data_ptr(), staging.numel(),
+                 stream.cuda_stream, side.cuda_stream)
+    stream.synchronize()
+    src_o = oracle_of(sk, sv, bs)
+    payloads = pack(src_o, src_ids)
+    assert np.array_equal(host.numpy(), packed_image(payloads).reshape(-1))
+    # The contiguous image back to dst_ids.
+    dst_o = oracle_of(dk, dv, bs)
+    _native.call("iekv_restore_ids", dst.native.handle, d_host.buffer_info()[0], blocks,
+                 host.data_ptr(), host.numel(), staging.data_ptr(), staging.numel(),
+                 stream.cuda_stream, side.cuda_stream)
+    side.synchronize()
+    for d, p in zip(dst_ids, payloads):
+        dst_o.write_block(d, p)
+    assert_pool_equals(dk, dv, dst_o)
+    # The same images in reverse order, one address each, onto a fresh table.
+    order = list(reversed(range(blocks)))
+    again = [int(b) for b in rng.permutation(n_pool)[:blocks]]
+    addresses = (ctypes.c_void_p * blocks)(*[host.data_ptr() + i * block for i in order])
+    a_host = array("i", again)
+    print(f"restore_blocks_ids {shape} x {blocks}", flush=True)
+    _native.call("iekv_restore_blocks_ids", dst.native.handle, a_host.buffer_info()[0], blocks,
+                 addresses, staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                 side.cuda_stream)
+    side.synchronize()
+    for d, i in zip(again, order):
+        dst_o.write_block(d, payloads[i])
     assert_pool_equals(dk, dv, dst_o)
 
 

@@ -11,6 +11,7 @@ No kernel runs: the pools are registered on a device that does not exist (their
 arrays are equally spaced, so registering touches no GPU), so a call whose ids
 pass every check stops at the device switch with IEKV_ERR_HIP.
 """
+import ctypes
 from types import SimpleNamespace
 
 import numpy as np
@@ -118,6 +119,37 @@ def test_pack_and_unpack_ids_are_refused_alike_by_the_library_and_numpy(seed):
         assert got == numpy_outcome(lambda: KVPool.host_ids(fake, ids)), ids
         got = library_outcome("iekv_unpack_ids", p.handle, addr(h), n, sp, staging.size, None)
         assert got == numpy_outcome(lambda: KVPool.host_ids(fake, ids, unique=True)), ids
+        p.close()
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_host_tier_ids_are_refused_alike_by_the_library_and_numpy(seed):
+    """iekv_offload_ids checks its source ids for range; iekv_restore_ids and
+    iekv_restore_blocks_ids check their destination ids for range and repeats,
+    as the pool's NumPy checks do."""
+    rng = np.random.default_rng(200 + seed)
+    for _ in range(150):
+        num_blocks = int(rng.integers(2, 30))
+        n = int(rng.integers(1, 12))
+        ids = [int(x) for x in rng.integers(-1, num_blocks + 1, size=n)]
+        p = pool(num_blocks)
+        h = _host_id_array(ids)
+        image = np.zeros(n * p.block_bytes, dtype=np.uint8)
+        ip = image.__array_interface__["data"][0]
+        staging = np.zeros(p.block_bytes, dtype=np.uint8)
+        sp = staging.__array_interface__["data"][0]
+        images = (ctypes.c_void_p * n)(*[ip + i * p.block_bytes for i in range(n)])
+        fake = SimpleNamespace(num_blocks=num_blocks)
+        got = library_outcome("iekv_offload_ids", p.handle, addr(h), n, ip, image.size, sp,
+                              staging.size, None, None)
+        assert got == numpy_outcome(lambda: KVPool.host_ids(fake, ids)), ids
+        want = numpy_outcome(lambda: KVPool.host_ids(fake, ids, unique=True))
+        got = library_outcome("iekv_restore_ids", p.handle, addr(h), n, ip, image.size, sp,
+                              staging.size, None, None)
+        assert got == want, ids
+        got = library_outcome("iekv_restore_blocks_ids", p.handle, addr(h), n, images, sp,
+                              staging.size, None, None)
+        assert got == want, ids
         p.close()
 
 
