@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 16
+#define IEKV_ABI_VERSION 17
 
 enum {
   IEKV_OK = 0,
@@ -277,15 +277,30 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
                         const void* const* host_blocks, void* staging, int64_t staging_bytes,
                         hipStream_t compute, hipStream_t copy);
 
-/* The three host-tier calls above with their block ids in HOST memory, any
+/* The offload with one host image per block: block src_ids[i] is packed into
+ * the image at host_blocks[i] ([2L][T] bytes, a HOST array of n_blocks
+ * addresses), so each image can live in its own allocation and be freed on its
+ * own. Up to IEKV_INLINE_IMAGES pinned images of at most
+ * IEKV_HOST_DIRECT_MAX_BYTES together are written by one pack launch on
+ * `compute`, the addresses in its kernel arguments; otherwise chunks are packed
+ * into `staging` and copied to the host on `copy` (one hipMemcpyAsync per run
+ * of images adjacent within one allocation), as iekv_offload does.
+ * Replaces: the same payload reads as iekv_offload
+ * (`copier.read_block(id)` in the offload hook, ie/core/block_manager.py:82),
+ * for a tier that keeps each block's payload on its own. */
+int iekv_offload_blocks(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                        void* const* host_blocks, void* staging, int64_t staging_bytes,
+                        hipStream_t compute, hipStream_t copy);
+
+/* The host-tier calls above with their block ids in HOST memory, any
  * number of them, as the *_ids handoff calls take theirs: the ids are checked
  * first (IEKV_ERR_RANGE for an id outside the pool; for the restores,
  * IEKV_ERR_IDS for a destination given twice), then travel in the launches'
  * own kernel arguments, so no id upload precedes the move on the stream.
  * Otherwise each behaves exactly as the call it mirrors.
- * Replace: the same reference lines as iekv_offload, iekv_restore and
- * iekv_restore_blocks, for callers whose block lists are host-side (the
- * block manager's tables). */
+ * Replace: the same reference lines as iekv_offload, iekv_restore,
+ * iekv_restore_blocks and iekv_offload_blocks, for callers whose block lists
+ * are host-side (the block manager's tables). */
 int iekv_offload_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
                      void* host_dst, int64_t host_bytes, void* staging, int64_t staging_bytes,
                      hipStream_t compute, hipStream_t copy);
@@ -295,6 +310,9 @@ int iekv_restore_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blo
 int iekv_restore_blocks_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
                             const void* const* host_blocks, void* staging,
                             int64_t staging_bytes, hipStream_t compute, hipStream_t copy);
+int iekv_offload_blocks_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                            void* const* host_blocks, void* staging, int64_t staging_bytes,
+                            hipStream_t compute, hipStream_t copy);
 
 /* Launch shape of the move kernels (process-wide):
  *   run_blocks  blocks per workgroup run, 1..64; 0 = automatic (currently one

@@ -392,31 +392,34 @@ kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
       i, pl.a, pl.p, tile_vecs, parts, group, n_arrays);
 }
 
-// Scattered host images restored directly: list entry i's image ([2L][T]
-// bytes, device-visible pinned host memory) starts at images.addr[i] and goes
-// to destination block dst_ids[i] (images.ids[i] when dst_ids is null). The
-// addresses, and host-side ids, ride in the kernel arguments. move_unit addresses entry i's image at stage + i * 2L * T, so
+// Scattered host images moved directly, in either direction: list entry i's
+// image ([2L][T] bytes, device-visible pinned host memory) starts at
+// images.addr[i]. A restore (DST_POOL) moves it onto block ids[i]; an offload
+// (SRC_POOL) packs block ids[i] into it. With ids null the ids are
+// images.ids[i]. The addresses, and host-side ids, ride in the kernel
+// arguments. move_unit addresses entry i's image at stage + i * 2L * T, so
 // shifting the base back by that much points it at images.addr[i].
 struct InlineImages {
   uint64_t addr[IEKV_INLINE_IMAGES];
-  int32_t ids[IEKV_INLINE_IMAGES];  // destination ids, when they come from host memory
+  int32_t ids[IEKV_INLINE_IMAGES];  // block ids, when they come from host memory
 };
 
 template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
 __global__ void __launch_bounds__(kThreads)
-kv_unpack_images(PoolView src, PoolView dst, const char* __restrict__ /*src_stage*/,
-                 char* __restrict__ /*dst_stage*/, InlineImages images,
-                 const int32_t* __restrict__ dst_ids, int32_t tile_vecs, int32_t n_arrays,
-                 int32_t runs, int32_t parts, int32_t group, int32_t order) {
-  static_assert(!SRC_POOL && DST_POOL, "images are restored into a pool");
+kv_move_images(PoolView src, PoolView dst, const char* __restrict__ /*src_stage*/,
+               char* __restrict__ /*dst_stage*/, InlineImages images,
+               const int32_t* __restrict__ ids, int32_t tile_vecs, int32_t n_arrays,
+               int32_t runs, int32_t parts, int32_t group, int32_t order) {
+  static_assert(SRC_POOL != DST_POOL, "images are packed from, or restored into, a pool");
   const Place pl = place_at(blockIdx.x, gridDim.x, (n_arrays + group - 1) / group, runs, parts,
                             order);
   const int i = pl.r;
   const uint64_t image_bytes = static_cast<uint64_t>(n_arrays) * tile_vecs * sizeof(V);
-  const char* stage = reinterpret_cast<const char*>(images.addr[i] - i * image_bytes);
-  const int32_t id = dst_ids ? dst_ids[i] : images.ids[i];
-  move_unit<V, U, NT, false, true>(src, dst, stage, nullptr, 0, id, i, pl.a, pl.p, tile_vecs,
-                                   parts, group, n_arrays);
+  char* stage = reinterpret_cast<char*>(images.addr[i] - i * image_bytes);
+  const int32_t id = ids ? ids[i] : images.ids[i];
+  move_unit<V, U, NT, SRC_POOL, DST_POOL>(src, dst, stage, stage, SRC_POOL ? id : 0,
+                                          DST_POOL ? id : 0, i, pl.a, pl.p, tile_vecs, parts,
+                                          group, n_arrays);
 }
 
 // Row kernels on either side of the handoff. A pool row is one token's
@@ -728,7 +731,7 @@ InlineKernel pick_inline_kernel(int align, int unroll, int lane_vecs, bool nt, i
 }
 template <bool SP, bool DP>
 ImagesKernel pick_images_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
-  IEKV_PICK(kv_unpack_images)
+  IEKV_PICK(kv_move_images)
 }
 #undef IEKV_PICK
 
@@ -855,21 +858,25 @@ int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src
 }
 
 // The scattered-image restore in one launch (n_blocks <= IEKV_INLINE_IMAGES).
-int launch_images(const iekv_pool* dp, const InlineImages& images, const int32_t* dst_ids,
+template <bool SP, bool DP>
+int launch_images(const iekv_pool* pool, const InlineImages& images, const int32_t* ids,
                   int32_t n_blocks, hipStream_t stream) {
-  int align = dp->align;
+  static_assert(SP != DP, "a pack or an unpack");
+  int align = pool->align;
   for (int32_t i = 0; i < n_blocks; ++i) align = std::min(align, align_of_ptr(images.addr[i]));
   MovePlan pl;
   int rc;
-  if ((rc = plan_move(n_blocks, dp->tile_bytes, dp->n_arrays, align, false, true, true, &pl))) return rc;
+  if ((rc = plan_move(n_blocks, pool->tile_bytes, pool->n_arrays, align, SP, DP, true, &pl)))
+    return rc;
   // At most IEKV_HOST_DIRECT_MAX_BYTES in chunks of at least 64 bytes: one launch holds them.
   if (pl.runs_per_launch < n_blocks)
     return set_error(IEKV_ERR_INVALID, "%d images do not fit one launch", n_blocks);
-  ImagesKernel k = pick_images_kernel<false, true>(align, g_unroll.load(), pl.lane_vecs,
-                                                   g_nontemporal.load() != 0, &pl.vec);
+  ImagesKernel k = pick_images_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
+                                              g_nontemporal.load() != 0, &pl.vec);
   const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(n_blocks) * pl.units * pl.parts);
-  return dispatch(k, grid, stream, PoolView{}, view_of(dp), nullptr, nullptr, images, dst_ids,
-                  pl.tile_vecs, dp->n_arrays, n_blocks, pl.parts, pl.group, pl.order);
+  return dispatch(k, grid, stream, SP ? view_of(pool) : PoolView{},
+                  DP ? view_of(pool) : PoolView{}, nullptr, nullptr, images, ids, pl.tile_vecs,
+                  pool->n_arrays, n_blocks, pl.parts, pl.group, pl.order);
 }
 
 // The shape of a row launch over n rows in each of n_arrays arrays: lanes per
@@ -1221,16 +1228,16 @@ int check_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks
 // staging slot on `compute` while `copy` moves chunk k-1 to the host (two
 // slots when the staging holds two blocks or more, else one). `preset` gives
 // the events to use; without it the call creates its own.
-int run_offload(const iekv_pool* src, IdList src_ids, int32_t n_blocks, void* host_dst,
-                int64_t need, char* staging, int64_t staging_bytes, hipStream_t compute,
-                hipStream_t copy, const OffloadEvents* preset) {
+// The staged offload of n_blocks >= 1 checked blocks with src's device
+// current: chunk k is packed into a staging slot on `compute` while `copy`
+// moves chunk k-1 to the host with store(slot, first, count) (two slots when
+// the staging holds two blocks or more, else one). `preset` gives the events
+// to use; without it the call creates its own.
+template <typename Store>
+int offload_pipeline(const iekv_pool* src, IdList src_ids, int32_t n_blocks, char* staging,
+                     int64_t staging_bytes, hipStream_t compute, hipStream_t copy,
+                     const OffloadEvents* preset, Store store) {
   int rc;
-  if (need <= kZeroCopyMaxBytes) {
-    if (char* mapped = device_view_of_host(host_dst, need)) {
-      const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
-      return launch_list<true, false>(src, nullptr, mapped, src_ids, n_blocks, zc_align, compute);
-    }
-  }
   const int64_t block_bytes = image_bytes(src, 1);
   int n_slots;
   int64_t slot_blocks;
@@ -1254,7 +1261,6 @@ int run_offload(const iekv_pool* src, IdList src_ids, int32_t n_blocks, void* ho
   IEKV_HIP(hipEventRecord(ev.fence, compute));
   IEKV_HIP(hipStreamWaitEvent(copy, ev.fence, 0));
 
-  char* host = static_cast<char*>(host_dst);
   int last = 0;
   for (int64_t first = 0, k = 0; first < n_blocks; first += slot_blocks, ++k) {
     const int32_t cnt = static_cast<int32_t>(std::min<int64_t>(slot_blocks, n_blocks - first));
@@ -1266,15 +1272,38 @@ int run_offload(const iekv_pool* src, IdList src_ids, int32_t n_blocks, void* ho
       return rc;
     IEKV_HIP(hipEventRecord(ev.packed[s], compute));
     IEKV_HIP(hipStreamWaitEvent(copy, ev.packed[s], 0));
-    IEKV_HIP(hipMemcpyAsync(host + first * block_bytes, slot, cnt * block_bytes,
-                            hipMemcpyDeviceToHost, copy));
+    if ((rc = store(slot, first, cnt))) return rc;
     IEKV_HIP(hipEventRecord(ev.copied[s], copy));
     last = s;
   }
-  // Later compute-stream work (reuse of staging, reads of host_dst after a
-  // sync of `compute`) is ordered after the last device-to-host copy.
+  // Later compute-stream work (reuse of staging, reads of the host images after
+  // a sync of `compute`) is ordered after the last device-to-host copy.
   IEKV_HIP(hipStreamWaitEvent(compute, ev.copied[last], 0));
   return IEKV_OK;
+}
+
+// The offload of n_blocks >= 1 checked blocks into one host image, with src's
+// device current. An image of at most kZeroCopyMaxBytes in one pinned,
+// device-mapped allocation is written by the pack kernel directly; otherwise
+// the staged pipeline copies each chunk with one hipMemcpyAsync.
+int run_offload(const iekv_pool* src, IdList src_ids, int32_t n_blocks, void* host_dst,
+                int64_t need, char* staging, int64_t staging_bytes, hipStream_t compute,
+                hipStream_t copy, const OffloadEvents* preset) {
+  if (need <= kZeroCopyMaxBytes) {
+    if (char* mapped = device_view_of_host(host_dst, need)) {
+      const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
+      return launch_list<true, false>(src, nullptr, mapped, src_ids, n_blocks, zc_align, compute);
+    }
+  }
+  const int64_t block_bytes = image_bytes(src, 1);
+  char* host = static_cast<char*>(host_dst);
+  return offload_pipeline(src, src_ids, n_blocks, staging, staging_bytes, compute, copy, preset,
+                          [&](char* slot, int64_t first, int32_t cnt) -> int {
+                            IEKV_HIP(hipMemcpyAsync(host + first * block_bytes, slot,
+                                                    cnt * block_bytes, hipMemcpyDeviceToHost,
+                                                    copy));
+                            return IEKV_OK;
+                          });
 }
 
 // The staging of iekv_offload_static on one device: the device address of
@@ -1358,6 +1387,52 @@ int restore_image(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks, const 
       });
 }
 
+// iekv_offload_blocks / iekv_offload_blocks_ids after their id checks: block
+// src_ids[i] packed into the host image at host_blocks[i]. Up to
+// IEKV_INLINE_IMAGES pinned images of at most kZeroCopyMaxBytes together are
+// written by one pack launch; otherwise the staged pipeline copies each run of
+// images adjacent within one allocation with one hipMemcpyAsync.
+int offload_images(const iekv_pool* src, IdList src_ids, int32_t n_blocks,
+                   void* const* host_blocks, void* staging, int64_t staging_bytes,
+                   hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if (n_blocks > 0 && !host_blocks)
+    return set_error(IEKV_ERR_INVALID, "host block address list is null");
+  for (int32_t i = 0; i < n_blocks; ++i)
+    if (!host_blocks[i]) return set_error(IEKV_ERR_INVALID, "host block %d address is null", i);
+  const int64_t block_bytes = image_bytes(src, 1);
+  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
+    return rc;
+  if (n_blocks == 0) return IEKV_OK;
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return guard.fail();
+  if (n_blocks <= IEKV_INLINE_IMAGES && block_bytes * n_blocks <= kZeroCopyMaxBytes) {
+    InlineImages images{};
+    if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
+      const int32_t* device_ids = src_ids.on_host ? nullptr : src_ids.ids;
+      if (src_ids.on_host) std::copy(src_ids.ids, src_ids.ids + n_blocks, images.ids);
+      return launch_images<true, false>(src, images, device_ids, n_blocks, compute);
+    }
+  }
+  return offload_pipeline(
+      src, src_ids, n_blocks, static_cast<char*>(staging), staging_bytes, compute, copy, nullptr,
+      [&](char* slot, int64_t first, int32_t cnt) -> int {
+        hipError_t err = hipSuccess;
+        iekv_plan::image_runs(
+            host_blocks + first, cnt, block_bytes,
+            [](uint64_t address) {
+              return bytes_to_allocation_end(reinterpret_cast<const char*>(address));
+            },
+            [&](int32_t i, int32_t len) {
+              if (err == hipSuccess)
+                err = hipMemcpyAsync(host_blocks[first + i], slot + i * block_bytes,
+                                     len * block_bytes, hipMemcpyDeviceToHost, copy);
+            });
+        IEKV_HIP(err);
+        return IEKV_OK;
+      });
+}
+
 // iekv_restore_blocks / iekv_restore_blocks_ids after their id checks: block
 // image i at host_blocks[i] onto dst_ids[i].
 int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
@@ -1378,7 +1453,8 @@ int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
     if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
       const int32_t* device_ids = dst_ids.on_host ? nullptr : dst_ids.ids;
       if (dst_ids.on_host) std::copy(dst_ids.ids, dst_ids.ids + n_blocks, images.ids);
-      if ((rc = launch_images(dst, images, device_ids, n_blocks, compute))) return rc;
+      if ((rc = launch_images<false, true>(dst, images, device_ids, n_blocks, compute)))
+        return rc;
       // As after the staged pipeline, `copy` is ordered after the last unpack.
       if (copy != compute) {
         Events done;
@@ -1881,6 +1957,27 @@ int iekv_restore_blocks_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_
       (rc = check_distinct(dst_ids, n_blocks, "destination")))
     return rc;
   return restore_images(dst, {dst_ids, true}, n_blocks, host_blocks, staging, staging_bytes,
+                        compute, copy);
+}
+
+int iekv_offload_blocks(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                        void* const* host_blocks, void* staging, int64_t staging_bytes,
+                        hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_ids(src_ids, n_blocks, "source")))
+    return rc;
+  return offload_images(src, {src_ids, false}, n_blocks, host_blocks, staging, staging_bytes,
+                        compute, copy);
+}
+
+int iekv_offload_blocks_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
+                            void* const* host_blocks, void* staging, int64_t staging_bytes,
+                            hipStream_t compute, hipStream_t copy) {
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_ids(src_ids, n_blocks, "source")) ||
+      (rc = check_host_range(src_ids, n_blocks, src->num_blocks, "source")))
+    return rc;
+  return offload_images(src, {src_ids, true}, n_blocks, host_blocks, staging, staging_bytes,
                         compute, copy);
 }
 

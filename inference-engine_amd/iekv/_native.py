@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most host ids one launch carries in its arguments
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
@@ -72,6 +72,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "iekv_restore_ids": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_int64, c_void_p,
                                  c_int64, c_void_p, c_void_p]),
     "iekv_restore_blocks_ids": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
+                                        c_int64, c_void_p, c_void_p]),
+    "iekv_offload_blocks": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64,
+                                    c_void_p, c_void_p]),
+    "iekv_offload_blocks_ids": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
                                         c_int64, c_void_p, c_void_p]),
     "iekv_set_launch": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "iekv_set_direct_chunk": (c_int, [c_int32]),

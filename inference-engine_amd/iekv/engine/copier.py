@@ -131,9 +131,15 @@ class PackedBlocks:
 
     def mark(self, stream: torch.cuda.Stream) -> None:
         """Record that async copies involving this (host) buffer end on ``stream``."""
+        PackedBlocks.mark_all([self], stream)
+
+    @staticmethod
+    def mark_all(buffers: Seq["PackedBlocks"], stream: torch.cuda.Stream) -> None:
+        """One event on ``stream`` marks the end of the copies of every buffer given."""
         ev = torch.cuda.Event()
         ev.record(stream)
-        self._root._event = ev
+        for buf in buffers:
+            buf._root._event = ev
 
     def synchronize(self) -> "PackedBlocks":
         """Block the host until pending copies into or out of this buffer are done."""
@@ -466,11 +472,44 @@ class HipSlotCopier:
             return 0
         pending, self._pending = self._pending, []
         live = [(block_id, p) for block_id, ref in pending if (p := ref()) is not None]
-        if live:
+        if live and self.payload_location == "host":
+            self._offload_each([b for b, _ in live], [p for _, p in live])
+        elif live:
             packed = self._gather([b for b, _ in live], self.payload_location)
             for i, (_, payload) in enumerate(live):
                 payload._resolve(packed, i)
         return len(live)
+
+    def _image_group(self) -> int:
+        """Most one-block host images one direct launch takes (IEKV_INLINE_IMAGES, and
+        IEKV_HOST_DIRECT_MAX_BYTES together)."""
+        return max(1, min(_native.INLINE_IMAGES, _native.HOST_DIRECT_MAX // self.pool.block_bytes))
+
+    def _offload_each(self, block_ids: list[int], payloads: list) -> None:
+        """Each deferred host read into a pinned buffer of its own (iekv_offload_blocks,
+        one launch per group of images). A tier payload then keeps only its own
+        block's bytes pinned, and buffers freed by the tier, all of one size, are
+        reused by torch's pinned cache."""
+        stream = torch.cuda.current_stream(self.device)
+        group = self._image_group()
+        for first in range(0, len(block_ids), group):
+            ids = self._ids(block_ids[first:first + group], what="source block")  # host list
+            n = len(ids)
+            bufs = [self._empty_packed(1, on_host=True) for _ in range(n)]
+            addresses = (ctypes.c_void_p * n)(*[b.data.data_ptr() for b in bufs])
+            staging = self._host_staging(n)
+            fn, id_ptr = ("iekv_offload_blocks_ids", ids.host_pointer()) if ids.inline else \
+                ("iekv_offload_blocks", ids.on_device().data_ptr())
+            # Pinned images of one group are written by the pack kernel on `stream`;
+            # the staged fallback orders `stream` after its last copy, so one event
+            # on `stream` marks every buffer.
+            _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging.data_ptr(),
+                         staging.numel(), stream.cuda_stream, self.copy_stream().cuda_stream)
+            PackedBlocks.mark_all(bufs, stream)
+            for buf, payload in zip(bufs, payloads[first:first + group]):
+                payload._resolve(buf, 0)
+            self.offload_launches += 1
+            self.blocks_offloaded += n
 
     def write_block(self, block_id: int, payload: Any) -> None:
         """Scatter one payload into ``block_id`` (ie/engine/copier.py:24-31)."""
@@ -609,25 +648,29 @@ class HipSlotCopier:
                          packed.data.data_ptr(), packed.nbytes, current_stream_handle(self.device))
 
     def _restore_scattered(self, ids: "_BlockIds", payloads: Seq[BlockPayload]) -> None:
-        """Host payloads from unrelated buffers (tier entries) -> one iekv_restore_blocks."""
+        """Host payloads from unrelated buffers (tier entries) -> iekv_restore_blocks, one
+        call per group of images one direct launch takes."""
         for p in payloads:
             self._check_packed(p.packed)
-        n = len(ids)
-        addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in payloads])
         stream = torch.cuda.current_stream(self.device)
-        staging = self._host_staging(n)
-        # Few, small pinned images are read by one unpack launch on the compute stream
-        # (IEKV_INLINE_IMAGES, IEKV_HOST_DIRECT_MAX_BYTES): no cross-stream hand-off.
-        direct = (n <= _native.INLINE_IMAGES and n * self.pool.block_bytes <= _native.HOST_DIRECT_MAX
-                  and all(p.packed.data.is_pinned() for p in payloads))
-        copy = stream if direct else self.copy_stream()
-        fn, id_ptr = ("iekv_restore_blocks_ids", ids.host_pointer()) if ids.inline else \
-            ("iekv_restore_blocks", ids.on_device().data_ptr())
-        _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging.data_ptr(),
-                     staging.numel(), stream.cuda_stream, copy.cuda_stream)
-        for root in {id(p.packed._root): p.packed._root for p in payloads}.values():
-            root.mark(copy)
-        self.restore_launches += 1
+        group = self._image_group()
+        for first in range(0, len(ids), group):
+            part = ids if len(ids) <= group else ids[first:first + group]
+            chunk = payloads[first:first + group]
+            n = len(part)
+            addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in chunk])
+            staging = self._host_staging(n)
+            # Pinned images are read by one unpack launch on the compute stream
+            # (IEKV_INLINE_IMAGES, IEKV_HOST_DIRECT_MAX_BYTES): no cross-stream hand-off.
+            direct = all(p.packed.data.is_pinned() for p in chunk)
+            copy = stream if direct else self.copy_stream()
+            fn, id_ptr = ("iekv_restore_blocks_ids", part.host_pointer()) if part.inline else \
+                ("iekv_restore_blocks", part.on_device().data_ptr())
+            _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging.data_ptr(),
+                         staging.numel(), stream.cuda_stream, copy.cuda_stream)
+            PackedBlocks.mark_all(list({id(p.packed._root): p.packed._root
+                                        for p in chunk}.values()), copy)
+            self.restore_launches += 1
 
     def copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids, *,
                     stream: torch.cuda.Stream | None = None) -> None:

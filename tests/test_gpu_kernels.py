@@ -613,6 +613,74 @@ def test_host_tier_calls_with_host_ids(gpu, shape, blocks, pinned):
     assert_pool_equals(dk, dv, dst_o)
 
 
+@pytest.mark.parametrize("blocks,memory,host_ids", [
+    (1, "pinned", False), (7, "pinned", True), (128, "pinned", True), (130, "pinned", False),
+    (9, "pageable", True), (300, "pinned", True)])
+def test_offload_into_one_image_per_block(gpu, blocks, memory, host_ids):
+    """iekv_offload_blocks(_ids) packs block ids[i] into its own host image: up to
+    IEKV_INLINE_IMAGES pinned images with one launch, more images or pageable ones
+    through the staged pipeline (one copy per run of images adjacent within one
+    allocation). Every image equals the oracle's payload."""
+    from array import array
+
+    from iekv import _native
+    from iekv.engine.pools import KVPool
+
+    bs, layers, heads, dim = 16, 2, 4, 32            # 32 KiB block images (4 arrays x 8 KiB)
+    sk, sv = allocate(400, bs, layers, heads, dim, torch.float32, gpu, seed=95)
+    src = KVPool(sk, sv, bs)
+    rng = np.random.default_rng(96 + blocks)
+    src_ids = [int(b) for b in rng.permutation(400)[:blocks]]
+    block = src.block_bytes
+    # The first half of the images are allocations of their own; the second half lie
+    # one after another in one shared buffer (copied as one run when staged).
+    half = blocks // 2
+    pinned = memory == "pinned"
+    shared = torch.empty((blocks - half) * block, dtype=torch.uint8, pin_memory=pinned)
+    own = [torch.empty(block, dtype=torch.uint8, pin_memory=pinned) for _ in range(half)]
+    images = own + [shared[j * block:(j + 1) * block] for j in range(blocks - half)]
+    addresses = (ctypes.c_void_p * blocks)(*[t.data_ptr() for t in images])
+    staging = torch.empty(3 * block, dtype=torch.uint8, device=gpu)
+    stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    ids = array("i", src_ids) if host_ids else src.block_ids(src_ids)
+    id_ptr = ids.buffer_info()[0] if host_ids else ids.data_ptr()
+    fn = "iekv_offload_blocks_ids" if host_ids else "iekv_offload_blocks"
+    print(f"{fn} x {blocks} {memory}", flush=True)
+    _native.call(fn, src.native.handle, id_ptr, blocks, addresses, staging.data_ptr(),
+                 staging.numel(), stream.cuda_stream, side.cuda_stream)
+    stream.synchronize()
+    payloads = pack(oracle_of(sk, sv, bs), src_ids)
+    for i, (img, want) in enumerate(zip(images, payloads)):
+        assert np.array_equal(img.numpy(), packed_image([want]).reshape(-1)), i
+
+
+def test_deferred_offloads_keep_one_buffer_per_block(gpu):
+    """Deferred host reads flush into pinned buffers of one block each, so a payload the
+    tier keeps holds only its own block; bytes equal the oracle's, and restoring a mix
+    of them writes the oracle's blocks."""
+    from iekv.engine.copier import HipSlotCopier
+
+    bs = 8
+    sk, sv = allocate(64, bs, 2, 2, 16, torch.bfloat16, gpu, seed=97)
+    dk, dv = allocate(64, bs, 2, 2, 16, torch.bfloat16, gpu, seed=98)
+    src = HipSlotCopier(sk, sv, bs, payload_location="host")
+    dst = HipSlotCopier(dk, dv, bs)
+    assert src.defer_reads
+    reads = [src.read_block(b) for b in (5, 9, 2, 40, 33)]
+    assert src.flush() == 5 and src.offload_launches == 1
+    roots = {id(p.packed._root) for p in reads}
+    assert len(roots) == 5 and all(len(p.packed._root) == 1 for p in reads)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    for p, b in zip(reads, (5, 9, 2, 40, 33)):
+        want = packed_image(pack(src_o, [b])).reshape(-1)
+        assert np.array_equal(p.packed.host_data()[p.index].reshape(-1).numpy(), want)
+    dst.write_blocks([1, 2, 3], [reads[4], reads[0], reads[2]])
+    torch.cuda.synchronize()
+    for d, b in zip((1, 2, 3), (33, 5, 2)):
+        dst_o.write_block(d, src_o.read_block(b))
+    assert_pool_equals(dk, dv, dst_o)
+
+
 def test_host_payload_views_wait_for_their_copy(gpu):
     """A host payload is read right after read_block / read_blocks returns, with no
     synchronisation by the caller: its tiles must already be the finished snapshot,
@@ -943,8 +1011,9 @@ def test_a_restore_never_merges_copies_across_pinned_allocations(gpu):
 
 
 def test_more_scattered_images_than_one_direct_launch_takes(gpu):
-    """130 one-block tier payloads (more than IEKV_INLINE_IMAGES) restore through
-    the staged pipeline in one call, bytes equal to the oracle's."""
+    """130 one-block tier payloads (more than IEKV_INLINE_IMAGES) restore through the
+    copier in two direct calls (128 images, then 2), and through the library's
+    staged pipeline in one call; bytes equal to the oracle's either way."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -958,10 +1027,21 @@ def test_more_scattered_images_than_one_direct_launch_takes(gpu):
     src_ids, dst_ids = random_tables(rng, 140, 140, n)
     payloads = [src.read_blocks([b])[0] for b in src_ids]
     dst.write_blocks(dst_ids, payloads)
-    assert dst.restore_launches == 1
+    assert dst.restore_launches == 2
     torch.cuda.synchronize()
     src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
     handoff(src_o, dst_o, [src_ids], [dst_ids])
+    assert_pool_equals(dk, dv, dst_o)
+    # All 130 in one library call: the staged pipeline.
+    again = [int(b) for b in rng.permutation(140)[:n]]
+    addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in payloads])
+    staging = torch.empty(8 * src.pool.block_bytes, dtype=torch.uint8, device=gpu)
+    stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    _native.call("iekv_restore_blocks", dst.pool.native.handle,
+                 dst.pool.block_ids(again).data_ptr(), n, addresses, staging.data_ptr(),
+                 staging.numel(), stream.cuda_stream, side.cuda_stream)
+    side.synchronize()
+    handoff(src_o, dst_o, [src_ids], [again])
     assert_pool_equals(dk, dv, dst_o)
 
 

@@ -124,7 +124,8 @@ def test_pack_and_unpack_ids_are_refused_alike_by_the_library_and_numpy(seed):
 
 @pytest.mark.parametrize("seed", range(3))
 def test_host_tier_ids_are_refused_alike_by_the_library_and_numpy(seed):
-    """iekv_offload_ids checks its source ids for range; iekv_restore_ids and
+    """iekv_offload_ids and iekv_offload_blocks_ids check their source ids for
+    range; iekv_restore_ids and
     iekv_restore_blocks_ids check their destination ids for range and repeats,
     as the pool's NumPy checks do."""
     rng = np.random.default_rng(200 + seed)
@@ -150,6 +151,9 @@ def test_host_tier_ids_are_refused_alike_by_the_library_and_numpy(seed):
         got = library_outcome("iekv_restore_blocks_ids", p.handle, addr(h), n, images, sp,
                               staging.size, None, None)
         assert got == want, ids
+        got = library_outcome("iekv_offload_blocks_ids", p.handle, addr(h), n, images, sp,
+                              staging.size, None, None)
+        assert got == numpy_outcome(lambda: KVPool.host_ids(fake, ids)), ids
         p.close()
 
 
