@@ -152,11 +152,18 @@ class PackedBlocks:
 
     def __del__(self) -> None:
         # The root owns the pinned memory, which goes back to torch's host cache
-        # when it dies (views keep it alive); no DMA may still use it by then.
+        # when it dies (views keep it alive); no DMA may still use it by then. A
+        # buffer whose last copy is still running is held, with that copy's event,
+        # until the event completes (_hold_until_done), so dying never blocks.
         if self._parent is not None:
             return
         ev = self._event
-        if ev is not None:
+        if ev is None:
+            return
+        try:
+            if not ev.query():
+                _hold_until_done(self.data, ev)
+        except Exception:
             try:
                 ev.synchronize()
             except Exception:
@@ -237,6 +244,24 @@ class DeferredBlockPayload(BlockPayload):
         if self._packed is None:
             self._copier.flush()
         return self._index
+
+
+# Pinned buffers whose PackedBlocks died while a copy still used them, each with
+# that copy's event. Holding them keeps torch's pinned cache from handing the
+# memory out again before the copy is done; they are dropped once it is.
+_UNFINISHED: list[tuple[torch.Tensor, torch.cuda.Event]] = []
+
+
+def _hold_until_done(data: torch.Tensor, ev: torch.cuda.Event) -> None:
+    _UNFINISHED.append((data, ev))
+    if len(_UNFINISHED) >= 32:
+        _release_finished()
+
+
+def _release_finished() -> None:
+    """Drop the held buffers whose copies have completed (no waiting)."""
+    if _UNFINISHED:
+        _UNFINISHED[:] = [(d, e) for d, e in _UNFINISHED if not e.query()]
 
 
 def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
@@ -390,6 +415,7 @@ class HipSlotCopier:
     def _empty_packed(self, n: int, on_host: bool) -> PackedBlocks:
         shape = (n, self.pool.n_arrays, self.pool.tile_bytes)
         if on_host:
+            _release_finished()
             data = torch.empty(shape, dtype=torch.uint8, pin_memory=True)
         else:
             data = torch.empty(shape, dtype=torch.uint8, device=self.device)

@@ -681,6 +681,36 @@ def test_deferred_offloads_keep_one_buffer_per_block(gpu):
     assert_pool_equals(dk, dv, dst_o)
 
 
+def test_a_payload_dropped_during_its_restore_keeps_its_memory_until_done(gpu):
+    """Host payloads restored and dropped at once, then new offloads made at once (which
+    torch's pinned cache would serve from freed buffers): the dropped buffers are held
+    until their restores finish, so every restored block is its source's bytes."""
+    from iekv.engine import copier as copier_mod
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 16, 4, 8, 128        # 1 MiB block images
+    sk, sv = allocate(96, bs, layers, heads, dim, torch.bfloat16, gpu, seed=99)
+    dk, dv = allocate(96, bs, layers, heads, dim, torch.bfloat16, gpu, seed=100)
+    src = HipSlotCopier(sk, sv, bs, payload_location="host")
+    dst = HipSlotCopier(dk, dv, bs)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    for rnd in range(4):
+        ids = list(range(rnd * 16, rnd * 16 + 16))
+        tier = [src.read_block(b) for b in ids]
+        src.flush()
+        dst.write_blocks([b + 1 for b in ids], tier)
+        del tier                                   # dies while the restore may still read it
+        again = [src.read_block(b) for b in range(64, 80)]
+        src.flush()                                # new pinned buffers, right away
+        del again
+        for b in ids:
+            dst_o.write_block(b + 1, src_o.read_block(b))
+    torch.cuda.synchronize()
+    assert_pool_equals(dk, dv, dst_o)
+    copier_mod._release_finished()
+    assert not copier_mod._UNFINISHED
+
+
 def test_host_payload_views_wait_for_their_copy(gpu):
     """A host payload is read right after read_block / read_blocks returns, with no
     synchronisation by the caller: its tiles must already be the finished snapshot,
