@@ -484,7 +484,8 @@ class Legs:
         One iekv_offload over the whole block list (pack on the compute stream
         overlapping device-to-host copies on a side stream), then one iekv_restore
         (host-to-device copies overlapping the unpack). Both are bounded by the
-        host link, not HBM.
+        host link, not HBM. Then, on a sample, the same pipelines called once per
+        block (the reference's pattern), and the drop-in tier path (_tier_roundtrip).
         """
         from iekv import _native
         from iekv.engine.copier import HOST_STAGING_BYTES
@@ -560,6 +561,9 @@ class Legs:
         torch.cuda.synchronize()
         each_d2h, each_h2d = a.elapsed_time(b), b.elapsed_time(c)
         del host
+        torch.cuda.synchronize()
+        torch._C._host_emptyCache()   # give the whole-list image's pinned memory back first
+        tier = self._tier_roundtrip(k)
         d2h_ms, h2d_ms = statistics.median(d2h), statistics.median(h2d)
         out = {"pinned_GB": round(P / 1e9, 2), "pin_alloc_s": round(pin_s, 2),
                "d2h_ms": round(d2h_ms, 2), "h2d_ms": round(h2d_ms, 2),
@@ -572,13 +576,63 @@ class Legs:
                    "d2h_GBps": round(k * bb / (each_d2h * 1e-3) / 1e9, 2),
                    "h2d_GBps": round(k * bb / (each_h2d * 1e-3) / 1e9, 2),
                    "d2h_us_per_block": round(1000 * each_d2h / k, 2),
-                   "h2d_us_per_block": round(1000 * each_h2d / k, 2)}}
+                   "h2d_us_per_block": round(1000 * each_h2d / k, 2)},
+               "through_the_tier": tier}
         log(f"[bench] host_roundtrip  {P / 1e9:.2f} GB pinned ({pin_s:.1f} s to pin): "
             f"D2H {out['d2h_GBps']} GB/s, H2D {out['h2d_GBps']} GB/s, "
             f"round trip {out['roundtrip_ms']} ms; one call per block ({k} blocks): "
             f"D2H {out['one_call_per_block']['d2h_GBps']} GB/s, "
-            f"H2D {out['one_call_per_block']['h2d_GBps']} GB/s")
+            f"H2D {out['one_call_per_block']['h2d_GBps']} GB/s; through the tier "
+            f"({tier['evictions_per_flush']} evictions per flush): D2H {tier['d2h_GBps']} GB/s, "
+            f"H2D {tier['h2d_GBps']} GB/s")
         return out
+
+    def _tier_roundtrip(self, k: int, per_flush: int = 64) -> dict:
+        """The same k blocks through the drop-in tier path, as the engine moves them.
+
+        A host-payload HipSlotCopier queues ``per_flush`` evictions (read_block, the
+        offload hook's call) and flushes them together, each block into a pinned
+        buffer of its own (iekv_offload_blocks); the payloads are then restored as
+        scattered tier entries (write_blocks -> iekv_restore_blocks), ``per_flush``
+        per call. Times are wall-clock to completion, host work included.
+        """
+        from iekv.engine.copier import HipSlotCopier
+
+        torch = self.torch
+        bs, bb = self.w.shape.block_size, self.w.shape.block_bytes
+        src = HipSlotCopier(self.src_k, self.src_v, bs, payload_location="host")
+        dst = HipSlotCopier(self.dst_k, self.dst_v, bs)
+        src_ids = [int(b) for b in self.src_all[:k].tolist()]
+        dst_ids = [int(b) for b in self.dst_all[:k].tolist()]
+
+        def offload():
+            payloads = []
+            for g in range(0, k, per_flush):
+                payloads += [src.read_block(b) for b in src_ids[g:g + per_flush]]
+                src.flush()
+            return payloads
+
+        def restore(payloads):
+            for g in range(0, k, per_flush):
+                dst.write_blocks(dst_ids[g:g + per_flush], payloads[g:g + per_flush])
+
+        restore(offload())                      # warm-up: pinned buffers, kernels
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        payloads = offload()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        restore(payloads)
+        t3 = time.perf_counter()
+        torch.cuda.synchronize()
+        t4 = time.perf_counter()
+        del payloads
+        return {"blocks": k, "block_bytes": bb, "evictions_per_flush": per_flush,
+                "d2h_GBps": round(k * bb / (t2 - t0) / 1e9, 2),
+                "h2d_GBps": round(k * bb / (t4 - t2) / 1e9, 2),
+                "host_us_per_block_offload": round(1e6 * (t1 - t0) / k, 2),
+                "host_us_per_block_restore": round(1e6 * (t3 - t2) / k, 2)}
 
     def verify(self) -> bool:
         """Every destination tile equals its source tile (whole workload, on the GPU)."""
@@ -1029,6 +1083,13 @@ def main() -> int:
     if not args.sweep and not any(x in HANDOFF_LEGS for x in names):
         print(f"--legs needs one handoff leg ({', '.join(HANDOFF_LEGS)}) for the line's value",
               file=sys.stderr)
+        return 2
+    if "host_roundtrip" in names and args.config == "cfg5":
+        # A run of this leg on cfg5 (43 GB pinned image, 2.5 MiB blocks) ended with a
+        # segmentation fault of the process; its cause has not been found, so the
+        # leg does not run there.
+        print("host_roundtrip is not run on cfg5: an earlier run of it there ended with a "
+              "segmentation fault whose cause is not yet found", file=sys.stderr)
         return 2
     if args.ab and not ab_ok(args.ab, args.config):
         print("--ab takes streams=N,... (N in 1..8), a launch setting ("

@@ -69,10 +69,15 @@ def test_the_bench_line_keeps_its_contract(gpu, tp):
     for name, leg in legs.items():
         if "ms_per_step" in leg:
             assert 0 < leg["host_issue_ms_per_step"] <= 1000 * leg["wall_s"] + 1.0, name
-    # the host tier's round trip: the whole block list each way, then one call per block
+    # the host tier's round trip: the whole block list each way, one call per block,
+    # and the drop-in tier path (deferred evictions flushed 64 at a time, scattered
+    # restores); the leg's verification covers the blocks the tier path restored
     host = legs["host_roundtrip"]
     assert host["d2h_GBps"] > 0 and host["h2d_GBps"] > 0
     assert host["one_call_per_block"]["blocks"] == min(1024, line["config"]["blocks"])
+    tier = host["through_the_tier"]
+    assert tier["blocks"] == host["one_call_per_block"]["blocks"]
+    assert tier["evictions_per_flush"] == 64 and tier["d2h_GBps"] > 0 and tier["h2d_GBps"] > 0
 
 
 @pytest.mark.parametrize("spec", ["pack_order=0,4", "direct_chunk=4096,8192", "streams=1,2"])
