@@ -1222,12 +1222,6 @@ int check_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks
   return check_buffer(host_dst, host_bytes, *need, "host");
 }
 
-// The offload of n_blocks >= 1 checked blocks with src's device current. An
-// image of at most kZeroCopyMaxBytes in one pinned, device-mapped allocation
-// is written by the pack kernel directly. Otherwise chunk k is packed into a
-// staging slot on `compute` while `copy` moves chunk k-1 to the host (two
-// slots when the staging holds two blocks or more, else one). `preset` gives
-// the events to use; without it the call creates its own.
 // The staged offload of n_blocks >= 1 checked blocks with src's device
 // current: chunk k is packed into a staging slot on `compute` while `copy`
 // moves chunk k-1 to the host with store(slot, first, count) (two slots when
