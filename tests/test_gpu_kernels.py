@@ -997,47 +997,58 @@ def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_b
     assert dst.blocks_written == 7
 
 
-def test_a_restore_never_merges_copies_across_pinned_allocations(gpu):
-    """Host images adjacent in memory are copied together only inside one
-    allocation. One-block offload batches each get their own pinned buffer;
-    when two of them happen to be adjacent in the address space, restoring
-    [last image of the first, first image of the second] must still move both
-    bytes-exact (one copy spanning both buffers would run past the end of the
-    allocation its source pointer belongs to). Torch's pinned allocator has
-    left gaps between such buffers on MI355X boxes so far, so the test skips
-    unless the address space gives it an adjacent pair."""
+def test_a_staged_restore_merges_images_only_within_one_allocation(gpu):
+    """The staged scattered restore copies each run of host images that are adjacent
+    inside one pinned allocation with one hipMemcpyAsync, and starts a new copy at
+    every allocation's end (a copy spanning two allocations would read past the end
+    of the one its source pointer belongs to).
+
+    Three host reads of 50 blocks each give three pinned buffers of 50 adjacent
+    images. One iekv_restore_blocks call of all 150 (more than one direct launch
+    takes, so the staged pipeline runs) lists them buffer after buffer, so the list
+    holds runs to merge and, at two places, a step from one allocation's last image
+    to another's first. Where the allocator placed two buffers back to back (on
+    MI355X boxes so far it has left a gap of at least one buffer's size after each
+    pinned allocation), that step is adjacent in memory too, and the run must still
+    end there. A second call interleaves the buffers image by image (no merges).
+    Bytes equal the oracle's."""
+    from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
-    bs, layers, heads, dim = 16, 32, 8, 128   # 2 MiB block images (the Llama-3-8B shape)
-    sk, sv = allocate(64, bs, layers, heads, dim, torch.bfloat16, gpu, seed=61)
-    dk, dv = allocate(64, bs, layers, heads, dim, torch.bfloat16, gpu, seed=62)
+    bs = 16
+    sk, sv = allocate(160, bs, 2, 2, 64, torch.bfloat16, gpu, seed=61)   # 16 KiB images
+    dk, dv = allocate(160, bs, 2, 2, 64, torch.bfloat16, gpu, seed=62)
     src = HipSlotCopier(sk, sv, bs, payload_location="host", defer_reads=False)
     dst = HipSlotCopier(dk, dv, bs)
-    batches = [src.read_blocks([b]) for b in range(48)]
+    rng = np.random.default_rng(63)
+    order = [int(b) for b in rng.permutation(160)[:150]]
+    packs = [src.read_blocks(order[i:i + 50]) for i in (0, 50, 100)]
     torch.cuda.synchronize()
-    start_of = {p.data.data_ptr(): i for i, p in enumerate(batches)}
-    pairs = [(i, start_of[p.data.data_ptr() + p.nbytes]) for i, p in enumerate(batches)
-             if p.data.data_ptr() + p.nbytes in start_of]
-    print(f"{len(pairs)} adjacent pinned payload buffers among {len(batches)}", flush=True)
-    if not pairs:
-        pytest.skip("no two pinned payload buffers were adjacent in the address space")
-    src_ids = [i for pair in pairs[:8] for i in pair]
-    dst_ids = list(range(len(src_ids)))
-    if len(set(src_ids)) != len(src_ids):   # chains a->b->c: keep disjoint pairs only
-        seen, keep = set(), []
-        for i, j in pairs:
-            if i not in seen and j not in seen:
-                keep.append((i, j))
-                seen.update((i, j))
-        src_ids = [i for pair in keep[:8] for i in pair]
-        dst_ids = list(range(len(src_ids)))
-    dst.write_blocks(dst_ids, [batches[i][0] for i in src_ids])
-    torch.cuda.synchronize()
-    src_o = oracle_of(sk, sv, bs)
-    for a, (s_arr, d_arr) in enumerate(zip(src_o.k_caches + src_o.v_caches,
-                                            host_bytes(dk) + host_bytes(dv))):
-        for s, d in zip(src_ids, dst_ids):
-            assert np.array_equal(d_arr[d * bs:(d + 1) * bs], s_arr[s * bs:(s + 1) * bs]), (a, s, d)
+    image = src.pool.block_bytes
+    ends = {p.data.data_ptr() + p.nbytes for p in packs}
+    starts = {p.data.data_ptr() for p in packs}
+    print(f"{len(ends & starts)} pinned buffers start where another ends", flush=True)
+    assert all(p.nbytes == 50 * image for p in packs)
+    # Two slots of 32 images: both steps between buffers (entries 50 and 100) fall
+    # inside a chunk, where the copies of one chunk are planned together.
+    staging = torch.empty(64 * image, dtype=torch.uint8, device=gpu)
+    stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    for layout in ("buffer after buffer", "interleaved"):
+        if layout == "interleaved":
+            picks = [(b, i) for i in range(50) for b in range(3)]
+        else:
+            picks = [(b, i) for b in range(3) for i in range(50)]
+        sources = [order[50 * b + i] for b, i in picks]
+        targets = [int(t) for t in rng.permutation(160)[:150]]
+        addresses = (ctypes.c_void_p * 150)(*[packs[b].data[i].data_ptr() for b, i in picks])
+        _native.call("iekv_restore_blocks", dst.pool.native.handle,
+                     dst.pool.block_ids(targets).data_ptr(), 150, addresses, staging.data_ptr(),
+                     staging.numel(), stream.cuda_stream, side.cuda_stream)
+        side.synchronize()
+        torch.cuda.synchronize()
+        handoff(src_o, dst_o, [sources], [targets])
+        assert_pool_equals(dk, dv, dst_o)
 
 
 def test_more_scattered_images_than_one_direct_launch_takes(gpu):
