@@ -135,3 +135,34 @@ def test_the_engine_accepts_preallocated_caches_of_its_size():
     with pytest.raises(ValueError):
         Engine(model, EngineConfig(block_size=8, num_blocks=17), copier_factory=oracle_factory,
                caches=caches)
+
+
+def test_an_eos_token_ends_a_request_before_its_token_limit():
+    """Greedy decoding of the same prompt, once to learn its third token, then with
+    that token as eos: the request stops right after emitting it."""
+    free = engine().generate([[1, 2, 3]], max_new_tokens=12, temperature=0.0)[0]
+    eos = free[2]
+    stop = free.index(eos) + 1                  # the first time eos comes out
+    e = engine()
+    seq = e.submit([1, 2, 3], max_new_tokens=12, temperature=0.0, eos_id=eos)
+    e.run()
+    assert seq.token_ids[3:] == free[:stop]
+    assert seq.num_generated == stop < 12
+    assert e.blocks.num_free == e.blocks.num_total
+
+
+def test_every_block_is_free_again_when_all_requests_finish():
+    e = engine()
+    e.generate([[1, 2, 3], [4, 5, 6, 7], [8, 9]], max_new_tokens=4)
+    assert e.blocks.num_free == e.blocks.num_total
+    assert not e.scheduler.has_work
+
+
+def test_a_pool_that_just_fits_the_batch_preempts_nothing():
+    """Four 12-token prompts with 5 new tokens need two 8-token blocks each at the end
+    (16 tokens); nine blocks hold them, since a block is taken only when a token
+    will be computed in it."""
+    e = engine(num_blocks=9, max_batch_tokens=256)
+    prompts = [list(range(i, i + 12)) for i in range(4)]
+    e.generate(prompts, max_new_tokens=5, temperature=0.0)
+    assert e.scheduler.stats.preemptions == 0
