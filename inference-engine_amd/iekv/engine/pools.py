@@ -32,6 +32,16 @@ def allocate_pool(num_blocks: int, block_size: int, num_layers: int, num_kv_head
     return [slab[0, l] for l in range(num_layers)], [slab[1, l] for l in range(num_layers)]
 
 
+def paged_view(cache: torch.Tensor, block_size: int) -> torch.Tensor:
+    """The ``[N, bs, H, D]`` view of one ``[N * bs, H, D]`` cache array
+    (ie/kernels/flash_backend.py:15-17): entry ``b`` is block ``b``'s tile, the
+    bytes the handoff kernels move for that block. No copy."""
+    slots, heads, dim = cache.shape
+    if block_size <= 0 or slots % block_size:
+        raise ValueError(f"{slots} slots are not whole blocks of {block_size}")
+    return cache.view(slots // block_size, block_size, heads, dim)
+
+
 def allocate_pool_pair(first_blocks: int, second_blocks: int, block_size: int,
                        num_layers: int, num_kv_heads: int, head_dim: int, *,
                        dtype: torch.dtype = torch.float16,

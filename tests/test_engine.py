@@ -166,3 +166,20 @@ def test_a_pool_that_just_fits_the_batch_preempts_nothing():
     prompts = [list(range(i, i + 12)) for i in range(4)]
     e.generate(prompts, max_new_tokens=5, temperature=0.0)
     assert e.scheduler.stats.preemptions == 0
+
+
+def test_the_paged_view_indexes_block_tiles_without_a_copy():
+    import torch
+
+    from iekv.engine.pools import allocate_pool, paged_view
+
+    k, v = allocate_pool(6, 4, 2, 3, 8, dtype=torch.float32, device="cpu")
+    k[1].copy_(torch.arange(k[1].numel(), dtype=torch.float32).view_as(k[1]))
+    view = paged_view(k[1], 4)
+    assert view.shape == (6, 4, 3, 8) and view.data_ptr() == k[1].data_ptr()
+    for b in range(6):
+        assert torch.equal(view[b], k[1][4 * b:4 * (b + 1)])
+    view[2].fill_(-1)                            # writes land in the cache itself
+    assert (k[1][8:12] == -1).all() and (k[1][:8] >= 0).all()
+    with pytest.raises(ValueError):
+        paged_view(k[1], 5)

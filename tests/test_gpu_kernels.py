@@ -81,6 +81,14 @@ def test_direct_copy_matches_the_oracle(gpu, dtype):
     assert_pool_equals(dk, dv, dst_o)
     assert_pool_equals(sk, sv, src_o)  # the source is untouched
     assert src.blocks_read == 37 and dst.blocks_written == 37
+    # The consumers' [N, bs, H, D] view (ie/kernels/flash_backend.py:15-17) sees
+    # each moved block at its new id.
+    from iekv.engine.pools import paged_view
+
+    for s_arr, d_arr in zip(sk + sv, dk + dv):
+        got = paged_view(d_arr, bs).view(torch.uint8)[torch.tensor(dst_ids, device=gpu)]
+        want = paged_view(s_arr, bs).view(torch.uint8)[torch.tensor(src_ids, device=gpu)]
+        assert torch.equal(got, want)
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
