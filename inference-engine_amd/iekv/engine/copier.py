@@ -141,6 +141,18 @@ class PackedBlocks:
         for buf in buffers:
             buf._root._event = ev
 
+    @staticmethod
+    def order_after(buffers: Seq["PackedBlocks"], stream: torch.cuda.Stream) -> None:
+        """Order ``stream`` after the pending copies of every buffer given (a device-side
+        wait, one per distinct event), so a restore issued on any stream reads host
+        payloads only once their offload has written them."""
+        seen = set()
+        for buf in buffers:
+            ev = buf._root._event
+            if ev is not None and id(ev) not in seen:
+                seen.add(id(ev))
+                stream.wait_event(ev)
+
     def synchronize(self) -> "PackedBlocks":
         """Block the host until pending copies into or out of this buffer are done."""
         ev = self._root._event
@@ -406,6 +418,7 @@ class HipSlotCopier:
         self._pending: list[tuple[int, weakref.ref]] = []
         self._copy_stream: torch.cuda.Stream | None = None
         self._staging: torch.Tensor | None = None
+        self._staging_stream: torch.cuda.Stream | None = None   # the last call that used it
 
     # -- helpers -------------------------------------------------------------
     @property
@@ -428,11 +441,27 @@ class HipSlotCopier:
         return self._copy_stream
 
     def _host_staging(self, n_blocks: int) -> torch.Tensor:
-        """Device staging for the host pipelines: up to two slots, bounded size."""
+        """Device staging for the host pipelines: up to two slots, bounded size.
+
+        One buffer serves every host call of this copier, on whichever stream the
+        call runs. The library leaves a call's compute stream ordered after its
+        last use of the buffer, so a call on another stream is first ordered
+        after the previous one's stream; a buffer replaced by a larger one is
+        kept from reuse until the streams that used it have finished with it.
+        """
         block = self.pool.block_bytes
         want = max(1, min(2 * n_blocks, max(2, HOST_STAGING_BYTES // block))) * block
+        stream = torch.cuda.current_stream(self.device)
+        last = self._staging_stream
         if self._staging is None or self._staging.numel() < want:
+            if self._staging is not None:
+                for used in (last, self._copy_stream):
+                    if used is not None:
+                        self._staging.record_stream(used)
             self._staging = torch.empty(want, dtype=torch.uint8, device=self.device)
+        elif last is not None and last != stream:
+            stream.wait_stream(last)
+        self._staging_stream = stream
         return self._staging
 
     def _check_packed(self, packed: PackedBlocks) -> None:
@@ -624,8 +653,11 @@ class HipSlotCopier:
                      stream: torch.cuda.Stream | None = None) -> None:
         """Scatter ``payloads[i]`` into ``block_ids[i]`` for every i (one launch when possible).
 
-        ``stream`` runs the call on that stream; it must be ordered after the work
-        that produced the payloads (the same stream as their read_blocks, say).
+        ``stream`` runs the call on that stream. Host payloads carry the event of
+        the offload that wrote them, and the call waits for it on the device, so a
+        restore may run on any stream. Device payloads carry none: the stream must
+        be ordered after the work that produced them (the same stream as their
+        read_blocks, say).
         """
         with self._on(stream):
             self._write_blocks(block_ids, payloads)
@@ -653,6 +685,7 @@ class HipSlotCopier:
         n = len(ids)
         if packed.on_host:
             stream = torch.cuda.current_stream(self.device)
+            PackedBlocks.order_after([packed], stream)
             staging = self._host_staging(n)
             # Small pinned images are read by the unpack kernel itself on the compute
             # stream (IEKV_HOST_DIRECT_MAX_BYTES); passing that stream as the copy
@@ -685,6 +718,7 @@ class HipSlotCopier:
             chunk = payloads[first:first + group]
             n = len(part)
             addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in chunk])
+            PackedBlocks.order_after([p.packed for p in chunk], stream)
             staging = self._host_staging(n)
             # Pinned images are read by one unpack launch on the compute stream
             # (IEKV_INLINE_IMAGES, IEKV_HOST_DIRECT_MAX_BYTES): no cross-stream hand-off.

@@ -689,6 +689,49 @@ def test_deferred_offloads_keep_one_buffer_per_block(gpu):
     assert_pool_equals(dk, dv, dst_o)
 
 
+def test_staged_host_calls_on_two_streams_share_one_staging_buffer(gpu):
+    """A host copier has one device staging buffer for all its staged transfers.
+    Two offloads larger than IEKV_HOST_DIRECT_MAX_BYTES issued back to back on two
+    streams, then two restores of them on the two streams, must each see only its
+    own bytes: the second call on a new stream is ordered after the first one's
+    use of the buffer. A third, larger offload then replaces the buffer while the
+    previous calls may still run. Bytes equal the oracle's."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim = 16, 2, 8, 128               # 128 KiB block images
+    sk, sv = allocate(2000, bs, layers, heads, dim, torch.bfloat16, gpu, seed=91)
+    dk, dv = allocate(2000, bs, layers, heads, dim, torch.bfloat16, gpu, seed=92)
+    src = HipSlotCopier(sk, sv, bs, payload_location="host", defer_reads=False)
+    dst = HipSlotCopier(dk, dv, bs)
+    image = src.pool.block_bytes
+    n = _native.HOST_DIRECT_MAX // image + 40           # staged, one chunk each
+    rng = np.random.default_rng(93)
+    order = [int(b) for b in rng.permutation(2000)]
+    ids_a, ids_b, ids_c = order[:n], order[n:2 * n], order[2 * n:3 * n + 100]
+    assert len(ids_c) == n + 100
+    main = torch.cuda.current_stream()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(main)
+    s2.wait_stream(main)
+    a = src.read_blocks(ids_a, stream=s1)
+    b = src.read_blocks(ids_b, stream=s2)
+    c = src.read_blocks(ids_c, stream=s1)                # a larger staging buffer
+    targets = [int(t) for t in rng.permutation(2000)]
+    da, db = targets[:n], targets[n:2 * n]
+    dst.write_blocks(da, a, stream=s2)
+    dst.write_blocks(db, b, stream=s1)
+    main.wait_stream(s1)
+    main.wait_stream(s2)
+    torch.cuda.synchronize()
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    for payload, ids in ((a, ids_a), (b, ids_b), (c, ids_c)):
+        got = payload.synchronize().data.view(torch.uint8).numpy()
+        assert np.array_equal(got, packed_image(pack(src_o, ids)))
+    handoff(src_o, dst_o, [ids_a, ids_b], [da, db])
+    assert_pool_equals(dk, dv, dst_o)
+
+
 def test_a_payload_dropped_during_its_restore_keeps_its_memory_until_done(gpu):
     """Host payloads restored and dropped at once, then new offloads made at once (which
     torch's pinned cache would serve from freed buffers): the dropped buffers are held
