@@ -12,8 +12,8 @@ moves, in the same order, to the oracle:
   - copy_requests over two streams;
   - single-block read_block / write_block protocol calls.
 Ids come as Python lists, tuples, NumPy arrays, CPU tensors or device tensors;
-some calls run on a side stream, ordered after and before the current stream
-as a caller must. Reads are snapshots at call time: deferred host reads are
+some calls (host offloads and restores included) run on a side stream, ordered
+after and before the current stream as a caller must. Reads are snapshots at call time: deferred host reads are
 flushed before anything writes their pool, as the engine does. At the end both
 pools equal their images byte for byte.
 """
@@ -140,7 +140,7 @@ def test_random_call_sequences_match_the_oracle(gpu, seed):
         elif op == "offload":
             s = pick(x, max(n, 1))
             if rng.integers(2):
-                payloads = list(host[x].read_blocks(_ids(rng, s, gpu)))
+                payloads = list(run(lambda st: host[x].read_blocks(_ids(rng, s, gpu), stream=st)))
             else:
                 payloads = [host[x].read_block(b) for b in s]
             tier.extend(zip(payloads, [oracle[x].read_block(b) for b in s]))
@@ -149,7 +149,10 @@ def test_random_call_sequences_match_the_oracle(gpu, seed):
             chosen = [tier[int(i)] for i in rng.choice(len(tier), size=k, replace=False)]
             d = pick(y, k)
             before_write(y)
-            dev[y].write_blocks(_ids(rng, d, gpu), [h for h, _ in chosen])
+            # Host payloads carry their offload's event: a restore on any stream
+            # waits for it (run() still orders the pool writes for the caller).
+            run(lambda st: dev[y].write_blocks(_ids(rng, d, gpu), [h for h, _ in chosen],
+                                               stream=st))
             for b, (_, p) in zip(d, chosen):
                 oracle[y].write_block(b, p)
         elif op == "requests":
