@@ -37,6 +37,10 @@
  *
  * Streams. Work is enqueued on the hipStream_t the caller passes (typically
  * torch.cuda.current_stream().cuda_stream); nothing synchronizes the host.
+ * The host pipelines (offload / restore) use a `compute` and a `copy` stream
+ * and leave the staging buffer free once the stream named in their comment has
+ * reached the point of return; a later call that reuses the same staging buffer
+ * on other streams must first be ordered after that point.
  * The library must run on the HIP runtime the caller's streams belong to:
  * load it into a process after that runtime (e.g. after `import torch`).
  */
