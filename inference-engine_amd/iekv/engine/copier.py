@@ -73,6 +73,32 @@ class PackedBlocks:
         self._event: torch.cuda.Event | None = None  # last async copy touching host data
         self._parent: PackedBlocks | None = None  # the buffer a slice views (kept alive)
         self._offset: int | None = 0   # first row in the root buffer (None: a strided view)
+        self._pinned: bool | None = None   # the root's data is pinned host memory (None: unknown)
+        self._checked = None           # the layout key of the last copier that accepted it
+
+    @classmethod
+    def _new(cls, data: torch.Tensor, num_layers: int, tile_shape: tuple[int, ...],
+             dtype: torch.dtype, pinned: bool) -> "PackedBlocks":
+        """A buffer a copier has just allocated in its pool's layout (no re-validation)."""
+        self = cls.__new__(cls)
+        self.data = data
+        self.num_layers = num_layers
+        self.tile_shape = tile_shape
+        self.dtype = dtype
+        self._event = None
+        self._parent = None
+        self._offset = 0
+        self._pinned = pinned
+        self._checked = None
+        return self
+
+    @property
+    def pinned(self) -> bool:
+        """Whether the data is pinned host memory (asked of torch once per buffer)."""
+        root = self._root
+        if root._pinned is None:
+            root._pinned = bool(root.data.is_pinned())
+        return root._pinned
 
     @property
     def _root(self) -> "PackedBlocks":
@@ -419,6 +445,10 @@ class HipSlotCopier:
         self._copy_stream: torch.cuda.Stream | None = None
         self._staging: torch.Tensor | None = None
         self._staging_stream: torch.cuda.Stream | None = None   # the last call that used it
+        # Payloads this copier has accepted carry this object, so a payload used
+        # again (a tier entry restored in a batch) is not validated again.
+        self._layout_key = (self.pool.n_arrays, self.pool.tile_bytes, self.pool.device)
+        self._tile_shape = tuple(self.pool.tile_shape)
 
     # -- helpers -------------------------------------------------------------
     @property
@@ -432,7 +462,10 @@ class HipSlotCopier:
             data = torch.empty(shape, dtype=torch.uint8, pin_memory=True)
         else:
             data = torch.empty(shape, dtype=torch.uint8, device=self.device)
-        return PackedBlocks(data, self.pool.num_layers, self.pool.tile_shape, self.pool.dtype)
+        out = PackedBlocks._new(data, self.pool.num_layers, self._tile_shape, self.pool.dtype,
+                                pinned=on_host)
+        out._checked = self._layout_key        # made in this pool's layout
+        return out
 
     def copy_stream(self) -> torch.cuda.Stream:
         """The side stream host copies run on (default priority)."""
@@ -465,6 +498,8 @@ class HipSlotCopier:
         return self._staging
 
     def _check_packed(self, packed: PackedBlocks) -> None:
+        if packed._checked is self._layout_key:
+            return
         if (packed.data.shape[1] != self.pool.n_arrays
                 or packed.data.shape[2] != self.pool.tile_bytes):
             raise ValueError(
@@ -474,6 +509,7 @@ class HipSlotCopier:
             raise ValueError("payload data must be contiguous")
         if not packed.on_host and packed.data.device != self.device:
             raise ValueError(f"payload on {packed.data.device}, pool on {self.device}")
+        packed._checked = self._layout_key
 
     def _from_tiles(self, payload: Any) -> PackedBlocks:
         """Pack a reference-structured payload ``(k_list, v_list)`` into one block image."""
@@ -690,7 +726,7 @@ class HipSlotCopier:
             # Small pinned images are read by the unpack kernel itself on the compute
             # stream (IEKV_HOST_DIRECT_MAX_BYTES); passing that stream as the copy
             # stream spares the call a cross-stream hand-off it would not use.
-            direct = packed.nbytes <= _native.HOST_DIRECT_MAX and packed.data.is_pinned()
+            direct = packed.nbytes <= _native.HOST_DIRECT_MAX and packed.pinned
             copy = stream if direct else self.copy_stream()
             fn, id_ptr = ("iekv_restore_ids", ids.host_pointer()) if ids.inline else \
                 ("iekv_restore", ids.on_device().data_ptr())
@@ -717,19 +753,23 @@ class HipSlotCopier:
             part = ids if len(ids) <= group else ids[first:first + group]
             chunk = payloads[first:first + group]
             n = len(part)
-            addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in chunk])
-            PackedBlocks.order_after([p.packed for p in chunk], stream)
+            packs = [p.packed for p in chunk]
+            # Checked payloads are contiguous [n, 2L, T] rows: image i starts
+            # index * block_bytes past its buffer's first byte.
+            block = self.pool.block_bytes
+            addresses = (ctypes.c_void_p * n)(*[q.data.data_ptr() + p.index * block
+                                                for q, p in zip(packs, chunk)])
+            PackedBlocks.order_after(packs, stream)
             staging = self._host_staging(n)
             # Pinned images are read by one unpack launch on the compute stream
             # (IEKV_INLINE_IMAGES, IEKV_HOST_DIRECT_MAX_BYTES): no cross-stream hand-off.
-            direct = all(p.packed.data.is_pinned() for p in chunk)
+            direct = all(q.pinned for q in packs)
             copy = stream if direct else self.copy_stream()
             fn, id_ptr = ("iekv_restore_blocks_ids", part.host_pointer()) if part.inline else \
                 ("iekv_restore_blocks", part.on_device().data_ptr())
             _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging.data_ptr(),
                          staging.numel(), stream.cuda_stream, copy.cuda_stream)
-            PackedBlocks.mark_all(list({id(p.packed._root): p.packed._root
-                                        for p in chunk}.values()), copy)
+            PackedBlocks.mark_all(list({id(q._root): q._root for q in packs}.values()), copy)
             self.restore_launches += 1
 
     def copy_blocks(self, source: "HipSlotCopier", src_ids, dst_ids, *,
