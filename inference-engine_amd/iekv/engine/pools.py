@@ -152,10 +152,7 @@ class KVPool:
         """Host-side ids as int64 NumPy, range-checked against this pool (IndexError)
         and, with ``unique``, checked for repeats (ValueError). ``ascending`` says the
         ids are already sorted, so repeats are adjacent."""
-        if isinstance(ids, torch.Tensor):
-            host = ids.detach().to(torch.int64).numpy().reshape(-1)
-        else:
-            host = np.asarray(ids, dtype=np.int64).reshape(-1)
+        host = integer_ids(ids, what)
         if host.size:
             lo, hi = (int(host[0]), int(host[-1])) if ascending else \
                 (int(host.min()), int(host.max()))
@@ -168,6 +165,22 @@ class KVPool:
                 if host.size > 1 and bool((ordered[1:] == ordered[:-1]).any()):
                     raise ValueError(f"{what} ids must be distinct")
         return host
+
+
+def integer_ids(ids, what: str = "block") -> np.ndarray:
+    """Host-side ids (a sequence, NumPy array or CPU tensor) as a flat int64 array.
+
+    Block ids index the pool as the reference's slices do (ie/engine/copier.py:14-16),
+    which refuse non-integers: floats and other non-integer values raise TypeError
+    instead of being truncated (booleans count as 0 and 1, as they do there)."""
+    if isinstance(ids, torch.Tensor):
+        if ids.numel() and (ids.dtype.is_floating_point or ids.dtype.is_complex):
+            raise TypeError(f"{what} ids must be integers, not {ids.dtype}")
+        return ids.detach().to(torch.int64).numpy().reshape(-1)
+    given = np.asarray(ids)
+    if given.size and given.dtype.kind not in "iub":
+        raise TypeError(f"{what} ids must be integers, not {given.dtype}")
+    return given.astype(np.int64, copy=False).reshape(-1)
 
 
 def _device_list(ids: torch.Tensor, pool: KVPool, what: str) -> torch.Tensor:

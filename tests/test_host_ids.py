@@ -173,3 +173,22 @@ def test_the_library_names_the_offending_id():
                      addr(tables["f"]), 2, None)
     p.close()
     q.close()
+
+
+def test_non_integer_ids_are_refused_not_truncated():
+    """The reference slices with ``b * bs`` (ie/engine/copier.py:14-16), which refuses a
+    float id; NumPy's int64 conversion would truncate it to a real block instead."""
+    import torch
+
+    from iekv.engine.pools import integer_ids
+
+    for bad in ([1.5], np.array([2.0]), torch.tensor([3.0]), [1, 2.5], np.array(["4"]),
+                [None]):
+        with pytest.raises(TypeError):
+            integer_ids(bad)
+        with pytest.raises(TypeError):
+            issue_order(bad, [0] * len(bad))
+    assert list(integer_ids([3, np.int32(1), True])) == [3, 1, 1]      # ints and bools
+    assert list(integer_ids(np.array([7], dtype=np.uint16))) == [7]
+    assert list(integer_ids(torch.tensor([5, 6], dtype=torch.int32))) == [5, 6]
+    assert integer_ids([]).size == 0 and integer_ids(np.array([])).size == 0
