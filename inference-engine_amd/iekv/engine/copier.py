@@ -33,6 +33,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import operator
 import weakref
 from array import array
 from typing import Any, Iterable, Sequence as Seq
@@ -540,7 +541,7 @@ class HipSlotCopier:
         """
         if not self.defer_reads:
             return self.read_blocks([block_id])[0]
-        block_id = int(block_id)
+        block_id = operator.index(block_id)      # a float id is refused, not truncated
         if not 0 <= block_id < self.pool.num_blocks:
             raise IndexError(f"source block id {block_id} out of range for a pool of "
                              f"{self.pool.num_blocks} blocks")
