@@ -438,8 +438,24 @@ def test_bad_ids_raise_before_any_launch(gpu):
         src.copy_blocks(src, [0, 1], [1, 2])
     with pytest.raises(ValueError):
         dst.write_blocks([0, 1], src.read_blocks([2]))
+    with pytest.raises(TypeError):
+        dst.copy_blocks(src, [0.0], [1])                   # not truncated to block 0
+    with pytest.raises(TypeError):
+        dst.write_blocks(np.array([1.5]), src.read_blocks([2]))
+    # A payload accepted by one copier is still checked by a copier of another layout.
+    ok = src.read_blocks([3])
+    dst.write_blocks([4], ok)
+    ek, ev = allocate(8, 16, 2, 4, 16, torch.float16, gpu, seed=16)   # twice the tile
+    other = HipSlotCopier(ek, ev, 16)
+    with pytest.raises(ValueError, match="does not fit"):
+        other.write_blocks([0], ok)
     torch.cuda.synchronize()
-    assert all(np.array_equal(a, b) for a, b in zip(before, host_bytes(dk)))
+    after = host_bytes(dk)
+    src_o = oracle_of(sk, sv, bs=16)
+    for a, (b, g) in enumerate(zip(before, after)):
+        want = b.copy()
+        want[4 * 16:5 * 16] = (src_o.k_caches + src_o.v_caches)[a][3 * 16:4 * 16]
+        assert np.array_equal(g, want)
 
 
 def test_device_ids_outside_the_pool_are_skipped_by_the_kernel(gpu):
