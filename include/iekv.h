@@ -347,7 +347,9 @@ int iekv_offload_blocks_ids(const iekv_pool* src, const int32_t* src_ids, int32_
  *               work-items halves the split, then spreads over several
  *               launches. This sets the chunk size of every move, pool-to-
  *               pool moves included (iekv_set_direct_chunk sets theirs
- *               alone).
+ *               alone), except the unpacks that read pinned host memory
+ *               themselves (direct restores), which move whole tiles, or
+ *               groups of tiles smaller than this size.
  * The defaults (run 0, unroll 8, nontemporal 1, order, pack_order and
  * chunk_bytes 4096; 8192 for pool-to-pool moves) are the library's measured
  * best; iekv_get_launch and iekv_get_direct_chunk report them.

@@ -769,12 +769,15 @@ class DeviceGuard {
 };
 
 // The launch shape of one move under the current settings (kv_plan.h); a
-// pool-to-pool move takes its own chunk size.
+// pool-to-pool move takes its own chunk size. `chunk` >= 0 sets this launch's
+// chunk size instead (host_read_chunk for moves that read pinned host memory).
 int plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
-              bool pool_reading, bool pool_writing, bool single_blocks, MovePlan* pl) {
+              bool pool_reading, bool pool_writing, bool single_blocks, MovePlan* pl,
+              int32_t chunk = -1) {
   iekv_plan::Settings settings;
   settings.run = g_run.load();
-  settings.chunk_bytes = pool_reading && pool_writing ? g_direct_chunk.load() : g_chunk.load();
+  settings.chunk_bytes = chunk >= 0 ? chunk
+                         : pool_reading && pool_writing ? g_direct_chunk.load() : g_chunk.load();
   settings.order = g_order.load();
   settings.pack_order = g_pack_order.load();
   switch (iekv_plan::plan_move(n_blocks, tile_bytes, n_arrays, align, pool_writing,
@@ -808,11 +811,13 @@ int dispatch(Kernel kernel, dim3 grid, hipStream_t stream, Args... args) {
 template <bool SP, bool DP>
 int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage, char* dst_stage,
                 const int32_t* src_ids, const int32_t* dst_ids, int32_t n_blocks,
-                int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream) {
+                int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream,
+                int32_t chunk = -1) {
   if (n_blocks == 0) return IEKV_OK;
   MovePlan pl;
   int rc;
-  if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, SP, DP, false, &pl))) return rc;
+  if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, SP, DP, false, &pl, chunk)))
+    return rc;
   MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
                                      g_nontemporal.load() != 0, &pl.vec);
   const int64_t block_image = tile_bytes * n_arrays;
@@ -838,11 +843,13 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
 template <bool SP, bool DP>
 int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
                        char* dst_stage, const InlineIds& ids, int32_t dst_off, int32_t n_blocks,
-                       int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream) {
+                       int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream,
+                       int32_t chunk = -1) {
   if (n_blocks == 0) return IEKV_OK;
   MovePlan pl;
   int rc;
-  if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, SP, DP, true, &pl))) return rc;
+  if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, SP, DP, true, &pl, chunk)))
+    return rc;
   InlineKernel k = pick_inline_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
                                               g_nontemporal.load() != 0, &pl.vec);
   for (int64_t r0 = 0; r0 < pl.total_runs; r0 += pl.runs_per_launch) {
@@ -860,13 +867,14 @@ int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src
 // The scattered-image restore in one launch (n_blocks <= IEKV_INLINE_IMAGES).
 template <bool SP, bool DP>
 int launch_images(const iekv_pool* pool, const InlineImages& images, const int32_t* ids,
-                  int32_t n_blocks, hipStream_t stream) {
+                  int32_t n_blocks, hipStream_t stream, int32_t chunk = -1) {
   static_assert(SP != DP, "a pack or an unpack");
   int align = pool->align;
   for (int32_t i = 0; i < n_blocks; ++i) align = std::min(align, align_of_ptr(images.addr[i]));
   MovePlan pl;
   int rc;
-  if ((rc = plan_move(n_blocks, pool->tile_bytes, pool->n_arrays, align, SP, DP, true, &pl)))
+  if ((rc = plan_move(n_blocks, pool->tile_bytes, pool->n_arrays, align, SP, DP, true, &pl,
+                      chunk)))
     return rc;
   // At most IEKV_HOST_DIRECT_MAX_BYTES in chunks of at least 64 bytes: one launch holds them.
   if (pl.runs_per_launch < n_blocks)
@@ -953,6 +961,26 @@ int64_t bytes_to_allocation_end(const char* p) {
 // 7 GB/s; at 16.8 MB both reach about 50 GB/s, and from 134 MB on the staged
 // pipelines are 3-5% faster (55-56 against 53-54 GB/s).
 constexpr int64_t kZeroCopyMaxBytes = IEKV_HOST_DIRECT_MAX_BYTES;
+
+// Chunk size of the unpack launches that read pinned host memory themselves (the
+// direct restores): 0, whole tiles per workgroup. Reads across the host link
+// gain from each workgroup streaming a longer contiguous run. Measured on MI355X,
+// one restore per block, bytes per second against 4 KiB chunks: 2 MiB blocks of
+// 32 KiB tiles 40.5 -> 51.0 GB/s, 2.5 MiB of 16 KiB tiles 41.5 -> 50.2, 3 MiB of
+// 64 KiB tiles 41.5 -> 53.7; 24 images per call 53.3 -> 56.6 on 32 KiB tiles, within
+// 3% either way on the others. Writes to host memory (direct offloads) measured
+// the same at either size, so they keep the staging chunk.
+// Tiles smaller than the staging chunk keep it, so several of them still share
+// a workgroup.
+#ifndef IEKV_HOST_READ_CHUNK
+#define IEKV_HOST_READ_CHUNK 0
+#endif
+constexpr int32_t kHostReadChunk = IEKV_HOST_READ_CHUNK;
+
+int32_t host_read_chunk(int64_t tile_bytes) {
+  const int32_t staged = g_chunk.load();
+  return staged > 0 && tile_bytes < staged ? staged : kHostReadChunk;
+}
 
 // The device address of the host range [p, p + bytes) when it lies in one
 // pinned allocation mapped for the device (HIP gives a pinned host pointer's
@@ -1104,7 +1132,7 @@ template <bool SP, bool DP>
 int launch_host_ids(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
                     char* dst_stage, const int32_t* src_ids, const int32_t* dst_ids,
                     int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
-                    hipStream_t stream) {
+                    hipStream_t stream, int32_t chunk = -1) {
   const int64_t image = tile_bytes * n_arrays;
   for (int32_t first = 0; first < n_blocks; first += IEKV_INLINE_IDS) {
     const int32_t m = std::min<int32_t>(IEKV_INLINE_IDS, n_blocks - first);
@@ -1117,7 +1145,7 @@ int launch_host_ids(const iekv_pool* sp, const iekv_pool* dp, const char* src_st
     if (DP) std::copy(dst_ids + first, dst_ids + first + m, ids.v + dst_off);
     const int rc = launch_move_inline<SP, DP>(
         sp, dp, SP ? nullptr : src_stage + first * image, DP ? nullptr : dst_stage + first * image,
-        ids, dst_off, m, tile_bytes, n_arrays, align, stream);
+        ids, dst_off, m, tile_bytes, n_arrays, align, stream, chunk);
     if (rc) return rc;
   }
   return IEKV_OK;
@@ -1137,7 +1165,7 @@ struct IdList {
 // blocks of `pool` whose ids are an IdList.
 template <bool SP, bool DP>
 int launch_list(const iekv_pool* pool, const char* src_stage, char* dst_stage, IdList list,
-                int32_t n_blocks, int align, hipStream_t stream) {
+                int32_t n_blocks, int align, hipStream_t stream, int32_t chunk = -1) {
   static_assert(SP != DP, "a pack or an unpack");
   const iekv_pool* sp = SP ? pool : nullptr;
   const iekv_pool* dp = DP ? pool : nullptr;
@@ -1145,9 +1173,9 @@ int launch_list(const iekv_pool* pool, const char* src_stage, char* dst_stage, I
   const int32_t* d = DP ? list.ids : nullptr;
   if (list.on_host)
     return launch_host_ids<SP, DP>(sp, dp, src_stage, dst_stage, s, d, n_blocks,
-                                   pool->tile_bytes, pool->n_arrays, align, stream);
+                                   pool->tile_bytes, pool->n_arrays, align, stream, chunk);
   return launch_move<SP, DP>(sp, dp, src_stage, dst_stage, s, d, n_blocks, pool->tile_bytes,
-                             pool->n_arrays, align, stream);
+                             pool->n_arrays, align, stream, chunk);
 }
 
 // Restore pipeline shared by the iekv_restore* calls: chunk k of the blocks is
@@ -1359,7 +1387,7 @@ int restore_image(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks, const 
     if (const char* mapped = device_view_of_host(host_src, need)) {
       const int zc_align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
       if ((rc = launch_list<false, true>(dst, mapped, nullptr, dst_ids, n_blocks, zc_align,
-                                         compute)))
+                                         compute, host_read_chunk(dst->tile_bytes))))
         return rc;
       // As after the staged pipeline, `copy` is ordered after the last unpack.
       if (copy != compute) {
@@ -1447,7 +1475,8 @@ int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
     if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
       const int32_t* device_ids = dst_ids.on_host ? nullptr : dst_ids.ids;
       if (dst_ids.on_host) std::copy(dst_ids.ids, dst_ids.ids + n_blocks, images.ids);
-      if ((rc = launch_images<false, true>(dst, images, device_ids, n_blocks, compute)))
+      if ((rc = launch_images<false, true>(dst, images, device_ids, n_blocks, compute,
+                                           host_read_chunk(dst->tile_bytes))))
         return rc;
       // As after the staged pipeline, `copy` is ordered after the last unpack.
       if (copy != compute) {
