@@ -541,6 +541,43 @@ def test_host_offload_and_restore_pipelines(gpu, staging_blocks, pinned):
     assert_pool_equals(dk, dv, dst_o)
 
 
+@pytest.mark.parametrize("bs,heads,dim,dtype", [
+    (5, 3, 3, torch.uint8),        # 45-byte tiles: byte vectors, grouped per workgroup
+    (2, 1, 24, torch.float32),     # 192-byte tiles
+    (16, 2, 64, torch.float16),    # 4 KiB tiles: one staging chunk
+    (64, 4, 64, torch.bfloat16),   # 32 KiB tiles: several chunks, whole tiles on reads
+    (256, 2, 64, torch.float16)])  # 64 KiB tiles
+def test_direct_host_transfers_of_every_tile_shape(gpu, bs, heads, dim, dtype):
+    """Pinned images restored directly by the unpack kernel (which reads whole tiles,
+    or groups of tiles smaller than the staging chunk) and offloaded directly by the
+    pack kernel, one contiguous image and scattered images: bytes equal the oracle's."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    layers = 3
+    sk, sv = allocate(40, bs, layers, heads, dim, dtype, gpu, seed=70)
+    dk, dv = allocate(40, bs, layers, heads, dim, dtype, gpu, seed=71)
+    src = HipSlotCopier(sk, sv, bs, payload_location="host", defer_reads=False)
+    dst = HipSlotCopier(dk, dv, bs)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    rng = np.random.default_rng(72)
+    src_ids, dst_ids = random_tables(rng, 40, 40, 17)
+    assert 17 * src.pool.block_bytes <= _native.HOST_DIRECT_MAX
+    whole = src.read_blocks(src_ids)                       # one pinned image, direct
+    single = [src.read_block(b) for b in src_ids[:9]]      # one buffer each
+    torch.cuda.synchronize()
+    payloads = pack(src_o, src_ids)
+    assert np.array_equal(whole.host_data().numpy(), packed_image(payloads))
+    dst.write_blocks(dst_ids, whole)                       # iekv_restore, direct
+    dst.write_blocks(dst_ids[:9][::-1], single[::-1])      # iekv_restore_blocks, direct
+    torch.cuda.synchronize()
+    for d, p in zip(dst_ids, payloads):
+        dst_o.write_block(d, p)
+    for d, p in zip(dst_ids[:9][::-1], payloads[:9][::-1]):
+        dst_o.write_block(d, p)
+    assert_pool_equals(dk, dv, dst_o)
+
+
 @pytest.mark.parametrize("blocks,offset", [(72, 0), (16, 4096), (1, 0)],
                          ids=["72MiB-staged", "16MiB-interior", "1MiB"])
 def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, offset):
