@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 17
+#define IEKV_ABI_VERSION 18
 
 enum {
   IEKV_OK = 0,
@@ -200,10 +200,11 @@ int iekv_gather_rows_arrays(const iekv_pool* pool, int32_t first_array, int32_t 
                             int32_t block_size, const int32_t* block_table, int32_t context_len,
                             void* out, int64_t out_bytes, hipStream_t stream);
 
-/* Largest host image iekv_offload and iekv_restore move directly between the
- * pool and pinned host memory (the move kernel reads or writes the host
- * buffer), when the host range lies in one pinned allocation mapped for the
- * device; larger images and pageable memory go through the staging buffer. */
+/* Largest host image iekv_offload moves directly from the pool into pinned
+ * host memory (the pack kernel writes the host buffer), when the host range
+ * lies in one pinned allocation mapped for the device; larger images and
+ * pageable memory go through the staging buffer. Restores read pinned images
+ * directly at any size, in launches of at most this many bytes of images. */
 #define IEKV_HOST_DIRECT_MAX_BYTES (64LL << 20)
 
 /* Offload to host: pack the blocks chunk by chunk into the device staging
@@ -248,13 +249,16 @@ int iekv_offload_static(const iekv_pool* src, const int32_t* src_ids, int32_t n_
                         void* host_dst, int64_t host_bytes, hipStream_t compute,
                         hipStream_t copy);
 
-/* Restore from host: hipMemcpyAsync chunk k of host_src into a staging slot on
- * `copy` while `compute` unpacks chunk k-1, then unpack onto dst_ids. An image
- * of at most IEKV_HOST_DIRECT_MAX_BYTES whose host range lies in one pinned
- * allocation mapped for the device skips the staging buffer: the unpack kernel
- * reads host_src itself, on `compute`. On return `copy` is ordered after the last unpack, so
- * the staging buffer and host_src may be reused by later work on either
- * stream.
+/* Restore from host onto dst_ids. An image whose host range lies in one pinned
+ * allocation mapped for the device, of any size, is read by the unpack kernel
+ * itself on `compute`, in launches of at most IEKV_HOST_DIRECT_MAX_BYTES of
+ * images: measured on MI355X this held 52-57 GB/s in every state of the box,
+ * where runtime copies of the same images ran at 28-56 GB/s. Otherwise (pageable
+ * memory) chunk k of host_src is copied into a staging slot with hipMemcpyAsync
+ * on `copy` while `compute` unpacks chunk k-1. A staging buffer of at least one
+ * block image is required either way. On return `copy` is ordered after the last
+ * unpack, so the staging buffer and host_src may be reused by later work on
+ * either stream.
  * Replaces: the restore write of a tier hit, `copier.write_block(block.id,
  * entry[1])` (ie/core/block_manager.py:159-162), batched over many blocks. */
 int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
@@ -267,12 +271,12 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
 
 /* Restore from scattered host images: like iekv_restore, but block i's image
  * ([2L][T] bytes) is read from host_blocks[i], a HOST array of n_blocks host
- * addresses (pinned memory for the copies to be asynchronous). Images that are
- * adjacent in host memory, within one allocation, are copied together. Up to
- * IEKV_INLINE_IMAGES images of at most IEKV_HOST_DIRECT_MAX_BYTES in all, each
- * in pinned host memory mapped for the device, are instead read by one unpack
- * launch directly, on `compute`. On return `copy` is ordered after the last
- * unpack, as for iekv_restore.
+ * addresses. When every image lies in pinned host memory mapped for the device,
+ * the unpack kernel reads them itself on `compute`, up to IEKV_INLINE_IMAGES
+ * images and IEKV_HOST_DIRECT_MAX_BYTES per launch, their addresses in the
+ * kernel arguments. Otherwise they go through the staging buffer, and images
+ * that are adjacent in host memory within one allocation are copied together.
+ * On return `copy` is ordered after the last unpack, as for iekv_restore.
  * Replaces: the restore loop of a prefix plan's tier hits,
  * `for key in offloaded: ... copier.write_block(block.id, payload)`
  * (ie/core/block_manager.py:159-167), whose payloads the tier took one by one

@@ -1370,8 +1370,24 @@ int static_staging(int device, const StaticStaging** out) {
   return IEKV_OK;
 }
 
+// `copy` ordered after the work enqueued so far on `compute` (the end state of
+// every restore: the staging buffer and the host images may then be reused on
+// either stream).
+int order_copy_after(hipStream_t compute, hipStream_t copy) {
+  if (copy == compute) return IEKV_OK;
+  int rc;
+  Events done;
+  if ((rc = done.create(1))) return rc;
+  IEKV_HIP(hipEventRecord(done[0], compute));
+  IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
+  return IEKV_OK;
+}
+
 // iekv_restore / iekv_restore_ids after their id checks: one contiguous host
-// image of n_blocks block images onto dst_ids.
+// image of n_blocks block images onto dst_ids. An image in one pinned,
+// device-mapped allocation is read by the unpack kernel itself, whatever its
+// size, in launches of at most kZeroCopyMaxBytes of images; pageable or
+// unknown memory goes through the staged pipeline.
 int restore_image(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks, const void* host_src,
                   int64_t host_bytes, void* staging, int64_t staging_bytes, hipStream_t compute,
                   hipStream_t copy) {
@@ -1380,23 +1396,24 @@ int restore_image(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks, const 
   if (need < 0) return set_error(IEKV_ERR_INVALID, "host image size overflows");
   if ((rc = check_buffer(host_src, host_bytes, need, "host"))) return rc;
   const int64_t block_bytes = image_bytes(dst, 1);
-  if (n_blocks > 0 && need <= kZeroCopyMaxBytes) {
+  if (n_blocks > 0) {
     if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
     DeviceGuard guard(dst->device);
     if (!guard.ok()) return guard.fail();
     if (const char* mapped = device_view_of_host(host_src, need)) {
-      const int zc_align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
-      if ((rc = launch_list<false, true>(dst, mapped, nullptr, dst_ids, n_blocks, zc_align,
-                                         compute, host_read_chunk(dst->tile_bytes))))
-        return rc;
-      // As after the staged pipeline, `copy` is ordered after the last unpack.
-      if (copy != compute) {
-        Events done;
-        if ((rc = done.create(1))) return rc;
-        IEKV_HIP(hipEventRecord(done[0], compute));
-        IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
+      const int32_t per = static_cast<int32_t>(
+          std::max<int64_t>(1, std::min<int64_t>(n_blocks, kZeroCopyMaxBytes / block_bytes)));
+      const int32_t chunk = host_read_chunk(dst->tile_bytes);
+      for (int32_t first = 0; first < n_blocks; first += per) {
+        const int32_t cnt = std::min(per, n_blocks - first);
+        const char* piece = mapped + first * block_bytes;
+        const int zc_align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(piece)));
+        if ((rc = launch_list<false, true>(dst, piece, nullptr, dst_ids.from(first), cnt,
+                                           zc_align, compute, chunk)))
+          return rc;
       }
-      return IEKV_OK;
+      // As after the staged pipeline, `copy` is ordered after the last unpack.
+      return order_copy_after(compute, copy);
     }
   }
   const char* host = static_cast<const char*>(host_src);
@@ -1456,7 +1473,10 @@ int offload_images(const iekv_pool* src, IdList src_ids, int32_t n_blocks,
 }
 
 // iekv_restore_blocks / iekv_restore_blocks_ids after their id checks: block
-// image i at host_blocks[i] onto dst_ids[i].
+// image i at host_blocks[i] onto dst_ids[i]. When every image lies in a pinned,
+// device-mapped allocation, the unpack kernel reads them itself, in launches
+// of at most IEKV_INLINE_IMAGES images and kZeroCopyMaxBytes (their addresses
+// in the kernel arguments); otherwise the staged pipeline copies them.
 int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
                    const void* const* host_blocks, void* staging, int64_t staging_bytes,
                    hipStream_t compute, hipStream_t copy) {
@@ -1466,26 +1486,32 @@ int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
   for (int32_t i = 0; i < n_blocks; ++i)
     if (!host_blocks[i]) return set_error(IEKV_ERR_INVALID, "host block %d address is null", i);
   const int64_t block_bytes = image_bytes(dst, 1);
-  if (n_blocks > 0 && n_blocks <= IEKV_INLINE_IMAGES &&
-      block_bytes * n_blocks <= kZeroCopyMaxBytes) {
+  if (n_blocks > 0) {
     if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
     DeviceGuard guard(dst->device);
     if (!guard.ok()) return guard.fail();
-    InlineImages images{};
-    if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
-      const int32_t* device_ids = dst_ids.on_host ? nullptr : dst_ids.ids;
-      if (dst_ids.on_host) std::copy(dst_ids.ids, dst_ids.ids + n_blocks, images.ids);
-      if ((rc = launch_images<false, true>(dst, images, device_ids, n_blocks, compute,
-                                           host_read_chunk(dst->tile_bytes))))
-        return rc;
-      // As after the staged pipeline, `copy` is ordered after the last unpack.
-      if (copy != compute) {
-        Events done;
-        if ((rc = done.create(1))) return rc;
-        IEKV_HIP(hipEventRecord(done[0], compute));
-        IEKV_HIP(hipStreamWaitEvent(copy, done[0], 0));
+    const int32_t per = static_cast<int32_t>(std::max<int64_t>(
+        1, std::min<int64_t>(IEKV_INLINE_IMAGES, kZeroCopyMaxBytes / block_bytes)));
+    // Every image's device address first: the call goes direct only if all of them
+    // have one, so it never mixes the two paths.
+    std::vector<uint64_t> views(n_blocks);
+    bool direct = true;
+    for (int32_t first = 0; direct && first < n_blocks; first += per)
+      direct = device_views_of_images(host_blocks + first, std::min(per, n_blocks - first),
+                                      block_bytes, views.data() + first);
+    if (direct) {
+      const int32_t chunk = host_read_chunk(dst->tile_bytes);
+      for (int32_t first = 0; first < n_blocks; first += per) {
+        const int32_t cnt = std::min(per, n_blocks - first);
+        InlineImages images{};
+        std::copy(views.begin() + first, views.begin() + first + cnt, images.addr);
+        const int32_t* device_ids = dst_ids.on_host ? nullptr : dst_ids.ids + first;
+        if (dst_ids.on_host) std::copy(dst_ids.ids + first, dst_ids.ids + first + cnt, images.ids);
+        if ((rc = launch_images<false, true>(dst, images, device_ids, cnt, compute, chunk)))
+          return rc;
       }
-      return IEKV_OK;
+      // As after the staged pipeline, `copy` is ordered after the last unpack.
+      return order_copy_after(compute, copy);
     }
   }
   return restore_pipeline(

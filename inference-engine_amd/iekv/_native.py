@@ -12,10 +12,10 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most host ids one launch carries in its arguments
-HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: pinned host images moved without staging
+HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: largest direct offload; restore launch size
 INLINE_IMAGES = 128          # IEKV_INLINE_IMAGES: scattered host images restored in one launch
 STATIC_STAGING = 32 << 20    # IEKV_STATIC_STAGING_BYTES: staging of iekv_offload_static
 

@@ -724,10 +724,10 @@ class HipSlotCopier:
             stream = torch.cuda.current_stream(self.device)
             PackedBlocks.order_after([packed], stream)
             staging = self._host_staging(n)
-            # Small pinned images are read by the unpack kernel itself on the compute
-            # stream (IEKV_HOST_DIRECT_MAX_BYTES); passing that stream as the copy
-            # stream spares the call a cross-stream hand-off it would not use.
-            direct = packed.nbytes <= _native.HOST_DIRECT_MAX and packed.pinned
+            # Pinned images are read by the unpack kernel itself on the compute
+            # stream, whatever their size; passing that stream as the copy stream
+            # spares the call a cross-stream hand-off it would not use.
+            direct = packed.pinned
             copy = stream if direct else self.copy_stream()
             fn, id_ptr = ("iekv_restore_ids", ids.host_pointer()) if ids.inline else \
                 ("iekv_restore", ids.on_device().data_ptr())
@@ -762,8 +762,9 @@ class HipSlotCopier:
                                                 for q, p in zip(packs, chunk)])
             PackedBlocks.order_after(packs, stream)
             staging = self._host_staging(n)
-            # Pinned images are read by one unpack launch on the compute stream
-            # (IEKV_INLINE_IMAGES, IEKV_HOST_DIRECT_MAX_BYTES): no cross-stream hand-off.
+            # Pinned images are read by the unpack kernel itself on the compute
+            # stream (IEKV_INLINE_IMAGES, IEKV_HOST_DIRECT_MAX_BYTES per launch): no
+            # cross-stream hand-off.
             direct = all(q.pinned for q in packs)
             copy = stream if direct else self.copy_stream()
             fn, id_ptr = ("iekv_restore_blocks_ids", part.host_pointer()) if part.inline else \

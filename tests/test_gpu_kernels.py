@@ -579,13 +579,13 @@ def test_direct_host_transfers_of_every_tile_shape(gpu, bs, heads, dim, dtype):
 
 
 @pytest.mark.parametrize("blocks,offset", [(72, 0), (16, 4096), (1, 0)],
-                         ids=["72MiB-staged", "16MiB-interior", "1MiB"])
+                         ids=["72MiB-staged-offload", "16MiB-interior", "1MiB"])
 def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, offset):
     """1 MiB blocks to and from pinned host memory: 72 blocks exceed the 64 MiB
-    limit of the direct (kernel-to-host) path and go through the staged
-    pipelines; 16 blocks at an offset inside a larger pinned buffer, and a
-    single block, go direct. Bytes equal the oracle's on the host and back in
-    the pool."""
+    limit of the direct offload and go through the staged pipeline, and are
+    restored directly in two unpack launches (64 and 8 blocks); 16 blocks at an
+    offset inside a larger pinned buffer, and a single block, go direct both
+    ways. Bytes equal the oracle's on the host and back in the pool."""
     from iekv import _native
     from iekv.engine.pools import KVPool
 
@@ -1101,51 +1101,54 @@ def test_host_payloads_from_unrelated_buffers_restore_in_one_call(gpu, staging_b
     assert dst.blocks_written == 7
 
 
-def test_a_staged_restore_merges_images_only_within_one_allocation(gpu):
-    """The staged scattered restore copies each run of host images that are adjacent
-    inside one pinned allocation with one hipMemcpyAsync, and starts a new copy at
-    every allocation's end (a copy spanning two allocations would read past the end
-    of the one its source pointer belongs to).
+def test_scattered_host_images_are_copied_together_only_within_one_allocation(gpu):
+    """The staged path of the scattered-image calls copies each run of host images
+    that are adjacent inside one pinned allocation with one hipMemcpyAsync, and
+    starts a new copy at every allocation's end (a copy spanning two allocations
+    would run past the end of the one its host pointer belongs to).
 
-    Three host reads of 50 blocks each give three pinned buffers of 50 adjacent
-    images. One iekv_restore_blocks call of all 150 (more than one direct launch
-    takes, so the staged pipeline runs) lists them buffer after buffer, so the list
-    holds runs to merge and, at two places, a step from one allocation's last image
-    to another's first. Where the allocator placed two buffers back to back (on
-    MI355X boxes so far it has left a gap of at least one buffer's size after each
-    pinned allocation), that step is adjacent in memory too, and the run must still
-    end there. A second call interleaves the buffers image by image (no merges).
-    Bytes equal the oracle's."""
+    Three pinned buffers of 50 block images each. One iekv_offload_blocks call of
+    150 blocks (more than one direct launch takes, so the staged pipeline runs)
+    lists their images buffer after buffer: runs to merge and, at two places, a step
+    from one allocation's last image to another's first. Where the allocator placed
+    two buffers back to back (on MI355X boxes so far it has left a gap of at least
+    one buffer's size after each pinned allocation), that step is adjacent in memory
+    too, and the run must still end there. A second offload interleaves the buffers
+    image by image (no merges). Every buffer equals the oracle's images, and one
+    iekv_restore_blocks of all 150 (direct: pinned images) writes the oracle's
+    blocks."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
     bs = 16
     sk, sv = allocate(160, bs, 2, 2, 64, torch.bfloat16, gpu, seed=61)   # 16 KiB images
     dk, dv = allocate(160, bs, 2, 2, 64, torch.bfloat16, gpu, seed=62)
-    src = HipSlotCopier(sk, sv, bs, payload_location="host", defer_reads=False)
-    dst = HipSlotCopier(dk, dv, bs)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
     rng = np.random.default_rng(63)
-    order = [int(b) for b in rng.permutation(160)[:150]]
-    packs = [src.read_blocks(order[i:i + 50]) for i in (0, 50, 100)]
-    torch.cuda.synchronize()
+    shape = (50, src.pool.n_arrays, src.pool.tile_bytes)
+    bufs = [torch.empty(shape, dtype=torch.uint8, pin_memory=True) for _ in range(3)]
+    ends = {b.data_ptr() + b.numel() for b in bufs}
+    print(f"{len(ends & {b.data_ptr() for b in bufs})} pinned buffers start where another "
+          f"ends", flush=True)
     image = src.pool.block_bytes
-    ends = {p.data.data_ptr() + p.nbytes for p in packs}
-    starts = {p.data.data_ptr() for p in packs}
-    print(f"{len(ends & starts)} pinned buffers start where another ends", flush=True)
-    assert all(p.nbytes == 50 * image for p in packs)
     # Two slots of 32 images: both steps between buffers (entries 50 and 100) fall
     # inside a chunk, where the copies of one chunk are planned together.
     staging = torch.empty(64 * image, dtype=torch.uint8, device=gpu)
     stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
     src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
     for layout in ("buffer after buffer", "interleaved"):
-        if layout == "interleaved":
-            picks = [(b, i) for i in range(50) for b in range(3)]
-        else:
-            picks = [(b, i) for b in range(3) for i in range(50)]
-        sources = [order[50 * b + i] for b, i in picks]
+        picks = [(b, i) for i in range(50) for b in range(3)] if layout == "interleaved" \
+            else [(b, i) for b in range(3) for i in range(50)]
+        sources = [int(x) for x in rng.permutation(160)[:150]]
+        addresses = (ctypes.c_void_p * 150)(*[bufs[b].data_ptr() + i * image for b, i in picks])
+        _native.call("iekv_offload_blocks", src.pool.native.handle,
+                     src.pool.block_ids(sources).data_ptr(), 150, addresses, staging.data_ptr(),
+                     staging.numel(), stream.cuda_stream, side.cuda_stream)
+        torch.cuda.synchronize()
+        want = packed_image(pack(src_o, sources))
+        for k, (b, i) in enumerate(picks):
+            assert np.array_equal(bufs[b][i].numpy(), want[k]), (layout, k)
         targets = [int(t) for t in rng.permutation(160)[:150]]
-        addresses = (ctypes.c_void_p * 150)(*[packs[b].data[i].data_ptr() for b, i in picks])
         _native.call("iekv_restore_blocks", dst.pool.native.handle,
                      dst.pool.block_ids(targets).data_ptr(), 150, addresses, staging.data_ptr(),
                      staging.numel(), stream.cuda_stream, side.cuda_stream)
@@ -1157,8 +1160,8 @@ def test_a_staged_restore_merges_images_only_within_one_allocation(gpu):
 
 def test_more_scattered_images_than_one_direct_launch_takes(gpu):
     """130 one-block tier payloads (more than IEKV_INLINE_IMAGES) restore through the
-    copier in two direct calls (128 images, then 2), and through the library's
-    staged pipeline in one call; bytes equal to the oracle's either way."""
+    copier in two direct calls (128 images, then 2), and in one library call, which
+    makes the two launches itself; bytes equal to the oracle's either way."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -1177,7 +1180,7 @@ def test_more_scattered_images_than_one_direct_launch_takes(gpu):
     src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
     handoff(src_o, dst_o, [src_ids], [dst_ids])
     assert_pool_equals(dk, dv, dst_o)
-    # All 130 in one library call: the staged pipeline.
+    # All 130 in one library call: two direct unpack launches inside the library.
     again = [int(b) for b in rng.permutation(140)[:n]]
     addresses = (ctypes.c_void_p * n)(*[p.packed.data[p.index].data_ptr() for p in payloads])
     staging = torch.empty(8 * src.pool.block_bytes, dtype=torch.uint8, device=gpu)
