@@ -328,7 +328,9 @@ int iekv_offload_blocks_ids(const iekv_pool* src, const int32_t* src_ids, int32_
  *   unroll      16-byte accesses in flight per lane per step: 1, 2, 4, 8 or
  *               16 (capped by what a chunk needs); 0 keeps the current setting;
  *   nontemporal 1 for streaming (non-temporal) loads and stores, 0 for
- *               ordinary ones, -1 keeps the current setting;
+ *               ordinary ones, -1 keeps the current setting; a pack that
+ *               writes pinned host memory itself (a direct offload) uses
+ *               ordinary ones for tiles of 16 KiB or more either way;
  *   order       which (array, block) tiles are in flight together in the
  *               launches that write a pool (direct copy, unpack, restore):
  *               0 array-major (the 2L tiles of one block), 1 block-major
