@@ -578,6 +578,49 @@ def test_direct_host_transfers_of_every_tile_shape(gpu, bs, heads, dim, dtype):
     assert_pool_equals(dk, dv, dst_o)
 
 
+def test_pinned_restores_of_any_size_leave_the_staging_buffer_untouched(gpu):
+    """A pinned image is restored by the unpack kernel itself at any size (72 MiB here,
+    above IEKV_HOST_DIRECT_MAX_BYTES: two launches), scattered pinned images too (130,
+    above IEKV_INLINE_IMAGES): the staging buffer keeps its sentinel bytes. A pageable
+    image of the same blocks goes through it. Bytes equal the oracle's each time."""
+    from iekv import _native
+    from iekv.engine.pools import KVPool
+
+    bs, layers, heads, dim = 16, 4, 8, 128     # 1 MiB block images
+    sk, sv = allocate(150, bs, layers, heads, dim, torch.bfloat16, gpu, seed=74)
+    dk, dv = allocate(150, bs, layers, heads, dim, torch.bfloat16, gpu, seed=75)
+    src, dst = KVPool(sk, sv, bs), KVPool(dk, dv, bs)
+    rng = np.random.default_rng(76)
+    block = src.block_bytes
+    staging = torch.full((4 * block,), 0xA5, dtype=torch.uint8, device=gpu)
+    stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    for n, memory, layout in ((72, "pinned", "one image"), (130, "pinned", "scattered"),
+                              (72, "pageable", "one image")):
+        src_ids, dst_ids = random_tables(rng, 150, 150, n)
+        image = torch.from_numpy(packed_image(pack(src_o, src_ids)).reshape(-1).copy())
+        host = image.pin_memory() if memory == "pinned" else image
+        ids = dst.block_ids(dst_ids)
+        if layout == "one image":
+            _native.call("iekv_restore", dst.native.handle, ids.data_ptr(), n, host.data_ptr(),
+                         host.numel(), staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                         side.cuda_stream)
+        else:
+            order = [int(i) for i in rng.permutation(n)]       # images out of order
+            addresses = (ctypes.c_void_p * n)(*[host.data_ptr() + i * block for i in order])
+            ids = dst.block_ids([dst_ids[i] for i in order])
+            _native.call("iekv_restore_blocks", dst.native.handle, ids.data_ptr(), n, addresses,
+                         staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                         side.cuda_stream)
+        side.synchronize()
+        torch.cuda.synchronize()
+        untouched = bool((staging == 0xA5).all())
+        assert untouched == (memory == "pinned"), (n, memory, layout)
+        for d, p in zip(dst_ids, pack(src_o, src_ids)):
+            dst_o.write_block(d, p)
+        assert_pool_equals(dk, dv, dst_o)
+
+
 @pytest.mark.parametrize("blocks,offset", [(72, 0), (16, 4096), (1, 0)],
                          ids=["72MiB-staged-offload", "16MiB-interior", "1MiB"])
 def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, offset):
