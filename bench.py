@@ -52,6 +52,7 @@ bit). ``cpu_baseline`` times the NumPy restatement of the reference handoff
 from __future__ import annotations
 
 import argparse
+import faulthandler
 import json
 import os
 import statistics
@@ -130,6 +131,61 @@ def fill_pool(arrays, dtype_name: str, seed: int) -> None:
             raw.copy_((r + (r >= 0x7F).to(torch.int16)).to(torch.uint8))
         else:
             t.normal_(generator=gen)
+
+
+def host_roundtrip_plan(workload, sample_blocks: int) -> dict:
+    """The pinned host memory the host_roundtrip leg holds, phase by phase.
+
+    The whole-list image is pinned at exactly the payload's size and freed
+    before the tier phase, whose one-block buffers (at most two flush groups'
+    worth beyond the sample, while the previous round's buffers are released)
+    are pinned at exactly one block image each.
+    """
+    P = workload.payload_bytes
+    bb = workload.shape.block_bytes
+    tier = (sample_blocks + 2 * 64) * bb
+    return {"image_bytes": P, "tier_bytes": tier, "peak_pinned_bytes": max(P, tier)}
+
+
+def host_memory_budget() -> int | None:
+    """Bytes of host memory this process can still take: the smaller of the kernel's
+    MemAvailable and the room left under the cgroup's memory limit (None when
+    neither can be read)."""
+    budget = []
+    try:
+        for line in Path("/proc/meminfo").read_text().splitlines():
+            if line.startswith("MemAvailable:"):
+                budget.append(int(line.split()[1]) * 1024)
+    except OSError:
+        pass
+    for limit_file, usage_file in (("/sys/fs/cgroup/memory.max", "/sys/fs/cgroup/memory.current"),
+                                   ("/sys/fs/cgroup/memory/memory.limit_in_bytes",
+                                    "/sys/fs/cgroup/memory/memory.usage_in_bytes")):
+        try:
+            limit = Path(limit_file).read_text().strip()
+            usage = int(Path(usage_file).read_text().strip())
+        except (OSError, ValueError):
+            continue
+        if limit.isdigit() and int(limit) < (1 << 60):
+            budget.append(int(limit) - usage)
+        break
+    return min(budget) if budget else None
+
+
+# Host memory the leg leaves to the rest of the process (Python, torch, the HIP
+# runtime's own buffers) on top of what it pins.
+HOST_MARGIN_BYTES = 8 << 30
+
+
+def check_host_budget(plan: dict, budget: int | None) -> None:
+    """Raise a clear error when the leg's pinned peak plus a margin exceeds the host
+    memory available, instead of pinning into a host that cannot hold it."""
+    need = plan["peak_pinned_bytes"] + HOST_MARGIN_BYTES
+    if budget is not None and need > budget:
+        raise RuntimeError(
+            f"host_roundtrip needs {need / 1e9:.1f} GB of host memory "
+            f"({plan['peak_pinned_bytes'] / 1e9:.1f} GB pinned + "
+            f"{HOST_MARGIN_BYTES / 1e9:.1f} GB margin); {budget / 1e9:.1f} GB is available")
 
 
 class Legs:
@@ -483,23 +539,36 @@ class Legs:
 
         One iekv_offload over the whole block list (pack on the compute stream
         overlapping device-to-host copies on a side stream), then one iekv_restore
-        (host-to-device copies overlapping the unpack). Both are bounded by the
-        host link, not HBM. Then, on a sample, the same pipelines called once per
-        block (the reference's pattern), and the drop-in tier path (_tier_roundtrip).
+        (the unpack kernel reading the pinned image). Both are bounded by the host
+        link, not HBM. Then, on a sample, the same calls once per block (the
+        reference's pattern), and the drop-in tier path (_tier_roundtrip). The host
+        image is pinned at exactly its size (iekv_host_alloc) and freed before the
+        tier runs; the leg refuses to start when the host cannot hold what it pins
+        (host_roundtrip_plan). Every phase logs a line as it starts.
         """
         from iekv import _native
         from iekv.engine.copier import HOST_STAGING_BYTES
+        from iekv.engine.pools import pinned_empty, release_pinned
 
         torch = self.torch
         P = self.w.payload_bytes
+        n = self.src_all.numel()
+        k = min(n, 1024)
+        plan = host_roundtrip_plan(self.w, k)
+        check_host_budget(plan, host_memory_budget())
+
+        def phase(msg: str) -> None:
+            log(f"[bench] host_roundtrip: {msg}")
+
+        phase(f"pinning {P / 1e9:.2f} GB (exactly the image; peak pinned "
+              f"{plan['peak_pinned_bytes'] / 1e9:.2f} GB)")
         t0 = time.perf_counter()
-        host = torch.empty(P, dtype=torch.uint8, pin_memory=True)
+        host = pinned_empty(P)
         pin_s = time.perf_counter() - t0
         staging = torch.empty(2 * HOST_STAGING_BYTES, dtype=torch.uint8,
                               device=self.src_k[0].device)
         side = torch.cuda.Stream(self.src_k[0].device)
         h = self.stream.cuda_stream
-        n = self.src_all.numel()
 
         def offload():
             _native.call("iekv_offload", self.src.native.handle, self.src_all.data_ptr(), n,
@@ -511,6 +580,7 @@ class Legs:
                          host.data_ptr(), P, staging.data_ptr(), staging.numel(), h,
                          side.cuda_stream)
 
+        phase(f"whole-list offload and restore, {warmup} warm-up and {steps} timed")
         for _ in range(warmup):
             offload()
             restore()
@@ -522,14 +592,13 @@ class Legs:
             offload()
             b.record(self.stream)     # the compute stream waits for the last copy
             restore()
-            c.record(self.stream)     # after the last unpack, which waited on its copy
+            c.record(self.stream)     # after the last unpack
             torch.cuda.synchronize()
             d2h.append(a.elapsed_time(b))
             h2d.append(b.elapsed_time(c))
-        # The same pipelines called once per block, as the reference offloads one
-        # block per eviction and restores one per tier hit (ie/core/block_manager.py:82,
+        # The same calls once per block, as the reference offloads one block per
+        # eviction and restores one per tier hit (ie/core/block_manager.py:82,
         # 159-162), on a bounded sample of the blocks.
-        k = min(n, 1024)
         bb = self.w.shape.block_bytes
 
         def offload_each():
@@ -538,17 +607,15 @@ class Legs:
                              self.src_all[i:].data_ptr(), 1, host.data_ptr() + i * bb, bb,
                              staging.data_ptr(), staging.numel(), h, side.cuda_stream)
 
-        # As HipSlotCopier does, a block small enough to be read by the unpack kernel
-        # itself (IEKV_HOST_DIRECT_MAX_BYTES) is restored with the compute stream as
-        # the copy stream.
-        copy_each = h if bb <= _native.HOST_DIRECT_MAX else side.cuda_stream
-
+        # As HipSlotCopier does, a pinned image is restored with the compute stream
+        # as the copy stream (the unpack kernel reads it itself).
         def restore_each():
             for i in range(k):
                 _native.call("iekv_restore", self.dst.native.handle,
                              self.dst_all[i:].data_ptr(), 1, host.data_ptr() + i * bb, bb,
-                             staging.data_ptr(), staging.numel(), h, copy_each)
+                             staging.data_ptr(), staging.numel(), h, h)
 
+        phase(f"one call per block on {k} blocks")
         offload_each()
         restore_each()
         torch.cuda.synchronize()
@@ -561,11 +628,12 @@ class Legs:
         torch.cuda.synchronize()
         each_d2h, each_h2d = a.elapsed_time(b), b.elapsed_time(c)
         del host
-        torch.cuda.synchronize()
-        torch._C._host_emptyCache()   # give the whole-list image's pinned memory back first
-        tier = self._tier_roundtrip(k)
+        freed = release_pinned()
+        phase(f"host image released ({freed / 1e9:.2f} GB)")
+        tier = self._tier_roundtrip(k, phase)
         d2h_ms, h2d_ms = statistics.median(d2h), statistics.median(h2d)
         out = {"pinned_GB": round(P / 1e9, 2), "pin_alloc_s": round(pin_s, 2),
+               "peak_pinned_GB": round(plan["peak_pinned_bytes"] / 1e9, 2),
                "d2h_ms": round(d2h_ms, 2), "h2d_ms": round(h2d_ms, 2),
                "d2h_GBps": round(P / (d2h_ms * 1e-3) / 1e9, 2),
                "h2d_GBps": round(P / (h2d_ms * 1e-3) / 1e9, 2),
@@ -587,7 +655,7 @@ class Legs:
             f"H2D {tier['h2d_GBps']} GB/s")
         return out
 
-    def _tier_roundtrip(self, k: int, per_flush: int = 64) -> dict:
+    def _tier_roundtrip(self, k: int, phase, per_flush: int = 64) -> dict:
         """The same k blocks through the drop-in tier path, as the engine moves them.
 
         A host-payload HipSlotCopier queues ``per_flush`` evictions (read_block, the
@@ -597,6 +665,7 @@ class Legs:
         per call. Times are wall-clock to completion, host work included.
         """
         from iekv.engine.copier import HipSlotCopier
+        from iekv.engine.pools import release_pinned
 
         torch = self.torch
         bs, bb = self.w.shape.block_size, self.w.shape.block_bytes
@@ -616,18 +685,23 @@ class Legs:
             for g in range(0, k, per_flush):
                 dst.write_blocks(dst_ids[g:g + per_flush], payloads[g:g + per_flush])
 
+        phase(f"tier warm-up: {k} evictions, {per_flush} per flush, then their restores")
         restore(offload())                      # warm-up: pinned buffers, kernels
         torch.cuda.synchronize()
+        phase("tier offload (timed)")
         t0 = time.perf_counter()
         payloads = offload()
         t1 = time.perf_counter()
         torch.cuda.synchronize()
         t2 = time.perf_counter()
+        phase("tier restore (timed)")
         restore(payloads)
         t3 = time.perf_counter()
         torch.cuda.synchronize()
         t4 = time.perf_counter()
         del payloads
+        freed = release_pinned()
+        phase(f"tier buffers released ({freed / 1e9:.2f} GB)")
         return {"blocks": k, "block_bytes": bb, "evictions_per_flush": per_flush,
                 "d2h_GBps": round(k * bb / (t2 - t0) / 1e9, 2),
                 "h2d_GBps": round(k * bb / (t4 - t2) / 1e9, 2),
@@ -1078,18 +1152,13 @@ def main() -> int:
                     help="allocate the two pools separately instead of as one reservation "
                          "(prefill pool first)")
     args = ap.parse_args()
+    # A fatal signal prints every thread's Python stack before the process ends.
+    faulthandler.enable()
 
     names = [x for x in args.legs.split(",") if x]
     if not args.sweep and not any(x in HANDOFF_LEGS for x in names):
         print(f"--legs needs one handoff leg ({', '.join(HANDOFF_LEGS)}) for the line's value",
               file=sys.stderr)
-        return 2
-    if "host_roundtrip" in names and args.config == "cfg5":
-        # A run of this leg on cfg5 (43 GB pinned image, 2.5 MiB blocks) ended with a
-        # segmentation fault of the process; its cause has not been found, so the
-        # leg does not run there.
-        print("host_roundtrip is not run on cfg5: an earlier run of it there ended with a "
-              "segmentation fault whose cause is not yet found", file=sys.stderr)
         return 2
     if args.ab and not ab_ok(args.ab, args.config):
         print("--ab takes streams=N,... (N in 1..8), a launch setting ("

@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 18
+#define IEKV_ABI_VERSION 19
 
 enum {
   IEKV_OK = 0,
@@ -143,7 +143,9 @@ int iekv_copy_direct_requests(const iekv_pool* src, const iekv_pool* dst, int32_
  * run_blocks. The ids are checked on the host before anything
  * is enqueued: an id outside its pool returns IEKV_ERR_RANGE; a destination id
  * given twice (iekv_copy_direct_ids, iekv_unpack_ids), or a copy within one pool
- * whose sources overlap its destinations, returns IEKV_ERR_IDS. iekv_copy_direct_ids
+ * whose sources overlap its destinations, returns IEKV_ERR_IDS ("one pool": two
+ * handles over the same arrays count as one; a source and a destination pool
+ * that overlap in memory otherwise return IEKV_ERR_INVALID). iekv_copy_direct_ids
  * issues its (src, dst) pairs in ascending destination order (the pairs are
  * independent; neighbouring destination tiles are then written together).
  * Replace: the same reference lines as iekv_copy_direct, iekv_pack and
@@ -215,7 +217,9 @@ int iekv_gather_rows_arrays(const iekv_pool* pool, int32_t first_array, int32_t 
  * pinned host memory for the copies to be asynchronous. An image of at most
  * IEKV_HOST_DIRECT_MAX_BYTES whose host range lies in one pinned allocation
  * mapped for the device skips the staging buffer: the pack kernel writes
- * host_dst itself, on `compute`. On return `compute` is ordered after every copy (so the staging
+ * host_dst itself, on `compute`, and `staging` may then be null (a staged
+ * offload needs at least one block image of it, IEKV_ERR_CAPACITY otherwise).
+ * On return `compute` is ordered after every copy (so the staging
  * buffer and host_dst are free / complete once `compute` reaches that point).
  * `copy` may equal `compute`.
  * Replaces: the payload read of the offload hook,
@@ -236,11 +240,14 @@ int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
  * first call on a device sets that device's buffer address and events up.
  * A block image (2L * T bytes) larger than IEKV_STATIC_STAGING_BYTES is
  * rejected with IEKV_ERR_CAPACITY before anything is enqueued. Every call on
- * one device shares that device's buffer and events: calls that overlap on
- * one device (other host threads, or streams not ordered after the previous
- * call's `compute`) race. The buffer keeps the last call's bytes; nothing in
- * it needs to start at zero. Streams, host image and ordering on return as
- * for iekv_offload.
+ * one device shares that device's buffer and events. Calls are enqueued one at
+ * a time (a lock is held while a call enqueues its work, so calls from several
+ * host threads wait for each other), and a call that uses the buffer makes its
+ * `compute` stream wait for the previous such call's last device-to-host copy:
+ * calls on unrelated streams, or from other threads, never overwrite a slot
+ * an earlier call still copies from. The buffer keeps the last call's bytes;
+ * nothing in it needs to start at zero. Streams, host image and ordering on
+ * return as for iekv_offload.
  * No counterpart in the reference: an entry point for callers that cannot
  * allocate device memory or call allocating routines (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc); it runs the
@@ -255,8 +262,9 @@ int iekv_offload_static(const iekv_pool* src, const int32_t* src_ids, int32_t n_
  * images: measured on MI355X this held 52-57 GB/s in every state of the box,
  * where runtime copies of the same images ran at 28-56 GB/s. Otherwise (pageable
  * memory) chunk k of host_src is copied into a staging slot with hipMemcpyAsync
- * on `copy` while `compute` unpacks chunk k-1. A staging buffer of at least one
- * block image is required either way. On return `copy` is ordered after the last
+ * on `copy` while `compute` unpacks chunk k-1; that path needs a staging buffer
+ * of at least one block image (IEKV_ERR_CAPACITY otherwise), the direct one none
+ * (`staging` may be null). On return `copy` is ordered after the last
  * unpack, so the staging buffer and host_src may be reused by later work on
  * either stream.
  * Replaces: the restore write of a tier hit, `copier.write_block(block.id,
@@ -274,8 +282,9 @@ int iekv_restore(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_blocks,
  * addresses. When every image lies in pinned host memory mapped for the device,
  * the unpack kernel reads them itself on `compute`, up to IEKV_INLINE_IMAGES
  * images and IEKV_HOST_DIRECT_MAX_BYTES per launch, their addresses in the
- * kernel arguments. Otherwise they go through the staging buffer, and images
- * that are adjacent in host memory within one allocation are copied together.
+ * kernel arguments, and `staging` may be null. Otherwise they go through the
+ * staging buffer (at least one block image), and images that are adjacent in
+ * host memory within one allocation are copied together.
  * On return `copy` is ordered after the last unpack, as for iekv_restore.
  * Replaces: the restore loop of a prefix plan's tier hits,
  * `for key in offloaded: ... copier.write_block(block.id, payload)`
@@ -290,9 +299,10 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
  * addresses), so each image can live in its own allocation and be freed on its
  * own. Up to IEKV_INLINE_IMAGES pinned images of at most
  * IEKV_HOST_DIRECT_MAX_BYTES together are written by one pack launch on
- * `compute`, the addresses in its kernel arguments; otherwise chunks are packed
- * into `staging` and copied to the host on `copy` (one hipMemcpyAsync per run
- * of images adjacent within one allocation), as iekv_offload does.
+ * `compute`, the addresses in its kernel arguments, and `staging` may be null;
+ * otherwise chunks are packed into `staging` (at least one block image) and
+ * copied to the host on `copy` (one hipMemcpyAsync per run of images adjacent
+ * within one allocation), as iekv_offload does.
  * Replaces: the same payload reads as iekv_offload
  * (`copier.read_block(id)` in the offload hook, ie/core/block_manager.py:82),
  * for a tier that keeps each block's payload on its own. */
@@ -321,6 +331,27 @@ int iekv_restore_blocks_ids(const iekv_pool* dst, const int32_t* dst_ids, int32_
 int iekv_offload_blocks_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
                             void* const* host_blocks, void* staging, int64_t staging_bytes,
                             hipStream_t compute, hipStream_t copy);
+
+/* Pinned host memory of exactly `bytes` bytes, mapped for every GPU
+ * (hipHostMalloc), for host images the calls above read or write directly:
+ * *out receives its address, or null with IEKV_ERR_HIP and the runtime's
+ * message when the memory cannot be had. iekv_host_free returns it (null is a
+ * no-op); no copy may still use it then. Allocators that round requests up (a
+ * caching allocator rounding to powers of two pins 4 MiB for a 2.5 MiB block
+ * image, 64 GiB for a 43 GB one) pin up to twice what the images need.
+ * Replaces: the host arrays the reference's payloads and tier entries live in
+ * (`.copy()` of each tile, ie/engine/copier.py:21-22; KVTier entries,
+ * ie/core/offload.py:26-69), page-locked so the GPU reaches them. */
+int iekv_host_alloc(int64_t bytes, void** out);
+int iekv_host_free(void* ptr);
+
+/* Launch floor, for measurement: `launches` launches of an empty kernel of
+ * `workgroups` workgroups of 256 lanes on `stream`, dispatched as the move
+ * kernels are (timed by iekv_profile_start like them). The in-dispatch time
+ * of one launch is what any launch costs before it moves a byte; the host time
+ * of the call over `launches` is the host's cost of issuing one.
+ * No reference counterpart: a measurement aid. */
+int iekv_noop(int32_t workgroups, int32_t launches, hipStream_t stream);
 
 /* Launch shape of the move kernels (process-wide):
  *   run_blocks  blocks per workgroup run, 1..64; 0 = automatic (currently one
@@ -395,7 +426,9 @@ int iekv_profile_stop(float* durations_ms, int32_t capacity, int32_t* count);
  * one pool). `workspace` is device memory of at least
  * IEKV_CHECK_WORKSPACE_BYTES(dst->num_blocks) bytes (none without dst);
  * `status` is one device int32, overwritten with the IEKV_IDS_* bits of the
- * failed checks. Two or three small launches on `stream`, no host
+ * failed checks. Pools are compared by the memory they describe: two handles
+ * over the same arrays count as one pool, and pools whose arrays overlap
+ * otherwise are refused (IEKV_ERR_INVALID). Two or three small launches on `stream`, no host
  * synchronisation: the caller reads *status after the stream has passed them
  * (and may skip the move, or read it after the move, to report). The launches
  * are not timed by iekv_profile_start. Calls that share a workspace or status

@@ -45,6 +45,7 @@ struct iekv_pool {
   int64_t stride;
   uint64_t* table;  // table mode: device copy of the n_arrays base addresses (else null)
   int32_t align;    // largest power of two <= 16 dividing tile_bytes and every base address
+  std::vector<uint64_t> arrays;   // the n_arrays base addresses (host copy)
 };
 
 // Staging buffer of iekv_offload_static, the allocation-free offload: every
@@ -660,6 +661,10 @@ ids_probe(const int32_t* __restrict__ ids, int32_t n, int64_t num_blocks,
   if (bitmap && (bitmap[id >> 5] >> (id & 31)) & 1u) atomicOr(status, IEKV_IDS_OVERLAP);
 }
 
+// The launch floor (iekv_noop): a kernel that does nothing, so its duration is
+// the cost of dispatching, running and retiring its workgroups alone.
+__global__ void __launch_bounds__(kThreads) kv_noop() {}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -923,6 +928,38 @@ int check_pool(const iekv_pool* p, const char* what) {
   return IEKV_OK;
 }
 
+// How two pool handles share memory: kSeparate (no byte in common), kSamePool
+// (one set of arrays described twice, or one handle), or kPartial (arrays that
+// overlap without being the same arrays, where block ids of one pool say
+// nothing about the other's). Handles are compared by the memory they describe,
+// not by identity, so two handles made over one cache count as one pool.
+enum Aliasing { kSeparate = 0, kSamePool = 1, kPartial = 2 };
+
+Aliasing pool_aliasing(const iekv_pool* a, const iekv_pool* b) {
+  if (a == b) return kSamePool;
+  if (a->device != b->device) return kSeparate;
+  if (a->arrays == b->arrays && a->tile_bytes == b->tile_bytes &&
+      a->num_blocks == b->num_blocks)
+    return kSamePool;
+  std::vector<iekv_plan::Span> spans;
+  spans.reserve(a->arrays.size() + b->arrays.size());
+  for (const iekv_pool* p : {a, b})
+    for (uint64_t base : p->arrays)
+      spans.push_back({base, base + static_cast<uint64_t>(p->num_blocks * p->tile_bytes),
+                       p == a ? 0 : 1});
+  return iekv_plan::spans_cross(spans) ? kPartial : kSeparate;
+}
+
+// The aliasing of a move's source and destination pools, with kPartial refused.
+int check_aliasing(const iekv_pool* src, const iekv_pool* dst, bool* same_pool) {
+  const Aliasing al = pool_aliasing(src, dst);
+  if (al == kPartial)
+    return set_error(IEKV_ERR_INVALID, "the source and destination pools overlap in memory "
+                     "without being the same pool");
+  *same_pool = al == kSamePool;
+  return IEKV_OK;
+}
+
 int check_ids(const int32_t* ids, int32_t n_blocks, const char* what) {
   if (n_blocks < 0) return set_error(IEKV_ERR_INVALID, "n_blocks is negative (%d)", n_blocks);
   if (n_blocks > 0 && !ids) return set_error(IEKV_ERR_INVALID, "%s ids are null", what);
@@ -1003,43 +1040,42 @@ int32_t host_write_nontemporal(int64_t tile_bytes) {
   return tile_bytes >= kHostWriteTemporalTile ? 0 : -1;
 }
 
-// The device address of the host range [p, p + bytes) when it lies in one
-// pinned allocation mapped for the device (HIP gives a pinned host pointer's
-// device address through hipPointerGetAttributes), else nullptr: pageable or
-// unknown memory, or a range running past its allocation. Failed lookups are
-// cleared from HIP's last error.
-char* device_view_of_host(const void* p, int64_t bytes) {
+// What HIP reports for the host allocation holding address p (iekv_plan::HostSpan):
+// pinned and mapped for the device (hipPointerGetAttributes gives a pinned host
+// pointer's device address), the bytes from p to the allocation's end
+// (hipMemGetAddressRange), and device minus host address. Failed lookups are
+// cleared from HIP's last error and report unmapped memory.
+iekv_plan::HostSpan host_span(uint64_t p) {
+  iekv_plan::HostSpan span;
+  const void* ptr = reinterpret_cast<const void*>(p);
   hipPointerAttribute_t attr{};
-  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess) {
     (void)hipGetLastError();
-    return nullptr;
+    return span;
   }
-  if (attr.type != hipMemoryTypeHost || !attr.devicePointer || !attr.hostPointer) return nullptr;
-  if (bytes_to_allocation_end(static_cast<const char*>(p)) < bytes) return nullptr;
-  return static_cast<char*>(attr.devicePointer) +
-         (static_cast<const char*>(p) - static_cast<const char*>(attr.hostPointer));
+  if (attr.type != hipMemoryTypeHost || !attr.devicePointer || !attr.hostPointer) return span;
+  span.room = bytes_to_allocation_end(static_cast<const char*>(ptr));
+  span.shift = static_cast<int64_t>(reinterpret_cast<uint64_t>(attr.devicePointer) -
+                                    reinterpret_cast<uint64_t>(attr.hostPointer));
+  span.mapped = span.room > 0;
+  return span;
+}
+
+// The device address of the host range [p, p + bytes) when it lies in one
+// pinned allocation mapped for the device, else nullptr: pageable or unknown
+// memory, or a range running past its allocation.
+char* device_view_of_host(const void* p, int64_t bytes) {
+  uint64_t view = 0;
+  if (!iekv_plan::image_views(&p, 1, bytes, host_span, &view)) return nullptr;
+  return reinterpret_cast<char*>(view);
 }
 
 // Device addresses of n host images of `bytes` each, when every one lies in a
-// pinned allocation mapped for the device (one lookup per allocation: an
-// image inside the range of the previous lookup reuses it). False otherwise.
+// pinned allocation mapped for the device (iekv_plan::image_views: one lookup
+// per allocation). False otherwise.
 bool device_views_of_images(const void* const* images, int32_t n, int64_t bytes,
                             uint64_t* out) {
-  const char* lo = nullptr;
-  const char* hi = nullptr;
-  int64_t shift = 0;
-  for (int32_t i = 0; i < n; ++i) {
-    const char* p = static_cast<const char*>(images[i]);
-    if (!(lo && p >= lo && p + bytes <= hi)) {
-      char* view = device_view_of_host(p, bytes);
-      if (!view) return false;
-      lo = p;
-      hi = p + bytes_to_allocation_end(p);
-      shift = view - p;
-    }
-    out[i] = reinterpret_cast<uint64_t>(p + shift);
-  }
-  return true;
+  return iekv_plan::image_views(images, n, bytes, host_span, out);
 }
 
 // A small set of events that lives for one pipeline call.
@@ -1070,14 +1106,6 @@ bool valid_order(int32_t order) {
 bool valid_chunk(int32_t chunk_bytes) {
   if (chunk_bytes == -1 || chunk_bytes == 0) return true;
   return chunk_bytes >= 64 && chunk_bytes <= (1 << 20) && !(chunk_bytes & (chunk_bytes - 1));
-}
-
-// Staging slots for a pipeline: two when the buffer holds two blocks or more.
-void plan_slots(int64_t staging_bytes, int64_t block_bytes, int32_t n_blocks, int* n_slots,
-                int64_t* slot_blocks) {
-  int64_t fit = staging_bytes / block_bytes;
-  *n_slots = fit >= 2 ? 2 : 1;
-  *slot_blocks = std::min<int64_t>(fit / *n_slots, n_blocks);
 }
 
 // IEKV_ERR_RANGE unless each of the n host ids lies in [0, num_blocks).
@@ -1218,7 +1246,8 @@ int restore_pipeline(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
 
   int n_slots;
   int64_t slot_blocks;
-  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
+  if (!iekv_plan::plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks))
+    return set_error(IEKV_ERR_CAPACITY, "staging buffer holds no block image");
   const int align =
       std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
   Events loaded, unpacked, fence;
@@ -1253,11 +1282,17 @@ int restore_pipeline(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
 
 // Events of one offload pipeline call: per staging slot, "packed" (recorded on
 // the compute stream after the slot's pack) and "copied" (on the copy stream
-// after its device-to-host copy), plus the entry fence.
+// after its device-to-host copy), plus the entry fence. `last` is the slot
+// whose "copied" event the previous call through these events recorded last
+// (-1 before the first): a call that shares the staging buffer with earlier
+// calls makes its compute stream wait on it, so its packs never overwrite a
+// slot an earlier call's device-to-host copy still reads, whatever streams the
+// two calls run on.
 struct OffloadEvents {
   hipEvent_t packed[2];
   hipEvent_t copied[2];
   hipEvent_t fence;
+  int last = -1;
 };
 
 // Arguments of an offload, checked before anything touches the GPU; *need is
@@ -1276,16 +1311,19 @@ int check_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks
 // current: chunk k is packed into a staging slot on `compute` while `copy`
 // moves chunk k-1 to the host with store(slot, first, count) (two slots when
 // the staging holds two blocks or more, else one). `preset` gives the events
-// to use; without it the call creates its own.
+// to use, and is ordered after the previous call that used them (its `last`
+// is updated); without it the call creates its own.
 template <typename Store>
 int offload_pipeline(const iekv_pool* src, IdList src_ids, int32_t n_blocks, char* staging,
                      int64_t staging_bytes, hipStream_t compute, hipStream_t copy,
-                     const OffloadEvents* preset, Store store) {
+                     OffloadEvents* preset, Store store) {
   int rc;
   const int64_t block_bytes = image_bytes(src, 1);
+  if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
   int n_slots;
   int64_t slot_blocks;
-  plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks);
+  if (!iekv_plan::plan_slots(staging_bytes, block_bytes, n_blocks, &n_slots, &slot_blocks))
+    return set_error(IEKV_ERR_CAPACITY, "staging buffer holds no block image");
   const int align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(staging)));
   Events own;
   OffloadEvents ev{};
@@ -1300,6 +1338,10 @@ int offload_pipeline(const iekv_pool* src, IdList src_ids, int32_t n_blocks, cha
     ev.fence = own[2 * n_slots];
   }
 
+  // A shared staging buffer: the previous call's last device-to-host copy
+  // comes after all of its packs and copies, so waiting on it frees every slot.
+  if (preset && preset->last >= 0)
+    IEKV_HIP(hipStreamWaitEvent(compute, ev.copied[preset->last], 0));
   // Entry fence: the copy stream must not read staging before the compute
   // stream's earlier work on it has finished.
   IEKV_HIP(hipEventRecord(ev.fence, compute));
@@ -1319,6 +1361,7 @@ int offload_pipeline(const iekv_pool* src, IdList src_ids, int32_t n_blocks, cha
     if ((rc = store(slot, first, cnt))) return rc;
     IEKV_HIP(hipEventRecord(ev.copied[s], copy));
     last = s;
+    if (preset) preset->last = s;
   }
   // Later compute-stream work (reuse of staging, reads of the host images after
   // a sync of `compute`) is ordered after the last device-to-host copy.
@@ -1332,7 +1375,7 @@ int offload_pipeline(const iekv_pool* src, IdList src_ids, int32_t n_blocks, cha
 // the staged pipeline copies each chunk with one hipMemcpyAsync.
 int run_offload(const iekv_pool* src, IdList src_ids, int32_t n_blocks, void* host_dst,
                 int64_t need, char* staging, int64_t staging_bytes, hipStream_t compute,
-                hipStream_t copy, const OffloadEvents* preset) {
+                hipStream_t copy, OffloadEvents* preset) {
   if (need <= kZeroCopyMaxBytes) {
     if (char* mapped = device_view_of_host(host_dst, need)) {
       const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
@@ -1353,7 +1396,10 @@ int run_offload(const iekv_pool* src, IdList src_ids, int32_t n_blocks, void* ho
 
 // The staging of iekv_offload_static on one device: the device address of
 // `scratch` there and the pipeline's events, set up by the first call on
-// that device and kept until the process ends.
+// that device and kept until the process ends. g_static_mu is held for the
+// whole of each call's enqueueing, so calls from several host threads are
+// enqueued one after another, each ordered on the device after the previous
+// one's copies (OffloadEvents::last).
 struct StaticStaging {
   bool ready = false;
   char* ptr = nullptr;
@@ -1363,12 +1409,12 @@ constexpr int kMaxStaticDevices = 64;
 std::mutex g_static_mu;
 StaticStaging g_static[kMaxStaticDevices];
 
-// The static staging of `device`, which must be the current device.
-int static_staging(int device, const StaticStaging** out) {
+// The static staging of `device`, which must be the current device; the caller
+// holds g_static_mu.
+int static_staging(int device, StaticStaging** out) {
   if (device < 0 || device >= kMaxStaticDevices)
     return set_error(IEKV_ERR_INVALID, "device %d is outside 0..%d", device,
                      kMaxStaticDevices - 1);
-  std::lock_guard<std::mutex> lock(g_static_mu);
   StaticStaging& st = g_static[device];
   if (!st.ready) {
     // `scratch` names the host-side stand-in of the device array; the address
@@ -1420,12 +1466,11 @@ int restore_image(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks, const 
   if ((rc = check_buffer(host_src, host_bytes, need, "host"))) return rc;
   const int64_t block_bytes = image_bytes(dst, 1);
   if (n_blocks > 0) {
-    if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
     DeviceGuard guard(dst->device);
     if (!guard.ok()) return guard.fail();
     if (const char* mapped = device_view_of_host(host_src, need)) {
-      const int32_t per = static_cast<int32_t>(
-          std::max<int64_t>(1, std::min<int64_t>(n_blocks, kZeroCopyMaxBytes / block_bytes)));
+      const int32_t per =
+          iekv_plan::images_per_launch(n_blocks, block_bytes, kZeroCopyMaxBytes, INT32_MAX);
       const int32_t chunk = host_read_chunk(dst->tile_bytes);
       for (int32_t first = 0; first < n_blocks; first += per) {
         const int32_t cnt = std::min(per, n_blocks - first);
@@ -1463,8 +1508,6 @@ int offload_images(const iekv_pool* src, IdList src_ids, int32_t n_blocks,
   for (int32_t i = 0; i < n_blocks; ++i)
     if (!host_blocks[i]) return set_error(IEKV_ERR_INVALID, "host block %d address is null", i);
   const int64_t block_bytes = image_bytes(src, 1);
-  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? block_bytes : 0, "staging")))
-    return rc;
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
@@ -1511,11 +1554,10 @@ int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
     if (!host_blocks[i]) return set_error(IEKV_ERR_INVALID, "host block %d address is null", i);
   const int64_t block_bytes = image_bytes(dst, 1);
   if (n_blocks > 0) {
-    if ((rc = check_buffer(staging, staging_bytes, block_bytes, "staging"))) return rc;
     DeviceGuard guard(dst->device);
     if (!guard.ok()) return guard.fail();
-    const int32_t per = static_cast<int32_t>(std::max<int64_t>(
-        1, std::min<int64_t>(IEKV_INLINE_IMAGES, kZeroCopyMaxBytes / block_bytes)));
+    const int32_t per = iekv_plan::images_per_launch(n_blocks, block_bytes, kZeroCopyMaxBytes,
+                                                     IEKV_INLINE_IMAGES);
     // Every image's device address first: the call goes direct only if all of them
     // have one, so it never mixes the two paths.
     std::vector<uint64_t> views(n_blocks);
@@ -1622,6 +1664,7 @@ int iekv_pool_create(const uint64_t* array_ptrs, int32_t n_arrays, int64_t tile_
   p->tile_bytes = tile_bytes;
   p->num_blocks = num_blocks;
   p->align = align;
+  p->arrays.assign(array_ptrs, array_ptrs + n_arrays);
   if (slab) {
     p->base = array_ptrs[0];
     p->stride = stride;
@@ -1771,9 +1814,11 @@ int iekv_copy_direct_ids(const iekv_pool* src, const iekv_pool* dst, const int32
     return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
                      dst->device);
   std::vector<int32_t> s, d;
-  if ((rc = check_host_range(src_ids, n_blocks, src->num_blocks, "source")) ||
+  bool same_pool = false;
+  if ((rc = check_aliasing(src, dst, &same_pool)) ||
+      (rc = check_host_range(src_ids, n_blocks, src->num_blocks, "source")) ||
       (rc = check_host_range(dst_ids, n_blocks, dst->num_blocks, "destination")) ||
-      (rc = order_pairs(src_ids, dst_ids, n_blocks, src == dst, &s, &d)))
+      (rc = order_pairs(src_ids, dst_ids, n_blocks, same_pool, &s, &d)))
     return rc;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
@@ -1935,9 +1980,6 @@ int iekv_offload(const iekv_pool* src, const int32_t* src_ids, int32_t n_blocks,
   int rc;
   int64_t need = 0;
   if ((rc = check_offload(src, src_ids, n_blocks, host_dst, host_bytes, &need))) return rc;
-  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? image_bytes(src, 1) : 0,
-                         "staging")))
-    return rc;
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
@@ -1952,9 +1994,6 @@ int iekv_offload_ids(const iekv_pool* src, const int32_t* src_ids, int32_t n_blo
   int64_t need = 0;
   if ((rc = check_offload(src, src_ids, n_blocks, host_dst, host_bytes, &need)) ||
       (rc = check_host_range(src_ids, n_blocks, src->num_blocks, "source")))
-    return rc;
-  if ((rc = check_buffer(staging, staging_bytes, n_blocks ? image_bytes(src, 1) : 0,
-                         "staging")))
     return rc;
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
@@ -1979,7 +2018,8 @@ int iekv_offload_static(const iekv_pool* src, const int32_t* src_ids, int32_t n_
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
-  const StaticStaging* st = nullptr;
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  StaticStaging* st = nullptr;
   if ((rc = static_staging(src->device, &st))) return rc;
   return run_offload(src, {src_ids, false}, n_blocks, host_dst, need, st->ptr,
                      IEKV_STATIC_STAGING_BYTES, compute, copy, &st->events);
@@ -2067,6 +2107,8 @@ int iekv_check_ids(const iekv_pool* src, const int32_t* src_ids, const iekv_pool
   if (src && dst && src->device != dst->device)
     return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
                      dst->device);
+  bool same_pool = false;
+  if (src && dst && (rc = check_aliasing(src, dst, &same_pool))) return rc;
   const int64_t words = dst ? (dst->num_blocks + 31) / 32 : 0;
   if ((rc = check_buffer(workspace, workspace_bytes, words * 4, "workspace"))) return rc;
   if (words && reinterpret_cast<uintptr_t>(workspace) % alignof(uint32_t))
@@ -2089,10 +2131,43 @@ int iekv_check_ids(const iekv_pool* src, const int32_t* src_ids, const iekv_pool
   }
   if (src) {
     hipLaunchKernelGGL(ids_probe, dim3(grid), dim3(kThreads), 0, stream, src_ids, n_blocks,
-                       src->num_blocks, src == dst ? static_cast<const uint32_t*>(bitmap)
-                                                   : nullptr, status);
+                       src->num_blocks, same_pool ? static_cast<const uint32_t*>(bitmap)
+                                                  : nullptr, status);
     IEKV_HIP(hipGetLastError());
   }
+  return IEKV_OK;
+}
+
+int iekv_noop(int32_t workgroups, int32_t launches, hipStream_t stream) {
+  if (workgroups <= 0 || workgroups > kMaxGrid)
+    return set_error(IEKV_ERR_INVALID, "workgroups %d out of range", workgroups);
+  if (launches < 0) return set_error(IEKV_ERR_INVALID, "launches is negative (%d)", launches);
+  for (int32_t i = 0; i < launches; ++i) {
+    const int rc = dispatch(kv_noop, dim3(static_cast<uint32_t>(workgroups)), stream);
+    if (rc) return rc;
+  }
+  return IEKV_OK;
+}
+
+int iekv_host_alloc(int64_t bytes, void** out) {
+  if (!out) return set_error(IEKV_ERR_INVALID, "out is null");
+  *out = nullptr;
+  if (bytes <= 0) return set_error(IEKV_ERR_INVALID, "bytes must be positive (%lld)",
+                                   static_cast<long long>(bytes));
+  const hipError_t e = hipHostMalloc(out, static_cast<size_t>(bytes), hipHostMallocDefault);
+  if (e != hipSuccess || !*out) {
+    (void)hipGetLastError();
+    *out = nullptr;
+    return set_error(IEKV_ERR_HIP, "hipHostMalloc of %lld bytes: %s",
+                     static_cast<long long>(bytes),
+                     e != hipSuccess ? hipGetErrorString(e) : "null pointer");
+  }
+  return IEKV_OK;
+}
+
+int iekv_host_free(void* ptr) {
+  if (!ptr) return IEKV_OK;
+  IEKV_HIP(hipHostFree(ptr));
   return IEKV_OK;
 }
 

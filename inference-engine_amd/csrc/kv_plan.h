@@ -7,7 +7,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <vector>
 
 namespace iekv_plan {
 
@@ -182,6 +184,87 @@ inline void image_runs(const void* const* images, int32_t n, int64_t image_bytes
     emit(i, len);
     i += len;
   }
+}
+
+// What the runtime reports for the host allocation holding one address: whether
+// it is pinned memory mapped for the device, the distance from the address to
+// the allocation's end, and device address minus host address (the same for
+// every byte of the allocation).
+struct HostSpan {
+  bool mapped = false;
+  int64_t room = 0;
+  int64_t shift = 0;
+};
+
+// Device addresses of n host images of `bytes` each (the direct host
+// transfers): out[i] = images[i] + shift of the allocation holding it. One
+// lookup per allocation: an image that lies inside [first looked-up address,
+// end of its allocation) reuses that lookup. False when an image is not in
+// mapped pinned memory or runs past its allocation's end; out is then
+// partly written. lookup(address) returns the HostSpan of that address.
+template <typename Lookup>
+inline bool image_views(const void* const* images, int32_t n, int64_t bytes, Lookup lookup,
+                        uint64_t* out) {
+  if (bytes <= 0) return false;
+  uint64_t lo = 0, hi = 0;
+  int64_t shift = 0;
+  bool have = false;
+  for (int32_t i = 0; i < n; ++i) {
+    const uint64_t p = reinterpret_cast<uint64_t>(images[i]);
+    if (p > UINT64_MAX - static_cast<uint64_t>(bytes)) return false;
+    if (!(have && p >= lo && p + static_cast<uint64_t>(bytes) <= hi)) {
+      const HostSpan span = lookup(p);
+      if (!span.mapped || span.room < bytes) return false;
+      lo = p;
+      hi = p + static_cast<uint64_t>(span.room);
+      shift = span.shift;
+      have = true;
+    }
+    out[i] = p + static_cast<uint64_t>(shift);
+  }
+  return true;
+}
+
+// Block images per launch of a direct host transfer: at most max_images, and at
+// most max_bytes of images unless a single image is larger (then one per launch).
+inline int32_t images_per_launch(int32_t n_blocks, int64_t block_bytes, int64_t max_bytes,
+                                 int32_t max_images) {
+  int64_t per = block_bytes > 0 ? max_bytes / block_bytes : 1;
+  if (per > max_images) per = max_images;
+  if (per > n_blocks) per = n_blocks;
+  return static_cast<int32_t>(per < 1 ? 1 : per);
+}
+
+// Staging slots of a host pipeline: two when the buffer holds two block images
+// or more, else one, each of slot_blocks images (at most n_blocks). False when
+// the buffer cannot hold one image: the pipeline would make no progress.
+inline bool plan_slots(int64_t staging_bytes, int64_t block_bytes, int32_t n_blocks,
+                       int* n_slots, int64_t* slot_blocks) {
+  const int64_t fit = block_bytes > 0 ? staging_bytes / block_bytes : 0;
+  *n_slots = fit >= 2 ? 2 : 1;
+  *slot_blocks = fit / *n_slots < n_blocks ? fit / *n_slots : n_blocks;
+  return *slot_blocks >= 1;
+}
+
+// A byte range [lo, hi) of owner 0 or 1 (one pool's array, say).
+struct Span {
+  uint64_t lo, hi;
+  int owner;
+};
+
+// Whether a span of owner 0 shares a byte with a span of owner 1. Sorted by
+// start, a span meets an earlier span of the other owner exactly when that
+// owner's furthest end so far lies past its start.
+inline bool spans_cross(std::vector<Span> spans) {
+  std::sort(spans.begin(), spans.end(),
+            [](const Span& x, const Span& y) { return x.lo < y.lo; });
+  uint64_t reach[2] = {0, 0};
+  for (const Span& s : spans) {
+    if (s.hi <= s.lo) continue;
+    if (reach[1 - s.owner] > s.lo) return true;
+    if (s.hi > reach[s.owner]) reach[s.owner] = s.hi;
+  }
+  return false;
 }
 
 }  // namespace iekv_plan

@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most host ids one launch carries in its arguments
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: largest direct offload; restore launch size
@@ -84,6 +84,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                 POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
     "iekv_check_ids": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
                                c_int64, c_void_p, c_void_p]),
+    "iekv_host_alloc": (c_int, [c_int64, POINTER(c_void_p)]),
+    "iekv_host_free": (c_int, [c_void_p]),
+    "iekv_noop": (c_int, [c_int32, c_int32, c_void_p]),
     "iekv_profile_start": (c_int, [c_int32]),
     "iekv_profile_stop": (c_int, [POINTER(ctypes.c_float), c_int32, POINTER(c_int32)]),
 }

@@ -42,8 +42,8 @@ import numpy as np
 import torch
 
 from .. import _native
-from .pools import (KVPool, StreamScope, check_device_ids, current_stream_handle, integer_ids,
-                    stage_ids, stream_handle)
+from .pools import (KVPool, StreamScope, check_device_ids, current_stream_handle, host_buffer,
+                    integer_ids, stage_ids, stream_handle)
 
 # Device staging the host pipelines use: two slots of at most this many bytes.
 HOST_STAGING_BYTES = 256 << 20
@@ -460,7 +460,13 @@ class HipSlotCopier:
         shape = (n, self.pool.n_arrays, self.pool.tile_bytes)
         if on_host:
             _release_finished()
-            data = torch.empty(shape, dtype=torch.uint8, pin_memory=True)
+            # A one-block buffer (a tier payload, kept for as long as the tier holds
+            # it) pins exactly one block image; torch would round a block image that
+            # is not a power of two up to one (2.5 MiB -> 4 MiB). Buffers of several
+            # blocks live for one transfer or swap and stay with torch's cache,
+            # whose power-of-two classes bound what it keeps for reuse.
+            data = host_buffer(shape) if n == 1 else \
+                torch.empty(shape, dtype=torch.uint8, pin_memory=True)
         else:
             data = torch.empty(shape, dtype=torch.uint8, device=self.device)
         out = PackedBlocks._new(data, self.pool.num_layers, self._tile_shape, self.pool.dtype,
@@ -497,6 +503,15 @@ class HipSlotCopier:
             stream.wait_stream(last)
         self._staging_stream = stream
         return self._staging
+
+    def _staging_for(self, n_blocks: int, direct: bool) -> tuple[int | None, int]:
+        """(address, bytes) of the device staging a host call hands the library: none
+        when the call moves pinned images directly (the library stages nothing then),
+        so a copier whose host payloads are all pinned holds no staging buffer."""
+        if direct:
+            return None, 0
+        staging = self._host_staging(n_blocks)
+        return staging.data_ptr(), staging.numel()
 
     def _check_packed(self, packed: PackedBlocks) -> None:
         if packed._checked is self._layout_key:
@@ -589,14 +604,17 @@ class HipSlotCopier:
             n = len(ids)
             bufs = [self._empty_packed(1, on_host=True) for _ in range(n)]
             addresses = (ctypes.c_void_p * n)(*[b.data.data_ptr() for b in bufs])
-            staging = self._host_staging(n)
+            # One group of pinned images within the direct limit is written by the
+            # pack kernel itself (no staging); a block image over the limit is staged.
+            staging, staging_bytes = self._staging_for(
+                n, n * self.pool.block_bytes <= _native.HOST_DIRECT_MAX)
             fn, id_ptr = ("iekv_offload_blocks_ids", ids.host_pointer()) if ids.inline else \
                 ("iekv_offload_blocks", ids.on_device().data_ptr())
             # Pinned images of one group are written by the pack kernel on `stream`;
             # the staged fallback orders `stream` after its last copy, so one event
             # on `stream` marks every buffer.
-            _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging.data_ptr(),
-                         staging.numel(), stream.cuda_stream, self.copy_stream().cuda_stream)
+            _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging,
+                         staging_bytes, stream.cuda_stream, self.copy_stream().cuda_stream)
             PackedBlocks.mark_all(bufs, stream)
             for buf, payload in zip(bufs, payloads[first:first + group]):
                 payload._resolve(buf, 0)
@@ -667,14 +685,15 @@ class HipSlotCopier:
             out = self._empty_packed(n, on_host=(location == "host"))
         if out.on_host:
             stream = torch.cuda.current_stream(self.device)
-            staging = self._host_staging(n)
+            # A pinned image within the direct limit is written by the pack kernel.
+            staging, staging_bytes = self._staging_for(
+                n, out.pinned and out.nbytes <= _native.HOST_DIRECT_MAX)
             copy = self.copy_stream()
             # Short host lists ride in the launches' kernel arguments (no id upload).
             fn, id_ptr = ("iekv_offload_ids", ids.host_pointer()) if ids.inline else \
                 ("iekv_offload", ids.on_device().data_ptr())
             _native.call(fn, self.pool.native.handle, id_ptr, n, out.data.data_ptr(), out.nbytes,
-                         staging.data_ptr(), staging.numel(), stream.cuda_stream,
-                         copy.cuda_stream)
+                         staging, staging_bytes, stream.cuda_stream, copy.cuda_stream)
             out.mark(stream)
             self.offload_launches += 1
             self.blocks_offloaded += n
@@ -723,16 +742,16 @@ class HipSlotCopier:
         if packed.on_host:
             stream = torch.cuda.current_stream(self.device)
             PackedBlocks.order_after([packed], stream)
-            staging = self._host_staging(n)
             # Pinned images are read by the unpack kernel itself on the compute
             # stream, whatever their size; passing that stream as the copy stream
             # spares the call a cross-stream hand-off it would not use.
             direct = packed.pinned
+            staging, staging_bytes = self._staging_for(n, direct)
             copy = stream if direct else self.copy_stream()
             fn, id_ptr = ("iekv_restore_ids", ids.host_pointer()) if ids.inline else \
                 ("iekv_restore", ids.on_device().data_ptr())
             _native.call(fn, self.pool.native.handle, id_ptr, n, packed.data.data_ptr(),
-                         packed.nbytes, staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                         packed.nbytes, staging, staging_bytes, stream.cuda_stream,
                          copy.cuda_stream)
             packed.mark(copy)
             self.restore_launches += 1
@@ -761,16 +780,16 @@ class HipSlotCopier:
             addresses = (ctypes.c_void_p * n)(*[q.data.data_ptr() + p.index * block
                                                 for q, p in zip(packs, chunk)])
             PackedBlocks.order_after(packs, stream)
-            staging = self._host_staging(n)
             # Pinned images are read by the unpack kernel itself on the compute
             # stream (IEKV_INLINE_IMAGES, IEKV_HOST_DIRECT_MAX_BYTES per launch): no
             # cross-stream hand-off.
             direct = all(q.pinned for q in packs)
+            staging, staging_bytes = self._staging_for(n, direct)
             copy = stream if direct else self.copy_stream()
             fn, id_ptr = ("iekv_restore_blocks_ids", part.host_pointer()) if part.inline else \
                 ("iekv_restore_blocks", part.on_device().data_ptr())
-            _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging.data_ptr(),
-                         staging.numel(), stream.cuda_stream, copy.cuda_stream)
+            _native.call(fn, self.pool.native.handle, id_ptr, n, addresses, staging,
+                         staging_bytes, stream.cuda_stream, copy.cuda_stream)
             PackedBlocks.mark_all(list({id(q._root): q._root for q in packs}.values()), copy)
             self.restore_launches += 1
 
@@ -797,7 +816,7 @@ class HipSlotCopier:
         on_device = (isinstance(src_ids, torch.Tensor) and src_ids.device.type == "cuda") or \
             (isinstance(dst_ids, torch.Tensor) and dst_ids.device.type == "cuda")
         stream = on.cuda_stream if on is not None else current_stream_handle(self.device)
-        same_pool = source.pool.native.handle.value == self.pool.native.handle.value
+        same_pool = source.pool.same_pool_as(self.pool)
         if on_device:
             with self._on(on):          # a host-side table's upload is ordered on the copy's stream
                 src = source.pool.block_ids(src_ids, what="source block")
@@ -884,8 +903,7 @@ class HipSlotCopier:
         s = source.pool.host_ids(np.concatenate(src_all) if src_all else [], what="source block")
         d = self.pool.host_ids(np.concatenate(dst_all) if dst_all else [], unique=True,
                                what="destination block")
-        if source.pool.native.handle.value == self.pool.native.handle.value and \
-                bool(np.isin(s, d).any()):
+        if source.pool.same_pool_as(self.pool) and bool(np.isin(s, d).any()):
             raise ValueError("a direct copy within one pool needs disjoint source "
                              "and destination blocks")
         if not counts:

@@ -11,6 +11,7 @@ keep the reference's per-layer shape, and the ``[N, bs, H, D]`` paged view
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Sequence as Seq
 
@@ -74,6 +75,78 @@ def allocate_pool_pair(first_blocks: int, second_blocks: int, block_size: int,
     return pools[0], pools[1]
 
 
+# Exact-size pinned host buffers (iekv_host_alloc). torch's caching host allocator
+# rounds every pinned request up to a power of two and keeps the block when the
+# tensor dies: a 2.5 MiB block image then pins 4 MiB and a 43 GB image 64 GiB.
+# Buffers made here pin exactly their size; one that dies goes back to a free list
+# of its size, so a tier that recycles its payloads allocates only while it grows.
+_PINNED_FREE: dict[int, list[int]] = {}
+_PINNED_TYPES: dict[int, type] = {}
+
+
+def _pinned_type(nbytes: int) -> type:
+    """A ctypes byte array type of ``nbytes`` whose instances hand their memory back
+    to the free list when the last tensor over them dies."""
+    t = _PINNED_TYPES.get(nbytes)
+    if t is None:
+        free = _PINNED_FREE.setdefault(nbytes, [])
+        addressof = ctypes.addressof
+
+        class _Pinned(ctypes.c_ubyte * nbytes):
+            __slots__ = ()
+
+            def __del__(self, _free=free, _addressof=addressof) -> None:
+                _free.append(_addressof(self))
+
+        t = _PINNED_TYPES[nbytes] = _Pinned
+    return t
+
+
+def pinned_empty(nbytes: int) -> torch.Tensor:
+    """A uint8 CPU tensor of exactly ``nbytes`` bytes of pinned host memory mapped for
+    the GPU (uninitialised). Its memory is reused by later calls of the same size once
+    every view of it is gone; :func:`release_pinned` returns unused buffers."""
+    if nbytes <= 0:
+        raise ValueError("nbytes must be positive")
+    free = _PINNED_FREE.get(nbytes)
+    if free:
+        ptr = free.pop()
+    else:
+        out = ctypes.c_void_p()
+        _native.call("iekv_host_alloc", nbytes, ctypes.byref(out))
+        ptr = out.value
+    return torch.frombuffer(_pinned_type(nbytes).from_address(ptr), dtype=torch.uint8)
+
+
+def pinned_bytes_cached() -> int:
+    """Bytes of pinned buffers :func:`pinned_empty` holds for reuse."""
+    return sum(size * len(ptrs) for size, ptrs in _PINNED_FREE.items())
+
+
+def release_pinned() -> int:
+    """Free every unused buffer :func:`pinned_empty` holds (no copy may use them: a
+    buffer is unused once its last tensor died, and host payloads keep their tensors
+    alive until their copies finish). Returns the bytes freed."""
+    freed = 0
+    for size, ptrs in _PINNED_FREE.items():
+        while ptrs:
+            _native.call("iekv_host_free", ptrs.pop())
+            freed += size
+    return freed
+
+
+def host_buffer(shape: tuple[int, ...], *, pinned: bool = True) -> torch.Tensor:
+    """A uint8 host buffer of ``shape``: pinned memory of exactly its size when its size
+    is not a power of two (:func:`pinned_empty`), else torch's pinned memory, which is
+    then exact and cached by torch; pageable memory when ``pinned`` is false."""
+    nbytes = math.prod(shape)
+    if not pinned or nbytes <= 0:
+        return torch.empty(shape, dtype=torch.uint8, pin_memory=pinned and nbytes > 0)
+    if nbytes & (nbytes - 1) == 0:
+        return torch.empty(shape, dtype=torch.uint8, pin_memory=True)
+    return pinned_empty(nbytes).view(shape)
+
+
 class KVPool:
     """A validated, registered set of per-layer caches (K arrays then V arrays)."""
 
@@ -112,6 +185,38 @@ class KVPool:
     @property
     def n_arrays(self) -> int:
         return 2 * self.num_layers
+
+    def memory_relation(self, other: "KVPool") -> str:
+        """How this pool's arrays share memory with ``other``'s: ``"same"`` (the same
+        arrays, also through another KVPool made over the same caches), ``"partial"``
+        (arrays that overlap without being the same) or ``"separate"``. Block ids of one
+        pool mean the same blocks of the other only when they are the same."""
+        mine = [t.data_ptr() for t in self._arrays]
+        theirs = [t.data_ptr() for t in other._arrays]
+        if mine == theirs and (self.tile_bytes, self.num_blocks) == (other.tile_bytes,
+                                                                     other.num_blocks):
+            return "same"
+        if self.device != other.device:
+            return "separate"
+        span = self.num_blocks * self.tile_bytes
+        other_span = other.num_blocks * other.tile_bytes
+        spans = sorted([(a, a + span, 0) for a in mine] + [(b, b + other_span, 1)
+                                                          for b in theirs])
+        reach = [0, 0]
+        for lo, hi, owner in spans:
+            if reach[1 - owner] > lo:
+                return "partial"
+            reach[owner] = max(reach[owner], hi)
+        return "separate"
+
+    def same_pool_as(self, other: "KVPool") -> bool:
+        """Whether ``other`` describes this pool's memory (see :meth:`memory_relation`);
+        ValueError for pools that overlap without being the same."""
+        relation = self.memory_relation(other)
+        if relation == "partial":
+            raise ValueError("the source and destination pools overlap in memory without "
+                             "being the same pool")
+        return relation == "same"
 
     @property
     def block_bytes(self) -> int:
@@ -199,7 +304,8 @@ def check_device_ids(src_pool: KVPool | None, src_ids: torch.Tensor | None,
 
     Source ids are checked against ``src_pool``'s size, destination ids against
     ``dst_pool``'s and for repeats, and when both pools are the same registered
-    pool, that no block is both a source and a destination. The check runs on
+    pool (the same arrays, whichever handles describe them), that no block is
+    both a source and a destination. The check runs on
     the current stream, ordered after whatever wrote the ids, and this call
     synchronises that stream to read the result: IndexError for an id outside
     its pool, ValueError for a repeated destination or an overlap.

@@ -13,7 +13,20 @@
 //     in order, merges only images adjacent in memory within the allocation of
 //     the run's first image, and merges every such pair: fixed layouts (one
 //     allocation, neighbouring allocations, gaps, unknown memory, descending
-//     addresses) and random ones.
+//     addresses) and random ones;
+//  6. image_views (device addresses of the direct host transfers) gives every
+//     image its own allocation's address shift, looks each allocation up once
+//     per stretch of images inside it, and refuses images in unmapped memory,
+//     images running past their allocation's end and addresses whose end would
+//     wrap, at the 70B-share workload's numbers (16,384 images of 2.5 MiB in one
+//     64 GiB pinned allocation, or each in its own) and on random layouts
+//     against a brute-force search;
+//  7. images_per_launch and plan_slots cut every count of images into pieces
+//     that stay within their byte limit and their staging slots (a simulated
+//     pipeline writes only inside the staging buffer and covers every image
+//     once); spans_cross agrees with a brute-force pairwise test.
+// Built twice by the CPU test: optimised, and with AddressSanitizer and
+// UndefinedBehaviorSanitizer (any report fails the run).
 // Prints "plan ok" and exits 0, or names the first failure and exits 1.
 #include <algorithm>
 #include <cstdint>
@@ -264,6 +277,205 @@ static void check_image_runs() {
   }
 }
 
+// Synthetic pinned allocations for image_views: [lo, hi) with a device shift.
+struct Pinned {
+  uint64_t lo, hi;
+  int64_t shift;
+  bool mapped;
+};
+
+struct HostMap {
+  std::vector<Pinned> allocs;
+  mutable int lookups = 0;
+  HostSpan span(uint64_t p) const {
+    ++lookups;
+    HostSpan s;
+    for (const Pinned& a : allocs)
+      if (p >= a.lo && p < a.hi) {
+        s.mapped = a.mapped;
+        s.room = static_cast<int64_t>(a.hi - p);
+        s.shift = a.shift;
+      }
+    return s;
+  }
+  // What a brute-force search says image [p, p + bytes) maps to (false: no view).
+  bool expect(uint64_t p, int64_t bytes, uint64_t* view) const {
+    for (const Pinned& a : allocs)
+      if (a.mapped && p >= a.lo && p < a.hi && bytes <= static_cast<int64_t>(a.hi - p)) {
+        *view = p + static_cast<uint64_t>(a.shift);
+        return true;
+      }
+    return false;
+  }
+};
+
+static bool views_of(const std::vector<uint64_t>& addresses, int64_t bytes, const HostMap& map,
+                     std::vector<uint64_t>* out) {
+  std::vector<const void*> images;
+  for (uint64_t a : addresses) images.push_back(reinterpret_cast<const void*>(a));
+  out->assign(addresses.size(), 0);
+  return image_views(images.data(), static_cast<int32_t>(images.size()), bytes,
+                     [&](uint64_t p) { return map.span(p); }, out->data());
+}
+
+static void check_image_views() {
+  const int64_t img = 2621440;                     // a 70B-share block image, 2.5 MiB
+  const int32_t n = 16384;                         // the 70B-share workload's blocks
+  const uint64_t base = uint64_t(0x7f12) << 32;    // a host virtual address
+  std::vector<uint64_t> addresses(n);
+  for (int32_t i = 0; i < n; ++i) addresses[i] = base + static_cast<uint64_t>(i) * img;
+  std::vector<uint64_t> views;
+
+  // One pinned allocation holding every image, rounded up to 64 GiB.
+  HostMap one{{{base, base + (uint64_t(1) << 36), 0, true}}};
+  EXPECT(views_of(addresses, img, one, &views) && one.lookups == 1,
+         "16,384 images in one allocation: one lookup (got %d)", one.lookups);
+  EXPECT(views == addresses, "identity-mapped pinned memory keeps the host addresses");
+
+  // The same images in an allocation of exactly their size: the last image ends
+  // at the allocation's end and is accepted; one byte less refuses it.
+  HostMap exact{{{base, base + static_cast<uint64_t>(n) * img, 4096, true}}};
+  EXPECT(views_of(addresses, img, exact, &views) && views[n - 1] == addresses[n - 1] + 4096,
+         "an allocation of exactly the images' size, with a device shift");
+  HostMap short_by_one{{{base, base + static_cast<uint64_t>(n) * img - 1, 0, true}}};
+  EXPECT(!views_of(addresses, img, short_by_one, &views),
+         "the last image runs one byte past its allocation: no view");
+
+  // Each image in its own exact-size allocation (the tier's one-block buffers),
+  // allocations 4 KiB apart, each with its own shift; groups of 25 images as
+  // one direct launch takes them (64 MiB / 2.5 MiB).
+  HostMap own;
+  std::vector<uint64_t> scattered;
+  for (int32_t i = 0; i < 1024; ++i) {
+    const uint64_t lo = base + static_cast<uint64_t>(i) * (img + 4096);
+    own.allocs.push_back({lo, lo + img, int64_t(i) << 12, true});
+    scattered.push_back(lo);
+  }
+  for (int32_t first = 0; first < 1024; first += 25) {
+    const int32_t cnt = std::min<int32_t>(25, 1024 - first);
+    std::vector<uint64_t> group(scattered.begin() + first, scattered.begin() + first + cnt);
+    own.lookups = 0;
+    bool ok = views_of(group, img, own, &views) && own.lookups == cnt;
+    for (int32_t j = 0; ok && j < cnt; ++j)
+      ok = views[j] == group[j] + (static_cast<uint64_t>(first + j) << 12);
+    EXPECT(ok, "group at %d: each image takes its own allocation's shift", first);
+  }
+
+  // Unmapped memory anywhere in the list refuses the whole list.
+  HostMap mixed{{{base, base + 8 * img, 0, true}, {base + 8 * img, base + 16 * img, 0, false}}};
+  std::vector<uint64_t> sixteen(addresses.begin(), addresses.begin() + 16);
+  EXPECT(!views_of(sixteen, img, mixed, &views), "an image in unmapped memory: no views");
+  EXPECT(views_of(std::vector<uint64_t>(addresses.begin(), addresses.begin() + 8), img, mixed,
+                  &views), "the mapped half alone has views");
+
+  // Interior pointers and descending order: every image is looked up again once
+  // it leaves the stretch [first looked-up address, allocation end).
+  std::vector<uint64_t> down(addresses.rbegin(), addresses.rbegin() + 64);
+  one.lookups = 0;
+  EXPECT(views_of(down, img, one, &views) && views == down && one.lookups == 64,
+         "descending images: one lookup each (%d)", one.lookups);
+
+  // Degenerate sizes and addresses whose end would wrap around.
+  EXPECT(!views_of({base}, 0, one, &views), "zero-byte images have no view");
+  EXPECT(!views_of({UINT64_MAX - 100}, 4096, one, &views), "an image whose end wraps: no view");
+
+  // Random layouts against the brute-force search.
+  std::mt19937_64 rng(11);
+  for (int trial = 0; trial < 4000; ++trial) {
+    const int64_t size = int64_t(16) << (rng() % 10);
+    HostMap map;
+    uint64_t at = base;
+    const int n_alloc = 1 + static_cast<int>(rng() % 5);
+    for (int a = 0; a < n_alloc; ++a) {
+      const uint64_t len = size * (1 + rng() % 5) + (rng() % 3 == 0 ? rng() % size : 0);
+      map.allocs.push_back({at, at + len, static_cast<int64_t>(rng() % 3) << 20, rng() % 6 != 0});
+      at += len + (rng() % 2 ? 0 : size);
+    }
+    std::vector<uint64_t> list;
+    const int count = 1 + static_cast<int>(rng() % 12);
+    for (int i = 0; i < count; ++i) {
+      const Pinned& a = map.allocs[rng() % map.allocs.size()];
+      list.push_back(a.lo + (rng() % ((a.hi - a.lo) / 16 + 1)) * 16);
+    }
+    bool want = true;
+    std::vector<uint64_t> expected(list.size());
+    for (size_t i = 0; i < list.size(); ++i) want = want && map.expect(list[i], size, &expected[i]);
+    const bool got = views_of(list, size, map, &views);
+    EXPECT(got == want, "random layout %d: views %d, brute force %d", trial, got, want);
+    if (got && want) EXPECT(views == expected, "random layout %d: addresses differ", trial);
+  }
+}
+
+static void check_pieces_and_slots() {
+  const int64_t max_bytes = int64_t(64) << 20;
+  // The direct launches of a restore: at most 128 images and 64 MiB each, one image
+  // per launch when an image alone is larger.
+  for (int64_t block : {int64_t(65536), int64_t(2) << 20, int64_t(2621440), int64_t(3) << 20,
+                        int64_t(100) << 20})
+    for (int32_t n : {1, 2, 24, 25, 26, 128, 129, 1024, 16384}) {
+      const int32_t per = images_per_launch(n, block, max_bytes, 128);
+      EXPECT(per >= 1 && per <= n && per <= 128, "per %d for %d images of %lld", per, n,
+             static_cast<long long>(block));
+      EXPECT(per * block <= max_bytes || per == 1, "%d images of %lld exceed a launch", per,
+             static_cast<long long>(block));
+      EXPECT(per == n || (per + 1) * block > max_bytes || per == 128,
+             "%d images of %lld per launch: one more would fit", per,
+             static_cast<long long>(block));
+    }
+  EXPECT(images_per_launch(16384, 2621440, max_bytes, 128) == 25,
+         "2.5 MiB images: 25 per 64 MiB launch");
+
+  // Staging slots: the pipeline's chunks stay inside the buffer and cover every
+  // image once, alternating between the slots.
+  int n_slots = 0;
+  int64_t slot_blocks = 0;
+  EXPECT(!plan_slots(2621440 - 1, 2621440, 10, &n_slots, &slot_blocks),
+         "a buffer smaller than one image makes no progress: refused");
+  EXPECT(!plan_slots(4096, 0, 10, &n_slots, &slot_blocks), "zero-byte images: refused");
+  for (int64_t block : {int64_t(65536), int64_t(2621440), int64_t(3) << 20})
+    for (int64_t staging : {block, 2 * block - 1, 2 * block, int64_t(512) << 20,
+                            int64_t(256) << 20})
+      for (int32_t n : {1, 2, 3, 101, 102, 103, 16384}) {
+        if (!plan_slots(staging, block, n, &n_slots, &slot_blocks)) {
+          EXPECT(false, "plan_slots refused %lld of staging for %lld-byte images",
+                 static_cast<long long>(staging), static_cast<long long>(block));
+          continue;
+        }
+        EXPECT(n_slots * slot_blocks * block <= staging, "slots overrun the staging buffer");
+        int64_t covered = 0;
+        for (int64_t first = 0, k = 0; first < n; first += slot_blocks, ++k) {
+          const int64_t cnt = std::min<int64_t>(slot_blocks, n - first);
+          const int64_t slot = (k % n_slots) * slot_blocks * block;
+          EXPECT(slot + cnt * block <= staging, "chunk %lld writes past the staging buffer",
+                 static_cast<long long>(k));
+          covered += cnt;
+        }
+        EXPECT(covered == n, "chunks cover %lld of %d images", static_cast<long long>(covered),
+               n);
+      }
+  EXPECT(plan_slots(int64_t(512) << 20, 2621440, 16384, &n_slots, &slot_blocks) &&
+             n_slots == 2 && slot_blocks == 102,
+         "512 MiB of staging: two slots of 102 images of 2.5 MiB");
+
+  // spans_cross against a pairwise test.
+  std::mt19937_64 rng(5);
+  for (int trial = 0; trial < 3000; ++trial) {
+    std::vector<Span> spans;
+    const int count = 1 + static_cast<int>(rng() % 10);
+    for (int i = 0; i < count; ++i) {
+      const uint64_t lo = rng() % 64, len = rng() % 12;
+      spans.push_back({lo, lo + len, static_cast<int>(rng() % 2)});
+    }
+    bool want = false;
+    for (const Span& x : spans)
+      for (const Span& y : spans)
+        if (x.owner == 0 && y.owner == 1 && x.lo < y.hi && y.lo < x.hi && x.lo < x.hi &&
+            y.lo < y.hi)
+          want = true;
+    EXPECT(spans_cross(spans) == want, "spans_cross trial %d", trial);
+  }
+}
+
 int main() {
   for (int grid = 1; grid <= 4096; ++grid) check_xcd_grouped(grid);
   for (int grid : {98816, 1048575, 4194304, 16777215}) check_xcd_grouped(grid);
@@ -324,6 +536,8 @@ int main() {
           }
 
   check_image_runs();
+  check_image_views();
+  check_pieces_and_slots();
 
   if (failures) {
     std::printf("%d failures\n", failures);

@@ -21,7 +21,6 @@ ROOT = Path(__file__).resolve().parents[1]
     (["--config", "cfg5", "--ab", "slack=64,engine"], "--ab takes"),
     (["--ab", "direct_chunk=4096,3000"], "--ab takes"),
     (["--ab", "direct_chunk=32"], "--ab takes"),
-    (["--config", "cfg5", "--legs", "direct,host_roundtrip"], "not run on cfg5"),
     (["--ab", "pack_order=0,3"], "--ab takes"),
     (["--ab", "unroll=0"], "--ab takes"),
 ])

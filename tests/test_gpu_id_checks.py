@@ -162,3 +162,42 @@ def test_the_copier_raises_for_bad_device_ids_and_moves_nothing(gpu):
     loose = copier(32, check=False)
     loose.copy_blocks(src, ids([0, 1]), ids([1, 32]))
     assert loose.blocks_written == 2
+
+
+def test_two_copiers_over_one_cache_are_one_pool(gpu):
+    """The engine makes several copiers over the same caches (transfer, offload,
+    swap). A direct copy between two of them is a copy within one pool: sources that
+    overlap destinations are refused for host lists, long host tables and checked
+    device ids alike, and nothing moves. Caches that overlap without being the same
+    arrays are refused as well."""
+    from iekv.engine.copier import HipSlotCopier
+    from iekv.engine.pools import allocate_pool
+
+    k, v = allocate_pool(600, 4, 2, 2, 8, dtype=torch.float16, device=gpu, zero=False)
+    for t in k + v:
+        t.copy_(torch.randn(t.shape, device=gpu, dtype=torch.float16))
+    a = HipSlotCopier(k, v, 4, check_device_ids=True)
+    b = HipSlotCopier(k, v, 4, check_device_ids=True)
+    assert a.pool.native.handle.value != b.pool.native.handle.value
+    assert a.pool.memory_relation(b.pool) == "same"
+    before = [t.clone() for t in k + v]
+    with pytest.raises(ValueError, match="disjoint|both"):
+        b.copy_blocks(a, [3, 4], [4, 9])                        # host list: the library
+    with pytest.raises(ValueError, match="disjoint"):
+        b.copy_blocks(a, list(range(0, 600)), list(range(599, -1, -1)))   # long: NumPy
+    ids = lambda xs: torch.tensor(xs, dtype=torch.int32, device=gpu)
+    with pytest.raises(ValueError, match="disjoint"):
+        b.copy_blocks(a, ids([3, 4]), ids([4, 9]))               # device ids, checked on GPU
+    torch.cuda.synchronize()
+    for x, y in zip(before, k + v):
+        assert torch.equal(x, y)
+    # disjoint blocks move between the two handles as within one
+    b.copy_blocks(a, [1, 2], [7, 8])
+    torch.cuda.synchronize()
+    for t in k + v:
+        assert torch.equal(t[7 * 4:9 * 4], t[1 * 4:3 * 4])
+    # a view of the caches shifted by one block overlaps them without being them
+    shifted = HipSlotCopier([t[4:] for t in k], [t[4:] for t in v], 4)
+    assert shifted.pool.memory_relation(a.pool) == "partial"
+    with pytest.raises(ValueError, match="overlap in memory"):
+        shifted.copy_blocks(a, [1], [2])

@@ -24,8 +24,8 @@ from iekv.engine.pools import KVPool
 NO_DEVICE = 99
 
 
-def pool(num_blocks, tile=64, arrays=2):
-    ptrs = [(1 << 30) + a * num_blocks * tile for a in range(arrays)]
+def pool(num_blocks, tile=64, arrays=2, base=1 << 30):
+    ptrs = [base + a * num_blocks * tile for a in range(arrays)]
     return _native.Pool(ptrs, tile_bytes=tile, num_blocks=num_blocks, device=NO_DEVICE)
 
 
@@ -83,7 +83,9 @@ def test_direct_copy_ids_are_refused_alike_by_the_library_and_numpy(seed):
         assert len(src) == len(dst) == n
         same = bool(rng.integers(3) == 0)
         a = pool(num_blocks)
-        b = a if same else pool(num_blocks)
+        # one pool: the same handle, or a second handle over the same arrays
+        b = (a if rng.integers(2) else pool(num_blocks)) if same else \
+            pool(num_blocks, base=1 << 31)
         s, d = _host_id_array(src), _host_id_array(dst)
         if s is None or d is None:
             continue
@@ -100,7 +102,8 @@ def test_direct_copy_ids_are_refused_alike_by_the_library_and_numpy(seed):
 
         assert got == numpy_outcome(numpy_check), (src, dst, same, num_blocks)
         a.close()
-        b.close()
+        if b is not a:
+            b.close()
 
 
 @pytest.mark.parametrize("seed", range(3))

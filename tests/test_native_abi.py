@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 18
+    assert lib.iekv_abi_version() == 19
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -172,6 +172,68 @@ def test_device_id_checks_validate_their_arguments_before_any_launch(lib):
     assert lib.iekv_check_ids(h, ids, None, None, 0, None, 0, status, None) == \
         _native.IEKV_ERR_HIP
     pool.close()
+
+
+def test_pools_are_compared_by_the_memory_they_describe(lib):
+    """Two handles over one set of arrays are one pool: a host-id direct copy between
+    them that uses a block as both source and destination is refused with
+    IEKV_ERR_IDS, as it is through a single handle. Handles whose arrays overlap
+    without being the same arrays are refused outright; separate pools pass the
+    checks and reach the device switch (device 99 does not exist)."""
+    from iekv import _native
+
+    base, tile, blocks = 1 << 30, 64, 16
+    stride = tile * blocks
+    one = _native.Pool([base, base + stride], tile_bytes=tile, num_blocks=blocks, device=99)
+    again = _native.Pool([base, base + stride], tile_bytes=tile, num_blocks=blocks, device=99)
+    shifted = _native.Pool([base + tile, base + tile + stride], tile_bytes=tile,
+                           num_blocks=blocks, device=99)
+    apart = _native.Pool([base + 4 * stride, base + 5 * stride], tile_bytes=tile,
+                         num_blocks=blocks, device=99)
+    src = (ctypes.c_int32 * 2)(0, 1)
+    dst = (ctypes.c_int32 * 2)(1, 2)
+    for a, b in ((one, one), (one, again), (again, one)):
+        assert lib.iekv_copy_direct_ids(a.handle, b.handle, src, dst, 2, None) == \
+            _native.IEKV_ERR_IDS
+        assert "block 1 is both" in lib.iekv_last_error().decode()
+    for a, b in ((one, shifted), (shifted, again)):
+        assert lib.iekv_copy_direct_ids(a.handle, b.handle, src, dst, 2, None) == \
+            _native.IEKV_ERR_INVALID
+        assert "overlap in memory" in lib.iekv_last_error().decode()
+    assert lib.iekv_copy_direct_ids(one.handle, apart.handle, src, dst, 2, None) == \
+        _native.IEKV_ERR_HIP
+    status = ctypes.c_void_p(1 << 24)
+    workspace = ctypes.c_void_p(1 << 24)
+    need = _native.check_workspace_bytes(blocks)
+    assert lib.iekv_check_ids(one.handle, src, shifted.handle, dst, 2, workspace, need, status,
+                              None) == _native.IEKV_ERR_INVALID
+    assert "overlap in memory" in lib.iekv_last_error().decode()
+    for pool in (one, again, shifted, apart):
+        pool.close()
+
+
+def test_host_allocation_and_launch_floor_check_their_arguments(lib):
+    """iekv_host_alloc needs an output and a positive size; a failed allocation
+    leaves a null address and the runtime's message. iekv_noop needs 1 to the
+    dispatch limit of workgroups and a non-negative launch count."""
+    from iekv import _native
+
+    out = ctypes.c_void_p(1234)
+    assert lib.iekv_host_alloc(4096, None) == _native.IEKV_ERR_INVALID
+    assert lib.iekv_host_alloc(0, ctypes.byref(out)) == _native.IEKV_ERR_INVALID
+    assert not out.value and "bytes must be positive" in lib.iekv_last_error().decode()
+    rc = lib.iekv_host_alloc(4096, ctypes.byref(out))
+    if rc == _native.IEKV_OK:           # a machine with a GPU
+        assert out.value
+        assert lib.iekv_host_free(out) == _native.IEKV_OK
+    else:
+        assert rc == _native.IEKV_ERR_HIP and not out.value
+        assert "hipHostMalloc of 4096 bytes" in lib.iekv_last_error().decode()
+    assert lib.iekv_host_free(None) == _native.IEKV_OK
+    assert lib.iekv_noop(0, 1, None) == _native.IEKV_ERR_INVALID
+    assert lib.iekv_noop(1 << 24, 1, None) == _native.IEKV_ERR_INVALID
+    assert lib.iekv_noop(1, -1, None) == _native.IEKV_ERR_INVALID
+    assert lib.iekv_noop(1, 0, None) == _native.IEKV_OK
 
 
 def test_scattered_restore_rejects_missing_host_addresses(lib):
