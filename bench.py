@@ -17,6 +17,9 @@ without NaN codes for fp8). Legs:
   pack_unpack  iekv_pack into a per-request staging buffer, then iekv_unpack (4P bytes)
   pack         the pack half alone (2P bytes); unpack: the unpack half alone (2P bytes)
   batched      all requests' blocks in ONE direct launch (2P bytes)
+  direct_ids   the direct leg with each request's table in host memory
+               (iekv_copy_direct_ids: ids checked on the host, carried in the launch's
+               kernel arguments)
   copier       the drop-in Python path: HipSlotCopier.copy_blocks per request with the
                block tables as Python lists (id checks and hand-over included; 2P bytes)
   copier_pack_unpack  the same for pack mode: read_blocks then write_blocks (4P bytes)
@@ -78,7 +81,7 @@ METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff
 # Legs that move the workload's blocks from the prefill pool to the decode pool; the
 # first of them in --legs gives the line's value (2P / step time).
 HANDOFF_LEGS = ("direct", "pack_unpack", "pack", "unpack", "batched", "copier",
-                "copier_pack_unpack", "requests")
+                "copier_pack_unpack", "requests", "direct_ids")
 # The slot kernels on either side of the handoff (prefill's KV writes, decode's reads).
 SLOT_LEGS = ("write_kv", "write_kv_per_layer", "gather_context", "gather_per_array")
 
@@ -258,6 +261,12 @@ class Legs:
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
         if name == "pack_unpack":
             return [x for r, n in enumerate(sizes) for x in ((2 * n * bb, r), (2 * n * bb, r))]
+        if name == "direct_ids":
+            from iekv import _native
+
+            step = _native.INLINE_IDS
+            return [(2 * min(step, n - k) * bb, r) for r, n in enumerate(sizes)
+                    for k in range(0, n, step)]
         if name in ("copier", "copier_pack_unpack"):
             # the copier hands a table of up to HOST_IDS_MAX ids to the library's
             # host-id entry points, which issue INLINE_IDS ids per launch; a longer
@@ -427,6 +436,24 @@ class Legs:
         for k, (s, d) in enumerate(zip(self.src_direct, self.dst_direct)):
             _native.call("iekv_copy_direct", self.src.native.handle, self.dst.native.handle,
                          s.data_ptr(), d.data_ptr(), s.numel(), hs[k % len(hs)])
+        self._join()
+
+    def direct_ids(self) -> None:
+        """The direct leg with each request's table in host memory, as a serving loop
+        holds it: iekv_copy_direct_ids checks the ids and carries them in the launch's
+        kernel arguments (IEKV_INLINE_IDS per launch), so no kernel reads an id from
+        device memory before its first data load."""
+        from array import array
+
+        from iekv import _native
+
+        if not hasattr(self, "_host_tables"):
+            self._host_tables = [(array("i", s.tolist()), array("i", d.tolist()))
+                                 for s, d in zip(self.src_direct, self.dst_direct)]
+        hs = self._fork()
+        for k, (s, d) in enumerate(self._host_tables):
+            _native.call("iekv_copy_direct_ids", self.src.native.handle, self.dst.native.handle,
+                         s.buffer_info()[0], d.buffer_info()[0], len(s), hs[k % len(hs)])
         self._join()
 
     def _drop_in(self):
@@ -856,8 +883,8 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
         "avg_launch_us": round(1000 * total_ms / max(1, len(durations)), 2),
         "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
     }
-    if name in ("direct", "copier", "requests", "pack_unpack", "copier_pack_unpack", "pack",
-                "unpack", *SLOT_LEGS):
+    if name in ("direct", "direct_ids", "copier", "requests", "pack_unpack",
+                "copier_pack_unpack", "pack", "unpack", *SLOT_LEGS):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
                                  "p50": round(req_ms[len(req_ms) // 2], 4),
                                  "p99": round(req_ms[min(len(req_ms) - 1,
@@ -941,6 +968,127 @@ def cpu_baseline(workload, budget_blocks: int, seed: int, min_seconds: float,
                        f"the GPU source pool's N(0,1) bytes, random src/dst ids, repeated "
                        f"{passes}x; NumPy restatement of copier.py:18-31 driven as "
                        f"disaggregated.py:50,81-82; 1 of {os.cpu_count()} host cores")}
+
+
+def _quantiles(ms: list[float]) -> dict:
+    """Median, 10th and 90th percentile of launch durations, in microseconds."""
+    us = sorted(1000 * x for x in ms)
+    return {"p50_us": round(us[len(us) // 2], 3), "p10_us": round(us[len(us) // 10], 3),
+            "p90_us": round(us[min(len(us) - 1, 9 * len(us) // 10)], 3), "launches": len(us)}
+
+
+def launch_floor(device, configs=("cfg1", "cfg2"), seed: int = 0, reps: int = 400) -> dict:
+    """What a launch costs before it moves a byte, and where a small request's time goes.
+
+    In-dispatch durations (iekv_profile_start: events in each launch's own packet),
+    launches issued one after another on one stream:
+      * noop: iekv_noop, an empty kernel of 1 to 2,048 workgroups;
+      * one_tile: iekv_copy_direct of one block between two one-array pools, tiles of
+        4 to 64 KiB, ids in device memory, and iekv_copy_direct_ids (ids in the
+        kernel arguments) for the same move;
+      * requests: each request of the workloads' direct leg alone, with device ids and
+        with host ids in the kernel arguments, against the bytes' time at peak.
+    Host cost of issuing one launch: iekv_noop issuing many launches from C in one
+    call, and a Python loop of one-launch calls.
+    """
+    import ctypes
+    from array import array
+
+    import torch
+
+    from iekv import _native, workloads
+
+    stream = torch.cuda.current_stream(device)
+    h = stream.cuda_stream
+    out: dict = {"unit": "microseconds", "noop": {}, "one_tile": {}, "host_us_per_launch": {},
+                 "requests": {}, "hip_force_dev_kernarg": os.environ.get("HIP_FORCE_DEV_KERNARG")}
+
+    def timed(issue, launches: int) -> list[float]:
+        torch.cuda.synchronize()
+        with _native.LaunchTimer(launches) as timer:
+            issue()
+            torch.cuda.synchronize()
+        if len(timer.durations_ms) != launches:
+            raise RuntimeError(f"{len(timer.durations_ms)} launches timed, {launches} issued")
+        return timer.durations_ms
+
+    for wg in (1, 8, 256, 2048):
+        _native.call("iekv_noop", wg, 20, h)
+        out["noop"][str(wg)] = _quantiles(timed(lambda: _native.call("iekv_noop", wg, reps, h),
+                                                reps))
+    log(f"[floor] noop: " + json.dumps(out["noop"]))
+
+    n_host = 4000
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    _native.call("iekv_noop", 1, n_host, h)
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    out["host_us_per_launch"]["noop_from_c"] = round(1e6 * (t1 - t0) / n_host, 3)
+    noop = _native.lib().iekv_noop
+    t0 = time.perf_counter()
+    for _ in range(n_host):
+        noop(1, 1, h)
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    out["host_us_per_launch"]["noop_python_loop"] = round(1e6 * (t1 - t0) / n_host, 3)
+
+    ok = True
+    for tile in (4096, 8192, 32768, 65536):
+        blocks = 64
+        src = torch.randint(0, 256, (blocks * tile,), dtype=torch.uint8, device=device)
+        dst = torch.zeros(blocks * tile, dtype=torch.uint8, device=device)
+        sp = _native.Pool([src.data_ptr()], tile, blocks, device.index or 0)
+        dp = _native.Pool([dst.data_ptr()], tile, blocks, device.index or 0)
+        sid = torch.tensor([5], dtype=torch.int32, device=device)
+        did = torch.tensor([9], dtype=torch.int32, device=device)
+        hs, hd = array("i", [5]), array("i", [9])
+
+        def device_ids(n=reps):
+            for _ in range(n):
+                _native.call("iekv_copy_direct", sp.handle, dp.handle, sid.data_ptr(),
+                             did.data_ptr(), 1, h)
+
+        def host_ids(n=reps):
+            for _ in range(n):
+                _native.call("iekv_copy_direct_ids", sp.handle, dp.handle, hs.buffer_info()[0],
+                             hd.buffer_info()[0], 1, h)
+
+        device_ids(20)
+        row = {"device_ids": _quantiles(timed(device_ids, reps)),
+               "host_ids": _quantiles(timed(host_ids, reps))}
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        device_ids(n_host // 4)
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        row["host_us_per_call_python"] = round(1e6 * (t1 - t0) / (n_host // 4), 3)
+        ok = ok and torch.equal(dst[9 * tile:10 * tile], src[5 * tile:6 * tile])
+        out["one_tile"][str(tile)] = row
+        sp.close()
+        dp.close()
+        del src, dst
+    log(f"[floor] one tile: " + json.dumps(out["one_tile"]))
+
+    for cfg in configs:
+        w = workloads.make(cfg, seed, None)
+        legs = Legs(w, device, seed, "paired", streams=1)
+        bb = w.shape.block_bytes
+        row = {"blocks_per_request": statistics.median(len(t) for t in w.src_tables),
+               "bytes_per_request_median": int(2 * bb * statistics.median(
+                   len(t) for t in w.src_tables))}
+        for leg in ("direct", "direct_ids"):
+            legs.clear_dst()
+            _, _, launches = time_leg(legs, leg, 10, 3)
+            row[leg] = _quantiles([ms for ms, _, _ in launches])
+            ok = ok and legs.verify()
+        row["bytes_at_peak_us"] = round(row["bytes_per_request_median"] / HBM_PEAK_GBS / 1e3, 3)
+        out["requests"][cfg] = row
+        log(f"[floor] {cfg}: " + json.dumps(row))
+        del legs
+        torch.cuda.empty_cache()
+    out["verified"] = bool(ok)
+    return out
 
 
 def sweep(legs: Legs, names: list[str]) -> list[dict]:
@@ -1148,6 +1296,9 @@ def main() -> int:
                          "pack_order=0,4 (pools re-made per round, every value "
                          "on each)")
     ap.add_argument("--rounds", type=int, default=3, help="rounds of an --ab comparison")
+    ap.add_argument("--floor", action="store_true",
+                    help="measure the launch floor (empty kernels, one-tile moves, the small "
+                         "workloads' requests) instead of the benchmark line")
     ap.add_argument("--separate-pools", action="store_true",
                     help="allocate the two pools separately instead of as one reservation "
                          "(prefill pool first)")
@@ -1198,6 +1349,10 @@ def main() -> int:
         return 2
     if args.ab:
         return ab(args, names, device)
+    if args.floor:
+        floor = launch_floor(device, seed=args.seed)
+        print(json.dumps({"launch_floor": floor}), flush=True)
+        return 0 if floor["verified"] else 1
     legs = Legs(w, device, args.seed, "separate" if args.separate_pools else "paired",
                 streams=args.streams)
     P = w.payload_bytes

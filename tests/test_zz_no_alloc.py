@@ -5,8 +5,13 @@ device staging buffer instead of a caller-allocated one. Called through the
 C-ABI twice in a row, the second time with fewer blocks, it must write the
 same host image, byte for byte, as iekv_offload with a staging buffer from
 torch, and both must equal the pool's tiles gathered by torch indexing.
+Calls on unrelated stream pairs, with no host synchronisation between them,
+and calls from two host threads at once share the one buffer without
+overwriting a slot another call still copies from.
 """
 from __future__ import annotations
+
+import threading
 
 import numpy as np
 import pytest
@@ -93,3 +98,75 @@ def test_static_offload_of_nothing_enqueues_nothing(gpu):
     stream = torch.cuda.current_stream()
     _native.call("iekv_offload_static", pool.native.handle, None, 0, host.data_ptr(), 0,
                  stream.cuda_stream, stream.cuda_stream)
+
+
+def staged_case(gpu, seed):
+    """A pool of 1 MiB block images (32 arrays of 32 KiB tiles): a call of more than
+    64 images goes through the static buffer's two 16 MiB slots."""
+    from iekv.engine.pools import KVPool
+
+    k, v = random_pool(400, 16, 16, 8, 128, gpu, seed=seed)
+    pool = KVPool(k, v, 16)
+    assert pool.block_bytes == 1 << 20
+    return k, v, pool
+
+
+def test_static_offloads_on_unrelated_streams_wait_for_each_other(gpu):
+    from iekv import _native
+
+    k, v, pool = staged_case(gpu, 94)
+    rng = np.random.default_rng(95)
+    pairs = [(torch.cuda.Stream(), torch.cuda.Stream()) for _ in range(3)]
+    calls = []
+    for n, (compute, copy) in zip((150, 100, 70), pairs):
+        ids = [int(b) for b in rng.permutation(400)[:n]]
+        dev_ids = pool.block_ids(ids)
+        torch.cuda.current_stream().synchronize()      # the ids are on the device
+        host = host_buffer(n, pool.n_arrays, pool.tile_bytes, True)
+        calls.append((ids, dev_ids, host, compute))
+    print("[no-alloc] three staged calls on three stream pairs, no host sync", flush=True)
+    for (ids, dev_ids, host, compute), (_, copy) in zip(calls, pairs):
+        _native.call("iekv_offload_static", pool.native.handle, dev_ids.data_ptr(), len(ids),
+                     host.data_ptr(), host.numel(), compute.cuda_stream, copy.cuda_stream)
+    for ids, _, host, compute in calls:
+        compute.synchronize()
+        assert np.array_equal(host.numpy(), expected_image(k, v, ids, pool.tile_bytes))
+
+
+def test_static_offloads_from_two_threads_share_the_buffer(gpu):
+    from iekv import _native
+
+    k, v, pool = staged_case(gpu, 96)
+    rng = np.random.default_rng(97)
+    plans = []
+    for t in range(2):
+        compute, copy = torch.cuda.Stream(), torch.cuda.Stream()
+        jobs = []
+        for n in (90, 120, 66):
+            ids = [int(b) for b in rng.permutation(400)[:n]]
+            jobs.append((ids, pool.block_ids(ids),
+                         host_buffer(n, pool.n_arrays, pool.tile_bytes, True)))
+        plans.append((compute, copy, jobs))
+    torch.cuda.synchronize()
+    errors = []
+
+    def run(compute, copy, jobs):
+        try:
+            for ids, dev_ids, host in jobs:
+                _native.call("iekv_offload_static", pool.native.handle, dev_ids.data_ptr(),
+                             len(ids), host.data_ptr(), host.numel(), compute.cuda_stream,
+                             copy.cuda_stream)
+        except Exception as e:          # reported below, in the test's thread
+            errors.append(e)
+
+    print("[no-alloc] two threads, three staged calls each", flush=True)
+    threads = [threading.Thread(target=run, args=plan) for plan in plans]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors and not any(t.is_alive() for t in threads)
+    torch.cuda.synchronize()
+    for _, _, jobs in plans:
+        for ids, _, host in jobs:
+            assert np.array_equal(host.numpy(), expected_image(k, v, ids, pool.tile_bytes))
