@@ -176,7 +176,7 @@ def test_the_drop_in_tier_path_at_the_70b_share_geometry(gpu):
     for d, s in zip(again, src_ids):
         dst_o.write_block(d, src_o.read_block(s))
     assert_equal_pools(dk, dv, dst_o)
-    del payloads, roots, staged, pageable
+    del payloads, roots, staged, pageable, p, buf     # the loops' last items hold buffers too
     gc.collect()
     torch.cuda.synchronize()
     from iekv.engine import copier as copier_module
