@@ -1033,6 +1033,34 @@ def launch_floor(device, configs=("cfg1", "cfg2"), seed: int = 0, reps: int = 40
     torch.cuda.synchronize()
     out["host_us_per_launch"]["noop_python_loop"] = round(1e6 * (t1 - t0) / n_host, 3)
 
+    # Back-to-back throughput: many empty launches issued together, no per-launch
+    # events, spread over 1, 2 or 4 streams (each at the default priority); the
+    # time per launch is what a stream of independent small requests pays.
+    streams = [stream] + [torch.cuda.Stream(device) for _ in range(3)]
+    out["noop_throughput_us_per_launch"] = {}
+    for n_streams in (1, 2, 4):
+        use = streams[:n_streams]
+        per = 1000
+        for _ in range(2):
+            fork = torch.cuda.Event()
+            fork.record(stream)
+            for st in use[1:]:
+                st.wait_event(fork)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for k in range(per):
+                noop(1, 1, use[k % n_streams].cuda_stream)
+            for st in use[1:]:
+                done = torch.cuda.Event()
+                done.record(st)
+                stream.wait_event(done)
+            b.record(stream)
+            torch.cuda.synchronize()
+        out["noop_throughput_us_per_launch"][str(n_streams)] = round(
+            1000 * a.elapsed_time(b) / per, 3)
+    log(f"[floor] host: " + json.dumps(out["host_us_per_launch"]) + "  throughput: "
+        + json.dumps(out["noop_throughput_us_per_launch"]))
+
     ok = True
     for tile in (4096, 8192, 32768, 65536):
         blocks = 64
@@ -1063,6 +1091,21 @@ def launch_floor(device, configs=("cfg1", "cfg2"), seed: int = 0, reps: int = 40
         t1 = time.perf_counter()
         torch.cuda.synchronize()
         row["host_us_per_call_python"] = round(1e6 * (t1 - t0) / (n_host // 4), 3)
+        # The same one-block moves issued from C: iekv_copy_direct_requests with one
+        # request per move on one stream (the library's own cost per launch).
+        n_req = n_host // 4
+        counts = array("i", [1] * n_req)
+        many_s = sid.repeat(n_req)
+        many_d = did.repeat(n_req)
+        handles = (ctypes.c_void_p * 1)(h)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        _native.call("iekv_copy_direct_requests", sp.handle, dp.handle, n_req,
+                     counts.buffer_info()[0], many_s.data_ptr(), many_d.data_ptr(), handles, 1,
+                     None)
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        row["host_us_per_launch_c"] = round(1e6 * (t1 - t0) / n_req, 3)
         ok = ok and torch.equal(dst[9 * tile:10 * tile], src[5 * tile:6 * tile])
         out["one_tile"][str(tile)] = row
         sp.close()
