@@ -37,7 +37,7 @@ without NaN codes for fp8). Legs:
                and array, as the reference calls gather_context once per cache
   host_roundtrip  every moved block offloaded to pinned host memory with one iekv_offload
                and restored with one iekv_restore (host-link bound), then the same
-               pipelines called once per block on up to 1,024 blocks
+               calls once per block on up to 1,024 blocks, then the drop-in tier path
 
 ``value`` is the direct leg's algorithmic read+write bandwidth, 2P / step
 time, in GB/s (P = blocks x 2L x T); the step time comes from two HIP events
@@ -564,10 +564,9 @@ class Legs:
     def host_roundtrip(self, steps: int, warmup: int) -> dict:
         """Offload every moved block to pinned host memory and restore it onto its dst id.
 
-        One iekv_offload over the whole block list (pack on the compute stream
-        overlapping device-to-host copies on a side stream), then one iekv_restore
-        (the unpack kernel reading the pinned image). Both are bounded by the host
-        link, not HBM. Then, on a sample, the same calls once per block (the
+        One iekv_offload over the whole block list (the pack kernel writing the
+        pinned image, 64 MiB of images per launch), then one iekv_restore (the
+        unpack kernel reading it). Both are bounded by the host link, not HBM. Then, on a sample, the same calls once per block (the
         reference's pattern), and the drop-in tier path (_tier_roundtrip). The host
         image is pinned at exactly its size (iekv_host_alloc) and freed before the
         tier runs; the leg refuses to start when the host cannot hold what it pins

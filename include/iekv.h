@@ -202,23 +202,26 @@ int iekv_gather_rows_arrays(const iekv_pool* pool, int32_t first_array, int32_t 
                             int32_t block_size, const int32_t* block_table, int32_t context_len,
                             void* out, int64_t out_bytes, hipStream_t stream);
 
-/* Largest host image iekv_offload moves directly from the pool into pinned
- * host memory (the pack kernel writes the host buffer), when the host range
- * lies in one pinned allocation mapped for the device; larger images and
- * pageable memory go through the staging buffer. Restores read pinned images
- * directly at any size, in launches of at most this many bytes of images. */
+/* Most bytes of block images one direct host launch moves: offloads and
+ * restores whose host range lies in one pinned allocation mapped for the device
+ * are moved by the pack / unpack kernel itself (it writes or reads the host
+ * buffer), whatever their size, in launches of at most this many bytes of
+ * images (one image per launch when a single image is larger); pageable memory
+ * goes through the staging buffer. */
 #define IEKV_HOST_DIRECT_MAX_BYTES (64LL << 20)
 
 /* Offload to host: pack the blocks chunk by chunk into the device staging
  * buffer (two slots when it holds at least two blocks, else one) on
  * `compute`, and copy each packed chunk to host_dst with hipMemcpyAsync on
  * `copy`, so the pack of chunk k+1 overlaps the device-to-host copy of chunk
- * k. host_dst receives the block-major image [n_blocks][2L][T]; it should be
- * pinned host memory for the copies to be asynchronous. An image of at most
- * IEKV_HOST_DIRECT_MAX_BYTES whose host range lies in one pinned allocation
- * mapped for the device skips the staging buffer: the pack kernel writes
- * host_dst itself, on `compute`, and `staging` may then be null (a staged
- * offload needs at least one block image of it, IEKV_ERR_CAPACITY otherwise).
+ * k. host_dst receives the block-major image [n_blocks][2L][T]. An image whose
+ * host range lies in one pinned allocation mapped for the device, of any size,
+ * skips the staging buffer: the pack kernel writes host_dst itself, on
+ * `compute`, in launches of at most IEKV_HOST_DIRECT_MAX_BYTES of images, and
+ * `staging` may then be null (measured on MI355X: 54.4 GB/s in every round on a
+ * box where the staged pipeline's runtime copies moved 32-33 GB/s). Pageable
+ * memory is staged, which needs at least one block image of staging
+ * (IEKV_ERR_CAPACITY otherwise).
  * On return `compute` is ordered after every copy (so the staging
  * buffer and host_dst are free / complete once `compute` reaches that point).
  * `copy` may equal `compute`.
@@ -297,12 +300,12 @@ int iekv_restore_blocks(const iekv_pool* dst, const int32_t* dst_ids, int32_t n_
 /* The offload with one host image per block: block src_ids[i] is packed into
  * the image at host_blocks[i] ([2L][T] bytes, a HOST array of n_blocks
  * addresses), so each image can live in its own allocation and be freed on its
- * own. Up to IEKV_INLINE_IMAGES pinned images of at most
- * IEKV_HOST_DIRECT_MAX_BYTES together are written by one pack launch on
- * `compute`, the addresses in its kernel arguments, and `staging` may be null;
- * otherwise chunks are packed into `staging` (at least one block image) and
- * copied to the host on `copy` (one hipMemcpyAsync per run of images adjacent
- * within one allocation), as iekv_offload does.
+ * own. When every image is in pinned memory mapped for the device, pack
+ * launches on `compute` write them, up to IEKV_INLINE_IMAGES images and
+ * IEKV_HOST_DIRECT_MAX_BYTES per launch, the addresses in the kernel arguments,
+ * and `staging` may be null; otherwise chunks are packed into `staging` (at
+ * least one block image) and copied to the host on `copy` (one hipMemcpyAsync
+ * per run of images adjacent within one allocation), as iekv_offload does.
  * Replaces: the same payload reads as iekv_offload
  * (`copier.read_block(id)` in the offload hook, ie/core/block_manager.py:82),
  * for a tier that keeps each block's payload on its own. */

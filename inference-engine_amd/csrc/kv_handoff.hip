@@ -994,14 +994,15 @@ int64_t bytes_to_allocation_end(const char* p) {
   return static_cast<int64_t>(static_cast<const char*>(base) + size - p);
 }
 
-// Host transfers of at most this many bytes skip the staging buffer when the
-// host range lies in one pinned allocation mapped for the device: the move
-// kernel writes (offload) or reads (restore) the host buffer itself over the
-// host link. Measured on MI355X against the staged pipelines, one call per
-// request: one 2 MiB block offloads in 40 us instead of 525 us and restores in
-// 52 us instead of 333 us; 64 blocks of 32 KiB move at 53 GB/s instead of
-// 7 GB/s; at 16.8 MB both reach about 50 GB/s, and from 134 MB on the staged
-// pipelines are 3-5% faster (55-56 against 53-54 GB/s).
+// Host transfers skip the staging buffer when the host range lies in one pinned
+// allocation mapped for the device: the move kernel writes (offload) or reads
+// (restore) the host buffer itself over the host link, in launches of at most
+// this many bytes of images. Measured on MI355X against the staged pipelines,
+// one call per request: one 2 MiB block offloads in 40 us instead of 525 us and
+// restores in 52 us instead of 333 us; 64 blocks of 32 KiB move at 53 GB/s
+// instead of 7 GB/s. For large images the staged pipelines' runtime copies
+// reached 55-56 GB/s on some boxes but 28-39 GB/s (host to device) and 32-33
+// GB/s (device to host) on others, where the direct launches held 54-57 GB/s.
 constexpr int64_t kZeroCopyMaxBytes = IEKV_HOST_DIRECT_MAX_BYTES;
 
 // Chunk size of the unpack launches that read pinned host memory themselves (the
@@ -1370,20 +1371,31 @@ int offload_pipeline(const iekv_pool* src, IdList src_ids, int32_t n_blocks, cha
 }
 
 // The offload of n_blocks >= 1 checked blocks into one host image, with src's
-// device current. An image of at most kZeroCopyMaxBytes in one pinned,
-// device-mapped allocation is written by the pack kernel directly; otherwise
-// the staged pipeline copies each chunk with one hipMemcpyAsync.
+// device current. An image in one pinned, device-mapped allocation is written by
+// the pack kernel directly, whatever its size, in launches of at most
+// kZeroCopyMaxBytes of images; otherwise (pageable memory) the staged pipeline
+// copies each chunk with one hipMemcpyAsync. Measured on MI355X, 4 GiB of 2 MiB
+// block images into pinned memory: the direct launches moved 54.4 GB/s in every
+// round on a box where the staged pipeline's device-to-host copies moved
+// 32-33 GB/s (on another box they had reached 56.6).
 int run_offload(const iekv_pool* src, IdList src_ids, int32_t n_blocks, void* host_dst,
                 int64_t need, char* staging, int64_t staging_bytes, hipStream_t compute,
                 hipStream_t copy, OffloadEvents* preset) {
-  if (need <= kZeroCopyMaxBytes) {
-    if (char* mapped = device_view_of_host(host_dst, need)) {
-      const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(mapped)));
-      return launch_list<true, false>(src, nullptr, mapped, src_ids, n_blocks, zc_align, compute,
-                                      -1, host_write_nontemporal(src->tile_bytes));
-    }
-  }
   const int64_t block_bytes = image_bytes(src, 1);
+  if (char* mapped = device_view_of_host(host_dst, need)) {
+    const int32_t per =
+        iekv_plan::images_per_launch(n_blocks, block_bytes, kZeroCopyMaxBytes, INT32_MAX);
+    const int32_t nt = host_write_nontemporal(src->tile_bytes);
+    for (int32_t first = 0; first < n_blocks; first += per) {
+      const int32_t cnt = std::min(per, n_blocks - first);
+      char* piece = mapped + first * block_bytes;
+      const int zc_align = std::min(src->align, align_of_ptr(reinterpret_cast<uint64_t>(piece)));
+      const int rc = launch_list<true, false>(src, nullptr, piece, src_ids.from(first), cnt,
+                                              zc_align, compute, -1, nt);
+      if (rc) return rc;
+    }
+    return IEKV_OK;
+  }
   char* host = static_cast<char*>(host_dst);
   return offload_pipeline(src, src_ids, n_blocks, staging, staging_bytes, compute, copy, preset,
                           [&](char* slot, int64_t first, int32_t cnt) -> int {
@@ -1495,9 +1507,10 @@ int restore_image(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks, const 
 }
 
 // iekv_offload_blocks / iekv_offload_blocks_ids after their id checks: block
-// src_ids[i] packed into the host image at host_blocks[i]. Up to
-// IEKV_INLINE_IMAGES pinned images of at most kZeroCopyMaxBytes together are
-// written by one pack launch; otherwise the staged pipeline copies each run of
+// src_ids[i] packed into the host image at host_blocks[i]. When every image lies
+// in pinned, device-mapped memory, pack launches write them directly, up to
+// IEKV_INLINE_IMAGES images and kZeroCopyMaxBytes per launch (their addresses
+// in the kernel arguments); otherwise the staged pipeline copies each run of
 // images adjacent within one allocation with one hipMemcpyAsync.
 int offload_images(const iekv_pool* src, IdList src_ids, int32_t n_blocks,
                    void* const* host_blocks, void* staging, int64_t staging_bytes,
@@ -1511,14 +1524,27 @@ int offload_images(const iekv_pool* src, IdList src_ids, int32_t n_blocks,
   if (n_blocks == 0) return IEKV_OK;
   DeviceGuard guard(src->device);
   if (!guard.ok()) return guard.fail();
-  if (n_blocks <= IEKV_INLINE_IMAGES && block_bytes * n_blocks <= kZeroCopyMaxBytes) {
-    InlineImages images{};
-    if (device_views_of_images(host_blocks, n_blocks, block_bytes, images.addr)) {
-      const int32_t* device_ids = src_ids.on_host ? nullptr : src_ids.ids;
-      if (src_ids.on_host) std::copy(src_ids.ids, src_ids.ids + n_blocks, images.ids);
-      return launch_images<true, false>(src, images, device_ids, n_blocks, compute, -1,
-                                        host_write_nontemporal(src->tile_bytes));
+  const int32_t per = iekv_plan::images_per_launch(n_blocks, block_bytes, kZeroCopyMaxBytes,
+                                                   IEKV_INLINE_IMAGES);
+  // Every image's device address first: the call goes direct only if all of them
+  // have one, so it never mixes the two paths.
+  std::vector<uint64_t> views(n_blocks);
+  bool direct = true;
+  for (int32_t first = 0; direct && first < n_blocks; first += per)
+    direct = device_views_of_images(host_blocks + first, std::min(per, n_blocks - first),
+                                    block_bytes, views.data() + first);
+  if (direct) {
+    const int32_t nt = host_write_nontemporal(src->tile_bytes);
+    for (int32_t first = 0; first < n_blocks; first += per) {
+      const int32_t cnt = std::min(per, n_blocks - first);
+      InlineImages images{};
+      std::copy(views.begin() + first, views.begin() + first + cnt, images.addr);
+      const int32_t* device_ids = src_ids.on_host ? nullptr : src_ids.ids + first;
+      if (src_ids.on_host) std::copy(src_ids.ids + first, src_ids.ids + first + cnt, images.ids);
+      if ((rc = launch_images<true, false>(src, images, device_ids, cnt, compute, -1, nt)))
+        return rc;
     }
+    return IEKV_OK;
   }
   return offload_pipeline(
       src, src_ids, n_blocks, static_cast<char*>(staging), staging_bytes, compute, copy, nullptr,

@@ -604,10 +604,8 @@ class HipSlotCopier:
             n = len(ids)
             bufs = [self._empty_packed(1, on_host=True) for _ in range(n)]
             addresses = (ctypes.c_void_p * n)(*[b.data.data_ptr() for b in bufs])
-            # One group of pinned images within the direct limit is written by the
-            # pack kernel itself (no staging); a block image over the limit is staged.
-            staging, staging_bytes = self._staging_for(
-                n, n * self.pool.block_bytes <= _native.HOST_DIRECT_MAX)
+            # Pinned images are written by the pack kernel itself (no staging).
+            staging, staging_bytes = self._staging_for(n, True)
             fn, id_ptr = ("iekv_offload_blocks_ids", ids.host_pointer()) if ids.inline else \
                 ("iekv_offload_blocks", ids.on_device().data_ptr())
             # Pinned images of one group are written by the pack kernel on `stream`;
@@ -685,9 +683,8 @@ class HipSlotCopier:
             out = self._empty_packed(n, on_host=(location == "host"))
         if out.on_host:
             stream = torch.cuda.current_stream(self.device)
-            # A pinned image within the direct limit is written by the pack kernel.
-            staging, staging_bytes = self._staging_for(
-                n, out.pinned and out.nbytes <= _native.HOST_DIRECT_MAX)
+            # A pinned image is written by the pack kernel itself, at any size.
+            staging, staging_bytes = self._staging_for(n, out.pinned)
             copy = self.copy_stream()
             # Short host lists ride in the launches' kernel arguments (no id upload).
             fn, id_ptr = ("iekv_offload_ids", ids.host_pointer()) if ids.inline else \

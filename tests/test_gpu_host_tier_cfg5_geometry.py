@@ -5,9 +5,11 @@ images, a size that is not a power of two. On bounded pools (400 blocks, 1 GB
 each) every host path moves such blocks and is compared byte for byte with the
 NumPy restatement of the reference copier (ie/engine/copier.py:18-31):
 
-* iekv_offload of a whole list (staged: 300 images, 750 MB, above the 64 MiB
-  direct limit) into a host image pinned at exactly its size, then iekv_restore
-  of that image onto other ids (the unpack kernel reads it, 25 images per launch);
+* iekv_offload of a whole list (300 images, 750 MB) into a host image pinned at
+  exactly its size (the pack kernel writes it, 25 images per launch), then
+  iekv_restore of that image onto other ids (the unpack kernel reads it); the same
+  list through pageable memory (the staged pipelines: 102 images per staging slot,
+  runtime copies);
 * the same calls once per block on interior addresses of that image (direct);
 * the drop-in tier path: deferred evictions flushed 64 at a time into one-block
   buffers of exactly 2.5 MiB (iekv_offload_blocks_ids, 25 images per launch),
@@ -96,6 +98,25 @@ def test_whole_list_and_per_block_host_calls_at_the_70b_share_geometry(gpu):
     for d, p in zip(dst_ids, payloads):
         dst_o.write_block(d, p)
     assert_equal_pools(dk, dv, dst_o)
+
+    print("[cfg5-geometry] the same list through pageable memory (staged)", flush=True)
+    pageable = torch.empty(n * bb, dtype=torch.uint8)
+    again = [int(b) for b in rng.permutation(BLOCKS)[:n]]
+    _native.call("iekv_offload", src.native.handle, s_ids.data_ptr(), n, pageable.data_ptr(),
+                 pageable.numel(), staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                 side.cuda_stream)
+    stream.synchronize()
+    assert np.array_equal(pageable.numpy().reshape(n, 160, 16384), packed_image(payloads))
+    a_ids = dst.block_ids(again, unique=True)
+    _native.call("iekv_restore", dst.native.handle, a_ids.data_ptr(), n, pageable.data_ptr(),
+                 pageable.numel(), staging.data_ptr(), staging.numel(), stream.cuda_stream,
+                 side.cuda_stream)
+    side.synchronize()
+    stream.synchronize()
+    for d, p in zip(again, payloads):
+        dst_o.write_block(d, p)
+    assert_equal_pools(dk, dv, dst_o)
+    del pageable
 
     print("[cfg5-geometry] one call per block on 64 blocks", flush=True)
     each_src = [int(b) for b in rng.permutation(BLOCKS)[:64]]

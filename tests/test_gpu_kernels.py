@@ -622,13 +622,14 @@ def test_pinned_restores_of_any_size_leave_the_staging_buffer_untouched(gpu):
 
 
 @pytest.mark.parametrize("blocks,offset", [(72, 0), (16, 4096), (1, 0)],
-                         ids=["72MiB-staged-offload", "16MiB-interior", "1MiB"])
+                         ids=["72MiB-two-launches", "16MiB-interior", "1MiB"])
 def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, offset):
-    """1 MiB blocks to and from pinned host memory: 72 blocks exceed the 64 MiB
-    limit of the direct offload and go through the staged pipeline, and are
-    restored directly in two unpack launches (64 and 8 blocks); 16 blocks at an
-    offset inside a larger pinned buffer, and a single block, go direct both
-    ways. Bytes equal the oracle's on the host and back in the pool."""
+    """1 MiB blocks to and from pinned host memory, always moved by the kernels
+    themselves: 72 blocks exceed the 64 MiB a direct launch takes and go in two
+    pack and two unpack launches (64 and 8 blocks); 16 blocks at an offset inside
+    a larger pinned buffer, and a single block, in one each. The staging buffer
+    keeps its sentinel bytes. Bytes equal the oracle's on the host and back in
+    the pool."""
     from iekv import _native
     from iekv.engine.pools import KVPool
 
@@ -641,7 +642,7 @@ def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, o
     block = src.block_bytes
     buf = torch.empty(offset + blocks * block + 4096, dtype=torch.uint8, pin_memory=True)
     host = buf[offset:offset + blocks * block]
-    staging = torch.empty(4 * block, dtype=torch.uint8, device=gpu)
+    staging = torch.full((4 * block,), 0xA5, dtype=torch.uint8, device=gpu)
     stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
     _native.call("iekv_offload", src.native.handle, src.block_ids(src_ids).data_ptr(), blocks,
                  host.data_ptr(), host.numel(), staging.data_ptr(), staging.numel(),
@@ -657,6 +658,7 @@ def test_pinned_host_transfers_on_either_side_of_the_direct_limit(gpu, blocks, o
     for d, p in zip(dst_ids, payloads):
         dst_o.write_block(d, p)
     assert_pool_equals(dk, dv, dst_o)
+    assert bool((staging == 0xA5).all())
 
 
 @pytest.mark.parametrize("shape,blocks,pinned", [
@@ -786,45 +788,49 @@ def test_deferred_offloads_keep_one_buffer_per_block(gpu):
 
 
 def test_staged_host_calls_on_two_streams_share_one_staging_buffer(gpu):
-    """A host copier has one device staging buffer for all its staged transfers.
-    Two offloads larger than IEKV_HOST_DIRECT_MAX_BYTES issued back to back on two
-    streams, then two restores of them on the two streams, must each see only its
-    own bytes: the second call on a new stream is ordered after the first one's
-    use of the buffer. A third, larger offload then replaces the buffer while the
-    previous calls may still run. Bytes equal the oracle's."""
-    from iekv import _native
-    from iekv.engine.copier import HipSlotCopier
+    """A host copier has one device staging buffer for all its staged transfers
+    (restores of pageable payloads; pinned ones are read by the kernel itself).
+    Two restores of pageable payloads issued back to back on two streams must
+    each write only their own bytes: the second call on a new stream is ordered
+    after the first one's use of the buffer. A third, larger restore then
+    replaces the buffer while the previous calls may still run. The pinned
+    offloads that made the payloads used no staging. Bytes equal the oracle's."""
+    from iekv.engine.copier import HipSlotCopier, PackedBlocks
 
     bs, layers, heads, dim = 16, 2, 8, 128               # 128 KiB block images
     sk, sv = allocate(2000, bs, layers, heads, dim, torch.bfloat16, gpu, seed=91)
     dk, dv = allocate(2000, bs, layers, heads, dim, torch.bfloat16, gpu, seed=92)
     src = HipSlotCopier(sk, sv, bs, payload_location="host", defer_reads=False)
     dst = HipSlotCopier(dk, dv, bs)
-    image = src.pool.block_bytes
-    n = _native.HOST_DIRECT_MAX // image + 40           # staged, one chunk each
+    n = 300                                  # 37.5 MiB: more than the first buffer holds
     rng = np.random.default_rng(93)
     order = [int(b) for b in rng.permutation(2000)]
-    ids_a, ids_b, ids_c = order[:n], order[n:2 * n], order[2 * n:3 * n + 100]
-    assert len(ids_c) == n + 100
+    ids_a, ids_b, ids_c = order[:n], order[n:2 * n], order[2 * n:3 * n + 900]
     main = torch.cuda.current_stream()
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
     s1.wait_stream(main)
     s2.wait_stream(main)
-    a = src.read_blocks(ids_a, stream=s1)
-    b = src.read_blocks(ids_b, stream=s2)
-    c = src.read_blocks(ids_c, stream=s1)                # a larger staging buffer
+    pinned = [src.read_blocks(ids, stream=s) for ids, s in ((ids_a, s1), (ids_b, s2),
+                                                            (ids_c, s1))]
+    assert src._staging is None                          # pinned offloads: direct
+    pageable = [PackedBlocks(p.synchronize().data.clone(), layers, (bs, heads, dim),
+                             torch.bfloat16) for p in pinned]
+    assert not any(p.pinned for p in pageable)
     targets = [int(t) for t in rng.permutation(2000)]
-    da, db = targets[:n], targets[n:2 * n]
-    dst.write_blocks(da, a, stream=s2)
-    dst.write_blocks(db, b, stream=s1)
+    da, db, dc = targets[:n], targets[n:2 * n], targets[2 * n:3 * n + 900]
+    dst.write_blocks(da, pageable[0], stream=s2)
+    dst.write_blocks(db, pageable[1], stream=s1)
+    first = dst._staging
+    dst.write_blocks(dc, pageable[2], stream=s2)         # a larger staging buffer
+    assert first is not None and dst._staging.numel() > first.numel()
     main.wait_stream(s1)
     main.wait_stream(s2)
     torch.cuda.synchronize()
     src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
-    for payload, ids in ((a, ids_a), (b, ids_b), (c, ids_c)):
+    for payload, ids in zip(pinned, (ids_a, ids_b, ids_c)):
         got = payload.synchronize().data.view(torch.uint8).numpy()
         assert np.array_equal(got, packed_image(pack(src_o, ids)))
-    handoff(src_o, dst_o, [ids_a, ids_b], [da, db])
+    handoff(src_o, dst_o, [ids_a, ids_b, ids_c], [da, db, dc])
     assert_pool_equals(dk, dv, dst_o)
 
 

@@ -101,8 +101,9 @@ def test_static_offload_of_nothing_enqueues_nothing(gpu):
 
 
 def staged_case(gpu, seed):
-    """A pool of 1 MiB block images (32 arrays of 32 KiB tiles): a call of more than
-    64 images goes through the static buffer's two 16 MiB slots."""
+    """A pool of 1 MiB block images (32 arrays of 32 KiB tiles). Offloads into
+    pageable memory go through the static buffer's two 16 MiB slots (pinned images
+    are written by the pack kernel itself and use no staging)."""
     from iekv.engine.pools import KVPool
 
     k, v = random_pool(400, 16, 16, 8, 128, gpu, seed=seed)
@@ -122,7 +123,7 @@ def test_static_offloads_on_unrelated_streams_wait_for_each_other(gpu):
         ids = [int(b) for b in rng.permutation(400)[:n]]
         dev_ids = pool.block_ids(ids)
         torch.cuda.current_stream().synchronize()      # the ids are on the device
-        host = host_buffer(n, pool.n_arrays, pool.tile_bytes, True)
+        host = host_buffer(n, pool.n_arrays, pool.tile_bytes, False)
         calls.append((ids, dev_ids, host, compute))
     print("[no-alloc] three staged calls on three stream pairs, no host sync", flush=True)
     for (ids, dev_ids, host, compute), (_, copy) in zip(calls, pairs):
@@ -145,7 +146,7 @@ def test_static_offloads_from_two_threads_share_the_buffer(gpu):
         for n in (90, 120, 66):
             ids = [int(b) for b in rng.permutation(400)[:n]]
             jobs.append((ids, pool.block_ids(ids),
-                         host_buffer(n, pool.n_arrays, pool.tile_bytes, True)))
+                         host_buffer(n, pool.n_arrays, pool.tile_bytes, False)))
         plans.append((compute, copy, jobs))
     torch.cuda.synchronize()
     errors = []
