@@ -46,6 +46,7 @@ struct iekv_pool {
   uint64_t* table;  // table mode: device copy of the n_arrays base addresses (else null)
   int32_t align;    // largest power of two <= 16 dividing tile_bytes and every base address
   std::vector<uint64_t> arrays;   // the n_arrays base addresses (host copy)
+  uint64_t lo, hi;  // the byte range the arrays span: [lowest base, highest base + array)
 };
 
 // Staging buffer of iekv_offload_static, the allocation-free offload: every
@@ -937,7 +938,7 @@ enum Aliasing { kSeparate = 0, kSamePool = 1, kPartial = 2 };
 
 Aliasing pool_aliasing(const iekv_pool* a, const iekv_pool* b) {
   if (a == b) return kSamePool;
-  if (a->device != b->device) return kSeparate;
+  if (a->device != b->device || a->hi <= b->lo || b->hi <= a->lo) return kSeparate;
   if (a->arrays == b->arrays && a->tile_bytes == b->tile_bytes &&
       a->num_blocks == b->num_blocks)
     return kSamePool;
@@ -1691,6 +1692,8 @@ int iekv_pool_create(const uint64_t* array_ptrs, int32_t n_arrays, int64_t tile_
   p->num_blocks = num_blocks;
   p->align = align;
   p->arrays.assign(array_ptrs, array_ptrs + n_arrays);
+  p->lo = sorted.front();
+  p->hi = sorted.back() + static_cast<uint64_t>(array_bytes);
   if (slab) {
     p->base = array_ptrs[0];
     p->stride = stride;

@@ -178,8 +178,12 @@ class KVPool:
         self.dtype = first.dtype
         self.device = first.device
         self._arrays = arrays  # keeps the memory alive while the handle exists
-        self.native = _native.Pool([t.data_ptr() for t in arrays], self.tile_bytes,
-                                   self.num_blocks, self.device.index or 0)
+        # Array addresses and the byte range they span, for comparing pools by memory
+        # (memory_relation) without asking torch again on every call.
+        self._ptrs = tuple(t.data_ptr() for t in arrays)
+        self._span = (min(self._ptrs), max(self._ptrs) + self.num_blocks * self.tile_bytes)
+        self.native = _native.Pool(list(self._ptrs), self.tile_bytes, self.num_blocks,
+                                   self.device.index or 0)
         self._check_buffers: tuple[torch.Tensor, torch.Tensor] | None = None
 
     @property
@@ -191,13 +195,15 @@ class KVPool:
         arrays, also through another KVPool made over the same caches), ``"partial"``
         (arrays that overlap without being the same) or ``"separate"``. Block ids of one
         pool mean the same blocks of the other only when they are the same."""
-        mine = [t.data_ptr() for t in self._arrays]
-        theirs = [t.data_ptr() for t in other._arrays]
+        if other is self:
+            return "same"
+        if self.device != other.device or self._span[1] <= other._span[0] or \
+                other._span[1] <= self._span[0]:
+            return "separate"          # the usual case, decided without a sort
+        mine, theirs = self._ptrs, other._ptrs
         if mine == theirs and (self.tile_bytes, self.num_blocks) == (other.tile_bytes,
                                                                      other.num_blocks):
             return "same"
-        if self.device != other.device:
-            return "separate"
         span = self.num_blocks * self.tile_bytes
         other_span = other.num_blocks * other.tile_bytes
         spans = sorted([(a, a + span, 0) for a in mine] + [(b, b + other_span, 1)
