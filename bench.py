@@ -193,7 +193,7 @@ def check_host_budget(plan: dict, budget: int | None) -> None:
 
 class Legs:
     def __init__(self, workload, device, seed: int, pool_layout: str = "paired",
-                 streams: int = 1) -> None:
+                 streams: int = 1, pad_blocks: int = 0) -> None:
         import torch
 
         from iekv.engine.copier import issue_order
@@ -208,18 +208,21 @@ class Legs:
         if pool_layout == "paired":
             (self.src_k, self.src_v), (self.dst_k, self.dst_v) = allocate_pool_pair(
                 workload.src_pool_blocks, workload.dst_pool_blocks, s.block_size, s.layers,
-                s.kv_heads, s.head_dim, dtype=dtype, device=device, zero=False)
+                s.kv_heads, s.head_dim, dtype=dtype, device=device, zero=False,
+                pad_blocks=pad_blocks)
             fill_pool(self.src_k + self.src_v, s.dtype, seed)
             for t in self.dst_k + self.dst_v:
                 t.zero_()
         else:
             self.src_k, self.src_v = allocate_pool(workload.src_pool_blocks, s.block_size,
                                                    s.layers, s.kv_heads, s.head_dim, dtype=dtype,
-                                                   device=device, zero=False)
+                                                   device=device, zero=False,
+                                                   pad_blocks=pad_blocks)
             fill_pool(self.src_k + self.src_v, s.dtype, seed)
             self.dst_k, self.dst_v = allocate_pool(workload.dst_pool_blocks, s.block_size,
                                                    s.layers, s.kv_heads, s.head_dim, dtype=dtype,
-                                                   device=device, zero=True)
+                                                   device=device, zero=True,
+                                                   pad_blocks=pad_blocks)
         self.src = KVPool(self.src_k, self.src_v, s.block_size)
         self.dst = KVPool(self.dst_k, self.dst_v, s.block_size)
         # pack/unpack move blocks in table order (the payload layout); direct copies
@@ -1207,6 +1210,8 @@ def ab_ok(spec: str, config: str) -> bool:
         return all(v.isdigit() and 1 <= int(v) <= 8 for v in values)
     if key == "slack":
         return config in ("cfg3", "cfg4") and all(v == "engine" or v.isdigit() for v in values)
+    if key == "pad":
+        return all(v.isdigit() and int(v) <= 4096 for v in values)
     if key in LAUNCH_AB:
         return all(v.isdigit() and LAUNCH_AB[key][1](int(v)) for v in values)
     return False
@@ -1255,7 +1260,7 @@ def ab(args, names: list[str], device) -> int:
         counts = [int(v) for v in values]
         w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
         legs = Legs(w, device, args.seed, "separate" if args.separate_pools else "paired",
-                    streams=max(counts))
+                    streams=max(counts), pad_blocks=args.pad)
         streams, stagings = legs.streams, legs.stagings
         for rnd in range(args.rounds):
             for n in counts:
@@ -1269,7 +1274,7 @@ def ab(args, names: list[str], device) -> int:
                 w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
                 legs = Legs(w, device, args.seed,
                             "separate" if args.separate_pools else "paired",
-                            streams=args.streams)
+                            streams=args.streams, pad_blocks=args.pad)
                 for v in values:
                     _native.set_launch(**{LAUNCH_AB[key][0]: int(v)})
                     measure(legs, rnd, v)
@@ -1277,6 +1282,16 @@ def ab(args, names: list[str], device) -> int:
                 torch.cuda.empty_cache()
         finally:
             _native.set_launch(**before)
+    elif key == "pad":
+        w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
+        for rnd in range(args.rounds):
+            for v in values:
+                legs = Legs(w, device, args.seed,
+                            "separate" if args.separate_pools else "paired",
+                            streams=args.streams, pad_blocks=int(v))
+                measure(legs, rnd, v)
+                del legs
+                torch.cuda.empty_cache()
     else:
         for rnd in range(args.rounds):
             for v in values:
@@ -1284,7 +1299,7 @@ def ab(args, names: list[str], device) -> int:
                 w = workloads.make(args.config, args.seed, slack, tp=args.tp)
                 legs = Legs(w, device, args.seed,
                             "separate" if args.separate_pools else "paired",
-                            streams=args.streams)
+                            streams=args.streams, pad_blocks=args.pad)
                 measure(legs, rnd, v)
                 del legs
                 torch.cuda.empty_cache()
@@ -1334,13 +1349,16 @@ def main() -> int:
     ap.add_argument("--ab", default="",
                     help="in-process A/B instead of the benchmark line: streams=1,2,4 (one set "
                          "of pools), slack=64,6600,engine (pools re-made per value; cfg3/cfg4), "
-                         "or a launch setting such as direct_chunk=4096,8192,0 or "
+                         "pad=0,1 (pools re-made per value with that many unused blocks after "
+                         "each array), or a launch setting such as direct_chunk=4096,8192,0 or "
                          "pack_order=0,4 (pools re-made per round, every value "
                          "on each)")
     ap.add_argument("--rounds", type=int, default=3, help="rounds of an --ab comparison")
     ap.add_argument("--floor", action="store_true",
                     help="measure the launch floor (empty kernels, one-tile moves, the small "
                          "workloads' requests) instead of the benchmark line")
+    ap.add_argument("--pad", type=int, default=0,
+                    help="unused blocks after each pool array (array stride = pool blocks + PAD)")
     ap.add_argument("--separate-pools", action="store_true",
                     help="allocate the two pools separately instead of as one reservation "
                          "(prefill pool first)")
@@ -1356,7 +1374,8 @@ def main() -> int:
     if args.ab and not ab_ok(args.ab, args.config):
         print("--ab takes streams=N,... (N in 1..8), a launch setting ("
               + ", ".join(f"{k}=V,..." for k in LAUNCH_AB)
-              + ") or, for cfg3 and cfg4, slack=N|engine,...", file=sys.stderr)
+              + "), pad=N,... (blocks after each pool array) or, for cfg3 and cfg4, "
+              "slack=N|engine,...", file=sys.stderr)
         return 2
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -1396,7 +1415,7 @@ def main() -> int:
         print(json.dumps({"launch_floor": floor}), flush=True)
         return 0 if floor["verified"] else 1
     legs = Legs(w, device, args.seed, "separate" if args.separate_pools else "paired",
-                streams=args.streams)
+                streams=args.streams, pad_blocks=args.pad)
     P = w.payload_bytes
     if args.sweep:
         names = [x for x in args.legs.split(",")

@@ -120,6 +120,31 @@ def test_a_pool_pair_is_one_allocation_with_the_first_pool_below():
     assert all(not t.any() for t in bk + bv + ak)
 
 
+def test_padded_pools_space_their_arrays_by_the_padding():
+    """pad_blocks leaves unused blocks after every array: arrays keep the reference's
+    [N*bs, H, D] shape and stay contiguous, consecutive arrays start (N + pad) tiles
+    apart, and the second pool of a pair starts after the first's padded slab."""
+    import torch
+
+    from iekv.engine.pools import allocate_pool, allocate_pool_pair
+
+    tile = 4 * 2 * 8 * 2                               # bs 4, H 2, D 8, bf16
+    k, v = allocate_pool(6, 4, 3, 2, 8, dtype=torch.bfloat16, device="cpu", pad_blocks=1)
+    assert all(t.shape == (24, 2, 8) and t.is_contiguous() for t in k + v)
+    arrays = k + v
+    for a, b in zip(arrays, arrays[1:]):
+        assert b.data_ptr() - a.data_ptr() == 7 * tile
+    (ak, av), (bk, bv) = allocate_pool_pair(5, 7, 4, 3, 2, 8, dtype=torch.bfloat16,
+                                            device="cpu", pad_blocks=3)
+    assert all(t.shape == (20, 2, 8) for t in ak + av)
+    assert all(t.shape == (28, 2, 8) for t in bk + bv)
+    assert av[0].data_ptr() - ak[0].data_ptr() == 3 * 8 * tile
+    assert bk[0].data_ptr() - ak[0].data_ptr() == 2 * 3 * 8 * tile
+    assert bk[1].data_ptr() - bk[0].data_ptr() == 10 * tile
+    with pytest.raises(ValueError):
+        allocate_pool(6, 4, 3, 2, 8, device="cpu", pad_blocks=-1)
+
+
 def test_the_engine_accepts_preallocated_caches_of_its_size():
     import torch
 
