@@ -1223,7 +1223,9 @@ def ab(args, names: list[str], device) -> int:
     ``streams=1,2,4``: one set of pools, request streams switched between
     values. ``slack=64,6600,engine``: pools re-made for each value (cfg3 or
     cfg4 sized to the workload plus that many spare blocks, ``engine`` for the
-    default pools), so every round also draws a new physical placement.
+    default pools), so every round also draws a new physical placement;
+    ``pad=0,1``: the same, with that many unused blocks after each array. For
+    these two the values run in reverse order every other round.
     ``direct_chunk=4096,8192,0`` (or another launch setting: ``chunk``,
     ``order``, ``pack_order``, ``unroll``, ``nontemporal``, ``run``): pools
     re-made for each round, and every value of the setting measured on the same
@@ -1236,7 +1238,7 @@ def ab(args, names: list[str], device) -> int:
 
     key, _, raw = args.ab.partition("=")
     values = [v for v in raw.split(",") if v]
-    legs_names = [n for n in names if n in HANDOFF_LEGS]
+    legs_names = [n for n in names if n in HANDOFF_LEGS or n in SLOT_LEGS]
     rows, ok = [], True
     legs = None
 
@@ -1247,7 +1249,8 @@ def ab(args, names: list[str], device) -> int:
         row = {"round": rnd, "value": value,
                "pools": [w.src_pool_blocks, w.dst_pool_blocks]}
         for name in legs_names:
-            legs.clear_dst()
+            if name not in ("gather_context", "gather_per_array"):
+                legs.clear_dst()
             ms, _, _ = time_leg(legs, name, args.steps, args.warmup, per_launch=False)
             row[name] = round(sum(b for b, _ in legs.plan(name)) / (ms * 1e-3) / 1e9, 1)
             if not legs.check(name):
@@ -1285,7 +1288,9 @@ def ab(args, names: list[str], device) -> int:
     elif key == "pad":
         w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
         for rnd in range(args.rounds):
-            for v in values:
+            # Re-made pools have alternated between two physical placements: reversing
+            # the order every other round lets each value land on both.
+            for v in (values if rnd % 2 == 0 else values[::-1]):
                 legs = Legs(w, device, args.seed,
                             "separate" if args.separate_pools else "paired",
                             streams=args.streams, pad_blocks=int(v))
@@ -1294,7 +1299,7 @@ def ab(args, names: list[str], device) -> int:
                 torch.cuda.empty_cache()
     else:
         for rnd in range(args.rounds):
-            for v in values:
+            for v in (values if rnd % 2 == 0 else values[::-1]):
                 slack = None if v == "engine" else int(v)
                 w = workloads.make(args.config, args.seed, slack, tp=args.tp)
                 legs = Legs(w, device, args.seed,
