@@ -235,10 +235,13 @@ __device__ __forceinline__ void move_entry(const PoolView& src, const PoolView& 
   const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
   const int chunk_vecs = tile_vecs / parts;
   const int64_t chunk_offset = static_cast<int64_t>(p) * chunk_vecs * sizeof(V);
-  if constexpr (IEKV_UNPACK_LOAD_FIRST && !SRC_POOL && DST_POOL) {
+  if constexpr (IEKV_UNPACK_LOAD_FIRST && !SRC_POOL && DST_POOL && U <= 4) {
     // Staging to pool: the chunk's address in the staging image does not depend
     // on the destination id, so its first vectors are loaded before the id is
-    // checked and the two latencies overlap.
+    // checked and the two latencies overlap. Only for up to 4 vectors per lane:
+    // with 8, the compiler kept a whole 32 KiB tile in registers (240 VGPRs, 2
+    // waves per SIMD) and whole-tile unpacks fell from 6.7 to 4.2 TB/s; the
+    // default 4 KiB chunks move one vector per lane.
     const gptr<const V> gs =
         as_global<V>(src_stage + (entry * n_arrays + a) * tile_bytes + chunk_offset);
     const int t = threadIdx.x;

@@ -1342,3 +1342,44 @@ def test_launch_timer_times_each_library_launch(gpu):
     with _native.LaunchTimer(2) as timer:     # a session with no launches
         pass
     assert timer.durations_ms == []
+
+
+@pytest.mark.parametrize("pad", [1, 3])
+def test_padded_pools_move_bit_exactly(gpu, pad):
+    """Pools whose arrays are padded by unused blocks (pad_blocks) are still one slab
+    of equally spaced arrays: direct copies, pack -> unpack and a host round trip
+    between a padded and an unpadded pool equal the oracle's, and the padding
+    bytes are never written."""
+    from iekv.engine.copier import HipSlotCopier
+    from iekv.engine.pools import allocate_pool
+
+    bs, layers, heads, dim = 16, 3, 2, 64
+    sk, sv = allocate_pool(40, bs, layers, heads, dim, dtype=torch.bfloat16, device=gpu,
+                           zero=False, pad_blocks=pad)
+    slab = sk[0]._base
+    raw = slab.view(torch.uint8)
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(61 + pad)
+    raw.copy_(torch.randint(0, 256, raw.shape, dtype=torch.uint8, device=gpu, generator=gen))
+    dk, dv = allocate_pool(50, bs, layers, heads, dim, dtype=torch.bfloat16, device=gpu,
+                           zero=True, pad_blocks=pad)
+    dslab = dk[0]._base
+    dslab.view(torch.uint8).fill_(0x5A)
+    for t in dk + dv:
+        t.zero_()                                     # the arrays; padding keeps 0x5A
+    src = HipSlotCopier(sk, sv, bs, payload_location="host")
+    dst = HipSlotCopier(dk, dv, bs)
+    assert src.pool.native.handle.value and len(sk[0].shape) == 3
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    rng = np.random.default_rng(62)
+    a_src, a_dst = random_tables(rng, 40, 50, 12)
+    dst.copy_blocks(src, a_src, a_dst)
+    b_src = [int(b) for b in rng.permutation(40)[:9]]
+    b_dst = [int(b) for b in rng.permutation([b for b in range(50) if b not in a_dst])[:9]]
+    dst.write_blocks(b_dst, src.read_blocks(b_src))            # host round trip
+    torch.cuda.synchronize()
+    handoff(src_o, dst_o, [a_src, b_src], [a_dst, b_dst])
+    assert_pool_equals(dk, dv, dst_o)
+    rows = 50 * bs
+    padding = dslab.view(2, layers, -1, heads, dim)[:, :, rows:]
+    assert bool((padding.contiguous().view(torch.uint8) == 0x5A).all())
