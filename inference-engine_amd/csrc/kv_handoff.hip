@@ -226,7 +226,7 @@ __device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
 // staging image of the entry) to pool tile dst_id (or the staging image).
 // Ids outside their pool move nothing, so a bad id never addresses memory
 // outside the pool.
-template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL, bool HOST = false>
 __device__ __forceinline__ void move_entry(const PoolView& src, const PoolView& dst,
                                            const char* src_stage, char* dst_stage,
                                            int32_t src_id, int32_t dst_id, int64_t entry,
@@ -235,13 +235,17 @@ __device__ __forceinline__ void move_entry(const PoolView& src, const PoolView& 
   const int64_t tile_bytes = static_cast<int64_t>(tile_vecs) * sizeof(V);
   const int chunk_vecs = tile_vecs / parts;
   const int64_t chunk_offset = static_cast<int64_t>(p) * chunk_vecs * sizeof(V);
-  if constexpr (IEKV_UNPACK_LOAD_FIRST && !SRC_POOL && DST_POOL && U <= 4) {
+  if constexpr (IEKV_UNPACK_LOAD_FIRST && !SRC_POOL && DST_POOL && (U <= 4 || HOST)) {
     // Staging to pool: the chunk's address in the staging image does not depend
     // on the destination id, so its first vectors are loaded before the id is
-    // checked and the two latencies overlap. Only for up to 4 vectors per lane:
-    // with 8, the compiler kept a whole 32 KiB tile in registers (240 VGPRs, 2
-    // waves per SIMD) and whole-tile unpacks fell from 6.7 to 4.2 TB/s; the
-    // default 4 KiB chunks move one vector per lane.
+    // checked and the two latencies overlap. From HBM staging only for up to 4
+    // vectors per lane: with 8, the compiler kept a whole 32 KiB tile in
+    // registers (240 VGPRs, 2 waves per SIMD) and whole-tile unpacks fell from
+    // 6.7 to 4.2 TB/s (the default 4 KiB chunks move one vector per lane). An
+    // unpack that reads pinned host memory (HOST) keeps it at any width: there
+    // the lower occupancy measured faster on 32 KiB tiles (a 37 GB restore 56.7
+    // against 53.7 GB/s, one 2 MiB block per call 50.4 against 43.1), the host
+    // link taking fewer reads in flight.
     const gptr<const V> gs =
         as_global<V>(src_stage + (entry * n_arrays + a) * tile_bytes + chunk_offset);
     const int t = threadIdx.x;
@@ -325,7 +329,7 @@ __device__ __forceinline__ void move_group(const PoolView& src, const PoolView& 
 // grouped path keeps at most 4 vectors per lane in flight: each one carries
 // its own source and destination address, and at 8 the kernel's register
 // count would lower the occupancy of every launch it serves.
-template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL, bool HOST = false>
 __device__ __forceinline__ void move_unit(const PoolView& src, const PoolView& dst,
                                           const char* src_stage, char* dst_stage,
                                           int32_t src_id, int32_t dst_id, int64_t entry,
@@ -336,7 +340,7 @@ __device__ __forceinline__ void move_unit(const PoolView& src, const PoolView& d
         src, dst, src_stage, dst_stage, src_id, dst_id, entry, a * group, tile_vecs, group,
         n_arrays);
   else
-    move_entry<V, U, NT, SRC_POOL, DST_POOL>(src, dst, src_stage, dst_stage, src_id, dst_id,
+    move_entry<V, U, NT, SRC_POOL, DST_POOL, HOST>(src, dst, src_stage, dst_stage, src_id, dst_id,
                                              entry, a, p, tile_vecs, parts, n_arrays);
 }
 
@@ -344,7 +348,7 @@ __device__ __forceinline__ void move_unit(const PoolView& src, const PoolView& d
 // (scalar) loads: staging it in LDS would add a store, a barrier and a load
 // before the first data access of a workgroup that lives for a single chunk.
 // A run of several blocks stages its slice of the src -> dst id map in LDS.
-template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL, bool HOST>
 __global__ void __launch_bounds__(kThreads)
 kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
         char* __restrict__ dst_stage, const int32_t* __restrict__ src_ids,
@@ -357,7 +361,7 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
                             order);
   const int first = pl.r * run;
   if (run == 1) {
-    move_unit<V, U, NT, SRC_POOL, DST_POOL>(
+    move_unit<V, U, NT, SRC_POOL, DST_POOL, HOST>(
         src, dst, src_stage, dst_stage, SRC_POOL ? src_ids[first] : 0,
         DST_POOL ? dst_ids[first] : 0, first, pl.a, pl.p, tile_vecs, parts, group, n_arrays);
     return;
@@ -370,7 +374,7 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
   }
   __syncthreads();
   for (int j = 0; j < count; ++j)
-    move_unit<V, U, NT, SRC_POOL, DST_POOL>(
+    move_unit<V, U, NT, SRC_POOL, DST_POOL, HOST>(
         src, dst, src_stage, dst_stage, SRC_POOL ? s_src[j] : 0, DST_POOL ? s_dst[j] : 0,
         first + j, pl.a, pl.p, tile_vecs, parts, group, n_arrays);
 }
@@ -383,7 +387,7 @@ struct InlineIds {
   int32_t v[2 * IEKV_INLINE_IDS];
 };
 
-template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL, bool HOST>
 __global__ void __launch_bounds__(kThreads)
 kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
                char* __restrict__ dst_stage, InlineIds ids, int32_t id_base, int32_t dst_off,
@@ -392,7 +396,7 @@ kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
   const Place pl = place_at(blockIdx.x, gridDim.x, (n_arrays + group - 1) / group, runs, parts,
                             order);
   const int i = id_base + pl.r;
-  move_unit<V, U, NT, SRC_POOL, DST_POOL>(
+  move_unit<V, U, NT, SRC_POOL, DST_POOL, HOST>(
       src, dst, src_stage, dst_stage, SRC_POOL ? ids.v[i] : 0, DST_POOL ? ids.v[dst_off + i] : 0,
       i, pl.a, pl.p, tile_vecs, parts, group, n_arrays);
 }
@@ -409,7 +413,7 @@ struct InlineImages {
   int32_t ids[IEKV_INLINE_IMAGES];  // block ids, when they come from host memory
 };
 
-template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL>
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL, bool HOST>
 __global__ void __launch_bounds__(kThreads)
 kv_move_images(PoolView src, PoolView dst, const char* __restrict__ /*src_stage*/,
                char* __restrict__ /*dst_stage*/, InlineImages images,
@@ -422,7 +426,7 @@ kv_move_images(PoolView src, PoolView dst, const char* __restrict__ /*src_stage*
   const uint64_t image_bytes = static_cast<uint64_t>(n_arrays) * tile_vecs * sizeof(V);
   char* stage = reinterpret_cast<char*>(images.addr[i] - i * image_bytes);
   const int32_t id = ids ? ids[i] : images.ids[i];
-  move_unit<V, U, NT, SRC_POOL, DST_POOL>(src, dst, stage, stage, SRC_POOL ? id : 0,
+  move_unit<V, U, NT, SRC_POOL, DST_POOL, HOST>(src, dst, stage, stage, SRC_POOL ? id : 0,
                                           DST_POOL ? id : 0, i, pl.a, pl.p, tile_vecs, parts,
                                           group, n_arrays);
 }
@@ -711,38 +715,65 @@ using InlineKernel = void (*)(PoolView, PoolView, const char*, char*, InlineIds,
     *vec_bytes = 16;                                                            \
     const int u = std::min(unroll, lane_vecs);                                  \
     if (nt) {                                                                   \
-      if (u >= 16) return KERNEL<u32x4, 16, true, SP, DP>;                      \
-      if (u >= 8) return KERNEL<u32x4, 8, true, SP, DP>;                        \
-      if (u >= 4) return KERNEL<u32x4, 4, true, SP, DP>;                        \
-      if (u >= 2) return KERNEL<u32x4, 2, true, SP, DP>;                        \
-      return KERNEL<u32x4, 1, true, SP, DP>;                                    \
+      if (u >= 16) return KERNEL<u32x4, 16, true, SP, DP, HP>;                      \
+      if (u >= 8) return KERNEL<u32x4, 8, true, SP, DP, HP>;                        \
+      if (u >= 4) return KERNEL<u32x4, 4, true, SP, DP, HP>;                        \
+      if (u >= 2) return KERNEL<u32x4, 2, true, SP, DP, HP>;                        \
+      return KERNEL<u32x4, 1, true, SP, DP, HP>;                                    \
     }                                                                           \
-    if (u >= 16) return KERNEL<u32x4, 16, false, SP, DP>;                       \
-    if (u >= 8) return KERNEL<u32x4, 8, false, SP, DP>;                         \
-    if (u >= 4) return KERNEL<u32x4, 4, false, SP, DP>;                         \
-    if (u >= 2) return KERNEL<u32x4, 2, false, SP, DP>;                         \
-    return KERNEL<u32x4, 1, false, SP, DP>;                                     \
+    if (u >= 16) return KERNEL<u32x4, 16, false, SP, DP, HP>;                       \
+    if (u >= 8) return KERNEL<u32x4, 8, false, SP, DP, HP>;                         \
+    if (u >= 4) return KERNEL<u32x4, 4, false, SP, DP, HP>;                         \
+    if (u >= 2) return KERNEL<u32x4, 2, false, SP, DP, HP>;                         \
+    return KERNEL<u32x4, 1, false, SP, DP, HP>;                                     \
   }                                                                             \
-  if (align >= 8) { *vec_bytes = 8; return KERNEL<u32x2, 4, false, SP, DP>; }   \
-  if (align >= 4) { *vec_bytes = 4; return KERNEL<uint32_t, 4, false, SP, DP>; } \
-  if (align >= 2) { *vec_bytes = 2; return KERNEL<uint16_t, 4, false, SP, DP>; } \
+  if (align >= 8) { *vec_bytes = 8; return KERNEL<u32x2, 4, false, SP, DP, HP>; }   \
+  if (align >= 4) { *vec_bytes = 4; return KERNEL<uint32_t, 4, false, SP, DP, HP>; } \
+  if (align >= 2) { *vec_bytes = 2; return KERNEL<uint16_t, 4, false, SP, DP, HP>; } \
   *vec_bytes = 1;                                                               \
-  return KERNEL<uint8_t, 4, false, SP, DP>;
+  return KERNEL<uint8_t, 4, false, SP, DP, HP>;
 
-template <bool SP, bool DP>
-MoveKernel pick_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
+template <bool SP, bool DP, bool HP>
+MoveKernel pick_kernel_as(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
   IEKV_PICK(kv_move)
 }
 
-template <bool SP, bool DP>
-InlineKernel pick_inline_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
+template <bool SP, bool DP, bool HP>
+InlineKernel pick_inline_kernel_as(int align, int unroll, int lane_vecs, bool nt,
+                                   int* vec_bytes) {
   IEKV_PICK(kv_move_inline)
 }
-template <bool SP, bool DP>
-ImagesKernel pick_images_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
+template <bool SP, bool DP, bool HP>
+ImagesKernel pick_images_kernel_as(int align, int unroll, int lane_vecs, bool nt,
+                                   int* vec_bytes) {
   IEKV_PICK(kv_move_images)
 }
 #undef IEKV_PICK
+
+// The kernels of a move; `host`: an unpack that reads pinned host memory (move_entry's
+// HOST variant). Only unpacks have one.
+#define IEKV_PICK_HOST(NAME)                                                           \
+  if constexpr (!SP && DP) {                                                           \
+    if (host) return NAME##_as<SP, DP, true>(align, unroll, lane_vecs, nt, vec_bytes); \
+  }                                                                                    \
+  return NAME##_as<SP, DP, false>(align, unroll, lane_vecs, nt, vec_bytes);
+
+template <bool SP, bool DP>
+MoveKernel pick_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes,
+                       bool host = false) {
+  IEKV_PICK_HOST(pick_kernel)
+}
+template <bool SP, bool DP>
+InlineKernel pick_inline_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes,
+                                bool host = false) {
+  IEKV_PICK_HOST(pick_inline_kernel)
+}
+template <bool SP, bool DP>
+ImagesKernel pick_images_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes,
+                                bool host = false) {
+  IEKV_PICK_HOST(pick_images_kernel)
+}
+#undef IEKV_PICK_HOST
 
 int align_of_ptr(uint64_t p) {
   int a = 16;
@@ -825,14 +856,14 @@ template <bool SP, bool DP>
 int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage, char* dst_stage,
                 const int32_t* src_ids, const int32_t* dst_ids, int32_t n_blocks,
                 int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream,
-                int32_t chunk = -1, int32_t nt = -1) {
+                int32_t chunk = -1, int32_t nt = -1, bool host = false) {
   if (n_blocks == 0) return IEKV_OK;
   MovePlan pl;
   int rc;
   if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, SP, DP, false, &pl, chunk)))
     return rc;
   MoveKernel k = pick_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs, nontemporal(nt),
-                                     &pl.vec);
+                                     &pl.vec, host);
   const int64_t block_image = tile_bytes * n_arrays;
   for (int64_t r0 = 0; r0 < pl.total_runs; r0 += pl.runs_per_launch) {
     const int64_t first = r0 * pl.run;
@@ -857,14 +888,14 @@ template <bool SP, bool DP>
 int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
                        char* dst_stage, const InlineIds& ids, int32_t dst_off, int32_t n_blocks,
                        int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream,
-                       int32_t chunk = -1, int32_t nt = -1) {
+                       int32_t chunk = -1, int32_t nt = -1, bool host = false) {
   if (n_blocks == 0) return IEKV_OK;
   MovePlan pl;
   int rc;
   if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, SP, DP, true, &pl, chunk)))
     return rc;
   InlineKernel k = pick_inline_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
-                                              nontemporal(nt), &pl.vec);
+                                              nontemporal(nt), &pl.vec, host);
   for (int64_t r0 = 0; r0 < pl.total_runs; r0 += pl.runs_per_launch) {
     const int32_t runs = static_cast<int32_t>(std::min<int64_t>(pl.runs_per_launch,
                                                                 pl.total_runs - r0));
@@ -881,7 +912,7 @@ int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src
 template <bool SP, bool DP>
 int launch_images(const iekv_pool* pool, const InlineImages& images, const int32_t* ids,
                   int32_t n_blocks, hipStream_t stream, int32_t chunk = -1,
-                  int32_t nt = -1) {
+                  int32_t nt = -1, bool host = false) {
   static_assert(SP != DP, "a pack or an unpack");
   int align = pool->align;
   for (int32_t i = 0; i < n_blocks; ++i) align = std::min(align, align_of_ptr(images.addr[i]));
@@ -894,7 +925,7 @@ int launch_images(const iekv_pool* pool, const InlineImages& images, const int32
   if (pl.runs_per_launch < n_blocks)
     return set_error(IEKV_ERR_INVALID, "%d images do not fit one launch", n_blocks);
   ImagesKernel k = pick_images_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
-                                              nontemporal(nt), &pl.vec);
+                                              nontemporal(nt), &pl.vec, host);
   const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(n_blocks) * pl.units * pl.parts);
   return dispatch(k, grid, stream, SP ? view_of(pool) : PoolView{},
                   DP ? view_of(pool) : PoolView{}, nullptr, nullptr, images, ids, pl.tile_vecs,
@@ -1186,7 +1217,8 @@ template <bool SP, bool DP>
 int launch_host_ids(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
                     char* dst_stage, const int32_t* src_ids, const int32_t* dst_ids,
                     int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
-                    hipStream_t stream, int32_t chunk = -1, int32_t nt = -1) {
+                    hipStream_t stream, int32_t chunk = -1, int32_t nt = -1,
+                    bool host = false) {
   const int64_t image = tile_bytes * n_arrays;
   for (int32_t first = 0; first < n_blocks; first += IEKV_INLINE_IDS) {
     const int32_t m = std::min<int32_t>(IEKV_INLINE_IDS, n_blocks - first);
@@ -1199,7 +1231,7 @@ int launch_host_ids(const iekv_pool* sp, const iekv_pool* dp, const char* src_st
     if (DP) std::copy(dst_ids + first, dst_ids + first + m, ids.v + dst_off);
     const int rc = launch_move_inline<SP, DP>(
         sp, dp, SP ? nullptr : src_stage + first * image, DP ? nullptr : dst_stage + first * image,
-        ids, dst_off, m, tile_bytes, n_arrays, align, stream, chunk, nt);
+        ids, dst_off, m, tile_bytes, n_arrays, align, stream, chunk, nt, host);
     if (rc) return rc;
   }
   return IEKV_OK;
@@ -1220,7 +1252,7 @@ struct IdList {
 template <bool SP, bool DP>
 int launch_list(const iekv_pool* pool, const char* src_stage, char* dst_stage, IdList list,
                 int32_t n_blocks, int align, hipStream_t stream, int32_t chunk = -1,
-                int32_t nt = -1) {
+                int32_t nt = -1, bool host = false) {
   static_assert(SP != DP, "a pack or an unpack");
   const iekv_pool* sp = SP ? pool : nullptr;
   const iekv_pool* dp = DP ? pool : nullptr;
@@ -1228,9 +1260,10 @@ int launch_list(const iekv_pool* pool, const char* src_stage, char* dst_stage, I
   const int32_t* d = DP ? list.ids : nullptr;
   if (list.on_host)
     return launch_host_ids<SP, DP>(sp, dp, src_stage, dst_stage, s, d, n_blocks,
-                                   pool->tile_bytes, pool->n_arrays, align, stream, chunk, nt);
+                                   pool->tile_bytes, pool->n_arrays, align, stream, chunk, nt,
+                                   host);
   return launch_move<SP, DP>(sp, dp, src_stage, dst_stage, s, d, n_blocks, pool->tile_bytes,
-                             pool->n_arrays, align, stream, chunk, nt);
+                             pool->n_arrays, align, stream, chunk, nt, host);
 }
 
 // Restore pipeline shared by the iekv_restore* calls: chunk k of the blocks is
@@ -1493,7 +1526,7 @@ int restore_image(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks, const 
         const char* piece = mapped + first * block_bytes;
         const int zc_align = std::min(dst->align, align_of_ptr(reinterpret_cast<uint64_t>(piece)));
         if ((rc = launch_list<false, true>(dst, piece, nullptr, dst_ids.from(first), cnt,
-                                           zc_align, compute, chunk)))
+                                           zc_align, compute, chunk, -1, true)))
           return rc;
       }
       // As after the staged pipeline, `copy` is ordered after the last unpack.
@@ -1603,7 +1636,8 @@ int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
         std::copy(views.begin() + first, views.begin() + first + cnt, images.addr);
         const int32_t* device_ids = dst_ids.on_host ? nullptr : dst_ids.ids + first;
         if (dst_ids.on_host) std::copy(dst_ids.ids + first, dst_ids.ids + first + cnt, images.ids);
-        if ((rc = launch_images<false, true>(dst, images, device_ids, cnt, compute, chunk)))
+        if ((rc = launch_images<false, true>(dst, images, device_ids, cnt, compute, chunk, -1,
+                                             true)))
           return rc;
       }
       // As after the staged pipeline, `copy` is ordered after the last unpack.
