@@ -12,8 +12,9 @@ without NaN codes for fp8). Legs:
 
   direct       one iekv_copy_direct launch per request (the headline: 2P bytes); like
                every per-request leg, consecutive requests alternate between --streams
-               streams (default 2), so one request's launch can start while the previous
-               one drains
+               streams, so one request's launch can start while the previous one drains
+               (default: two when the workload's median request moves at most 512 MiB
+               each way, else one; see OVERLAP_MAX_REQUEST_BYTES)
   pack_unpack  iekv_pack into a per-request staging buffer, then iekv_unpack (4P bytes)
   pack         the pack half alone (2P bytes); unpack: the unpack half alone (2P bytes)
   batched      all requests' blocks in ONE direct launch (2P bytes)
@@ -84,6 +85,22 @@ HANDOFF_LEGS = ("direct", "pack_unpack", "pack", "unpack", "batched", "copier",
                 "copier_pack_unpack", "requests", "direct_ids")
 # The slot kernels on either side of the handoff (prefill's KV writes, decode's reads).
 SLOT_LEGS = ("write_kv", "write_kv_per_layer", "gather_context", "gather_per_array")
+# Requests of up to this many payload bytes (one direction) overlap on two request
+# streams: one launch's drain and the next one's ramp-up (about 5 us) then run at the
+# same time. Longer launches gain less from that than two concurrent scattered moves
+# lose to each other. Measured in one process per workload, one stream against two:
+# requests of 33-508 MiB (the 8B shape and its tp=2/tp=8 shares) gained 1-12% on the
+# direct leg from two; requests of 640 MiB to 2.5 GiB (the 70B share at tp=4, tp=2 and
+# whole) ran every leg faster on one: direct +0.3-1.6%, pack +1.8-4.5%, unpack
+# +1.3-3.5%, pack -> unpack +2.4-3.0%.
+OVERLAP_MAX_REQUEST_BYTES = 512 << 20
+
+
+def request_streams(w) -> int:
+    """Request streams for a workload's per-request legs: two when its median request
+    moves at most OVERLAP_MAX_REQUEST_BYTES each way, else one."""
+    sizes = sorted(len(t) * w.shape.block_bytes for t in w.src_tables)
+    return 2 if sizes and sizes[len(sizes) // 2] <= OVERLAP_MAX_REQUEST_BYTES else 1
 
 
 def log(msg: str) -> None:
@@ -1288,8 +1305,9 @@ def ab(args, names: list[str], device) -> int:
     elif key == "pad":
         w = workloads.make(args.config, args.seed, args.slack, tp=args.tp)
         for rnd in range(args.rounds):
-            # Re-made pools have alternated between two physical placements: reversing
-            # the order every other round lets each value land on both.
+            # Re-made pools land on physical placements that repeat every few
+            # allocations, one of them slow: reversing the order every other round
+            # moves each value to other placements.
             for v in (values if rnd % 2 == 0 else values[::-1]):
                 legs = Legs(w, device, args.seed,
                             "separate" if args.separate_pools else "paired",
@@ -1347,10 +1365,11 @@ def main() -> int:
     ap.add_argument("--tp", type=int, default=1,
                     help="measure one rank's share under head-sharded tensor parallelism "
                          "(H/tp KV heads per tile, same block tables)")
-    ap.add_argument("--streams", type=int, default=2,
+    ap.add_argument("--streams", type=int, default=0,
                     help="issue request k of the per-request legs on stream k mod STREAMS "
-                         "(default 2: on the Llama-3-8B shape the direct leg gained 2.3%% over "
-                         "one stream; the per-launch timing pass always uses one)")
+                         "(default 0: two streams when the workload's median request moves at "
+                         "most 512 MiB each way, one otherwise; the per-launch timing pass "
+                         "always uses one)")
     ap.add_argument("--ab", default="",
                     help="in-process A/B instead of the benchmark line: streams=1,2,4 (one set "
                          "of pools), slack=64,6600,engine (pools re-made per value; cfg3/cfg4), "
@@ -1389,6 +1408,10 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    if not 0 <= args.streams <= 8:
+        print("--streams must be 0 (by request size) or 1..8", file=sys.stderr)
+        return 2
+
     from iekv import workloads
 
     try:
@@ -1408,11 +1431,11 @@ def main() -> int:
     _native.lib()
     if args.launch:
         _native.set_launch(*[int(x) for x in args.launch.split(",")])
+    if args.streams == 0:
+        args.streams = request_streams(w)
     log(f"[bench] {w.name}: {w.num_requests} requests, {w.num_blocks} blocks, "
-        f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B")
-    if not 1 <= args.streams <= 8:
-        print("--streams must be 1..8", file=sys.stderr)
-        return 2
+        f"P = {w.payload_bytes / 1e9:.2f} GB, tile {w.shape.tile_bytes} B, "
+        f"{args.streams} request stream(s)")
     if args.ab:
         return ab(args, names, device)
     if args.floor:
