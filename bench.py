@@ -1209,8 +1209,8 @@ def _chunk_ok(v: int) -> bool:
 LAUNCH_AB = {
     "direct_chunk": ("direct_chunk_bytes", _chunk_ok),
     "chunk": ("chunk_bytes", _chunk_ok),
-    "order": ("order", lambda v: v in (0, 1, 2, 4, 5, 6)),
-    "pack_order": ("pack_order", lambda v: v in (0, 1, 2, 4, 5, 6)),
+    "order": ("order", lambda v: 0 <= v <= 7),
+    "pack_order": ("pack_order", lambda v: 0 <= v <= 7),
     "unroll": ("unroll", lambda v: v in (1, 2, 4, 8, 16)),
     "nontemporal": ("nontemporal", lambda v: v in (0, 1)),
     "run": ("run_blocks", lambda v: 0 <= v <= 64),

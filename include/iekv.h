@@ -369,7 +369,9 @@ int iekv_noop(int32_t workgroups, int32_t launches, hipStream_t stream);
  *               launches that write a pool (direct copy, unpack, restore):
  *               0 array-major (the 2L tiles of one block), 1 block-major
  *               (random blocks of one array), 2 diagonal (array a takes list
- *               run r + a, so 2L arrays and 2L blocks at once); adding 4
+ *               run r + a, so 2L arrays and 2L blocks at once), 3 scattered
+ *               (the (array, block) pairs in a multiplicative-hash order over
+ *               the whole move); adding 4
  *               gives each of the 8 XCDs one contiguous share of that order
  *               (with 5, its own eighth of the arrays); -1 keeps the current
  *               setting;

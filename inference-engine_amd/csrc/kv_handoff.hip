@@ -1135,7 +1135,7 @@ class Events {
 // -1 (keep), or a base order 0..2 with or without the kXcdGrouped flag.
 bool valid_order(int32_t order) {
   if (order == -1) return true;
-  return order >= 0 && order <= (kXcdGrouped | kDiagonal) && (order & ~kXcdGrouped) <= kDiagonal;
+  return order >= 0 && order <= (kXcdGrouped | iekv_plan::kScattered);
 }
 
 // A chunk setting: -1 (keep), 0 (whole tiles) or a power of two from 64 to 1 MiB.
@@ -2289,9 +2289,9 @@ int iekv_set_launch(int32_t run_blocks, int32_t unroll, int32_t nontemporal, int
   if (nontemporal < -1 || nontemporal > 1)
     return set_error(IEKV_ERR_INVALID, "nontemporal must be -1, 0 or 1 (got %d)", nontemporal);
   if (!valid_order(order))
-    return set_error(IEKV_ERR_INVALID, "order must be -1, 0, 1, 2, 4, 5 or 6 (got %d)", order);
+    return set_error(IEKV_ERR_INVALID, "order must be -1 or 0..7 (got %d)", order);
   if (!valid_order(pack_order))
-    return set_error(IEKV_ERR_INVALID, "pack_order must be -1, 0, 1, 2, 4, 5 or 6 (got %d)",
+    return set_error(IEKV_ERR_INVALID, "pack_order must be -1 or 0..7 (got %d)",
                      pack_order);
   if (!valid_chunk(chunk_bytes))
     return set_error(IEKV_ERR_INVALID,

@@ -16,7 +16,12 @@ namespace iekv_plan {
 constexpr int kThreads = 256;   // four wave64 per workgroup
 constexpr int kXcds = 8;        // MI355X: the dispatcher deals workgroups to 8 XCDs in turn
 constexpr int kXcdGrouped = 4;  // order flag: give each XCD a contiguous share of the work
-enum Order : int32_t { kArrayMajor = 0, kBlockMajor = 1, kDiagonal = 2 };
+enum Order : int32_t { kArrayMajor = 0, kBlockMajor = 1, kDiagonal = 2, kScattered = 3 };
+// Multiplier of the scattered order: a prime above every unit-run count a
+// launch can hold (at most kMaxGrid), so u -> u * kScatterMul mod count is a
+// bijection; 2654435761 is the prime nearest 2^32 / golden ratio, which spreads
+// consecutive positions far apart.
+constexpr int64_t kScatterMul = 2654435761LL;
 
 // A dispatch holds at most 2^32 - 1 work-items, so one launch takes at most
 // this many workgroups; larger moves are split over several launches.
@@ -32,7 +37,10 @@ constexpr int64_t kMaxGrid = static_cast<int64_t>(UINT32_MAX) / kThreads;
 //                addresses differ by multiples of the array stride;
 //   kBlockMajor  u = a * runs + run: random blocks of one array;
 //   kDiagonal    as array-major, but unit a takes run (run + a) mod runs, so
-//                the tiles in flight span 2L arrays AND 2L different blocks.
+//                the tiles in flight span 2L arrays AND 2L different blocks;
+//   kScattered   array-major position v = u * kScatterMul mod (units * runs):
+//                the (array, block) pairs in flight are spread over the whole
+//                move, so its reads and writes hit unrelated addresses.
 // The chunks of one tile are consecutive: position w = u * parts + p.
 // Plain orders take w = the workgroup index. The dispatcher deals consecutive
 // workgroups to the kXcds XCDs in turn, so with the kXcdGrouped flag set,
@@ -65,6 +73,11 @@ __host__ __device__ inline Place place_at(int i, int grid, int32_t n_units, int3
   if (base_order == kBlockMajor) {
     pl.a = u / runs;
     pl.r = u % runs;
+  } else if (base_order == kScattered) {
+    const int64_t count = static_cast<int64_t>(n_units) * runs;
+    const int64_t v = static_cast<int64_t>(u) * kScatterMul % count;
+    pl.a = static_cast<int>(v % n_units);
+    pl.r = static_cast<int>(v / n_units);
   } else {
     pl.a = u % n_units;
     pl.r = u / n_units;

@@ -50,7 +50,7 @@ static int failures = 0;
     }                                            \
   } while (0)
 
-static const int32_t kOrders[] = {0, 1, 2, 4, 5, 6};
+static const int32_t kOrders[] = {0, 1, 2, 3, 4, 5, 6, 7};
 
 static void check_xcd_grouped(int grid) {
   std::vector<char> seen(grid, 0);

@@ -21,7 +21,7 @@ ROOT = Path(__file__).resolve().parents[1]
     (["--config", "cfg5", "--ab", "slack=64,engine"], "--ab takes"),
     (["--ab", "direct_chunk=4096,3000"], "--ab takes"),
     (["--ab", "direct_chunk=32"], "--ab takes"),
-    (["--ab", "pack_order=0,3"], "--ab takes"),
+    (["--ab", "pack_order=0,8"], "--ab takes"),
     (["--ab", "unroll=0"], "--ab takes"),
     (["--streams", "9"], "--streams must be"),
 ])

@@ -164,7 +164,7 @@ def test_random_tiles_and_launch_shapes_match_the_oracle(gpu, case):
     n_src, n_dst = int(rng.integers(8, 48)), int(rng.integers(8, 48))
     count = int(rng.integers(2, min(n_src, n_dst) + 1))
     shape = (int(rng.choice([0, 1, 3])), int(rng.choice([1, 2, 4, 8, 16])), int(rng.integers(2)),
-             int(rng.choice([0, 1, 2, 4, 5, 6])), int(rng.choice([0, 1, 2, 4, 5, 6])),
+             int(rng.choice([0, 1, 2, 3, 4, 5, 6, 7])), int(rng.choice([0, 1, 2, 3, 4, 5, 6, 7])),
              int(rng.choice([0, 64, 256, 1024, 4096, 8192])))
     sk, sv = allocate(n_src, bs, layers, heads, dim, dtype, gpu, seed=2000 + case)
     dk, dv = allocate(n_dst, bs, layers, heads, dim, dtype, gpu, seed=3000 + case)
@@ -193,7 +193,8 @@ def test_random_tiles_and_launch_shapes_match_the_oracle(gpu, case):
 def test_every_launch_shape_is_bit_exact(gpu):
     """Pack, unpack and direct copy under every run / unroll / non-temporal /
     workgroup-order / chunk setting (order for the pool-writing launches,
-    pack_order for the staging-writing ones; 4-6 are the XCD-grouped orders,
+    pack_order for the staging-writing ones; 3 and 7 the scattered order,
+    plain and XCD-grouped; 4-7 are the XCD-grouped orders,
     here on grids of 8 to 19,712 workgroups, most not a multiple of the 8
     XCDs; chunks of 64 B to whole 32 KiB tiles)."""
     from iekv import _native
@@ -213,8 +214,8 @@ def test_every_launch_shape_is_bit_exact(gpu):
     try:
         shapes = [(run, unroll, nt, order, chunk)
                   for run in (1, 3, 0, 64) for unroll in (1, 4, 8, 16) for nt in (0, 1)
-                  for order in (0, 1, 2, 4, 5, 6) for chunk in (0, 4096)]
-        shapes += [(0, unroll, 1, order, chunk) for unroll in (1, 2, 8) for order in (0, 5)
+                  for order in range(8) for chunk in (0, 4096)]
+        shapes += [(0, unroll, 1, order, chunk) for unroll in (1, 2, 8) for order in (0, 3, 5)
                    for chunk in (64, 512, 1024, 16384, 32768, 1 << 20)]
         rows = np.concatenate([np.arange(b * bs, (b + 1) * bs) for b in dst_ids])
         dev = lambda ids: torch.tensor(ids, dtype=torch.int32, device=gpu)  # noqa: E731
@@ -1156,16 +1157,17 @@ def test_scattered_host_images_are_copied_together_only_within_one_allocation(gp
     starts a new copy at every allocation's end (a copy spanning two allocations
     would run past the end of the one its host pointer belongs to).
 
-    Three pinned buffers of 50 block images each. One iekv_offload_blocks call of
-    150 blocks (more than one direct launch takes, so the staged pipeline runs)
-    lists their images buffer after buffer: runs to merge and, at two places, a step
-    from one allocation's last image to another's first. Where the allocator placed
-    two buffers back to back (on MI355X boxes so far it has left a gap of at least
-    one buffer's size after each pinned allocation), that step is adjacent in memory
-    too, and the run must still end there. A second offload interleaves the buffers
-    image by image (no merges). Every buffer equals the oracle's images, and one
-    iekv_restore_blocks of all 150 (direct: pinned images) writes the oracle's
-    blocks."""
+    Three pinned buffers of 50 block images each, and one pageable image: a list
+    with any image outside pinned memory takes the staged pipeline (an all-pinned
+    list is moved by the kernels directly). One iekv_offload_blocks call of 151
+    blocks lists the pinned images buffer after buffer, then the pageable one: runs
+    to merge and, at two places, a step from one allocation's last image to
+    another's first. Where the allocator placed two buffers back to back (on MI355X
+    boxes so far it has left a gap of at least one buffer's size after each pinned
+    allocation), that step is adjacent in memory too, and the run must still end
+    there. A second offload interleaves the buffers image by image (no merges).
+    Every image equals the oracle's, and one iekv_restore_blocks of all 151 (staged
+    as well) writes the oracle's blocks."""
     from iekv import _native
     from iekv.engine.copier import HipSlotCopier
 
@@ -1176,8 +1178,9 @@ def test_scattered_host_images_are_copied_together_only_within_one_allocation(gp
     rng = np.random.default_rng(63)
     shape = (50, src.pool.n_arrays, src.pool.tile_bytes)
     bufs = [torch.empty(shape, dtype=torch.uint8, pin_memory=True) for _ in range(3)]
-    ends = {b.data_ptr() + b.numel() for b in bufs}
-    print(f"{len(ends & {b.data_ptr() for b in bufs})} pinned buffers start where another "
+    bufs.append(torch.empty((1,) + shape[1:], dtype=torch.uint8))     # pageable
+    ends = {b.data_ptr() + b.numel() for b in bufs[:3]}
+    print(f"{len(ends & {b.data_ptr() for b in bufs[:3]})} pinned buffers start where another "
           f"ends", flush=True)
     image = src.pool.block_bytes
     # Two slots of 32 images: both steps between buffers (entries 50 and 100) fall
@@ -1185,21 +1188,23 @@ def test_scattered_host_images_are_copied_together_only_within_one_allocation(gp
     staging = torch.empty(64 * image, dtype=torch.uint8, device=gpu)
     stream, side = torch.cuda.current_stream(), torch.cuda.Stream()
     src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    n = 151
     for layout in ("buffer after buffer", "interleaved"):
         picks = [(b, i) for i in range(50) for b in range(3)] if layout == "interleaved" \
             else [(b, i) for b in range(3) for i in range(50)]
-        sources = [int(x) for x in rng.permutation(160)[:150]]
-        addresses = (ctypes.c_void_p * 150)(*[bufs[b].data_ptr() + i * image for b, i in picks])
+        picks.append((3, 0))
+        sources = [int(x) for x in rng.permutation(160)[:n]]
+        addresses = (ctypes.c_void_p * n)(*[bufs[b].data_ptr() + i * image for b, i in picks])
         _native.call("iekv_offload_blocks", src.pool.native.handle,
-                     src.pool.block_ids(sources).data_ptr(), 150, addresses, staging.data_ptr(),
+                     src.pool.block_ids(sources).data_ptr(), n, addresses, staging.data_ptr(),
                      staging.numel(), stream.cuda_stream, side.cuda_stream)
         torch.cuda.synchronize()
         want = packed_image(pack(src_o, sources))
         for k, (b, i) in enumerate(picks):
             assert np.array_equal(bufs[b][i].numpy(), want[k]), (layout, k)
-        targets = [int(t) for t in rng.permutation(160)[:150]]
+        targets = [int(t) for t in rng.permutation(160)[:n]]
         _native.call("iekv_restore_blocks", dst.pool.native.handle,
-                     dst.pool.block_ids(targets).data_ptr(), 150, addresses, staging.data_ptr(),
+                     dst.pool.block_ids(targets).data_ptr(), n, addresses, staging.data_ptr(),
                      staging.numel(), stream.cuda_stream, side.cuda_stream)
         side.synchronize()
         torch.cuda.synchronize()

@@ -327,7 +327,7 @@ def test_launch_settings_are_validated(lib):
         _native.set_launch(unroll=3)
     with pytest.raises(_native.NativeError):
         _native.set_launch(nontemporal=2)
-    for bad in (3, 7, 8, -2):
+    for bad in (8, 9, -2):
         with pytest.raises(_native.NativeError):
             _native.set_launch(order=bad)
         with pytest.raises(_native.NativeError):
@@ -337,6 +337,8 @@ def test_launch_settings_are_validated(lib):
             _native.set_launch(chunk_bytes=bad)
         with pytest.raises(_native.NativeError):
             _native.set_launch(direct_chunk_bytes=bad)
+    _native.set_launch(order=3, pack_order=7)
+    assert (_native.get_launch()["order"], _native.get_launch()["pack_order"]) == (3, 7)
     _native.set_launch(run_blocks=8, unroll=16, nontemporal=0, order=6, pack_order=1,
                        chunk_bytes=1024)
     # chunk_bytes sets the pool-to-pool moves' chunk too.
