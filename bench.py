@@ -574,10 +574,15 @@ class Legs:
         """A contiguous device-to-device copy of a known size (torch copy_), for reference."""
         torch = self.torch
         if not hasattr(self, "_plain"):
+            # Random bytes, like the pools: on this GPU the bytes' values move the
+            # rate a little (a contiguous copy of zeros ran 1.4% faster).
             n = 4 << 30
-            self._plain = (torch.empty(n, dtype=torch.uint8, device=self.src_k[0].device),
-                           torch.zeros(n, dtype=torch.uint8, device=self.src_k[0].device))
-            self._plain[0].fill_(7)
+            device = self.src_k[0].device
+            gen = torch.Generator(device=device)
+            gen.manual_seed(7)
+            self._plain = (torch.randint(0, 256, (n,), dtype=torch.uint8, device=device,
+                                         generator=gen),
+                           torch.zeros(n, dtype=torch.uint8, device=device))
         a, b = self._plain
         b.copy_(a)
 
