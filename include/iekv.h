@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 19
+#define IEKV_ABI_VERSION 20
 
 enum {
   IEKV_OK = 0,
@@ -387,13 +387,14 @@ int iekv_noop(int32_t workgroups, int32_t launches, hipStream_t stream);
  *               power of two from 64 to 1 MiB; -1 keeps the current setting.
  *               A launch that would exceed the dispatch limit of 2^32 - 1
  *               work-items halves the split, then spreads over several
- *               launches. This sets the chunk size of every move, pool-to-
- *               pool moves included (iekv_set_direct_chunk sets theirs
- *               alone), except the unpacks that read pinned host memory
- *               themselves (direct restores), which move whole tiles, or
- *               groups of tiles smaller than this size.
+ *               launches. This sets the chunk size of every move, the
+ *               launches that write a pool included (iekv_set_direct_chunk
+ *               sets theirs alone), except the unpacks that read pinned host
+ *               memory themselves (direct restores), which move whole tiles,
+ *               or groups of tiles smaller than this size.
  * The defaults (run 0, unroll 8, nontemporal 1, order, pack_order and
- * chunk_bytes 4096; 8192 for pool-to-pool moves) are the library's measured
+ * chunk_bytes 4096 for the launches that write a staging image; 8192 for the
+ * launches that write a pool, iekv_set_direct_chunk) are the library's measured
  * best; iekv_get_launch and iekv_get_direct_chunk report them.
  * No reference counterpart: a tuning knob for the launches the entry points
  * above make. */
@@ -449,11 +450,15 @@ int iekv_check_ids(const iekv_pool* src, const int32_t* src_ids, const iekv_pool
 int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
                     int32_t* order, int32_t* pack_order, int32_t* chunk_bytes);
 
-/* chunk_bytes of iekv_set_launch for the pool-to-pool moves alone
- * (iekv_copy_direct, iekv_copy_direct_ids and iekv_copy_direct_requests):
- * the same values and meaning; -1 keeps the current
- * setting. iekv_get_direct_chunk reports it (chunk_bytes of iekv_get_launch is
- * the setting of the other moves).
+/* chunk_bytes of iekv_set_launch for the launches that write a pool from HBM
+ * alone: pool-to-pool moves (iekv_copy_direct, iekv_copy_direct_ids and
+ * iekv_copy_direct_requests) and, since ABI 20, unpacks of a device or
+ * pageable-host staging image (iekv_unpack, iekv_unpack_ids, the staged
+ * restores) whose tiles are at least this large; unpacks of smaller tiles keep
+ * the staging chunk, which groups them as the pack does. The same values and
+ * meaning; -1 keeps the current setting. iekv_get_direct_chunk reports it
+ * (chunk_bytes of iekv_get_launch is the setting of the launches that write a
+ * staging image).
  * No reference counterpart: a tuning knob, like iekv_set_launch. */
 int iekv_set_direct_chunk(int32_t chunk_bytes);
 int iekv_get_direct_chunk(int32_t* chunk_bytes);

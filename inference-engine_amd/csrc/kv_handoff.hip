@@ -115,21 +115,24 @@ std::atomic<int> g_pack_order{0};
 // Bytes each workgroup moves: a tile larger than this splits into a
 // power-of-two number of chunks of at least this size, one workgroup each; a
 // smaller one is moved together with the same block's tiles in the next
-// arrays, up to this size per workgroup (iekv_plan::tile_group).
-// Measured on MI355X (one box, all five benchmark workloads, 4 KiB against
-// 8 KiB): on 32 KiB tiles 4 KiB gains 2-6% on pack, unpack and pack->unpack
-// and ties on the direct copy; the prefix-sharing workload gains 2-6% on every
-// leg; 16 KiB tiles in 16,384-block pools (the 70B-share workload) lose 1-4%.
-// Against whole tiles, 8 KiB chunks were best or tied on every leg.
+// arrays, up to this size per workgroup (iekv_plan::tile_group). This one is
+// for the launches that write a staging buffer (pack, offload). Measured on
+// MI355X in one process per workload, pools made anew each round and both
+// sizes timed on the same pools: the pack ran 5.2-5.5% faster with 4 KiB than
+// with 8 KiB on the Llama-3-8B and prefix-sharing workloads, 1.8% on the
+// 70B share.
 std::atomic<int> g_chunk{4096};
-// The same setting for pool-to-pool moves (copy_direct and its variants).
-// Measured on MI355X in one process per workload, pools made anew each round
-// and every setting timed on the same pools, two request streams: 8 KiB chunks
-// moved the per-request direct copy at 6.52 / 6.50 / 6.41 TB/s (Llama-3-8B,
-// prefix-sharing, 70B-share workloads) against 6.44 / 6.42 / 6.37 for 4 KiB,
-// ahead in every placement; whole tiles tied 8 KiB on the first two and lost
-// on the third. The one loss: a small move issued as one launch (0.3 GB in
-// about 37,000 workgroups) ran 4.7% slower than with 4 KiB chunks.
+// The same setting for the launches that write a pool from HBM (chunk_of):
+// pool-to-pool moves (copy_direct and its variants) and unpacks of a device or
+// pageable-host staging image whose tiles are at least this large (unpacks
+// that read pinned host memory move whole tiles). Measured the same way, two
+// request streams: 8 KiB chunks moved the per-request direct copy at 6.52 /
+// 6.50 / 6.41 TB/s (Llama-3-8B, prefix-sharing, 70B-share workloads) against
+// 6.44 / 6.42 / 6.37 for 4 KiB, ahead in every placement, and the unpack
+// 2.3% / 2.8% / 1.2% faster; whole tiles tied 8 KiB on the direct copy of the
+// first two and lost on the third. The one loss: a small move issued as one
+// launch (0.3 GB in about 37,000 workgroups) ran 4.7% slower than with 4 KiB
+// chunks.
 std::atomic<int> g_direct_chunk{8192};
 
 // ---------------------------------------------------------------------------
@@ -812,16 +815,28 @@ class DeviceGuard {
 // 1) when a launch chooses for itself (host_write_nontemporal).
 bool nontemporal(int32_t nt) { return nt >= 0 ? nt != 0 : g_nontemporal.load() != 0; }
 
-// The launch shape of one move under the current settings (kv_plan.h); a
-// pool-to-pool move takes its own chunk size. `chunk` >= 0 sets this launch's
-// chunk size instead (host_read_chunk for moves that read pinned host memory).
+// Chunk size of a launch under the current settings: a pool-to-pool move takes
+// the pool-writing chunk; an unpack takes it when its tiles are at least that
+// large (split into pool-writing chunks), else the staging chunk, so small tiles
+// stay grouped as in the pack (grouping tiles of 2-4 KiB to 8 KiB per workgroup
+// slowed the unpack of the tensor-parallel shares by 1.2-3.4%); a launch that
+// writes a staging image takes the staging chunk.
+int32_t chunk_of(bool pool_reading, bool pool_writing, int64_t tile_bytes) {
+  const int32_t staged = g_chunk.load();
+  if (!pool_writing) return staged;
+  const int32_t pw = g_direct_chunk.load();
+  return pool_reading || pw == 0 || tile_bytes >= pw ? pw : staged;
+}
+
+// The launch shape of one move under the current settings (kv_plan.h), with
+// chunk_of's chunk size; `chunk` >= 0 sets this launch's chunk size instead
+// (host_read_chunk for moves that read pinned host memory).
 int plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int align,
               bool pool_reading, bool pool_writing, bool single_blocks, MovePlan* pl,
               int32_t chunk = -1) {
   iekv_plan::Settings settings;
   settings.run = g_run.load();
-  settings.chunk_bytes = chunk >= 0 ? chunk
-                         : pool_reading && pool_writing ? g_direct_chunk.load() : g_chunk.load();
+  settings.chunk_bytes = chunk >= 0 ? chunk : chunk_of(pool_reading, pool_writing, tile_bytes);
   settings.order = g_order.load();
   settings.pack_order = g_pack_order.load();
   switch (iekv_plan::plan_move(n_blocks, tile_bytes, n_arrays, align, pool_writing,

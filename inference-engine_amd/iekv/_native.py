@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most host ids one launch carries in its arguments
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: largest direct offload; restore launch size
@@ -206,7 +206,8 @@ def set_launch(run_blocks: int = -1, unroll: int = 0, nontemporal: int = -1,
     """Launch shape of the move kernels; see iekv_set_launch in include/iekv.h.
 
     ``chunk_bytes`` sets the chunk size of every move; ``direct_chunk_bytes``
-    (iekv_set_direct_chunk) then sets the pool-to-pool moves' own, when not -1.
+    (iekv_set_direct_chunk) then sets that of the launches that write a pool
+    (pool-to-pool moves and unpacks), when not -1.
     """
     call("iekv_set_launch", run_blocks, unroll, nontemporal, order, pack_order, chunk_bytes)
     call("iekv_set_direct_chunk", direct_chunk_bytes)

@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 19
+    assert lib.iekv_abi_version() == 20
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
