@@ -263,6 +263,13 @@ class Legs:
         self.streams = [self.stream] + [torch.cuda.Stream(device) for _ in range(streams - 1)]
         self.stagings = [self.staging] + [torch.empty_like(self.staging)
                                           for _ in range(streams - 1)]
+        # Random bytes in the staging buffers, so an unpack leg timed before any pack
+        # reads data like the pools' (zero-filled memory reads faster on this GPU).
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed + 1)
+        for st in self.stagings:
+            st.copy_(torch.randint(0, 256, st.shape, dtype=torch.uint8, device=device,
+                                   generator=gen))
         self.last_streams = 1     # request streams the most recent timed pass used
         self._fork_event = torch.cuda.Event()
         self._join_events = [torch.cuda.Event() for _ in self.streams[1:]]
