@@ -1388,3 +1388,41 @@ def test_padded_pools_move_bit_exactly(gpu, pad):
     rows = 50 * bs
     padding = dslab.view(2, layers, -1, heads, dim)[:, :, rows:]
     assert bool((padding.contiguous().view(torch.uint8) == 0x5A).all())
+
+
+@pytest.mark.parametrize("chunks", [(4096, 8192), (1024, 16384), (8192, 2048)],
+                         ids=["staging4K-pool8K", "staging1K-pool16K", "staging8K-pool2K"])
+def test_unpack_chunk_follows_the_tile_size(gpu, chunks):
+    """An unpack takes the pool-writing chunk (iekv_set_direct_chunk) when its tiles
+    are at least that large and the staging chunk otherwise, so with the two settings
+    apart every tile size takes another launch shape on each side of the pair: tiles
+    of 1 to 32 KiB, split or grouped, through pack -> unpack and the direct copy,
+    against the oracle byte for byte."""
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    staging_chunk, pool_chunk = chunks
+    before = _native.get_launch()
+    try:
+        _native.set_launch(chunk_bytes=staging_chunk, direct_chunk_bytes=pool_chunk)
+        for heads, dim in ((1, 32), (2, 64), (4, 64), (8, 64), (8, 128)):   # 1 .. 32 KiB tiles
+            bs, layers = 16, 3
+            sk, sv = allocate(48, bs, layers, heads, dim, torch.bfloat16, gpu, seed=70 + heads)
+            dk, dv = allocate(40, bs, layers, heads, dim, torch.bfloat16, gpu, seed=80 + heads)
+            src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+            rng = np.random.default_rng(90 + heads)
+            src_ids, dst_ids = random_tables(rng, 48, 40, 30)
+            src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+            tile = src.pool.tile_bytes
+            print(f"[unpack chunk] {chunks} tile {tile} B", flush=True)
+            dev = lambda ids: torch.tensor(ids, dtype=torch.int32, device=gpu)  # noqa: E731
+            packed = src.read_blocks(dev(src_ids[:18]))
+            dst.write_blocks(dev(dst_ids[:18]), packed)
+            dst.copy_blocks(src, dev(src_ids[18:]), dev(dst_ids[18:]))
+            torch.cuda.synchronize()
+            assert np.array_equal(packed.data.cpu().numpy(),
+                                  packed_image(pack(src_o, src_ids[:18]))), (chunks, tile)
+            handoff(src_o, dst_o, [src_ids], [dst_ids])
+            assert_pool_equals(dk, dv, dst_o)
+    finally:
+        _native.set_launch(**before)
