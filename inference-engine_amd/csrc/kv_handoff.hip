@@ -822,10 +822,8 @@ bool nontemporal(int32_t nt) { return nt >= 0 ? nt != 0 : g_nontemporal.load() !
 // slowed the unpack of the tensor-parallel shares by 1.2-3.4%); a launch that
 // writes a staging image takes the staging chunk.
 int32_t chunk_of(bool pool_reading, bool pool_writing, int64_t tile_bytes) {
-  const int32_t staged = g_chunk.load();
-  if (!pool_writing) return staged;
-  const int32_t pw = g_direct_chunk.load();
-  return pool_reading || pw == 0 || tile_bytes >= pw ? pw : staged;
+  return iekv_plan::launch_chunk(pool_reading, pool_writing, tile_bytes, g_chunk.load(),
+                                 g_direct_chunk.load());
 }
 
 // The launch shape of one move under the current settings (kv_plan.h), with

@@ -87,6 +87,18 @@ __host__ __device__ inline Place place_at(int i, int grid, int32_t n_units, int3
   return pl;
 }
 
+// Chunk size of a launch: a pool-to-pool move takes the pool-writing chunk; an
+// unpack (staging to pool) takes it when its tiles are at least that large (they
+// are then split into pool-writing chunks), else the staging chunk, which groups
+// small tiles as the pack does; a launch that writes a staging image takes the
+// staging chunk. 0 means whole tiles.
+inline int32_t launch_chunk(bool pool_reading, bool pool_writing, int64_t tile_bytes,
+                            int32_t staging_chunk, int32_t pool_chunk) {
+  if (!pool_writing) return staging_chunk;
+  return pool_reading || pool_chunk == 0 || tile_bytes >= pool_chunk ? pool_chunk
+                                                                      : staging_chunk;
+}
+
 // Chunks per tile for a requested chunk size: the largest power of two that
 // divides the tile's vector count and leaves chunks of at least chunk_bytes
 // (1 when chunk_bytes is 0 or the tile is no larger than the chunk).

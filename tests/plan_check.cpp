@@ -476,6 +476,30 @@ static void check_pieces_and_slots() {
   }
 }
 
+// Which chunk each kind of launch takes (iekv_plan::launch_chunk), against the rule
+// written out case by case: packs and offloads the staging chunk; pool-to-pool moves
+// the pool-writing chunk; unpacks the pool-writing chunk for tiles at least that
+// large or when it is 0 (whole tiles), else the staging chunk.
+static void check_launch_chunk() {
+  using iekv_plan::launch_chunk;
+  for (int32_t staged : {0, 1024, 4096, 8192})
+    for (int32_t pool : {0, 2048, 8192, 16384})
+      for (int64_t tile : {16, 1024, 2048, 4096, 8192, 16384, 32768, 65536}) {
+        EXPECT(launch_chunk(true, false, tile, staged, pool) == staged, "pack chunk");
+        EXPECT(launch_chunk(false, false, tile, staged, pool) == staged, "host pack chunk");
+        EXPECT(launch_chunk(true, true, tile, staged, pool) == pool, "direct chunk");
+        const int32_t want = (pool == 0 || tile >= pool) ? pool : staged;
+        EXPECT(launch_chunk(false, true, tile, staged, pool) == want,
+               "unpack chunk: staged %d pool %d tile %lld", staged, pool, (long long)tile);
+      }
+  // The defaults on the benchmark workloads' tiles: 8 KiB and larger tiles are
+  // unpacked in 8 KiB chunks, the tensor-parallel shares' 2 and 4 KiB tiles keep 4 KiB.
+  EXPECT(launch_chunk(false, true, 32768, 4096, 8192) == 8192, "cfg3 unpack");
+  EXPECT(launch_chunk(false, true, 8192, 4096, 8192) == 8192, "cfg1 / tp unpack");
+  EXPECT(launch_chunk(false, true, 4096, 4096, 8192) == 4096, "cfg3 tp8 unpack");
+  EXPECT(launch_chunk(false, true, 2048, 4096, 8192) == 4096, "cfg5 tp8 unpack");
+}
+
 int main() {
   for (int grid = 1; grid <= 4096; ++grid) check_xcd_grouped(grid);
   for (int grid : {98816, 1048575, 4194304, 16777215}) check_xcd_grouped(grid);
@@ -538,6 +562,7 @@ int main() {
   check_image_runs();
   check_image_views();
   check_pieces_and_slots();
+  check_launch_chunk();
 
   if (failures) {
     std::printf("%d failures\n", failures);

@@ -9,7 +9,8 @@ the copies of a scattered restore (image_runs) merge exactly the images that
 are adjacent within one allocation, over fixed and random layouts; the device
 addresses of direct host transfers (image_views), the launch and staging-slot
 splits of the host pipelines, and the pool-overlap test (spans_cross) hold at
-the 70B-share workload's numbers and on random layouts.
+the 70B-share workload's numbers and on random layouts; each kind of launch
+takes the chunk size its rule gives it (launch_chunk).
 """
 from __future__ import annotations
 
