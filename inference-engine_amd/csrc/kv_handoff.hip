@@ -31,6 +31,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "iekv.h"
@@ -64,7 +65,7 @@ using iekv_plan::kThreads;
 using iekv_plan::kXcdGrouped;
 using iekv_plan::MovePlan;
 using iekv_plan::Place;
-using iekv_plan::place_at;
+using iekv_plan::place_in_grid;
 constexpr int kMaxRun = 64;    // block ids staged in LDS per workgroup
 constexpr int64_t kMaxTileBytes = int64_t(1) << 30;
 
@@ -219,7 +220,10 @@ __device__ __forceinline__ void move_tile(gptr<const V> s, gptr<V> d, int n) {
 }
 
 // Workgroups take (array unit, run of list entries, chunk) triples in the
-// order iekv_plan::place_at describes (kv_plan.h).
+// order iekv_plan::place_at describes (kv_plan.h). Every move launch has
+// exactly units * runs * parts workgroups, so the kernels take the grid size
+// from the plan (place_in_grid) and never read gridDim: no kernel of this
+// library has hidden arguments, which keeps each launch's argument copy small.
 
 #ifndef IEKV_UNPACK_LOAD_FIRST
 #define IEKV_UNPACK_LOAD_FIRST 1
@@ -360,8 +364,7 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
         int32_t order) {
   __shared__ int32_t s_src[kMaxRun];
   __shared__ int32_t s_dst[kMaxRun];
-  const Place pl = place_at(blockIdx.x, gridDim.x, (n_arrays + group - 1) / group, runs, parts,
-                            order);
+  const Place pl = place_in_grid(blockIdx.x, (n_arrays + group - 1) / group, runs, parts, order);
   const int first = pl.r * run;
   if (run == 1) {
     move_unit<V, U, NT, SRC_POOL, DST_POOL, HOST>(
@@ -386,18 +389,24 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
 // destination ids at ids[dst_off + i], for list entries id_base + i. One block
 // per workgroup; each workgroup reads its id pair with scalar loads from the
 // kernel-argument segment, so no id buffer or upload is needed.
+// The runtime copies a launch's whole argument segment for every launch, and
+// on slower hosts each KiB of it adds about half a microsecond to the launch,
+// so the id block comes in two sizes: kSmallIdWords words for short lists (a
+// small workload's per-request tables) and the full 2 * IEKV_INLINE_IDS.
+template <int W>
 struct InlineIds {
-  int32_t v[2 * IEKV_INLINE_IDS];
+  int32_t v[W];
 };
+constexpr int kSmallIdWords = 64;
+constexpr int kIdWords = 2 * IEKV_INLINE_IDS;
 
-template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL, bool HOST>
+template <typename V, int U, bool NT, bool SRC_POOL, bool DST_POOL, bool HOST, int W>
 __global__ void __launch_bounds__(kThreads)
 kv_move_inline(PoolView src, PoolView dst, const char* __restrict__ src_stage,
-               char* __restrict__ dst_stage, InlineIds ids, int32_t id_base, int32_t dst_off,
+               char* __restrict__ dst_stage, InlineIds<W> ids, int32_t id_base, int32_t dst_off,
                int32_t tile_vecs, int32_t n_arrays, int32_t runs, int32_t parts,
                int32_t group, int32_t order) {
-  const Place pl = place_at(blockIdx.x, gridDim.x, (n_arrays + group - 1) / group, runs, parts,
-                            order);
+  const Place pl = place_in_grid(blockIdx.x, (n_arrays + group - 1) / group, runs, parts, order);
   const int i = id_base + pl.r;
   move_unit<V, U, NT, SRC_POOL, DST_POOL, HOST>(
       src, dst, src_stage, dst_stage, SRC_POOL ? ids.v[i] : 0, DST_POOL ? ids.v[dst_off + i] : 0,
@@ -423,8 +432,7 @@ kv_move_images(PoolView src, PoolView dst, const char* __restrict__ /*src_stage*
                const int32_t* __restrict__ ids, int32_t tile_vecs, int32_t n_arrays,
                int32_t runs, int32_t parts, int32_t group, int32_t order) {
   static_assert(SRC_POOL != DST_POOL, "images are packed from, or restored into, a pool");
-  const Place pl = place_at(blockIdx.x, gridDim.x, (n_arrays + group - 1) / group, runs, parts,
-                            order);
+  const Place pl = place_in_grid(blockIdx.x, (n_arrays + group - 1) / group, runs, parts, order);
   const int i = pl.r;
   const uint64_t image_bytes = static_cast<uint64_t>(n_arrays) * tile_vecs * sizeof(V);
   char* stage = reinterpret_cast<char*>(images.addr[i] - i * image_bytes);
@@ -468,11 +476,12 @@ struct RowShape {
   int32_t lanes;     // lanes per row (a power of two dividing kWave)
   int32_t chunks;    // groups of kThreads / lanes rows per array
   int32_t xcd;       // 1: XCD-grouped workgroup positions
+  int32_t groups;    // workgroups in the launch (chunks * arrays; read instead of gridDim)
 };
 
 // The (array index, first row) of this workgroup.
 __device__ __forceinline__ void row_place(const RowShape& sh, int* array, int64_t* first) {
-  const int w = sh.xcd ? iekv_plan::xcd_grouped(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int w = sh.xcd ? iekv_plan::xcd_grouped(blockIdx.x, sh.groups) : blockIdx.x;
   *array = w / sh.chunks;
   *first = static_cast<int64_t>(w % sh.chunks) * (kThreads / sh.lanes);
 }
@@ -637,8 +646,9 @@ kv_gather_rows(PoolView pool, int32_t first_array, const int32_t* __restrict__ t
 // index one pool). A bit of *status is set only when a check fails, so a valid
 // list costs one id load and, for a destination, one bitmap atomic per id.
 __global__ void __launch_bounds__(kThreads)
-ids_clear(uint32_t* __restrict__ bitmap, int64_t words, int32_t* __restrict__ status) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+ids_clear(uint32_t* __restrict__ bitmap, int64_t words, int32_t* __restrict__ status,
+          int32_t workgroups) {
+  const int64_t stride = static_cast<int64_t>(workgroups) * kThreads;
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; w < words;
        w += stride)
     bitmap[w] = 0u;
@@ -707,34 +717,38 @@ using MoveKernel = void (*)(PoolView, PoolView, const char*, char*, const int32_
 using ImagesKernel = void (*)(PoolView, PoolView, const char*, char*, InlineImages,
                               const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t,
                               int32_t);
-using InlineKernel = void (*)(PoolView, PoolView, const char*, char*, InlineIds, int32_t,
+template <int W>
+using InlineKernel = void (*)(PoolView, PoolView, const char*, char*, InlineIds<W>, int32_t,
                               int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t);
 
 // Kernel for vectors of the widest width the alignment allows, keeping up to
 // `unroll` of them in flight per lane; `lane_vecs` (vectors per lane per
 // chunk) caps the unroll so small chunks do not carry dead predicated slots.
+// IEKV_EXTRA holds template arguments after HOST (the inline kernels' id-block
+// size W), empty for the other kernels.
+#define IEKV_EXTRA
 #define IEKV_PICK(KERNEL)                                                       \
   if (align >= 16) {                                                            \
     *vec_bytes = 16;                                                            \
     const int u = std::min(unroll, lane_vecs);                                  \
     if (nt) {                                                                   \
-      if (u >= 16) return KERNEL<u32x4, 16, true, SP, DP, HP>;                      \
-      if (u >= 8) return KERNEL<u32x4, 8, true, SP, DP, HP>;                        \
-      if (u >= 4) return KERNEL<u32x4, 4, true, SP, DP, HP>;                        \
-      if (u >= 2) return KERNEL<u32x4, 2, true, SP, DP, HP>;                        \
-      return KERNEL<u32x4, 1, true, SP, DP, HP>;                                    \
+      if (u >= 16) return KERNEL<u32x4, 16, true, SP, DP, HP IEKV_EXTRA>;                      \
+      if (u >= 8) return KERNEL<u32x4, 8, true, SP, DP, HP IEKV_EXTRA>;                        \
+      if (u >= 4) return KERNEL<u32x4, 4, true, SP, DP, HP IEKV_EXTRA>;                        \
+      if (u >= 2) return KERNEL<u32x4, 2, true, SP, DP, HP IEKV_EXTRA>;                        \
+      return KERNEL<u32x4, 1, true, SP, DP, HP IEKV_EXTRA>;                                    \
     }                                                                           \
-    if (u >= 16) return KERNEL<u32x4, 16, false, SP, DP, HP>;                       \
-    if (u >= 8) return KERNEL<u32x4, 8, false, SP, DP, HP>;                         \
-    if (u >= 4) return KERNEL<u32x4, 4, false, SP, DP, HP>;                         \
-    if (u >= 2) return KERNEL<u32x4, 2, false, SP, DP, HP>;                         \
-    return KERNEL<u32x4, 1, false, SP, DP, HP>;                                     \
+    if (u >= 16) return KERNEL<u32x4, 16, false, SP, DP, HP IEKV_EXTRA>;                       \
+    if (u >= 8) return KERNEL<u32x4, 8, false, SP, DP, HP IEKV_EXTRA>;                         \
+    if (u >= 4) return KERNEL<u32x4, 4, false, SP, DP, HP IEKV_EXTRA>;                         \
+    if (u >= 2) return KERNEL<u32x4, 2, false, SP, DP, HP IEKV_EXTRA>;                         \
+    return KERNEL<u32x4, 1, false, SP, DP, HP IEKV_EXTRA>;                                     \
   }                                                                             \
-  if (align >= 8) { *vec_bytes = 8; return KERNEL<u32x2, 4, false, SP, DP, HP>; }   \
-  if (align >= 4) { *vec_bytes = 4; return KERNEL<uint32_t, 4, false, SP, DP, HP>; } \
-  if (align >= 2) { *vec_bytes = 2; return KERNEL<uint16_t, 4, false, SP, DP, HP>; } \
+  if (align >= 8) { *vec_bytes = 8; return KERNEL<u32x2, 4, false, SP, DP, HP IEKV_EXTRA>; }   \
+  if (align >= 4) { *vec_bytes = 4; return KERNEL<uint32_t, 4, false, SP, DP, HP IEKV_EXTRA>; } \
+  if (align >= 2) { *vec_bytes = 2; return KERNEL<uint16_t, 4, false, SP, DP, HP IEKV_EXTRA>; } \
   *vec_bytes = 1;                                                               \
-  return KERNEL<uint8_t, 4, false, SP, DP, HP>;
+  return KERNEL<uint8_t, 4, false, SP, DP, HP IEKV_EXTRA>;
 
 template <bool SP, bool DP, bool HP>
 MoveKernel pick_kernel_as(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes) {
@@ -742,24 +756,28 @@ MoveKernel pick_kernel_as(int align, int unroll, int lane_vecs, bool nt, int* ve
 }
 
 template <bool SP, bool DP, bool HP>
-InlineKernel pick_inline_kernel_as(int align, int unroll, int lane_vecs, bool nt,
-                                   int* vec_bytes) {
-  IEKV_PICK(kv_move_inline)
-}
-template <bool SP, bool DP, bool HP>
 ImagesKernel pick_images_kernel_as(int align, int unroll, int lane_vecs, bool nt,
                                    int* vec_bytes) {
   IEKV_PICK(kv_move_images)
 }
+#undef IEKV_EXTRA
+#define IEKV_EXTRA , W
+template <bool SP, bool DP, bool HP, int W>
+InlineKernel<W> pick_inline_kernel_as(int align, int unroll, int lane_vecs, bool nt,
+                                      int* vec_bytes) {
+  IEKV_PICK(kv_move_inline)
+}
+#undef IEKV_EXTRA
+#define IEKV_EXTRA
 #undef IEKV_PICK
 
 // The kernels of a move; `host`: an unpack that reads pinned host memory (move_entry's
 // HOST variant). Only unpacks have one.
 #define IEKV_PICK_HOST(NAME)                                                           \
   if constexpr (!SP && DP) {                                                           \
-    if (host) return NAME##_as<SP, DP, true>(align, unroll, lane_vecs, nt, vec_bytes); \
+    if (host) return NAME##_as<SP, DP, true IEKV_EXTRA>(align, unroll, lane_vecs, nt, vec_bytes); \
   }                                                                                    \
-  return NAME##_as<SP, DP, false>(align, unroll, lane_vecs, nt, vec_bytes);
+  return NAME##_as<SP, DP, false IEKV_EXTRA>(align, unroll, lane_vecs, nt, vec_bytes);
 
 template <bool SP, bool DP>
 MoveKernel pick_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes,
@@ -767,15 +785,18 @@ MoveKernel pick_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_b
   IEKV_PICK_HOST(pick_kernel)
 }
 template <bool SP, bool DP>
-InlineKernel pick_inline_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes,
-                                bool host = false) {
-  IEKV_PICK_HOST(pick_inline_kernel)
-}
-template <bool SP, bool DP>
 ImagesKernel pick_images_kernel(int align, int unroll, int lane_vecs, bool nt, int* vec_bytes,
                                 bool host = false) {
   IEKV_PICK_HOST(pick_images_kernel)
 }
+#undef IEKV_EXTRA
+#define IEKV_EXTRA , W
+template <bool SP, bool DP, int W>
+InlineKernel<W> pick_inline_kernel(int align, int unroll, int lane_vecs, bool nt,
+                                   int* vec_bytes, bool host = false) {
+  IEKV_PICK_HOST(pick_inline_kernel)
+}
+#undef IEKV_EXTRA
 #undef IEKV_PICK_HOST
 
 int align_of_ptr(uint64_t p) {
@@ -897,9 +918,9 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
 
 // The same move with its ids in the kernel arguments (n_blocks <=
 // IEKV_INLINE_IDS): src ids at ids.v[i], dst ids at ids.v[dst_off + i].
-template <bool SP, bool DP>
+template <bool SP, bool DP, int W>
 int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
-                       char* dst_stage, const InlineIds& ids, int32_t dst_off, int32_t n_blocks,
+                       char* dst_stage, const InlineIds<W>& ids, int32_t dst_off, int32_t n_blocks,
                        int64_t tile_bytes, int32_t n_arrays, int align, hipStream_t stream,
                        int32_t chunk = -1, int32_t nt = -1, bool host = false) {
   if (n_blocks == 0) return IEKV_OK;
@@ -907,8 +928,8 @@ int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src
   int rc;
   if ((rc = plan_move(n_blocks, tile_bytes, n_arrays, align, SP, DP, true, &pl, chunk)))
     return rc;
-  InlineKernel k = pick_inline_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
-                                              nontemporal(nt), &pl.vec, host);
+  InlineKernel<W> k = pick_inline_kernel<SP, DP, W>(align, g_unroll.load(), pl.lane_vecs,
+                                                    nontemporal(nt), &pl.vec, host);
   for (int64_t r0 = 0; r0 < pl.total_runs; r0 += pl.runs_per_launch) {
     const int32_t runs = static_cast<int32_t>(std::min<int64_t>(pl.runs_per_launch,
                                                                 pl.total_runs - r0));
@@ -959,7 +980,8 @@ bool row_shape(int64_t row_bytes, int vec_bytes, int64_t n, int32_t n_arrays, bo
   if (chunks * n_arrays > kMaxGrid) return false;
   sh->chunks = static_cast<int32_t>(chunks);
   sh->xcd = xcd ? 1 : 0;
-  *grid = static_cast<uint32_t>(chunks * n_arrays);
+  sh->groups = static_cast<int32_t>(chunks * n_arrays);
+  *grid = static_cast<uint32_t>(sh->groups);
   return true;
 }
 
@@ -1233,18 +1255,26 @@ int launch_host_ids(const iekv_pool* sp, const iekv_pool* dp, const char* src_st
                     hipStream_t stream, int32_t chunk = -1, int32_t nt = -1,
                     bool host = false) {
   const int64_t image = tile_bytes * n_arrays;
-  for (int32_t first = 0; first < n_blocks; first += IEKV_INLINE_IDS) {
-    const int32_t m = std::min<int32_t>(IEKV_INLINE_IDS, n_blocks - first);
-    InlineIds ids{};
+  // One launch's m ids in an id block of W words: sources first, then destinations.
+  auto launch = [&](auto words, int32_t first, int32_t m) {
+    constexpr int W = decltype(words)::value;
+    InlineIds<W> ids{};
     int32_t dst_off = 0;
     if (SP) {
       std::copy(src_ids + first, src_ids + first + m, ids.v);
       dst_off = m;
     }
     if (DP) std::copy(dst_ids + first, dst_ids + first + m, ids.v + dst_off);
-    const int rc = launch_move_inline<SP, DP>(
+    return launch_move_inline<SP, DP, W>(
         sp, dp, SP ? nullptr : src_stage + first * image, DP ? nullptr : dst_stage + first * image,
         ids, dst_off, m, tile_bytes, n_arrays, align, stream, chunk, nt, host);
+  };
+  constexpr int32_t kWordsPerId = (SP ? 1 : 0) + (DP ? 1 : 0);
+  for (int32_t first = 0; first < n_blocks; first += IEKV_INLINE_IDS) {
+    const int32_t m = std::min<int32_t>(IEKV_INLINE_IDS, n_blocks - first);
+    const int rc = m * kWordsPerId <= kSmallIdWords
+                       ? launch(std::integral_constant<int, kSmallIdWords>{}, first, m)
+                       : launch(std::integral_constant<int, kIdWords>{}, first, m);
     if (rc) return rc;
   }
   return IEKV_OK;
@@ -2198,7 +2228,7 @@ int iekv_check_ids(const iekv_pool* src, const int32_t* src_ids, const iekv_pool
   const uint32_t clear_grid =
       static_cast<uint32_t>(std::clamp<int64_t>((words + kThreads - 1) / kThreads, 1, 4096));
   hipLaunchKernelGGL(ids_clear, dim3(clear_grid), dim3(kThreads), 0, stream, bitmap, words,
-                     status);
+                     status, static_cast<int32_t>(clear_grid));
   IEKV_HIP(hipGetLastError());
   if (n_blocks == 0) return IEKV_OK;
   const uint32_t grid = static_cast<uint32_t>((static_cast<int64_t>(n_blocks) + kThreads - 1) /

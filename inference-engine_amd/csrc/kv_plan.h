@@ -87,6 +87,16 @@ __host__ __device__ inline Place place_at(int i, int grid, int32_t n_units, int3
   return pl;
 }
 
+// The same for a launch of exactly n_units * runs * parts workgroups, as every
+// move launch is: the grid size follows from the plan, so a kernel need not
+// read it from the dispatch. (A kernel that reads gridDim makes the runtime
+// append its 256-byte block of hidden arguments to every launch's argument
+// segment, and copying arguments is most of a small launch's host cost.)
+__host__ __device__ inline Place place_in_grid(int i, int32_t n_units, int32_t runs,
+                                               int32_t parts, int32_t order) {
+  return place_at(i, n_units * runs * parts, n_units, runs, parts, order);
+}
+
 // Chunk size of a launch: a pool-to-pool move takes the pool-writing chunk; an
 // unpack (staging to pool) takes it when its tiles are at least that large (they
 // are then split into pool-writing chunks), else the staging chunk, which groups

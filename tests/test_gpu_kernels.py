@@ -290,12 +290,16 @@ def test_tiles_smaller_than_a_chunk_are_grouped_bit_exact(gpu, bs, heads, dim, d
     assert all(np.array_equal(a, b) for a, b in zip(source, host_bytes(sk) + host_bytes(sv)))
 
 
-@pytest.mark.parametrize("count", [1, 255, 256, 257, 600, 1300])
+@pytest.mark.parametrize("count", [1, 64, 66, 128, 130, 255, 256, 257, 600, 1300])
 def test_host_ids_in_the_kernel_arguments_and_beyond(gpu, count):
     """Host id lists ride in the launches' kernel arguments (iekv_*_ids), 256 per
     launch: lists of 1 to 256 blocks in one launch, 257 and 300 in two; a longer
-    one (650 of a 1300-block request) is uploaded and moved in one launch. All
-    give the oracle's bytes."""
+    one (650 of a 1300-block request) is uploaded and moved in one launch. A
+    launch whose ids fill at most 64 words takes the kernels with the small id
+    block: the first half of the request is packed and unpacked (one word per
+    id: 32 and 33 ids small, 64 small, 65 large), the second half copied
+    directly (two words per id: 32 small, 33, 64 and 65 large). All give the
+    oracle's bytes."""
     from iekv.engine.copier import HipSlotCopier
 
     bs, layers, heads, dim = 4, 2, 2, 32

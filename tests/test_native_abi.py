@@ -420,3 +420,59 @@ def test_the_header_is_plain_c_and_links_from_c(lib, tmp_path):
     assert int(version) == lib.iekv_abi_version() == _native.ABI_VERSION
     assert int(inline_ids) == _native.INLINE_IDS      # the binding mirrors the header
     assert int(direct_max) == _native.HOST_DIRECT_MAX
+
+
+def kernel_arguments(library) -> dict[str, tuple[int, list[str]]]:
+    """(argument-segment bytes, argument kinds) of every gfx950 kernel in the
+    library, read from the code object's metadata notes with the ROCm LLVM tools."""
+    import shutil
+    import subprocess
+    import tempfile
+    from pathlib import Path
+
+    tools = Path("/opt/rocm/llvm/bin")
+    needed = ["llvm-objcopy", "clang-offload-bundler", "llvm-readelf"]
+    if not all((tools / t).exists() or shutil.which(t) for t in needed):
+        pytest.skip("the ROCm LLVM tools are not installed")
+    tool = {t: str(tools / t) if (tools / t).exists() else shutil.which(t) for t in needed}
+    with tempfile.TemporaryDirectory() as tmp:
+        bundle, code = Path(tmp) / "fatbin", Path(tmp) / "gfx950.co"
+        subprocess.run([tool["llvm-objcopy"], f"--dump-section=.hip_fatbin={bundle}",
+                        str(library), str(Path(tmp) / "stripped")], check=True, timeout=60)
+        subprocess.run([tool["clang-offload-bundler"], "--unbundle", "--type=o",
+                        f"--input={bundle}", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                        f"--output={code}"], check=True, timeout=60)
+        notes = subprocess.run([tool["llvm-readelf"], "--notes", str(code)], check=True,
+                               capture_output=True, text=True, timeout=60).stdout
+    kernels = {}
+    for entry in notes.split("\n  - ")[1:]:
+        name = re.search(r"^\s*\.name:\s+(\S+)", entry, re.M)
+        size = re.search(r"\.kernarg_segment_size:\s*(\d+)", entry)
+        if name and size:
+            kinds = re.findall(r"\.value_kind:\s+(\S+)", entry)
+            kernels[name.group(1)] = (int(size.group(1)), kinds)
+    return kernels
+
+
+def test_kernel_arguments_stay_small(lib):
+    """The runtime copies a launch's whole argument segment into device memory for
+    every launch, and on slower hosts that copy is most of a small launch's host
+    cost (about 0.4 us per KiB, plus 0.2 to 0.8 us when a kernel reads gridDim and
+    so carries the runtime's 256-byte block of hidden arguments). No kernel of the
+    library has hidden arguments; the move kernel with device ids takes 128 bytes,
+    and the kernels with ids in their arguments come in two sizes, the smaller
+    (for up to 64 words of ids) under 400 bytes."""
+    from iekv import _native
+
+    kernels = kernel_arguments(_native.library_path())
+    assert len(kernels) > 100
+    hidden = sorted(n for n, (_, kinds) in kernels.items()
+                    if any(k.startswith("hidden_") for k in kinds))
+    assert not hidden, hidden[:5]
+    def sizes(tag):
+        return {size for name, (size, _) in kernels.items() if tag in name}
+    assert sizes("kv_move_inline")
+    assert max(sizes("7kv_moveI")) <= 128
+    small, large = sorted(sizes("kv_move_inline"))
+    assert small < 400 and large > 2 * _native.INLINE_IDS * 4
+    assert max(sizes("kv_scatter_rows") | sizes("kv_gather_rows")) <= 128
