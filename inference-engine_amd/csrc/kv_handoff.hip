@@ -10,8 +10,9 @@
 // One workgroup owns one (array a, run of up to `run` consecutive list
 // entries, chunk of each tile). With one entry per run (the default) each tile
 // is split into chunks of at least the chunk size (4 KiB for launches that
-// read or write staging: one 16-byte vector per lane; 8 KiB for pool-to-pool
-// copies: two), one workgroup per chunk, and the workgroup reads its id pair with
+// write staging: one 16-byte vector per lane; 8 KiB for launches that write a
+// pool, i.e. pool-to-pool copies and unpacks of tiles at least that large:
+// two), one workgroup per chunk, and the workgroup reads its id pair with
 // scalar loads; tiles smaller than the chunk size are grouped instead, one
 // workgroup taking a block's tiles in several consecutive arrays; a run of
 // several entries stages its ids in LDS. Data moves
