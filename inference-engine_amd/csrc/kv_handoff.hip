@@ -905,7 +905,7 @@ int launch_move(const iekv_pool* sp, const iekv_pool* dp, const char* src_stage,
     const int32_t cnt = static_cast<int32_t>(
         std::min<int64_t>(pl.runs_per_launch * pl.run, n_blocks - first));
     const int32_t runs = static_cast<int32_t>((cnt + pl.run - 1) / pl.run);
-    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * pl.units * pl.parts);
+    const uint32_t grid = iekv_plan::launch_workgroups(pl, runs);
     if ((rc = dispatch(k, grid, stream, view_of(sp), view_of(dp),
                        SP ? nullptr : src_stage + first * block_image,
                        DP ? nullptr : dst_stage + first * block_image,
@@ -934,7 +934,7 @@ int launch_move_inline(const iekv_pool* sp, const iekv_pool* dp, const char* src
   for (int64_t r0 = 0; r0 < pl.total_runs; r0 += pl.runs_per_launch) {
     const int32_t runs = static_cast<int32_t>(std::min<int64_t>(pl.runs_per_launch,
                                                                 pl.total_runs - r0));
-    const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(runs) * pl.units * pl.parts);
+    const uint32_t grid = iekv_plan::launch_workgroups(pl, runs);
     if ((rc = dispatch(k, grid, stream, view_of(sp), view_of(dp), src_stage, dst_stage, ids,
                        static_cast<int32_t>(r0), dst_off, pl.tile_vecs, n_arrays, runs, pl.parts,
                        pl.group, pl.order)))
@@ -961,7 +961,7 @@ int launch_images(const iekv_pool* pool, const InlineImages& images, const int32
     return set_error(IEKV_ERR_INVALID, "%d images do not fit one launch", n_blocks);
   ImagesKernel k = pick_images_kernel<SP, DP>(align, g_unroll.load(), pl.lane_vecs,
                                               nontemporal(nt), &pl.vec, host);
-  const uint32_t grid = static_cast<uint32_t>(static_cast<int64_t>(n_blocks) * pl.units * pl.parts);
+  const uint32_t grid = iekv_plan::launch_workgroups(pl, n_blocks);
   return dispatch(k, grid, stream, SP ? view_of(pool) : PoolView{},
                   DP ? view_of(pool) : PoolView{}, nullptr, nullptr, images, ids, pl.tile_vecs,
                   pool->n_arrays, n_blocks, pl.parts, pl.group, pl.order);

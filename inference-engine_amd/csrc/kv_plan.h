@@ -195,6 +195,14 @@ inline Status plan_move(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, 
   return kPlanned;
 }
 
+// Workgroups of one launch of a plan that covers `runs` runs (at most
+// runs_per_launch): every launch of the move kernels has exactly this many,
+// and the kernels rely on it (place_in_grid derives the grid size from the
+// same three factors instead of reading it from the dispatch).
+inline uint32_t launch_workgroups(const MovePlan& pl, int64_t runs) {
+  return static_cast<uint32_t>(runs * pl.units * pl.parts);
+}
+
 // Copies of a scattered restore (iekv_restore_blocks): list entry i's host
 // image of image_bytes bytes starts at address images[i]. Consecutive entries
 // whose images follow each other in memory are copied with one transfer, but

@@ -7,8 +7,10 @@
 //  3. plan_move's shapes respect the dispatch limit, the chunk and tile-group
 //     rules and the vector width, over a sweep of tiles, alignments, arrays,
 //     block counts and settings;
-//  4. simulating every launch and workgroup of small plans moves every vector
-//     of every listed tile exactly once;
+//  4. simulating every launch and workgroup of small plans (each launch's
+//     grid from launch_workgroups, as the host launches it, each workgroup
+//     placed by place_in_grid, as the kernels place it) moves every vector of
+//     every listed tile exactly once;
 //  5. image_runs (the copies of a scattered restore) covers every image once,
 //     in order, merges only images adjacent in memory within the allocation of
 //     the run's first image, and merges every such pair: fixed layouts (one
@@ -135,9 +137,10 @@ static void simulate(int32_t n_blocks, int64_t tile_bytes, int32_t n_arrays, int
     const int64_t first = r0 * pl.run;
     const int64_t cnt = std::min<int64_t>(pl.runs_per_launch * pl.run, n_blocks - first);
     const int32_t runs = int32_t((cnt + pl.run - 1) / pl.run);
-    const int grid = runs * pl.units * pl.parts;
+    // The grid the host launches, decoded the way the kernels decode it.
+    const int grid = static_cast<int>(launch_workgroups(pl, runs));
     for (int i = 0; i < grid; ++i) {
-      const Place p = place_at(i, grid, pl.units, runs, pl.parts, pl.order);
+      const Place p = place_in_grid(i, pl.units, runs, pl.parts, pl.order);
       const int64_t e0 = first + int64_t(p.r) * pl.run;
       const int64_t e1 = std::min<int64_t>(e0 + pl.run, first + cnt);
       for (int64_t e = e0; e < e1; ++e)

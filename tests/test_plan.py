@@ -10,7 +10,8 @@ are adjacent within one allocation, over fixed and random layouts; the device
 addresses of direct host transfers (image_views), the launch and staging-slot
 splits of the host pipelines, and the pool-overlap test (spans_cross) hold at
 the 70B-share workload's numbers and on random layouts; each kind of launch
-takes the chunk size its rule gives it (launch_chunk).
+takes the chunk size its rule gives it (launch_chunk). Seven mistakes planted one at
+a time in a copy of the header each make it fail.
 """
 from __future__ import annotations
 
@@ -44,3 +45,54 @@ def test_the_launch_plan_covers_every_tile_once(tmp_path, build):
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
     assert out.returncode == 0 and out.stdout.strip().endswith("plan ok"), \
         (out.stdout[-3000:] + out.stderr[-3000:])
+
+
+# Mistakes planted one at a time in a copy of kv_plan.h: each is a plausible slip in
+# the planning the kernels rely on, and plan_check must fail on every one of them.
+# (name, the header's text, the same text with the mistake)
+MISTAKES = [
+    ("xcd remainder dropped",
+     "return x * q + (x < rem ? x : rem) + i / kXcds;",
+     "return x * q + i / kXcds;"),
+    ("diagonal taken modulo the units",
+     "pl.r = static_cast<int>((static_cast<int64_t>(pl.r) + pl.a) % runs);",
+     "pl.r = static_cast<int>((static_cast<int64_t>(pl.r) + pl.a) % n_units);"),
+    ("no halving of the split at the dispatch limit",
+     "  while (pl->parts > 1 && pl->total_runs * n_arrays * pl->parts > kMaxGrid) pl->parts /= 2;\n",
+     ""),
+    ("tile group not capped at the array count",
+     "return static_cast<int>(group < n_arrays ? group : n_arrays);",
+     "return static_cast<int>(group);"),
+    ("unit count truncated",
+     "pl->units = (n_arrays + pl->group - 1) / pl->group;",
+     "pl->units = n_arrays / pl->group;"),
+    ("unpack chunk rule with a strict comparison",
+     "tile_bytes >= pool_chunk ? pool_chunk",
+     "tile_bytes > pool_chunk ? pool_chunk"),
+    ("launch grid without the chunk factor",
+     "return static_cast<uint32_t>(runs * pl.units * pl.parts);",
+     "return static_cast<uint32_t>(runs * pl.units);"),
+]
+
+
+@pytest.mark.parametrize("name,right,wrong", MISTAKES, ids=[m[0] for m in MISTAKES])
+def test_each_planted_mistake_fails_the_check(tmp_path, name, right, wrong):
+    """The check has teeth: with any one of these mistakes in the header, plan_check
+    names a failure instead of printing "plan ok"."""
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ is not installed")
+    header = (ROOT / "inference-engine_amd" / "csrc" / "kv_plan.h").read_text()
+    assert header.count(right) == 1, f"{name}: the header no longer holds {right!r}"
+    (tmp_path / "inference-engine_amd" / "csrc").mkdir(parents=True)
+    (tmp_path / "tests").mkdir()
+    (tmp_path / "inference-engine_amd" / "csrc" / "kv_plan.h").write_text(
+        header.replace(right, wrong))
+    shutil.copy(ROOT / "tests" / "plan_check.cpp", tmp_path / "tests" / "plan_check.cpp")
+    exe = tmp_path / "plan_check"
+    subprocess.run([gxx, "-std=c++17", "-O2", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    str(tmp_path / "tests" / "plan_check.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True, text=True, timeout=300)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
+    assert out.returncode != 0 and not out.stdout.strip().endswith("plan ok"), \
+        f"{name}: plan_check passed with the mistake planted"
