@@ -10,8 +10,9 @@ are adjacent within one allocation, over fixed and random layouts; the device
 addresses of direct host transfers (image_views), the launch and staging-slot
 splits of the host pipelines, and the pool-overlap test (spans_cross) hold at
 the 70B-share workload's numbers and on random layouts; each kind of launch
-takes the chunk size its rule gives it (launch_chunk). Seven mistakes planted one at
-a time in a copy of the header each make it fail.
+takes the chunk size its rule gives it (launch_chunk). Thirteen mistakes planted one
+at a time in a copy of the header (seven in the launch planning, six in the host-address
+arithmetic) each make it fail.
 """
 from __future__ import annotations
 
@@ -72,6 +73,25 @@ MISTAKES = [
     ("launch grid without the chunk factor",
      "return static_cast<uint32_t>(runs * pl.units * pl.parts);",
      "return static_cast<uint32_t>(runs * pl.units);"),
+    # The host-address arithmetic of the host-memory transfers.
+    ("a copy run past its first image's allocation",
+     "static_cast<int64_t>(len + 1) * image_bytes <= space)",
+     "space >= 0)"),
+    ("a looked-up allocation reused for an image that runs past its end",
+     "if (!(have && p >= lo && p + static_cast<uint64_t>(bytes) <= hi)) {",
+     "if (!(have && p >= lo && p < hi)) {"),
+    ("an image longer than the rest of its allocation accepted",
+     "if (!span.mapped || span.room < bytes) return false;",
+     "if (!span.mapped) return false;"),
+    ("two staging slots when the buffer holds one image",
+     "*n_slots = fit >= 2 ? 2 : 1;",
+     "*n_slots = 2;"),
+    ("more images per launch than the argument block holds",
+     "  if (per > max_images) per = max_images;\n",
+     ""),
+    ("touching pools counted as overlapping",
+     "if (reach[1 - s.owner] > s.lo) return true;",
+     "if (reach[1 - s.owner] >= s.lo) return true;"),
 ]
 
 
