@@ -93,3 +93,37 @@ def test_in_process_ab_checks_every_leg(gpu, spec):
     assert set(line["mean"]) == set(values)
     for row in line["rows"]:
         assert all(row[leg] > 0 for leg in ("direct", "unpack", "pack", "pack_unpack"))
+
+
+def test_the_bench_verifier_notices_one_wrong_byte(gpu):
+    """Every figure the bench reports is followed by its tile check, so that check
+    must notice the smallest error: after a correct direct handoff of the small
+    workload, one flipped bit in the last byte of the last destination tile makes
+    verify() fail, and flipping it back passes again; the same for one byte of the
+    last packed staging image and verify_pack()."""
+    import torch
+
+    import bench
+    from iekv import workloads
+
+    w = workloads.make("cfg1", 0, None)
+    legs = bench.Legs(w, gpu, 0, "paired", streams=1)
+    T = w.shape.tile_bytes
+    legs.direct()
+    torch.cuda.synchronize()
+    assert legs.verify()
+    tiles = legs.dst_v[-1].view(torch.uint8).view(-1, T)
+    last = int(legs.dst_all[-1])
+    tiles[last, T - 1] ^= 1
+    assert not legs.verify()
+    tiles[last, T - 1] ^= 1
+    assert legs.verify()
+    legs.pack()
+    torch.cuda.synchronize()
+    assert legs.verify_pack()
+    n = legs.src_ids[-1].numel()
+    image = legs.stagings[0][:n * w.shape.block_bytes]
+    image[-1] ^= 1
+    assert not legs.verify_pack()
+    image[-1] ^= 1
+    assert legs.verify_pack()
