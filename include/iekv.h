@@ -139,7 +139,10 @@ int iekv_copy_direct_requests(const iekv_pool* src, const iekv_pool* dst, int32_
  * them: the ids travel in the launches' own kernel arguments, IEKV_INLINE_IDS
  * blocks per launch (a longer list is issued as consecutive launches), so the
  * caller needs no device id buffer and no host-to-device id copy sits on the
- * stream between launches. One block per workgroup whatever iekv_set_launch's
+ * stream between launches. A launch whose ids fill at most 64 words (32 direct
+ * pairs, or 64 pack or unpack ids) carries them in a 256-byte block, a longer
+ * one in a 2 KiB block: the runtime copies each launch's arguments on the host,
+ * so short lists launch faster. One block per workgroup whatever iekv_set_launch's
  * run_blocks. The ids are checked on the host before anything
  * is enqueued: an id outside its pool returns IEKV_ERR_RANGE; a destination id
  * given twice (iekv_copy_direct_ids, iekv_unpack_ids), or a copy within one pool
