@@ -390,6 +390,80 @@ def test_a_move_beyond_one_dispatch_spreads_over_launches(gpu, chunk, launches):
         assert torch.equal(packed.data[:, a], want)
 
 
+@pytest.mark.parametrize("chunk", [-1, 0], ids=["grouped tiles", "whole tiles"])
+def test_block_ids_at_the_top_of_the_int32_range(gpu, chunk):
+    """A pool of INT32_MAX blocks, the largest iekv_pool_create takes (16-byte tiles,
+    one layer's K and V: 64 GiB): ids next to the int32 limit address the last tiles
+    of both arrays, 32 GiB into each, so every move path must form 64-bit offsets from
+    32-bit ids. The direct copy with device ids and with host ids and pack -> unpack
+    each move their tiles, under the default launch shape (a block's two tiles in one
+    workgroup) and with whole tiles per workgroup; the neighbours of every destination
+    tile keep their bytes."""
+    from array import array
+
+    from iekv import _native
+
+    n, T, A = 2**31 - 1, 16, 2
+    top = n - 1
+    slab = torch.empty(A * n * T, dtype=torch.uint8, device=gpu)
+    tiles = slab.view(A, n, T)
+    pool = _native.Pool([slab.data_ptr(), slab.data_ptr() + n * T], T, n, gpu.index or 0)
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(61)
+    cases = {   # (sources, destinations), all within one pool and disjoint
+        "device ids": ([top, top - 2, 3, top - 7], [top - 1, 0, top - 3, top - 5]),
+        "host ids": ([top - 11, 9, top - 13], [top - 12, top - 4, 17]),
+        "pack/unpack": ([top - 21, 25, top - 23], [top - 22, top - 6, 27]),
+    }
+    touched = sorted({b for src, dst in cases.values() for b in src + dst}
+                     | {b + d for _, dst in cases.values() for b in dst for d in (-1, 1)
+                        if 0 <= b + d < n})
+    idx = torch.tensor(touched, dtype=torch.long, device=gpu)
+    for a in range(A):
+        tiles[a].index_copy_(0, idx, torch.randint(0, 256, (len(touched), T), dtype=torch.uint8,
+                                                   device=gpu, generator=gen))
+    before_tiles = tiles[:, idx].clone()
+    stream = torch.cuda.current_stream().cuda_stream
+    settings = _native.get_launch()
+    print(f"int32-limit pool, chunk {chunk}", flush=True)
+    try:
+        if chunk >= 0:
+            _native.set_launch(0, 0, -1, -1, -1, chunk)
+        src, dst = cases["device ids"]
+        s_dev = torch.tensor(src, dtype=torch.int32, device=gpu)
+        d_dev = torch.tensor(dst, dtype=torch.int32, device=gpu)
+        _native.call("iekv_copy_direct", pool.handle, pool.handle, s_dev.data_ptr(),
+                     d_dev.data_ptr(), len(src), stream)
+        src, dst = cases["host ids"]
+        hs, hd = array("i", src), array("i", dst)
+        _native.call("iekv_copy_direct_ids", pool.handle, pool.handle, hs.buffer_info()[0],
+                     hd.buffer_info()[0], len(src), stream)
+        src, dst = cases["pack/unpack"]
+        staging = torch.empty(len(src) * A * T, dtype=torch.uint8, device=gpu)
+        hs, hd = array("i", src), array("i", dst)
+        _native.call("iekv_pack_ids", pool.handle, hs.buffer_info()[0], len(src),
+                     staging.data_ptr(), staging.numel(), stream)
+        _native.call("iekv_unpack_ids", pool.handle, hd.buffer_info()[0], len(dst),
+                     staging.data_ptr(), staging.numel(), stream)
+        torch.cuda.synchronize()
+    finally:
+        _native.set_launch(**settings)
+    # Expected: every tile as it was, then each case's destinations from their sources.
+    want = {b: before_tiles[:, i] for i, b in enumerate(touched)}
+    for src, dst in cases.values():
+        moved = {d: want[s] for s, d in zip(src, dst)}
+        want.update(moved)
+    got = tiles[:, idx]
+    for i, b in enumerate(touched):
+        assert torch.equal(got[:, i], want[b]), f"block {b} (top - {top - b})"
+    assert torch.equal(staging.view(len(cases["pack/unpack"][0]), A, T),
+                       before_tiles[:, [touched.index(s) for s in cases["pack/unpack"][0]]]
+                       .transpose(0, 1))
+    pool.close()
+    del slab, tiles, staging
+    torch.cuda.empty_cache()
+
+
 def test_separately_allocated_layers_use_an_address_table(gpu):
     from iekv.engine.copier import HipSlotCopier
 
