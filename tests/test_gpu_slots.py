@@ -171,3 +171,54 @@ def test_the_model_decodes_identically_through_the_slot_kernels(gpu, cache_dtype
     hip_split = DisaggregatedEngine(model(True), cfg, mode="direct").generate(
         g["prompts"], max_new_tokens=6, temperature=0.0)
     assert hip_colocated == torch_path == hip_split
+
+
+def test_slots_and_table_entries_at_the_top_of_a_pool_of_int32_max_blocks(gpu):
+    """A pool of INT32_MAX blocks of 2 slots (8-byte rows, one layer's K and V: 64 GiB)
+    has 2^32 - 2 slots: write_kv's int64 slots above 2^32 - 5 and past 2^31, and
+    gather_context's table entries next to INT32_MAX, address rows 32 GiB into each
+    array. Both kernels move exactly those rows, and the rows beside each written one
+    keep their bytes."""
+    from iekv.engine.pools import KVPool, allocate_pool
+    from iekv.engine.slots import gather_rows_arrays, write_slots_layers
+
+    n, bs = 2**31 - 1, 2
+    rows = n * bs
+    k, v = allocate_pool(n, bs, 1, 1, 8, dtype=torch.uint8, device=gpu, zero=False)
+    pool = KVPool(k, v, bs)
+    gen = torch.Generator(gpu).manual_seed(71)
+    slots = [rows - 1, rows - 4, 5, 2**31 + 7, 2**32 - 9]
+    beside = sorted({s + d for s in slots for d in (-1, 1) if 0 <= s + d < rows} - set(slots))
+    idx = torch.tensor(beside, dtype=torch.long, device=gpu)
+    for arr in (k[0], v[0]):
+        arr.view(rows, 8).index_copy_(0, idx, torch.randint(
+            0, 256, (len(beside), 8), dtype=torch.uint8, device=gpu, generator=gen))
+    kept = [arr.view(rows, 8)[idx].clone() for arr in (k[0], v[0])]
+    new_k = torch.randint(0, 256, (1, len(slots), 1, 8), dtype=torch.uint8, device=gpu,
+                          generator=gen)
+    new_v = torch.randint(0, 256, (1, len(slots), 1, 8), dtype=torch.uint8, device=gpu,
+                          generator=gen)
+    print("int32-limit slot pool: write_kv", flush=True)
+    write_slots_layers(pool, new_k, new_v, slots)
+    torch.cuda.synchronize()
+    sl = torch.tensor(slots, dtype=torch.long, device=gpu)
+    assert torch.equal(k[0].view(rows, 8)[sl], new_k[0].view(-1, 8))
+    assert torch.equal(v[0].view(rows, 8)[sl], new_v[0].view(-1, 8))
+    for arr, before in zip((k[0], v[0]), kept):
+        assert torch.equal(arr.view(rows, 8)[idx], before)
+    # gather_context over a table whose blocks sit at the top of the pool
+    table = [n - 1, n - 2, 3, n - 5]
+    context = 7                                          # the last block half used
+    want_rows = torch.tensor([table[j // bs] * bs + j % bs for j in range(context)],
+                             dtype=torch.long, device=gpu)
+    for arr in (k[0], v[0]):
+        arr.view(rows, 8).index_copy_(0, want_rows, torch.randint(
+            0, 256, (context, 8), dtype=torch.uint8, device=gpu, generator=gen))
+    print("int32-limit slot pool: gather_context", flush=True)
+    out = gather_rows_arrays(pool, table, context)
+    torch.cuda.synchronize()
+    for a, arr in enumerate((k[0], v[0])):
+        assert torch.equal(out[a].view(context, 8), arr.view(rows, 8)[want_rows])
+    pool.native.close()
+    del k, v, pool, out
+    torch.cuda.empty_cache()
