@@ -201,3 +201,31 @@ def test_two_copiers_over_one_cache_are_one_pool(gpu):
     assert shifted.pool.memory_relation(a.pool) == "partial"
     with pytest.raises(ValueError, match="overlap in memory"):
         shifted.copy_blocks(a, [1], [2])
+
+
+def test_the_checks_at_the_top_of_a_pool_of_int32_max_blocks(gpu):
+    """A pool of INT32_MAX blocks (16-byte tiles, one layer: 64 GiB; a 256 MiB
+    bitmap): ids next to the int32 limit land in the bitmap's last word, and each
+    check still tells them apart: a valid same-pool list passes, a destination
+    repeated at the top, a source that is also a destination at the top, and ids
+    just outside the pool at either end are each reported."""
+    from iekv.engine.pools import KVPool, allocate_pool
+
+    n = 2**31 - 1
+    top = n - 1
+    pool = KVPool(*allocate_pool(n, 1, 1, 1, 16, dtype=torch.uint8, device=gpu, zero=False), 1)
+    a = np.array
+    cases = [   # (sources, destinations, expected bits), one pool
+        (a([top, top - 2, 3]), a([top - 1, 0, top - 3]), 0),
+        (a([top, top - 2]), a([top - 1, top - 1]), _native.IEKV_IDS_DST_REPEATED),
+        (a([top, 5]), a([top - 1, top]), _native.IEKV_IDS_OVERLAP),
+        (a([top, 5]), a([n, 7]), _native.IEKV_IDS_DST_RANGE),
+        (a([-1, 5]), a([top, 7]), _native.IEKV_IDS_SRC_RANGE),
+    ]
+    for src, dst, bits in cases:
+        print(f"int32-limit id check {src.tolist()} -> {dst.tolist()}", flush=True)
+        assert expected_bits(src, dst, n, n, True) == bits
+        assert run_check(pool, src, pool, dst) == bits, (src, dst)
+    pool.native.close()
+    del pool
+    torch.cuda.empty_cache()
