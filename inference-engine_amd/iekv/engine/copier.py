@@ -307,11 +307,16 @@ def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:
     """The PackedBlocks slice that ``payloads`` are consecutive rows of, if any.
 
     Payloads from different slices of one buffer count when their rows follow
-    each other there (a staging buffer filled request by request)."""
+    each other there (a staging buffer filled request by request). A strided slice
+    (``payloads[::2]``) is not one run; a single payload always is (its own row,
+    whatever buffer or slice it came from)."""
     if isinstance(payloads, PackedBlocks):
-        return payloads
+        return payloads if payloads.data.is_contiguous() else None
     if not payloads or not all(isinstance(p, BlockPayload) for p in payloads):
         return None
+    if len(payloads) == 1:
+        p = payloads[0]
+        return p.packed[p.index:p.index + 1]
     first = payloads[0].packed
     if first._offset is None:
         return None
@@ -762,6 +767,9 @@ class HipSlotCopier:
     def _restore_scattered(self, ids: "_BlockIds", payloads: Seq[BlockPayload]) -> None:
         """Host payloads from unrelated buffers (tier entries) -> iekv_restore_blocks, one
         call per group of images one direct launch takes."""
+        # A row of a strided slice is addressed through a one-row view of itself.
+        payloads = [p if p.packed.data.is_contiguous()
+                    else BlockPayload(p.packed[p.index:p.index + 1], 0) for p in payloads]
         for p in payloads:
             self._check_packed(p.packed)
         stream = torch.cuda.current_stream(self.device)

@@ -41,7 +41,7 @@ _NAMES = {v: k for k, v in _DTYPES.items()}
 
 
 def _packed_of(transfer: KVTransfer):
-    from ..engine.copier import PackedBlocks, _consecutive_views
+    from ..engine.copier import BlockPayload, PackedBlocks, _consecutive_views, stack_payloads
 
     payloads = transfer.block_payloads
     if payloads is None:
@@ -52,10 +52,13 @@ def _packed_of(transfer: KVTransfer):
         return packed
     if isinstance(payloads, PackedBlocks):
         return payloads
-    view = _consecutive_views(list(payloads))
-    if view is None:
-        raise TypeError("wire transfers need PackedBlocks payloads (the HIP copier's)")
-    return view
+    items = list(payloads)
+    view = _consecutive_views(items)
+    if view is not None:
+        return view
+    if items and all(isinstance(p, BlockPayload) for p in items):
+        return stack_payloads(items)     # rows of several buffers: gathered with one copy
+    raise TypeError("wire transfers need PackedBlocks payloads (the HIP copier's)")
 
 
 def encode_header(transfer: KVTransfer, packed) -> bytes:
