@@ -49,6 +49,29 @@ def test_round_trip_keeps_state_and_bytes():
     assert k_tiles[0].shape == (4, 2, 8) and k_tiles[0].dtype == torch.float32
 
 
+def test_payloads_of_several_buffers_and_strided_slices_go_on_the_wire():
+    """A transfer whose payload list mixes rows of two buffers, or takes every other
+    row of one (both fine for the reference's list of payloads), goes on the wire
+    as the rows in list order, gathered with one copy; the receiver's payloads are
+    those rows. A list of something other than payloads is refused."""
+    from iekv.serve.wire import from_wire, to_wire
+
+    a, _ = packed_from_oracle(blocks=(5, 1, 7), seed=1)
+    b, _ = packed_from_oracle(blocks=(2, 3), seed=2)
+    for payloads, rows in (([a[2], b[0], a[0]], [a.data[2], b.data[0], a.data[0]]),
+                           (a[::2], [a.data[0], a.data[2]]),
+                           ([a[::2][1], b[1]], [a.data[2], b.data[1]])):
+        transfer = make_transfer(a)
+        transfer.block_payloads = payloads
+        header, payload = to_wire(transfer)
+        back = from_wire(header, payload.contiguous().clone())
+        assert torch.equal(back.block_payloads.data, torch.stack(rows))
+    transfer = make_transfer(a)
+    transfer.block_payloads = [([np.zeros(4)], [np.zeros(4)])]
+    with pytest.raises(TypeError):
+        to_wire(transfer)
+
+
 def test_payload_tiles_are_the_reference_payload():
     from iekv.serve.wire import from_wire, to_wire
 
