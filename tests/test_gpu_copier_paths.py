@@ -46,7 +46,8 @@ def test_payloads_keep_the_reference_shape_and_index_like_a_list(gpu):
         assert p.nbytes == 2 * layers * bs * heads * dim * 2
         assert np.array_equal(image_of(p), want[i % 4]), i
         k, v = p
-        assert all(torch.equal(a, b) for a, b in zip(k + v, p[0] + p[1]))
+        assert all(torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+                   for a, b in zip(k + v, p[0] + p[1]))
     for bad in (4, -5):
         with pytest.raises(IndexError):
             packed[bad]
@@ -156,3 +157,61 @@ def test_host_buffers_dropped_while_their_copies_run_are_held_then_released(gpu)
     src_o = oracle_of(sk, sv, bs)
     for i, p in kept:
         assert np.array_equal(image_of(p), packed_image([src_o.read_block(i)])[0]), i
+
+
+def test_the_copier_without_torchs_raw_stream_accessors(gpu, monkeypatch):
+    """Where torch lacks its raw stream accessors the copier uses the public ones:
+    torch.cuda.current_stream for the launch stream and torch.cuda.stream for a
+    stream= call. The same calls then run on the same streams and move the same
+    bytes, and each call leaves the current stream as it found it."""
+    from iekv.engine import pools
+    from iekv.engine.copier import HipSlotCopier
+
+    monkeypatch.setattr(pools, "_raw_current_stream", None)
+    monkeypatch.setattr(pools, "_LIGHT_SCOPE", False)
+    bs, layers, heads, dim = 4, 2, 2, 16
+    sk, sv = allocate(24, bs, layers, heads, dim, torch.float16, gpu, seed=92)
+    dk, dv = allocate(24, bs, layers, heads, dim, torch.float16, gpu, seed=93)
+    src, dst = HipSlotCopier(sk, sv, bs), HipSlotCopier(dk, dv, bs)
+    src_o, dst_o = oracle_of(sk, sv, bs), oracle_of(dk, dv, bs)
+    assert pools.current_stream_handle(gpu) == torch.cuda.current_stream(gpu).cuda_stream
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    before = torch.cuda.current_stream(gpu)
+    packed = src.read_blocks([3, 9, 14], stream=side)
+    assert torch.cuda.current_stream(gpu) == before
+    dst.write_blocks([1, 2, 3], packed, stream=side)
+    dst.copy_blocks(src, [20, 21], [10, 11], stream=side)
+    assert torch.cuda.current_stream(gpu) == before
+    side.synchronize()
+    for d, s in ((1, 3), (2, 9), (3, 14), (10, 20), (11, 21)):
+        dst_o.write_block(d, src_o.read_block(s))
+    assert_pool_equals(dk, dv, dst_o)
+
+
+def test_pools_whose_arrays_interleave_in_memory_are_told_apart(gpu):
+    """Two pools may take turns along one allocation (pool A's arrays at even
+    positions, pool B's at odd ones). Their spans overlap, so only the sorted walk
+    over every array decides: they share no byte and copy into each other like two
+    allocations. A pool over part of another's arrays is refused."""
+    from iekv.engine.copier import HipSlotCopier
+    from iekv.engine.pools import KVPool
+
+    bs, heads, dim, n = 2, 2, 8, 16
+    slab = torch.randint(0, 256, (8, n * bs, heads, dim * 2), dtype=torch.uint8,
+                         device=gpu).view(torch.float16)
+    arrays = [slab[i] for i in range(8)]
+    a_k, a_v = arrays[0:4:2], arrays[4:8:2]       # arrays 0, 2 | 4, 6
+    b_k, b_v = arrays[1:4:2], arrays[5:8:2]       # arrays 1, 3 | 5, 7
+    a, b = HipSlotCopier(a_k, a_v, bs), HipSlotCopier(b_k, b_v, bs)
+    assert a.pool.memory_relation(b.pool) == "separate"
+    a_o, b_o = oracle_of(a_k, a_v, bs), oracle_of(b_k, b_v, bs)
+    b.copy_blocks(a, [0, 5, 9], [9, 5, 0])         # the same ids: separate pools
+    torch.cuda.synchronize()
+    for d, s in ((9, 0), (5, 5), (0, 9)):
+        b_o.write_block(d, a_o.read_block(s))
+    assert_pool_equals(b_k, b_v, b_o)
+    assert_pool_equals(a_k, a_v, a_o)              # the source is untouched
+    half = [t[: n * bs // 2] for t in a_k], [t[: n * bs // 2] for t in a_v]
+    with pytest.raises(ValueError, match="overlap"):
+        KVPool(*half, bs).same_pool_as(a.pool)

@@ -285,7 +285,8 @@ def test_batched_pack_moves_on_gpu_unpack_in_one_launch(gpu, monkeypatch):
     """Pack mode with batched moves: each prompt packs into the next slice of one
     staging buffer and the flush unpacks every request with one launch; the decode
     pool then holds the same bytes as after per-request admission, and decoding
-    gives the same tokens. A buffer too small for the batch flushes when full."""
+    gives the same tokens. A buffer too small for the batch flushes when full, and a
+    request larger than the whole buffer packs into a payload of its own."""
     from iekv import _native
     from iekv.serve import disaggregated
     from iekv.serve.disaggregated import DisaggregatedEngine
@@ -319,6 +320,12 @@ def test_batched_pack_moves_on_gpu_unpack_in_one_launch(gpu, monkeypatch):
     monkeypatch.setattr(disaggregated, "STAGING_ARENA_BYTES", 5 * block)
     small = DisaggregatedEngine(m, engine_config())
     assert small.generate(G["prompts"], max_new_tokens=8, batch_moves=True) == expected
+    # A one-block buffer: every request of several blocks packs into a payload of its
+    # own, the one-block ones share the buffer; the tokens do not change.
+    assert max(r["num_blocks"] for r in G["requests"]) > 1
+    monkeypatch.setattr(disaggregated, "STAGING_ARENA_BYTES", block)
+    tiny = DisaggregatedEngine(m, engine_config())
+    assert tiny.generate(G["prompts"], max_new_tokens=8, batch_moves=True) == expected
 
 
 def test_batched_prefix_aware_moves_on_gpu(gpu):

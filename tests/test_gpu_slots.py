@@ -222,3 +222,29 @@ def test_slots_and_table_entries_at_the_top_of_a_pool_of_int32_max_blocks(gpu):
     pool.native.close()
     del k, v, pool, out
     torch.cuda.empty_cache()
+
+
+def test_gather_takes_the_block_table_as_a_list_or_a_tensor(gpu):
+    """A decode loop may keep its block tables on the GPU or in a CPU tensor:
+    gather_context and the every-array gather read the same rows through a device
+    int32 or int64 tensor, a CPU tensor and a Python list, and a table too short
+    for the context raises IndexError in every form, as the reference's does."""
+    from iekv.engine.slots import gather_rows, gather_rows_arrays
+
+    bs, heads, dim = 4, 2, 16
+    k, v, pool = random_pool(30, bs, heads, dim, torch.float16, gpu, seed=91)
+    table, context = [17, 2, 29, 8], 14
+    raw = lambda t: t.view(torch.uint8)       # NaN bit patterns compare as bytes
+    want = gather_rows_arrays(pool, table, context)
+    for form in (torch.tensor(table, dtype=torch.int32, device=gpu),
+                 torch.tensor(table, dtype=torch.int64, device=gpu),
+                 torch.tensor(table, dtype=torch.int32)):
+        assert torch.equal(raw(gather_rows_arrays(pool, form, context)), raw(want))
+        for array in (0, 3):
+            assert torch.equal(raw(gather_rows(pool, array, form, context)), raw(want[array]))
+        with pytest.raises(IndexError):
+            gather_rows_arrays(pool, form[:3], context)
+        with pytest.raises(IndexError):
+            gather_rows(pool, 0, form[:3], context)
+    oracle = gather_context(as_np(k[1]), table, context, bs)
+    assert np.array_equal(as_np(want[1]), oracle.reshape(as_np(want[1]).shape))
