@@ -476,3 +476,46 @@ def test_kernel_arguments_stay_small(lib):
     small, large = sorted(sizes("kv_move_inline"))
     assert small < 400 and large > 2 * _native.INLINE_IDS * 4
     assert max(sizes("kv_scatter_rows") | sizes("kv_gather_rows")) <= 128
+
+
+def test_a_missing_or_mismatched_library_fails_loudly(tmp_path):
+    """There is no fallback: with IEKV_LIBRARY naming a file that does not exist, the
+    first use of the library raises RuntimeError naming the path and how to build
+    it; a library that exports every entry point but reports another ABI version
+    is refused by that version. Each case runs in a child process of its own."""
+    import os
+    import shutil
+    import subprocess
+    import sys
+
+    from iekv import _native
+
+    probe = ("import sys\nsys.path.insert(0, {pkg!r})\nfrom iekv import _native\n"
+             "try:\n    _native.lib()\n    print('loaded')\n"
+             "except RuntimeError as e:\n    print('refused:', e)\n"
+             ).format(pkg=str(ROOT / "inference-engine_amd"))
+
+    def first_use(library):
+        env = dict(os.environ, IEKV_LIBRARY=str(library))
+        out = subprocess.run([sys.executable, "-c", probe], env=env, capture_output=True,
+                             text=True, timeout=300)
+        assert out.returncode == 0, out.stderr[-2000:]
+        return out.stdout.strip()
+
+    missing = tmp_path / "absent" / "libiekv.so"
+    said = first_use(missing)
+    assert said.startswith("refused:") and str(missing) in said and "build" in said
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc is not installed")
+    stub = tmp_path / "stub.c"
+    stub.write_text("".join(
+        f"int {name}(void) {{ return {_native.ABI_VERSION - 1}; }}\n"
+        if name == "iekv_abi_version" else f"int {name}(void) {{ return -1; }}\n"
+        for name in _native.SIGNATURES))
+    lib = tmp_path / "libiekv_stub.so"
+    subprocess.run([gcc, "-shared", "-fPIC", str(stub), "-o", str(lib)], check=True,
+                   capture_output=True, timeout=120)
+    said = first_use(lib)
+    assert said.startswith("refused:")
+    assert f"ABI version {_native.ABI_VERSION - 1}, expected {_native.ABI_VERSION}" in said
