@@ -279,3 +279,35 @@ def test_the_two_pools_share_one_reservation_with_prefill_first():
     want = G["disaggregated"]["10"]
     assert paired.generate(G["prompts"], max_new_tokens=10, temperature=0.0) == want
     assert apart.generate(G["prompts"], max_new_tokens=10, temperature=0.0) == want
+
+
+def test_the_halved_rotary_form_is_the_interleaved_one_on_reordered_pairs():
+    """ModelConfig.rope_halved (the reference's option, ie/model/transformer.py:24)
+    rotates the pairs (i, i + D/2) of a head instead of (2i, 2i + 1): reordering the
+    head so those pairs sit side by side, applying the interleaved form and undoing
+    the reordering gives the halved form. A model built with it serves
+    disaggregated exactly as it serves colocated."""
+    import torch
+
+    from iekv.engine.engine import Engine
+    from iekv.engine.toy_model import ModelConfig, ToyTransformer, _rope
+    from iekv.serve.disaggregated import DisaggregatedEngine
+
+    gen = torch.Generator().manual_seed(5)
+    d, positions = 8, torch.tensor([0, 3, 7, 2])
+    x = torch.randn(4, 2, d, generator=gen)
+    angles = torch.randn(16, d // 2, generator=gen)
+    cos, sin = torch.cos(angles), torch.sin(angles)
+    order = torch.stack([torch.arange(d // 2), torch.arange(d // 2) + d // 2], 1).reshape(-1)
+    undo = torch.argsort(order)
+    halved = _rope(x, positions, cos, sin, True)
+    via_pairs = _rope(x[..., order], positions, cos, sin, False)[..., undo]
+    assert torch.allclose(halved, via_pairs, atol=1e-6)
+    assert not torch.allclose(halved, _rope(x, positions, cos, sin, False), atol=1e-3)
+    config = ModelConfig(**{**G["model"], "rope_halved": True})
+    make = lambda: ToyTransformer(config, seed=G["model_seed"], device="cpu")
+    alone = Engine(make(), engine_config(), copier_factory=oracle_factory).generate(
+        G["prompts"], max_new_tokens=6, temperature=0.0)
+    apart = DisaggregatedEngine(make(), engine_config(), copier_factory=oracle_factory).generate(
+        G["prompts"], max_new_tokens=6, temperature=0.0)
+    assert apart == alone
