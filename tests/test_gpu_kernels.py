@@ -464,24 +464,45 @@ def test_block_ids_at_the_top_of_the_int32_range(gpu, chunk):
     torch.cuda.empty_cache()
 
 
-def test_separately_allocated_layers_use_an_address_table(gpu):
+@pytest.mark.parametrize("layout", ["descending", "irregular"])
+def test_separately_allocated_layers_use_an_address_table(gpu, layout):
+    """Per-layer caches that do not sit at equal steps in memory make the pool keep
+    their base addresses in a device table that every kernel reads. The arrays here
+    are views of one buffer at descending or irregular positions (tensors allocated
+    one after another can land at equal steps by chance, and the library then keeps
+    only a base and a stride). Direct copy, pack -> unpack and a round trip through
+    pinned host memory between two such pools move the oracle's bytes."""
     from iekv.engine.copier import HipSlotCopier
 
-    bs, heads, dim = 16, 2, 16
-    k = [torch.randint(-128, 127, (40 * bs, heads, dim), dtype=torch.int8, device=gpu)
-         for _ in range(3)]
-    v = [torch.randint(-128, 127, (40 * bs, heads, dim), dtype=torch.int8, device=gpu)
-         for _ in range(3)]
-    dk = [torch.zeros_like(t) for t in k]
-    dv = [torch.zeros_like(t) for t in v]
-    src, dst = HipSlotCopier(k, v, bs), HipSlotCopier(dk, dv, bs)
-    assert src.pool.native.handle.value
+    bs, heads, dim, n, L = 16, 2, 16, 40, 3
+    order = {"descending": ([5, 4, 3, 2, 1, 0], [10, 8, 6, 4, 2, 0]),
+             "irregular": ([0, 3, 1, 7, 4, 9], [8, 2, 5, 0, 11, 6])}[layout]
+
+    def arrays(positions, seed):
+        gen = torch.Generator(device=gpu).manual_seed(seed)
+        buf = torch.randint(-128, 127, (max(positions) + 1, n * bs, heads, dim),
+                            dtype=torch.int8, device=gpu, generator=gen)
+        views = [buf[i] for i in positions]
+        ptrs = [t.data_ptr() for t in views]
+        steps = {b - a for a, b in zip(ptrs, ptrs[1:])}
+        assert len(steps) > 1 or ptrs[1] < ptrs[0]      # the library's table rule
+        return views[:L], views[L:]
+
+    k, v = arrays(order[0], 47)
+    dk, dv = arrays(order[1], 48)
+    src = HipSlotCopier(k, v, bs, payload_location="host", defer_reads=False)
+    dst = HipSlotCopier(dk, dv, bs)
     src_o, dst_o = oracle_of(k, v, bs), oracle_of(dk, dv, bs)
     src_ids, dst_ids = [5, 0, 39, 17], [1, 38, 2, 20]
     dst.copy_blocks(src, src_ids, dst_ids)
+    packed = src.read_blocks([6, 9, 33], location="device")
+    dst.write_blocks([10, 11, 12], packed)
+    host = src.read_blocks([21, 3], location="host")
+    dst.write_blocks([30, 31], host)
     torch.cuda.synchronize()
-    handoff(src_o, dst_o, [src_ids], [dst_ids])
+    handoff(src_o, dst_o, [src_ids, [6, 9, 33], [21, 3]], [dst_ids, [10, 11, 12], [30, 31]])
     assert_pool_equals(dk, dv, dst_o)
+    assert np.array_equal(host.host_data().numpy(), packed_image(pack(src_o, [21, 3])))
 
 
 def test_empty_requests_move_nothing(gpu):
