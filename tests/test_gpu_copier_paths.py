@@ -11,8 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.copier import pack, packed_image
-from test_gpu_kernels import allocate, assert_pool_equals, oracle_of
+from oracle.copier import handoff, pack, packed_image
+from test_gpu_kernels import allocate, assert_pool_equals, oracle_of, random_tables
 
 pytestmark = pytest.mark.gpu
 
@@ -215,3 +215,64 @@ def test_pools_whose_arrays_interleave_in_memory_are_told_apart(gpu):
     half = [t[: n * bs // 2] for t in a_k], [t[: n * bs // 2] for t in a_v]
     with pytest.raises(ValueError, match="overlap"):
         KVPool(*half, bs).same_pool_as(a.pool)
+
+
+def test_copiers_used_from_several_host_threads_at_once(gpu):
+    """The library keeps no shared mutable state on its launch path (error text is
+    per thread, launch settings are atomics, pool handles never change), so four
+    host threads, each moving requests between pools of its own on a stream of its
+    own by direct copy, pack -> unpack and with host and device ids, interleave
+    freely; every pool ends byte for byte as the oracle's sequential handoffs leave
+    it, and an error raised in one thread carries that thread's message."""
+    import threading
+
+    from iekv import _native
+    from iekv.engine.copier import HipSlotCopier
+
+    bs, layers, heads, dim, n = 4, 2, 2, 32, 64
+    jobs = []
+    for t in range(4):
+        sk, sv = allocate(n, bs, layers, heads, dim, torch.bfloat16, gpu, seed=300 + t)
+        dk, dv = allocate(n, bs, layers, heads, dim, torch.bfloat16, gpu, seed=400 + t)
+        rng = np.random.default_rng(500 + t)
+        tables = [random_tables(rng, n, n, int(rng.integers(1, 12))) for _ in range(25)]
+        jobs.append(dict(src=HipSlotCopier(sk, sv, bs), dst=HipSlotCopier(dk, dv, bs),
+                         src_o=oracle_of(sk, sv, bs), dst_o=oracle_of(dk, dv, bs),
+                         pools=(dk, dv), tables=tables, stream=torch.cuda.Stream(gpu),
+                         error=None, message=None))
+    torch.cuda.synchronize()
+    start = threading.Barrier(len(jobs))
+
+    def work(job):
+        try:
+            start.wait()
+            with torch.cuda.stream(job["stream"]):
+                for i, (s, d) in enumerate(job["tables"]):
+                    if i % 3 == 0:
+                        job["dst"].copy_blocks(job["src"], s, d)
+                    elif i % 3 == 1:
+                        job["dst"].write_blocks(d, job["src"].read_blocks(s))
+                    else:
+                        ids = lambda x: torch.tensor(x, dtype=torch.int32, device=gpu)
+                        job["dst"].copy_blocks(job["src"], ids(s), ids(d))
+                try:
+                    job["dst"].copy_blocks(job["src"], [0], [n + 7])
+                except IndexError as e:
+                    job["message"] = str(e)
+            job["stream"].synchronize()
+        except BaseException as e:        # reported by the main thread
+            job["error"] = e
+
+    threads = [threading.Thread(target=work, args=(job,)) for job in jobs]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads)
+    for job in jobs:
+        assert job["error"] is None, job["error"]
+        assert job["message"] is not None and str(n + 7) in job["message"]
+        for s, d in job["tables"]:
+            handoff(job["src_o"], job["dst_o"], [s], [d])
+        assert_pool_equals(*job["pools"], job["dst_o"])
+    assert _native.lib().iekv_abi_version() == _native.ABI_VERSION
