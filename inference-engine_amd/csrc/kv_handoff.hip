@@ -391,7 +391,7 @@ kv_move(PoolView src, PoolView dst, const char* __restrict__ src_stage,
 // per workgroup; each workgroup reads its id pair with scalar loads from the
 // kernel-argument segment, so no id buffer or upload is needed.
 // The runtime copies a launch's whole argument segment for every launch, and
-// on slower hosts each KiB of it adds about half a microsecond to the launch,
+// on slower hosts each KiB of it adds 0.5-0.8 us to the launch's host cost,
 // so the id block comes in two sizes: kSmallIdWords words for short lists (a
 // small workload's per-request tables) and the full 2 * IEKV_INLINE_IDS.
 template <int W>
@@ -728,27 +728,27 @@ using InlineKernel = void (*)(PoolView, PoolView, const char*, char*, InlineIds<
 // IEKV_EXTRA holds template arguments after HOST (the inline kernels' id-block
 // size W), empty for the other kernels.
 #define IEKV_EXTRA
-#define IEKV_PICK(KERNEL)                                                       \
-  if (align >= 16) {                                                            \
-    *vec_bytes = 16;                                                            \
-    const int u = std::min(unroll, lane_vecs);                                  \
-    if (nt) {                                                                   \
-      if (u >= 16) return KERNEL<u32x4, 16, true, SP, DP, HP IEKV_EXTRA>;                      \
-      if (u >= 8) return KERNEL<u32x4, 8, true, SP, DP, HP IEKV_EXTRA>;                        \
-      if (u >= 4) return KERNEL<u32x4, 4, true, SP, DP, HP IEKV_EXTRA>;                        \
-      if (u >= 2) return KERNEL<u32x4, 2, true, SP, DP, HP IEKV_EXTRA>;                        \
-      return KERNEL<u32x4, 1, true, SP, DP, HP IEKV_EXTRA>;                                    \
-    }                                                                           \
-    if (u >= 16) return KERNEL<u32x4, 16, false, SP, DP, HP IEKV_EXTRA>;                       \
-    if (u >= 8) return KERNEL<u32x4, 8, false, SP, DP, HP IEKV_EXTRA>;                         \
-    if (u >= 4) return KERNEL<u32x4, 4, false, SP, DP, HP IEKV_EXTRA>;                         \
-    if (u >= 2) return KERNEL<u32x4, 2, false, SP, DP, HP IEKV_EXTRA>;                         \
-    return KERNEL<u32x4, 1, false, SP, DP, HP IEKV_EXTRA>;                                     \
-  }                                                                             \
-  if (align >= 8) { *vec_bytes = 8; return KERNEL<u32x2, 4, false, SP, DP, HP IEKV_EXTRA>; }   \
+#define IEKV_PICK(KERNEL)                                                                       \
+  if (align >= 16) {                                                                            \
+    *vec_bytes = 16;                                                                            \
+    const int u = std::min(unroll, lane_vecs);                                                  \
+    if (nt) {                                                                                   \
+      if (u >= 16) return KERNEL<u32x4, 16, true, SP, DP, HP IEKV_EXTRA>;                       \
+      if (u >= 8) return KERNEL<u32x4, 8, true, SP, DP, HP IEKV_EXTRA>;                         \
+      if (u >= 4) return KERNEL<u32x4, 4, true, SP, DP, HP IEKV_EXTRA>;                         \
+      if (u >= 2) return KERNEL<u32x4, 2, true, SP, DP, HP IEKV_EXTRA>;                         \
+      return KERNEL<u32x4, 1, true, SP, DP, HP IEKV_EXTRA>;                                     \
+    }                                                                                           \
+    if (u >= 16) return KERNEL<u32x4, 16, false, SP, DP, HP IEKV_EXTRA>;                        \
+    if (u >= 8) return KERNEL<u32x4, 8, false, SP, DP, HP IEKV_EXTRA>;                          \
+    if (u >= 4) return KERNEL<u32x4, 4, false, SP, DP, HP IEKV_EXTRA>;                          \
+    if (u >= 2) return KERNEL<u32x4, 2, false, SP, DP, HP IEKV_EXTRA>;                          \
+    return KERNEL<u32x4, 1, false, SP, DP, HP IEKV_EXTRA>;                                      \
+  }                                                                                             \
+  if (align >= 8) { *vec_bytes = 8; return KERNEL<u32x2, 4, false, SP, DP, HP IEKV_EXTRA>; }    \
   if (align >= 4) { *vec_bytes = 4; return KERNEL<uint32_t, 4, false, SP, DP, HP IEKV_EXTRA>; } \
   if (align >= 2) { *vec_bytes = 2; return KERNEL<uint16_t, 4, false, SP, DP, HP IEKV_EXTRA>; } \
-  *vec_bytes = 1;                                                               \
+  *vec_bytes = 1;                                                                               \
   return KERNEL<uint8_t, 4, false, SP, DP, HP IEKV_EXTRA>;
 
 template <bool SP, bool DP, bool HP>
@@ -774,10 +774,10 @@ InlineKernel<W> pick_inline_kernel_as(int align, int unroll, int lane_vecs, bool
 
 // The kernels of a move; `host`: an unpack that reads pinned host memory (move_entry's
 // HOST variant). Only unpacks have one.
-#define IEKV_PICK_HOST(NAME)                                                           \
-  if constexpr (!SP && DP) {                                                           \
+#define IEKV_PICK_HOST(NAME)                                                                    \
+  if constexpr (!SP && DP) {                                                                    \
     if (host) return NAME##_as<SP, DP, true IEKV_EXTRA>(align, unroll, lane_vecs, nt, vec_bytes); \
-  }                                                                                    \
+  }                                                                                             \
   return NAME##_as<SP, DP, false IEKV_EXTRA>(align, unroll, lane_vecs, nt, vec_bytes);
 
 template <bool SP, bool DP>
