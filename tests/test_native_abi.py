@@ -519,3 +519,46 @@ def test_a_missing_or_mismatched_library_fails_loudly(tmp_path):
     said = first_use(lib)
     assert said.startswith("refused:")
     assert f"ABI version {_native.ABI_VERSION - 1}, expected {_native.ABI_VERSION}" in said
+
+
+def test_pool_shapes_devices_and_slot_ranges_are_checked_before_any_launch(lib):
+    """Moves between pools of different tile layouts or devices, slot calls over
+    layers or arrays the pool does not have or with a block size that does not
+    divide the tile, and a timing session of no launches are each refused with
+    IEKV_ERR_INVALID and a message naming the problem, before any HIP call (slab
+    pools register without touching a GPU, whatever device they name)."""
+    from iekv import _native
+
+    a = _native.Pool([1 << 20, (1 << 20) + 64 * 16], tile_bytes=64, num_blocks=16, device=0)
+    b = _native.Pool([1 << 24, (1 << 24) + 128 * 16], tile_bytes=128, num_blocks=16, device=0)
+    c = _native.Pool([1 << 28, (1 << 28) + 64 * 16], tile_bytes=64, num_blocks=16, device=1)
+    ids = (ctypes.c_int32 * 2)(0, 1)
+    counts = (ctypes.c_int32 * 1)(2)
+    streams = (ctypes.c_void_p * 1)(None)
+    slots = (ctypes.c_int64 * 2)(0, 1)
+    rows = ctypes.create_string_buffer(4096)
+    table = (ctypes.c_int32 * 2)(0, 1)
+
+    def refused(code, *expect):
+        assert code == _native.IEKV_ERR_INVALID, code
+        message = lib.iekv_last_error().decode()
+        assert all(e in message for e in expect), message
+
+    for other, why in ((b, "differ in shape"), (c, "devices 0 and 1")):
+        refused(lib.iekv_copy_direct(a.handle, other.handle, ids, ids, 2, None), why)
+        refused(lib.iekv_copy_direct_ids(a.handle, other.handle, ids, ids, 2, None), why)
+        refused(lib.iekv_copy_direct_requests(a.handle, other.handle, 1, counts, ids, ids,
+                                              streams, 1, None), why)
+    # a has one layer (a K and a V array) of 64-byte tiles
+    refused(lib.iekv_write_slots_layers(a.handle, 0, 2, 4, rows, rows, 0, slots, 2, None),
+            "layers 0..1 out of range for 1 layers")
+    refused(lib.iekv_write_slots_layers(a.handle, 0, 1, 3, rows, rows, 0, slots, 2, None),
+            "block_size 3 does not divide the 64-byte tile")
+    refused(lib.iekv_gather_rows_arrays(a.handle, 1, 2, 4, table, 8, rows, len(rows), None),
+            "arrays 1..2 out of range for 2 arrays")
+    refused(lib.iekv_gather_rows_arrays(a.handle, 0, 2, 5, table, 8, rows, len(rows), None),
+            "block_size 5 does not divide the 64-byte tile")
+    for n in (0, (1 << 20) + 1):
+        refused(lib.iekv_profile_start(n), f"max_launches {n} out of range")
+    for pool in (a, b, c):
+        pool.close()
