@@ -562,3 +562,23 @@ def test_pool_shapes_devices_and_slot_ranges_are_checked_before_any_launch(lib):
         refused(lib.iekv_profile_start(n), f"max_launches {n} out of range")
     for pool in (a, b, c):
         pool.close()
+
+
+def test_the_integration_guides_ctypes_stub_matches_the_abi():
+    """INTEGRATION.md shows the ctypes binding a maintainer of the reference would
+    add; every argument list it declares must be the one the library is bound with
+    here (iekv._native.SIGNATURES, itself checked against include/iekv.h)."""
+    from ctypes import POINTER, c_int32, c_int64, c_uint64, c_void_p
+
+    from iekv import _native
+
+    text = (ROOT / "INTEGRATION.md").read_text()
+    aliases = {"u64p": POINTER(c_uint64), "vp": c_void_p, "i32": c_int32, "i64": c_int64,
+               "ctypes.POINTER(vp)": POINTER(c_void_p)}
+    declared = re.findall(r"^lib\.(iekv_\w+)\.argtypes = \[([^\]]*)\]", text, re.M)
+    assert len(declared) >= 5
+    for name, args in declared:
+        got = [aliases[a.strip()] for a in args.split(",")]
+        want = _native.SIGNATURES[name][1]
+        assert got == want, (name, got, want)
+    assert "lib.iekv_last_error.restype = ctypes.c_char_p" in text
