@@ -565,9 +565,9 @@ def test_pool_shapes_devices_and_slot_ranges_are_checked_before_any_launch(lib):
 
 
 def test_the_integration_guides_ctypes_stub_matches_the_abi():
-    """INTEGRATION.md shows the ctypes binding a maintainer of the reference would
-    add; every argument list it declares must be the one the library is bound with
-    here (iekv._native.SIGNATURES, itself checked against include/iekv.h)."""
+    """The integration guide shows the ctypes binding a maintainer of the reference
+    would add; every argument list it declares must be the one the library is bound
+    with here (iekv._native.SIGNATURES, itself checked against include/iekv.h)."""
     from ctypes import POINTER, c_int32, c_int64, c_uint64, c_void_p
 
     from iekv import _native
