@@ -34,6 +34,7 @@ from __future__ import annotations
 import contextlib
 import ctypes
 import operator
+import threading
 import weakref
 from array import array
 from typing import Any, Iterable, Sequence as Seq
@@ -287,20 +288,32 @@ class DeferredBlockPayload(BlockPayload):
 
 # Pinned buffers whose PackedBlocks died while a copy still used them, each with
 # that copy's event. Holding them keeps torch's pinned cache from handing the
-# memory out again before the copy is done; they are dropped once it is.
+# memory out again before the copy is done; they are dropped once it is. Payloads
+# die in whatever thread drops them, even inside the pruning below (a garbage
+# collection there runs their __del__ in the same thread), so the lock is
+# reentrant and pruning pops entries one by one: one added meanwhile is popped
+# and judged too, never lost.
 _UNFINISHED: list[tuple[torch.Tensor, torch.cuda.Event]] = []
+_UNFINISHED_LOCK = threading.RLock()
 
 
 def _hold_until_done(data: torch.Tensor, ev: torch.cuda.Event) -> None:
-    _UNFINISHED.append((data, ev))
-    if len(_UNFINISHED) >= 32:
+    with _UNFINISHED_LOCK:
+        _UNFINISHED.append((data, ev))
+        crowded = len(_UNFINISHED) >= 32
+    if crowded:
         _release_finished()
 
 
 def _release_finished() -> None:
     """Drop the held buffers whose copies have completed (no waiting)."""
-    if _UNFINISHED:
-        _UNFINISHED[:] = [(d, e) for d, e in _UNFINISHED if not e.query()]
+    with _UNFINISHED_LOCK:
+        running = []
+        while _UNFINISHED:
+            held = _UNFINISHED.pop()
+            if not held[1].query():
+                running.append(held)
+        _UNFINISHED.extend(running)
 
 
 def _consecutive_views(payloads: Seq[Any]) -> PackedBlocks | None:

@@ -117,3 +117,66 @@ def test_the_round_trip_leg_pins_exactly_its_image_and_checks_the_host():
         bench.check_host_budget(plan, 40 << 30)
     budget = bench.host_memory_budget()
     assert budget is None or budget > 0
+
+
+def test_held_pinned_buffers_survive_pruning_reentry_and_threads():
+    """Buffers whose copy still runs are held until their event completes. Pruning
+    must lose none of them: not one added from inside the pruning itself (a payload
+    dying in a garbage collection there, in the same thread, which must not
+    deadlock either), nor ones added by other threads while it runs. Stand-in events
+    whose query() answers from a flag play the copies."""
+    import threading
+
+    import torch
+
+    from iekv.engine import copier
+
+    class Copy:
+        def __init__(self, done=False, on_query=None):
+            self.done, self.on_query = done, on_query
+
+        def query(self):
+            if self.on_query is not None:
+                hook, self.on_query = self.on_query, None
+                hook()
+            return self.done
+
+    data = torch.zeros(1)
+    copier._release_finished()
+    saved = list(copier._UNFINISHED)
+    copier._UNFINISHED.clear()
+    try:
+        late = Copy()
+        copier._hold_until_done(data, Copy(done=True))
+        copier._hold_until_done(data, Copy(on_query=lambda: copier._hold_until_done(data, late)))
+        copier._release_finished()
+        events = [e for _, e in copier._UNFINISHED]
+        assert late in events and len(events) == 2       # the finished one went, none lost
+        running = [Copy() for _ in range(400)]
+        start = threading.Barrier(5)
+
+        def add(chunk):
+            start.wait()
+            for ev in chunk:
+                copier._hold_until_done(data, ev)
+
+        def prune():
+            start.wait()
+            for _ in range(200):
+                copier._release_finished()
+
+        threads = [threading.Thread(target=add, args=(running[i::4],)) for i in range(4)]
+        threads.append(threading.Thread(target=prune))
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join(timeout=60)
+        assert not any(th.is_alive() for th in threads)
+        held = {id(e) for _, e in copier._UNFINISHED}
+        assert all(id(ev) in held for ev in running)
+        for _, ev in copier._UNFINISHED:
+            ev.done = True
+        copier._release_finished()
+        assert copier._UNFINISHED == []
+    finally:
+        copier._UNFINISHED[:] = saved
