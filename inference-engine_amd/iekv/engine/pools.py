@@ -117,10 +117,9 @@ def pinned_empty(nbytes: int) -> torch.Tensor:
     every view of it is gone; :func:`release_pinned` returns unused buffers."""
     if nbytes <= 0:
         raise ValueError("nbytes must be positive")
-    free = _PINNED_FREE.get(nbytes)
-    if free:
-        ptr = free.pop()
-    else:
+    try:   # the pop alone: another thread may take the last free buffer first
+        ptr = _PINNED_FREE[nbytes].pop()
+    except (KeyError, IndexError):
         out = ctypes.c_void_p()
         _native.call("iekv_host_alloc", nbytes, ctypes.byref(out))
         ptr = out.value
@@ -129,7 +128,7 @@ def pinned_empty(nbytes: int) -> torch.Tensor:
 
 def pinned_bytes_cached() -> int:
     """Bytes of pinned buffers :func:`pinned_empty` holds for reuse."""
-    return sum(size * len(ptrs) for size, ptrs in _PINNED_FREE.items())
+    return sum(size * len(ptrs) for size, ptrs in list(_PINNED_FREE.items()))
 
 
 def release_pinned() -> int:
@@ -137,9 +136,13 @@ def release_pinned() -> int:
     buffer is unused once its last tensor died, and host payloads keep their tensors
     alive until their copies finish). Returns the bytes freed."""
     freed = 0
-    for size, ptrs in _PINNED_FREE.items():
-        while ptrs:
-            _native.call("iekv_host_free", ptrs.pop())
+    for size, ptrs in list(_PINNED_FREE.items()):   # sizes other threads add are skipped
+        while True:
+            try:
+                ptr = ptrs.pop()
+            except IndexError:
+                break
+            _native.call("iekv_host_free", ptr)
             freed += size
     return freed
 
