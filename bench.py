@@ -36,6 +36,13 @@ without NaN codes for fp8). Legs:
                included), one iekv_gather_rows_arrays launch per request (read + write
                of every row); gather_per_array: one iekv_gather_rows launch per request
                and array, as the reference calls gather_context once per cache
+  queue        the direct handoffs served by the resident request queue
+               (iekv.engine.queue.HandoffQueue): each step's requests submitted with one
+               library call (iekv_queue_submit_requests, one descriptor and ticket per
+               request), then the last ticket waited for; timed by the host clock from
+               the first submission to the last completion (2P bytes). Also reports each
+               request's latency, submitted and waited for alone (ms_per_request)
+  queue_py     the same with one HandoffQueue.submit call per request from Python
   host_roundtrip  every moved block offloaded to pinned host memory with one iekv_offload
                and restored with one iekv_restore (host-link bound), then the same
                calls once per block on up to 1,024 blocks, then the drop-in tier path
@@ -82,7 +89,10 @@ METRIC = "KV handoff GB/s (read+write) and % of HBM peak; ms per request handoff
 # Legs that move the workload's blocks from the prefill pool to the decode pool; the
 # first of them in --legs gives the line's value (2P / step time).
 HANDOFF_LEGS = ("direct", "pack_unpack", "pack", "unpack", "batched", "copier",
-                "copier_pack_unpack", "requests", "direct_ids")
+                "copier_pack_unpack", "requests", "direct_ids", "queue", "queue_py")
+# Legs served by the resident request queue: timed by the host clock (the kernel runs
+# for the whole pass, so there are no launches to time), the queue stopped after them.
+QUEUE_LEGS = ("queue", "queue_py")
 # The slot kernels on either side of the handoff (prefill's KV writes, decode's reads).
 SLOT_LEGS = ("write_kv", "write_kv_per_layer", "gather_context", "gather_per_array")
 # Requests of up to this many payload bytes (one direction) overlap on two request
@@ -284,7 +294,7 @@ class Legs:
     def plan(self, name: str) -> list[tuple[int, int]]:
         bb = self.w.shape.block_bytes
         sizes = [len(t) for t in self.w.src_tables]
-        if name in ("direct", "requests"):
+        if name in ("direct", "requests", *QUEUE_LEGS):
             return [(2 * n * bb, r) for r, n in enumerate(sizes)]
         if name == "pack_unpack":
             return [x for r, n in enumerate(sizes) for x in ((2 * n * bb, r), (2 * n * bb, r))]
@@ -569,6 +579,50 @@ class Legs:
                      len(counts), counts.buffer_info()[0], src.data_ptr(), dst.data_ptr(),
                      handles, len(hs), None)
         self._join()
+
+    def _queue(self):
+        """The request queue over the two pools and the step's tables as int32 arrays."""
+        if not hasattr(self, "_handoff_queue"):
+            import numpy as np
+
+            from iekv.engine.queue import HandoffQueue
+
+            self._handoff_queue = HandoffQueue(self.src, self.dst)
+            tables = [(np.asarray(s, dtype=np.int32), np.asarray(d, dtype=np.int32))
+                      for s, d in zip(self.w.src_tables, self.w.dst_tables)]
+            self._queue_tables = tables
+            self._queue_batch = (np.array([s.size for s, _ in tables], dtype=np.int32),
+                                 np.concatenate([s for s, _ in tables]),
+                                 np.concatenate([d for _, d in tables]))
+        return self._handoff_queue
+
+    def queue(self) -> None:
+        """Every request submitted to the resident queue in one library call (its own
+        descriptor and ticket each), then the last ticket waited for."""
+        q = self._queue()
+        q.submit_requests(*self._queue_batch)
+        q.wait()
+
+    def queue_py(self) -> None:
+        """Every request submitted to the resident queue with its own Python call."""
+        q = self._queue()
+        for s, d in self._queue_tables:
+            q.submit(s, d)
+        q.wait()
+
+    def queue_latency(self) -> list[float]:
+        """Milliseconds from submitting each request alone to its completion."""
+        q = self._queue()
+        out = []
+        for s, d in self._queue_tables:
+            t0 = time.perf_counter()
+            q.wait(q.submit(s, d))
+            out.append(1000 * (time.perf_counter() - t0))
+        return out
+
+    def stop_queue(self) -> None:
+        if hasattr(self, "_handoff_queue"):
+            self._handoff_queue.stop()
 
     def batched(self) -> None:
         from iekv import _native
@@ -887,6 +941,34 @@ def time_leg(legs: Legs, name: str, steps: int, warmup: int, per_launch: bool = 
     return ms_step, wall, launches
 
 
+def time_queue_leg(legs: Legs, name: str, steps: int, warmup: int):
+    """Warm up, then time ``steps`` steps of a queue leg by the host clock: each step
+    from its first submission to the completion of its last request (the queue's
+    kernel stays resident over the whole pass, and a step ends only when the host
+    has seen every request done). Then every request once more, each submitted and
+    waited for alone (``legs.queue_ms``), and the queue stopped. Returns (ms per
+    step, wall seconds, [])."""
+    step = getattr(legs, name)
+    legs.torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    times = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        h0 = time.perf_counter()
+        step()
+        times.append(1000 * (time.perf_counter() - h0))
+    wall = time.perf_counter() - t0
+    legs.step_ms[name] = times
+    legs.issue_ms[name] = times
+    legs.queue_ms = legs.queue_latency()
+    stats = legs._handoff_queue.stats()
+    legs.stop_queue()
+    log(f"[bench] {name}: {stats['descriptors']} descriptors in {stats['launches']} kernel "
+        f"launch(es)")
+    return sum(times) / steps, wall, []
+
+
 def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: int, steps: int):
     w = legs.w
     if not launches:   # not a kv_move leg: one "launch" per step, timed by the step events
@@ -914,8 +996,11 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
         "avg_launch_us": round(1000 * total_ms / max(1, len(durations)), 2),
         "blocks_per_s": round(w.num_blocks / (ms_step * 1e-3), 1),
     }
+    if name in QUEUE_LEGS:
+        # each request submitted and waited for alone: its latency seen from the host
+        req_ms = sorted(getattr(legs, "queue_ms", None) or [ms_step])
     if name in ("direct", "direct_ids", "copier", "requests", "pack_unpack",
-                "copier_pack_unpack", "pack", "unpack", *SLOT_LEGS):
+                "copier_pack_unpack", "pack", "unpack", *SLOT_LEGS, *QUEUE_LEGS):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),
                                  "p50": round(req_ms[len(req_ms) // 2], 4),
                                  "p99": round(req_ms[min(len(req_ms) - 1,
@@ -1361,8 +1446,9 @@ def main() -> int:
                          "(default: cfg3 64; cfg4 the cfg3 engine's pools, 49,598 blocks)")
     ap.add_argument("--legs", default="direct,pack_unpack,plain_copy",
                     help="comma list of direct, pack_unpack, pack, unpack, batched, copier, "
-                         "copier_pack_unpack, requests, write_kv, write_kv_per_layer, "
-                         "gather_context, gather_per_array, plain_copy, host_roundtrip")
+                         "copier_pack_unpack, requests, queue, queue_py, write_kv, "
+                         "write_kv_per_layer, gather_context, gather_per_array, plain_copy, "
+                         "host_roundtrip")
     ap.add_argument("--cpu-blocks", type=int, default=1536,
                     help="blocks in the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -1477,7 +1563,10 @@ def main() -> int:
             continue
         if name not in ("gather_context", "gather_per_array"):
             legs.clear_dst()
-        ms, wall, launches = time_leg(legs, name, args.steps, args.warmup)
+        if name in QUEUE_LEGS:
+            ms, wall, launches = time_queue_leg(legs, name, args.steps, args.warmup)
+        else:
+            ms, wall, launches = time_leg(legs, name, args.steps, args.warmup)
         nbytes = 2 * (4 << 30) if name == "plain_copy" else sum(b for b, _ in legs.plan(name))
         res, kgbs, avg_us, avg_bytes = summarize(legs, name, ms, launches, nbytes, args.steps)
         res["wall_s"] = round(wall, 3)
@@ -1535,7 +1624,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(kgbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_source": traffic_source,
-                     "kernel": f"kv_move ({name})", "avg_launch_us": round(avg_us, 2),
+                     "kernel": "kv_queue" if name in QUEUE_LEGS else f"kv_move ({name})",
+                     "avg_launch_us": round(avg_us, 2),
                      "algorithmic_bytes_per_launch": int(avg_bytes)},
         "cpu_baseline": cpu,
     }

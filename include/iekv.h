@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define IEKV_ABI_VERSION 20
+#define IEKV_ABI_VERSION 21
 
 enum {
   IEKV_OK = 0,
@@ -62,8 +62,9 @@ enum {
   IEKV_ERR_HIP = -2,     /* a HIP runtime call failed */
   IEKV_ERR_CAPACITY = -3, /* a buffer is too small for the requested blocks */
   IEKV_ERR_RANGE = -4,   /* a host block id outside its pool (the *_ids entry points) */
-  IEKV_ERR_IDS = -5      /* host ids that conflict: a destination block twice in one call,
+  IEKV_ERR_IDS = -5,     /* host ids that conflict: a destination block twice in one call,
                             or a copy within one pool whose sources overlap its destinations */
+  IEKV_ERR_TIMEOUT = -6  /* iekv_queue_wait: the requests did not finish in time */
 };
 
 /* Opaque handle describing one paged pool: the base address of each of its
@@ -465,6 +466,91 @@ int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
  * No reference counterpart: a tuning knob, like iekv_set_launch. */
 int iekv_set_direct_chunk(int32_t chunk_bytes);
 int iekv_get_direct_chunk(int32_t* chunk_bytes);
+
+/* ---- Request queue: per-request direct handoffs without a launch each ----
+ *
+ * A queue serves direct handoffs (iekv_copy_direct_ids's move) between one
+ * source and one destination pool through a resident kernel, so a request costs
+ * the host a descriptor write instead of a kernel launch. The kernel (one
+ * leader workgroup and `workers` mover workgroups) reads descriptors from a
+ * ring in pinned host memory, copies them to device memory, and the movers
+ * claim each request's tiles a few at a time; the last mover to finish a
+ * request writes its completion to the ring, where iekv_queue_wait reads it.
+ *
+ * Every wait of the kernel is bounded: it ends after iekv_queue_stop, after
+ * `idle_us` without a new request, or `life_us` after it started, whichever
+ * comes first. The library restarts it by itself (a stop that drains every
+ * request already submitted, then one launch) before a submission when the
+ * last one is more than idle_us / 2 old, or the kernel more than life_us / 2,
+ * so a submitted request is never left to a kernel that may already have ended.
+ *
+ * Ordering. Requests are moved as soon as they are submitted, independently of
+ * every stream: the caller submits only requests whose source blocks are
+ * written (e.g. after synchronizing the stream that wrote them), and reads a
+ * destination only after iekv_queue_wait (or iekv_queue_poll) reports its
+ * ticket done. Requests in flight together must not share destination blocks,
+ * nor write blocks another one reads. Each request's ids are checked as
+ * iekv_copy_direct_ids checks them. Calls on one queue are serialized by a
+ * lock; the pools must outlive the queue. While it runs, the kernel holds
+ * workers + 1 workgroups resident (by default 4 per compute unit, a quarter of
+ * the wave slots), so other kernels share the GPU with it.
+ *
+ * No reference counterpart: the reference hands off one request at a time
+ * (DisaggregatedEngine.generate, ie/serve/disaggregated.py:106-116, each a
+ * disaggregated.py:50 read + :81-82 write); this serves that call pattern for
+ * requests of a few MB, whose launches otherwise cost more than their bytes. */
+typedef struct iekv_queue iekv_queue;
+
+/* Descriptors in flight at once (a submission waits for the one IEKV_QUEUE_SLOTS
+ * earlier to finish), and blocks per descriptor (a longer request is split into
+ * several descriptors; its ticket is that of the last). */
+#define IEKV_QUEUE_SLOTS 256
+#define IEKV_QUEUE_MAX_BLOCKS 1024
+/* Ticket of an empty request: already done. */
+#define IEKV_QUEUE_DONE UINT64_MAX
+
+/* Make a queue for direct handoffs from `src` to `dst` (same n_arrays and
+ * tile_bytes, one device). workers: mover workgroups (0: 4 per compute unit);
+ * claim_bytes: most bytes one mover claims at once (0: 128 KiB); idle_us /
+ * life_us: the kernel's idle and lifetime limits (0: 200 ms / 60 s). Allocates
+ * the rings (about 2 MiB of pinned host memory, 11 MiB of device memory) and a
+ * stream; launches nothing until the first submission. */
+int iekv_queue_create(const iekv_pool* src, const iekv_pool* dst, int32_t workers,
+                      int64_t claim_bytes, int64_t idle_us, int64_t life_us,
+                      iekv_queue** out);
+
+/* Submit one request: tile src_ids[i] of every array onto tile dst_ids[i]
+ * (HOST memory, n_blocks of each, checked first). *ticket identifies it for
+ * iekv_queue_wait / iekv_queue_poll (tickets grow by one per descriptor over
+ * the queue's life); n_blocks == 0 gives IEKV_QUEUE_DONE. */
+int iekv_queue_submit(iekv_queue* q, const int32_t* src_ids, const int32_t* dst_ids,
+                      int32_t n_blocks, uint64_t* ticket);
+
+/* Submit n_requests requests in one call, as iekv_queue_submit would one after
+ * another: request k moves counts[k] blocks, its ids following request k-1's in
+ * src_ids / dst_ids (HOST memory); tickets[k] receives its ticket. Every request
+ * is checked before any is submitted. */
+int iekv_queue_submit_requests(iekv_queue* q, int32_t n_requests, const int32_t* counts,
+                               const int32_t* src_ids, const int32_t* dst_ids,
+                               uint64_t* tickets);
+
+/* Wait until every request up to and including `ticket` is done, or return
+ * IEKV_ERR_TIMEOUT after timeout_us (< 0: 10 s). IEKV_ERR_INVALID for a ticket
+ * not issued yet. */
+int iekv_queue_wait(iekv_queue* q, uint64_t ticket, int64_t timeout_us);
+
+/* *done = 1 when every request up to and including `ticket` is done, else 0. */
+int iekv_queue_poll(iekv_queue* q, uint64_t ticket, int32_t* done);
+
+/* Finish every submitted request, end the kernel and wait for it to exit.
+ * The next submission starts it again. */
+int iekv_queue_stop(iekv_queue* q);
+
+/* Stop the queue and release it. */
+int iekv_queue_destroy(iekv_queue* q);
+
+/* Counters of a queue: requests (descriptors) served, kernel launches (sessions). */
+int iekv_queue_stats(const iekv_queue* q, uint64_t* descriptors, uint64_t* launches);
 
 #ifdef __cplusplus
 }

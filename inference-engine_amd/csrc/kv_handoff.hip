@@ -26,10 +26,14 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdint>
 #include <cstdio>
+#include <cstring>
 #include <mutex>
+#include <thread>
 #include <new>
 #include <string>
 #include <type_traits>
@@ -1709,6 +1713,599 @@ int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
       });
 }
 
+// ---------------------------------------------------------------------------
+// Request queue (iekv_queue_*): a resident kernel serving direct handoffs
+// ---------------------------------------------------------------------------
+// The host writes descriptor r (a header and the request's ids) into slot
+// r % kQueueSlots of a ring in pinned, coherent host memory and publishes it by
+// raising `tail` to r + 1. Workgroup 0 of the kernel (the leader) polls `tail`,
+// copies each new descriptor to the device's ring, maps the descriptor's claims
+// in the claim ring (iekv_plan::queue_claims) and raises `published_claims`.
+// The other workgroups (movers) take claims from one cursor, `next_claim`, wait
+// until their claim is published, move its units, and count it in the slot's
+// `done` word; the mover that finishes a descriptor's last claim writes r + 1
+// into the slot's `complete` word in host memory. The host reuses a slot only
+// after its descriptor is complete, so no mover reads a slot that is being
+// rewritten, and the claim ring holds twice the claims of every descriptor in
+// flight, so no entry is rewritten while its claim waits.
+// Every wait ends: the leader's poll and a mover's wait for its claim both end
+// on the stop flag, after idle_ticks without a new descriptor, or life_ticks
+// after the workgroup started. The host keeps its submissions inside half of
+// each limit (queue_publish), so no descriptor is published to a kernel that
+// may be ending.
+constexpr int kQueueSlots = IEKV_QUEUE_SLOTS;
+constexpr int kQueueBlocks = IEKV_QUEUE_MAX_BLOCKS;
+constexpr int64_t kQueueClaimRing = iekv_plan::queue_claim_ring(kQueueSlots);
+
+struct QueueHeader {
+  uint64_t claim_base;   // the descriptor's first claim in its session
+  uint64_t done_target;  // the slot's `done` count once the descriptor is finished
+  int32_t n_blocks;
+  int32_t n_units;       // n_blocks * units per block
+  int32_t k;             // units per claim
+  int32_t n_claims;
+};
+
+// Pinned host memory, mapped for the device. The host writes tail, stop,
+// stop_claims, the headers and the ids; the device writes `complete`.
+struct QueueRing {
+  alignas(64) uint64_t tail;
+  alignas(64) uint64_t stop;
+  uint64_t stop_claims;
+  alignas(64) uint64_t complete[kQueueSlots];
+  alignas(64) QueueHeader header[kQueueSlots];
+  alignas(64) int32_t ids[kQueueSlots][2 * kQueueBlocks];  // sources, destinations at +kQueueBlocks
+};
+
+// Device memory. Everything before `header` is cleared when a session starts.
+struct QueueState {
+  alignas(64) uint64_t next_claim;
+  alignas(64) uint64_t published_claims;
+  uint64_t stop;
+  uint64_t stop_claims;
+  alignas(64) uint64_t done[kQueueSlots];
+  alignas(64) QueueHeader header[kQueueSlots];
+  alignas(64) int32_t ids[kQueueSlots][2 * kQueueBlocks];
+  alignas(64) uint32_t claim_desc[kQueueClaimRing];
+};
+
+struct QueueArgs {
+  PoolView src, dst;
+  QueueState* state;
+  QueueRing* ring;         // the device's address of the host ring
+  int32_t tile_vecs;
+  int32_t n_arrays;
+  int32_t group;           // tiles per unit (small tiles are moved in groups)
+  int32_t units_per_block;
+  uint64_t idle_ticks;     // wall-clock ticks
+  uint64_t life_ticks;
+};
+
+// A word of the host ring, read over the host link as the host last wrote it.
+template <typename T>
+__device__ __forceinline__ T host_word(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// A word of the device ring, after the acquire that made it visible. An atomic
+// load is always a vector load: a plain one of a uniform address may be read
+// through the scalar cache, which an acquire does not refresh, and a slot's
+// words change between descriptors.
+template <typename T>
+__device__ __forceinline__ T ring_word(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <typename T>
+__device__ __forceinline__ T agent_word(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A pause of about 0.25 us per unit (s_sleep 8 is 512 clocks).
+__device__ __forceinline__ void queue_nap(int units) {
+  for (int i = 0; i < units; ++i) __builtin_amdgcn_s_sleep(8);
+}
+
+__device__ __forceinline__ bool queue_expired(const QueueArgs& q, uint64_t start,
+                                              uint64_t last) {
+  const uint64_t now = wall_clock64();
+  return now - last > q.idle_ticks || now - start > q.life_ticks;
+}
+
+// Inclusive sum of v over the workgroup's threads (`scratch`: kThreads words of LDS).
+__device__ int64_t workgroup_scan(int64_t v, int64_t* scratch) {
+  const int t = threadIdx.x;
+  scratch[t] = v;
+  __syncthreads();
+  for (int d = 1; d < kThreads; d <<= 1) {
+    const int64_t add = t >= d ? scratch[t - d] : 0;
+    __syncthreads();
+    scratch[t] += add;
+    __syncthreads();
+  }
+  return scratch[t];
+}
+
+// The last of the first `count` entries of ascending `first` that is at most w.
+__device__ __forceinline__ int owner_of(const int64_t* first, int count, int64_t w) {
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (first[mid] <= w) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+static_assert(kQueueSlots <= kThreads, "the leader reads every new header at once");
+constexpr int kLeaderBatch = 8;   // host-ring words in flight per lane
+
+// Workgroup 0: publish the host's descriptors to the movers. Every descriptor
+// published since the last round is fetched at once: one header per thread, then
+// the ids and the claim map over one index space spanning them all, so a round
+// costs a few trips over the host link however many descriptors it brings.
+__device__ void queue_leader(const QueueArgs& q, uint64_t start) {
+  __shared__ uint64_t s_word[2];
+  __shared__ QueueHeader s_head[kQueueSlots];
+  __shared__ int64_t s_scan[kThreads];
+  __shared__ int64_t s_first_id[kThreads];   // first id word of each new descriptor
+  const int t = threadIdx.x;
+  QueueState* st = q.state;
+  const QueueRing* ring = q.ring;
+  uint64_t published = 0, last = start;
+  int nap = 1;
+  for (;;) {
+    if (t == 0) {
+      // stop before tail: a stop the host raised after its last tail is seen
+      // together with that tail.
+      s_word[0] = __hip_atomic_load(&ring->stop, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+      s_word[1] = __hip_atomic_load(&ring->tail, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    __syncthreads();
+    const uint64_t stop = s_word[0], tail = s_word[1];
+    __syncthreads();
+    if (tail > published) {
+      // The host has at most kQueueSlots descriptors unfinished, so at most that
+      // many are new.
+      const int fresh = static_cast<int>(min<uint64_t>(tail - published, kQueueSlots));
+      int32_t n_blocks = 0;
+      if (t < fresh) {
+        // Clamped to what the rings hold, so no index a mover derives from a
+        // header can leave them.
+        const QueueHeader* h = &ring->header[(published + t) % kQueueSlots];
+        QueueHeader v;
+        v.claim_base = host_word(&h->claim_base);
+        v.done_target = host_word(&h->done_target);
+        n_blocks = min(max(host_word(&h->n_blocks), 0), kQueueBlocks);
+        v.n_blocks = n_blocks;
+        v.n_units = min(max(host_word(&h->n_units), 0), n_blocks * q.units_per_block);
+        v.k = max(host_word(&h->k), 1);
+        v.n_claims = min(max(host_word(&h->n_claims), 0),
+                         static_cast<int32_t>(iekv_plan::kQueueMaxClaims));
+        s_head[t] = v;
+        st->header[(published + t) % kQueueSlots] = v;
+      }
+      const int64_t ids_end = workgroup_scan(n_blocks, s_scan);
+      s_first_id[t] = ids_end - n_blocks;
+      __syncthreads();
+      const int64_t total_ids = s_scan[kThreads - 1];
+      // Ids: word w of the new descriptors' ids, kLeaderBatch reads in flight per lane.
+      for (int64_t w0 = 0; w0 < total_ids; w0 += kThreads * kLeaderBatch) {
+        int32_t src_id[kLeaderBatch], dst_id[kLeaderBatch];
+#pragma unroll
+        for (int b = 0; b < kLeaderBatch; ++b) {
+          const int64_t w = w0 + b * kThreads + t;
+          if (w < total_ids) {
+            const int i = owner_of(s_first_id, fresh, w);
+            const int j = static_cast<int>(w - s_first_id[i]);
+            const int32_t* from = ring->ids[(published + i) % kQueueSlots];
+            src_id[b] = host_word(&from[j]);
+            dst_id[b] = host_word(&from[kQueueBlocks + j]);
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < kLeaderBatch; ++b) {
+          const int64_t w = w0 + b * kThreads + t;
+          if (w < total_ids) {
+            const int i = owner_of(s_first_id, fresh, w);
+            const int j = static_cast<int>(w - s_first_id[i]);
+            int32_t* to = st->ids[(published + i) % kQueueSlots];
+            to[j] = src_id[b];
+            to[kQueueBlocks + j] = dst_id[b];
+          }
+        }
+      }
+      // Claim map: the new descriptors' claims follow each other from the first's base.
+      const int64_t claims_end =
+          workgroup_scan(t < fresh ? s_head[t].n_claims : 0, s_scan);
+      s_first_id[t] = claims_end - (t < fresh ? s_head[t].n_claims : 0);
+      __syncthreads();
+      const int64_t total_claims = s_scan[kThreads - 1];
+      const uint64_t base = s_head[0].claim_base;
+      for (int64_t w = t; w < total_claims; w += kThreads) {
+        const int i = owner_of(s_first_id, fresh, w);
+        st->claim_desc[(base + w) % kQueueClaimRing] = static_cast<uint32_t>(published + i);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __syncthreads();
+      if (t == 0)
+        __hip_atomic_store(&st->published_claims, base + total_claims, __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      published += fresh;
+      last = wall_clock64();
+      nap = 1;
+      continue;
+    }
+    if (stop) {
+      if (t == 0) {
+        __hip_atomic_store(&st->stop_claims, host_word(&ring->stop_claims), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&st->stop, uint64_t{1}, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return;
+    }
+    if (queue_expired(q, start, last)) return;
+    queue_nap(nap);
+    nap = nap < 16 ? 2 * nap : 16;
+  }
+}
+
+// A store a mover makes to a destination tile: an agent-scope atomic store,
+// which the compiler issues with the device-coherence bit (sc1), so the data is
+// written through the XCD's L2 to where every XCD reads it. Completing such
+// stores (the vector-memory counter at zero) is then all a mover waits for
+// before it counts a claim done: an agent-scope release would instead write
+// back the whole L2 of the XCD, after every claim of every mover. 16-byte
+// vectors go as two 8-byte stores.
+template <typename V>
+__device__ __forceinline__ void queue_store(gptr<V> p, V v) {
+  if constexpr (sizeof(V) == 16) {
+    uint64_t w[2];
+    __builtin_memcpy(w, &v, 16);
+    gptr<uint64_t> d = (gptr<uint64_t>)p;
+    __hip_atomic_store(d, w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(d + 1, w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if constexpr (sizeof(V) == 8) {
+    uint64_t w;
+    __builtin_memcpy(&w, &v, 8);
+    __hip_atomic_store((gptr<uint64_t>)p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Every store this lane made is complete (and, being device-coherent, visible
+// to every XCD). The empty asm statements keep the compiler from moving memory
+// accesses across the wait.
+__device__ __forceinline__ void queue_stores_done() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  __asm__ __volatile__("" ::: "memory");
+}
+
+// Move unit a of a block (tile a, or tiles a * group .. of a group) from block
+// src_id of the source pool to block dst_id of the destination. Lane t moves
+// vectors t, t + kThreads, ..., U loads in flight before their stores; an id
+// outside its pool moves nothing.
+template <typename V, int U, bool NT>
+__device__ __forceinline__ void queue_move_unit(const QueueArgs& q, int32_t src_id,
+                                                int32_t dst_id, int a) {
+  if (src_id < 0 || src_id >= q.src.num_blocks || dst_id < 0 || dst_id >= q.dst.num_blocks)
+    return;
+  const int64_t tile_bytes = static_cast<int64_t>(q.tile_vecs) * sizeof(V);
+  const int t = threadIdx.x;
+  if (q.group == 1) {
+    const gptr<const V> s = as_global<V>(array_base(q.src, a) + src_id * tile_bytes);
+    const gptr<V> d = as_global<V>(array_base(q.dst, a) + dst_id * tile_bytes);
+    for (int v = t; v < q.tile_vecs; v += U * kThreads) {
+      V r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (v + u * kThreads < q.tile_vecs) r[u] = load_vec<V, NT>(s + v + u * kThreads);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (v + u * kThreads < q.tile_vecs) queue_store(d + v + u * kThreads, r[u]);
+    }
+    return;
+  }
+  // Small tiles: tile_vecs divides kThreads; lane t takes vector t % tile_vecs of
+  // tiles a0 + t / tile_vecs, a0 + t / tile_vecs + per_pass, ...
+  const int a0 = a * q.group;
+  const int tiles = min(q.group, q.n_arrays - a0);
+  const int per_pass = kThreads / q.tile_vecs;
+  const int64_t lane_offset = static_cast<int64_t>(t % q.tile_vecs) * sizeof(V);
+  for (int j = t / q.tile_vecs; j < tiles; j += U * per_pass) {
+    V r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (j + u * per_pass < tiles)
+        r[u] = load_vec<V, NT>(as_global<V>(array_base(q.src, a0 + j + u * per_pass) +
+                                            src_id * tile_bytes + lane_offset));
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (j + u * per_pass < tiles)
+        queue_store(as_global<V>(array_base(q.dst, a0 + j + u * per_pass) +
+                                 dst_id * tile_bytes + lane_offset), r[u]);
+  }
+}
+
+// The other workgroups: take a claim, wait for it to be published, move its
+// units, count it done. Thread 0 runs the claim protocol and hands each claim
+// to the workgroup through LDS.
+template <typename V, int U, bool NT>
+__device__ void queue_mover(const QueueArgs& q, uint64_t start) {
+  __shared__ int32_t s_go, s_slot, s_first, s_end;
+  __shared__ uint32_t s_desc;
+  __shared__ uint64_t s_target;
+  const int t = threadIdx.x;
+  QueueState* st = q.state;
+  uint64_t next = 0, known = 0, last = start;   // thread 0's
+  if (t == 0)
+    next = __hip_atomic_fetch_add(&st->next_claim, uint64_t{1}, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {
+    if (t == 0) {
+      const uint64_t claim = next;
+      int go = wall_clock64() - start <= q.life_ticks ? 1 : 0, nap = 1;
+      while (go && claim >= known) {
+        const uint64_t pc = agent_word(&st->published_claims);
+        if (pc > known) {
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          known = pc;
+          last = wall_clock64();
+          nap = 1;
+          continue;
+        }
+        if (agent_word(&st->stop)) {
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          const uint64_t final_claims = agent_word(&st->published_claims);
+          if (final_claims > known) {
+            known = final_claims;
+            continue;
+          }
+          if (claim >= agent_word(&st->stop_claims)) {
+            go = 0;
+            break;
+          }
+        }
+        if (queue_expired(q, start, last)) {
+          go = 0;
+          break;
+        }
+        queue_nap(nap);
+        nap = nap < 16 ? 2 * nap : 16;
+      }
+      if (go) {
+        const uint32_t r = ring_word(&st->claim_desc[claim % kQueueClaimRing]);
+        const int slot = static_cast<int>(r % kQueueSlots);
+        const QueueHeader* h = &st->header[slot];
+        const int64_t first =
+            static_cast<int64_t>(claim - ring_word(&h->claim_base)) * ring_word(&h->k);
+        s_first = static_cast<int32_t>(first);
+        s_end = static_cast<int32_t>(min<int64_t>(first + ring_word(&h->k), ring_word(&h->n_units)));
+        s_slot = slot;
+        s_desc = r;
+        s_target = ring_word(&h->done_target);
+        // The next claim, taken now so its atomic's latency hides behind this one's moves.
+        next = __hip_atomic_fetch_add(&st->next_claim, uint64_t{1}, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+      }
+      s_go = go;
+    }
+    __syncthreads();
+    if (!s_go) return;
+    const int slot = s_slot, end = s_end;
+    const int32_t* ids = st->ids[slot];
+    for (int u = s_first; u < end; ++u) {
+      const int i = u / q.units_per_block;
+      queue_move_unit<V, U, NT>(q, ring_word(&ids[i]), ring_word(&ids[kQueueBlocks + i]),
+                                u - i * q.units_per_block);
+    }
+    // Every lane's device-coherent stores are complete before the claim counts as
+    // done, and the descriptor's last claim before its completion reaches the host.
+    queue_stores_done();
+    __syncthreads();
+    if (t == 0) {
+      const uint64_t done = __hip_atomic_fetch_add(&st->done[slot], uint64_t{1},
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (done + 1 == s_target)
+        __hip_atomic_store(&q.ring->complete[slot], uint64_t{s_desc} + 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+}
+
+template <typename V, int U, bool NT>
+__global__ void __launch_bounds__(kThreads) kv_queue(QueueArgs q) {
+  const uint64_t start = wall_clock64();
+  if (blockIdx.x == 0) queue_leader(q, start);
+  else queue_mover<V, U, NT>(q, start);
+}
+
+using QueueKernel = void (*)(QueueArgs);
+
+template <typename V, bool NT>
+QueueKernel queue_kernel_of(int u) {
+  if (u >= 8) return kv_queue<V, 8, NT>;
+  if (u >= 4) return kv_queue<V, 4, NT>;
+  if (u >= 2) return kv_queue<V, 2, NT>;
+  return kv_queue<V, 1, NT>;
+}
+
+// The queue's kernel for vectors of `vec` bytes, up to lane_vecs of them in
+// flight per lane (capped by the unroll setting), as pick_kernel chooses.
+QueueKernel pick_queue_kernel(int vec, int lane_vecs, bool nt) {
+  const int u = std::min(g_unroll.load(), lane_vecs);
+  switch (vec) {
+    case 16: return nt ? queue_kernel_of<u32x4, true>(u) : queue_kernel_of<u32x4, false>(u);
+    case 8: return kv_queue<u32x2, 4, false>;
+    case 4: return kv_queue<uint32_t, 4, false>;
+    case 2: return kv_queue<uint16_t, 4, false>;
+    default: return kv_queue<uint8_t, 4, false>;
+  }
+}
+
+}  // namespace
+
+// A request queue: its rings, its stream, and the session the host keeps
+// with the kernel (see the protocol at queue_leader).
+struct iekv_queue {
+  const iekv_pool* src = nullptr;
+  const iekv_pool* dst = nullptr;
+  bool same_pool = false;
+  int32_t workers = 0;
+  int64_t max_k = 1;               // units per claim at most (claim_bytes)
+  int64_t idle_us = 0, life_us = 0;
+  QueueRing* ring = nullptr;       // host address of the pinned ring
+  QueueState* state = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t ended = nullptr;      // recorded after each launch of the kernel
+  QueueKernel kernel = nullptr;
+  QueueArgs args{};
+  bool running = false;
+  bool broken = false;             // a kernel ended with descriptors unfinished
+  uint64_t ticket_base = 0;        // ticket of the session's descriptor 0
+  uint64_t published = 0;          // descriptors of this session
+  uint64_t claims = 0;             // claims of this session
+  uint64_t retired = 0;            // descriptors [0, retired) of this session are done
+  uint64_t slot_claims[kQueueSlots] = {};
+  uint64_t launches = 0;
+  std::chrono::steady_clock::time_point started, last_publish;
+  std::mutex mu;
+};
+
+namespace {
+
+using QueueClock = std::chrono::steady_clock;
+constexpr int64_t kQueueWaitUs = 10'000'000;
+
+int64_t us_since(QueueClock::time_point t) {
+  return std::chrono::duration_cast<std::chrono::microseconds>(QueueClock::now() - t).count();
+}
+
+// Advance q->retired over the descriptors whose completion the kernel wrote.
+void queue_retire(iekv_queue* q) {
+  while (q->retired < q->published) {
+    const uint64_t seen =
+        __atomic_load_n(&q->ring->complete[q->retired % kQueueSlots], __ATOMIC_ACQUIRE);
+    if (seen < q->retired + 1) break;
+    ++q->retired;
+  }
+}
+
+// Whether the kernel of the current session has ended.
+bool queue_ended(iekv_queue* q) {
+  const hipError_t e = hipEventQuery(q->ended);
+  if (e == hipErrorNotReady) return false;
+  if (e != hipSuccess) (void)hipGetLastError();
+  return true;
+}
+
+int queue_broken() {
+  return set_error(IEKV_ERR_HIP, "the queue's kernel ended before finishing its requests; "
+                   "the queue cannot be used further");
+}
+
+// Start a session: clear both rings' counters and launch the kernel.
+int queue_launch(iekv_queue* q) {
+  std::memset(static_cast<void*>(q->ring), 0, offsetof(QueueRing, header));
+  IEKV_HIP(hipMemsetAsync(q->state, 0, offsetof(QueueState, header), q->stream));
+  q->published = q->claims = q->retired = 0;
+  std::fill(std::begin(q->slot_claims), std::end(q->slot_claims), uint64_t{0});
+  hipLaunchKernelGGL(q->kernel, dim3(static_cast<uint32_t>(q->workers) + 1), dim3(kThreads), 0,
+                     q->stream, q->args);
+  IEKV_HIP(hipGetLastError());
+  IEKV_HIP(hipEventRecord(q->ended, q->stream));
+  q->running = true;
+  q->started = q->last_publish = QueueClock::now();
+  ++q->launches;
+  return IEKV_OK;
+}
+
+// End the session: the kernel serves every published claim, then exits. The
+// wait is bounded by the kernel's own limits (it ends idle_us after its last
+// descriptor at the latest).
+int queue_end(iekv_queue* q) {
+  if (!q->running) return IEKV_OK;
+  __atomic_store_n(&q->ring->stop_claims, q->claims, __ATOMIC_RELAXED);
+  __atomic_store_n(&q->ring->stop, uint64_t{1}, __ATOMIC_RELEASE);
+  const int64_t limit = q->idle_us + kQueueWaitUs;
+  const auto t0 = QueueClock::now();
+  while (!queue_ended(q)) {
+    if (us_since(t0) > limit)
+      return set_error(IEKV_ERR_TIMEOUT, "the queue's kernel did not end within %lld us of "
+                       "its stop", static_cast<long long>(limit));
+    std::this_thread::yield();
+  }
+  q->running = false;
+  queue_retire(q);
+  const bool lost = q->retired < q->published;
+  q->ticket_base += q->published;
+  q->published = q->retired = q->claims = 0;
+  if (lost) {
+    q->broken = true;
+    return queue_broken();
+  }
+  return IEKV_OK;
+}
+
+// Wait (bounded) until the session's descriptors [0, upto] are done.
+int queue_wait_local(iekv_queue* q, uint64_t upto, int64_t timeout_us) {
+  const auto t0 = QueueClock::now();
+  for (uint32_t spin = 0;; ++spin) {
+    queue_retire(q);
+    if (q->retired > upto) return IEKV_OK;
+    if (queue_ended(q)) {
+      queue_retire(q);
+      if (q->retired > upto) return IEKV_OK;
+      q->broken = true;
+      return queue_broken();
+    }
+    if (us_since(t0) > timeout_us)
+      return set_error(IEKV_ERR_TIMEOUT, "request %llu not done after %lld us",
+                       static_cast<unsigned long long>(q->ticket_base + upto),
+                       static_cast<long long>(timeout_us));
+    if (spin % 64 == 63) std::this_thread::yield();
+    else __builtin_ia32_pause();
+  }
+}
+
+// Publish one descriptor of n <= kQueueBlocks checked (src, dst) pairs.
+int queue_publish(iekv_queue* q, const int32_t* s, const int32_t* d, int32_t n,
+                  uint64_t* ticket) {
+  int rc;
+  if (q->running && q->published >= kQueueSlots &&
+      (rc = queue_wait_local(q, q->published - kQueueSlots, kQueueWaitUs)))
+    return rc;
+  // A kernel that may end (its idle or lifetime limit) before it sees this
+  // descriptor is ended first, and a new one started.
+  if (q->running && (us_since(q->last_publish) > q->idle_us / 2 ||
+                     us_since(q->started) > q->life_us / 2 || q->published >= (1u << 31)) &&
+      (rc = queue_end(q)))
+    return rc;
+  if (!q->running && (rc = queue_launch(q))) return rc;
+  const uint64_t r = q->published;
+  const int slot = static_cast<int>(r % kQueueSlots);
+  const int64_t n_units = static_cast<int64_t>(n) * q->args.units_per_block;
+  const iekv_plan::QueueClaims c = iekv_plan::queue_claims(n_units, q->workers, q->max_k);
+  q->slot_claims[slot] += c.n_claims;
+  QueueHeader& h = q->ring->header[slot];
+  h.claim_base = q->claims;
+  h.done_target = q->slot_claims[slot];
+  h.n_blocks = n;
+  h.n_units = static_cast<int32_t>(n_units);
+  h.k = static_cast<int32_t>(c.k);
+  h.n_claims = static_cast<int32_t>(c.n_claims);
+  std::memcpy(q->ring->ids[slot], s, sizeof(int32_t) * n);
+  std::memcpy(q->ring->ids[slot] + kQueueBlocks, d, sizeof(int32_t) * n);
+  __atomic_store_n(&q->ring->tail, r + 1, __ATOMIC_RELEASE);
+  q->published = r + 1;
+  q->claims += c.n_claims;
+  q->last_publish = QueueClock::now();
+  *ticket = q->ticket_base + r;
+  return IEKV_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -2376,6 +2973,222 @@ int iekv_get_launch(int32_t* run_blocks, int32_t* unroll, int32_t* nontemporal,
   if (order) *order = g_order.load();
   if (pack_order) *pack_order = g_pack_order.load();
   if (chunk_bytes) *chunk_bytes = g_chunk.load();
+  return IEKV_OK;
+}
+
+int iekv_queue_create(const iekv_pool* src, const iekv_pool* dst, int32_t workers,
+                      int64_t claim_bytes, int64_t idle_us, int64_t life_us, iekv_queue** out) {
+  if (!out) return set_error(IEKV_ERR_INVALID, "out is null");
+  *out = nullptr;
+  int rc;
+  if ((rc = check_pool(src, "source")) || (rc = check_pool(dst, "destination"))) return rc;
+  if (src->n_arrays != dst->n_arrays || src->tile_bytes != dst->tile_bytes)
+    return set_error(IEKV_ERR_INVALID, "pools differ in shape");
+  if (src->device != dst->device)
+    return set_error(IEKV_ERR_INVALID, "pools live on devices %d and %d", src->device,
+                     dst->device);
+  bool same_pool = false;
+  if ((rc = check_aliasing(src, dst, &same_pool))) return rc;
+  if (workers < 0 || claim_bytes < 0 || idle_us < 0 || life_us < 0)
+    return set_error(IEKV_ERR_INVALID, "negative queue setting");
+  if (idle_us == 0) idle_us = 200'000;
+  if (life_us == 0) life_us = 60'000'000;
+  if (idle_us < 1000 || idle_us > 60'000'000 || life_us < 2 * idle_us || life_us > 3'600'000'000LL)
+    return set_error(IEKV_ERR_INVALID, "idle_us %lld / life_us %lld out of range (idle 1 ms to "
+                     "60 s, life at least twice idle and at most 1 h)",
+                     static_cast<long long>(idle_us), static_cast<long long>(life_us));
+  if (claim_bytes == 0) claim_bytes = 128 << 10;
+  DeviceGuard guard(src->device);
+  if (!guard.ok()) return guard.fail();
+  int cus = 0, clock_khz = 0;
+  IEKV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, src->device));
+  IEKV_HIP(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, src->device));
+  if (clock_khz <= 0) return set_error(IEKV_ERR_HIP, "the device reports no wall clock");
+  if (workers == 0) workers = 4 * std::max(cus, 1);
+  if (workers > 65535) return set_error(IEKV_ERR_INVALID, "workers %d out of range", workers);
+
+  // The unit of work: one tile, or a group of small tiles of one block, as the
+  // pool-to-pool launches move them (plan_move with the pool-writing chunk).
+  MovePlan pl;
+  const int align = std::min(src->align, dst->align);
+  if ((rc = plan_move(1, src->tile_bytes, src->n_arrays, align, true, true, true, &pl,
+                      g_direct_chunk.load())))
+    return rc;
+  // Whole tiles per unit: the plan's chunks only split a launch's work.
+  const int group = iekv_plan::tile_group(pl.tile_vecs, pl.vec, g_direct_chunk.load(),
+                                          src->n_arrays);
+  const int64_t lane_vecs = (static_cast<int64_t>(pl.tile_vecs) * group + kThreads - 1) / kThreads;
+  const int64_t unit_bytes = src->tile_bytes * group;
+
+  iekv_queue* q = new (std::nothrow) iekv_queue{};
+  if (!q) return set_error(IEKV_ERR_INVALID, "out of host memory");
+  auto fail = [&](int code) {
+    if (q->ended) (void)hipEventDestroy(q->ended);
+    if (q->stream) (void)hipStreamDestroy(q->stream);
+    if (q->state) (void)hipFree(q->state);
+    if (q->ring) (void)hipHostFree(q->ring);
+    delete q;
+    return code;
+  };
+#define IEKV_QUEUE_HIP(expr)                                                                  \
+  do {                                                                                        \
+    const hipError_t e_ = (expr);                                                             \
+    if (e_ != hipSuccess) {                                                                   \
+      (void)hipGetLastError();                                                                \
+      return fail(set_error(IEKV_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)));           \
+    }                                                                                         \
+  } while (0)
+  IEKV_QUEUE_HIP(hipHostMalloc(reinterpret_cast<void**>(&q->ring), sizeof(QueueRing),
+                               hipHostMallocCoherent | hipHostMallocMapped));
+  std::memset(static_cast<void*>(q->ring), 0, sizeof(QueueRing));
+  void* ring_dev = nullptr;
+  IEKV_QUEUE_HIP(hipHostGetDevicePointer(&ring_dev, q->ring, 0));
+  IEKV_QUEUE_HIP(hipMalloc(reinterpret_cast<void**>(&q->state), sizeof(QueueState)));
+  IEKV_QUEUE_HIP(hipMemset(q->state, 0, sizeof(QueueState)));
+  // Non-blocking: work on the legacy default stream must not wait for the
+  // resident kernel.
+  IEKV_QUEUE_HIP(hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking));
+  IEKV_QUEUE_HIP(hipEventCreateWithFlags(&q->ended, hipEventDisableTiming));
+  IEKV_QUEUE_HIP(hipEventRecord(q->ended, q->stream));
+#undef IEKV_QUEUE_HIP
+  q->src = src;
+  q->dst = dst;
+  q->same_pool = same_pool;
+  q->workers = workers;
+  q->max_k = std::max<int64_t>(1, claim_bytes / unit_bytes);
+  q->idle_us = idle_us;
+  q->life_us = life_us;
+  q->kernel = pick_queue_kernel(pl.vec, static_cast<int>(std::min<int64_t>(lane_vecs, 16)),
+                                nontemporal(-1));
+  const uint64_t ticks_per_us = static_cast<uint64_t>(clock_khz) / 1000;
+  q->args = QueueArgs{view_of(src), view_of(dst), q->state, static_cast<QueueRing*>(ring_dev),
+                      pl.tile_vecs, src->n_arrays, group,
+                      (src->n_arrays + group - 1) / group,
+                      static_cast<uint64_t>(idle_us) * std::max<uint64_t>(ticks_per_us, 1),
+                      static_cast<uint64_t>(life_us) * std::max<uint64_t>(ticks_per_us, 1)};
+  *out = q;
+  return IEKV_OK;
+}
+
+int iekv_queue_submit(iekv_queue* q, const int32_t* src_ids, const int32_t* dst_ids,
+                      int32_t n_blocks, uint64_t* ticket) {
+  if (!ticket) return set_error(IEKV_ERR_INVALID, "ticket is null");
+  return iekv_queue_submit_requests(q, 1, &n_blocks, src_ids, dst_ids, ticket);
+}
+
+int iekv_queue_submit_requests(iekv_queue* q, int32_t n_requests, const int32_t* counts,
+                               const int32_t* src_ids, const int32_t* dst_ids,
+                               uint64_t* tickets) {
+  if (!q) return set_error(IEKV_ERR_INVALID, "queue is null");
+  if (n_requests < 0)
+    return set_error(IEKV_ERR_INVALID, "n_requests is negative (%d)", n_requests);
+  if (n_requests == 0) return IEKV_OK;
+  if (!counts || !tickets) return set_error(IEKV_ERR_INVALID, "counts or tickets is null");
+  int64_t total = 0;
+  for (int32_t k = 0; k < n_requests; ++k) {
+    if (counts[k] < 0)
+      return set_error(IEKV_ERR_INVALID, "request %d has a negative count (%d)", k, counts[k]);
+    total += counts[k];
+  }
+  if (total > INT32_MAX)
+    return set_error(IEKV_ERR_INVALID, "%lld blocks exceed one call",
+                     static_cast<long long>(total));
+  int rc;
+  if ((rc = check_host_count(static_cast<int32_t>(total), src_ids, dst_ids))) return rc;
+  // Every request is checked before any is published.
+  std::vector<int32_t> s(static_cast<size_t>(total)), d(static_cast<size_t>(total));
+  std::vector<int32_t> rs, rd;
+  for (int64_t k = 0, at = 0; k < n_requests; at += counts[k], ++k) {
+    const int32_t n = counts[k];
+    if ((rc = check_host_range(src_ids + at, n, q->src->num_blocks, "source")) ||
+        (rc = check_host_range(dst_ids + at, n, q->dst->num_blocks, "destination")) ||
+        (rc = order_pairs(src_ids + at, dst_ids + at, n, q->same_pool, &rs, &rd)))
+      return rc;
+    std::copy(rs.begin(), rs.end(), s.begin() + at);
+    std::copy(rd.begin(), rd.end(), d.begin() + at);
+  }
+  std::lock_guard<std::mutex> lock(q->mu);
+  if (q->broken) return queue_broken();
+  DeviceGuard guard(q->src->device);
+  if (!guard.ok()) return guard.fail();
+  for (int64_t k = 0, at = 0; k < n_requests; at += counts[k], ++k) {
+    tickets[k] = IEKV_QUEUE_DONE;
+    for (int32_t first = 0; first < counts[k]; first += kQueueBlocks) {
+      const int32_t m = std::min<int32_t>(kQueueBlocks, counts[k] - first);
+      if ((rc = queue_publish(q, s.data() + at + first, d.data() + at + first, m, &tickets[k])))
+        return rc;
+    }
+  }
+  return IEKV_OK;
+}
+
+int iekv_queue_wait(iekv_queue* q, uint64_t ticket, int64_t timeout_us) {
+  if (!q) return set_error(IEKV_ERR_INVALID, "queue is null");
+  if (ticket == IEKV_QUEUE_DONE) return IEKV_OK;
+  std::lock_guard<std::mutex> lock(q->mu);
+  if (q->broken) return queue_broken();
+  if (ticket >= q->ticket_base + q->published)
+    return set_error(IEKV_ERR_INVALID, "ticket %llu was not issued",
+                     static_cast<unsigned long long>(ticket));
+  if (ticket < q->ticket_base) return IEKV_OK;   // an ended session served all of its own
+  return queue_wait_local(q, ticket - q->ticket_base, timeout_us < 0 ? kQueueWaitUs : timeout_us);
+}
+
+int iekv_queue_poll(iekv_queue* q, uint64_t ticket, int32_t* done) {
+  if (!q || !done) return set_error(IEKV_ERR_INVALID, "queue or done is null");
+  *done = 0;
+  if (ticket == IEKV_QUEUE_DONE) {
+    *done = 1;
+    return IEKV_OK;
+  }
+  std::lock_guard<std::mutex> lock(q->mu);
+  if (q->broken) return queue_broken();
+  if (ticket >= q->ticket_base + q->published)
+    return set_error(IEKV_ERR_INVALID, "ticket %llu was not issued",
+                     static_cast<unsigned long long>(ticket));
+  if (ticket >= q->ticket_base) queue_retire(q);
+  *done = ticket < q->ticket_base + q->retired ? 1 : 0;
+  return IEKV_OK;
+}
+
+int iekv_queue_stop(iekv_queue* q) {
+  if (!q) return set_error(IEKV_ERR_INVALID, "queue is null");
+  std::lock_guard<std::mutex> lock(q->mu);
+  DeviceGuard guard(q->src->device);
+  if (!guard.ok()) return guard.fail();
+  return queue_end(q);
+}
+
+int iekv_queue_destroy(iekv_queue* q) {
+  if (!q) return IEKV_OK;
+  int rc;
+  {
+    std::lock_guard<std::mutex> lock(q->mu);
+    DeviceGuard guard(q->src->device);
+    if (!guard.ok()) return guard.fail();
+    rc = queue_end(q);
+    // The kernel ends by its own limits even if the stop above timed out:
+    // nothing it reads is freed before that.
+    const hipError_t e = hipStreamSynchronize(q->stream);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      if (!rc) rc = set_error(IEKV_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    }
+    (void)hipEventDestroy(q->ended);
+    (void)hipStreamDestroy(q->stream);
+    (void)hipFree(q->state);
+    (void)hipHostFree(q->ring);
+    (void)hipGetLastError();
+  }
+  delete q;
+  return rc;
+}
+
+int iekv_queue_stats(const iekv_queue* q, uint64_t* descriptors, uint64_t* launches) {
+  if (!q) return set_error(IEKV_ERR_INVALID, "queue is null");
+  std::lock_guard<std::mutex> lock(const_cast<iekv_queue*>(q)->mu);
+  if (descriptors) *descriptors = q->ticket_base + q->published;
+  if (launches) *launches = q->launches;
   return IEKV_OK;
 }
 

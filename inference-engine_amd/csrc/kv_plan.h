@@ -310,6 +310,38 @@ inline bool spans_cross(std::vector<Span> spans) {
   return false;
 }
 
+// Request queue (iekv_queue_*). A descriptor of n_units units (a unit is one
+// tile, or one group of small tiles, of one block) is served in claims of k
+// consecutive units; movers take claims from one cursor that runs over every
+// descriptor of a session, and a ring of kQueueClaimRing entries maps a claim to
+// its descriptor. A descriptor has at most kQueueMaxClaims claims, so the claims
+// of `slots` descriptors in flight fill at most half the ring: an entry is
+// rewritten only after the descriptor of the claim it held has finished.
+constexpr int64_t kQueueMaxClaims = 4096;
+
+constexpr int64_t queue_claim_ring(int64_t slots) { return 2 * slots * kQueueMaxClaims; }
+
+struct QueueClaims {
+  int64_t k = 1;         // units per claim
+  int64_t n_claims = 0;  // ceil(n_units / k)
+};
+
+// Claims of a descriptor: spread over all `workers` (one unit per claim for a
+// request smaller than the mover count), at most max_k units per claim, and
+// never more than kQueueMaxClaims claims.
+inline QueueClaims queue_claims(int64_t n_units, int64_t workers, int64_t max_k) {
+  QueueClaims c;
+  if (n_units <= 0) return c;
+  int64_t k = workers > 0 ? n_units / workers : n_units;
+  if (k > max_k) k = max_k;
+  if (k < 1) k = 1;
+  const int64_t least = (n_units + kQueueMaxClaims - 1) / kQueueMaxClaims;
+  if (k < least) k = least;
+  c.k = k;
+  c.n_claims = (n_units + k - 1) / k;
+  return c;
+}
+
 }  // namespace iekv_plan
 
 #endif  // IEKV_KV_PLAN_H_

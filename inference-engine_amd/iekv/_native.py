@@ -12,12 +12,15 @@ from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libiekv.so"
-ABI_VERSION = 20
+ABI_VERSION = 21
 
 INLINE_IDS = 256   # IEKV_INLINE_IDS: most host ids one launch carries in its arguments
 HOST_DIRECT_MAX = 64 << 20   # IEKV_HOST_DIRECT_MAX_BYTES: largest direct offload; restore launch size
 INLINE_IMAGES = 128          # IEKV_INLINE_IMAGES: scattered host images restored in one launch
 STATIC_STAGING = 32 << 20    # IEKV_STATIC_STAGING_BYTES: staging of iekv_offload_static
+QUEUE_SLOTS = 256            # IEKV_QUEUE_SLOTS: queue descriptors in flight at once
+QUEUE_MAX_BLOCKS = 1024      # IEKV_QUEUE_MAX_BLOCKS: blocks per queue descriptor
+QUEUE_DONE = (1 << 64) - 1   # IEKV_QUEUE_DONE: ticket of an empty request
 
 IEKV_OK = 0
 IEKV_ERR_INVALID = -1
@@ -25,6 +28,7 @@ IEKV_ERR_HIP = -2
 IEKV_ERR_CAPACITY = -3
 IEKV_ERR_RANGE = -4      # a host block id outside its pool
 IEKV_ERR_IDS = -5        # host ids that conflict (a destination twice; overlap within a pool)
+IEKV_ERR_TIMEOUT = -6    # iekv_queue_wait: the requests did not finish in time
 # Bits iekv_check_ids writes to its status word.
 IEKV_IDS_SRC_RANGE = 1
 IEKV_IDS_DST_RANGE = 2
@@ -89,6 +93,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "iekv_noop": (c_int, [c_int32, c_int32, c_void_p]),
     "iekv_profile_start": (c_int, [c_int32]),
     "iekv_profile_stop": (c_int, [POINTER(ctypes.c_float), c_int32, POINTER(c_int32)]),
+    "iekv_queue_create": (c_int, [c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64,
+                                  POINTER(c_void_p)]),
+    "iekv_queue_submit": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_uint64)]),
+    "iekv_queue_submit_requests": (c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
+                                           c_void_p]),
+    "iekv_queue_wait": (c_int, [c_void_p, c_uint64, c_int64]),
+    "iekv_queue_poll": (c_int, [c_void_p, c_uint64, POINTER(c_int32)]),
+    "iekv_queue_stop": (c_int, [c_void_p]),
+    "iekv_queue_destroy": (c_int, [c_void_p]),
+    "iekv_queue_stats": (c_int, [c_void_p, POINTER(c_uint64), POINTER(c_uint64)]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -111,7 +125,12 @@ class NativeValueError(NativeError, ValueError):
     """IEKV_ERR_IDS: ids that conflict (a destination twice; overlap within a pool)."""
 
 
-_ERRORS = {IEKV_ERR_RANGE: NativeIndexError, IEKV_ERR_IDS: NativeValueError}
+class NativeTimeoutError(NativeError, TimeoutError):
+    """IEKV_ERR_TIMEOUT: queued requests that did not finish in time."""
+
+
+_ERRORS = {IEKV_ERR_RANGE: NativeIndexError, IEKV_ERR_IDS: NativeValueError,
+           IEKV_ERR_TIMEOUT: NativeTimeoutError}
 
 
 def library_path() -> Path:

@@ -503,7 +503,53 @@ static void check_launch_chunk() {
   EXPECT(launch_chunk(false, true, 2048, 4096, 8192) == 4096, "cfg5 tp8 unpack");
 }
 
+// The request queue's claims (queue_claims): the claims of a descriptor cover each
+// of its units exactly once, none is empty, there are at most kQueueMaxClaims of
+// them, a request no larger than the mover count is spread one unit per claim, and
+// k stays within max_k unless the claim cap needs more. The claim ring then holds
+// the claims of twice the descriptors that can be in flight, so the entry of a claim
+// still waiting is never rewritten: the claims between an entry's two uses span at
+// least 2 * slots descriptors, and a descriptor is published only after the one
+// `slots` before it has finished.
+static void check_queue_claims() {
+  for (int64_t workers : {1, 7, 1024})
+    for (int64_t max_k : {1, 4, 64})
+      for (int64_t n : {1, 2, 3, 7, 63, 64, 65, 1000, 1024, 1025, 4095, 4096, 4097, 8192,
+                        25920, 65536, 163840, 1 << 26}) {
+        const QueueClaims c = queue_claims(n, workers, max_k);
+        EXPECT(c.k >= 1 && c.n_claims >= 1, "n %lld: k %lld claims %lld", (long long)n,
+               (long long)c.k, (long long)c.n_claims);
+        EXPECT(c.n_claims <= kQueueMaxClaims, "n %lld: %lld claims", (long long)n,
+               (long long)c.n_claims);
+        EXPECT(c.n_claims * c.k >= n && (c.n_claims - 1) * c.k < n,
+               "n %lld: claims of %lld do not cover the units exactly", (long long)n,
+               (long long)c.k);
+        const int64_t least = (n + kQueueMaxClaims - 1) / kQueueMaxClaims;
+        EXPECT(c.k <= (max_k > least ? max_k : least), "n %lld: k %lld above max_k %lld",
+               (long long)n, (long long)c.k, (long long)max_k);
+        if (n <= workers) EXPECT(c.k == 1, "n %lld <= workers %lld: k %lld", (long long)n,
+                                 (long long)workers, (long long)c.k);
+        if (n / workers >= max_k)   // a request of max_k units per mover or more: full claims
+          EXPECT(c.k == (max_k > least ? max_k : least), "n %lld: k %lld, not max_k %lld",
+                 (long long)n, (long long)c.k, (long long)max_k);
+        if (n <= 70000) {   // brute force: every unit in exactly one claim
+          std::vector<int> hit(static_cast<size_t>(n), 0);
+          for (int64_t claim = 0; claim < c.n_claims; ++claim)
+            for (int64_t u = claim * c.k; u < claim * c.k + c.k && u < n; ++u) ++hit[u];
+          for (int64_t u = 0; u < n; ++u)
+            if (hit[u] != 1) {
+              EXPECT(false, "n %lld: unit %lld in %d claims", (long long)n, (long long)u, hit[u]);
+              break;
+            }
+        }
+      }
+  EXPECT(queue_claims(0, 1024, 4).n_claims == 0, "an empty descriptor has no claims");
+  for (int64_t slots : {1, 16, 256})
+    EXPECT(queue_claim_ring(slots) >= 2 * slots * kQueueMaxClaims, "claim ring too small");
+}
+
 int main() {
+  check_queue_claims();
   for (int grid = 1; grid <= 4096; ++grid) check_xcd_grouped(grid);
   for (int grid : {98816, 1048575, 4194304, 16777215}) check_xcd_grouped(grid);
 

@@ -40,7 +40,7 @@ def test_every_declared_function_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iekv_abi_version() == 20
+    assert lib.iekv_abi_version() == 21
 
 
 def test_pool_create_rejects_bad_arguments_before_touching_the_gpu(lib):
@@ -574,7 +574,7 @@ def test_the_integration_guides_ctypes_stub_matches_the_abi():
 
     text = (ROOT / "INTEGRATION.md").read_text()
     aliases = {"u64p": POINTER(c_uint64), "vp": c_void_p, "i32": c_int32, "i64": c_int64,
-               "ctypes.POINTER(vp)": POINTER(c_void_p)}
+               "ctypes.POINTER(vp)": POINTER(c_void_p), "ctypes.c_uint64": c_uint64}
     declared = re.findall(r"^lib\.(iekv_\w+)\.argtypes = \[([^\]]*)\]", text, re.M)
     assert len(declared) >= 5
     for name, args in declared:

@@ -89,6 +89,16 @@ MISTAKES = [
     ("more images per launch than the argument block holds",
      "  if (per > max_images) per = max_images;\n",
      ""),
+    # The request queue's claims.
+    ("a descriptor's claims not capped",
+     "  if (k < least) k = least;\n",
+     ""),
+    ("the last claim of a descriptor dropped",
+     "c.n_claims = (n_units + k - 1) / k;",
+     "c.n_claims = n_units / k;"),
+    ("claims never larger than one unit for a big request",
+     "if (k > max_k) k = max_k;",
+     "if (k > 1) k = 1;"),
     ("touching pools counted as overlapping",
      "if (reach[1 - s.owner] > s.lo) return true;",
      "if (reach[1 - s.owner] >= s.lo) return true;"),
