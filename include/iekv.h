@@ -492,8 +492,9 @@ int iekv_get_direct_chunk(int32_t* chunk_bytes);
  * nor write blocks another one reads. Each request's ids are checked as
  * iekv_copy_direct_ids checks them. Calls on one queue are serialized by a
  * lock; the pools must outlive the queue. While it runs, the kernel holds
- * workers + 1 workgroups resident (by default 4 per compute unit, a quarter of
- * the wave slots), so other kernels share the GPU with it.
+ * workers + 1 workgroups resident (by default as many as fit, at most 4 per
+ * compute unit), so other kernels share the GPU with it; hipDeviceSynchronize
+ * and hipFree wait for it to end (iekv_queue_stop ends it at once).
  *
  * No reference counterpart: the reference hands off one request at a time
  * (DisaggregatedEngine.generate, ie/serve/disaggregated.py:106-116, each a
@@ -510,7 +511,8 @@ typedef struct iekv_queue iekv_queue;
 #define IEKV_QUEUE_DONE UINT64_MAX
 
 /* Make a queue for direct handoffs from `src` to `dst` (same n_arrays and
- * tile_bytes, one device). workers: mover workgroups (0: 4 per compute unit);
+ * tile_bytes, one device). workers: mover workgroups, each wave of which is a
+ * mover (0: as many as the device holds at once, at most 4 per compute unit);
  * claim_bytes: most bytes one mover claims at once (0: 128 KiB); idle_us /
  * life_us: the kernel's idle and lifetime limits (0: 200 ms / 60 s). Allocates
  * the rings (about 2 MiB of pinned host memory, 11 MiB of device memory) and a

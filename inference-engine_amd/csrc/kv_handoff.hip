@@ -1721,9 +1721,9 @@ int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
 // raising `tail` to r + 1. Workgroup 0 of the kernel (the leader) polls `tail`,
 // copies each new descriptor to the device's ring, maps the descriptor's claims
 // in the claim ring (iekv_plan::queue_claims) and raises `published_claims`.
-// The other workgroups (movers) take claims from one cursor, `next_claim`, wait
-// until their claim is published, move its units, and count it in the slot's
-// `done` word; the mover that finishes a descriptor's last claim writes r + 1
+// The waves of the other workgroups (movers) take claims from a set of cursors,
+// wait until their claim is published, move its units, and count it down in the slot's
+// `remaining` word; the mover that finishes a descriptor's last claim writes r + 1
 // into the slot's `complete` word in host memory. The host reuses a slot only
 // after its descriptor is complete, so no mover reads a slot that is being
 // rewritten, and the claim ring holds twice the claims of every descriptor in
@@ -1737,14 +1737,25 @@ constexpr int kQueueSlots = IEKV_QUEUE_SLOTS;
 constexpr int kQueueBlocks = IEKV_QUEUE_MAX_BLOCKS;
 constexpr int64_t kQueueClaimRing = iekv_plan::queue_claim_ring(kQueueSlots);
 
+// One descriptor as the host writes it (k, per_block and n_claims from
+// iekv_plan::queue_claims).
 struct QueueHeader {
   uint64_t claim_base;   // the descriptor's first claim in its session
-  uint64_t done_target;  // the slot's `done` count once the descriptor is finished
   int32_t n_blocks;
-  int32_t n_units;       // n_blocks * units per block
-  int32_t k;             // units per claim
   int32_t n_claims;
+  int32_t k;             // units per claim
+  int32_t per_block;     // claims per block
+  int64_t reserved;
 };
+
+// A claim as the leader publishes it: the block's id pair, its units, and the
+// descriptor it belongs to (its number in the session).
+struct QueueClaim {
+  int32_t src_id, dst_id;
+  uint32_t units;        // first unit | unit count << 16
+  uint32_t desc;
+};
+constexpr int32_t kQueueMaxUnits = 32768;   // units per block, so both fit 16 bits
 
 // Pinned host memory, mapped for the device. The host writes tail, stop,
 // stop_claims, the headers and the ids; the device writes `complete`.
@@ -1757,16 +1768,25 @@ struct QueueRing {
   alignas(64) int32_t ids[kQueueSlots][2 * kQueueBlocks];  // sources, destinations at +kQueueBlocks
 };
 
-// Device memory. Everything before `header` is cleared when a session starts.
+// Claims of a slot's descriptor not yet finished, one cache line per slot: the
+// movers of neighbouring descriptors count down concurrently.
+struct alignas(128) QueueCount {
+  uint64_t left;
+};
+
+// Movers take claims from kQueueCursors cursors, cursor p handing out claims p,
+// p + kQueueCursors, ...: each cursor is updated by a 1/kQueueCursors share of
+// the movers, and any running mover keeps its cursor's claims moving.
+constexpr int kQueueCursors = 32;
+
+// Device memory. Everything before `claims` is cleared when a session starts.
 struct QueueState {
-  alignas(64) uint64_t next_claim;
-  alignas(64) uint64_t published_claims;
+  alignas(128) uint64_t published_claims;
   uint64_t stop;
   uint64_t stop_claims;
-  alignas(64) uint64_t done[kQueueSlots];
-  alignas(64) QueueHeader header[kQueueSlots];
-  alignas(64) int32_t ids[kQueueSlots][2 * kQueueBlocks];
-  alignas(64) uint32_t claim_desc[kQueueClaimRing];
+  QueueCount cursor[kQueueCursors];
+  QueueCount remaining[kQueueSlots];
+  alignas(128) QueueClaim claims[kQueueClaimRing];
 };
 
 struct QueueArgs {
@@ -1812,6 +1832,25 @@ __device__ __forceinline__ bool queue_expired(const QueueArgs& q, uint64_t start
   return now - last > q.idle_ticks || now - start > q.life_ticks;
 }
 
+// Device-coherent stores: agent-scope atomic stores, which the compiler issues
+// with the device-coherence bit (sc1), so the data is written through the XCD's
+// L2 to where every XCD reads it. Once such stores are complete (the
+// vector-memory counter at zero, queue_stores_done) other workgroups may rely on
+// them, without the agent-scope release fence that would write back the whole L2
+// of the XCD.
+template <typename T>
+__device__ __forceinline__ void coherent_store(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every store this lane made is complete. The empty asm statements keep the
+// compiler from moving memory accesses across the wait.
+__device__ __forceinline__ void queue_stores_done() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  __asm__ __volatile__("" ::: "memory");
+}
+
 // Inclusive sum of v over the workgroup's threads (`scratch`: kThreads words of LDS).
 __device__ int64_t workgroup_scan(int64_t v, int64_t* scratch) {
   const int t = threadIdx.x;
@@ -1842,13 +1881,16 @@ constexpr int kLeaderBatch = 8;   // host-ring words in flight per lane
 
 // Workgroup 0: publish the host's descriptors to the movers. Every descriptor
 // published since the last round is fetched at once: one header per thread, then
-// the ids and the claim map over one index space spanning them all, so a round
-// costs a few trips over the host link however many descriptors it brings.
+// the ids over one index space spanning them all, so a round costs two trips over
+// the host link however many descriptors it brings. Each block's id pair goes
+// straight into the records of its claims, written with device-coherent stores;
+// published_claims is raised once they are complete.
 __device__ void queue_leader(const QueueArgs& q, uint64_t start) {
   __shared__ uint64_t s_word[2];
   __shared__ QueueHeader s_head[kQueueSlots];
   __shared__ int64_t s_scan[kThreads];
-  __shared__ int64_t s_first_id[kThreads];   // first id word of each new descriptor
+  __shared__ int64_t s_first[kThreads];   // first block of each new descriptor
+  __shared__ int64_t s_claim[kThreads];   // first claim of each new descriptor
   const int t = threadIdx.x;
   QueueState* st = q.state;
   const QueueRing* ring = q.ring;
@@ -1868,36 +1910,47 @@ __device__ void queue_leader(const QueueArgs& q, uint64_t start) {
       // The host has at most kQueueSlots descriptors unfinished, so at most that
       // many are new.
       const int fresh = static_cast<int>(min<uint64_t>(tail - published, kQueueSlots));
-      int32_t n_blocks = 0;
+      int32_t n_blocks = 0, n_claims = 0;
       if (t < fresh) {
-        // Clamped to what the rings hold, so no index a mover derives from a
-        // header can leave them.
-        const QueueHeader* h = &ring->header[(published + t) % kQueueSlots];
-        QueueHeader v;
+        // Clamped to what the rings hold, so no index derived from a header can
+        // leave them.
+        const int slot = static_cast<int>((published + t) % kQueueSlots);
+        const QueueHeader* h = &ring->header[slot];
+        QueueHeader v{};
         v.claim_base = host_word(&h->claim_base);
-        v.done_target = host_word(&h->done_target);
         n_blocks = min(max(host_word(&h->n_blocks), 0), kQueueBlocks);
+        v.per_block = min(max(host_word(&h->per_block), 1), q.units_per_block);
+        v.k = min(max(host_word(&h->k), 1), q.units_per_block);
+        n_claims = min(max(host_word(&h->n_claims), 0),
+                       min(n_blocks * v.per_block, static_cast<int32_t>(iekv_plan::kQueueMaxClaims)));
         v.n_blocks = n_blocks;
-        v.n_units = min(max(host_word(&h->n_units), 0), n_blocks * q.units_per_block);
-        v.k = max(host_word(&h->k), 1);
-        v.n_claims = min(max(host_word(&h->n_claims), 0),
-                         static_cast<int32_t>(iekv_plan::kQueueMaxClaims));
+        v.n_claims = n_claims;
         s_head[t] = v;
-        st->header[(published + t) % kQueueSlots] = v;
+        coherent_store(&st->remaining[slot].left, static_cast<uint64_t>(n_claims));
       }
-      const int64_t ids_end = workgroup_scan(n_blocks, s_scan);
-      s_first_id[t] = ids_end - n_blocks;
+      // The new descriptors' blocks over one index space (s_first: each one's first
+      // block), and their claims, which follow each other from the first one's base
+      // (s_claim: each one's first claim).
+      const int64_t blocks_end = workgroup_scan(n_blocks, s_scan);
+      s_first[t] = blocks_end - n_blocks;
       __syncthreads();
-      const int64_t total_ids = s_scan[kThreads - 1];
-      // Ids: word w of the new descriptors' ids, kLeaderBatch reads in flight per lane.
-      for (int64_t w0 = 0; w0 < total_ids; w0 += kThreads * kLeaderBatch) {
+      const int64_t total_blocks = s_scan[kThreads - 1];
+      const int64_t claims_end = workgroup_scan(n_claims, s_scan);
+      s_claim[t] = claims_end - n_claims;
+      __syncthreads();
+      const int64_t total_claims = s_scan[kThreads - 1];
+      const uint64_t base = s_head[0].claim_base;
+      // Block w's id pair from the host ring, kLeaderBatch blocks in flight per lane,
+      // then the records of its claims: claim c of a descriptor is block
+      // c / per_block, units (c % per_block) * k onward.
+      for (int64_t w0 = 0; w0 < total_blocks; w0 += kThreads * kLeaderBatch) {
         int32_t src_id[kLeaderBatch], dst_id[kLeaderBatch];
 #pragma unroll
         for (int b = 0; b < kLeaderBatch; ++b) {
           const int64_t w = w0 + b * kThreads + t;
-          if (w < total_ids) {
-            const int i = owner_of(s_first_id, fresh, w);
-            const int j = static_cast<int>(w - s_first_id[i]);
+          if (w < total_blocks) {
+            const int i = owner_of(s_first, fresh, w);
+            const int j = static_cast<int>(w - s_first[i]);
             const int32_t* from = ring->ids[(published + i) % kQueueSlots];
             src_id[b] = host_word(&from[j]);
             dst_id[b] = host_word(&from[kQueueBlocks + j]);
@@ -1906,30 +1959,31 @@ __device__ void queue_leader(const QueueArgs& q, uint64_t start) {
 #pragma unroll
         for (int b = 0; b < kLeaderBatch; ++b) {
           const int64_t w = w0 + b * kThreads + t;
-          if (w < total_ids) {
-            const int i = owner_of(s_first_id, fresh, w);
-            const int j = static_cast<int>(w - s_first_id[i]);
-            int32_t* to = st->ids[(published + i) % kQueueSlots];
-            to[j] = src_id[b];
-            to[kQueueBlocks + j] = dst_id[b];
+          if (w < total_blocks) {
+            const int i = owner_of(s_first, fresh, w);
+            const QueueHeader& h = s_head[i];
+            const int32_t block = static_cast<int32_t>(w - s_first[i]);
+            const uint64_t ids = static_cast<uint64_t>(static_cast<uint32_t>(src_id[b])) |
+                                 (static_cast<uint64_t>(static_cast<uint32_t>(dst_id[b])) << 32);
+            const uint64_t desc = (published + i) << 32;
+            for (int32_t p = 0; p < h.per_block; ++p) {
+              const int64_t c = static_cast<int64_t>(block) * h.per_block + p;
+              if (c >= h.n_claims) break;
+              const int32_t first = min(p * h.k, q.units_per_block);
+              const int32_t count = min(h.k, q.units_per_block - first);
+              uint64_t* rec = reinterpret_cast<uint64_t*>(
+                  &st->claims[(base + s_claim[i] + c) % kQueueClaimRing]);
+              coherent_store(rec, ids);
+              coherent_store(rec + 1, desc | static_cast<uint32_t>(first) |
+                                          (static_cast<uint64_t>(count) << 16));
+            }
           }
         }
       }
-      // Claim map: the new descriptors' claims follow each other from the first's base.
-      const int64_t claims_end =
-          workgroup_scan(t < fresh ? s_head[t].n_claims : 0, s_scan);
-      s_first_id[t] = claims_end - (t < fresh ? s_head[t].n_claims : 0);
-      __syncthreads();
-      const int64_t total_claims = s_scan[kThreads - 1];
-      const uint64_t base = s_head[0].claim_base;
-      for (int64_t w = t; w < total_claims; w += kThreads) {
-        const int i = owner_of(s_first_id, fresh, w);
-        st->claim_desc[(base + w) % kQueueClaimRing] = static_cast<uint32_t>(published + i);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      queue_stores_done();
       __syncthreads();
       if (t == 0)
-        __hip_atomic_store(&st->published_claims, base + total_claims, __ATOMIC_RELEASE,
+        __hip_atomic_store(&st->published_claims, base + total_claims, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       published += fresh;
       last = wall_clock64();
@@ -1950,13 +2004,15 @@ __device__ void queue_leader(const QueueArgs& q, uint64_t start) {
   }
 }
 
-// A store a mover makes to a destination tile: an agent-scope atomic store,
-// which the compiler issues with the device-coherence bit (sc1), so the data is
-// written through the XCD's L2 to where every XCD reads it. Completing such
-// stores (the vector-memory counter at zero) is then all a mover waits for
-// before it counts a claim done: an agent-scope release would instead write
-// back the whole L2 of the XCD, after every claim of every mover. 16-byte
-// vectors go as two 8-byte stores.
+// Stores a mover makes to destination tiles are device-coherent (see
+// coherent_store). Whole tiles of 16-byte vectors are written through a buffer
+// resource spanning the tile, with 16-byte stores carrying the coherence bit
+// (kQueueStorePolicy); other tiles with agent-scope atomic stores of 8 bytes or
+// less, a 16-byte vector as two.
+constexpr bool kQueueTileBufferStores = true;
+constexpr int kQueueStorePolicy = 16;        // sc1: device-coherent
+constexpr int kBufferWordFormat = 0x00020000;   // buffer resource word 3: 32-bit data format
+
 template <typename V>
 __device__ __forceinline__ void queue_store(gptr<V> p, V v) {
   if constexpr (sizeof(V) == 16) {
@@ -1974,47 +2030,67 @@ __device__ __forceinline__ void queue_store(gptr<V> p, V v) {
   }
 }
 
-// Every store this lane made is complete (and, being device-coherent, visible
-// to every XCD). The empty asm statements keep the compiler from moving memory
-// accesses across the wait.
-__device__ __forceinline__ void queue_stores_done() {
-  __asm__ __volatile__("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0);
-  __asm__ __volatile__("" ::: "memory");
+// An address every lane of the wave holds, marked uniform for the compiler (it
+// cannot see that a value read from LDS at one address is the same in every
+// lane), so a buffer resource built on it lives in scalar registers.
+__device__ __forceinline__ char* wave_uniform(char* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<char*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // Move unit a of a block (tile a, or tiles a * group .. of a group) from block
-// src_id of the source pool to block dst_id of the destination. Lane t moves
-// vectors t, t + kThreads, ..., U loads in flight before their stores; an id
-// outside its pool moves nothing.
+// src_id of the source pool to block dst_id of the destination, with the lanes of
+// one wave: lane l moves vectors l, l + kWave, ..., U loads in flight before their
+// stores. An id outside its pool moves nothing.
 template <typename V, int U, bool NT>
 __device__ __forceinline__ void queue_move_unit(const QueueArgs& q, int32_t src_id,
                                                 int32_t dst_id, int a) {
   if (src_id < 0 || src_id >= q.src.num_blocks || dst_id < 0 || dst_id >= q.dst.num_blocks)
     return;
   const int64_t tile_bytes = static_cast<int64_t>(q.tile_vecs) * sizeof(V);
-  const int t = threadIdx.x;
+  const int l = threadIdx.x % kWave;
   if (q.group == 1) {
-    const gptr<const V> s = as_global<V>(array_base(q.src, a) + src_id * tile_bytes);
-    const gptr<V> d = as_global<V>(array_base(q.dst, a) + dst_id * tile_bytes);
-    for (int v = t; v < q.tile_vecs; v += U * kThreads) {
+    const gptr<const V> s = as_global<V>(wave_uniform(array_base(q.src, a) + src_id * tile_bytes));
+    char* d = wave_uniform(array_base(q.dst, a) + dst_id * tile_bytes);
+    auto store = [&](int v, V r) {
+      if constexpr (sizeof(V) == 16 && kQueueTileBufferStores) {
+        // tile_bytes <= kMaxTileBytes: the tile's offsets fit the resource.
+        const __amdgpu_buffer_rsrc_t tile = __builtin_amdgcn_make_buffer_rsrc(
+            d, 0, static_cast<int32_t>(tile_bytes), kBufferWordFormat);
+        __builtin_amdgcn_raw_buffer_store_b128(r, tile, v * 16, 0, kQueueStorePolicy);
+      } else {
+        queue_store(as_global<V>(d) + v, r);
+      }
+    };
+    const int full = q.tile_vecs - (U - 1) * kWave;   // v < full: all U vectors in range
+    int v = l;
+    for (; v < full; v += U * kWave) {
+      V r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) r[u] = load_vec<V, NT>(s + v + u * kWave);
+#pragma unroll
+      for (int u = 0; u < U; ++u) store(v + u * kWave, r[u]);
+    }
+    if (v < q.tile_vecs) {
       V r[U];
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (v + u * kThreads < q.tile_vecs) r[u] = load_vec<V, NT>(s + v + u * kThreads);
+        if (v + u * kWave < q.tile_vecs) r[u] = load_vec<V, NT>(s + v + u * kWave);
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (v + u * kThreads < q.tile_vecs) queue_store(d + v + u * kThreads, r[u]);
+        if (v + u * kWave < q.tile_vecs) store(v + u * kWave, r[u]);
     }
     return;
   }
-  // Small tiles: tile_vecs divides kThreads; lane t takes vector t % tile_vecs of
-  // tiles a0 + t / tile_vecs, a0 + t / tile_vecs + per_pass, ...
+  // Small tiles: tile_vecs divides kWave; lane l takes vector l % tile_vecs of
+  // tiles a0 + l / tile_vecs, a0 + l / tile_vecs + per_pass, ...
   const int a0 = a * q.group;
   const int tiles = min(q.group, q.n_arrays - a0);
-  const int per_pass = kThreads / q.tile_vecs;
-  const int64_t lane_offset = static_cast<int64_t>(t % q.tile_vecs) * sizeof(V);
-  for (int j = t / q.tile_vecs; j < tiles; j += U * per_pass) {
+  const int per_pass = kWave / q.tile_vecs;
+  const int64_t lane_offset = static_cast<int64_t>(l % q.tile_vecs) * sizeof(V);
+  for (int j = l / q.tile_vecs; j < tiles; j += U * per_pass) {
     V r[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -2029,28 +2105,44 @@ __device__ __forceinline__ void queue_move_unit(const QueueArgs& q, int32_t src_
   }
 }
 
-// The other workgroups: take a claim, wait for it to be published, move its
-// units, count it done. Thread 0 runs the claim protocol and hands each claim
-// to the workgroup through LDS.
+// Every wave of the other workgroups is a mover: it takes a claim from its
+// cursor, waits for the claim to be published, reads its record, moves its units,
+// and counts it finished. Claims hold at most k units each, so they are close in
+// size. A claim is taken while the previous one moves, so the atomic's latency
+// hides behind the data. Movers are spread over the cursors wave by wave, so the
+// claims of a small request land on different compute units.
+// Lane 0 runs the claim protocol; the wave's other lanes wait for it (they are
+// masked off meanwhile) and take its values with readfirstlane. Nothing is
+// shared between the waves of a workgroup, so no barrier is needed: a wave's
+// wait for its stores covers all of its lanes.
 template <typename V, int U, bool NT>
 __device__ void queue_mover(const QueueArgs& q, uint64_t start) {
-  __shared__ int32_t s_go, s_slot, s_first, s_end;
-  __shared__ uint32_t s_desc;
-  __shared__ uint64_t s_target;
-  const int t = threadIdx.x;
+  const int l = threadIdx.x % kWave;
   QueueState* st = q.state;
-  uint64_t next = 0, known = 0, last = start;   // thread 0's
-  if (t == 0)
-    next = __hip_atomic_fetch_add(&st->next_claim, uint64_t{1}, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
+  const int cursor = ((blockIdx.x - 1) * (kThreads / kWave) + threadIdx.x / kWave) % kQueueCursors;
+  auto take = [&]() -> uint64_t {
+    return cursor + kQueueCursors * __hip_atomic_fetch_add(&st->cursor[cursor].left, uint64_t{1},
+                                                           __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+  };
+  uint64_t next = 0, known = 0, last = start;   // lane 0's
+  if (l == 0) next = take();
   for (;;) {
-    if (t == 0) {
+    int32_t go = 0, src = 0, dst = 0, first = 0, end = 0;
+    uint32_t desc = 0;
+    if (l == 0) {
       const uint64_t claim = next;
-      int go = wall_clock64() - start <= q.life_ticks ? 1 : 0, nap = 1;
+      go = wall_clock64() - start <= q.life_ticks ? 1 : 0;
+      int nap = 1;
       while (go && claim >= known) {
         const uint64_t pc = agent_word(&st->published_claims);
         if (pc > known) {
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          // Sources were written before their descriptor was submitted: lines this
+          // CU or XCD cached earlier are dropped before any of them is read. Only
+          // a mover whose claim is now published does so: a publication wakes
+          // every waiting mover, and thousands of invalidations at once would
+          // hold up the few that have work.
+          if (claim < pc) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
           known = pc;
           last = wall_clock64();
           nap = 1;
@@ -2073,43 +2165,35 @@ __device__ void queue_mover(const QueueArgs& q, uint64_t start) {
           break;
         }
         queue_nap(nap);
-        nap = nap < 16 ? 2 * nap : 16;
+        nap = nap < 8 ? 2 * nap : 8;
       }
       if (go) {
-        const uint32_t r = ring_word(&st->claim_desc[claim % kQueueClaimRing]);
-        const int slot = static_cast<int>(r % kQueueSlots);
-        const QueueHeader* h = &st->header[slot];
-        const int64_t first =
-            static_cast<int64_t>(claim - ring_word(&h->claim_base)) * ring_word(&h->k);
-        s_first = static_cast<int32_t>(first);
-        s_end = static_cast<int32_t>(min<int64_t>(first + ring_word(&h->k), ring_word(&h->n_units)));
-        s_slot = slot;
-        s_desc = r;
-        s_target = ring_word(&h->done_target);
-        // The next claim, taken now so its atomic's latency hides behind this one's moves.
-        next = __hip_atomic_fetch_add(&st->next_claim, uint64_t{1}, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t* rec =
+            reinterpret_cast<const uint64_t*>(&st->claims[claim % kQueueClaimRing]);
+        const uint64_t ids = ring_word(rec), work = ring_word(rec + 1);
+        src = static_cast<int32_t>(static_cast<uint32_t>(ids));
+        dst = static_cast<int32_t>(static_cast<uint32_t>(ids >> 32));
+        first = min(static_cast<int32_t>(work & 0xffff), q.units_per_block);
+        end = min(first + static_cast<int32_t>((work >> 16) & 0xffff), q.units_per_block);
+        desc = static_cast<uint32_t>(work >> 32);
+        next = take();
       }
-      s_go = go;
     }
-    __syncthreads();
-    if (!s_go) return;
-    const int slot = s_slot, end = s_end;
-    const int32_t* ids = st->ids[slot];
-    for (int u = s_first; u < end; ++u) {
-      const int i = u / q.units_per_block;
-      queue_move_unit<V, U, NT>(q, ring_word(&ids[i]), ring_word(&ids[kQueueBlocks + i]),
-                                u - i * q.units_per_block);
-    }
-    // Every lane's device-coherent stores are complete before the claim counts as
-    // done, and the descriptor's last claim before its completion reaches the host.
+    if (!__builtin_amdgcn_readfirstlane(go)) return;
+    src = __builtin_amdgcn_readfirstlane(src);
+    dst = __builtin_amdgcn_readfirstlane(dst);
+    end = __builtin_amdgcn_readfirstlane(end);
+    for (int u = __builtin_amdgcn_readfirstlane(first); u < end; ++u)
+      queue_move_unit<V, U, NT>(q, src, dst, u);
+    // The wave's device-coherent stores are complete before the claim counts as
+    // finished, and the descriptor's last claim before its completion reaches the host.
     queue_stores_done();
-    __syncthreads();
-    if (t == 0) {
-      const uint64_t done = __hip_atomic_fetch_add(&st->done[slot], uint64_t{1},
+    if (l == 0) {
+      const int slot = static_cast<int>(desc % kQueueSlots);
+      const uint64_t left = __hip_atomic_fetch_sub(&st->remaining[slot].left, uint64_t{1},
                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (done + 1 == s_target)
-        __hip_atomic_store(&q.ring->complete[slot], uint64_t{s_desc} + 1, __ATOMIC_RELAXED,
+      if (left == 1)
+        __hip_atomic_store(&q.ring->complete[slot], uint64_t{desc} + 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
@@ -2153,7 +2237,8 @@ struct iekv_queue {
   const iekv_pool* src = nullptr;
   const iekv_pool* dst = nullptr;
   bool same_pool = false;
-  int32_t workers = 0;
+  int32_t workers = 0;              // mover workgroups
+  int64_t movers = 0;              // mover waves
   int64_t max_k = 1;               // units per claim at most (claim_bytes)
   int64_t idle_us = 0, life_us = 0;
   QueueRing* ring = nullptr;       // host address of the pinned ring
@@ -2168,7 +2253,6 @@ struct iekv_queue {
   uint64_t published = 0;          // descriptors of this session
   uint64_t claims = 0;             // claims of this session
   uint64_t retired = 0;            // descriptors [0, retired) of this session are done
-  uint64_t slot_claims[kQueueSlots] = {};
   uint64_t launches = 0;
   std::chrono::steady_clock::time_point started, last_publish;
   std::mutex mu;
@@ -2209,9 +2293,8 @@ int queue_broken() {
 // Start a session: clear both rings' counters and launch the kernel.
 int queue_launch(iekv_queue* q) {
   std::memset(static_cast<void*>(q->ring), 0, offsetof(QueueRing, header));
-  IEKV_HIP(hipMemsetAsync(q->state, 0, offsetof(QueueState, header), q->stream));
+  IEKV_HIP(hipMemsetAsync(q->state, 0, offsetof(QueueState, claims), q->stream));
   q->published = q->claims = q->retired = 0;
-  std::fill(std::begin(q->slot_claims), std::end(q->slot_claims), uint64_t{0});
   hipLaunchKernelGGL(q->kernel, dim3(static_cast<uint32_t>(q->workers) + 1), dim3(kThreads), 0,
                      q->stream, q->args);
   IEKV_HIP(hipGetLastError());
@@ -2270,9 +2353,11 @@ int queue_wait_local(iekv_queue* q, uint64_t upto, int64_t timeout_us) {
   }
 }
 
-// Publish one descriptor of n <= kQueueBlocks checked (src, dst) pairs.
+// Publish one descriptor of n <= kQueueBlocks checked (src, dst) pairs, its
+// claims planned for `movers` of the kernel's mover waves (its share of a batch
+// submitted together).
 int queue_publish(iekv_queue* q, const int32_t* s, const int32_t* d, int32_t n,
-                  uint64_t* ticket) {
+                  int64_t movers, uint64_t* ticket) {
   int rc;
   if (q->running && q->published >= kQueueSlots &&
       (rc = queue_wait_local(q, q->published - kQueueSlots, kQueueWaitUs)))
@@ -2286,16 +2371,14 @@ int queue_publish(iekv_queue* q, const int32_t* s, const int32_t* d, int32_t n,
   if (!q->running && (rc = queue_launch(q))) return rc;
   const uint64_t r = q->published;
   const int slot = static_cast<int>(r % kQueueSlots);
-  const int64_t n_units = static_cast<int64_t>(n) * q->args.units_per_block;
-  const iekv_plan::QueueClaims c = iekv_plan::queue_claims(n_units, q->workers, q->max_k);
-  q->slot_claims[slot] += c.n_claims;
+  const iekv_plan::QueueClaims c =
+      iekv_plan::queue_claims(n, q->args.units_per_block, movers, q->max_k);
   QueueHeader& h = q->ring->header[slot];
   h.claim_base = q->claims;
-  h.done_target = q->slot_claims[slot];
   h.n_blocks = n;
-  h.n_units = static_cast<int32_t>(n_units);
-  h.k = static_cast<int32_t>(c.k);
   h.n_claims = static_cast<int32_t>(c.n_claims);
+  h.k = static_cast<int32_t>(c.k);
+  h.per_block = static_cast<int32_t>(c.per_block);
   std::memcpy(q->ring->ids[slot], s, sizeof(int32_t) * n);
   std::memcpy(q->ring->ids[slot] + kQueueBlocks, d, sizeof(int32_t) * n);
   __atomic_store_n(&q->ring->tail, r + 1, __ATOMIC_RELEASE);
@@ -3004,7 +3087,6 @@ int iekv_queue_create(const iekv_pool* src, const iekv_pool* dst, int32_t worker
   IEKV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, src->device));
   IEKV_HIP(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, src->device));
   if (clock_khz <= 0) return set_error(IEKV_ERR_HIP, "the device reports no wall clock");
-  if (workers == 0) workers = 4 * std::max(cus, 1);
   if (workers > 65535) return set_error(IEKV_ERR_INVALID, "workers %d out of range", workers);
 
   // The unit of work: one tile, or a group of small tiles of one block, as the
@@ -3014,11 +3096,15 @@ int iekv_queue_create(const iekv_pool* src, const iekv_pool* dst, int32_t worker
   if ((rc = plan_move(1, src->tile_bytes, src->n_arrays, align, true, true, true, &pl,
                       g_direct_chunk.load())))
     return rc;
-  // Whole tiles per unit: the plan's chunks only split a launch's work.
-  const int group = iekv_plan::tile_group(pl.tile_vecs, pl.vec, g_direct_chunk.load(),
-                                          src->n_arrays);
-  const int64_t lane_vecs = (static_cast<int64_t>(pl.tile_vecs) * group + kThreads - 1) / kThreads;
+  // A unit is a whole tile, or a group of small tiles, moved by one wave.
+  const int group = iekv_plan::queue_tile_group(pl.tile_vecs, pl.vec, g_direct_chunk.load(),
+                                                src->n_arrays);
+  const int64_t lane_vecs = (static_cast<int64_t>(pl.tile_vecs) * group + kWave - 1) / kWave;
   const int64_t unit_bytes = src->tile_bytes * group;
+  const int32_t units_per_block = (src->n_arrays + group - 1) / group;
+  if (units_per_block > kQueueMaxUnits)
+    return set_error(IEKV_ERR_INVALID, "%d units per block exceed the queue's %d",
+                     units_per_block, kQueueMaxUnits);
 
   iekv_queue* q = new (std::nothrow) iekv_queue{};
   if (!q) return set_error(IEKV_ERR_INVALID, "out of host memory");
@@ -3055,15 +3141,26 @@ int iekv_queue_create(const iekv_pool* src, const iekv_pool* dst, int32_t worker
   q->dst = dst;
   q->same_pool = same_pool;
   q->workers = workers;
+  q->movers = workers * (kThreads / kWave);
   q->max_k = std::max<int64_t>(1, claim_bytes / unit_bytes);
   q->idle_us = idle_us;
   q->life_us = life_us;
   q->kernel = pick_queue_kernel(pl.vec, static_cast<int>(std::min<int64_t>(lane_vecs, 16)),
                                 nontemporal(-1));
+  if (workers == 0) {
+    // As many workgroups as the device holds at once, leader included: a workgroup
+    // waiting for room would hold no claim, but would add nothing either.
+    int per_cu = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, reinterpret_cast<const void*>(q->kernel), kThreads, 0);
+    if (e != hipSuccess) (void)hipGetLastError();
+    workers = std::max(1, std::min(4, per_cu > 0 ? per_cu : 4) * std::max(cus, 1) - 1);
+    q->workers = workers;
+    q->movers = static_cast<int64_t>(workers) * (kThreads / kWave);
+  }
   const uint64_t ticks_per_us = static_cast<uint64_t>(clock_khz) / 1000;
   q->args = QueueArgs{view_of(src), view_of(dst), q->state, static_cast<QueueRing*>(ring_dev),
-                      pl.tile_vecs, src->n_arrays, group,
-                      (src->n_arrays + group - 1) / group,
+                      pl.tile_vecs, src->n_arrays, group, units_per_block,
                       static_cast<uint64_t>(idle_us) * std::max<uint64_t>(ticks_per_us, 1),
                       static_cast<uint64_t>(life_us) * std::max<uint64_t>(ticks_per_us, 1)};
   *out = q;
@@ -3111,11 +3208,15 @@ int iekv_queue_submit_requests(iekv_queue* q, int32_t n_requests, const int32_t*
   if (q->broken) return queue_broken();
   DeviceGuard guard(q->src->device);
   if (!guard.ok()) return guard.fail();
+  // The batch's units are spread over every mover: a descriptor's claims are
+  // planned for its share of them.
   for (int64_t k = 0, at = 0; k < n_requests; at += counts[k], ++k) {
     tickets[k] = IEKV_QUEUE_DONE;
     for (int32_t first = 0; first < counts[k]; first += kQueueBlocks) {
       const int32_t m = std::min<int32_t>(kQueueBlocks, counts[k] - first);
-      if ((rc = queue_publish(q, s.data() + at + first, d.data() + at + first, m, &tickets[k])))
+      const int64_t share = std::max<int64_t>(1, q->movers * m / total);
+      if ((rc = queue_publish(q, s.data() + at + first, d.data() + at + first, m, share,
+                              &tickets[k])))
         return rc;
     }
   }

@@ -310,35 +310,58 @@ inline bool spans_cross(std::vector<Span> spans) {
   return false;
 }
 
-// Request queue (iekv_queue_*). A descriptor of n_units units (a unit is one
-// tile, or one group of small tiles, of one block) is served in claims of k
-// consecutive units; movers take claims from one cursor that runs over every
-// descriptor of a session, and a ring of kQueueClaimRing entries maps a claim to
-// its descriptor. A descriptor has at most kQueueMaxClaims claims, so the claims
-// of `slots` descriptors in flight fill at most half the ring: an entry is
-// rewritten only after the descriptor of the claim it held has finished.
+// Request queue (iekv_queue_*). A descriptor's n_blocks blocks have `units`
+// units each (a unit is one tile, or one group of small tiles); it is served in
+// claims of at most k consecutive units of one block, so the claim's record can
+// carry that block's id pair. Movers take claims from one cursor that runs over
+// every descriptor of a session, and a ring of kQueueClaimRing records maps a
+// claim to its work. A descriptor has at most kQueueMaxClaims claims, so the
+// claims of `slots` descriptors in flight fill at most half the ring: a record
+// is rewritten only after the descriptor of the claim it held has finished.
 constexpr int64_t kQueueMaxClaims = 4096;
 
 constexpr int64_t queue_claim_ring(int64_t slots) { return 2 * slots * kQueueMaxClaims; }
 
+// Lanes that move one unit: each wave of the queue's kernel is a mover.
+constexpr int kQueueWave = 64;
+
+// Tiles per unit of the queue's movers: small tiles whose vector count divides
+// the wave are grouped, chunk_bytes / tile bytes tiles of one block in
+// consecutive arrays (at most n_arrays); any other tile is a unit of its own.
+inline int queue_tile_group(int64_t tile_vecs, int vec_bytes, int64_t chunk_bytes,
+                            int32_t n_arrays) {
+  if (chunk_bytes <= 0 || tile_vecs * vec_bytes >= chunk_bytes || kQueueWave % tile_vecs)
+    return 1;
+  const int64_t group = chunk_bytes / (tile_vecs * vec_bytes);
+  return static_cast<int>(group < n_arrays ? group : n_arrays);
+}
+
 struct QueueClaims {
-  int64_t k = 1;         // units per claim
-  int64_t n_claims = 0;  // ceil(n_units / k)
+  int64_t k = 1;          // units per claim (the last claim of a block may hold fewer)
+  int64_t per_block = 0;  // claims per block: ceil(units / k)
+  int64_t n_claims = 0;   // n_blocks * per_block
 };
 
 // Claims of a descriptor: spread over all `workers` (one unit per claim for a
-// request smaller than the mover count), at most max_k units per claim, and
-// never more than kQueueMaxClaims claims.
-inline QueueClaims queue_claims(int64_t n_units, int64_t workers, int64_t max_k) {
+// request no larger than the mover count), at most max_k units and at most one
+// block per claim, and never more than kQueueMaxClaims claims (n_blocks is at
+// most kQueueMaxClaims). Claim c is block c / per_block, units
+// (c % per_block) * k onward.
+inline QueueClaims queue_claims(int64_t n_blocks, int64_t units, int64_t workers,
+                                int64_t max_k) {
   QueueClaims c;
-  if (n_units <= 0) return c;
+  if (n_blocks <= 0 || units <= 0) return c;
+  const int64_t n_units = n_blocks * units;
   int64_t k = workers > 0 ? n_units / workers : n_units;
   if (k > max_k) k = max_k;
+  if (k > units) k = units;
   if (k < 1) k = 1;
-  const int64_t least = (n_units + kQueueMaxClaims - 1) / kQueueMaxClaims;
-  if (k < least) k = least;
+  const int64_t most = kQueueMaxClaims / n_blocks > 0 ? kQueueMaxClaims / n_blocks : 1;
+  const int64_t least_k = (units + most - 1) / most;
+  if (k < least_k) k = least_k;
   c.k = k;
-  c.n_claims = (n_units + k - 1) / k;
+  c.per_block = (units + k - 1) / k;
+  c.n_claims = n_blocks * c.per_block;
   return c;
 }
 

@@ -503,47 +503,70 @@ static void check_launch_chunk() {
   EXPECT(launch_chunk(false, true, 2048, 4096, 8192) == 4096, "cfg5 tp8 unpack");
 }
 
-// The request queue's claims (queue_claims): the claims of a descriptor cover each
-// of its units exactly once, none is empty, there are at most kQueueMaxClaims of
-// them, a request no larger than the mover count is spread one unit per claim, and
-// k stays within max_k unless the claim cap needs more. The claim ring then holds
-// the claims of twice the descriptors that can be in flight, so the entry of a claim
-// still waiting is never rewritten: the claims between an entry's two uses span at
-// least 2 * slots descriptors, and a descriptor is published only after the one
+// The request queue's claims (queue_claims): a descriptor's claims cover each
+// (block, unit) pair exactly once, no claim is empty or spans two blocks, there
+// are at most kQueueMaxClaims of them, a request no larger than the mover count
+// is spread one unit per claim, and k reaches max_k for a large request unless
+// the claim cap needs more. The claim ring then holds the claims of twice the
+// descriptors that can be in flight, so the record of a claim still waiting is
+// never rewritten: the claims between a record's two uses span at least
+// 2 * slots descriptors, and a descriptor is published only after the one
 // `slots` before it has finished.
 static void check_queue_claims() {
   for (int64_t workers : {1, 7, 1024})
     for (int64_t max_k : {1, 4, 64})
-      for (int64_t n : {1, 2, 3, 7, 63, 64, 65, 1000, 1024, 1025, 4095, 4096, 4097, 8192,
-                        25920, 65536, 163840, 1 << 26}) {
-        const QueueClaims c = queue_claims(n, workers, max_k);
-        EXPECT(c.k >= 1 && c.n_claims >= 1, "n %lld: k %lld claims %lld", (long long)n,
-               (long long)c.k, (long long)c.n_claims);
-        EXPECT(c.n_claims <= kQueueMaxClaims, "n %lld: %lld claims", (long long)n,
-               (long long)c.n_claims);
-        EXPECT(c.n_claims * c.k >= n && (c.n_claims - 1) * c.k < n,
-               "n %lld: claims of %lld do not cover the units exactly", (long long)n,
-               (long long)c.k);
-        const int64_t least = (n + kQueueMaxClaims - 1) / kQueueMaxClaims;
-        EXPECT(c.k <= (max_k > least ? max_k : least), "n %lld: k %lld above max_k %lld",
-               (long long)n, (long long)c.k, (long long)max_k);
-        if (n <= workers) EXPECT(c.k == 1, "n %lld <= workers %lld: k %lld", (long long)n,
-                                 (long long)workers, (long long)c.k);
-        if (n / workers >= max_k)   // a request of max_k units per mover or more: full claims
-          EXPECT(c.k == (max_k > least ? max_k : least), "n %lld: k %lld, not max_k %lld",
-                 (long long)n, (long long)c.k, (long long)max_k);
-        if (n <= 70000) {   // brute force: every unit in exactly one claim
-          std::vector<int> hit(static_cast<size_t>(n), 0);
-          for (int64_t claim = 0; claim < c.n_claims; ++claim)
-            for (int64_t u = claim * c.k; u < claim * c.k + c.k && u < n; ++u) ++hit[u];
-          for (int64_t u = 0; u < n; ++u)
-            if (hit[u] != 1) {
-              EXPECT(false, "n %lld: unit %lld in %d claims", (long long)n, (long long)u, hit[u]);
-              break;
+      for (int64_t units : {1, 2, 3, 8, 10, 48, 64, 160, 65536})
+        for (int64_t n_blocks : {1, 2, 5, 19, 64, 405, 1000, 1024}) {
+          const QueueClaims c = queue_claims(n_blocks, units, workers, max_k);
+          const int64_t n_units = n_blocks * units;
+          EXPECT(c.k >= 1 && c.k <= units && c.per_block >= 1, "k %lld per block %lld",
+                 (long long)c.k, (long long)c.per_block);
+          EXPECT(c.n_claims == n_blocks * c.per_block && c.n_claims <= kQueueMaxClaims,
+                 "%lld blocks x %lld units: %lld claims", (long long)n_blocks, (long long)units,
+                 (long long)c.n_claims);
+          EXPECT(c.per_block * c.k >= units && (c.per_block - 1) * c.k < units,
+                 "units %lld: claims of %lld do not cover a block exactly", (long long)units,
+                 (long long)c.k);
+          if (n_units <= workers)
+            EXPECT(c.k == 1, "n %lld <= workers %lld: k %lld", (long long)n_units,
+                   (long long)workers, (long long)c.k);
+          if (n_units / workers >= max_k && max_k <= units &&
+              n_blocks * ((units + max_k - 1) / max_k) <= kQueueMaxClaims)
+            EXPECT(c.k == max_k, "n %lld: k %lld, not max_k %lld", (long long)n_units,
+                   (long long)c.k, (long long)max_k);
+          if (n_units <= 200000) {   // brute force: every (block, unit) in exactly one claim
+            std::vector<int> hit(static_cast<size_t>(n_units), 0);
+            for (int64_t claim = 0; claim < c.n_claims; ++claim) {
+              const int64_t b = claim / c.per_block, first = (claim % c.per_block) * c.k;
+              const int64_t count = std::min(c.k, units - first);
+              EXPECT(count >= 1, "claim %lld is empty", (long long)claim);
+              for (int64_t u = first; u < first + count; ++u) ++hit[b * units + u];
             }
+            for (int64_t u = 0; u < n_units; ++u)
+              if (hit[u] != 1) {
+                EXPECT(false, "unit %lld in %d claims", (long long)u, hit[u]);
+                break;
+              }
+          }
         }
-      }
-  EXPECT(queue_claims(0, 1024, 4).n_claims == 0, "an empty descriptor has no claims");
+  EXPECT(queue_claims(0, 8, 1024, 4).n_claims == 0, "an empty descriptor has no claims");
+  // Units of the queue's movers: a group of small tiles is moved by one wave, lane l
+  // taking vector l % tile_vecs of a tile, so tile_vecs divides the wave; a group
+  // stays within the chunk and the block's arrays.
+  for (int64_t tile_vecs : {1, 2, 3, 4, 8, 16, 32, 48, 64, 128, 256, 2048})
+    for (int vec : {1, 4, 16})
+      for (int64_t chunk : {0, 1024, 8192})
+        for (int32_t n_arrays : {1, 6, 64, 160}) {
+          const int g = queue_tile_group(tile_vecs, vec, chunk, n_arrays);
+          EXPECT(g >= 1 && g <= n_arrays, "group %d of %d arrays", g, n_arrays);
+          if (g > 1)
+            EXPECT(kQueueWave % tile_vecs == 0 && g * tile_vecs * vec <= chunk,
+                   "group %d of %lld-vector tiles", g, (long long)tile_vecs);
+          if (chunk > 0 && kQueueWave % tile_vecs == 0 && 2 * tile_vecs * vec <= chunk &&
+              n_arrays > 1)
+            EXPECT(g > 1, "small tiles (%lld vectors of %d B) left ungrouped", (long long)tile_vecs,
+                   vec);
+        }
   for (int64_t slots : {1, 16, 256})
     EXPECT(queue_claim_ring(slots) >= 2 * slots * kQueueMaxClaims, "claim ring too small");
 }

@@ -91,14 +91,20 @@ MISTAKES = [
      ""),
     # The request queue's claims.
     ("a descriptor's claims not capped",
-     "  if (k < least) k = least;\n",
+     "  if (k < least_k) k = least_k;\n",
      ""),
-    ("the last claim of a descriptor dropped",
-     "c.n_claims = (n_units + k - 1) / k;",
-     "c.n_claims = n_units / k;"),
+    ("the last claim of a block dropped",
+     "c.per_block = (units + k - 1) / k;",
+     "c.per_block = units / k;"),
     ("claims never larger than one unit for a big request",
      "if (k > max_k) k = max_k;",
      "if (k > 1) k = 1;"),
+    ("queue tile groups for tiles that do not divide the wave",
+     "tile_vecs * vec_bytes >= chunk_bytes || kQueueWave % tile_vecs)",
+     "tile_vecs * vec_bytes >= chunk_bytes)"),
+    ("claims spanning two blocks",
+     "  if (k > units) k = units;\n",
+     ""),
     ("touching pools counted as overlapping",
      "if (reach[1 - s.owner] > s.lo) return true;",
      "if (reach[1 - s.owner] >= s.lo) return true;"),
