@@ -41,7 +41,9 @@ without NaN codes for fp8). Legs:
                library call (iekv_queue_submit_requests, one descriptor and ticket per
                request), then the last ticket waited for; timed by the host clock from
                the first submission to the last completion (2P bytes). Also reports each
-               request's latency, submitted and waited for alone (ms_per_request)
+               request's latency, submitted and waited for alone (ms_per_request), beside
+               that of one direct launch per request with a stream synchronize after it
+               (launch_latency_ms), measured before the queue's kernel starts
   queue_py     the same with one HandoffQueue.submit call per request from Python
   host_roundtrip  every moved block offloaded to pinned host memory with one iekv_offload
                and restored with one iekv_restore (host-link bound), then the same
@@ -620,6 +622,22 @@ class Legs:
             out.append(1000 * (time.perf_counter() - t0))
         return out
 
+    def launch_latency(self) -> list[float]:
+        """Milliseconds from issuing each request's direct launch (host ids, as
+        iekv_copy_direct_ids takes them) to the host seeing it done (a stream
+        synchronize): the per-launch path's counterpart of queue_latency."""
+        from iekv import _native
+
+        self._queue()
+        out = []
+        for s, d in self._queue_tables:
+            t0 = time.perf_counter()
+            _native.call("iekv_copy_direct_ids", self.src.native.handle, self.dst.native.handle,
+                         s.ctypes.data, d.ctypes.data, s.size, self.stream.cuda_stream)
+            self.stream.synchronize()
+            out.append(1000 * (time.perf_counter() - t0))
+        return out
+
     def stop_queue(self) -> None:
         if hasattr(self, "_handoff_queue"):
             self._handoff_queue.stop()
@@ -950,6 +968,8 @@ def time_queue_leg(legs: Legs, name: str, steps: int, warmup: int):
     step, wall seconds, [])."""
     step = getattr(legs, name)
     legs.torch.cuda.synchronize()
+    legs.launch_latency()                      # warm-up of the per-launch path
+    legs.launch_ms = legs.launch_latency()     # before the queue's kernel starts
     for _ in range(warmup):
         step()
     times = []
@@ -999,6 +1019,10 @@ def summarize(legs: Legs, name: str, ms_step: float, launches, bytes_per_step: i
     if name in QUEUE_LEGS:
         # each request submitted and waited for alone: its latency seen from the host
         req_ms = sorted(getattr(legs, "queue_ms", None) or [ms_step])
+        launch = sorted(getattr(legs, "launch_ms", None) or [0.0])
+        out["launch_latency_ms"] = {"p50": round(launch[len(launch) // 2], 4),
+                                    "p99": round(launch[min(len(launch) - 1,
+                                                            int(0.99 * len(launch)))], 4)}
     if name in ("direct", "direct_ids", "copier", "requests", "pack_unpack",
                 "copier_pack_unpack", "pack", "unpack", *SLOT_LEGS, *QUEUE_LEGS):
         out["ms_per_request"] = {"mean": round(statistics.fmean(req_ms), 4),

@@ -333,7 +333,7 @@ inline int queue_tile_group(int64_t tile_vecs, int vec_bytes, int64_t chunk_byte
   if (chunk_bytes <= 0 || tile_vecs * vec_bytes >= chunk_bytes || kQueueWave % tile_vecs)
     return 1;
   const int64_t group = chunk_bytes / (tile_vecs * vec_bytes);
-  return static_cast<int>(group < n_arrays ? group : n_arrays);
+  return static_cast<int>(group > n_arrays ? n_arrays : group);
 }
 
 struct QueueClaims {
