@@ -492,8 +492,8 @@ int iekv_get_direct_chunk(int32_t* chunk_bytes);
  * nor write blocks another one reads. Each request's ids are checked as
  * iekv_copy_direct_ids checks them. Calls on one queue are serialized by a
  * lock; the pools must outlive the queue. While it runs, the kernel holds
- * workers + 1 workgroups resident (by default as many as fit, at most 4 per
- * compute unit), so other kernels share the GPU with it; hipDeviceSynchronize
+ * workers + 1 workgroups resident (by default one per compute unit), so other
+ * kernels share the GPU with it; hipDeviceSynchronize
  * and hipFree wait for it to end (iekv_queue_stop ends it at once).
  *
  * No reference counterpart: the reference hands off one request at a time
@@ -512,8 +512,8 @@ typedef struct iekv_queue iekv_queue;
 
 /* Make a queue for direct handoffs from `src` to `dst` (same n_arrays and
  * tile_bytes, one device). workers: mover workgroups, each wave of which is a
- * mover (0: as many as the device holds at once, at most 4 per compute unit);
- * claim_bytes: most bytes one mover claims at once (0: 128 KiB); idle_us /
+ * mover (0: one per compute unit, the leader's workgroup included);
+ * claim_bytes: most bytes one mover claims at once (0: 512 KiB); idle_us /
  * life_us: the kernel's idle and lifetime limits (0: 200 ms / 60 s). Allocates
  * the rings (about 2 MiB of pinned host memory, 11 MiB of device memory) and a
  * stream; launches nothing until the first submission. */

@@ -52,8 +52,9 @@ def _id_array(ids, what: str) -> np.ndarray:
 class HandoffQueue:
     """Direct handoffs from ``src`` to ``dst`` (two :class:`KVPool` of one shape).
 
-    ``workers``: mover workgroups (0: four per compute unit); ``claim_bytes``: most
-    bytes a mover claims at once (0: 128 KiB); ``idle_ms`` / ``life_ms``: the
+    ``workers``: mover workgroups, each wave of which is a mover (0: one per compute
+    unit, the leader's included); ``claim_bytes``: most bytes a mover claims at once
+    (0: 512 KiB); ``idle_ms`` / ``life_ms``: the
     kernel's idle and lifetime limits (0: 200 ms / 60 s). The library restarts the
     kernel by itself when a submission comes near either limit.
     """
