@@ -7,7 +7,7 @@ reserved ids in its pool and continues decoding. The KV bytes move through
 the copier the workers own: by default the HIP copier, so a request's whole
 block table moves in one launch.
 
-Three transfer modes (``mode=``):
+Transfer modes (``mode=``):
 
 ``"pack"`` (default, reference-exact)
     prefill packs the blocks into a device staging buffer (one fused pack
@@ -21,6 +21,16 @@ Three transfer modes (``mode=``):
     of 4P) and only then releases the prefill blocks. Destination ids and
     decode output are the same as in "pack" mode; the prefill pool's blocks
     are released at admit instead of at the end of prefill.
+
+``"queue"``
+    as "direct", but each admitted request's copy is submitted to a resident
+    request queue (iekv_queue_*, :class:`iekv.engine.queue.HandoffQueue`) instead
+    of being launched: its own descriptor, ticket and completion, no launch. The
+    current stream is synchronized first (the prefill's writes of the sources and
+    any earlier reads of the destinations are done), and the decode worker waits
+    for the ticket before the request decodes, so admission stays synchronous per
+    request as in the reference. ``generate`` ends the queue's kernel once every
+    prompt is admitted, before decoding.
 
 ``prefix_aware=True`` (any mode)
     the decode worker is asked first which leading full blocks of the prompt
@@ -40,7 +50,7 @@ from ..core.sequence import Sequence, Status
 from ..engine.copier import join_payloads
 from ..engine.engine import CopierFactory, Engine, EngineConfig
 
-MODES = ("pack", "direct")
+MODES = ("pack", "direct", "queue")
 
 # Largest device staging buffer a batched pack-mode generate() fills before it
 # unpacks what it holds (then it starts again at the beginning).
@@ -178,7 +188,7 @@ class PrefillWorker:
             raise ValueError(f"cannot skip {skip_blocks} of {len(seq.block_table)} blocks")
         moved = seq.block_table[skip_blocks:]
         nbytes = self._payload_bytes(len(moved))
-        if self.mode == "direct":
+        if self.mode in ("direct", "queue"):
             source = DirectSource(self.copier, list(moved), release=lambda: self._retire(seq))
             return KVTransfer(token_ids=list(seq.token_ids), num_computed=seq.num_computed,
                               block_payloads=None, bytes_moved=nbytes,
@@ -215,6 +225,8 @@ class DecodeWorker:
         self.engine = Engine(model, config, copier_factory=copier_factory, caches=caches)
         self.copier = self.engine.make_copier("transfer")
         self.prefix_aware = prefix_aware
+        self.use_queue = False      # direct transfers through a request queue ("queue" mode)
+        self._queues: dict[int, Any] = {}
 
     def cached_prefix_blocks(self, prompt_ids: list[int]) -> int:
         """Leading full blocks of ``prompt_ids`` this pool already holds (0 unless prefix-aware).
@@ -294,15 +306,50 @@ class DecodeWorker:
                                f"carries {transfer.table_length}")
         return seq.block_table[transfer.first_block:]
 
+    def queue_from(self, source_copier):
+        """The request queue from ``source_copier``'s pool into this worker's (made on
+        first use); the current stream is synchronized, so the queue's moves see
+        every write issued before."""
+        import torch
+
+        from ..engine.queue import HandoffQueue
+
+        q = self._queues.get(id(source_copier))
+        if q is None:
+            if not (hasattr(source_copier, "pool") and hasattr(self.copier, "pool")):
+                raise TypeError("queue transfers need HIP copiers on both sides")
+            q = self._queues[id(source_copier)] = HandoffQueue(source_copier.pool,
+                                                                self.copier.pool)
+        torch.cuda.current_stream(self.copier.pool.device).synchronize()
+        return q
+
+    def stop_queues(self) -> None:
+        """End the request queues' kernels (the next submission starts them again)."""
+        for q in self._queues.values():
+            q.stop()
+
     def _move(self, transfer: KVTransfer, dst_ids: list[int]) -> None:
         if transfer.source is not None:
             src = transfer.source
+            if self.use_queue:
+                q = self.queue_from(src.copier)
+                q.wait(q.submit(src.block_ids, dst_ids))
+                _count_copy(src.copier, self.copier, len(dst_ids))
+                src.done()   # the copy has finished
+                return
             if not hasattr(self.copier, "copy_blocks"):
                 raise TypeError("direct transfers need a copier with copy_blocks()")
             self.copier.copy_blocks(src.copier, src.block_ids, dst_ids)
             src.done()   # stream-ordered after the copy's reads
         else:
             _write(self.copier, dst_ids, transfer.block_payloads)
+
+
+def _count_copy(source, copier, n: int) -> None:
+    """Count a queued copy of n blocks as copy_blocks counts its own: n blocks read
+    from the source copier's pool and n written to the destination's."""
+    source.blocks_read += n
+    copier.blocks_written += n
 
 
 def _write(copier, dst_ids: list[int], payloads) -> None:
@@ -332,6 +379,7 @@ class DisaggregatedEngine:
                                      caches=caches[0])
         self.decode = DecodeWorker(model, config, prefix_aware=prefix_aware,
                                    copier_factory=copier_factory, caches=caches[1])
+        self.decode.use_queue = mode == "queue"
         self.stats = DisaggregationStats()
 
     def handoff(self, prompt: list[int], max_new_tokens: int, temperature: float = 0.0,
@@ -375,7 +423,18 @@ class DisaggregatedEngine:
                 entry[2].append(move.payloads)
         moved = 0
         for src_copier, dst_copier, src_all, dst_all, sources in copies.values():
-            if src_all:
+            if src_all and self.decode.use_queue:
+                # one request per move, submitted together, then waited for
+                import numpy as np
+
+                q = self.decode.queue_from(src_copier)
+                q.submit_requests([len(x.block_ids) for x in sources],
+                                  np.asarray(src_all, dtype=np.int32),
+                                  np.asarray(dst_all, dtype=np.int32))
+                q.wait()
+                _count_copy(src_copier, dst_copier, len(src_all))
+                moved += len(src_all)
+            elif src_all:
                 dst_copier.copy_blocks(src_copier, src_all, dst_all)
                 moved += len(src_all)
             for source in sources:
@@ -422,12 +481,14 @@ class DisaggregatedEngine:
             payload_buffer = _StagingArena(self, capacity, pending).take
         sequences = []
         for prompt in prompts:
-            if pending and self.prefill.mode == "direct" and not self._prefill_has_room(prompt):
+            if pending and self.prefill.mode in ("direct", "queue") and \
+                    not self._prefill_has_room(prompt):
                 self.flush_moves(pending)
             sequences.append(self.handoff(prompt, max_new_tokens, temperature, pending,
                                           payload_buffer))
         if pending:
             self.flush_moves(pending)
+        self.decode.stop_queues()   # every prompt is admitted: the GPU is the decode's
         self.decode_until_done()
         return [s.token_ids[s.num_prompt:] for s in sequences]
 

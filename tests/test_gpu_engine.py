@@ -38,7 +38,7 @@ def tiles(caches, block_ids, bs):
             for c in caches]
 
 
-@pytest.mark.parametrize("mode", ["pack", "direct"])
+@pytest.mark.parametrize("mode", ["pack", "direct", "queue"])
 def test_handoff_tables_and_bytes_match_the_reference(gpu, mode):
     from iekv.engine.copier import HipSlotCopier
     from iekv.serve.disaggregated import DisaggregatedEngine
@@ -57,6 +57,9 @@ def test_handoff_tables_and_bytes_match_the_reference(gpu, mode):
             assert transfer.source.block_ids == want["src_table"]
         seq = engine.decode.admit(transfer, 10, 0.0)
         assert seq.block_table == want["dst_table"]
+        if mode == "queue":   # the copy went through the request queue, one descriptor each
+            (q,) = engine.decode._queues.values()
+            q.stop()          # torch reads the pools below
         assert transfer.bytes_moved == want["bytes_moved"]
         assert transfer.token_ids == want["token_ids"]
         dst_bytes = tiles(dk + dv, seq.block_table, bs)
@@ -66,6 +69,9 @@ def test_handoff_tables_and_bytes_match_the_reference(gpu, mode):
     assert engine.decode.copier.blocks_written == G["decode_copier"]["blocks_written"]
     assert engine.decode.copier.bytes_moved == G["decode_copier"]["bytes_moved"]
     assert engine.decode.engine.blocks.num_free == G["decode_free_after_admit"]
+    if mode == "queue":
+        (q,) = engine.decode._queues.values()
+        assert q.stats()["descriptors"] == len(G["requests"])
 
 
 @pytest.mark.parametrize("cache_dtype", [torch.float32, torch.bfloat16], ids=str)
@@ -80,10 +86,14 @@ def test_decode_is_token_identical_after_the_handoff(gpu, cache_dtype):
                                                              temperature=0.0)
     direct = DisaggregatedEngine(m, engine_config(), mode="direct").generate(
         G["prompts"], max_new_tokens=10, temperature=0.0)
+    queued = DisaggregatedEngine(m, engine_config(), mode="queue").generate(
+        G["prompts"], max_new_tokens=10, temperature=0.0)
+    queued_batch = DisaggregatedEngine(m, engine_config(), mode="queue").generate(
+        G["prompts"], max_new_tokens=10, temperature=0.0, batch_moves=True)
     # Identity is among this build's own paths: the model's float32 products on the
     # GPU need not round like the reference's NumPy ones, so its golden tokens are
     # asserted on the CPU (test_disaggregation.py).
-    assert packed == direct == colocated
+    assert packed == direct == queued == queued_batch == colocated
 
 
 def test_the_decode_worker_refuses_a_cache_it_cannot_hold_on_gpu(gpu):
