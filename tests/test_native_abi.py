@@ -582,3 +582,51 @@ def test_the_integration_guides_ctypes_stub_matches_the_abi():
         want = _native.SIGNATURES[name][1]
         assert got == want, (name, got, want)
     assert "lib.iekv_last_error.restype = ctypes.c_char_p" in text
+
+
+def test_request_queue_arguments_are_checked_before_any_hip_call(lib):
+    """The request queue refuses, with IEKV_ERR_INVALID and a message, what it can tell
+    is wrong without a GPU: a null handle or output, pools of other layouts, devices or
+    overlapping memory, and idle / lifetime limits out of range; the calls on a queue
+    refuse a null queue, and an empty submission needs no queue state at all. Nothing
+    here reaches HIP (slab pools register without touching a GPU)."""
+    from iekv import _native
+
+    a = _native.Pool([1 << 20, (1 << 20) + 64 * 16], tile_bytes=64, num_blocks=16, device=0)
+    b = _native.Pool([1 << 24, (1 << 24) + 128 * 16], tile_bytes=128, num_blocks=16, device=0)
+    c = _native.Pool([1 << 28, (1 << 28) + 64 * 16], tile_bytes=64, num_blocks=16, device=1)
+    # overlaps a without being the same pool: a's second array starts inside it
+    d = _native.Pool([(1 << 20) + 64 * 8, 1 << 26], tile_bytes=64, num_blocks=16, device=0)
+    out = ctypes.c_void_p()
+    ticket = ctypes.c_uint64()
+    flag = ctypes.c_int32()
+
+    def refused(code, *expect):
+        assert code == _native.IEKV_ERR_INVALID, code
+        message = lib.iekv_last_error().decode()
+        assert all(e in message for e in expect), message
+
+    refused(lib.iekv_queue_create(a.handle, a.handle, 0, 0, 0, 0, None), "out is null")
+    refused(lib.iekv_queue_create(None, a.handle, 0, 0, 0, 0, ctypes.byref(out)), "null")
+    refused(lib.iekv_queue_create(a.handle, b.handle, 0, 0, 0, 0, ctypes.byref(out)),
+            "differ in shape")
+    refused(lib.iekv_queue_create(a.handle, c.handle, 0, 0, 0, 0, ctypes.byref(out)),
+            "devices 0 and 1")
+    refused(lib.iekv_queue_create(a.handle, d.handle, 0, 0, 0, 0, ctypes.byref(out)),
+            "overlap")
+    refused(lib.iekv_queue_create(a.handle, a.handle, -1, 0, 0, 0, ctypes.byref(out)),
+            "negative")
+    for idle, life in ((999, 0), (200_000, 300_000), (61_000_000, 0)):
+        refused(lib.iekv_queue_create(a.handle, a.handle, 0, 0, idle, life, ctypes.byref(out)),
+                "out of range")
+    assert out.value is None
+    ids = (ctypes.c_int32 * 1)(0)
+    counts = (ctypes.c_int32 * 1)(1)
+    tickets = (ctypes.c_uint64 * 1)()
+    refused(lib.iekv_queue_submit(None, ids, ids, 1, ctypes.byref(ticket)), "queue is null")
+    refused(lib.iekv_queue_submit_requests(None, 1, counts, ids, ids, tickets), "queue is null")
+    refused(lib.iekv_queue_wait(None, 0, 0), "queue is null")
+    refused(lib.iekv_queue_poll(None, 0, ctypes.byref(flag)), "null")
+    refused(lib.iekv_queue_stop(None), "queue is null")
+    refused(lib.iekv_queue_stats(None, None, None), "queue is null")
+    assert lib.iekv_queue_destroy(None) == _native.IEKV_OK
