@@ -1,6 +1,7 @@
 // kv_handoff.hip — gfx950 (MI355X) kernels and C-ABI for the paged KV-cache
-// handoff: direct pool-to-pool copy, fused multi-layer pack, unpack, and the
-// chunked host offload / restore pipelines. The ABI is declared in iekv.h.
+// handoff: direct pool-to-pool copy, fused multi-layer pack, unpack, the
+// chunked host offload / restore pipelines, and a resident request queue for
+// per-request direct handoffs (kv_queue). The ABI is declared in iekv.h.
 //
 // All three device-side moves are one kernel template, kv_move<>, that differs
 // only in where a tile comes from and where it goes:
@@ -1719,15 +1720,16 @@ int restore_images(const iekv_pool* dst, IdList dst_ids, int32_t n_blocks,
 // The host writes descriptor r (a header and the request's ids) into slot
 // r % kQueueSlots of a ring in pinned, coherent host memory and publishes it by
 // raising `tail` to r + 1. Workgroup 0 of the kernel (the leader) polls `tail`,
-// copies each new descriptor to the device's ring, maps the descriptor's claims
-// in the claim ring (iekv_plan::queue_claims) and raises `published_claims`.
-// The waves of the other workgroups (movers) take claims from a set of cursors,
-// wait until their claim is published, move its units, and count it down in the slot's
-// `remaining` word; the mover that finishes a descriptor's last claim writes r + 1
-// into the slot's `complete` word in host memory. The host reuses a slot only
-// after its descriptor is complete, so no mover reads a slot that is being
-// rewritten, and the claim ring holds twice the claims of every descriptor in
-// flight, so no entry is rewritten while its claim waits.
+// reads each new descriptor, writes one record per claim of it (its block's id
+// pair and units, iekv_plan::queue_claims) into the device's claim ring, sets
+// the slot's `remaining` count, and raises `published_claims`. The waves of the
+// other workgroups (movers) take claim numbers from a set of cursors, wait until
+// their claim is published, read its record, move its units, and count it down
+// in the slot's `remaining` word; the mover that finishes a descriptor's last
+// claim writes r + 1 into the slot's `complete` word in host memory. The host
+// reuses a slot only after its descriptor is complete, so no slot is rewritten
+// while its descriptor is served, and the claim ring holds twice the claims of
+// every descriptor in flight, so no record is rewritten while its claim waits.
 // Every wait ends: the leader's poll and a mover's wait for its claim both end
 // on the stop flag, after idle_ticks without a new descriptor, or life_ticks
 // after the workgroup started. The host keeps its submissions inside half of
